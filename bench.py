@@ -1,0 +1,257 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged FP8-KV decode attention step on one MI355X.
+
+Workload (one "step" = one decode-attention call for one layer): batch 256,
+32 query / 8 KV heads, head_dim 128, block_size 256, context lengths
+floor(exp(U(ln 512, ln 8192))), fragmented block tables over a 4096-block
+pool per layer, FP8 e4m3fn KV with a per-tensor scale, bf16 queries.  Steps
+rotate over --layers distinct layer pools (default 8, i.e. 16 GiB of FP8 KV)
+so the working set is far larger than the 256 MiB Infinity Cache.
+
+Prints ONE JSON line.  `value` is the algorithmic HBM throughput of the step
+(every visible K/V byte once + q + out + used block-table entries +
+context_lens, divided by the step time measured with HIP events on the
+launch stream).  `roofline` compares that with the 8 TB/s HBM peak,
+`cpu_baseline` times the reference's PyTorch decode path
+(decode_torch_optimized semantics, restated in oracle/) on a bounded sample
+of the same workload on the host CPU.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--kv fp8|bf16]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (str(REPO / "mini-kvllm_amd"), str(REPO)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "paged FP8-KV decode attn HBM GB/s (% of peak) at bs=256; e2e decode tok/s"
+PEAK_HBM_GBPS = 8000.0
+HEAD_DIM = 128
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--kv", choices=["fp8", "bf16"], default="fp8")
+    ap.add_argument("--layers", type=int, default=8, help="distinct layer pools rotated per step")
+    ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--cpu-seqs", type=int, default=16,
+                    help="sequences in the CPU-baseline sample (0 = skip the CPU baseline)")
+    ap.add_argument("--no-extra", action="store_true", help="skip the secondary measurements")
+    return ap.parse_args()
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def time_launches(fn, steps: int, warmup: int, stream) -> float:
+    """Average ms per call of fn(i), timed with events on `stream`."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        fn(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_baseline(kcs, vcs, scale_kv, q, meta, n_seqs: int) -> dict:
+    """The reference's PyTorch decode path on the host cores, on the first
+    n_seqs sequences of the workload (one micro-batch of 16 at a time)."""
+    import torch
+
+    from mkv import workloads as W
+    from oracle import reference as R
+
+    threads = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit():
+        threads = min(threads, int(env))
+    torch.set_num_threads(threads)
+    ctx = meta["context_lens"][:n_seqs]
+    bt = meta["block_tables"][:n_seqs]
+    bs = meta["block_size"]
+    # copy just the sample's blocks to host memory, re-indexed compactly
+    used = sorted({int(x) for x in bt[bt >= 0]})
+    remap = {p: i for i, p in enumerate(used)}
+    idx = torch.tensor(used, dtype=torch.int64, device=kcs.device)
+    kc = kcs.index_select(0, idx).cpu()
+    vc = vcs.index_select(0, idx).cpu()
+    bt_c = bt.clone()
+    for (i, j), p in zip(torch.nonzero(bt >= 0).tolist(), bt[bt >= 0].tolist()):
+        bt_c[i, j] = remap[int(p)]
+    qc = q[:n_seqs].float().cpu()
+    ks, vs = scale_kv if scale_kv else (None, None)
+    sm = 1.0 / math.sqrt(HEAD_DIM)
+
+    def run():
+        return R.decode_torch_optimized_ref(qc, kc, vc, bt_c, ctx, sm, 32, 8, HEAD_DIM, bs,
+                                            ks, vs, micro_batch=16)
+
+    run()  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    nbytes = W.alg_bytes_decode(ctx, bs, 32, 8, kv_bytes=kcs.element_size())
+    return {
+        "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": (f"first {n_seqs} of 256 sequences (context sum {int(ctx.sum())}), "
+                   f"decode_torch_optimized semantics in fp32 on dequantised KV, micro-batch 16, "
+                   f"median of 3; {t:.3f} s per sample; CPU {cpu_model()}, os.cpu_count "
+                   f"{os.cpu_count()}"),
+    }
+
+
+def traffic_from_profiles(name: str):
+    """HBM bytes per launch measured by a committed rocprofv3 PMC run, if any."""
+    p = REPO / "profiles" / name
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get("traffic_bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+def main() -> int:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the decode path is per-GPU work and this build runs "
+              f"no collectives, so --gpus {args.gpus} (WORLD_SIZE={world}) is not supported; "
+              f"run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import mkv
+    from mkv import attention as A
+    from mkv import workloads as W
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    meta = W.decode_b256_metadata(seed=3)
+    N, bs = meta["num_blocks"], meta["block_size"]
+    kv_dtype = torch.float8_e4m3fn if args.kv == "fp8" else torch.bfloat16
+    layers = []
+    for l in range(args.layers):
+        kc = torch.empty(N, bs, 8, HEAD_DIM, dtype=kv_dtype, device=dev)
+        vc = torch.empty_like(kc)
+        ks = W.fill_pool_on_device(kc, 1000 + 2 * l)
+        vs = W.fill_pool_on_device(vc, 1001 + 2 * l)
+        sc = (torch.tensor([ks], device=dev), torch.tensor([vs], device=dev)) if ks else (None, None)
+        layers.append((kc, vc, sc, (ks, vs) if ks else None))
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(256, 32, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    bt = meta["block_tables"].to(dev)
+    ctx = meta["context_lens"].to(dev)
+    out = torch.empty_like(q)
+    sm = 1.0 / math.sqrt(HEAD_DIM)
+    stream = torch.cuda.current_stream(dev)
+
+    def step(i):
+        kc, vc, (ksd, vsd), _ = layers[i % len(layers)]
+        A._decode(q, kc, vc, bt, ctx, sm, 32, 8, HEAD_DIM, ksd, vsd,
+                  split_tokens=args.split_tokens, out=out)
+
+    nbytes = W.alg_bytes_decode(meta["context_lens"], bs, 32, 8, kv_bytes=kv_dtype.itemsize)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    ms = time_launches(step, args.steps, args.warmup, stream)
+    t_wall = time.perf_counter() - t_wall
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    split = mkv._lib.query("mkv_paged_decode_split_tokens", 256, 8, meta["max_blocks"], bs,
+                           args.split_tokens)
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8" if args.kv == "fp8" else "bf16",
+        "data": "synthetic (seeded N(0,1) KV pools and queries, seeded context lengths/tables)",
+        "config": {
+            "workload": ("paged decode attention, batch 256, 32 q / 8 kv heads, head_dim 128, "
+                         f"block 256, ctx floor(exp(U(ln512, ln8192))) sum {int(meta['context_lens'].sum())}, "
+                         f"fragmented tables over 4096 blocks, {args.kv} KV "
+                         f"({'per-tensor e4m3fn' if args.kv == 'fp8' else 'bf16'}), bf16 q/out, "
+                         f"{args.layers} rotating layer pools"),
+            "batch": 256, "num_heads": 32, "num_kv_heads": 8, "head_dim": HEAD_DIM,
+            "block_size": bs, "split_tokens": split, "algorithmic_bytes_per_step": nbytes,
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(gbps, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+            "frac": round(gbps / PEAK_HBM_GBPS, 4),
+            "traffic": traffic_from_profiles(f"decode_b256_{args.kv}_pmc.json"),
+        },
+        "wall_s_timed_region": round(t_wall, 3),
+    }
+
+    if not args.no_extra:
+        extra = {}
+        # KV append + FP8 quantisation: 4096 tokens (5% padding) and 65536 tokens
+        for T in (4096, 65536):
+            w = W.append_fp8(seed=2, num_tokens=T) if T == 4096 else None
+            if w is None:
+                gg = torch.Generator().manual_seed(20)
+                kk = torch.randn(T, 8, HEAD_DIM, generator=gg).to(torch.bfloat16)
+                vv = torch.randn(T, 8, HEAD_DIM, generator=gg).to(torch.bfloat16)
+                sl = torch.randperm(1024 * 256, generator=gg)[:T].to(torch.int64)
+                w = dict(key=kk, value=vv, slot_mapping=sl)
+            kd, vd, sd = w["key"].to(dev), w["value"].to(dev), w["slot_mapping"].to(dev)
+            kp = torch.zeros(1024, 256, 8, HEAD_DIM, dtype=torch.float8_e4m3fn, device=dev)
+            vp = torch.zeros_like(kp)
+            ksd = torch.tensor([0.05], device=dev)
+            vsd = torch.tensor([0.05], device=dev)
+            ams = time_launches(lambda i: A._append(kd, vd, kp, vp, sd, ksd, vsd), 50, 5, stream)
+            ab = W.alg_bytes_append(w["slot_mapping"], 8, 2, 1)
+            extra[f"append_fp8_T{T}"] = {"us": round(ams * 1e3, 2), "GBps": round(ab / ams / 1e6, 1)}
+            del kp, vp
+        result["extra"] = extra
+
+    if args.cpu_seqs > 0:
+        kc0, vc0, _, scales = layers[0]
+        result["cpu_baseline"] = cpu_baseline(kc0, vc0, scales, q, meta, args.cpu_seqs)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

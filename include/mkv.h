@@ -1,0 +1,243 @@
+/*
+ * mkv.h — C ABI of the MI355X (gfx950) KV-cache hot path.
+ *
+ * The library behind this header (libmkv.so) implements the paged-KV
+ * operators of the mini-kvllm engine (src/myvllm/layers/attention.py in the
+ * reference) as hand-written HIP kernels:
+ *
+ *   K1  slot-mapped KV append, plain copy or fused per-tensor FP8 quantisation
+ *   K2  paged decode attention (GQA-shared K/V tiles, split-K + LSE merge)
+ *   K3  paged / contiguous causal prefill attention on MFMA
+ *   K4  block-table gather (shared device functions + a standalone kernel)
+ *
+ * Conventions
+ *   - Every pointer is a device pointer unless stated otherwise.  The library
+ *     never allocates, frees or synchronises; callers own all memory.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Work is only enqueued; no host reads of device data happen inside.
+ *   - Every function returns an int status: 0 = ok, negative = argument or
+ *     unsupported-combination error (see MKV_ERR_*), positive = a hipError_t
+ *     reported by the launch.  mkv_status_string() names each code.
+ *   - Element counts and strides are in elements of the tensor's dtype.
+ *   - KV pool layout per layer: (num_blocks, block_size, num_kv_heads,
+ *     head_dim), contiguous; slot s lives at (s / block_size, s % block_size).
+ *     This is the layout the reference runner allocates
+ *     (src/myvllm/engine/model_runner.py:311-314, views at :376-395).
+ */
+#ifndef MKV_H_
+#define MKV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MKV_ABI_VERSION 1
+
+/* Element dtypes (torch.float32, torch.bfloat16, torch.float16,
+ * torch.float8_e4m3fn).  FP8 is OCP e4m3fn: max 448, no infinities, NaN =
+ * S.1111.111 (reference: model_runner.py:247, attention.py:113). */
+#define MKV_DTYPE_F32 0
+#define MKV_DTYPE_BF16 1
+#define MKV_DTYPE_F16 2
+#define MKV_DTYPE_FP8E4M3 3
+
+/* Index dtypes for context_lens (the engine uses int64, model_runner.py:617;
+ * the reference's micro-benchmarks use int32, benchmark_decoding.py:290). */
+#define MKV_INDEX_I32 0
+#define MKV_INDEX_I64 1
+
+#define MKV_OK 0
+#define MKV_ERR_NULL_POINTER (-1)
+#define MKV_ERR_BAD_SHAPE (-2)
+#define MKV_ERR_UNSUPPORTED_DTYPE (-3)
+#define MKV_ERR_UNSUPPORTED_HEAD_DIM (-4)
+#define MKV_ERR_UNSUPPORTED_GROUP (-5)
+#define MKV_ERR_BAD_BLOCK_SIZE (-6)
+#define MKV_ERR_WORKSPACE_TOO_SMALL (-7)
+#define MKV_ERR_MISALIGNED (-8)
+#define MKV_ERR_BAD_STRIDE (-9)
+
+/* ABI version of the loaded library (MKV_ABI_VERSION at build time). */
+int mkv_abi_version(void);
+
+/* Static, NUL-terminated description of a status code. */
+const char* mkv_status_string(int status);
+
+/*
+ * K1: slot-mapped KV append.
+ *
+ * Replaces store_kvcache (attention.py:67-108, kernel :7-64) when
+ * cache_dtype == in_dtype, and the per-tensor branch of store_kvcache_fp8
+ * (attention.py:281-333, kernel :118-191) when cache_dtype ==
+ * MKV_DTYPE_FP8E4M3.
+ *
+ * For every token t < num_tokens with slot = slot_mapping[t] >= 0 and
+ * slot < num_blocks * block_size, row t of key (num_kv_heads * head_dim
+ * elements starting at key + t * key_row_stride) is written to k_cache slot
+ * `slot`, likewise value -> v_cache.  slot == -1 means "skip"; any other
+ * negative or out-of-pool slot is skipped as well (never written).
+ *
+ * FP8 mode: q = clamp(float(x) / scale, -448, 448) rounded to e4m3fn with
+ * round-to-nearest-even, scale = *k_scale (resp. *v_scale), a device fp32
+ * scalar.  The divide is the IEEE-754 correctly rounded fp32 divide and NaN
+ * inputs stay NaN, so the bytes equal torch's
+ *   torch.clamp(x.float() / scale, -448, 448).to(torch.float8_e4m3fn).
+ * Copy mode: the bytes are copied unchanged; k_scale/v_scale are ignored.
+ *
+ * Rows must be 16-byte aligned (base pointers and row strides).
+ * in_dtype in {F32, BF16, F16}; cache_dtype == in_dtype or FP8E4M3.
+ * head_dim * num_kv_heads must be a multiple of 16.
+ */
+int mkv_kv_append(const void* key, int64_t key_row_stride,
+                  const void* value, int64_t value_row_stride,
+                  void* k_cache, void* v_cache,
+                  const int64_t* slot_mapping, int64_t num_tokens,
+                  int num_kv_heads, int head_dim,
+                  int block_size, int64_t num_blocks,
+                  int in_dtype, int cache_dtype,
+                  const float* k_scale, const float* v_scale,
+                  void* stream);
+
+/*
+ * Per-tensor FP8 calibration (attention.py:308-323), done on the device so
+ * that no host synchronisation is needed.
+ *
+ * If *k_scale == 1.0f (the "not yet calibrated" sentinel that the runner
+ * initialises with torch.ones, model_runner.py:327), it is replaced by
+ *   round_in(max(round_in(amax|key|), round_in(1e-8)) / 448)
+ * where round_in() rounds an fp32 value to in_dtype (RNE) and amax runs over
+ * ALL num_tokens rows, including rows whose slot is -1.  Same for *v_scale.
+ * A scale that is not exactly 1.0 is left untouched (calibrate once, then
+ * freeze).  This is the reference's
+ *   scale.fill_((x.abs().amax().clamp(min=1e-8) / 448.0).item())
+ * evaluated in x's dtype.
+ *
+ * workspace: >= mkv_fp8_calibrate_workspace_size() bytes of device memory
+ * that is zero before the first call; the kernel leaves it zero again.
+ * Calls that share a workspace must be ordered on one stream.
+ */
+size_t mkv_fp8_calibrate_workspace_size(void);
+int mkv_fp8_calibrate_per_tensor(const void* key, int64_t key_row_stride,
+                                 const void* value, int64_t value_row_stride,
+                                 int64_t num_tokens, int row_elems,
+                                 int in_dtype,
+                                 float* k_scale, float* v_scale,
+                                 void* workspace, void* stream);
+
+/*
+ * K2: paged decode attention.
+ *
+ * Replaces paged_attention_decode (attention.py:895-950, kernel :517-646)
+ * and the per-tensor FP8 path of paged_attention_decode_quantized
+ * (attention.py:1213-1268, kernel :953-1121).
+ *
+ * out[b, h, :] = softmax_t(sm_scale * q[b,h,:] . K_t) @ V_t over the tokens
+ * t < context_lens[b] of sequence b whose logical block
+ * block_tables[b, t / block_size] is a valid pool index (entries of -1 are
+ * skipped), with K_t/V_t taken from kv head h / (num_heads / num_kv_heads).
+ * FP8 caches are dequantised as fp8 * (*k_scale) / fp8 * (*v_scale).
+ * A sequence with no visible token (context_lens[b] == 0) gets zeros.
+ *
+ * q, out: (batch, num_heads, head_dim), rows contiguous, row stride
+ * q_batch_stride / out_batch_stride elements; out has q's dtype.
+ * block_tables: int32 (batch, bt_stride) with max_blocks usable columns.
+ * head_dim == 128; num_heads / num_kv_heads in 1..16; block_size a power of
+ * two >= 16.  kv_dtype F32 requires q_dtype F32.
+ *
+ * split_tokens: tokens per split-K work item (multiple of 32; 0 = library
+ * default).  workspace: >= mkv_paged_decode_workspace_size(...) bytes.
+ */
+size_t mkv_paged_decode_workspace_size(int batch, int num_heads,
+                                       int num_kv_heads, int max_blocks,
+                                       int block_size, int head_dim,
+                                       int split_tokens);
+
+/* Tokens per split-K work item that mkv_paged_decode uses for these sizes
+ * (split_tokens itself when it is > 0). */
+int mkv_paged_decode_split_tokens(int batch, int num_kv_heads, int max_blocks,
+                                  int block_size, int split_tokens);
+int mkv_paged_decode(void* out, int64_t out_batch_stride,
+                     const void* q, int64_t q_batch_stride, int q_dtype,
+                     const void* k_cache, const void* v_cache, int kv_dtype,
+                     int64_t num_blocks,
+                     const float* k_scale, const float* v_scale,
+                     const int32_t* block_tables, int64_t bt_stride,
+                     int max_blocks,
+                     const void* context_lens, int context_lens_dtype,
+                     int batch, int num_heads, int num_kv_heads, int head_dim,
+                     int block_size, float sm_scale, int split_tokens,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * K3: causal prefill / extend attention over the paged cache.
+ *
+ * Replaces paged_attention_prefill_triton (attention.py:852-891, kernel
+ * :704-847) and, with FP8 caches, fills the path that the reference leaves
+ * unimplemented (attention.py:1702-1708).
+ *
+ * For query row i of sequence s (rows cu_seqlens_q[s] .. cu_seqlens_q[s+1])
+ * and head h: visible = min(context_lens[s], positions[i] + 1); out[i, h] is
+ * attention over logical tokens [0, visible) of sequence s, read through
+ * block_tables as in K2 (-1 entries skipped).
+ *
+ * q, out: (total_q, num_heads, head_dim) contiguous.  positions: int64
+ * (total_q).  cu_seqlens_q: int32 (num_seqs + 1).
+ * workspace: >= mkv_paged_prefill_workspace_size(...) bytes (tile list).
+ */
+size_t mkv_paged_prefill_workspace_size(int num_seqs, int64_t total_q,
+                                        int num_heads, int num_kv_heads);
+int mkv_paged_prefill(void* out, const void* q, int q_dtype,
+                      const void* k_cache, const void* v_cache, int kv_dtype,
+                      int64_t num_blocks,
+                      const float* k_scale, const float* v_scale,
+                      const int32_t* block_tables, int64_t bt_stride,
+                      int max_blocks,
+                      const void* context_lens, int context_lens_dtype,
+                      const int32_t* cu_seqlens_q, const int64_t* positions,
+                      int num_seqs, int64_t total_q,
+                      int num_heads, int num_kv_heads, int head_dim,
+                      int block_size, float sm_scale,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * K3 on contiguous K/V: causal varlen attention over freshly projected
+ * q/k/v (full prefill, every sequence starts at position 0).
+ *
+ * Replaces flash_attention_prefill (attention.py:446-514, kernel :336-443).
+ * Row i of sequence s attends to rows cu_seqlens[s] .. i of k/v.
+ * q, out: (total, num_heads, head_dim); k, v: (total, num_kv_heads,
+ * head_dim); all contiguous and of one dtype (F32, BF16 or F16).
+ */
+size_t mkv_flash_prefill_workspace_size(int num_seqs, int64_t total,
+                                        int num_heads, int num_kv_heads);
+int mkv_flash_prefill(void* out, const void* q, const void* k, const void* v,
+                      int dtype, const int32_t* cu_seqlens, int num_seqs,
+                      int64_t total, int num_heads, int num_kv_heads,
+                      int head_dim, float sm_scale,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * K4: block-table gather, paged -> contiguous.
+ *
+ * The torch form of this gather is benchmark_decoding.py:166-178; every
+ * paged kernel of the reference inlines it (attention.py:578-590, :787-798).
+ * dst[b, t, :, :] = cache[block_tables[b, t / bs], t % bs, :, :] for
+ * t < context_lens[b]; rows t >= context_lens[b] (up to max_len) and rows
+ * whose block entry is -1 are zero-filled.  dst: (batch, max_len,
+ * num_kv_heads, head_dim) in the cache dtype, contiguous.
+ */
+int mkv_gather_kv(void* dst, const void* cache, int dtype, int64_t num_blocks,
+                  const int32_t* block_tables, int64_t bt_stride,
+                  int max_blocks,
+                  const void* context_lens, int context_lens_dtype,
+                  int batch, int max_len, int num_kv_heads, int head_dim,
+                  int block_size, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MKV_H_ */

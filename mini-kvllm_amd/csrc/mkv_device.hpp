@@ -1,0 +1,195 @@
+// Shared device-side helpers for the gfx950 KV-cache kernels: element
+// conversions, the OCP e4m3fn codec, MFMA operand types and the block-table
+// gather (K4) that the append, decode and prefill kernels all use.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mkv.h"
+
+#define MKV_DEV __device__ __forceinline__
+
+namespace mkv {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kFp8Max = 448.0f;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWave = 64;
+
+template <int DT>
+struct DTypeInfo;
+template <>
+struct DTypeInfo<MKV_DTYPE_F32> {
+  static constexpr int kBytes = 4;
+};
+template <>
+struct DTypeInfo<MKV_DTYPE_BF16> {
+  static constexpr int kBytes = 2;
+};
+template <>
+struct DTypeInfo<MKV_DTYPE_F16> {
+  static constexpr int kBytes = 2;
+};
+template <>
+struct DTypeInfo<MKV_DTYPE_FP8E4M3> {
+  static constexpr int kBytes = 1;
+};
+
+// ---------------------------------------------------------------------------
+// Scalar conversions.  bf16 <-> f32 is done on the bit pattern; f32 -> bf16
+// and f32 -> f16 round to nearest even like torch's Tensor.to().
+// ---------------------------------------------------------------------------
+MKV_DEV float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+MKV_DEV uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // NaN (torch's canonical)
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+MKV_DEV float f16_bits_to_f32(uint32_t bits16) {
+  _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
+  return (float)h;
+}
+
+MKV_DEV uint32_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;  // v_cvt_f16_f32, round to nearest even
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+// Round an fp32 value to the precision of dtype DT and return it as fp32.
+MKV_DEV float round_to_dtype(float f, int dt) {
+  if (dt == MKV_DTYPE_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(f));
+  if (dt == MKV_DTYPE_F16) return f16_bits_to_f32(f32_to_f16_bits(f));
+  return f;
+}
+
+// ---------------------------------------------------------------------------
+// OCP e4m3fn codec (the native fp8 format of gfx950's conversion units).
+// ---------------------------------------------------------------------------
+
+// torch.clamp(x, -448, 448) semantics: NaN passes through unchanged.
+MKV_DEV float clamp_fp8_range(float v) {
+  v = (v < -kFp8Max) ? -kFp8Max : v;
+  v = (v > kFp8Max) ? kFp8Max : v;
+  return v;
+}
+
+// Sign bit of a NaN input moved to bit 7 of byte k (0 for non-NaN inputs).
+MKV_DEV uint32_t nan_sign_byte(float v, int k) {
+  return (v != v) ? ((__float_as_uint(v) >> 31) << (8 * k + 7)) : 0u;
+}
+
+// Four fp32 values (already within +-448 or NaN) -> four e4m3fn bytes packed
+// little-endian, rounding to nearest even (v_cvt_pk_fp8_f32).  The converter
+// emits one canonical NaN; the input's sign is kept on NaN bytes so that the
+// result equals torch's cast (S.1111.111).
+MKV_DEV uint32_t pack_fp8x4(float a, float b, float c, float d) {
+  uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
+  return w | nan_sign_byte(a, 0) | nan_sign_byte(b, 1) | nan_sign_byte(c, 2) | nan_sign_byte(d, 3);
+}
+
+// Two e4m3fn bytes (low or high half-word of w) -> exact fp16 pair.
+template <bool kHi>
+MKV_DEV f16x2 fp8x2_to_f16x2(uint32_t w) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, kHi);
+}
+
+// Two e4m3fn bytes -> exact fp32 pair.
+template <bool kHi>
+MKV_DEV f32x2 fp8x2_to_f32x2(uint32_t w) {
+  return __builtin_amdgcn_cvt_pk_f32_fp8(w, kHi);
+}
+
+// ---------------------------------------------------------------------------
+// Byte / half-word shuffles used to transpose K/V sub-tiles in registers.
+// __builtin_amdgcn_perm(a, b, sel): result byte k = byte sel[k] of the 8-byte
+// value {b (bytes 0-3), a (bytes 4-7)}.
+// ---------------------------------------------------------------------------
+MKV_DEV uint32_t perm(uint32_t a, uint32_t b, uint32_t sel) {
+  return __builtin_amdgcn_perm(a, b, sel);
+}
+
+// 4x4 byte transpose: rows r0..r3 (one dword each) -> columns c0..c3 where
+// byte k of column j is byte j of row k.
+MKV_DEV void transpose_bytes_4x4(uint32_t r0, uint32_t r1, uint32_t r2,
+                                 uint32_t r3, uint32_t& c0, uint32_t& c1,
+                                 uint32_t& c2, uint32_t& c3) {
+  const uint32_t t01l = perm(r1, r0, 0x05010400u);  // r0.0 r1.0 r0.1 r1.1
+  const uint32_t t01h = perm(r1, r0, 0x07030602u);  // r0.2 r1.2 r0.3 r1.3
+  const uint32_t t23l = perm(r3, r2, 0x05010400u);
+  const uint32_t t23h = perm(r3, r2, 0x07030602u);
+  c0 = perm(t23l, t01l, 0x05040100u);
+  c1 = perm(t23l, t01l, 0x07060302u);
+  c2 = perm(t23h, t01h, 0x05040100u);
+  c3 = perm(t23h, t01h, 0x07060302u);
+}
+
+// Low half-words of (a, b) -> {a.lo, b.lo}; high half-words -> {a.hi, b.hi}.
+MKV_DEV uint32_t pack_lo16(uint32_t a, uint32_t b) { return perm(b, a, 0x05040100u); }
+MKV_DEV uint32_t pack_hi16(uint32_t a, uint32_t b) { return perm(b, a, 0x07060302u); }
+
+// ---------------------------------------------------------------------------
+// Global memory access helpers.
+// ---------------------------------------------------------------------------
+MKV_DEV u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+MKV_DEV u32x2 ld8(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
+MKV_DEV void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// Non-temporal 16-byte load for streamed-once KV bytes.
+MKV_DEV u32x4 ld16_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+MKV_DEV u32x2 ld8_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+}
+
+MKV_DEV int64_t load_index(const void* p, int64_t i, int is_i64) {
+  return is_i64 ? reinterpret_cast<const int64_t*>(p)[i]
+                : (int64_t)reinterpret_cast<const int32_t*>(p)[i];
+}
+
+MKV_DEV int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// ---------------------------------------------------------------------------
+// K4: block-table gather.  Logical token t of sequence b lives in physical
+// block block_tables[b, t >> log2(bs)] at offset t & (bs - 1).  An entry of -1
+// (or any entry outside the pool) marks the block absent; the caller masks
+// such tokens.  Offsets are 64-bit: a bf16 pool of a few thousand 256-token
+// blocks already exceeds 2^31 bytes.
+// ---------------------------------------------------------------------------
+struct PagedIndex {
+  const int32_t* block_tables;
+  int64_t bt_stride;
+  int max_blocks;
+  int64_t num_blocks;
+  int bs_log2;
+  int64_t row_elems;  // num_kv_heads * head_dim: elements per token row
+
+  // Physical block of logical block `blk` of sequence `seq`, or -1.
+  MKV_DEV int64_t physical_block(int seq, int64_t blk) const {
+    if (blk < 0 || blk >= max_blocks) return -1;
+    const int64_t p = block_tables[(int64_t)seq * bt_stride + blk];
+    return (p >= 0 && p < num_blocks) ? p : -1;
+  }
+
+  // Element offset of token row (phys, t) in the pool (head 0, dim 0).
+  MKV_DEV int64_t row_offset(int64_t phys, int64_t t) const {
+    return ((phys << bs_log2) + (t & ((int64_t(1) << bs_log2) - 1))) * row_elems;
+  }
+};
+
+}  // namespace mkv

@@ -1,0 +1,692 @@
+// K2: paged decode attention for gfx950.
+//
+// Reference semantics: paged_attention_decode (attention.py:895-950, kernel
+// :517-646) and the per-tensor FP8 path of paged_attention_decode_quantized
+// (attention.py:1213-1268, kernel :953-1121, dequant :1051-1062/:1098-1107).
+//
+// Work item = (sequence b, kv head g, split s): one wavefront reads the
+// split's K/V tokens of kv head g exactly once and serves all G = Hq/Hkv
+// query heads of the group (the reference launches one program per query
+// head and so reads K/V G times).
+//
+// Per 32-token tile the wave computes S^T = K q^T and O += P V on the MFMA
+// units with operands loaded straight from HBM into registers:
+//   * QK: A = K (16 tokens x 32 dims per lane group), B = q^T (dims x heads).
+//     The contraction order over head_dim is a free permutation, so each lane
+//     loads 32 *contiguous* dims of one token row.
+//   * PV: A = P (heads x tokens), B = V (tokens x dims).  The token set of a
+//     lane group is chosen to be exactly the 8 tokens whose scores that lane
+//     already holds in its QK accumulators, so P never leaves registers; the
+//     output-dim order is also free, so each lane loads 8 contiguous dims of
+//     8 token rows and transposes them with v_perm (bytes for FP8,
+//     half-words for 16-bit caches).
+//   * FP8 bytes convert exactly to fp16 (v_cvt_scalef32_pk_f16_fp8) and run
+//     on the fp16 MFMA; q is normalised by a power of two so it is exact in
+//     fp16, and the per-tensor k/v scales are applied to scores / output in
+//     fp32 (legal because the scale is per tensor).
+// Splits that do not cover a whole sequence write (acc, m, l) partials that a
+// second kernel merges with the log-sum-exp rule.
+#include "mkv_device.hpp"
+
+namespace mkv {
+namespace {
+
+constexpr int kHeadDim = 128;
+constexpr int kDecWaves = 4;
+constexpr float kNegBig = -1e30f;
+
+struct DecodeArgs {
+  void* out;
+  int64_t out_stride;
+  const void* q;
+  int64_t q_stride;
+  int q_dtype;
+  const char* k_cache;
+  const char* v_cache;
+  const float* k_scale;
+  const float* v_scale;
+  PagedIndex idx;
+  const void* context_lens;
+  int ctx_i64;
+  int batch;
+  int num_heads;
+  int num_kv_heads;
+  int group;
+  float sm_scale;
+  int split_tokens;
+  int max_splits;
+  float* ws_acc;  // [batch * num_heads][max_splits][head_dim]
+  float* ws_ml;   // [batch * num_heads][max_splits][2]  (m, l), log2 domain
+};
+
+MKV_DEV float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+// Load 8 consecutive q elements (any q dtype) as fp32.
+MKV_DEV void load_q8(const void* q, int dt, int64_t off, float* x) {
+  if (dt == MKV_DTYPE_F32) {
+    const float* p = reinterpret_cast<const float*>(q) + off;
+    const u32x4 a = ld16(p), b = ld16(p + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[j] = __uint_as_float(a[j]);
+      x[4 + j] = __uint_as_float(b[j]);
+    }
+  } else {
+    const u32x4 a = ld16(reinterpret_cast<const uint16_t*>(q) + off);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (dt == MKV_DTYPE_BF16) {
+        x[2 * j] = bf16_bits_to_f32(a[j] & 0xffffu);
+        x[2 * j + 1] = bf16_bits_to_f32(a[j] >> 16);
+      } else {
+        x[2 * j] = f16_bits_to_f32(a[j] & 0xffffu);
+        x[2 * j + 1] = f16_bits_to_f32(a[j] >> 16);
+      }
+    }
+  }
+}
+
+// Store 8 consecutive fp32 values in the output dtype.
+MKV_DEV void store_out8(void* out, int dt, int64_t off, const float* x) {
+  if (dt == MKV_DTYPE_F32) {
+    float* p = reinterpret_cast<float*>(out) + off;
+    u32x4 a, b;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      a[j] = __float_as_uint(x[j]);
+      b[j] = __float_as_uint(x[4 + j]);
+    }
+    st16(p, a);
+    st16(p + 4, b);
+  } else {
+    u32x4 a;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = dt == MKV_DTYPE_BF16 ? f32_to_bf16_bits(x[2 * j]) : f32_to_f16_bits(x[2 * j]);
+      const uint32_t hi =
+          dt == MKV_DTYPE_BF16 ? f32_to_bf16_bits(x[2 * j + 1]) : f32_to_f16_bits(x[2 * j + 1]);
+      a[j] = lo | (hi << 16);
+    }
+    st16(reinterpret_cast<uint16_t*>(out) + off, a);
+  }
+}
+
+struct WorkItem {
+  int b, kvh, split, num_splits;
+  int64_t t_begin, t_end;
+};
+
+// Decode the flat work index; returns false if the item has nothing to do.
+// A sequence with context length 0 keeps split 0 so that zeros get written.
+MKV_DEV bool decode_work_item(const DecodeArgs& a, int64_t w, WorkItem& it) {
+  const int64_t per_split = (int64_t)a.batch * a.num_kv_heads;
+  if (w >= per_split * a.max_splits) return false;
+  it.split = (int)(w / per_split);
+  const int64_t rem = w - (int64_t)it.split * per_split;
+  it.b = (int)(rem / a.num_kv_heads);
+  it.kvh = (int)(rem - (int64_t)it.b * a.num_kv_heads);
+  int64_t L = load_index(a.context_lens, it.b, a.ctx_i64);
+  const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
+  L = L < 0 ? 0 : (L > cap ? cap : L);
+  it.num_splits = L > 0 ? (int)((L + a.split_tokens - 1) / a.split_tokens) : 1;
+  if (it.split >= it.num_splits) return false;
+  it.t_begin = (int64_t)it.split * a.split_tokens;
+  it.t_end = it.t_begin + a.split_tokens < L ? it.t_begin + a.split_tokens : L;
+  return true;
+}
+
+// Final normalisation / partial write for one wave.  Lane (kg, c) holds
+// O[head 4kg + r][dim 8c + mm] in acc[mm][r]; m_col / l_col hold the running
+// max and the (lane-group summed) denominator of head c.
+MKV_DEV void finish_item(const DecodeArgs& a, const WorkItem& it, f32x4 (&acc)[8], float m_col,
+                         float l_col, float v_mul) {
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * kg + r;
+    const float lh = __shfl(l_col, h);
+    const float mh = __shfl(m_col, h);
+    if (h >= a.group) continue;
+    const int hq = it.kvh * a.group + h;
+    float x[8];
+    if (it.num_splits == 1) {
+      const float inv = lh > 0.0f ? v_mul / lh : 0.0f;
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) x[mm] = acc[mm][r] * inv;
+      store_out8(a.out, a.q_dtype, (int64_t)it.b * a.out_stride + (int64_t)hq * kHeadDim + 8 * c, x);
+    } else {
+      const int64_t slot = ((int64_t)it.b * a.num_heads + hq) * a.max_splits + it.split;
+      float* p = a.ws_acc + slot * kHeadDim + 8 * c;
+      u32x4 lo, hi;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        lo[j] = __float_as_uint(acc[j][r]);
+        hi[j] = __float_as_uint(acc[4 + j][r]);
+      }
+      st16(p, lo);
+      st16(p + 4, hi);
+      if (c == 0) {
+        a.ws_ml[slot * 2] = mh;
+        a.ws_ml[slot * 2 + 1] = lh;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit MFMA kernel: KV in FP8 (via exact fp16), bf16 or fp16.
+// ---------------------------------------------------------------------------
+template <int KV_DT>
+struct Tile16 {
+  // K: 2 token sub-tiles x 32 dims; V: 8 tokens x 8 dims.
+  static constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
+  static constexpr int kKVec = (32 * kEb) / 16;  // 16-byte loads per K row chunk
+  u32x4 k[2][kKVec];
+  typename std::conditional<kEb == 1, u32x2, u32x4>::type v[8];
+  int64_t phys[2];
+};
+
+template <int KV_DT>
+MKV_DEV void load_tile16(const DecodeArgs& a, const WorkItem& it, int64_t t0, Tile16<KV_DT>& T) {
+  constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+  const int64_t bs_mask = (int64_t(1) << a.idx.bs_log2) - 1;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) T.phys[h] = a.idx.physical_block(it.b, (t0 + 16 * h) >> a.idx.bs_log2);
+  const int64_t head_off = (int64_t)it.kvh * kHeadDim;
+  // K rows: token t0 + 16m + c, dims 32kg .. 32kg+31.
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const int64_t t = t0 + 16 * m + c;
+    const bool ok = t < it.t_end && T.phys[m] >= 0;
+    const int64_t base =
+        (((T.phys[m] << a.idx.bs_log2) + (t & bs_mask)) * a.idx.row_elems + head_off + 32 * kg) * kEb;
+#pragma unroll
+    for (int i = 0; i < Tile16<KV_DT>::kKVec; ++i)
+      T.k[m][i] = ok ? ld16_stream(a.k_cache + base + 16 * i) : u32x4{0, 0, 0, 0};
+  }
+  // V rows: token t0 + 16(i/4) + 4kg + (i%4), dims 8c .. 8c+7.
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int hf = i >> 2;
+    const int64_t t = t0 + 16 * hf + 4 * kg + (i & 3);
+    const bool ok = t < it.t_end && T.phys[hf] >= 0;
+    const int64_t base =
+        (((T.phys[hf] << a.idx.bs_log2) + (t & bs_mask)) * a.idx.row_elems + head_off + 8 * c) * kEb;
+    if constexpr (kEb == 1) {
+      T.v[i] = ok ? ld8_stream(a.v_cache + base) : u32x2{0, 0};
+    } else {
+      T.v[i] = ok ? ld16_stream(a.v_cache + base) : u32x4{0, 0, 0, 0};
+    }
+  }
+}
+
+template <int KV_DT>
+using Op16 = typename std::conditional<KV_DT == MKV_DTYPE_BF16, bf16x8, f16x8>::type;
+
+template <int KV_DT>
+MKV_DEV f32x4 mfma16(Op16<KV_DT> A, Op16<KV_DT> B, f32x4 C) {
+  if constexpr (KV_DT == MKV_DTYPE_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, C, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, C, 0, 0, 0);
+}
+
+// Four fp32 -> MFMA operand element type.
+template <int KV_DT>
+MKV_DEV Op16<KV_DT> to_op16(const float* x) {
+  Op16<KV_DT> r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if constexpr (KV_DT == MKV_DTYPE_BF16)
+      r[j] = (__bf16)x[j];
+    else
+      r[j] = (_Float16)x[j];
+  }
+  return r;
+}
+
+// A operand of QK step st for K sub-tile m (8 dims: 32kg + 8st .. +7).
+template <int KV_DT>
+MKV_DEV Op16<KV_DT> k_operand(const Tile16<KV_DT>& T, int m, int st) {
+  if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) {
+    const u32x4 w = T.k[m][st >> 1];
+    const uint32_t d0 = (st & 1) ? w[2] : w[0];
+    const uint32_t d1 = (st & 1) ? w[3] : w[1];
+    const f16x2 a0 = fp8x2_to_f16x2<false>(d0), a1 = fp8x2_to_f16x2<true>(d0);
+    const f16x2 a2 = fp8x2_to_f16x2<false>(d1), a3 = fp8x2_to_f16x2<true>(d1);
+    return f16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+  } else {
+    return __builtin_bit_cast(Op16<KV_DT>, T.k[m][st]);
+  }
+}
+
+// B operands of the 8 PV MFMAs (one per output dim 8c + mm): element j is
+// V[token T_j][8c + mm].
+template <int KV_DT>
+MKV_DEV void v_operands(const Tile16<KV_DT>& T, Op16<KV_DT> (&B)[8]) {
+  if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) {
+    uint32_t X[8], Y[8];
+    transpose_bytes_4x4(T.v[0][0], T.v[1][0], T.v[2][0], T.v[3][0], X[0], X[1], X[2], X[3]);
+    transpose_bytes_4x4(T.v[0][1], T.v[1][1], T.v[2][1], T.v[3][1], X[4], X[5], X[6], X[7]);
+    transpose_bytes_4x4(T.v[4][0], T.v[5][0], T.v[6][0], T.v[7][0], Y[0], Y[1], Y[2], Y[3]);
+    transpose_bytes_4x4(T.v[4][1], T.v[5][1], T.v[6][1], T.v[7][1], Y[4], Y[5], Y[6], Y[7]);
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm) {
+      const f16x2 a0 = fp8x2_to_f16x2<false>(X[mm]), a1 = fp8x2_to_f16x2<true>(X[mm]);
+      const f16x2 a2 = fp8x2_to_f16x2<false>(Y[mm]), a3 = fp8x2_to_f16x2<true>(Y[mm]);
+      B[mm] = f16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      u32x4 lo, hi;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        lo[q] = pack_lo16(T.v[2 * q][p], T.v[2 * q + 1][p]);
+        hi[q] = pack_hi16(T.v[2 * q][p], T.v[2 * q + 1][p]);
+      }
+      B[2 * p] = __builtin_bit_cast(Op16<KV_DT>, lo);
+      B[2 * p + 1] = __builtin_bit_cast(Op16<KV_DT>, hi);
+    }
+  }
+}
+
+template <int KV_DT>
+__global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(DecodeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+  WorkItem it;
+  if (!decode_work_item(a, (int64_t)blockIdx.x * kDecWaves + (threadIdx.x >> 6), it)) return;
+
+  // q of head c, dims 32kg .. 32kg+31 (zero for padding heads c >= G).
+  float qf[32];
+  const int hq = it.kvh * a.group + c;
+  if (c < a.group) {
+    const int64_t qoff = (int64_t)it.b * a.q_stride + (int64_t)hq * kHeadDim + 32 * kg;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) load_q8(a.q, a.q_dtype, qoff + 8 * i, qf + 8 * i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
+  }
+  float score_mul = a.sm_scale * kLog2e;
+  if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) score_mul *= *a.k_scale;
+  if constexpr (KV_DT != MKV_DTYPE_BF16) {
+    // Normalise q by a power of two so that fp16 holds it without overflow;
+    // the factor is undone on the fp32 scores.
+    float qm = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) qm = fmaxf(qm, fabsf(qf[i]));
+    qm = wave_max(qm);
+    if (qm > 0.0f && qm < __builtin_huge_valf()) {
+      const int e = ilogbf(qm);
+      const float f = ldexpf(1.0f, 8 - e);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) qf[i] *= f;
+      score_mul *= ldexpf(1.0f, e - 8);
+    }
+  }
+  Op16<KV_DT> qop[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) qop[st] = to_op16<KV_DT>(qf + 8 * st);
+
+  f32x4 acc[8];
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegBig, l_run = 0.0f;
+
+  for (int64_t t0 = it.t_begin; t0 < it.t_end; t0 += 32) {
+    Tile16<KV_DT> cur;
+    load_tile16<KV_DT>(a, it, t0, cur);
+
+    // S^T = K q^T: lane holds scores of tokens t0 + 16m + 4kg + r for head c.
+    f32x4 s[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      s[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) s[m] = mfma16<KV_DT>(k_operand<KV_DT>(cur, m, st), qop[st], s[m]);
+    }
+    float mx = kNegBig;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t t = t0 + 16 * m + 4 * kg + r;
+        const bool ok = t < it.t_end && cur.phys[m] >= 0;
+        s[m][r] = ok ? s[m][r] * score_mul : -__builtin_huge_valf();
+        mx = fmaxf(mx, s[m][r]);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    float p[8];
+    float psum = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[4 * m + r] = __builtin_amdgcn_exp2f(s[m][r] - m_new);
+        psum += p[4 * m + r];
+      }
+    }
+    l_run = l_run * alpha + psum;
+    // Rescale the output accumulators of heads 4kg + r.
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float ar = __shfl(alpha, 4 * kg + r);
+#pragma unroll
+        for (int mm = 0; mm < 8; ++mm) acc[mm][r] *= ar;
+      }
+    }
+    const Op16<KV_DT> pop = to_op16<KV_DT>(p);
+    Op16<KV_DT> vop[8];
+    v_operands<KV_DT>(cur, vop);
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm) acc[mm] = mfma16<KV_DT>(pop, vop[mm], acc[mm]);
+    if constexpr (KV_DT == MKV_DTYPE_BF16) {
+      // bf16 keeps 8 significant bits of P; add the rounding residual as a
+      // second bf16 term so P carries ~16 bits like the fp32 reference.
+      float plo[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) plo[j] = p[j] - (float)pop[j];
+      const Op16<KV_DT> plop = to_op16<KV_DT>(plo);
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) acc[mm] = mfma16<KV_DT>(plop, vop[mm], acc[mm]);
+    }
+  }
+  float l_col = l_run + __shfl_xor(l_run, 16);
+  l_col += __shfl_xor(l_col, 32);
+  const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? *a.v_scale : 1.0f;
+  finish_item(a, it, acc, m_run, l_col, v_mul);
+}
+
+// ---------------------------------------------------------------------------
+// fp32 KV kernel: v_mfma_f32_16x16x4_f32, 16-token tiles, same lane mapping.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma32_kernel(DecodeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+  WorkItem it;
+  if (!decode_work_item(a, (int64_t)blockIdx.x * kDecWaves + (threadIdx.x >> 6), it)) return;
+
+  float qf[32];
+  const int hq = it.kvh * a.group + c;
+  if (c < a.group) {
+    const int64_t qoff = (int64_t)it.b * a.q_stride + (int64_t)hq * kHeadDim + 32 * kg;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) load_q8(a.q, a.q_dtype, qoff + 8 * i, qf + 8 * i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
+  }
+  const float score_mul = a.sm_scale * kLog2e;
+  f32x4 acc[8];
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegBig, l_run = 0.0f;
+  const int64_t bs_mask = (int64_t(1) << a.idx.bs_log2) - 1;
+  const int64_t head_off = (int64_t)it.kvh * kHeadDim;
+  const float* kc = reinterpret_cast<const float*>(a.k_cache);
+  const float* vc = reinterpret_cast<const float*>(a.v_cache);
+
+  for (int64_t t0 = it.t_begin; t0 < it.t_end; t0 += 16) {
+    const int64_t phys = a.idx.physical_block(it.b, t0 >> a.idx.bs_log2);
+    // K row of token t0 + c, dims 32kg .. 32kg+31.
+    u32x4 kr[8];
+    {
+      const int64_t t = t0 + c;
+      const bool ok = t < it.t_end && phys >= 0;
+      const int64_t base = ((phys << a.idx.bs_log2) + (t & bs_mask)) * a.idx.row_elems + head_off + 32 * kg;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kr[i] = ok ? ld16_stream(kc + base + 4 * i) : u32x4{0, 0, 0, 0};
+    }
+    // V rows of tokens t0 + 4kg + r, dims 8c .. 8c+7.
+    u32x4 vr[4][2];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t t = t0 + 4 * kg + r;
+      const bool ok = t < it.t_end && phys >= 0;
+      const int64_t base = ((phys << a.idx.bs_log2) + (t & bs_mask)) * a.idx.row_elems + head_off + 8 * c;
+      vr[r][0] = ok ? ld16_stream(vc + base) : u32x4{0, 0, 0, 0};
+      vr[r][1] = ok ? ld16_stream(vc + base + 4) : u32x4{0, 0, 0, 0};
+    }
+    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 32; ++st)
+      s = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kr[st >> 2][st & 3]), qf[st], s, 0, 0, 0);
+    float mx = kNegBig;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t t = t0 + 4 * kg + r;
+      const bool ok = t < it.t_end && phys >= 0;
+      s[r] = ok ? s[r] * score_mul : -__builtin_huge_valf();
+      mx = fmaxf(mx, s[r]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    float p[4], psum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = __builtin_amdgcn_exp2f(s[r] - m_new);
+      psum += p[r];
+    }
+    l_run = l_run * alpha + psum;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float ar = __shfl(alpha, 4 * kg + r);
+#pragma unroll
+        for (int mm = 0; mm < 8; ++mm) acc[mm][r] *= ar;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm)
+        acc[mm] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], __uint_as_float(vr[r][mm >> 2][mm & 3]),
+                                                        acc[mm], 0, 0, 0);
+    }
+  }
+  float l_col = l_run + __shfl_xor(l_run, 16);
+  l_col += __shfl_xor(l_col, 32);
+  finish_item(a, it, acc, m_run, l_col, 1.0f);
+}
+
+// ---------------------------------------------------------------------------
+// Split-K merge: one wave per (b, query head) whose sequence used > 1 split.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_merge_kernel(DecodeArgs a,
+                                                                              int kv_fp8) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * kDecWaves + (threadIdx.x >> 6);
+  if (w >= (int64_t)a.batch * a.num_heads) return;
+  const int b = (int)(w / a.num_heads);
+  const int hq = (int)(w - (int64_t)b * a.num_heads);
+  int64_t L = load_index(a.context_lens, b, a.ctx_i64);
+  const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
+  L = L < 0 ? 0 : (L > cap ? cap : L);
+  const int ns = L > 0 ? (int)((L + a.split_tokens - 1) / a.split_tokens) : 1;
+  if (ns <= 1) return;
+  const int64_t slot0 = ((int64_t)b * a.num_heads + hq) * a.max_splits;
+  float M = kNegBig;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.ws_ml[(slot0 + s) * 2]);
+  float l = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  for (int s = 0; s < ns; ++s) {
+    const float wgt = __builtin_amdgcn_exp2f(a.ws_ml[(slot0 + s) * 2] - M);
+    l += wgt * a.ws_ml[(slot0 + s) * 2 + 1];
+    const f32x2 x = *reinterpret_cast<const f32x2*>(a.ws_acc + (slot0 + s) * kHeadDim + 2 * lane);
+    o0 += wgt * x[0];
+    o1 += wgt * x[1];
+  }
+  const float inv = l > 0.0f ? (kv_fp8 ? *a.v_scale : 1.0f) / l : 0.0f;
+  const int64_t off = (int64_t)b * a.out_stride + (int64_t)hq * kHeadDim + 2 * lane;
+  if (a.q_dtype == MKV_DTYPE_F32) {
+    *reinterpret_cast<f32x2*>(reinterpret_cast<float*>(a.out) + off) = f32x2{o0 * inv, o1 * inv};
+  } else {
+    const uint32_t lo = a.q_dtype == MKV_DTYPE_BF16 ? f32_to_bf16_bits(o0 * inv) : f32_to_f16_bits(o0 * inv);
+    const uint32_t hi = a.q_dtype == MKV_DTYPE_BF16 ? f32_to_bf16_bits(o1 * inv) : f32_to_f16_bits(o1 * inv);
+    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + off) = lo | (hi << 16);
+  }
+}
+
+int ilog2_exact(int v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int l = 0;
+  while ((1 << l) < v) ++l;
+  return l;
+}
+
+int default_split_tokens(int batch, int num_kv_heads, int max_blocks, int block_size) {
+  // Aim for >= ~4096 work items (256 CUs x 16 waves) so that the grid fills
+  // the chip even when the batch is small, but never split below 64 tokens.
+  const int64_t items = (int64_t)batch * num_kv_heads;
+  const int64_t max_len = (int64_t)max_blocks * block_size;
+  int64_t want_splits = (4096 + items - 1) / (items > 0 ? items : 1);
+  int64_t st = (max_len + want_splits - 1) / (want_splits > 0 ? want_splits : 1);
+  st = ((st + 31) / 32) * 32;
+  if (st < 64) st = 64;
+  if (st > 512) st = 512;
+  return (int)st;
+}
+
+int resolve_split(int split_tokens, int batch, int num_kv_heads, int max_blocks, int block_size) {
+  if (split_tokens <= 0) return default_split_tokens(batch, num_kv_heads, max_blocks, block_size);
+  return split_tokens;
+}
+
+}  // namespace
+}  // namespace mkv
+
+using namespace mkv;
+
+extern "C" int mkv_paged_decode_split_tokens(int batch, int num_kv_heads, int max_blocks,
+                                             int block_size, int split_tokens) {
+  return resolve_split(split_tokens, batch, num_kv_heads, max_blocks, block_size);
+}
+
+extern "C" size_t mkv_paged_decode_workspace_size(int batch, int num_heads, int num_kv_heads,
+                                                  int max_blocks, int block_size, int head_dim,
+                                                  int split_tokens) {
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks <= 0 || block_size <= 0 ||
+      head_dim <= 0)
+    return 0;
+  const int st = resolve_split(split_tokens, batch, num_kv_heads, max_blocks, block_size);
+  const int64_t max_splits = ((int64_t)max_blocks * block_size + st - 1) / st;
+  if (max_splits <= 1) return 0;
+  return (size_t)batch * num_heads * max_splits * (head_dim + 2) * sizeof(float);
+}
+
+extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void* q,
+                                int64_t q_batch_stride, int q_dtype, const void* k_cache,
+                                const void* v_cache, int kv_dtype, int64_t num_blocks,
+                                const float* k_scale, const float* v_scale,
+                                const int32_t* block_tables, int64_t bt_stride, int max_blocks,
+                                const void* context_lens, int context_lens_dtype, int batch,
+                                int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                float sm_scale, int split_tokens, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks < 0 || num_blocks < 0)
+    return MKV_ERR_BAD_SHAPE;
+  if (batch == 0) return MKV_OK;
+  if (!out || !q || !k_cache || !v_cache || !block_tables || !context_lens) return MKV_ERR_NULL_POINTER;
+  if (head_dim != kHeadDim) return MKV_ERR_UNSUPPORTED_HEAD_DIM;
+  if (num_heads % num_kv_heads != 0) return MKV_ERR_UNSUPPORTED_GROUP;
+  const int group = num_heads / num_kv_heads;
+  if (group < 1 || group > 16) return MKV_ERR_UNSUPPORTED_GROUP;
+  const int bs_log2 = ilog2_exact(block_size);
+  if (bs_log2 < 4) return MKV_ERR_BAD_BLOCK_SIZE;
+  if (q_dtype != MKV_DTYPE_F32 && q_dtype != MKV_DTYPE_BF16 && q_dtype != MKV_DTYPE_F16)
+    return MKV_ERR_UNSUPPORTED_DTYPE;
+  if (kv_dtype != MKV_DTYPE_F32 && kv_dtype != MKV_DTYPE_BF16 && kv_dtype != MKV_DTYPE_F16 &&
+      kv_dtype != MKV_DTYPE_FP8E4M3)
+    return MKV_ERR_UNSUPPORTED_DTYPE;
+  if (kv_dtype == MKV_DTYPE_FP8E4M3 && (!k_scale || !v_scale)) return MKV_ERR_NULL_POINTER;
+  if (context_lens_dtype != MKV_INDEX_I32 && context_lens_dtype != MKV_INDEX_I64)
+    return MKV_ERR_UNSUPPORTED_DTYPE;
+  if (q_batch_stride < (int64_t)num_heads * head_dim || out_batch_stride < (int64_t)num_heads * head_dim ||
+      bt_stride < max_blocks)
+    return MKV_ERR_BAD_STRIDE;
+  if (split_tokens < 0 || split_tokens % 32 != 0) return MKV_ERR_BAD_SHAPE;
+  const int qb = q_dtype == MKV_DTYPE_F32 ? 4 : 2;
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
+       reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u)
+    return MKV_ERR_MISALIGNED;
+  if ((q_batch_stride * qb) % 16 || (out_batch_stride * qb) % 16) return MKV_ERR_MISALIGNED;
+
+  DecodeArgs a;
+  a.out = out;
+  a.out_stride = out_batch_stride;
+  a.q = q;
+  a.q_stride = q_batch_stride;
+  a.q_dtype = q_dtype;
+  a.k_cache = reinterpret_cast<const char*>(k_cache);
+  a.v_cache = reinterpret_cast<const char*>(v_cache);
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
+  a.idx.block_tables = block_tables;
+  a.idx.bt_stride = bt_stride;
+  a.idx.max_blocks = max_blocks;
+  a.idx.num_blocks = num_blocks;
+  a.idx.bs_log2 = bs_log2;
+  a.idx.row_elems = (int64_t)num_kv_heads * head_dim;
+  a.context_lens = context_lens;
+  a.ctx_i64 = context_lens_dtype == MKV_INDEX_I64;
+  a.batch = batch;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.group = group;
+  a.sm_scale = sm_scale;
+  const int st = resolve_split(split_tokens, batch, num_kv_heads, max_blocks, block_size);
+  a.split_tokens = st;
+  const int64_t max_len = (int64_t)max_blocks * block_size;
+  a.max_splits = max_len > 0 ? (int)((max_len + st - 1) / st) : 1;
+  a.ws_acc = nullptr;
+  a.ws_ml = nullptr;
+  if (a.max_splits > 1) {
+    const size_t need = (size_t)batch * num_heads * a.max_splits * (head_dim + 2) * sizeof(float);
+    if (!workspace) return MKV_ERR_NULL_POINTER;
+    if (workspace_bytes < need) return MKV_ERR_WORKSPACE_TOO_SMALL;
+    if (reinterpret_cast<uintptr_t>(workspace) & 15u) return MKV_ERR_MISALIGNED;
+    a.ws_acc = reinterpret_cast<float*>(workspace);
+    a.ws_ml = a.ws_acc + (size_t)batch * num_heads * a.max_splits * head_dim;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t items = (int64_t)batch * num_kv_heads * a.max_splits;
+  const dim3 grid((unsigned)((items + kDecWaves - 1) / kDecWaves));
+  const dim3 block(kDecWaves * kWave);
+  switch (kv_dtype) {
+    case MKV_DTYPE_FP8E4M3:
+      hipLaunchKernelGGL(paged_decode_mfma16_kernel<MKV_DTYPE_FP8E4M3>, grid, block, 0, s, a);
+      break;
+    case MKV_DTYPE_BF16:
+      hipLaunchKernelGGL(paged_decode_mfma16_kernel<MKV_DTYPE_BF16>, grid, block, 0, s, a);
+      break;
+    case MKV_DTYPE_F16:
+      hipLaunchKernelGGL(paged_decode_mfma16_kernel<MKV_DTYPE_F16>, grid, block, 0, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL(paged_decode_mfma32_kernel, grid, block, 0, s, a);
+      break;
+  }
+  if (a.max_splits > 1) {
+    const int64_t mitems = (int64_t)batch * num_heads;
+    hipLaunchKernelGGL(paged_decode_merge_kernel, dim3((unsigned)((mitems + kDecWaves - 1) / kDecWaves)),
+                       block, 0, s, a, (int)(kv_dtype == MKV_DTYPE_FP8E4M3));
+  }
+  return (int)hipGetLastError();
+}

@@ -1,0 +1,690 @@
+// K3: causal prefill / extend attention on the MFMA units, over the paged
+// KV cache (chunked prefill) or over fresh contiguous K/V (full prefill).
+//
+// Reference semantics: paged_attention_prefill_kernel (attention.py:704-847,
+// wrapper :852-891; visible = min(context_len, position + 1) at :747) and
+// flash_attention_varlen_kernel (attention.py:336-443, wrapper :446-514).
+// FP8 caches are dequantised exactly (e4m3fn -> fp16) in the kernel, which
+// the reference leaves unimplemented (attention.py:1702-1708).
+//
+// Work decomposition: a workgroup of 4 wavefronts owns 128 "rows" of one
+// sequence and one KV head, where a row is a (query token, query head of the
+// GQA group) pair, token-major; every row of the group reads the same K/V,
+// so each K/V tile is staged in LDS once for G query heads.  Tiles of 64 keys
+// are gathered through the block table into double-buffered LDS with an XOR
+// swizzle on 16-byte chunks (conflict-free MFMA operand reads).  Each wave
+// owns 2 row tiles of 16 and computes
+//   S^T = K Q^T     (A = K from LDS, B = Q^T resident in registers)
+//   O  += P V       (A = P straight from the S^T accumulators, B = V from LDS
+//                    transposed in registers with v_perm)
+// with an online softmax in the log2 domain.  The varlen tile list is built on
+// the device by a one-workgroup scan, so the launch needs no host sync; the
+// grid is ordered so that all tiles of one KV head run on one XCD and share
+// its L2.
+#include "mkv_device.hpp"
+
+namespace mkv {
+namespace {
+
+constexpr int kHeadDim = 128;
+constexpr int kPfWaves = 4;
+constexpr int kPfThreads = kPfWaves * kWave;
+constexpr int kRowTiles = 2;                       // 16-row MFMA tiles per wave
+constexpr int kRowsPerWg = kPfWaves * kRowTiles * 16;  // 128
+constexpr int kBN = 64;                            // keys per LDS tile
+constexpr int kXcds = 8;
+constexpr float kNegBig = -1e30f;
+
+struct PrefillArgs {
+  void* out;
+  const void* q;
+  int q_dtype;
+  const char* k;  // paged pool (N, bs, Hkv, D) or contiguous (total, Hkv, D)
+  const char* v;
+  const float* k_scale;
+  const float* v_scale;
+  PagedIndex idx;  // paged only
+  const void* context_lens;
+  int ctx_i64;
+  const int32_t* cu_seqlens_q;
+  const int64_t* positions;  // paged only
+  int num_seqs;
+  int64_t total_q;
+  int num_heads;
+  int num_kv_heads;
+  int group;
+  int tok_per_wg;
+  float sm_scale;
+  int32_t* tile_start;  // [num_seqs + 1]
+  int64_t tiles_ub;     // upper bound of tiles per KV head (grid rows)
+};
+
+// ---------------------------------------------------------------------------
+// Tile list: tile_start[s] = sum_{s' < s} ceil(qlen_s' / tok_per_wg).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void prefill_tile_scan_kernel(const int32_t* __restrict__ cu,
+                                                                int num_seqs, int tok_per_wg,
+                                                                int32_t* __restrict__ tile_start) {
+  __shared__ int32_t part[256];
+  int32_t running = 0;
+  for (int base = 0; base < num_seqs; base += 256) {
+    const int s = base + threadIdx.x;
+    int32_t n = 0;
+    if (s < num_seqs) {
+      const int32_t len = cu[s + 1] - cu[s];
+      n = len > 0 ? (len + tok_per_wg - 1) / tok_per_wg : 0;
+    }
+    part[threadIdx.x] = n;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {  // Hillis-Steele inclusive scan
+      const int32_t add = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
+      __syncthreads();
+      part[threadIdx.x] += add;
+      __syncthreads();
+    }
+    if (s < num_seqs) tile_start[s] = running + part[threadIdx.x] - n;
+    running += part[255];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) tile_start[num_seqs] = running;
+}
+
+template <int KV_DT>
+using Op16 = typename std::conditional<KV_DT == MKV_DTYPE_BF16, bf16x8, f16x8>::type;
+
+template <int KV_DT>
+MKV_DEV f32x4 mfma16(Op16<KV_DT> A, Op16<KV_DT> B, f32x4 C) {
+  if constexpr (KV_DT == MKV_DTYPE_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, C, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, C, 0, 0, 0);
+}
+
+template <int KV_DT>
+MKV_DEV Op16<KV_DT> to_op16(const float* x) {
+  Op16<KV_DT> r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if constexpr (KV_DT == MKV_DTYPE_BF16)
+      r[j] = (__bf16)x[j];
+    else
+      r[j] = (_Float16)x[j];
+  }
+  return r;
+}
+
+MKV_DEV void load_q8(const void* q, int dt, int64_t off, float* x) {
+  if (dt == MKV_DTYPE_F32) {
+    const float* p = reinterpret_cast<const float*>(q) + off;
+    const u32x4 a = ld16(p), b = ld16(p + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[j] = __uint_as_float(a[j]);
+      x[4 + j] = __uint_as_float(b[j]);
+    }
+  } else {
+    const u32x4 a = ld16(reinterpret_cast<const uint16_t*>(q) + off);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[2 * j] = dt == MKV_DTYPE_BF16 ? bf16_bits_to_f32(a[j] & 0xffffu) : f16_bits_to_f32(a[j] & 0xffffu);
+      x[2 * j + 1] = dt == MKV_DTYPE_BF16 ? bf16_bits_to_f32(a[j] >> 16) : f16_bits_to_f32(a[j] >> 16);
+    }
+  }
+}
+
+MKV_DEV void store_out8(void* out, int dt, int64_t off, const float* x) {
+  if (dt == MKV_DTYPE_F32) {
+    float* p = reinterpret_cast<float*>(out) + off;
+    u32x4 a, b;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      a[j] = __float_as_uint(x[j]);
+      b[j] = __float_as_uint(x[4 + j]);
+    }
+    st16(p, a);
+    st16(p + 4, b);
+  } else {
+    u32x4 a;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = dt == MKV_DTYPE_BF16 ? f32_to_bf16_bits(x[2 * j]) : f32_to_f16_bits(x[2 * j]);
+      const uint32_t hi = dt == MKV_DTYPE_BF16 ? f32_to_bf16_bits(x[2 * j + 1]) : f32_to_f16_bits(x[2 * j + 1]);
+      a[j] = lo | (hi << 16);
+    }
+    st16(reinterpret_cast<uint16_t*>(out) + off, a);
+  }
+}
+
+// LDS geometry of one K or V tile: kBN key rows of kRowBytes, 16-byte chunks
+// XOR-swizzled by the key index.
+template <int KV_DT>
+struct LdsTile {
+  static constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
+  static constexpr int kRowBytes = kHeadDim * kEb;      // 256 (16-bit) or 128 (fp8)
+  static constexpr int kChunks = kRowBytes / 16;        // 16 or 8
+  static constexpr int kBytes = kBN * kRowBytes;
+  static constexpr int kChunksPerThread = kBN * kChunks / kPfThreads;  // 4 or 2
+  MKV_DEV static int offset(int key, int chunk) {
+    return key * kRowBytes + ((chunk ^ (key & (kChunks - 1))) << 4);
+  }
+};
+
+// Source of key rows: paged (through the block table) or contiguous.
+template <bool PAGED>
+struct KeySource {
+  const char* base;  // k or v
+  int64_t row_bytes_stride;  // bytes between consecutive token rows (contiguous)
+  int64_t head_bytes;        // byte offset of this kv head inside a token row
+  // byte offset of key t's head slice, or -1 when absent
+  MKV_DEV int64_t key_offset(const PrefillArgs& a, int seq, int64_t seq_row0, int64_t t,
+                             int eb) const {
+    if constexpr (PAGED) {
+      const int64_t phys = a.idx.physical_block(seq, t >> a.idx.bs_log2);
+      if (phys < 0) return -1;
+      return a.idx.row_offset(phys, t) * eb + head_bytes;
+    } else {
+      return (seq_row0 + t) * row_bytes_stride + head_bytes;
+    }
+  }
+};
+
+template <int KV_DT, bool PAGED>
+__global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(PrefillArgs a) {
+  using LT = LdsTile<KV_DT>;
+  constexpr int kEb = LT::kEb;
+  extern __shared__ __align__(16) char smem[];
+  // buffer b: K tile at smem + 2b*kBytes, V tile right after it
+#define KBUF(b) (smem + (b) * 2 * LT::kBytes)
+#define VBUF(b) (smem + (b) * 2 * LT::kBytes + LT::kBytes)
+  int* vis_lds = reinterpret_cast<int*>(smem + 4 * LT::kBytes);  // [kRowsPerWg]
+  int* red_lds = vis_lds + kRowsPerWg;                             // [2]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 15, kg = lane >> 4;
+
+  // XCD-aware order: consecutive logical tiles (same KV head) share an XCD.
+  const int64_t nwg = gridDim.x;
+  const int64_t per_xcd = nwg / kXcds;
+  const int64_t logical = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  const int kvh = (int)(logical / a.tiles_ub);
+  const int64_t tau = logical - (int64_t)kvh * a.tiles_ub;
+  if (kvh >= a.num_kv_heads) return;
+  const int32_t total_tiles = a.tile_start[a.num_seqs];
+  if (tau >= total_tiles) return;
+  int lo = 0, hi = a.num_seqs;  // largest s with tile_start[s] <= tau
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (a.tile_start[mid] <= tau) lo = mid; else hi = mid;
+  }
+  const int seq = lo;
+  const int64_t q_seq0 = a.cu_seqlens_q[seq];
+  const int64_t q_seq1 = a.cu_seqlens_q[seq + 1];
+  const int64_t q0 = q_seq0 + (tau - a.tile_start[seq]) * (int64_t)a.tok_per_wg;
+  const int64_t q1 = q0 + a.tok_per_wg < q_seq1 ? q0 + a.tok_per_wg : q_seq1;
+  const int G = a.group;
+
+  int64_t ctx;
+  if constexpr (PAGED) {
+    ctx = load_index(a.context_lens, seq, a.ctx_i64);
+    const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
+    ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+  } else {
+    ctx = q_seq1 - q_seq0;
+  }
+
+  // Visible length of every row (0 for padding rows), and the WG's min / max.
+  if (tid < kRowsPerWg) {
+    const int64_t tok = q0 + tid / G;
+    int vis = 0;
+    if (tid < a.tok_per_wg * G && tok < q1) {
+      const int64_t pos = PAGED ? a.positions[tok] : tok - q_seq0;
+      const int64_t v = pos + 1 < ctx ? pos + 1 : ctx;
+      vis = v < 0 ? 0 : (int)v;
+    }
+    vis_lds[tid] = vis;
+  }
+  if (tid == 0) {
+    red_lds[0] = 0x7fffffff;
+    red_lds[1] = 0;
+  }
+  __syncthreads();
+  if (tid < kRowsPerWg && tid < a.tok_per_wg * G && q0 + tid / G < q1) {
+    atomicMin(&red_lds[0], vis_lds[tid]);
+    atomicMax(&red_lds[1], vis_lds[tid]);
+  }
+  __syncthreads();
+  const int min_vis = red_lds[0];
+  const int max_vis = red_lds[1];
+
+  // Query rows of this wave: row tile rt covers rows (2*wave + rt)*16 + 0..15.
+  int vis_c[kRowTiles];
+  float qf[kRowTiles][32];
+  float qmax = 0.0f;
+#pragma unroll
+  for (int rt = 0; rt < kRowTiles; ++rt) {
+    const int row = (kRowTiles * wave + rt) * 16 + c;
+    vis_c[rt] = vis_lds[row];
+    const int64_t tok = q0 + row / G;
+    const bool ok = row < a.tok_per_wg * G && tok < q1;
+    if (ok) {
+      const int hq = kvh * G + row % G;
+      const int64_t off = (tok * a.num_heads + hq) * kHeadDim + 32 * kg;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) load_q8(a.q, a.q_dtype, off + 8 * i, qf[rt] + 8 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) qf[rt][i] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) qmax = fmaxf(qmax, fabsf(qf[rt][i]));
+  }
+  float score_mul = a.sm_scale * kLog2e;
+  if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) score_mul *= *a.k_scale;
+  if constexpr (KV_DT != MKV_DTYPE_BF16) {
+    // power-of-two normalisation so that q is exact and in range in fp16
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) qmax = fmaxf(qmax, __shfl_xor(qmax, off));
+    if (qmax > 0.0f && qmax < __builtin_huge_valf()) {
+      const int e = ilogbf(qmax);
+      const float f = ldexpf(1.0f, 8 - e);
+#pragma unroll
+      for (int rt = 0; rt < kRowTiles; ++rt)
+#pragma unroll
+        for (int i = 0; i < 32; ++i) qf[rt][i] *= f;
+      score_mul *= ldexpf(1.0f, e - 8);
+    }
+  }
+  Op16<KV_DT> qop[kRowTiles][4];
+#pragma unroll
+  for (int rt = 0; rt < kRowTiles; ++rt)
+#pragma unroll
+    for (int st = 0; st < 4; ++st) qop[rt][st] = to_op16<KV_DT>(qf[rt] + 8 * st);
+
+  f32x4 acc[kRowTiles][8];
+#pragma unroll
+  for (int rt = 0; rt < kRowTiles; ++rt)
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm) acc[rt][mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[kRowTiles], l_run[kRowTiles];
+#pragma unroll
+  for (int rt = 0; rt < kRowTiles; ++rt) {
+    m_run[rt] = kNegBig;
+    l_run[rt] = 0.0f;
+  }
+
+  KeySource<PAGED> ksrc, vsrc;
+  ksrc.base = a.k;
+  vsrc.base = a.v;
+  ksrc.row_bytes_stride = vsrc.row_bytes_stride = (int64_t)a.num_kv_heads * kHeadDim * kEb;
+  ksrc.head_bytes = vsrc.head_bytes = (int64_t)kvh * kHeadDim * kEb;
+
+  // Global -> register staging of one K/V tile (kChunksPerThread 16-byte
+  // chunks each), then register -> LDS.
+  u32x4 kst[LT::kChunksPerThread], vst[LT::kChunksPerThread];
+  auto load_tile = [&](int kb) {
+#pragma unroll
+    for (int j = 0; j < LT::kChunksPerThread; ++j) {
+      const int i = tid + kPfThreads * j;
+      const int key = i / LT::kChunks, ch = i % LT::kChunks;
+      const int64_t t = kb + key;
+      int64_t ko = -1, vo = -1;
+      if (t < max_vis) {
+        ko = ksrc.key_offset(a, seq, q_seq0, t, kEb);
+        vo = ko < 0 ? -1 : vsrc.key_offset(a, seq, q_seq0, t, kEb);
+      }
+      kst[j] = ko >= 0 ? ld16(a.k + ko + 16 * ch) : u32x4{0, 0, 0, 0};
+      vst[j] = vo >= 0 ? ld16(a.v + vo + 16 * ch) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < LT::kChunksPerThread; ++j) {
+      const int i = tid + kPfThreads * j;
+      const int key = i / LT::kChunks, ch = i % LT::kChunks;
+      *reinterpret_cast<u32x4*>(KBUF(buf) + LT::offset(key, ch)) = kst[j];
+      *reinterpret_cast<u32x4*>(VBUF(buf) + LT::offset(key, ch)) = vst[j];
+    }
+  };
+
+  const int n_tiles = (max_vis + kBN - 1) / kBN;
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int it = 0; it < n_tiles; ++it) {
+    const int buf = it & 1;
+    const int kb = it * kBN;
+    if (it + 1 < n_tiles) load_tile(kb + kBN);
+
+    // Key sub-tile validity (16 keys never straddle a block: bs >= 16).
+    bool kvalid[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      if constexpr (PAGED)
+        kvalid[kt] = a.idx.physical_block(seq, (int64_t)(kb + 16 * kt) >> a.idx.bs_log2) >= 0;
+      else
+        kvalid[kt] = true;
+    }
+    const bool full = kb + kBN <= min_vis && kvalid[0] && kvalid[1] && kvalid[2] && kvalid[3];
+
+    // ---- S^T = K Q^T ----
+    f32x4 s[4][kRowTiles];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+      for (int rt = 0; rt < kRowTiles; ++rt) s[kt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int key = 16 * kt + c;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        Op16<KV_DT> kop;
+        if constexpr (kEb == 2) {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(KBUF(buf) + LT::offset(key, 4 * kg + st));
+          kop = __builtin_bit_cast(Op16<KV_DT>, w);
+        } else {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(KBUF(buf) + LT::offset(key, 2 * kg + (st >> 1)));
+          const uint32_t d0 = (st & 1) ? w[2] : w[0];
+          const uint32_t d1 = (st & 1) ? w[3] : w[1];
+          const f16x2 a0 = fp8x2_to_f16x2<false>(d0), a1 = fp8x2_to_f16x2<true>(d0);
+          const f16x2 a2 = fp8x2_to_f16x2<false>(d1), a3 = fp8x2_to_f16x2<true>(d1);
+          kop = f16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+        }
+#pragma unroll
+        for (int rt = 0; rt < kRowTiles; ++rt) s[kt][rt] = mfma16<KV_DT>(kop, qop[rt][st], s[kt][rt]);
+      }
+    }
+
+    // ---- online softmax (log2 domain), per row = lane column c ----
+    float p[4][kRowTiles][4];
+    float alpha[kRowTiles];
+#pragma unroll
+    for (int rt = 0; rt < kRowTiles; ++rt) {
+      float mx = kNegBig;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float x = s[kt][rt][r] * score_mul;
+          if (!full) {
+            const int t = kb + 16 * kt + 4 * kg + r;
+            x = (t < vis_c[rt] && kvalid[kt]) ? x : -__builtin_huge_valf();
+          }
+          s[kt][rt][r] = x;
+          mx = fmaxf(mx, x);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run[rt], mx);
+      alpha[rt] = __builtin_amdgcn_exp2f(m_run[rt] - m_new);
+      m_run[rt] = m_new;
+      float psum = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[kt][rt][r] = __builtin_amdgcn_exp2f(s[kt][rt][r] - m_new);
+          psum += p[kt][rt][r];
+        }
+      l_run[rt] = l_run[rt] * alpha[rt] + psum;
+      if (__builtin_amdgcn_ballot_w64(alpha[rt] != 1.0f)) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float ar = __shfl(alpha[rt], 4 * kg + r);
+#pragma unroll
+          for (int mm = 0; mm < 8; ++mm) acc[rt][mm][r] *= ar;
+        }
+      }
+    }
+
+    // ---- O += P V, 32 keys per MFMA k-step ----
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      Op16<KV_DT> B[8];
+      if constexpr (kEb == 2) {
+        u32x4 vr[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int key = 32 * ks + 16 * (j >> 2) + 4 * kg + (j & 3);
+          vr[j] = *reinterpret_cast<const u32x4*>(VBUF(buf) + LT::offset(key, c));
+        }
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+          u32x4 lo, hi;
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq) {
+            lo[qq] = pack_lo16(vr[2 * qq][pp], vr[2 * qq + 1][pp]);
+            hi[qq] = pack_hi16(vr[2 * qq][pp], vr[2 * qq + 1][pp]);
+          }
+          B[2 * pp] = __builtin_bit_cast(Op16<KV_DT>, lo);
+          B[2 * pp + 1] = __builtin_bit_cast(Op16<KV_DT>, hi);
+        }
+      } else {
+        u32x2 vr[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int key = 32 * ks + 16 * (j >> 2) + 4 * kg + (j & 3);
+          vr[j] = *reinterpret_cast<const u32x2*>(VBUF(buf) + LT::offset(key, c >> 1) + 8 * (c & 1));
+        }
+        uint32_t X[8], Y[8];
+        transpose_bytes_4x4(vr[0][0], vr[1][0], vr[2][0], vr[3][0], X[0], X[1], X[2], X[3]);
+        transpose_bytes_4x4(vr[0][1], vr[1][1], vr[2][1], vr[3][1], X[4], X[5], X[6], X[7]);
+        transpose_bytes_4x4(vr[4][0], vr[5][0], vr[6][0], vr[7][0], Y[0], Y[1], Y[2], Y[3]);
+        transpose_bytes_4x4(vr[4][1], vr[5][1], vr[6][1], vr[7][1], Y[4], Y[5], Y[6], Y[7]);
+#pragma unroll
+        for (int mm = 0; mm < 8; ++mm) {
+          const f16x2 a0 = fp8x2_to_f16x2<false>(X[mm]), a1 = fp8x2_to_f16x2<true>(X[mm]);
+          const f16x2 a2 = fp8x2_to_f16x2<false>(Y[mm]), a3 = fp8x2_to_f16x2<true>(Y[mm]);
+          B[mm] = f16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+        }
+      }
+#pragma unroll
+      for (int rt = 0; rt < kRowTiles; ++rt) {
+        float pv[8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pv[r] = p[2 * ks][rt][r];
+          pv[4 + r] = p[2 * ks + 1][rt][r];
+        }
+        const Op16<KV_DT> pop = to_op16<KV_DT>(pv);
+#pragma unroll
+        for (int mm = 0; mm < 8; ++mm) acc[rt][mm] = mfma16<KV_DT>(pop, B[mm], acc[rt][mm]);
+        if constexpr (KV_DT == MKV_DTYPE_BF16) {
+          // second bf16 term carrying P's rounding residual (~16-bit P)
+          float plo[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) plo[j] = pv[j] - (float)pop[j];
+          const Op16<KV_DT> plop = to_op16<KV_DT>(plo);
+#pragma unroll
+          for (int mm = 0; mm < 8; ++mm) acc[rt][mm] = mfma16<KV_DT>(plop, B[mm], acc[rt][mm]);
+        }
+      }
+    }
+
+    if (it + 1 < n_tiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+#undef KBUF
+#undef VBUF
+  // ---- normalise and write rows 4kg + r of each row tile ----
+  const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? *a.v_scale : 1.0f;
+#pragma unroll
+  for (int rt = 0; rt < kRowTiles; ++rt) {
+    float l_col = l_run[rt] + __shfl_xor(l_run[rt], 16);
+    l_col += __shfl_xor(l_col, 32);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float lh = __shfl(l_col, 4 * kg + r);
+      const int row = (kRowTiles * wave + rt) * 16 + 4 * kg + r;
+      const int64_t tok = q0 + row / G;
+      if (row >= a.tok_per_wg * G || tok >= q1) continue;
+      const int hq = kvh * G + row % G;
+      const float inv = lh > 0.0f ? v_mul / lh : 0.0f;
+      float x[8];
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) x[mm] = acc[rt][mm][r] * inv;
+      store_out8(a.out, a.q_dtype, (tok * a.num_heads + hq) * kHeadDim + 8 * c, x);
+    }
+  }
+}
+
+int ilog2_exact(int v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int l = 0;
+  while ((1 << l) < v) ++l;
+  return l;
+}
+
+int tok_per_wg_for(int group) { return kRowsPerWg / group; }
+
+int64_t tiles_upper_bound(int num_seqs, int64_t total_q, int group) {
+  const int tpw = tok_per_wg_for(group);
+  return (total_q + tpw - 1) / tpw + num_seqs;
+}
+
+template <int KV_DT, bool PAGED>
+int launch_prefill(const PrefillArgs& a, hipStream_t s) {
+  using LT = LdsTile<KV_DT>;
+  const size_t lds = 4 * LT::kBytes + (kRowsPerWg + 2) * sizeof(int);
+  int64_t nwg = a.tiles_ub * a.num_kv_heads;
+  nwg = ((nwg + kXcds - 1) / kXcds) * kXcds;
+  hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED>), dim3((unsigned)nwg), dim3(kPfThreads), lds,
+                     s, a);
+  return (int)hipGetLastError();
+}
+
+size_t prefill_ws_bytes(int num_seqs) { return ((size_t)(num_seqs + 1) * sizeof(int32_t) + 255) / 256 * 256; }
+
+}  // namespace
+}  // namespace mkv
+
+using namespace mkv;
+
+extern "C" size_t mkv_paged_prefill_workspace_size(int num_seqs, int64_t total_q, int num_heads,
+                                                   int num_kv_heads) {
+  (void)total_q;
+  (void)num_heads;
+  (void)num_kv_heads;
+  return num_seqs > 0 ? prefill_ws_bytes(num_seqs) : 0;
+}
+
+extern "C" size_t mkv_flash_prefill_workspace_size(int num_seqs, int64_t total, int num_heads,
+                                                   int num_kv_heads) {
+  return mkv_paged_prefill_workspace_size(num_seqs, total, num_heads, num_kv_heads);
+}
+
+namespace {
+
+int check_common(int num_seqs, int64_t total_q, int num_heads, int num_kv_heads, int head_dim,
+                 int q_dtype, int kv_dtype) {
+  if (num_seqs < 0 || total_q < 0 || num_heads <= 0 || num_kv_heads <= 0) return MKV_ERR_BAD_SHAPE;
+  if (head_dim != kHeadDim) return MKV_ERR_UNSUPPORTED_HEAD_DIM;
+  if (num_heads % num_kv_heads) return MKV_ERR_UNSUPPORTED_GROUP;
+  const int g = num_heads / num_kv_heads;
+  if (g < 1 || g > 16) return MKV_ERR_UNSUPPORTED_GROUP;
+  if (q_dtype != MKV_DTYPE_F32 && q_dtype != MKV_DTYPE_BF16 && q_dtype != MKV_DTYPE_F16)
+    return MKV_ERR_UNSUPPORTED_DTYPE;
+  if (kv_dtype != MKV_DTYPE_BF16 && kv_dtype != MKV_DTYPE_F16 && kv_dtype != MKV_DTYPE_FP8E4M3)
+    return MKV_ERR_UNSUPPORTED_DTYPE;
+  return MKV_OK;
+}
+
+template <bool PAGED>
+int dispatch_prefill(PrefillArgs& a, int kv_dtype, void* workspace, size_t workspace_bytes,
+                     hipStream_t s) {
+  if (workspace_bytes < prefill_ws_bytes(a.num_seqs) || !workspace) return MKV_ERR_WORKSPACE_TOO_SMALL;
+  a.tile_start = reinterpret_cast<int32_t*>(workspace);
+  a.tok_per_wg = tok_per_wg_for(a.group);
+  a.tiles_ub = tiles_upper_bound(a.num_seqs, a.total_q, a.group);
+  hipLaunchKernelGGL(prefill_tile_scan_kernel, dim3(1), dim3(256), 0, s, a.cu_seqlens_q, a.num_seqs,
+                     a.tok_per_wg, a.tile_start);
+  switch (kv_dtype) {
+    case MKV_DTYPE_FP8E4M3: return launch_prefill<MKV_DTYPE_FP8E4M3, PAGED>(a, s);
+    case MKV_DTYPE_BF16: return launch_prefill<MKV_DTYPE_BF16, PAGED>(a, s);
+    default: return launch_prefill<MKV_DTYPE_F16, PAGED>(a, s);
+  }
+}
+
+}  // namespace
+
+extern "C" int mkv_paged_prefill(void* out, const void* q, int q_dtype, const void* k_cache,
+                                 const void* v_cache, int kv_dtype, int64_t num_blocks,
+                                 const float* k_scale, const float* v_scale,
+                                 const int32_t* block_tables, int64_t bt_stride, int max_blocks,
+                                 const void* context_lens, int context_lens_dtype,
+                                 const int32_t* cu_seqlens_q, const int64_t* positions,
+                                 int num_seqs, int64_t total_q, int num_heads, int num_kv_heads,
+                                 int head_dim, int block_size, float sm_scale, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  int st = check_common(num_seqs, total_q, num_heads, num_kv_heads, head_dim, q_dtype, kv_dtype);
+  if (st) return st;
+  if (num_seqs == 0 || total_q == 0) return MKV_OK;
+  if (!out || !q || !k_cache || !v_cache || !block_tables || !context_lens || !cu_seqlens_q ||
+      !positions)
+    return MKV_ERR_NULL_POINTER;
+  if (kv_dtype == MKV_DTYPE_FP8E4M3 && (!k_scale || !v_scale)) return MKV_ERR_NULL_POINTER;
+  if (context_lens_dtype != MKV_INDEX_I32 && context_lens_dtype != MKV_INDEX_I64)
+    return MKV_ERR_UNSUPPORTED_DTYPE;
+  const int bs_log2 = ilog2_exact(block_size);
+  if (bs_log2 < 4) return MKV_ERR_BAD_BLOCK_SIZE;
+  if (bt_stride < max_blocks || max_blocks < 0 || num_blocks < 0) return MKV_ERR_BAD_STRIDE;
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
+       reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u)
+    return MKV_ERR_MISALIGNED;
+  PrefillArgs a{};
+  a.out = out;
+  a.q = q;
+  a.q_dtype = q_dtype;
+  a.k = reinterpret_cast<const char*>(k_cache);
+  a.v = reinterpret_cast<const char*>(v_cache);
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
+  a.idx.block_tables = block_tables;
+  a.idx.bt_stride = bt_stride;
+  a.idx.max_blocks = max_blocks;
+  a.idx.num_blocks = num_blocks;
+  a.idx.bs_log2 = bs_log2;
+  a.idx.row_elems = (int64_t)num_kv_heads * head_dim;
+  a.context_lens = context_lens;
+  a.ctx_i64 = context_lens_dtype == MKV_INDEX_I64;
+  a.cu_seqlens_q = cu_seqlens_q;
+  a.positions = positions;
+  a.num_seqs = num_seqs;
+  a.total_q = total_q;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.group = num_heads / num_kv_heads;
+  a.sm_scale = sm_scale;
+  return dispatch_prefill<true>(a, kv_dtype, workspace, workspace_bytes,
+                                reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int mkv_flash_prefill(void* out, const void* q, const void* k, const void* v, int dtype,
+                                 const int32_t* cu_seqlens, int num_seqs, int64_t total,
+                                 int num_heads, int num_kv_heads, int head_dim, float sm_scale,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  int st = check_common(num_seqs, total, num_heads, num_kv_heads, head_dim, dtype, dtype);
+  if (st) return st;
+  if (num_seqs == 0 || total == 0) return MKV_OK;
+  if (!out || !q || !k || !v || !cu_seqlens) return MKV_ERR_NULL_POINTER;
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
+       reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u)
+    return MKV_ERR_MISALIGNED;
+  PrefillArgs a{};
+  a.out = out;
+  a.q = q;
+  a.q_dtype = dtype;
+  a.k = reinterpret_cast<const char*>(k);
+  a.v = reinterpret_cast<const char*>(v);
+  a.cu_seqlens_q = cu_seqlens;
+  a.num_seqs = num_seqs;
+  a.total_q = total;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.group = num_heads / num_kv_heads;
+  a.sm_scale = sm_scale;
+  return dispatch_prefill<false>(a, dtype, workspace, workspace_bytes,
+                                 reinterpret_cast<hipStream_t>(stream));
+}

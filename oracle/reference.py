@@ -1,0 +1,338 @@
+"""CPU restatement of the reference's KV-cache hot path (torch on CPU).
+
+ORACLE — test infrastructure only.  Only tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg may import this module, and only as the checker
+or as the timed CPU baseline; the product (mini-kvllm_amd/mkv) never does.
+
+Every function names the reference code (paths relative to the reference
+repository heart1128/mini-kvllm) whose behaviour it restates.  Two kinds of
+functions live here:
+
+* vectorised restatements (``*_ref``) used as the parity oracle at test
+  sizes and as the CPU baseline;
+* literal restatements (``*_literal``) that follow the reference's loop
+  structure step by step, in float64, for tiny inputs only.  They pin the
+  vectorised ones (see tests/test_oracle.py).
+
+Tensors are CPU tensors.  Index conventions follow the engine:
+slot_mapping int64 with -1 = skip, block_tables int32 padded with -1,
+context_lens int64 (or int32), cu_seqlens_q int32, positions int64.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+FP8_E4M3_MAX = 448.0
+
+
+# ---------------------------------------------------------------------------
+# a1 / a2 / a3: append, FP8 quantisation, per-tensor calibration
+# ---------------------------------------------------------------------------
+def store_kvcache_ref(key, value, k_cache, v_cache, slot_mapping) -> None:
+    """In-place slot-mapped copy (attention.py:7-64, wrapper :67-108):
+    cache.view(-1, H, D)[slot] = row for every slot != -1 (the cast to the
+    cache dtype is Triton's store-time cast)."""
+    H, D = key.shape[1], key.shape[2]
+    valid = slot_mapping >= 0
+    slots = slot_mapping[valid]
+    k_cache.view(-1, H, D)[slots] = key[valid].to(k_cache.dtype)
+    v_cache.view(-1, H, D)[slots] = value[valid].to(v_cache.dtype)
+
+
+def fp8_quantize_ref(x: torch.Tensor, scale: float) -> torch.Tensor:
+    """clamp(float32(x) / scale, -448, 448) -> float8_e4m3fn (RNE), the
+    per-tensor branch of store_kvcache_fp8_kernel (attention.py:183-191)."""
+    s = torch.tensor(scale, dtype=torch.float32)
+    return torch.clamp(x.float() / s, -FP8_E4M3_MAX, FP8_E4M3_MAX).to(torch.float8_e4m3fn)
+
+
+def calibrate_scale_ref(x: torch.Tensor) -> float:
+    """(x.abs().amax().clamp(min=1e-8) / 448.0).item(), evaluated in x's dtype
+    (attention.py:318-323)."""
+    return float((x.abs().amax().clamp(min=1e-8) / FP8_E4M3_MAX).item())
+
+
+def store_kvcache_fp8_ref(key, value, k_cache, v_cache, k_scale, v_scale, slot_mapping) -> None:
+    """store_kvcache_fp8 per-tensor mode (attention.py:281-333): calibrate a
+    scale still equal to 1.0 from ALL rows (slot -1 rows included), then
+    quantise and store the valid rows.  k_scale/v_scale: fp32 (1,) tensors,
+    updated in place like the reference's fill_()."""
+    if float(k_scale.reshape(-1)[0].item()) == 1.0:
+        k_scale.fill_(calibrate_scale_ref(key))
+    if float(v_scale.reshape(-1)[0].item()) == 1.0:
+        v_scale.fill_(calibrate_scale_ref(value))
+    H, D = key.shape[1], key.shape[2]
+    valid = slot_mapping >= 0
+    slots = slot_mapping[valid]
+    k_cache.view(-1, H, D)[slots] = fp8_quantize_ref(key[valid], float(k_scale.reshape(-1)[0]))
+    v_cache.view(-1, H, D)[slots] = fp8_quantize_ref(value[valid], float(v_scale.reshape(-1)[0]))
+
+
+def dequant_ref(cache: torch.Tensor, scale: float | None) -> torch.Tensor:
+    """fp8 -> fp32 times the per-tensor scale, in fp32 (attention.py:1051-1062,
+    :1098-1107); bf16/fp16/fp32 are upcast to fp32 exactly, fp64 is kept."""
+    if cache.dtype == torch.float8_e4m3fn:
+        return cache.to(torch.float32) * scale
+    if cache.dtype == torch.float64:
+        return cache
+    return cache.to(torch.float32)
+
+
+# ---------------------------------------------------------------------------
+# a8: block-table gather
+# ---------------------------------------------------------------------------
+def gather_kv_ref(cache, block_tables, context_lens, max_len: int) -> torch.Tensor:
+    """(batch, max_len, H, D) gather through the block table, zero past the
+    context or in absent (-1) blocks (torch form: benchmark_decoding.py:166-178)."""
+    B = block_tables.shape[0]
+    N, bs, H, D = cache.shape
+    out = torch.zeros(B, max_len, H, D, dtype=cache.dtype)
+    for b in range(B):
+        L = min(int(context_lens[b]), max_len)
+        for t in range(L):
+            blk = t // bs
+            if blk >= block_tables.shape[1]:
+                break
+            p = int(block_tables[b, blk])
+            if 0 <= p < N:
+                out[b, t] = cache[p, t % bs]
+    return out
+
+
+def _seq_kv(k_cache, v_cache, block_tables, b, L, k_scale=None, v_scale=None):
+    """K/V rows [0, L) of sequence b as fp32 plus a validity mask (tokens in
+    absent blocks are invalid, attention.py:586)."""
+    N, bs, H, D = k_cache.shape
+    nb = (L + bs - 1) // bs
+    tbl = block_tables[b, :nb].to(torch.int64)
+    ok_blk = (tbl >= 0) & (tbl < N)
+    safe = torch.where(ok_blk, tbl, torch.zeros_like(tbl))
+    k = dequant_ref(k_cache[safe], k_scale).reshape(nb * bs, H, D)[:L]
+    v = dequant_ref(v_cache[safe], v_scale).reshape(nb * bs, H, D)[:L]
+    valid = ok_blk.repeat_interleave(bs)[:L]
+    return k, v, valid
+
+
+# ---------------------------------------------------------------------------
+# a4 / a5: paged decode
+# ---------------------------------------------------------------------------
+def paged_decode_ref(query, k_cache, v_cache, block_tables, context_lens, scale, num_heads,
+                     num_kv_heads, k_scale=None, v_scale=None,
+                     compute_dtype=torch.float64) -> torch.Tensor:
+    """Decode attention (paged_attention_decode_kernel, attention.py:517-646;
+    FP8 variant :953-1121): for head h of sequence b, softmax over the tokens
+    t < context_lens[b] whose block is present, of scale * q . K_t, applied
+    to V_t, with kv head h // (num_heads // num_kv_heads) (:541).  A sequence
+    without visible tokens yields zeros (the reference yields 0/0 = NaN
+    there; only padded graph rows hit that case).  Output in query's dtype."""
+    B, Hq, D = query.shape
+    G = num_heads // num_kv_heads
+    max_blocks = block_tables.shape[1]
+    bs = k_cache.shape[1]
+    out = torch.zeros(B, Hq, D, dtype=compute_dtype)
+    for b in range(B):
+        L = min(int(context_lens[b]), max_blocks * bs)
+        if L <= 0:
+            continue
+        k, v, valid = _seq_kv(k_cache, v_cache, block_tables, b, L, k_scale, v_scale)
+        if not bool(valid.any()):
+            continue
+        k = k.to(compute_dtype)
+        v = v.to(compute_dtype)
+        q = query[b].to(compute_dtype).reshape(num_kv_heads, G, D)
+        s = torch.einsum("hgd,thd->hgt", q, k) * scale
+        s = s.masked_fill(~valid[None, None, :], float("-inf"))
+        p = torch.softmax(s, dim=-1)
+        out[b] = torch.einsum("hgt,thd->hgd", p, v).reshape(Hq, D)
+    return out.to(query.dtype)
+
+
+def decode_torch_optimized_ref(q, k_cache, v_cache, block_tables, context_lens, scale,
+                               num_heads, num_kv_heads, head_dim, block_size,
+                               k_scale=None, v_scale=None, micro_batch: int | None = None):
+    """The reference's PyTorch decode path, decode_torch_optimized
+    (benchmark_decoding.py:145-198): gather each sequence's blocks into a
+    zero-padded (B, Lmax, H, D) tensor, repeat_interleave the kv heads, then
+    matmul -> -inf mask -> softmax -> matmul, in q's dtype.  FP8 caches are
+    dequantised first (attention.py:1051-1062).  ``micro_batch`` bounds the
+    padded working set (the full-batch form needs tens of GB at batch 256)."""
+    B = q.shape[0]
+    if micro_batch is not None and micro_batch < B:
+        return torch.cat([
+            decode_torch_optimized_ref(q[i:i + micro_batch], k_cache, v_cache,
+                                       block_tables[i:i + micro_batch],
+                                       context_lens[i:i + micro_batch], scale, num_heads,
+                                       num_kv_heads, head_dim, block_size, k_scale, v_scale)
+            for i in range(0, B, micro_batch)])
+    dtype = q.dtype
+    max_context_len = int(context_lens.max().item())
+    padded_k = torch.zeros(B, max_context_len, num_kv_heads, head_dim, dtype=dtype)
+    padded_v = torch.zeros(B, max_context_len, num_kv_heads, head_dim, dtype=dtype)
+    for i in range(B):
+        seq_len = int(context_lens[i].item())
+        nb = (seq_len + block_size - 1) // block_size
+        blocks = block_tables[i, :nb]
+        blocks = blocks[blocks != -1].to(torch.int64)
+        if len(blocks) > 0:
+            kk = dequant_ref(k_cache[blocks], k_scale).to(dtype).reshape(-1, num_kv_heads, head_dim)
+            vv = dequant_ref(v_cache[blocks], v_scale).to(dtype).reshape(-1, num_kv_heads, head_dim)
+            padded_k[i, :seq_len] = kk[:seq_len]
+            padded_v[i, :seq_len] = vv[:seq_len]
+    if num_kv_heads != num_heads:
+        g = num_heads // num_kv_heads
+        padded_k = padded_k.repeat_interleave(g, dim=2)
+        padded_v = padded_v.repeat_interleave(g, dim=2)
+    qq = q.unsqueeze(2)
+    pk = padded_k.transpose(1, 2)
+    pv = padded_v.transpose(1, 2)
+    scores = torch.matmul(qq, pk.transpose(-2, -1)) * scale
+    mask = torch.arange(max_context_len)[None, :] < context_lens[:, None]
+    scores = scores.masked_fill(~mask[:, None, None, :], float("-inf"))
+    probs = torch.softmax(scores, dim=-1)
+    return torch.matmul(probs, pv).squeeze(2)
+
+
+def paged_decode_literal(query, k_cache, v_cache, block_tables, context_lens, scale, num_heads,
+                         num_kv_heads, k_scale=None, v_scale=None) -> torch.Tensor:
+    """Step-by-step restatement of paged_attention_decode_kernel /
+    paged_attention_decode_fp8_kernel (attention.py:517-646, :953-1121) in
+    float64 Python loops: 64-token chunks, -1e10 score sentinel, online
+    softmax with separate K and V passes, blocks with entry -1 skipped.
+    Tiny inputs only."""
+    B, Hq, D = query.shape
+    G = num_heads // num_kv_heads
+    max_blocks = block_tables.shape[1]
+    bs = k_cache.shape[1]
+    BLOCK_N = 64
+    out = torch.zeros(B, Hq, D, dtype=torch.float64)
+    kf = dequant_ref(k_cache, k_scale).double()
+    vf = dequant_ref(v_cache, v_scale).double()
+    for b in range(B):
+        L = int(context_lens[b])
+        for h in range(Hq):
+            kvh = h // G
+            q = query[b, h].double()
+            acc = torch.zeros(D, dtype=torch.float64)
+            l_i, m_i = 0.0, -1e10
+            for start in range(0, max_blocks * bs, BLOCK_N):
+                if start >= L:
+                    continue
+                qk = [-1e10] * BLOCK_N
+                for i in range(BLOCK_N):
+                    t = start + i
+                    if t < L and t // bs < max_blocks:
+                        p = int(block_tables[b, t // bs])
+                        if p != -1:
+                            qk[i] = float((q * kf[p, t % bs, kvh]).sum()) * scale
+                m_new = max(m_i, max(qk))
+                alpha = math.exp(m_i - m_new)
+                pw = [math.exp(x - m_new) for x in qk]
+                acc = acc * alpha
+                l_i = l_i * alpha
+                for i in range(BLOCK_N):
+                    t = start + i
+                    if t < L and t // bs < max_blocks:
+                        p = int(block_tables[b, t // bs])
+                        if p != -1:
+                            acc = acc + pw[i] * vf[p, t % bs, kvh]
+                            l_i += pw[i]
+                m_i = m_new
+            out[b, h] = acc / l_i if l_i > 0 else 0.0
+    return out
+
+
+# ---------------------------------------------------------------------------
+# a6: chunked prefill over the paged cache; a7: full prefill on fresh K/V
+# ---------------------------------------------------------------------------
+def paged_prefill_ref(query, k_cache, v_cache, block_tables, context_lens, cu_seqlens_q,
+                      positions, scale, num_heads, num_kv_heads, k_scale=None, v_scale=None,
+                      compute_dtype=torch.float64) -> torch.Tensor:
+    """paged_attention_prefill_kernel semantics (attention.py:704-847): row i
+    of sequence s attends to logical tokens [0, min(context_lens[s],
+    positions[i] + 1)) (:747) through the block table, absent blocks
+    skipped.  FP8 caches are dequantised first (the reference raises for
+    FP8 here, attention.py:1702-1708; dequantise-then-attend is the
+    semantics its decode path uses).  Output in query's dtype."""
+    Tq, Hq, D = query.shape
+    G = num_heads // num_kv_heads
+    bs = k_cache.shape[1]
+    max_blocks = block_tables.shape[1]
+    out = torch.zeros(Tq, Hq, D, dtype=compute_dtype)
+    cu = [int(x) for x in cu_seqlens_q]
+    for s in range(len(cu) - 1):
+        r0, r1 = cu[s], cu[s + 1]
+        if r1 <= r0:
+            continue
+        L = min(int(context_lens[s]), max_blocks * bs)
+        if L <= 0:
+            continue
+        k, v, valid = _seq_kv(k_cache, v_cache, block_tables, s, L, k_scale, v_scale)
+        k = k.to(compute_dtype)
+        v = v.to(compute_dtype)
+        pos = positions[r0:r1].to(torch.int64)
+        vis = torch.minimum(torch.full_like(pos, L), pos + 1)  # (rows,)
+        q = query[r0:r1].to(compute_dtype).reshape(r1 - r0, num_kv_heads, G, D)
+        sc = torch.einsum("rhgd,thd->rhgt", q, k) * scale
+        t = torch.arange(L)
+        allowed = (t[None, :] < vis[:, None]) & valid[None, :]
+        sc = sc.masked_fill(~allowed[:, None, None, :], float("-inf"))
+        has = allowed.any(dim=1)
+        p = torch.softmax(sc, dim=-1)
+        p = torch.where(has[:, None, None, None], p, torch.zeros_like(p))
+        out[r0:r1] = torch.einsum("rhgt,thd->rhgd", p, v).reshape(r1 - r0, Hq, D)
+    return out.to(query.dtype)
+
+
+def paged_prefill_literal(query, k_cache, v_cache, block_tables, context_lens, cu_seqlens_q,
+                          positions, scale, num_heads, num_kv_heads, k_scale=None,
+                          v_scale=None) -> torch.Tensor:
+    """Literal restatement of paged_attention_prefill_torch
+    (attention.py:649-696) in float64: per sequence, stack the context rows
+    through the block table, then per query row and head a softmax over
+    history[:pos + 1].  Tiny inputs only; every block must be present."""
+    G = num_heads // num_kv_heads
+    bs = k_cache.shape[1]
+    kf = dequant_ref(k_cache, k_scale).double()
+    vf = dequant_ref(v_cache, v_scale).double()
+    out = torch.zeros(query.shape, dtype=torch.float64)
+    cu = [int(x) for x in cu_seqlens_q]
+    for s in range(len(cu) - 1):
+        L = int(context_lens[s])
+        hk = torch.stack([kf[int(block_tables[s, t // bs]), t % bs] for t in range(L)])
+        hv = torch.stack([vf[int(block_tables[s, t // bs]), t % bs] for t in range(L)])
+        for i in range(cu[s], cu[s + 1]):
+            pos = int(positions[i])
+            vk, vv = hk[:pos + 1], hv[:pos + 1]
+            for h in range(num_heads):
+                kvh = h // G
+                sc = (query[i, h].double()[None, :] * vk[:, kvh]).sum(-1) * scale
+                p = torch.softmax(sc, dim=-1)
+                out[i, h] = (p[:, None] * vv[:, kvh]).sum(0)
+    return out
+
+
+def flash_prefill_ref(q, k, v, cu_seqlens, scale, num_heads, num_kv_heads,
+                      compute_dtype=torch.float64) -> torch.Tensor:
+    """Causal varlen attention on fresh contiguous q/k/v, the semantics of
+    flash_attention_varlen_kernel (attention.py:336-443) and of the
+    reference's torch form pytorch_standard_attention
+    (benchmark_prefilling.py:9-52).  Output in q's dtype."""
+    T, Hq, D = q.shape
+    G = num_heads // num_kv_heads
+    out = torch.zeros(T, Hq, D, dtype=compute_dtype)
+    cu = [int(x) for x in cu_seqlens]
+    for s in range(len(cu) - 1):
+        a, b = cu[s], cu[s + 1]
+        n = b - a
+        if n <= 0:
+            continue
+        qs = q[a:b].to(compute_dtype).transpose(0, 1)
+        ks = k[a:b].to(compute_dtype).transpose(0, 1).repeat_interleave(G, dim=0)
+        vs = v[a:b].to(compute_dtype).transpose(0, 1).repeat_interleave(G, dim=0)
+        sc = torch.matmul(qs, ks.transpose(1, 2)) * scale
+        causal = torch.triu(torch.ones(n, n, dtype=torch.bool), diagonal=1)
+        sc = sc.masked_fill(causal[None], float("-inf"))
+        out[a:b] = torch.matmul(torch.softmax(sc, dim=-1), vs).transpose(0, 1)
+    return out.to(q.dtype)

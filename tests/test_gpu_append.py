@@ -1,0 +1,160 @@
+"""GPU parity of K1 (slot-mapped append, FP8 quantisation, calibration).
+
+Bar: bit-exact.  Every byte of the pool is compared, including slots the
+append must not touch.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from mkv import attention as A
+from mkv import workloads as W
+from oracle import fp8_codec
+from oracle import reference as R
+
+pytestmark = pytest.mark.gpu
+FP8 = torch.float8_e4m3fn
+
+
+def _u8(t):
+    return t.detach().cpu().contiguous().view(torch.uint8)
+
+
+def test_append_fp8_workload_byte_identical(dev):
+    announce("append fp8: 4096 tokens bf16 -> 1024x256x8x128 pool, 5% slot -1")
+    w = W.append_fp8(seed=2)
+    N, bs, H = w["num_blocks"], w["block_size"], w["num_kv_heads"]
+    kc = torch.zeros(N, bs, H, 128, dtype=FP8, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.ones(1, device=dev)
+    vs = torch.ones(1, device=dev)
+    A.store_kvcache_fp8(w["key"].to(dev), w["value"].to(dev), kc, vc, ks, vs,
+                        w["slot_mapping"].to(dev), bs, "fp8_per_tensor")
+    kr = torch.zeros(N, bs, H, 128, dtype=FP8)
+    vr = torch.zeros_like(kr)
+    ksr, vsr = torch.ones(1), torch.ones(1)
+    R.store_kvcache_fp8_ref(w["key"], w["value"], kr, vr, ksr, vsr, w["slot_mapping"])
+    assert float(ks) == float(ksr) and float(vs) == float(vsr)
+    assert torch.equal(_u8(kc), kr.view(torch.uint8))
+    assert torch.equal(_u8(vc), vr.view(torch.uint8))
+
+
+@pytest.mark.parametrize("scale", [0.5, 1.0, 0.125, 0.0123, 7.3])
+def test_fp8_encoding_exhaustive_bf16(dev, scale):
+    announce(f"fp8 encode of all 65536 bf16 patterns, scale {scale}")
+    bits = torch.from_numpy(np.arange(65536, dtype=np.uint16).view(np.int16))
+    x = bits.view(torch.bfloat16).reshape(64, 8, 128)
+    slots = torch.arange(64, dtype=torch.int64)
+    kc = torch.zeros(1, 64, 8, 128, dtype=FP8, device=dev)
+    vc = torch.zeros_like(kc)
+    s = torch.full((1,), scale, device=dev)
+    A._append(x.to(dev), x.to(dev), kc, vc, slots.to(dev), s, s)
+    got = _u8(kc).reshape(-1).numpy()
+    want = R.fp8_quantize_ref(x, scale).view(torch.uint8).reshape(-1).numpy()
+    xf = x.float().reshape(-1).numpy()
+    nan = np.isnan(xf)
+    assert np.array_equal(got[~nan], want[~nan])
+    # NaN inputs stay NaN (0x7f / 0xff, the sign kept as torch does)
+    assert np.array_equal(got[nan] & 0x7F, np.full(int(nan.sum()), 0x7F, np.uint8))
+    assert np.array_equal(got, want)
+
+
+def test_fp8_encoding_random_fp32_inputs(dev):
+    announce("fp8 encode of random fp32 inputs over 2^-20..2^12")
+    g = torch.Generator().manual_seed(11)
+    T, H, D = 512, 8, 128
+    mag = torch.exp2(torch.randint(-20, 12, (T, H, D), generator=g).float())
+    x = torch.randn(T, H, D, generator=g) * mag
+    slots = torch.randperm(T, generator=g).to(torch.int64)
+    kc = torch.zeros(2, 256, H, D, dtype=FP8, device=dev)
+    vc = torch.zeros_like(kc)
+    s = torch.full((1,), 0.37, device=dev)
+    A._append(x.to(dev), x.to(dev), kc, vc, slots.to(dev), s, s)
+    want = torch.zeros(2 * 256, H, D, dtype=FP8)
+    want[slots] = R.fp8_quantize_ref(x, 0.37)
+    assert torch.equal(_u8(kc).reshape(-1), want.view(torch.uint8).reshape(-1))
+    # the independent codec agrees on the same bytes
+    assert np.array_equal(_u8(kc).reshape(-1, H, D)[slots].reshape(-1).numpy(),
+                          fp8_codec.quantize_per_tensor(x.reshape(-1).numpy(), 0.37))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_copy_append_bit_exact_with_padding_and_bounds(dev, dtype):
+    announce(f"copy append {dtype}")
+    g = torch.Generator().manual_seed(5)
+    T, H, D, N, bs = 300, 8, 128, 16, 32
+    k = torch.randn(T, H, D, generator=g).to(dtype)
+    v = torch.randn(T, H, D, generator=g).to(dtype)
+    slots = torch.randperm(N * bs, generator=g)[:T].to(torch.int64)
+    slots[::7] = -1
+    slots[5] = N * bs + 3  # outside the pool: must be skipped, not written
+    slots[6] = -5
+    kc = torch.full((N, bs, H, D), 7.0, dtype=dtype, device=dev)
+    vc = torch.full((N, bs, H, D), 7.0, dtype=dtype, device=dev)
+    A.store_kvcache(k.to(dev), v.to(dev), kc, vc, slots.to(dev), bs)
+    kr = torch.full((N, bs, H, D), 7.0, dtype=dtype)
+    vr = torch.full((N, bs, H, D), 7.0, dtype=dtype)
+    keep = (slots >= 0) & (slots < N * bs)
+    R.store_kvcache_ref(k[keep], v[keep], kr, vr, slots[keep])
+    assert torch.equal(kc.cpu(), kr) and torch.equal(vc.cpu(), vr)
+
+
+def test_append_from_strided_qkv_view(dev):
+    announce("append from k/v views into a fused qkv buffer")
+    g = torch.Generator().manual_seed(6)
+    T, Hq, H, D, N, bs = 64, 32, 8, 128, 4, 256
+    qkv = torch.randn(T, (Hq + 2 * H) * D, generator=g).to(torch.bfloat16).to(dev)
+    k = qkv[:, Hq * D:(Hq + H) * D].view(T, H, D)
+    v = qkv[:, (Hq + H) * D:].view(T, H, D)
+    assert not v.is_contiguous()
+    slots = torch.randperm(N * bs, generator=g)[:T].to(torch.int64)
+    kc = torch.zeros(N, bs, H, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    A.store_kvcache(k, v, kc, vc, slots.to(dev), bs)
+    kr = torch.zeros(N, bs, H, D, dtype=torch.bfloat16)
+    vr = torch.zeros_like(kr)
+    R.store_kvcache_ref(k.cpu(), v.cpu(), kr, vr, slots)
+    assert torch.equal(kc.cpu(), kr) and torch.equal(vc.cpu(), vr)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_device_calibration_matches_reference_rule(dev, dtype):
+    announce(f"fp8 calibration {dtype}")
+    g = torch.Generator().manual_seed(8)
+    for mag in (1.0, 37.5, 1e-3, 900.0):
+        k = (torch.randn(257, 8, 128, generator=g) * mag).to(dtype)
+        v = (torch.randn(257, 8, 128, generator=g) * mag * 0.5).to(dtype)
+        ks = torch.ones(1, device=dev)
+        vs = torch.ones(1, device=dev)
+        A.calibrate_fp8_per_tensor(k.to(dev), v.to(dev), ks, vs)
+        assert float(ks) == R.calibrate_scale_ref(k), (dtype, mag)
+        assert float(vs) == R.calibrate_scale_ref(v), (dtype, mag)
+        # frozen: a second call with other data keeps the scales
+        A.calibrate_fp8_per_tensor((k * 3).to(dev), (v * 3).to(dev), ks, vs)
+        assert float(ks) == R.calibrate_scale_ref(k)
+
+
+def test_calibration_sentinel_and_zero_input(dev):
+    announce("fp8 calibration: sentinel 1.0 and all-zero input")
+    # amax 448 -> scale 1.0, which is the sentinel: the next call calibrates again
+    k = torch.zeros(4, 8, 128, dtype=torch.bfloat16)
+    k[2, 1, 5] = 448.0
+    v = torch.zeros(4, 8, 128, dtype=torch.bfloat16)
+    ks = torch.ones(1, device=dev)
+    vs = torch.ones(1, device=dev)
+    A.calibrate_fp8_per_tensor(k.to(dev), v.to(dev), ks, vs)
+    assert float(ks) == 1.0
+    assert float(vs) == R.calibrate_scale_ref(v)
+    k2 = k * 0.5
+    A.calibrate_fp8_per_tensor(k2.to(dev), v.to(dev), ks, vs)
+    assert float(ks) == R.calibrate_scale_ref(k2)
+    # an fp16 zero input calibrates to 0 exactly as the reference does
+    z = torch.zeros(3, 8, 128, dtype=torch.float16)
+    ks = torch.ones(1, device=dev)
+    vs = torch.ones(1, device=dev)
+    A.calibrate_fp8_per_tensor(z.to(dev), z.to(dev), ks, vs)
+    assert float(ks) == R.calibrate_scale_ref(z) == 0.0
+

@@ -1,0 +1,195 @@
+"""GPU parity of K2 (paged decode attention).
+
+Tolerances (absolute, on the attention output): 2e-3 for fp32 / bf16 / fp16
+KV and 2e-2 for FP8 KV, against the float64 oracle (small cases) or a float32
+torch reference computed on the GPU (batch-256 sizes).
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from conftest import announce
+from mkv import attention as A
+from mkv import workloads as W
+from oracle import reference as R
+
+pytestmark = pytest.mark.gpu
+TOL = {torch.float32: 2e-3, torch.bfloat16: 2e-3, torch.float16: 2e-3, torch.float8_e4m3fn: 2e-2}
+
+
+def _run(dev, q, k, v, bt, ctx, scale, Hq, Hkv, ks=None, vs=None, split_tokens=0):
+    ksd = None if ks is None else torch.tensor([ks], dtype=torch.float32, device=dev)
+    vsd = None if vs is None else torch.tensor([vs], dtype=torch.float32, device=dev)
+    out = A._decode(q.to(dev), k.to(dev), v.to(dev), bt.to(dev), ctx.to(dev), scale, Hq, Hkv, 128,
+                    ksd, vsd, split_tokens=split_tokens)
+    return out.float().cpu()
+
+
+def _oracle(q, k, v, bt, ctx, scale, Hq, Hkv, ks=None, vs=None):
+    return R.paged_decode_ref(q.double(), k, v, bt, ctx, scale, Hq, Hkv, ks, vs).float()
+
+
+def test_decode_small_fp32(dev):
+    announce("decode: batch 4, 16/8 heads, fp32, bs 256, pool 64")
+    w = W.decode_small(seed=1)
+    args = (w["q"], w["k_cache"], w["v_cache"], w["block_tables"], w["context_lens"], w["scale"],
+            w["num_heads"], w["num_kv_heads"])
+    got = _run(dev, *args)
+    want = _oracle(*args)
+    assert (got - want).abs().max().item() <= 2e-3
+
+
+def test_decode_fp8_batch32_over_appended_pool(dev):
+    announce("decode fp8: batch 32, 32/8 heads over the appended 1024-block pool")
+    w = W.decode_fp8_b32(seed=2)
+    N, bs, H = w["num_blocks"], w["block_size"], w["num_kv_heads"]
+    kc = torch.zeros(N, bs, H, 128, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.ones(1, device=dev)
+    vs = torch.ones(1, device=dev)
+    # the per-tensor scales are calibrated on the 4096-token append (outliers
+    # included), then every slot is filled and the append applied with them
+    A.calibrate_fp8_per_tensor(w["key"].to(dev), w["value"].to(dev), ks, vs)
+    A.store_kvcache_fp8(w["fill_key"].to(dev), w["fill_value"].to(dev), kc, vc, ks, vs,
+                        w["fill_slots"].to(dev), bs, "fp8_per_tensor")
+    A.store_kvcache_fp8(w["key"].to(dev), w["value"].to(dev), kc, vc, ks, vs,
+                        w["slot_mapping"].to(dev), bs, "fp8_per_tensor")
+    assert float(ks) == R.calibrate_scale_ref(w["key"])
+    out = A.paged_attention_decode_quantized(
+        w["q"].to(dev), kc, vc, ks, vs, w["block_tables"].to(dev), w["context_lens"].to(dev),
+        w["scale"], w["num_heads"], H, 128, bs, "fp8_per_tensor").float().cpu()
+    kcc, vcc = kc.cpu(), vc.cpu()
+    want = _oracle(w["q"], kcc, vcc, w["block_tables"], w["context_lens"], w["scale"],
+                   w["num_heads"], H, float(ks), float(vs))
+    assert (out - want).abs().max().item() <= 2e-2
+    # against the unquantised bf16 values (information: FP8 storage error)
+    kb = torch.zeros(N * bs, H, 128, dtype=torch.bfloat16)
+    vb = torch.zeros_like(kb)
+    kb[w["fill_slots"]] = w["fill_key"]
+    vb[w["fill_slots"]] = w["fill_value"]
+    ok = w["slot_mapping"] >= 0
+    kb[w["slot_mapping"][ok]] = w["key"][ok]
+    vb[w["slot_mapping"][ok]] = w["value"][ok]
+    exact = _oracle(w["q"], kb.view(N, bs, H, 128), vb.view(N, bs, H, 128), w["block_tables"],
+                    w["context_lens"], w["scale"], w["num_heads"], H)
+    err = (out - exact).abs().max().item()
+    print(f"fp8 decode vs unquantised bf16 cache: max abs err {err:.3e}")
+    assert err < 0.25
+
+
+def _case(seed, B, Hq, Hkv, bs, N, max_blocks, dtype, ctx=None):
+    g = torch.Generator().manual_seed(seed)
+    if ctx is None:
+        ctx = torch.randint(1, max_blocks * bs + 1, (B,), generator=g)
+    bt = W.fragmented_block_tables(ctx, bs, N, g, max_blocks=max_blocks)
+    q = torch.randn(B, Hq, 128, generator=g)
+    k = torch.randn(N, bs, Hkv, 128, generator=g)
+    v = torch.randn(N, bs, Hkv, 128, generator=g)
+    ks = vs = None
+    if dtype == torch.float8_e4m3fn:
+        ks, vs = R.calibrate_scale_ref(k.to(torch.bfloat16)), R.calibrate_scale_ref(v.to(torch.bfloat16))
+        k, v = R.fp8_quantize_ref(k.to(torch.bfloat16), ks), R.fp8_quantize_ref(v.to(torch.bfloat16), vs)
+        q = q.to(torch.bfloat16)
+    else:
+        k, v = k.to(dtype), v.to(dtype)
+        q = q.to(dtype if dtype != torch.float32 else torch.float32)
+    return q, k, v, bt, ctx.to(torch.int64), ks, vs
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn, torch.float32])
+@pytest.mark.parametrize("group", [1, 2, 4, 8, 16])
+def test_decode_group_sizes(dev, dtype, group):
+    announce(f"decode {dtype} group {group}")
+    Hkv = 2
+    q, k, v, bt, ctx, ks, vs = _case(100 + group, 6, Hkv * group, Hkv, 32, 64, 10, dtype)
+    got = _run(dev, q, k, v, bt, ctx, 1 / math.sqrt(128), Hkv * group, Hkv, ks, vs)
+    want = _oracle(q, k, v, bt, ctx, 1 / math.sqrt(128), Hkv * group, Hkv, ks, vs)
+    assert (got - want).abs().max().item() <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn, torch.float32])
+@pytest.mark.parametrize("bs", [16, 32, 128])
+def test_decode_block_sizes_and_edges(dev, dtype, bs):
+    announce(f"decode {dtype} bs {bs} with ctx 0/1/holes")
+    ctx = torch.tensor([0, 1, 2, bs - 1, bs, bs + 1, 5 * bs + 7, 31], dtype=torch.int64)
+    q, k, v, bt, ctx, ks, vs = _case(7 * bs, 8, 8, 2, bs, 80, 6, dtype, ctx=ctx)
+    bt[6, 2] = -1  # an absent block inside a context: its tokens are skipped
+    got = _run(dev, q, k, v, bt, ctx, 0.09, 8, 2, ks, vs)
+    want = _oracle(q, k, v, bt, ctx, 0.09, 8, 2, ks, vs)
+    assert (got - want).abs().max().item() <= TOL[dtype]
+    assert torch.count_nonzero(got[0]) == 0  # context 0 -> zeros
+    got32 = _run(dev, q, k, v, bt, ctx.to(torch.int32), 0.09, 8, 2, ks, vs)
+    assert torch.equal(got, got32)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
+def test_decode_split_count_independence(dev, dtype):
+    announce(f"decode {dtype} split-K sizes")
+    q, k, v, bt, ctx, ks, vs = _case(55, 4, 32, 8, 256, 64, 16, dtype)
+    want = _oracle(q, k, v, bt, ctx, 0.088, 32, 8, ks, vs)
+    outs = []
+    for st in (32, 64, 256, 512, 4096):
+        got = _run(dev, q, k, v, bt, ctx, 0.088, 32, 8, ks, vs, split_tokens=st)
+        assert (got - want).abs().max().item() <= TOL[dtype], st
+        outs.append(got)
+    # deterministic run to run
+    again = _run(dev, q, k, v, bt, ctx, 0.088, 32, 8, ks, vs, split_tokens=256)
+    assert torch.equal(again, outs[2])
+
+
+def test_decode_query_dtypes_over_bf16_and_fp8(dev):
+    announce("decode: fp32 / fp16 queries over bf16 and fp8 caches")
+    for dtype in (torch.bfloat16, torch.float8_e4m3fn):
+        q, k, v, bt, ctx, ks, vs = _case(77, 3, 8, 2, 64, 40, 8, dtype)
+        want = _oracle(q, k, v, bt, ctx, 0.1, 8, 2, ks, vs)
+        for qd in (torch.float32, torch.float16):
+            got = _run(dev, q.to(qd), k, v, bt, ctx, 0.1, 8, 2, ks, vs)
+            assert (got - want).abs().max().item() <= TOL[dtype] + 2e-3
+
+
+def _torch_gpu_reference(q, kc, vc, bt, ctx, scale, Hq, Hkv, ks=None, vs=None):
+    """float32 torch reference on the GPU, one sequence at a time."""
+    bs = kc.shape[1]
+    G = Hq // Hkv
+    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    for b in range(q.shape[0]):
+        L = int(ctx[b])
+        nb = (L + bs - 1) // bs
+        blocks = bt[b, :nb].long()
+        kk = kc[blocks].float().reshape(-1, Hkv, 128)[:L]
+        vv = vc[blocks].float().reshape(-1, Hkv, 128)[:L]
+        if ks is not None:
+            kk = kk * ks
+            vv = vv * vs
+        qq = q[b].float().reshape(Hkv, G, 128)
+        s = torch.matmul(qq, kk.permute(1, 2, 0).contiguous()) * scale  # (Hkv, G, L)
+        p = torch.softmax(s, dim=-1)
+        out[b] = torch.matmul(p, vv.permute(1, 0, 2).contiguous()).reshape(Hq, 128)
+    return out
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_decode_batch256_full_size(dev, kv):
+    announce(f"decode batch 256, 32/8 heads, ctx log-U[512, 8192], {kv} KV")
+    m = W.decode_b256_metadata(seed=3)
+    N, bs = m["num_blocks"], m["block_size"]
+    dtype = torch.bfloat16 if kv == "bf16" else torch.float8_e4m3fn
+    kc = torch.empty(N, bs, 8, 128, dtype=dtype, device=dev)
+    vc = torch.empty_like(kc)
+    ks = vs = None
+    if kv == "fp8":
+        ks, vs = 4.5 / 448, 4.4 / 448
+    W.fill_pool_on_device(kc, 31, ks)
+    W.fill_pool_on_device(vc, 32, vs)
+    g = torch.Generator().manual_seed(33)
+    q = torch.randn(256, 32, 128, generator=g).to(torch.bfloat16).to(dev)
+    bt, ctx = m["block_tables"].to(dev), m["context_lens"].to(dev)
+    ksd = None if ks is None else torch.tensor([ks], device=dev)
+    vsd = None if vs is None else torch.tensor([vs], device=dev)
+    got = A._decode(q, kc, vc, bt, ctx, 1 / math.sqrt(128), 32, 8, 128, ksd, vsd).float()
+    want = _torch_gpu_reference(q, kc, vc, bt, ctx, 1 / math.sqrt(128), 32, 8, ks, vs)
+    err = (got - want).abs().max().item()
+    assert err <= (2e-2 if kv == "fp8" else 2e-3), err

@@ -1,0 +1,250 @@
+"""GPU parity of K3 (chunked-prefill attention over the paged cache and full
+prefill over contiguous K/V), and of the Attention layer's dispatch.
+
+Tolerances (absolute): 2e-3 for bf16 / fp16 KV, 2e-2 for FP8 KV, against the
+float64 oracle (small cases) or a float32 torch reference on the GPU (the
+512-row chunk workload).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+import mkv
+from mkv import attention as A
+from mkv import context as C
+from mkv import workloads as W
+from oracle import reference as R
+
+pytestmark = pytest.mark.gpu
+TOL = {torch.bfloat16: 2e-3, torch.float16: 2e-3, torch.float8_e4m3fn: 2e-2}
+
+
+def _make(seed, prior, qlen, Hq, Hkv, bs, dtype, N=None, holes=()):
+    g = torch.Generator().manual_seed(seed)
+    ctx = torch.tensor([p + n for p, n in zip(prior, qlen)], dtype=torch.int64)
+    need = sum((int(c) + bs - 1) // bs for c in ctx)
+    N = N or need + 3
+    bt = W.fragmented_block_tables(ctx, bs, N, g)
+    for s, j in holes:
+        bt[s, j] = -1
+    cu = torch.zeros(len(qlen) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(qlen), 0).to(torch.int32)
+    pos = torch.tensor([p + j for p, n in zip(prior, qlen) for j in range(n)], dtype=torch.int64)
+    q = torch.randn(int(cu[-1]), Hq, 128, generator=g)
+    k = torch.randn(N, bs, Hkv, 128, generator=g)
+    v = torch.randn(N, bs, Hkv, 128, generator=g)
+    ks = vs = None
+    if dtype == torch.float8_e4m3fn:
+        kb, vb = k.to(torch.bfloat16), v.to(torch.bfloat16)
+        ks, vs = R.calibrate_scale_ref(kb), R.calibrate_scale_ref(vb)
+        k, v = R.fp8_quantize_ref(kb, ks), R.fp8_quantize_ref(vb, vs)
+        q = q.to(torch.bfloat16)
+    else:
+        k, v, q = k.to(dtype), v.to(dtype), q.to(dtype)
+    return q, k, v, bt, ctx, cu, pos, ks, vs
+
+
+def _gpu(dev, q, k, v, bt, ctx, cu, pos, scale, Hq, Hkv, ks, vs):
+    fp8 = k.dtype == torch.float8_e4m3fn
+    ksd = torch.tensor([ks], device=dev) if fp8 else None
+    vsd = torch.tensor([vs], device=dev) if fp8 else None
+    out = A.paged_attention_prefill_triton(
+        q.to(dev), k.to(dev), v.to(dev), bt.to(dev), ctx.to(dev), cu.to(dev), pos.to(dev), scale,
+        Hq, Hkv, 128, k.shape[1], k_scale=ksd, v_scale=vsd,
+        kv_cache_dtype="fp8_per_tensor" if fp8 else "auto")
+    return out.float().cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("group", [1, 2, 4, 8, 16])
+def test_prefill_small_groups(dev, dtype, group):
+    announce(f"prefill {dtype} group {group}")
+    Hkv = 2
+    prior = [0, 37, 130, 5, 0]
+    qlen = [70, 33, 1, 200, 1]
+    q, k, v, bt, ctx, cu, pos, ks, vs = _make(group, prior, qlen, Hkv * group, Hkv, 32, dtype)
+    sc = 1 / math.sqrt(128)
+    got = _gpu(dev, q, k, v, bt, ctx, cu, pos, sc, Hkv * group, Hkv, ks, vs)
+    want = R.paged_prefill_ref(q.double(), k, v, bt, ctx, cu, pos, sc, Hkv * group, Hkv, ks, vs).float()
+    assert (got - want).abs().max().item() <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("bs", [16, 256])
+def test_prefill_block_sizes_holes_and_context_caps(dev, dtype, bs):
+    announce(f"prefill {dtype} bs {bs} holes")
+    prior = [3, 0, 300]
+    qlen = [129, 64, 17]
+    q, k, v, bt, ctx, cu, pos, ks, vs = _make(bs, prior, qlen, 8, 2, bs, dtype, holes=[(2, 0)])
+    ctx2 = ctx.clone()
+    ctx2[0] = 50  # context shorter than some positions: visible = min(ctx, pos + 1)
+    got = _gpu(dev, q, k, v, bt, ctx2, cu, pos, 0.1, 8, 2, ks, vs)
+    want = R.paged_prefill_ref(q.double(), k, v, bt, ctx2, cu, pos, 0.1, 8, 2, ks, vs).float()
+    assert (got - want).abs().max().item() <= TOL[dtype]
+
+
+def _torch_prefill_gpu(q, kc, vc, bt, ctx, cu, pos, scale, Hq, Hkv, ks=None, vs=None):
+    """float32 torch reference on the GPU, one sequence at a time."""
+    bs = kc.shape[1]
+    G = Hq // Hkv
+    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    cuh = cu.tolist()
+    for s in range(len(cuh) - 1):
+        a, b = cuh[s], cuh[s + 1]
+        L = int(ctx[s])
+        nb = (L + bs - 1) // bs
+        blocks = bt[s, :nb].long()
+        kk = kc[blocks].float().reshape(-1, Hkv, 128)[:L]
+        vv = vc[blocks].float().reshape(-1, Hkv, 128)[:L]
+        if ks is not None:
+            kk, vv = kk * ks, vv * vs
+        qq = q[a:b].float().reshape(b - a, Hkv, G, 128).permute(1, 0, 2, 3).reshape(Hkv, (b - a) * G, 128)
+        sc = torch.matmul(qq.contiguous(), kk.permute(1, 2, 0).contiguous()) * scale  # (Hkv, rows*G, L)
+        vis = torch.minimum(pos[a:b] + 1, torch.full_like(pos[a:b], L)).repeat_interleave(G)
+        mask = torch.arange(L, device=q.device)[None, :] < vis[:, None]
+        sc = sc.masked_fill(~mask[None], float("-inf"))
+        o = torch.matmul(torch.softmax(sc, -1), vv.permute(1, 0, 2).contiguous())
+        out[a:b] = o.reshape(Hkv, b - a, G, 128).permute(1, 0, 2, 3).reshape(b - a, Hq, 128)
+    return out
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_prefill_chunk_workload_full_size(dev, kv):
+    announce(f"prefill 8 x 512-row chunks, prior U[0,4096], 32/8 heads, {kv} KV")
+    m = W.prefill_mixed(seed=4, num_decode=0)
+    N, bs = m["num_blocks"], m["block_size"]
+    dtype = torch.bfloat16 if kv == "bf16" else torch.float8_e4m3fn
+    kc = torch.empty(N, bs, 8, 128, dtype=dtype, device=dev)
+    vc = torch.empty_like(kc)
+    ks = W.fill_pool_on_device(kc, 41)
+    vs = W.fill_pool_on_device(vc, 42)
+    g = torch.Generator().manual_seed(43)
+    T = int(m["cu_seqlens_q"][-1])
+    q = torch.randn(T, 32, 128, generator=g).to(torch.bfloat16).to(dev)
+    args = (m["block_tables"].to(dev), m["context_lens"].to(dev), m["cu_seqlens_q"].to(dev),
+            m["positions"].to(dev))
+    sc = 1 / math.sqrt(128)
+    ksd = torch.tensor([ks], device=dev) if ks else None
+    vsd = torch.tensor([vs], device=dev) if vs else None
+    got = A.paged_attention_prefill_triton(q, kc, vc, *args, sc, 32, 8, 128, bs, k_scale=ksd,
+                                           v_scale=vsd, kv_cache_dtype="fp8_per_tensor" if ks else "auto")
+    want = _torch_prefill_gpu(q, kc, vc, *args, sc, 32, 8, ks, vs)
+    err = (got.float() - want).abs().max().item()
+    assert err <= (2e-2 if ks else 2e-3), err
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("group", [1, 4])
+def test_flash_prefill_contiguous(dev, dtype, group):
+    announce(f"flash prefill contiguous {dtype} group {group}")
+    g = torch.Generator().manual_seed(90 + group)
+    lens = [1, 77, 130, 5, 300]
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    T, Hkv = int(cu[-1]), 2
+    q = torch.randn(T, Hkv * group, 128, generator=g).to(dtype)
+    k = torch.randn(T, Hkv, 128, generator=g).to(dtype)
+    v = torch.randn(T, Hkv, 128, generator=g).to(dtype)
+    got = mkv.flash_attention_prefill(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), 0.08,
+                                      Hkv * group, Hkv, 128).float().cpu()
+    want = R.flash_prefill_ref(q.double(), k.double(), v.double(), cu, 0.08, Hkv * group, Hkv).float()
+    assert (got - want).abs().max().item() <= 2e-3
+
+
+def test_chunked_equals_one_shot_and_append_path(dev):
+    announce("prefill: two chunks == one shot; paged(prior 0) == flash prefill")
+    g = torch.Generator().manual_seed(5)
+    n, Hq, Hkv, bs, N = 300, 8, 2, 16, 40
+    q = torch.randn(n, Hq, 128, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(n, Hkv, 128, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(n, Hkv, 128, generator=g).to(torch.bfloat16).to(dev)
+    ctx = torch.tensor([n])
+    bt = W.fragmented_block_tables(ctx, bs, N, g).to(dev)
+    slots = torch.cat([bt[0, t // bs:t // bs + 1].long() * bs + t % bs for t in range(n)])
+    kc = torch.zeros(N, bs, Hkv, 128, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    mkv.store_kvcache(k, v, kc, vc, slots, bs)
+    pos = torch.arange(n, device=dev)
+    one = A.paged_attention_prefill_triton(q, kc, vc, bt, ctx.to(dev), torch.tensor([0, n], dtype=torch.int32, device=dev),
+                                           pos, 0.1, Hq, Hkv, 128, bs)
+    # two chunks of the same sequence as two "sequences" sharing the table
+    cu2 = torch.tensor([0, 123, n], dtype=torch.int32, device=dev)
+    ctx2 = torch.tensor([123, n], device=dev)
+    two = A.paged_attention_prefill_triton(q, kc, vc, bt.repeat(2, 1), ctx2, cu2, pos, 0.1, Hq, Hkv, 128, bs)
+    assert torch.equal(one, two)
+    flash = mkv.flash_attention_prefill(q, k, v, torch.tensor([0, n], dtype=torch.int32, device=dev),
+                                        0.1, Hq, Hkv, 128)
+    assert (one.float() - flash.float()).abs().max().item() <= 2e-3
+
+
+@pytest.mark.parametrize("mode", ["auto", "fp8_per_tensor"])
+def test_attention_layer_mixed_batch(dev, mode):
+    """The Attention layer stores the step's K/V, then routes decode rows to
+    the decode kernel and prefill rows to the prefill kernel."""
+    announce(f"Attention layer mixed batch {mode}")
+    g = torch.Generator().manual_seed(17)
+    Hq, Hkv, bs, N = 8, 2, 16, 64
+    prior = [40, 0, 99, 7]
+    qlen = [1, 50, 1, 20]
+    is_dec = [True, False, True, False]
+    ctx = torch.tensor([p + n for p, n in zip(prior, qlen)])
+    bt = W.fragmented_block_tables(ctx, bs, N, g)
+    cu = torch.zeros(5, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(qlen), 0).to(torch.int32)
+    pos = torch.tensor([p + j for p, n in zip(prior, qlen) for j in range(n)], dtype=torch.int64)
+    seq_of_row = torch.repeat_interleave(torch.arange(4), torch.tensor(qlen))
+    slots = torch.tensor([int(bt[s, int(p) // bs]) * bs + int(p) % bs for s, p in zip(seq_of_row, pos)])
+    T = int(cu[-1])
+    q = torch.randn(T, Hq, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(T, Hkv, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(T, Hkv, 128, generator=g).to(torch.bfloat16)
+    hist_k = torch.randn(N, bs, Hkv, 128, generator=g).to(torch.bfloat16)
+    hist_v = torch.randn(N, bs, Hkv, 128, generator=g).to(torch.bfloat16)
+    layer = A.Attention(Hq, 128, scale=1.0, num_kv_heads=Hkv, block_size=bs)
+    layer.kv_cache_dtype = mode
+    fp8 = mode == "fp8_per_tensor"
+    cdt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+    kcr = torch.zeros(N, bs, Hkv, 128, dtype=cdt)
+    vcr = torch.zeros_like(kcr)
+    ksr, vsr = torch.ones(1), torch.ones(1)
+    all_slots = torch.arange(N * bs)
+    if fp8:
+        R.store_kvcache_fp8_ref(hist_k.view(-1, Hkv, 128), hist_v.view(-1, Hkv, 128), kcr, vcr, ksr, vsr, all_slots)
+        R.store_kvcache_fp8_ref(k, v, kcr, vcr, ksr, vsr, slots)
+    else:
+        R.store_kvcache_ref(hist_k.view(-1, Hkv, 128), hist_v.view(-1, Hkv, 128), kcr, vcr, all_slots)
+        R.store_kvcache_ref(k, v, kcr, vcr, slots)
+    layer.k_cache = torch.zeros(N, bs, Hkv, 128, dtype=cdt, device=dev)
+    layer.v_cache = torch.zeros_like(layer.k_cache)
+    if fp8:
+        layer.k_scale = torch.ones(1, device=dev)
+        layer.v_scale = torch.ones(1, device=dev)
+        A.store_kvcache_fp8(hist_k.view(-1, Hkv, 128).to(dev), hist_v.view(-1, Hkv, 128).to(dev),
+                            layer.k_cache, layer.v_cache, layer.k_scale, layer.v_scale,
+                            all_slots.to(dev), bs, mode)
+    else:
+        A.store_kvcache(hist_k.view(-1, Hkv, 128).to(dev), hist_v.view(-1, Hkv, 128).to(dev),
+                        layer.k_cache, layer.v_cache, all_slots.to(dev), bs)
+    split = C.split_mixed_decode_prefill_metadata(cu.tolist(), qlen, is_dec)
+    split.decode_token_indices_tensor = torch.tensor(split.decode_token_indices, device=dev)
+    split.decode_seq_indices_tensor = torch.tensor(split.decode_seq_indices, device=dev)
+    split.prefill_token_indices_tensor = torch.tensor(split.prefill_token_indices, device=dev)
+    split.prefill_seq_indices_tensor = torch.tensor(split.prefill_seq_indices, device=dev)
+    split.prefill_cu_seqlens_q_tensor = torch.tensor(split.prefill_cu_seqlens_q, dtype=torch.int32, device=dev)
+    C.set_context(True, cu_seqlens_q=cu.to(dev), max_seqlen_q=max(qlen), slot_mapping=slots.to(dev),
+                  context_lens=ctx.to(dev), block_tables=bt.to(dev), positions=pos.to(dev),
+                  mixed_attention_split=split, is_full_prefill=False)
+    try:
+        out = layer(q.to(dev), k.to(dev), v.to(dev)).float().cpu()
+    finally:
+        C.reset_context()
+    assert torch.equal(layer.k_cache.cpu().view(torch.uint8), kcr.view(torch.uint8))
+    ks = float(ksr) if fp8 else None
+    vs = float(vsr) if fp8 else None
+    want = R.paged_prefill_ref(q.double(), kcr, vcr, bt, ctx, cu, pos, 1 / math.sqrt(128), Hq, Hkv, ks, vs)
+    tol = 2e-2 if fp8 else 2e-3
+    assert (out - want.float().reshape(T, Hq * 128)).abs().max().item() <= tol

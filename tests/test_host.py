@@ -1,0 +1,148 @@
+"""CPU tests of the host side: the C-ABI library, the Python wrappers'
+argument handling, the per-step metadata helpers and the workloads.  No
+kernel is launched here (there is no GPU in this environment)."""
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+import torch
+
+from conftest import REPO
+from mkv import _lib
+from mkv import attention as A
+from mkv import context as C
+from mkv import workloads as W
+
+
+def _declared_functions() -> set[str]:
+    text = (REPO / "include" / "mkv.h").read_text()
+    return set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(mkv_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared_functions()
+    for n in ("mkv_kv_append", "mkv_fp8_calibrate_per_tensor", "mkv_paged_decode",
+              "mkv_paged_prefill", "mkv_flash_prefill", "mkv_gather_kv", "mkv_abi_version",
+              "mkv_status_string"):
+        assert n in names
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.mkv_abi_version() == _lib.ABI_VERSION
+
+
+def test_status_strings():
+    lib = _lib.load()
+    for code in range(0, -10, -1):
+        s = lib.mkv_status_string(code).decode()
+        assert s and s != "unknown mkv status"
+    assert lib.mkv_status_string(-1234).decode() == "unknown mkv status"
+
+
+def test_argument_validation_without_launch():
+    """Bad arguments are rejected before any device work is enqueued."""
+    lib = _lib.load()
+    nul = None
+    # null pointers
+    assert lib.mkv_kv_append(nul, 1024, nul, 1024, nul, nul, nul, 4, 8, 128, 16, 4, 1, 3,
+                             nul, nul, nul) == -1
+    # unsupported head_dim / group / block size in decode
+    p = ctypes.c_void_p(16)
+    base = [p, 4096, p, 4096, 1, p, p, 1, 10, nul, nul, p, 4, 4, p, 1, 2]
+    assert lib.mkv_paged_decode(*base, 32, 8, 64, 256, 0.1, 0, nul, 0, nul) == -4
+    assert lib.mkv_paged_decode(*base, 32, 6, 128, 256, 0.1, 0, nul, 0, nul) == -5
+    assert lib.mkv_paged_decode(*base, 32, 8, 128, 100, 0.1, 0, nul, 0, nul) == -6
+    assert lib.mkv_paged_decode(*base, 32, 8, 128, 8, 0.1, 0, nul, 0, nul) == -6
+    # workspace too small for a split-K launch
+    assert lib.mkv_paged_decode(*base, 32, 8, 128, 256, 0.1, 32, p, 16, nul) == -7
+    # zero tokens / batch is a no-op that succeeds
+    assert lib.mkv_kv_append(nul, 1024, nul, 1024, nul, nul, nul, 0, 8, 128, 16, 4, 1, 3,
+                             nul, nul, nul) == 0
+
+
+def test_decode_workspace_and_split_queries():
+    lib = _lib.load()
+    st = lib.mkv_paged_decode_split_tokens(256, 8, 32, 256, 0)
+    assert st % 32 == 0 and 64 <= st <= 512
+    n = lib.mkv_paged_decode_workspace_size(256, 32, 8, 32, 256, 128, 0)
+    splits = (32 * 256 + st - 1) // st
+    assert n == 256 * 32 * splits * 130 * 4
+    # one split covers the table: no workspace
+    assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 1, 256, 128, 512) == 0
+    # small batches split finer
+    assert lib.mkv_paged_decode_split_tokens(4, 8, 8, 256, 0) < st or st == 64
+
+
+def test_wrappers_reject_cpu_tensors_and_unimplemented_modes():
+    k = torch.zeros(2, 8, 128)
+    kc = torch.zeros(1, 16, 8, 128)
+    slots = torch.zeros(2, dtype=torch.int64)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        A.store_kvcache(k, k, kc, kc, slots, 16)
+    with pytest.raises(NotImplementedError):
+        A.store_kvcache_fp8(k, k, kc, kc, None, None, slots, 16, "fp8_per_token_head")
+    with pytest.raises(NotImplementedError):
+        A.paged_attention_decode_quantized(k, kc, kc, None, None, None, None, 0.1, 8, 8, 128, 16,
+                                           "int8_per_token_head")
+    with pytest.raises(AssertionError):
+        A.store_kvcache(k, k, kc, torch.zeros(2, 16, 8, 128), slots, 16)
+    with pytest.raises(AssertionError):
+        A.store_kvcache(k, k, kc, kc, torch.zeros(3, dtype=torch.int64), 16)
+    layer = A.Attention(8, 128, num_kv_heads=8)
+    layer.kv_cache_dtype = "kivi_2bit"
+    with pytest.raises(NotImplementedError):
+        layer(torch.zeros(1, 8, 128), k[:1], k[:1])
+
+
+def test_mixed_split_metadata_matches_reference_rules():
+    cu = [0, 4, 5, 6, 9]
+    qlens = [4, 1, 1, 3]
+    dec = [False, True, True, False]
+    s = C.split_mixed_decode_prefill_metadata(cu, qlens, dec)
+    assert s.decode_token_indices == [4, 5]
+    assert s.decode_seq_indices == [1, 2]
+    assert s.prefill_token_indices == [0, 1, 2, 3, 6, 7, 8]
+    assert s.prefill_seq_indices == [0, 3]
+    assert s.prefill_cu_seqlens_q == [0, 4, 7]
+    t = C.split_mixed_decode_prefill_metadata(torch.tensor(cu), torch.tensor(qlens), torch.tensor(dec))
+    assert t == s
+
+
+def test_context_round_trip():
+    C.set_context(True, cu_seqlens_q=torch.tensor([0, 3]), max_seqlen_q=3, is_full_prefill=True)
+    ctx = C.get_context()
+    assert ctx.is_prefill and ctx.max_seqlen_q == 3 and ctx.is_full_prefill
+    C.reset_context()
+    assert C.get_context() == C.Context()
+
+
+def test_workloads_are_seeded_and_consistent():
+    a, b = W.decode_small(1), W.decode_small(1)
+    assert torch.equal(a["q"], b["q"]) and torch.equal(a["block_tables"], b["block_tables"])
+    bt, ctx = a["block_tables"], a["context_lens"]
+    used = bt[bt >= 0]
+    assert used.unique().numel() == used.numel()  # fragmented but disjoint
+    for i in range(bt.shape[0]):
+        nb = (int(ctx[i]) + 255) // 256
+        assert (bt[i, :nb] >= 0).all() and (bt[i, nb:] == -1).all()
+    m = W.decode_b256_metadata(3)
+    L = m["context_lens"]
+    assert L.min() >= 512 and L.max() < 8192 and 2000 < float(L.float().mean()) < 3600
+    ap = W.append_fp8(2)
+    s = ap["slot_mapping"]
+    v = s[s >= 0]
+    assert v.unique().numel() == v.numel() and 0.03 < float((s < 0).float().mean()) < 0.07
+    pm = W.prefill_mixed(4)
+    assert int(pm["cu_seqlens_q"][-1]) == 8 * 512 + 120 == pm["positions"].numel()
+
+
+def test_algorithmic_bytes():
+    ctx = torch.tensor([512, 1000])
+    n = W.alg_bytes_decode(ctx, 256, 32, 8, kv_bytes=1)
+    assert n == 1512 * 8 * 128 * 2 + 2 * 32 * 128 * 4 + (2 + 4) * 4 + 2 * 8
