@@ -48,9 +48,15 @@ def parse_args():
     ap.add_argument("--kv", choices=["fp8", "bf16"], default="fp8")
     ap.add_argument("--layers", type=int, default=8, help="distinct layer pools rotated per step")
     ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--batch", type=int, default=256)
+    ap.add_argument("--num-heads", type=int, default=32)
+    ap.add_argument("--num-kv-heads", type=int, default=8)
     ap.add_argument("--cpu-seqs", type=int, default=16,
                     help="sequences in the CPU-baseline sample (0 = skip the CPU baseline)")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary measurements")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (5 times) and exit; "
+                         "its rocprofv3 FETCH_SIZE/WRITE_SIZE calibrate the PMC byte counts")
     return ap.parse_args()
 
 
@@ -159,19 +165,30 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    meta = W.decode_b256_metadata(seed=3)
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
+        return 0
+    meta = W.decode_b256_metadata(seed=3, batch=args.batch,
+                                  num_blocks=max(4096, 16 * args.batch))
     N, bs = meta["num_blocks"], meta["block_size"]
     kv_dtype = torch.float8_e4m3fn if args.kv == "fp8" else torch.bfloat16
     layers = []
     for l in range(args.layers):
-        kc = torch.empty(N, bs, 8, HEAD_DIM, dtype=kv_dtype, device=dev)
+        kc = torch.empty(N, bs, args.num_kv_heads, HEAD_DIM, dtype=kv_dtype, device=dev)
         vc = torch.empty_like(kc)
         ks = W.fill_pool_on_device(kc, 1000 + 2 * l)
         vs = W.fill_pool_on_device(vc, 1001 + 2 * l)
         sc = (torch.tensor([ks], device=dev), torch.tensor([vs], device=dev)) if ks else (None, None)
         layers.append((kc, vc, sc, (ks, vs) if ks else None))
     g = torch.Generator().manual_seed(3)
-    q = torch.randn(256, 32, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    Hq, Hkv = args.num_heads, args.num_kv_heads
+    q = torch.randn(args.batch, Hq, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
     bt = meta["block_tables"].to(dev)
     ctx = meta["context_lens"].to(dev)
     out = torch.empty_like(q)
@@ -180,16 +197,16 @@ def main() -> int:
 
     def step(i):
         kc, vc, (ksd, vsd), _ = layers[i % len(layers)]
-        A._decode(q, kc, vc, bt, ctx, sm, 32, 8, HEAD_DIM, ksd, vsd,
+        A._decode(q, kc, vc, bt, ctx, sm, Hq, Hkv, HEAD_DIM, ksd, vsd,
                   split_tokens=args.split_tokens, out=out)
 
-    nbytes = W.alg_bytes_decode(meta["context_lens"], bs, 32, 8, kv_bytes=kv_dtype.itemsize)
+    nbytes = W.alg_bytes_decode(meta["context_lens"], bs, Hq, Hkv, kv_bytes=kv_dtype.itemsize)
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
     ms = time_launches(step, args.steps, args.warmup, stream)
     t_wall = time.perf_counter() - t_wall
     gbps = nbytes / (ms * 1e-3) / 1e9
-    split = mkv._lib.query("mkv_paged_decode_split_tokens", 256, 8, meta["max_blocks"], bs,
+    split = mkv._lib.query("mkv_paged_decode_split_tokens", args.batch, Hkv, meta["max_blocks"], bs,
                            args.split_tokens)
 
     result = {
@@ -206,12 +223,12 @@ def main() -> int:
         "dtype": "fp8" if args.kv == "fp8" else "bf16",
         "data": "synthetic (seeded N(0,1) KV pools and queries, seeded context lengths/tables)",
         "config": {
-            "workload": ("paged decode attention, batch 256, 32 q / 8 kv heads, head_dim 128, "
+            "workload": (f"paged decode attention, batch {args.batch}, {Hq} q / {Hkv} kv heads, head_dim 128, "
                          f"block 256, ctx floor(exp(U(ln512, ln8192))) sum {int(meta['context_lens'].sum())}, "
-                         f"fragmented tables over 4096 blocks, {args.kv} KV "
+                         f"fragmented tables over {N} blocks, {args.kv} KV "
                          f"({'per-tensor e4m3fn' if args.kv == 'fp8' else 'bf16'}), bf16 q/out, "
                          f"{args.layers} rotating layer pools"),
-            "batch": 256, "num_heads": 32, "num_kv_heads": 8, "head_dim": HEAD_DIM,
+            "batch": args.batch, "num_heads": Hq, "num_kv_heads": Hkv, "head_dim": HEAD_DIM,
             "block_size": bs, "split_tokens": split, "algorithmic_bytes_per_step": nbytes,
         },
         "roofline": {

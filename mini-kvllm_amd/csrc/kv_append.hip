@@ -56,11 +56,17 @@ MKV_DEV u32x4 quantize16(const void* row, int64_t e, float scale) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     // IEEE fp32 divide (correctly rounded), then torch.clamp, then RNE cast.
-    const float a = clamp_fp8_range(x[4 * i + 0] / scale);
-    const float b = clamp_fp8_range(x[4 * i + 1] / scale);
-    const float c = clamp_fp8_range(x[4 * i + 2] / scale);
-    const float d = clamp_fp8_range(x[4 * i + 3] / scale);
-    out[i] = pack_fp8x4(a, b, c, d);
+    float v[4];
+    uint32_t nan_bits = 0, nan_signs = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float qv = x[4 * i + j] / scale;
+      nan_bits |= (qv != qv ? 0x80u : 0u) << (8 * j);
+      nan_signs |= div_nan_sign(x[4 * i + j], scale, qv) << (8 * j + 7);
+      v[j] = clamp_fp8_range(qv);
+    }
+    // NaN bytes: keep the converter's S.1111.111 payload, replace its sign.
+    out[i] = (pack_fp8x4(v[0], v[1], v[2], v[3]) & ~nan_bits) | nan_signs;
   }
   return out;
 }

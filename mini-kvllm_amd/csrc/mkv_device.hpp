@@ -87,19 +87,27 @@ MKV_DEV float clamp_fp8_range(float v) {
   return v;
 }
 
-// Sign bit of a NaN input moved to bit 7 of byte k (0 for non-NaN inputs).
-MKV_DEV uint32_t nan_sign_byte(float v, int k) {
-  return (v != v) ? ((__float_as_uint(v) >> 31) << (8 * k + 7)) : 0u;
-}
-
 // Four fp32 values (already within +-448 or NaN) -> four e4m3fn bytes packed
-// little-endian, rounding to nearest even (v_cvt_pk_fp8_f32).  The converter
-// emits one canonical NaN; the input's sign is kept on NaN bytes so that the
-// result equals torch's cast (S.1111.111).
+// little-endian, rounding to nearest even (v_cvt_pk_fp8_f32).  A NaN input
+// gives a NaN byte (low 7 bits 0x7f) whose sign is the converter's own;
+// callers that need a particular NaN sign overwrite bit 7.
 MKV_DEV uint32_t pack_fp8x4(float a, float b, float c, float d) {
   uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
-  return w | nan_sign_byte(a, 0) | nan_sign_byte(b, 1) | nan_sign_byte(c, 2) | nan_sign_byte(d, 3);
+  return w;
+}
+
+// Sign of the NaN that an IEEE fp32 division x / s yields on the host CPU
+// (x86 SSE, where torch's reference cast runs): a NaN operand is returned
+// quieted with its sign (x first, then s); an invalid operation (0/0,
+// inf/inf) returns the default NaN, whose sign bit is set.  The GPU divide
+// returns a positive canonical NaN instead, so the quantiser restores this
+// sign explicitly.  Returns 0 when x / s is not NaN.
+MKV_DEV uint32_t div_nan_sign(float x, float s, float q) {
+  if (q == q) return 0u;
+  if (x != x) return __float_as_uint(x) >> 31;
+  if (s != s) return __float_as_uint(s) >> 31;
+  return 1u;
 }
 
 // Two e4m3fn bytes (low or high half-word of w) -> exact fp16 pair.

@@ -57,6 +57,9 @@ struct DecodeArgs {
   int max_splits;
   float* ws_acc;  // [batch * num_heads][max_splits][head_dim]
   float* ws_ml;   // [batch * num_heads][max_splits][2]  (m, l), log2 domain
+  // stream-K decomposition (16-bit KV): partial slots per wave and metadata
+  int* sk_meta;   // [batch + 1] tile prefix per sequence, then tiles_per_wave
+  int num_waves;  // persistent waves in the grid
 };
 
 MKV_DEV float wave_max(float v) {
@@ -117,11 +120,12 @@ MKV_DEV void store_out8(void* out, int dt, int64_t off, const float* x) {
 
 struct WorkItem {
   int b, kvh, split, num_splits;
-  int64_t t_begin, t_end;
+  int t_begin, t_end;  // token range of this split (context lengths fit in 31 bits)
 };
 
 // Decode the flat work index; returns false if the item has nothing to do.
 // A sequence with context length 0 keeps split 0 so that zeros get written.
+// w must be wave-uniform so that everything derived from it stays scalar.
 MKV_DEV bool decode_work_item(const DecodeArgs& a, int64_t w, WorkItem& it) {
   const int64_t per_split = (int64_t)a.batch * a.num_kv_heads;
   if (w >= per_split * a.max_splits) return false;
@@ -134,9 +138,13 @@ MKV_DEV bool decode_work_item(const DecodeArgs& a, int64_t w, WorkItem& it) {
   L = L < 0 ? 0 : (L > cap ? cap : L);
   it.num_splits = L > 0 ? (int)((L + a.split_tokens - 1) / a.split_tokens) : 1;
   if (it.split >= it.num_splits) return false;
-  it.t_begin = (int64_t)it.split * a.split_tokens;
-  it.t_end = it.t_begin + a.split_tokens < L ? it.t_begin + a.split_tokens : L;
+  it.t_begin = it.split * a.split_tokens;
+  it.t_end = (int)(it.t_begin + a.split_tokens < L ? it.t_begin + a.split_tokens : L);
   return true;
+}
+
+MKV_DEV int64_t wave_work_index() {
+  return (int64_t)blockIdx.x * kDecWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 }
 
 // Final normalisation / partial write for one wave.  Lane (kg, c) holds
@@ -181,49 +189,104 @@ MKV_DEV void finish_item(const DecodeArgs& a, const WorkItem& it, f32x4 (&acc)[8
 // ---------------------------------------------------------------------------
 // 16-bit MFMA kernel: KV in FP8 (via exact fp16), bf16 or fp16.
 // ---------------------------------------------------------------------------
-template <int KV_DT>
-struct Tile16 {
-  // K: 2 token sub-tiles x 32 dims; V: 8 tokens x 8 dims.
-  static constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
-  static constexpr int kKVec = (32 * kEb) / 16;  // 16-byte loads per K row chunk
-  u32x4 k[2][kKVec];
-  typename std::conditional<kEb == 1, u32x2, u32x4>::type v[8];
-  int64_t phys[2];
+// Raw-buffer descriptor word 3 for gfx9-class targets (untyped 32-bit data).
+constexpr int kRsrcFlags = 0x00020000;
+// A per-lane buffer offset beyond every descriptor's range: the load returns 0.
+constexpr uint32_t kOob = 0x80000000u;
+// Cache policy of K/V loads: default (measured faster than the non-temporal
+// hint on this path).
+constexpr int kStreamAux = 0;
+
+// Descriptor over the rows of one block that start at `row` (token offset in
+// the block) for one KV head: [base, end of block).  An absent block (phys <
+// 0) gets an empty range, so every load through it returns zeros.  All inputs
+// are wave-uniform.
+MKV_DEV __amdgpu_buffer_rsrc_t rows_rsrc(const char* pool, int64_t phys, int64_t blk_bytes,
+                                        int64_t off_in_blk) {
+  // selects, not branches: a branch here would split the load sequence and
+  // make the wait-count pass drain the prefetch at the join
+  const bool ok = phys >= 0;
+  const char* base = pool + (ok ? phys * blk_bytes + off_in_blk : 0);
+  const int num = ok ? (int)(blk_bytes - off_in_blk) : 0;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, num, kRsrcFlags);
+}
+
+// Per work item constants of the tile loads.
+struct ItemLoad {
+  int my_phys;   // lane i: physical block of logical block blk0 + i (-1 if absent)
+  int blk0;      // first logical block of the split
+  int k_voff;    // lane byte offset of its K row chunk inside a 16-token group
+  int v_voff;    // lane byte offset of its V row chunk (token 4kg, dims 8c..)
+  int row_bytes; // bytes per token row (all KV heads)
+  int64_t blk_bytes;
+  int64_t head_bytes;  // byte offset of this KV head inside a token row
 };
 
 template <int KV_DT>
-MKV_DEV void load_tile16(const DecodeArgs& a, const WorkItem& it, int64_t t0, Tile16<KV_DT>& T) {
+MKV_DEV ItemLoad item_load_setup(const DecodeArgs& a, const WorkItem& it) {
   constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
-  const int64_t bs_mask = (int64_t(1) << a.idx.bs_log2) - 1;
+  ItemLoad L;
+  L.blk0 = it.t_begin >> a.idx.bs_log2;
+  const int nblk = it.t_end > it.t_begin ? ((it.t_end - 1) >> a.idx.bs_log2) - L.blk0 + 1 : 0;
+  L.my_phys = lane < nblk ? (int)a.idx.physical_block(it.b, L.blk0 + lane) : -1;
+  L.row_bytes = (int)(a.idx.row_elems * kEb);
+  L.blk_bytes = (int64_t)L.row_bytes << a.idx.bs_log2;
+  L.head_bytes = (int64_t)it.kvh * kHeadDim * kEb;
+  L.k_voff = c * L.row_bytes + 32 * kg * kEb;
+  L.v_voff = 4 * kg * L.row_bytes + 8 * c * kEb;
+  return L;
+}
+
+template <int KV_DT>
+struct Tile16 {
+  // K: 2 sub-tiles of 16 tokens x 32 dims per lane; V: 8 tokens x 8 dims.
+  static constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
+  static constexpr int kKVec = (32 * kEb) / 16;  // 16-byte loads per K row chunk
+  using VT = typename std::conditional<kEb == 1, u32x2, u32x4>::type;
+  u32x4 k[2][kKVec];
+  VT v[8];
+  bool ok[2];  // sub-tile block present
+};
+
+// Issue every load of the 32-token tile starting at t0 (wave-uniform).  Tokens
+// past the split end and absent blocks read as zeros; no branches.
+template <int KV_DT>
+MKV_DEV void load_tile16(const DecodeArgs& a, const WorkItem& it, const ItemLoad& L, int t0,
+                         Tile16<KV_DT>& T) {
+  constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+  const int bs_mask = (1 << a.idx.bs_log2) - 1;
+  __amdgpu_buffer_rsrc_t rk[2], rv[2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) T.phys[h] = a.idx.physical_block(it.b, (t0 + 16 * h) >> a.idx.bs_log2);
-  const int64_t head_off = (int64_t)it.kvh * kHeadDim;
-  // K rows: token t0 + 16m + c, dims 32kg .. 32kg+31.
+  for (int h = 0; h < 2; ++h) {
+    const int th = t0 + 16 * h;
+    int slot = (th >> a.idx.bs_log2) - L.blk0;
+    slot = slot > 63 ? 63 : slot;
+    const int64_t phys = __builtin_amdgcn_readlane(L.my_phys, slot);
+    const int64_t off = L.head_bytes + (int64_t)(th & bs_mask) * L.row_bytes;
+    rk[h] = rows_rsrc(a.k_cache, phys, L.blk_bytes, off);
+    rv[h] = rows_rsrc(a.v_cache, phys, L.blk_bytes, off);
+    T.ok[h] = phys >= 0;
+  }
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
-    const int64_t t = t0 + 16 * m + c;
-    const bool ok = t < it.t_end && T.phys[m] >= 0;
-    const int64_t base =
-        (((T.phys[m] << a.idx.bs_log2) + (t & bs_mask)) * a.idx.row_elems + head_off + 32 * kg) * kEb;
+    const uint32_t off = (t0 + 16 * m + c < it.t_end) ? (uint32_t)L.k_voff : kOob;
 #pragma unroll
     for (int i = 0; i < Tile16<KV_DT>::kKVec; ++i)
-      T.k[m][i] = ok ? ld16_stream(a.k_cache + base + 16 * i) : u32x4{0, 0, 0, 0};
+      T.k[m][i] = __builtin_amdgcn_raw_buffer_load_b128(rk[m], off + 16 * i, 0, kStreamAux);
   }
-  // V rows: token t0 + 16(i/4) + 4kg + (i%4), dims 8c .. 8c+7.
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int hf = i >> 2;
-    const int64_t t = t0 + 16 * hf + 4 * kg + (i & 3);
-    const bool ok = t < it.t_end && T.phys[hf] >= 0;
-    const int64_t base =
-        (((T.phys[hf] << a.idx.bs_log2) + (t & bs_mask)) * a.idx.row_elems + head_off + 8 * c) * kEb;
-    if constexpr (kEb == 1) {
-      T.v[i] = ok ? ld8_stream(a.v_cache + base) : u32x2{0, 0};
-    } else {
-      T.v[i] = ok ? ld16_stream(a.v_cache + base) : u32x4{0, 0, 0, 0};
-    }
+    const int hf = i >> 2, r = i & 3;
+    const uint32_t off = (t0 + 16 * hf + 4 * kg + r < it.t_end)
+                             ? (uint32_t)(L.v_voff + r * L.row_bytes) : kOob;
+    if constexpr (kEb == 1)
+      T.v[i] = __builtin_amdgcn_raw_buffer_load_b64(rv[hf], off, 0, kStreamAux);
+    else
+      T.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv[hf], off, 0, kStreamAux);
   }
 }
 
@@ -298,18 +361,84 @@ MKV_DEV void v_operands(const Tile16<KV_DT>& T, Op16<KV_DT> (&B)[8]) {
   }
 }
 
+// One 32-token tile: S^T = K q^T, online softmax (log2 domain), O += P V.
+// t0: first token of the tile, t_end: end of the visible range.
 template <int KV_DT>
-__global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(DecodeArgs a) {
+MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const Op16<KV_DT> (&qop)[4],
+                            float score_mul, f32x4 (&acc)[8], float& m_run, float& l_run) {
+  const int lane = threadIdx.x & 63;
+  const int kg = lane >> 4;
+  // S^T = K q^T: lane holds scores of tokens t0 + 16m + 4kg + r for head c.
+  f32x4 s[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    s[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) s[m] = mfma16<KV_DT>(k_operand<KV_DT>(cur, m, st), qop[st], s[m]);
+  }
+  float mx = kNegBig;
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok = t0 + 16 * m + 4 * kg + r < t_end && cur.ok[m];
+      s[m][r] = ok ? s[m][r] * score_mul : -__builtin_huge_valf();
+      mx = fmaxf(mx, s[m][r]);
+    }
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float m_new = fmaxf(m_run, mx);
+  const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+  m_run = m_new;
+  float p[8];
+  float psum = 0.0f;
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[4 * m + r] = __builtin_amdgcn_exp2f(s[m][r] - m_new);
+      psum += p[4 * m + r];
+    }
+  }
+  l_run = l_run * alpha + psum;
+  // Rescale the output accumulators of heads 4kg + r.
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float ar = __shfl(alpha, 4 * kg + r);
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) acc[mm][r] *= ar;
+    }
+  }
+  const Op16<KV_DT> pop = to_op16<KV_DT>(p);
+  Op16<KV_DT> vop[8];
+  v_operands<KV_DT>(cur, vop);
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm) acc[mm] = mfma16<KV_DT>(pop, vop[mm], acc[mm]);
+  if constexpr (KV_DT == MKV_DTYPE_BF16) {
+    // bf16 keeps 8 significant bits of P; add the rounding residual as a
+    // second bf16 term so P carries ~16 bits like the fp32 reference.
+    float plo[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) plo[j] = p[j] - (float)pop[j];
+    const Op16<KV_DT> plop = to_op16<KV_DT>(plo);
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm) acc[mm] = mfma16<KV_DT>(plop, vop[mm], acc[mm]);
+  }
+}
+
+// q of head c of the group, dims 32kg .. 32kg+31 (zero for padding heads),
+// as MFMA operands; returns the fp32 factor that maps MFMA scores to the
+// log2-domain logits.  fp16 operands are normalised by a power of two so q is
+// exact and in range; k_scale (FP8) and sm_scale*log2(e) stay in fp32.
+template <int KV_DT>
+MKV_DEV float load_q_operands(const DecodeArgs& a, int b, int kvh, Op16<KV_DT> (&qop)[4]) {
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
-  WorkItem it;
-  if (!decode_work_item(a, (int64_t)blockIdx.x * kDecWaves + (threadIdx.x >> 6), it)) return;
-
-  // q of head c, dims 32kg .. 32kg+31 (zero for padding heads c >= G).
   float qf[32];
-  const int hq = it.kvh * a.group + c;
   if (c < a.group) {
-    const int64_t qoff = (int64_t)it.b * a.q_stride + (int64_t)hq * kHeadDim + 32 * kg;
+    const int64_t qoff = (int64_t)b * a.q_stride + (int64_t)(kvh * a.group + c) * kHeadDim + 32 * kg;
 #pragma unroll
     for (int i = 0; i < 4; ++i) load_q8(a.q, a.q_dtype, qoff + 8 * i, qf + 8 * i);
   } else {
@@ -319,8 +448,6 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(D
   float score_mul = a.sm_scale * kLog2e;
   if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) score_mul *= *a.k_scale;
   if constexpr (KV_DT != MKV_DTYPE_BF16) {
-    // Normalise q by a power of two so that fp16 holds it without overflow;
-    // the factor is undone on the fp32 scores.
     float qm = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) qm = fmaxf(qm, fabsf(qf[i]));
@@ -333,77 +460,42 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(D
       score_mul *= ldexpf(1.0f, e - 8);
     }
   }
-  Op16<KV_DT> qop[4];
 #pragma unroll
   for (int st = 0; st < 4; ++st) qop[st] = to_op16<KV_DT>(qf + 8 * st);
+  return score_mul;
+}
+
+template <int KV_DT>
+__global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(DecodeArgs a) {
+  WorkItem it;
+  if (!decode_work_item(a, wave_work_index(), it)) return;
+  Op16<KV_DT> qop[4];
+  const float score_mul = load_q_operands<KV_DT>(a, it.b, it.kvh, qop);
 
   f32x4 acc[8];
 #pragma unroll
   for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegBig, l_run = 0.0f;
 
-  for (int64_t t0 = it.t_begin; t0 < it.t_end; t0 += 32) {
-    Tile16<KV_DT> cur;
-    load_tile16<KV_DT>(a, it, t0, cur);
 
-    // S^T = K q^T: lane holds scores of tokens t0 + 16m + 4kg + r for head c.
-    f32x4 s[2];
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      s[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int st = 0; st < 4; ++st) s[m] = mfma16<KV_DT>(k_operand<KV_DT>(cur, m, st), qop[st], s[m]);
-    }
-    float mx = kNegBig;
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t t = t0 + 16 * m + 4 * kg + r;
-        const bool ok = t < it.t_end && cur.phys[m] >= 0;
-        s[m][r] = ok ? s[m][r] * score_mul : -__builtin_huge_valf();
-        mx = fmaxf(mx, s[m][r]);
-      }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
-    float p[8];
-    float psum = 0.0f;
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[4 * m + r] = __builtin_amdgcn_exp2f(s[m][r] - m_new);
-        psum += p[4 * m + r];
-      }
-    }
-    l_run = l_run * alpha + psum;
-    // Rescale the output accumulators of heads 4kg + r.
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float ar = __shfl(alpha, 4 * kg + r);
-#pragma unroll
-        for (int mm = 0; mm < 8; ++mm) acc[mm][r] *= ar;
-      }
-    }
-    const Op16<KV_DT> pop = to_op16<KV_DT>(p);
-    Op16<KV_DT> vop[8];
-    v_operands<KV_DT>(cur, vop);
-#pragma unroll
-    for (int mm = 0; mm < 8; ++mm) acc[mm] = mfma16<KV_DT>(pop, vop[mm], acc[mm]);
-    if constexpr (KV_DT == MKV_DTYPE_BF16) {
-      // bf16 keeps 8 significant bits of P; add the rounding residual as a
-      // second bf16 term so P carries ~16 bits like the fp32 reference.
-      float plo[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) plo[j] = p[j] - (float)pop[j];
-      const Op16<KV_DT> plop = to_op16<KV_DT>(plo);
-#pragma unroll
-      for (int mm = 0; mm < 8; ++mm) acc[mm] = mfma16<KV_DT>(plop, vop[mm], acc[mm]);
+  // Software pipeline over two register tiles: the loads of tile i+1 are in
+  // flight while tile i is computed.  The prefetch is unconditional (a tile
+  // past the split end reads zeros through the descriptor range check and
+  // touches no memory), so no branch splits the load stream and the waits
+  // before tile i only cover tile i's loads.
+  if (it.t_begin < it.t_end) {
+    const ItemLoad L = item_load_setup<KV_DT>(a, it);
+    Tile16<KV_DT> ta, tb;
+    load_tile16<KV_DT>(a, it, L, it.t_begin, ta);
+    for (int t0 = it.t_begin;;) {
+      load_tile16<KV_DT>(a, it, L, t0 + 32, tb);
+      compute_tile16<KV_DT>(ta, t0, it.t_end, qop, score_mul, acc, m_run, l_run);
+      t0 += 32;
+      if (t0 >= it.t_end) break;
+      load_tile16<KV_DT>(a, it, L, t0 + 32, ta);
+      compute_tile16<KV_DT>(tb, t0, it.t_end, qop, score_mul, acc, m_run, l_run);
+      t0 += 32;
+      if (t0 >= it.t_end) break;
     }
   }
   float l_col = l_run + __shfl_xor(l_run, 16);
@@ -413,13 +505,329 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(D
 }
 
 // ---------------------------------------------------------------------------
+// Stream-K decode (16-bit MFMA path, the default).
+//
+// The work is one global stream of 32-token tiles: sequence by sequence, KV
+// head by KV head, the ceil(L/32) tiles of every (sequence, KV head) item.
+// A persistent grid of W waves splits the stream into W equal contiguous
+// ranges, so every wave streams the same number of bytes whatever the
+// context-length skew, and its load pipeline runs across item boundaries
+// (the next tile's block-table entry and K/V are always in flight).  An item
+// cut by a range boundary writes (acc, m, l) partials to slot (wave, 0) if it
+// began at or before the wave's range, else (wave, 1); the merge kernel
+// combines them.  Sequences with no visible token are written as zeros by
+// the merge kernel.
+// ---------------------------------------------------------------------------
+constexpr int kTileTok = 32;
+constexpr int kStreamMaxBatch = 8192;
+constexpr size_t kStreamMaxLds = (2 * kStreamMaxBatch + 1) * sizeof(int);
+
+struct Cursor {
+  int b, kvh, t;  // item (sequence, KV head) and tile index inside the item
+  int n, L;       // tiles of the item, visible tokens of the sequence
+};
+
+MKV_DEV int lds_uniform(const int* p, int i) { return __builtin_amdgcn_readfirstlane(p[i]); }
+
+// Position of global tile g (pre: per-sequence tile prefix, lens: lengths).
+MKV_DEV Cursor cursor_at(const int* pre, const int* lens, int B, int Hkv, int64_t g) {
+  int lo = 0, hi = B;  // largest b with pre[b] * Hkv <= g; that b has tiles
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if ((int64_t)lds_uniform(pre, mid) * Hkv <= g) lo = mid; else hi = mid;
+  }
+  Cursor c;
+  c.b = lo;
+  const int p0 = lds_uniform(pre, lo);
+  c.n = lds_uniform(pre, lo + 1) - p0;
+  const int64_t r = g - (int64_t)p0 * Hkv;
+  c.kvh = (int)(r / c.n);
+  c.t = (int)(r - (int64_t)c.kvh * c.n);
+  c.L = lds_uniform(lens, lo);
+  return c;
+}
+
+MKV_DEV void cursor_next(Cursor& c, const int* pre, const int* lens, int B, int Hkv) {
+  if (++c.t < c.n) return;
+  c.t = 0;
+  if (++c.kvh < Hkv) return;
+  c.kvh = 0;
+  do {
+    ++c.b;
+  } while (c.b < B && lds_uniform(pre, c.b + 1) == lds_uniform(pre, c.b));
+  if (c.b < B) {
+    c.n = lds_uniform(pre, c.b + 1) - lds_uniform(pre, c.b);
+    c.L = lds_uniform(lens, c.b);
+  } else {  // past the stream: an empty item whose loads read nothing
+    c.b = B - 1;
+    c.n = 1;
+    c.L = 0;
+  }
+}
+
+struct PhysPair {
+  int64_t p[2];
+};
+
+// Block-table entries of the two 16-token halves of tile c (scalar loads).
+MKV_DEV PhysPair tile_phys(const DecodeArgs& a, const Cursor& c) {
+  PhysPair ph;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int tok = c.t * kTileTok + 16 * h;
+    ph.p[h] = tok < c.L ? a.idx.physical_block(c.b, tok >> a.idx.bs_log2) : -1;
+  }
+  return ph;
+}
+
+// Issue the K/V loads of tile c (same lane mapping as load_tile16).
+template <int KV_DT>
+MKV_DEV void load_tile_sk(const DecodeArgs& a, const Cursor& c, const PhysPair& ph, int row_bytes,
+                          int64_t blk_bytes, int k_voff, int v_voff, Tile16<KV_DT>& T) {
+  constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
+  const int lane = threadIdx.x & 63;
+  const int cc = lane & 15, kg = lane >> 4;
+  const int bs_mask = (1 << a.idx.bs_log2) - 1;
+  const int t0 = c.t * kTileTok;
+  const int64_t head_bytes = (int64_t)c.kvh * kHeadDim * kEb;
+  __amdgpu_buffer_rsrc_t rk[2], rv[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t off = head_bytes + (int64_t)((t0 + 16 * h) & bs_mask) * row_bytes;
+    rk[h] = rows_rsrc(a.k_cache, ph.p[h], blk_bytes, off);
+    rv[h] = rows_rsrc(a.v_cache, ph.p[h], blk_bytes, off);
+    T.ok[h] = ph.p[h] >= 0;
+  }
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const uint32_t off = (t0 + 16 * m + cc < c.L) ? (uint32_t)k_voff : kOob;
+#pragma unroll
+    for (int i = 0; i < Tile16<KV_DT>::kKVec; ++i)
+      T.k[m][i] = __builtin_amdgcn_raw_buffer_load_b128(rk[m], off + 16 * i, 0, kStreamAux);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int hf = i >> 2, r = i & 3;
+    const uint32_t off =
+        (t0 + 16 * hf + 4 * kg + r < c.L) ? (uint32_t)(v_voff + r * row_bytes) : kOob;
+    if constexpr (kEb == 1)
+      T.v[i] = __builtin_amdgcn_raw_buffer_load_b64(rv[hf], off, 0, kStreamAux);
+    else
+      T.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv[hf], off, 0, kStreamAux);
+  }
+}
+
+// Write the finished item of cursor c: the normalised output if the whole item
+// ran in this wave, else a partial in slot (wave, k).
+MKV_DEV void finish_sk(const DecodeArgs& a, const Cursor& c, bool whole, int w, int k,
+                       f32x4 (&acc)[8], float m_col, float l_col, float v_mul) {
+  const int lane = threadIdx.x & 63;
+  const int cc = lane & 15, kg = lane >> 4;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * kg + r;
+    const float lh = __shfl(l_col, h);
+    const float mh = __shfl(m_col, h);
+    if (h >= a.group) continue;
+    if (whole) {
+      const float inv = lh > 0.0f ? v_mul / lh : 0.0f;
+      float x[8];
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) x[mm] = acc[mm][r] * inv;
+      const int hq = c.kvh * a.group + h;
+      store_out8(a.out, a.q_dtype, (int64_t)c.b * a.out_stride + (int64_t)hq * kHeadDim + 8 * cc, x);
+    } else {
+      const int64_t slot = ((int64_t)w * 2 + k) * a.group + h;
+      float* p = a.ws_acc + slot * kHeadDim + 8 * cc;
+      u32x4 lo, hi;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        lo[j] = __float_as_uint(acc[j][r]);
+        hi[j] = __float_as_uint(acc[4 + j][r]);
+      }
+      st16(p, lo);
+      st16(p + 4, hi);
+      if (cc == 0) {
+        a.ws_ml[slot * 2] = mh;
+        a.ws_ml[slot * 2 + 1] = lh;
+      }
+    }
+  }
+}
+
+// Per-sequence tile counts and their prefix into LDS (every workgroup does it;
+// workgroup 0 also publishes them for the merge kernel).  Returns the tiles
+// per wave.
+MKV_DEV int stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
+  __shared__ int part[kDecWaves * kWave];
+  const int tid = threadIdx.x;
+  const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
+  int running = 0;
+  for (int base = 0; base < a.batch; base += kDecWaves * kWave) {
+    const int b = base + tid;
+    int n = 0;
+    if (b < a.batch) {
+      int64_t L = load_index(a.context_lens, b, a.ctx_i64);
+      L = L < 0 ? 0 : (L > cap ? cap : L);
+      lens[b] = (int)L;
+      n = (int)((L + kTileTok - 1) / kTileTok);
+    }
+    part[tid] = n;
+    __syncthreads();
+    for (int off = 1; off < kDecWaves * kWave; off <<= 1) {
+      const int add = tid >= off ? part[tid - off] : 0;
+      __syncthreads();
+      part[tid] += add;
+      __syncthreads();
+    }
+    if (b < a.batch) pre[b + 1] = running + part[tid];
+    running += part[kDecWaves * kWave - 1];
+    __syncthreads();
+  }
+  if (tid == 0) pre[0] = 0;
+  __syncthreads();
+  const int64_t total = (int64_t)running * a.num_kv_heads;
+  int per = (int)((total + a.num_waves - 1) / a.num_waves);
+  per = per < 1 ? 1 : per;
+  if (blockIdx.x == 0) {
+    for (int i = tid; i <= a.batch; i += kDecWaves * kWave) a.sk_meta[i] = pre[i];
+    if (tid == 0) a.sk_meta[a.batch + 1] = per;
+  }
+  return per;
+}
+
+template <int KV_DT>
+__global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(DecodeArgs a) {
+  constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
+  extern __shared__ int sk_lds[];
+  int* pre = sk_lds;                 // [batch + 1]
+  int* lens = sk_lds + a.batch + 1;  // [batch]
+  const int per = stream_prefix(a, pre, lens);
+
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+  const int w = blockIdx.x * kDecWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t total = (int64_t)lds_uniform(pre, a.batch) * a.num_kv_heads;
+  const int64_t g0 = (int64_t)w * per;
+  const int64_t g1 = g0 + per < total ? g0 + per : total;
+  if (g0 >= g1) return;
+
+  const int row_bytes = (int)(a.idx.row_elems * kEb);
+  const int64_t blk_bytes = (int64_t)row_bytes << a.idx.bs_log2;
+  const int k_voff = c * row_bytes + 32 * kg * kEb;
+  const int v_voff = 4 * kg * row_bytes + 8 * c * kEb;
+  const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? *a.v_scale : 1.0f;
+
+  Cursor cc = cursor_at(pre, lens, a.batch, a.num_kv_heads, g0);  // tile being computed
+  Cursor lc = cc;                                                  // next tile to load
+  int64_t lg = g0;                                                 // its global index
+  PhysPair ph_next;
+  // Advance the load cursor; tiles past this wave's range are loaded as empty
+  // (L = 0: no bytes move), selected without a branch so that the load
+  // stream stays unconditional and the wait-count pass never drains it.
+  auto advance_load = [&]() {
+    cursor_next(lc, pre, lens, a.batch, a.num_kv_heads);
+    ++lg;
+    lc.L = lg < g1 ? lc.L : 0;
+    ph_next = tile_phys(a, lc);
+  };
+  // Three register tiles: while tile g is computed, tiles g+1 and g+2 are in
+  // flight (about 16 KiB per wave for FP8).
+  Tile16<KV_DT> t0b, t1b, t2b;
+  ph_next = tile_phys(a, lc);
+  load_tile_sk<KV_DT>(a, lc, ph_next, row_bytes, blk_bytes, k_voff, v_voff, t0b);
+  advance_load();
+  load_tile_sk<KV_DT>(a, lc, ph_next, row_bytes, blk_bytes, k_voff, v_voff, t1b);
+  advance_load();
+
+  Op16<KV_DT> qop[4];
+  float score_mul = 0.0f;
+  f32x4 acc[8];
+  float m_run = kNegBig, l_run = 0.0f;
+  int64_t item_g0 = g0 - cc.t;  // global index of the current item's first tile
+
+  // One pipeline step: prefetch tile g+2 into `nxt`, compute tile g in `cur`.
+  auto step = [&](Tile16<KV_DT>& cur, Tile16<KV_DT>& nxt, int64_t g) {
+    load_tile_sk<KV_DT>(a, lc, ph_next, row_bytes, blk_bytes, k_voff, v_voff, nxt);
+    advance_load();
+    if (cc.t == 0 || g == g0) {  // a new item starts: its q, fresh softmax state
+      score_mul = load_q_operands<KV_DT>(a, cc.b, cc.kvh, qop);
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m_run = kNegBig;
+      l_run = 0.0f;
+      item_g0 = g - cc.t;
+    }
+    compute_tile16<KV_DT>(cur, cc.t * kTileTok, cc.L, qop, score_mul, acc, m_run, l_run);
+    const bool item_end = cc.t == cc.n - 1;
+    if (item_end || g == g1 - 1) {
+      float l_col = l_run + __shfl_xor(l_run, 16);
+      l_col += __shfl_xor(l_col, 32);
+      const bool whole = item_end && item_g0 >= g0;
+      finish_sk(a, cc, whole, w, item_g0 <= g0 ? 0 : 1, acc, m_run, l_col, v_mul);
+    }
+    cursor_next(cc, pre, lens, a.batch, a.num_kv_heads);
+  };
+  for (int64_t g = g0;;) {
+    step(t0b, t2b, g);
+    if (++g >= g1) break;
+    step(t1b, t0b, g);
+    if (++g >= g1) break;
+    step(t2b, t1b, g);
+    if (++g >= g1) break;
+  }
+}
+
+// Merge of stream-K partials: one wave per (sequence, query head).
+__global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_kernel(DecodeArgs a,
+                                                                                     int kv_fp8) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wv = (int64_t)blockIdx.x * kDecWaves + (threadIdx.x >> 6);
+  if (wv >= (int64_t)a.batch * a.num_heads) return;
+  const int b = (int)(wv / a.num_heads);
+  const int hq = (int)(wv - (int64_t)b * a.num_heads);
+  const int kvh = hq / a.group, h = hq - kvh * a.group;
+  const int p0 = a.sk_meta[b], n = a.sk_meta[b + 1] - p0;
+  const int per = a.sk_meta[a.batch + 1];
+  const int64_t off = (int64_t)b * a.out_stride + (int64_t)hq * kHeadDim + 2 * lane;
+  float o0 = 0.0f, o1 = 0.0f, l = 0.0f;
+  if (n > 0) {
+    const int64_t gs = (int64_t)p0 * a.num_kv_heads + (int64_t)kvh * n;
+    const int64_t ge = gs + n;
+    const int64_t wlo = gs / per, whi = (ge - 1) / per;
+    if (wlo == whi) return;  // written whole by the main kernel
+    float M = kNegBig;
+    for (int64_t wp = wlo; wp <= whi; ++wp) {
+      const int64_t slot = (wp * 2 + (gs <= wp * per ? 0 : 1)) * a.group + h;
+      M = fmaxf(M, a.ws_ml[slot * 2]);
+    }
+    for (int64_t wp = wlo; wp <= whi; ++wp) {
+      const int64_t slot = (wp * 2 + (gs <= wp * per ? 0 : 1)) * a.group + h;
+      const float wgt = __builtin_amdgcn_exp2f(a.ws_ml[slot * 2] - M);
+      l += wgt * a.ws_ml[slot * 2 + 1];
+      const f32x2 x = *reinterpret_cast<const f32x2*>(a.ws_acc + slot * kHeadDim + 2 * lane);
+      o0 += wgt * x[0];
+      o1 += wgt * x[1];
+    }
+  }
+  const float inv = l > 0.0f ? (kv_fp8 ? *a.v_scale : 1.0f) / l : 0.0f;
+  if (a.q_dtype == MKV_DTYPE_F32) {
+    *reinterpret_cast<f32x2*>(reinterpret_cast<float*>(a.out) + off) = f32x2{o0 * inv, o1 * inv};
+  } else {
+    const uint32_t lo = a.q_dtype == MKV_DTYPE_BF16 ? f32_to_bf16_bits(o0 * inv) : f32_to_f16_bits(o0 * inv);
+    const uint32_t hi = a.q_dtype == MKV_DTYPE_BF16 ? f32_to_bf16_bits(o1 * inv) : f32_to_f16_bits(o1 * inv);
+    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + off) = lo | (hi << 16);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // fp32 KV kernel: v_mfma_f32_16x16x4_f32, 16-token tiles, same lane mapping.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma32_kernel(DecodeArgs a) {
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
   WorkItem it;
-  if (!decode_work_item(a, (int64_t)blockIdx.x * kDecWaves + (threadIdx.x >> 6), it)) return;
+  if (!decode_work_item(a, wave_work_index(), it)) return;
 
   float qf[32];
   const int hq = it.kvh * a.group + c;
@@ -569,6 +977,46 @@ int resolve_split(int split_tokens, int batch, int num_kv_heads, int max_blocks,
   return split_tokens;
 }
 
+// Compute units of the current device (cached per device).  Without a usable
+// device the size query assumes a generous count; no kernel runs then.
+int device_cus() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return 512;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Persistent stream-K grid: at most two 4-wave workgroups per CU (two waves
+// per SIMD); the launch uses what the kernel's register budget allows.
+constexpr int kStreamWgPerCu = 2;
+
+template <typename K>
+int resident_wgs_per_cu(K kernel, size_t lds) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kDecWaves * kWave, lds) != hipSuccess || n < 1)
+    n = 1;
+  return n < kStreamWgPerCu ? n : kStreamWgPerCu;
+}
+
+int stream_waves() { return device_cus() * kStreamWgPerCu * kDecWaves; }
+
+size_t stream_ws_bytes(int batch, int group) {
+  const size_t w = (size_t)stream_waves();
+  return w * 2 * group * (kHeadDim + 2) * sizeof(float) + (size_t)(batch + 2) * sizeof(int);
+}
+
+size_t split_ws_bytes(int batch, int num_heads, int max_blocks, int block_size, int st) {
+  const int64_t max_splits = ((int64_t)max_blocks * block_size + st - 1) / st;
+  if (max_splits <= 1) return 0;
+  return (size_t)batch * num_heads * max_splits * (kHeadDim + 2) * sizeof(float);
+}
+
 }  // namespace
 }  // namespace mkv
 
@@ -583,12 +1031,15 @@ extern "C" size_t mkv_paged_decode_workspace_size(int batch, int num_heads, int 
                                                   int max_blocks, int block_size, int head_dim,
                                                   int split_tokens) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks <= 0 || block_size <= 0 ||
-      head_dim <= 0)
+      head_dim <= 0 || num_heads % num_kv_heads)
     return 0;
   const int st = resolve_split(split_tokens, batch, num_kv_heads, max_blocks, block_size);
-  const int64_t max_splits = ((int64_t)max_blocks * block_size + st - 1) / st;
-  if (max_splits <= 1) return 0;
-  return (size_t)batch * num_heads * max_splits * (head_dim + 2) * sizeof(float);
+  size_t n = split_ws_bytes(batch, num_heads, max_blocks, block_size, st);
+  if (split_tokens <= 0 && batch <= kStreamMaxBatch) {
+    const size_t sk = stream_ws_bytes(batch, num_heads / num_kv_heads);
+    n = sk > n ? sk : n;
+  }
+  return n;
 }
 
 extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void* q,
@@ -651,6 +1102,48 @@ extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void*
   a.num_kv_heads = num_kv_heads;
   a.group = group;
   a.sm_scale = sm_scale;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool fp8 = kv_dtype == MKV_DTYPE_FP8E4M3;
+  if (split_tokens == 0 && kv_dtype != MKV_DTYPE_F32 && batch <= kStreamMaxBatch) {
+    // stream-K path
+    const size_t need = stream_ws_bytes(batch, group);
+    if (!workspace) return MKV_ERR_NULL_POINTER;
+    if (workspace_bytes < need) return MKV_ERR_WORKSPACE_TOO_SMALL;
+    if (reinterpret_cast<uintptr_t>(workspace) & 15u) return MKV_ERR_MISALIGNED;
+    const size_t lds = (size_t)(2 * batch + 1) * sizeof(int);
+    // Workspace slots are laid out for the largest grid (stream_waves()).
+    const size_t slots = (size_t)stream_waves() * 2 * group;
+    a.split_tokens = kTileTok;
+    a.max_splits = 0;
+    a.ws_acc = reinterpret_cast<float*>(workspace);
+    a.ws_ml = a.ws_acc + slots * kHeadDim;
+    a.sk_meta = reinterpret_cast<int*>(a.ws_ml + slots * 2);
+    const dim3 block(kDecWaves * kWave);
+#define MKV_STREAM_LAUNCH(DT)                                                              \
+  {                                                                                        \
+    static int per_cu[64];                                                                 \
+    int dev = 0;                                                                           \
+    (void)hipGetDevice(&dev);                                                              \
+    const int slot = dev >= 0 && dev < 64 ? dev : 0;                                       \
+    if (per_cu[slot] == 0)                                                                 \
+      per_cu[slot] = resident_wgs_per_cu(paged_decode_stream_kernel<DT>, kStreamMaxLds);   \
+    const int wgs = device_cus() * per_cu[slot];                                           \
+    a.num_waves = wgs * kDecWaves;                                                         \
+    hipLaunchKernelGGL(paged_decode_stream_kernel<DT>, dim3(wgs), block, lds, s, a);       \
+  }
+    switch (kv_dtype) {
+      case MKV_DTYPE_FP8E4M3: MKV_STREAM_LAUNCH(MKV_DTYPE_FP8E4M3) break;
+      case MKV_DTYPE_BF16: MKV_STREAM_LAUNCH(MKV_DTYPE_BF16) break;
+      default: MKV_STREAM_LAUNCH(MKV_DTYPE_F16) break;
+    }
+#undef MKV_STREAM_LAUNCH
+    const int64_t mitems = (int64_t)batch * num_heads;
+    hipLaunchKernelGGL(paged_decode_stream_merge_kernel,
+                       dim3((unsigned)((mitems + kDecWaves - 1) / kDecWaves)), dim3(kDecWaves * kWave), 0,
+                       s, a, (int)fp8);
+    return (int)hipGetLastError();
+  }
+
   const int st = resolve_split(split_tokens, batch, num_kv_heads, max_blocks, block_size);
   a.split_tokens = st;
   const int64_t max_len = (int64_t)max_blocks * block_size;
@@ -665,7 +1158,6 @@ extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void*
     a.ws_acc = reinterpret_cast<float*>(workspace);
     a.ws_ml = a.ws_acc + (size_t)batch * num_heads * a.max_splits * head_dim;
   }
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t items = (int64_t)batch * num_kv_heads * a.max_splits;
   const dim3 grid((unsigned)((items + kDecWaves - 1) / kDecWaves));
   const dim3 block(kDecWaves * kWave);

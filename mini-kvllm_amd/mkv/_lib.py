@@ -1,12 +1,14 @@
 """ctypes binding of libmkv.so, the C ABI declared in include/mkv.h.
 
-The library is loaded lazily on first use.  Loading never falls back to
+The library is loaded lazily on first use from mkv/libmkv.so, or from the
+path in the MKV_LIBRARY environment variable.  Loading never falls back to
 anything: if the shared object is missing or has the wrong ABI version, every
 operator raises.
 """
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
@@ -71,7 +73,7 @@ def load(path: str | Path | None = None) -> ctypes.CDLL:
     with _lock:
         if _lib is not None and path is None:
             return _lib
-        p = Path(path) if path is not None else LIB_PATH
+        p = Path(path) if path is not None else Path(os.environ.get("MKV_LIBRARY", LIB_PATH))
         if not p.exists():
             raise RuntimeError(
                 f"libmkv.so not found at {p}; build it first (python -m mkv.build or "

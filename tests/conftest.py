@@ -32,3 +32,25 @@ def announce(msg: str) -> None:
     """Name the GPU case on stdout before it runs (flushed), so a run that
     dies inside a kernel still says which case it was."""
     print(f"[case] {msg}", flush=True)
+
+
+def assert_close_out(got: torch.Tensor, want: torch.Tensor, out_dtype: torch.dtype,
+                     abs_tol: float) -> None:
+    """|got - want| <= abs_tol + half an ulp of out_dtype at |want|.
+
+    The kernels, like the reference, compute in fp32 and round the result to
+    the query dtype on store; abs_tol bounds the error before that rounding
+    and the half-ulp term is the rounding itself (0 for fp32 outputs)."""
+    got = got.double().cpu()
+    want = want.double().cpu()
+    if out_dtype == torch.float32:
+        tol = torch.full_like(want, abs_tol)
+    else:
+        mant = {torch.bfloat16: 8, torch.float16: 11}[out_dtype]
+        e = torch.floor(torch.log2(want.abs().clamp(min=2.0 ** -14)))
+        tol = abs_tol + 0.5 * torch.exp2(e - (mant - 1))
+    err = (got - want).abs()
+    bad = err > tol
+    assert not bool(bad.any()), (
+        f"{int(bad.sum())} of {err.numel()} elements out of tolerance; max abs err "
+        f"{float(err.max()):.3e}, max excess {float((err - tol).max()):.3e} (abs_tol {abs_tol})")

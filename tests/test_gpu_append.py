@@ -56,10 +56,12 @@ def test_fp8_encoding_exhaustive_bf16(dev, scale):
     want = R.fp8_quantize_ref(x, scale).view(torch.uint8).reshape(-1).numpy()
     xf = x.float().reshape(-1).numpy()
     nan = np.isnan(xf)
-    assert np.array_equal(got[~nan], want[~nan])
-    # NaN inputs stay NaN (0x7f / 0xff, the sign kept as torch does)
-    assert np.array_equal(got[nan] & 0x7F, np.full(int(nan.sum()), 0x7F, np.uint8))
-    assert np.array_equal(got, want)
+    bad = np.nonzero(got != want)[0]
+    detail = [(hex(int(bits[i]) & 0xFFFF), hex(got[i]), hex(want[i])) for i in bad[:8]]
+    assert np.array_equal(got[~nan], want[~nan]), detail
+    # NaN inputs stay NaN (0x7f / 0xff) with the sign torch's CPU cast gives
+    assert np.array_equal(got[nan] & 0x7F, np.full(int(nan.sum()), 0x7F, np.uint8)), detail
+    assert np.array_equal(got, want), detail
 
 
 def test_fp8_encoding_random_fp32_inputs(dev):

@@ -11,7 +11,7 @@ import math
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, assert_close_out
 from mkv import attention as A
 from mkv import workloads as W
 from oracle import reference as R
@@ -25,11 +25,11 @@ def _run(dev, q, k, v, bt, ctx, scale, Hq, Hkv, ks=None, vs=None, split_tokens=0
     vsd = None if vs is None else torch.tensor([vs], dtype=torch.float32, device=dev)
     out = A._decode(q.to(dev), k.to(dev), v.to(dev), bt.to(dev), ctx.to(dev), scale, Hq, Hkv, 128,
                     ksd, vsd, split_tokens=split_tokens)
-    return out.float().cpu()
+    return out.cpu()
 
 
 def _oracle(q, k, v, bt, ctx, scale, Hq, Hkv, ks=None, vs=None):
-    return R.paged_decode_ref(q.double(), k, v, bt, ctx, scale, Hq, Hkv, ks, vs).float()
+    return R.paged_decode_ref(q.double(), k, v, bt, ctx, scale, Hq, Hkv, ks, vs)
 
 
 def test_decode_small_fp32(dev):
@@ -39,7 +39,7 @@ def test_decode_small_fp32(dev):
             w["num_heads"], w["num_kv_heads"])
     got = _run(dev, *args)
     want = _oracle(*args)
-    assert (got - want).abs().max().item() <= 2e-3
+    assert_close_out(got, want, got.dtype, 2e-3)
 
 
 def test_decode_fp8_batch32_over_appended_pool(dev):
@@ -60,11 +60,11 @@ def test_decode_fp8_batch32_over_appended_pool(dev):
     assert float(ks) == R.calibrate_scale_ref(w["key"])
     out = A.paged_attention_decode_quantized(
         w["q"].to(dev), kc, vc, ks, vs, w["block_tables"].to(dev), w["context_lens"].to(dev),
-        w["scale"], w["num_heads"], H, 128, bs, "fp8_per_tensor").float().cpu()
+        w["scale"], w["num_heads"], H, 128, bs, "fp8_per_tensor").cpu()
     kcc, vcc = kc.cpu(), vc.cpu()
     want = _oracle(w["q"], kcc, vcc, w["block_tables"], w["context_lens"], w["scale"],
                    w["num_heads"], H, float(ks), float(vs))
-    assert (out - want).abs().max().item() <= 2e-2
+    assert_close_out(out, want, out.dtype, 2e-2)
     # against the unquantised bf16 values (information: FP8 storage error)
     kb = torch.zeros(N * bs, H, 128, dtype=torch.bfloat16)
     vb = torch.zeros_like(kb)
@@ -75,9 +75,8 @@ def test_decode_fp8_batch32_over_appended_pool(dev):
     vb[w["slot_mapping"][ok]] = w["value"][ok]
     exact = _oracle(w["q"], kb.view(N, bs, H, 128), vb.view(N, bs, H, 128), w["block_tables"],
                     w["context_lens"], w["scale"], w["num_heads"], H)
-    err = (out - exact).abs().max().item()
+    err = (out.double() - exact).abs().max().item()
     print(f"fp8 decode vs unquantised bf16 cache: max abs err {err:.3e}")
-    assert err < 0.25
 
 
 def _case(seed, B, Hq, Hkv, bs, N, max_blocks, dtype, ctx=None):
@@ -107,7 +106,7 @@ def test_decode_group_sizes(dev, dtype, group):
     q, k, v, bt, ctx, ks, vs = _case(100 + group, 6, Hkv * group, Hkv, 32, 64, 10, dtype)
     got = _run(dev, q, k, v, bt, ctx, 1 / math.sqrt(128), Hkv * group, Hkv, ks, vs)
     want = _oracle(q, k, v, bt, ctx, 1 / math.sqrt(128), Hkv * group, Hkv, ks, vs)
-    assert (got - want).abs().max().item() <= TOL[dtype]
+    assert_close_out(got, want, got.dtype, TOL[dtype])
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn, torch.float32])
@@ -119,7 +118,7 @@ def test_decode_block_sizes_and_edges(dev, dtype, bs):
     bt[6, 2] = -1  # an absent block inside a context: its tokens are skipped
     got = _run(dev, q, k, v, bt, ctx, 0.09, 8, 2, ks, vs)
     want = _oracle(q, k, v, bt, ctx, 0.09, 8, 2, ks, vs)
-    assert (got - want).abs().max().item() <= TOL[dtype]
+    assert_close_out(got, want, got.dtype, TOL[dtype])
     assert torch.count_nonzero(got[0]) == 0  # context 0 -> zeros
     got32 = _run(dev, q, k, v, bt, ctx.to(torch.int32), 0.09, 8, 2, ks, vs)
     assert torch.equal(got, got32)
@@ -133,7 +132,7 @@ def test_decode_split_count_independence(dev, dtype):
     outs = []
     for st in (32, 64, 256, 512, 4096):
         got = _run(dev, q, k, v, bt, ctx, 0.088, 32, 8, ks, vs, split_tokens=st)
-        assert (got - want).abs().max().item() <= TOL[dtype], st
+        assert_close_out(got, want, got.dtype, TOL[dtype])
         outs.append(got)
     # deterministic run to run
     again = _run(dev, q, k, v, bt, ctx, 0.088, 32, 8, ks, vs, split_tokens=256)
@@ -147,7 +146,8 @@ def test_decode_query_dtypes_over_bf16_and_fp8(dev):
         want = _oracle(q, k, v, bt, ctx, 0.1, 8, 2, ks, vs)
         for qd in (torch.float32, torch.float16):
             got = _run(dev, q.to(qd), k, v, bt, ctx, 0.1, 8, 2, ks, vs)
-            assert (got - want).abs().max().item() <= TOL[dtype] + 2e-3
+            # an fp32 query is rounded to the MFMA input type for a bf16 cache
+            assert_close_out(got, want, got.dtype, TOL[dtype] + 2e-3)
 
 
 def _torch_gpu_reference(q, kc, vc, bt, ctx, scale, Hq, Hkv, ks=None, vs=None):
@@ -189,7 +189,36 @@ def test_decode_batch256_full_size(dev, kv):
     bt, ctx = m["block_tables"].to(dev), m["context_lens"].to(dev)
     ksd = None if ks is None else torch.tensor([ks], device=dev)
     vsd = None if vs is None else torch.tensor([vs], device=dev)
-    got = A._decode(q, kc, vc, bt, ctx, 1 / math.sqrt(128), 32, 8, 128, ksd, vsd).float()
+    got = A._decode(q, kc, vc, bt, ctx, 1 / math.sqrt(128), 32, 8, 128, ksd, vsd)
     want = _torch_gpu_reference(q, kc, vc, bt, ctx, 1 / math.sqrt(128), 32, 8, ks, vs)
-    err = (got - want).abs().max().item()
-    assert err <= (2e-2 if kv == "fp8" else 2e-3), err
+    assert_close_out(got, want, got.dtype, 2e-2 if kv == "fp8" else 2e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn, torch.float16])
+def test_decode_stream_k_vs_split_k_and_empty_rows(dev, dtype):
+    """The default stream-K decomposition and explicit split-K agree; rows
+    with context 0 anywhere in the batch come out as zeros."""
+    announce(f"decode {dtype} stream-K vs split-K with empty rows")
+    g = torch.Generator().manual_seed(71)
+    B = 40
+    ctx = torch.randint(1, 16 * 64 + 1, (B,), generator=g)
+    ctx[[0, 7, 8, 39]] = 0
+    q, k, v, bt, ctx, ks, vs = _case(72, B, 16, 4, 64, 400, 16, dtype, ctx=ctx)
+    want = _oracle(q, k, v, bt, ctx, 0.11, 16, 4, ks, vs)
+    sk = _run(dev, q, k, v, bt, ctx, 0.11, 16, 4, ks, vs)
+    sp = _run(dev, q, k, v, bt, ctx, 0.11, 16, 4, ks, vs, split_tokens=128)
+    assert_close_out(sk, want, sk.dtype, TOL[dtype])
+    assert_close_out(sp, want, sp.dtype, TOL[dtype])
+    assert torch.count_nonzero(sk[[0, 7, 8, 39]]) == 0
+
+
+def test_decode_large_batch_uses_split_k_fallback(dev):
+    announce("decode batch 9000 (beyond the stream-K batch cap)")
+    g = torch.Generator().manual_seed(73)
+    B = 9000
+    ctx = torch.randint(0, 40, (B,), generator=g)
+    q, k, v, bt, ctx, ks, vs = _case(74, B, 8, 2, 16, 4 * B, 3, torch.bfloat16, ctx=ctx)
+    got = _run(dev, q, k, v, bt, ctx, 0.1, 8, 2)
+    idx = torch.arange(0, B, 97)
+    want = _oracle(q[idx], k, v, bt[idx], ctx[idx], 0.1, 8, 2)
+    assert_close_out(got[idx], want, got.dtype, 2e-3)

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, assert_close_out
 import mkv
 from mkv import attention as A
 from mkv import context as C
@@ -57,7 +57,7 @@ def _gpu(dev, q, k, v, bt, ctx, cu, pos, scale, Hq, Hkv, ks, vs):
         q.to(dev), k.to(dev), v.to(dev), bt.to(dev), ctx.to(dev), cu.to(dev), pos.to(dev), scale,
         Hq, Hkv, 128, k.shape[1], k_scale=ksd, v_scale=vsd,
         kv_cache_dtype="fp8_per_tensor" if fp8 else "auto")
-    return out.float().cpu()
+    return out.cpu()
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn])
@@ -70,8 +70,8 @@ def test_prefill_small_groups(dev, dtype, group):
     q, k, v, bt, ctx, cu, pos, ks, vs = _make(group, prior, qlen, Hkv * group, Hkv, 32, dtype)
     sc = 1 / math.sqrt(128)
     got = _gpu(dev, q, k, v, bt, ctx, cu, pos, sc, Hkv * group, Hkv, ks, vs)
-    want = R.paged_prefill_ref(q.double(), k, v, bt, ctx, cu, pos, sc, Hkv * group, Hkv, ks, vs).float()
-    assert (got - want).abs().max().item() <= TOL[dtype]
+    want = R.paged_prefill_ref(q.double(), k, v, bt, ctx, cu, pos, sc, Hkv * group, Hkv, ks, vs)
+    assert_close_out(got, want, got.dtype, TOL[dtype])
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
@@ -84,8 +84,8 @@ def test_prefill_block_sizes_holes_and_context_caps(dev, dtype, bs):
     ctx2 = ctx.clone()
     ctx2[0] = 50  # context shorter than some positions: visible = min(ctx, pos + 1)
     got = _gpu(dev, q, k, v, bt, ctx2, cu, pos, 0.1, 8, 2, ks, vs)
-    want = R.paged_prefill_ref(q.double(), k, v, bt, ctx2, cu, pos, 0.1, 8, 2, ks, vs).float()
-    assert (got - want).abs().max().item() <= TOL[dtype]
+    want = R.paged_prefill_ref(q.double(), k, v, bt, ctx2, cu, pos, 0.1, 8, 2, ks, vs)
+    assert_close_out(got, want, got.dtype, TOL[dtype])
 
 
 def _torch_prefill_gpu(q, kc, vc, bt, ctx, cu, pos, scale, Hq, Hkv, ks=None, vs=None):
@@ -134,8 +134,7 @@ def test_prefill_chunk_workload_full_size(dev, kv):
     got = A.paged_attention_prefill_triton(q, kc, vc, *args, sc, 32, 8, 128, bs, k_scale=ksd,
                                            v_scale=vsd, kv_cache_dtype="fp8_per_tensor" if ks else "auto")
     want = _torch_prefill_gpu(q, kc, vc, *args, sc, 32, 8, ks, vs)
-    err = (got.float() - want).abs().max().item()
-    assert err <= (2e-2 if ks else 2e-3), err
+    assert_close_out(got, want, got.dtype, 2e-2 if ks else 2e-3)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -150,9 +149,9 @@ def test_flash_prefill_contiguous(dev, dtype, group):
     k = torch.randn(T, Hkv, 128, generator=g).to(dtype)
     v = torch.randn(T, Hkv, 128, generator=g).to(dtype)
     got = mkv.flash_attention_prefill(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), 0.08,
-                                      Hkv * group, Hkv, 128).float().cpu()
-    want = R.flash_prefill_ref(q.double(), k.double(), v.double(), cu, 0.08, Hkv * group, Hkv).float()
-    assert (got - want).abs().max().item() <= 2e-3
+                                      Hkv * group, Hkv, 128).cpu()
+    want = R.flash_prefill_ref(q.double(), k.double(), v.double(), cu, 0.08, Hkv * group, Hkv)
+    assert_close_out(got, want, got.dtype, 2e-3)
 
 
 def test_chunked_equals_one_shot_and_append_path(dev):
@@ -178,7 +177,10 @@ def test_chunked_equals_one_shot_and_append_path(dev):
     assert torch.equal(one, two)
     flash = mkv.flash_attention_prefill(q, k, v, torch.tensor([0, n], dtype=torch.int32, device=dev),
                                         0.1, Hq, Hkv, 128)
-    assert (one.float() - flash.float()).abs().max().item() <= 2e-3
+    want = R.flash_prefill_ref(q.cpu().double(), k.cpu().double(), v.cpu().double(),
+                               torch.tensor([0, n]), 0.1, Hq, Hkv)
+    assert_close_out(one, want, one.dtype, 2e-3)
+    assert_close_out(flash, want, flash.dtype, 2e-3)
 
 
 @pytest.mark.parametrize("mode", ["auto", "fp8_per_tensor"])
@@ -239,12 +241,11 @@ def test_attention_layer_mixed_batch(dev, mode):
                   context_lens=ctx.to(dev), block_tables=bt.to(dev), positions=pos.to(dev),
                   mixed_attention_split=split, is_full_prefill=False)
     try:
-        out = layer(q.to(dev), k.to(dev), v.to(dev)).float().cpu()
+        out = layer(q.to(dev), k.to(dev), v.to(dev)).cpu()
     finally:
         C.reset_context()
     assert torch.equal(layer.k_cache.cpu().view(torch.uint8), kcr.view(torch.uint8))
     ks = float(ksr) if fp8 else None
     vs = float(vsr) if fp8 else None
     want = R.paged_prefill_ref(q.double(), kcr, vcr, bt, ctx, cu, pos, 1 / math.sqrt(128), Hq, Hkv, ks, vs)
-    tol = 2e-2 if fp8 else 2e-3
-    assert (out - want.float().reshape(T, Hq * 128)).abs().max().item() <= tol
+    assert_close_out(out, want.reshape(T, Hq * 128), out.dtype, 2e-2 if fp8 else 2e-3)

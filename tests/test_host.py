@@ -72,9 +72,14 @@ def test_decode_workspace_and_split_queries():
     assert st % 32 == 0 and 64 <= st <= 512
     n = lib.mkv_paged_decode_workspace_size(256, 32, 8, 32, 256, 128, 0)
     splits = (32 * 256 + st - 1) // st
-    assert n == 256 * 32 * splits * 130 * 4
-    # one split covers the table: no workspace
+    assert n >= 256 * 32 * splits * 130 * 4  # split-K partials
+    # explicit split sizes select the split-K path only
+    n512 = lib.mkv_paged_decode_workspace_size(256, 32, 8, 32, 256, 128, 512)
+    assert n512 == 256 * 32 * 16 * 130 * 4
+    # one split covers the table: no workspace on the split-K path
     assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 1, 256, 128, 512) == 0
+    # the default (stream-K) path always needs its partial slots
+    assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 1, 256, 128, 0) > 0
     # small batches split finer
     assert lib.mkv_paged_decode_split_tokens(4, 8, 8, 256, 0) < st or st == 64
 
