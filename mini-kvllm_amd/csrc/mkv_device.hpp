@@ -187,10 +187,15 @@ struct PagedIndex {
   int bs_log2;
   int64_t row_elems;  // num_kv_heads * head_dim: elements per token row
 
-  // Physical block of logical block `blk` of sequence `seq`, or -1.
+  // Physical block of logical block `blk` of sequence `seq`, or -1.  The table
+  // is read through the constant address space (no kernel writes it): with a
+  // wave-uniform index this becomes a scalar load, which is counted apart from
+  // the vector-memory counter, so looking up the next tile never waits for the
+  // K/V loads already in flight.
   MKV_DEV int64_t physical_block(int seq, int64_t blk) const {
     if (blk < 0 || blk >= max_blocks) return -1;
-    const int64_t p = block_tables[(int64_t)seq * bt_stride + blk];
+    typedef const int32_t __attribute__((address_space(4))) const_i32;
+    const int64_t p = ((const_i32*)block_tables)[(int64_t)seq * bt_stride + blk];
     return (p >= 0 && p < num_blocks) ? p : -1;
   }
 
