@@ -193,9 +193,51 @@ MKV_DEV void finish_item(const DecodeArgs& a, const WorkItem& it, f32x4 (&acc)[8
 constexpr int kRsrcFlags = 0x00020000;
 // A per-lane buffer offset beyond every descriptor's range: the load returns 0.
 constexpr uint32_t kOob = 0x80000000u;
-// Cache policy of K/V loads: default (measured faster than the non-temporal
-// hint on this path).
-constexpr int kStreamAux = 0;
+// Cache policy of the K/V loads.  The non-temporal hint (bit 1) speeds up
+// streamed-once reads only when every load instruction covers whole 128-byte
+// lines; when two instructions share a line it costs bandwidth instead.  The
+// V loads and the FP8 K loads cover whole lines; the 16-bit K loads do not.
+constexpr int kAuxNt = 2;
+template <int KV_DT>
+struct LoadPolicy {
+  static constexpr int kK = DTypeInfo<KV_DT>::kBytes == 1 ? kAuxNt : 0;
+  static constexpr int kV = kAuxNt;
+};
+
+// FP8 K rows are 128 bytes and an MFMA row is owned by the four lanes c +
+// 16*kg, which keep bytes 32kg .. 32kg+31.  One load instruction can cover
+// whole lines only if eight lanes read each row, so a 16-row sub-tile is read
+// by two instructions: A reads rows 0-7 (lane c < 8: row c, bytes 32kg..+15;
+// lane c >= 8: row c-8, bytes 32kg+16..+31), B reads rows 8-15 the other way
+// round.  k_exchange() then swaps the borrowed halves between lanes c and
+// c^8 (same kg) with one DPP rotate, leaving lane (c, kg) with bytes
+// 32kg .. 32kg+15 of row c in piece 0 and 32kg+16 .. 32kg+31 in piece 1.
+struct Fp8KLanes {
+  int off_a, off_b;  // byte offsets inside the sub-tile (row * row_bytes + col)
+  int row_a, row_b;  // rows the lane reads in instructions A and B
+};
+MKV_DEV Fp8KLanes fp8_k_lanes(int row_bytes) {
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+  const bool top = c < 8;
+  Fp8KLanes f;
+  f.row_a = c & 7;
+  f.row_b = (c & 7) + 8;
+  f.off_a = f.row_a * row_bytes + 32 * kg + (top ? 0 : 16);
+  f.off_b = f.row_b * row_bytes + 32 * kg + (top ? 16 : 0);
+  return f;
+}
+MKV_DEV void k_exchange(u32x4& a, u32x4& b) {
+  const bool top = (threadIdx.x & 15) < 8;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t send = top ? b[d] : a[d];
+    const uint32_t own = top ? a[d] : b[d];
+    // row_ror:8 inside each 16-lane row: lane c receives from lane c ^ 8
+    b[d] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)send, 0x128, 0xf, 0xf, false);
+    a[d] = own;
+  }
+}
 
 // Descriptor over the rows of one block that start at `row` (token offset in
 // the block) for one KV head: [base, end of block).  An absent block (phys <
@@ -250,6 +292,45 @@ struct Tile16 {
   bool ok[2];  // sub-tile block present
 };
 
+// Issue the K/V loads of one 32-token tile through the per-half descriptors
+// rk/rv (rows t0 .. t0+15 and t0+16 .. t0+31).  Rows at or past t_end read as
+// zeros (out-of-range offset); no branches.
+template <int KV_DT>
+MKV_DEV void load_tile_rows(const __amdgpu_buffer_rsrc_t (&rk)[2], const __amdgpu_buffer_rsrc_t (&rv)[2],
+                            int t0, int t_end, int k_voff, int v_voff, int row_bytes, Tile16<KV_DT>& T) {
+  constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+  if constexpr (kEb == 1) {
+    const Fp8KLanes f = fp8_k_lanes(row_bytes);
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const uint32_t oa = (t0 + 16 * m + f.row_a < t_end) ? (uint32_t)f.off_a : kOob;
+      const uint32_t ob = (t0 + 16 * m + f.row_b < t_end) ? (uint32_t)f.off_b : kOob;
+      T.k[m][0] = __builtin_amdgcn_raw_buffer_load_b128(rk[m], oa, 0, LoadPolicy<KV_DT>::kK);
+      T.k[m][1] = __builtin_amdgcn_raw_buffer_load_b128(rk[m], ob, 0, LoadPolicy<KV_DT>::kK);
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const uint32_t off = (t0 + 16 * m + c < t_end) ? (uint32_t)k_voff : kOob;
+#pragma unroll
+      for (int i = 0; i < Tile16<KV_DT>::kKVec; ++i)
+        T.k[m][i] = __builtin_amdgcn_raw_buffer_load_b128(rk[m], off + 16 * i, 0, LoadPolicy<KV_DT>::kK);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int hf = i >> 2, r = i & 3;
+    const uint32_t off =
+        (t0 + 16 * hf + 4 * kg + r < t_end) ? (uint32_t)(v_voff + r * row_bytes) : kOob;
+    if constexpr (kEb == 1)
+      T.v[i] = __builtin_amdgcn_raw_buffer_load_b64(rv[hf], off, 0, LoadPolicy<KV_DT>::kV);
+    else
+      T.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv[hf], off, 0, LoadPolicy<KV_DT>::kV);
+  }
+}
+
 // Issue every load of the 32-token tile starting at t0 (wave-uniform).  Tokens
 // past the split end and absent blocks read as zeros; no branches.
 template <int KV_DT>
@@ -271,23 +352,7 @@ MKV_DEV void load_tile16(const DecodeArgs& a, const WorkItem& it, const ItemLoad
     rv[h] = rows_rsrc(a.v_cache, phys, L.blk_bytes, off);
     T.ok[h] = phys >= 0;
   }
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const uint32_t off = (t0 + 16 * m + c < it.t_end) ? (uint32_t)L.k_voff : kOob;
-#pragma unroll
-    for (int i = 0; i < Tile16<KV_DT>::kKVec; ++i)
-      T.k[m][i] = __builtin_amdgcn_raw_buffer_load_b128(rk[m], off + 16 * i, 0, kStreamAux);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int hf = i >> 2, r = i & 3;
-    const uint32_t off = (t0 + 16 * hf + 4 * kg + r < it.t_end)
-                             ? (uint32_t)(L.v_voff + r * L.row_bytes) : kOob;
-    if constexpr (kEb == 1)
-      T.v[i] = __builtin_amdgcn_raw_buffer_load_b64(rv[hf], off, 0, kStreamAux);
-    else
-      T.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv[hf], off, 0, kStreamAux);
-  }
+  load_tile_rows<KV_DT>(rk, rv, t0, it.t_end, L.k_voff, L.v_voff, L.row_bytes, T);
 }
 
 template <int KV_DT>
@@ -315,18 +380,19 @@ MKV_DEV Op16<KV_DT> to_op16(const float* x) {
   return r;
 }
 
-// A operand of QK step st for K sub-tile m (8 dims: 32kg + 8st .. +7).
+// A operand of QK step st for K sub-tile m (8 dims: 32kg + 8st .. +7) from
+// the lane's K words (FP8 words already passed through k_exchange).
 template <int KV_DT>
-MKV_DEV Op16<KV_DT> k_operand(const Tile16<KV_DT>& T, int m, int st) {
+MKV_DEV Op16<KV_DT> k_operand(const u32x4 (&K)[2][Tile16<KV_DT>::kKVec], int m, int st) {
   if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) {
-    const u32x4 w = T.k[m][st >> 1];
+    const u32x4 w = K[m][st >> 1];
     const uint32_t d0 = (st & 1) ? w[2] : w[0];
     const uint32_t d1 = (st & 1) ? w[3] : w[1];
     const f16x2 a0 = fp8x2_to_f16x2<false>(d0), a1 = fp8x2_to_f16x2<true>(d0);
     const f16x2 a2 = fp8x2_to_f16x2<false>(d1), a3 = fp8x2_to_f16x2<true>(d1);
     return f16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
   } else {
-    return __builtin_bit_cast(Op16<KV_DT>, T.k[m][st]);
+    return __builtin_bit_cast(Op16<KV_DT>, K[m][st]);
   }
 }
 
@@ -369,12 +435,19 @@ MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const O
   const int lane = threadIdx.x & 63;
   const int kg = lane >> 4;
   // S^T = K q^T: lane holds scores of tokens t0 + 16m + 4kg + r for head c.
+  u32x4 kw[2][Tile16<KV_DT>::kKVec];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+#pragma unroll
+    for (int i = 0; i < Tile16<KV_DT>::kKVec; ++i) kw[m][i] = cur.k[m][i];
+    if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) k_exchange(kw[m][0], kw[m][1]);
+  }
   f32x4 s[2];
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
     s[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int st = 0; st < 4; ++st) s[m] = mfma16<KV_DT>(k_operand<KV_DT>(cur, m, st), qop[st], s[m]);
+    for (int st = 0; st < 4; ++st) s[m] = mfma16<KV_DT>(k_operand<KV_DT>(kw, m, st), qop[st], s[m]);
   }
   float mx = kNegBig;
 #pragma unroll
@@ -598,23 +671,7 @@ MKV_DEV void load_tile_sk(const DecodeArgs& a, const Cursor& c, const PhysPair& 
     rv[h] = rows_rsrc(a.v_cache, ph.p[h], blk_bytes, off);
     T.ok[h] = ph.p[h] >= 0;
   }
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const uint32_t off = (t0 + 16 * m + cc < c.L) ? (uint32_t)k_voff : kOob;
-#pragma unroll
-    for (int i = 0; i < Tile16<KV_DT>::kKVec; ++i)
-      T.k[m][i] = __builtin_amdgcn_raw_buffer_load_b128(rk[m], off + 16 * i, 0, kStreamAux);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int hf = i >> 2, r = i & 3;
-    const uint32_t off =
-        (t0 + 16 * hf + 4 * kg + r < c.L) ? (uint32_t)(v_voff + r * row_bytes) : kOob;
-    if constexpr (kEb == 1)
-      T.v[i] = __builtin_amdgcn_raw_buffer_load_b64(rv[hf], off, 0, kStreamAux);
-    else
-      T.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv[hf], off, 0, kStreamAux);
-  }
+  load_tile_rows<KV_DT>(rk, rv, t0, c.L, k_voff, v_voff, row_bytes, T);
 }
 
 // Write the finished item of cursor c: the normalised output if the whole item
