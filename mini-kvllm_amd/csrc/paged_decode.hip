@@ -58,8 +58,9 @@ struct DecodeArgs {
   float* ws_acc;  // [batch * num_heads][max_splits][head_dim]
   float* ws_ml;   // [batch * num_heads][max_splits][2]  (m, l), log2 domain
   // stream-K decomposition (16-bit KV): partial slots per wave and metadata
-  int* sk_meta;   // [batch + 1] tile prefix per sequence, then tiles_per_wave
-  int num_waves;  // persistent waves in the grid
+  int* sk_meta;     // [batch + 1] tile prefix per sequence
+  int num_waves;    // persistent waves in the grid
+  int first_waves;  // waves of the first dispatch round (== num_waves: even split)
 };
 
 MKV_DEV float wave_max(float v) {
@@ -501,23 +502,13 @@ MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const O
   }
 }
 
-// q of head c of the group, dims 32kg .. 32kg+31 (zero for padding heads),
-// as MFMA operands; returns the fp32 factor that maps MFMA scores to the
-// log2-domain logits.  fp16 operands are normalised by a power of two so q is
-// exact and in range; k_scale (FP8) and sm_scale*log2(e) stay in fp32.
+// MFMA operands of q (the lane holds dims 32kg .. 32kg+31 of head c of the
+// group, zero for padding heads); returns the fp32 factor that maps MFMA
+// scores to the log2-domain logits.  fp16 operands are normalised by a power
+// of two so q is exact and in range; k_scale (FP8) and sm_scale*log2(e) stay
+// in fp32.
 template <int KV_DT>
-MKV_DEV float load_q_operands(const DecodeArgs& a, int b, int kvh, Op16<KV_DT> (&qop)[4]) {
-  const int lane = threadIdx.x & 63;
-  const int c = lane & 15, kg = lane >> 4;
-  float qf[32];
-  if (c < a.group) {
-    const int64_t qoff = (int64_t)b * a.q_stride + (int64_t)(kvh * a.group + c) * kHeadDim + 32 * kg;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) load_q8(a.q, a.q_dtype, qoff + 8 * i, qf + 8 * i);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
-  }
+MKV_DEV float q_operands(const DecodeArgs& a, float (&qf)[32], Op16<KV_DT> (&qop)[4]) {
   float score_mul = a.sm_scale * kLog2e;
   if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) score_mul *= *a.k_scale;
   if constexpr (KV_DT != MKV_DTYPE_BF16) {
@@ -536,6 +527,60 @@ MKV_DEV float load_q_operands(const DecodeArgs& a, int b, int kvh, Op16<KV_DT> (
 #pragma unroll
   for (int st = 0; st < 4; ++st) qop[st] = to_op16<KV_DT>(qf + 8 * st);
   return score_mul;
+}
+
+// q of item (b, kvh) loaded and converted on the spot (any q dtype).
+template <int KV_DT>
+MKV_DEV float load_q_operands(const DecodeArgs& a, int b, int kvh, Op16<KV_DT> (&qop)[4]) {
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+  float qf[32];
+  if (c < a.group) {
+    const int64_t qoff = (int64_t)b * a.q_stride + (int64_t)(kvh * a.group + c) * kHeadDim + 32 * kg;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) load_q8(a.q, a.q_dtype, qoff + 8 * i, qf + 8 * i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
+  }
+  return q_operands<KV_DT>(a, qf, qop);
+}
+
+// Raw 16-bit q of one item (dims 32kg .. 32kg+31 of head c), loaded a
+// pipeline step before the item's first tile is computed so that its latency
+// hides behind that tile's loads.
+struct QStage {
+  u32x4 w[4];
+};
+
+// Issue the q loads of item (b, kvh) for a bf16/fp16 q (unconditional buffer
+// loads; padding heads read zeros).
+MKV_DEV void load_q_stage(const DecodeArgs& a, int b, int kvh, QStage& qs) {
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+  const char* base = reinterpret_cast<const char*>(a.q) +
+                     ((int64_t)b * a.q_stride + (int64_t)kvh * a.group * kHeadDim) * 2;
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, a.group * kHeadDim * 2, kRsrcFlags);
+  const uint32_t off = c < a.group ? (uint32_t)((c * kHeadDim + 32 * kg) * 2) : kOob;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) qs.w[i] = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 0);
+}
+
+template <int KV_DT>
+MKV_DEV float staged_q_operands(const DecodeArgs& a, const QStage& qs, Op16<KV_DT> (&qop)[4]) {
+  float qf[32];
+  const bool bf = a.q_dtype == MKV_DTYPE_BF16;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t w = qs.w[i][j];
+      qf[8 * i + 2 * j] = bf ? bf16_bits_to_f32(w & 0xffffu) : f16_bits_to_f32(w & 0xffffu);
+      qf[8 * i + 2 * j + 1] = bf ? bf16_bits_to_f32(w >> 16) : f16_bits_to_f32(w >> 16);
+    }
+  }
+  return q_operands<KV_DT>(a, qf, qop);
 }
 
 template <int KV_DT>
@@ -594,6 +639,8 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(D
 constexpr int kTileTok = 32;
 constexpr int kStreamMaxBatch = 8192;
 constexpr size_t kStreamMaxLds = (2 * kStreamMaxBatch + 1) * sizeof(int);
+constexpr int kStreamSmallBatch = 2047;
+constexpr size_t kStreamSmallLds = (2 * kStreamSmallBatch + 1) * sizeof(int);
 
 struct Cursor {
   int b, kvh, t;  // item (sequence, KV head) and tile index inside the item
@@ -713,9 +760,9 @@ MKV_DEV void finish_sk(const DecodeArgs& a, const Cursor& c, bool whole, int w, 
 }
 
 // Per-sequence tile counts and their prefix into LDS (every workgroup does it;
-// workgroup 0 also publishes them for the merge kernel).  Returns the tiles
-// per wave.
-MKV_DEV int stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
+// workgroup 0 also publishes them for the merge kernel).  Returns the total
+// number of tiles of the stream.
+MKV_DEV int64_t stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
   __shared__ int part[kDecWaves * kWave];
   const int tid = threadIdx.x;
   const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
@@ -743,14 +790,63 @@ MKV_DEV int stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
   }
   if (tid == 0) pre[0] = 0;
   __syncthreads();
-  const int64_t total = (int64_t)running * a.num_kv_heads;
-  int per = (int)((total + a.num_waves - 1) / a.num_waves);
-  per = per < 1 ? 1 : per;
-  if (blockIdx.x == 0) {
+  if (blockIdx.x == 0)
     for (int i = tid; i <= a.batch; i += kDecWaves * kWave) a.sk_meta[i] = pre[i];
-    if (tid == 0) a.sk_meta[a.batch + 1] = per;
+  return (int64_t)running * a.num_kv_heads;
+}
+
+// Static split of the T tiles of the stream over the W waves: wave w runs the
+// contiguous range [begin(w), end(w)).  When two workgroups share each CU, the
+// two waves on a SIMD do not progress at the same rate: issue arbitration
+// favours the older wave, i.e. the one whose workgroup was dispatched in the
+// first round (workgroups 0 .. CUs-1).  Those first w1 waves therefore get
+// kFirstSharePct percent of the tiles and the second-round waves the rest;
+// with one workgroup per CU the split is even (w1 = W).
+constexpr int kFirstSharePct = 55;
+
+struct StreamSplit {
+  int64_t total;
+  int64_t base;  // tiles of the first group
+  int64_t per1, per2;
+  int w1, waves;
+
+  MKV_DEV int64_t begin(int w) const {
+    const int64_t b = w < w1 ? (int64_t)w * per1 : base + (int64_t)(w - w1) * per2;
+    const int64_t cap = w < w1 ? base : total;
+    return b < cap ? b : cap;
   }
-  return per;
+  MKV_DEV int64_t end(int w) const {
+    const int64_t e = w < w1 ? (int64_t)(w + 1) * per1 : base + (int64_t)(w - w1 + 1) * per2;
+    const int64_t cap = w < w1 ? base : total;
+    return e < cap ? e : cap;
+  }
+  MKV_DEV int wave_of(int64_t g) const {
+    return g < base ? (int)(g / per1) : w1 + (int)((g - base) / per2);
+  }
+};
+
+MKV_DEV StreamSplit make_split(int64_t total, int waves, int first_waves) {
+  StreamSplit p;
+  p.total = total;
+  p.waves = waves;
+  if (first_waves <= 0 || first_waves >= waves) {
+    p.w1 = waves;
+    p.per1 = (total + waves - 1) / waves;
+    p.per1 = p.per1 < 1 ? 1 : p.per1;
+    p.base = total;
+    p.per2 = 1;
+    return p;
+  }
+  p.w1 = first_waves;
+  const int64_t t1 = total * kFirstSharePct / 100;
+  p.per1 = (t1 + first_waves - 1) / first_waves;
+  p.per1 = p.per1 < 1 ? 1 : p.per1;
+  const int64_t head = (int64_t)first_waves * p.per1;
+  p.base = head < total ? head : total;
+  const int w2 = waves - first_waves;
+  p.per2 = (total - p.base + w2 - 1) / w2;
+  p.per2 = p.per2 < 1 ? 1 : p.per2;
+  return p;
 }
 
 template <int KV_DT>
@@ -759,14 +855,13 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(D
   extern __shared__ int sk_lds[];
   int* pre = sk_lds;                 // [batch + 1]
   int* lens = sk_lds + a.batch + 1;  // [batch]
-  const int per = stream_prefix(a, pre, lens);
+  const StreamSplit sp = make_split(stream_prefix(a, pre, lens), a.num_waves, a.first_waves);
 
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
   const int w = blockIdx.x * kDecWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t total = (int64_t)lds_uniform(pre, a.batch) * a.num_kv_heads;
-  const int64_t g0 = (int64_t)w * per;
-  const int64_t g1 = g0 + per < total ? g0 + per : total;
+  const int64_t g0 = sp.begin(w);
+  const int64_t g1 = sp.end(w);
   if (g0 >= g1) return;
 
   const int row_bytes = (int)(a.idx.row_elems * kEb);
@@ -788,13 +883,17 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(D
     lc.L = lg < g1 ? lc.L : 0;
     ph_next = tile_phys(a, lc);
   };
-  // Three register tiles: while tile g is computed, tiles g+1 and g+2 are in
-  // flight (about 16 KiB per wave for FP8).
-  Tile16<KV_DT> t0b, t1b, t2b;
+  // Two register tiles: while tile g is computed, tile g+1 is in flight.  Two
+  // waves share each SIMD (three tiles would push the FP8 kernel past the 256
+  // registers that allow it), so each SIMD still has two tiles in flight.
+  Tile16<KV_DT> t0b, t1b;
+  // q of the item whose tile was issued last (16-bit q; an fp32 q is loaded
+  // when its item starts).
+  QStage qs;
+  const bool q16 = a.q_dtype != MKV_DTYPE_F32;
   ph_next = tile_phys(a, lc);
   load_tile_sk<KV_DT>(a, lc, ph_next, row_bytes, blk_bytes, k_voff, v_voff, t0b);
-  advance_load();
-  load_tile_sk<KV_DT>(a, lc, ph_next, row_bytes, blk_bytes, k_voff, v_voff, t1b);
+  load_q_stage(a, lc.b, lc.kvh, qs);
   advance_load();
 
   Op16<KV_DT> qop[4];
@@ -803,18 +902,20 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(D
   float m_run = kNegBig, l_run = 0.0f;
   int64_t item_g0 = g0 - cc.t;  // global index of the current item's first tile
 
-  // One pipeline step: prefetch tile g+2 into `nxt`, compute tile g in `cur`.
+  // One pipeline step: prefetch tile g+1 into `nxt`, compute tile g in `cur`.
   auto step = [&](Tile16<KV_DT>& cur, Tile16<KV_DT>& nxt, int64_t g) {
     load_tile_sk<KV_DT>(a, lc, ph_next, row_bytes, blk_bytes, k_voff, v_voff, nxt);
-    advance_load();
     if (cc.t == 0 || g == g0) {  // a new item starts: its q, fresh softmax state
-      score_mul = load_q_operands<KV_DT>(a, cc.b, cc.kvh, qop);
+      score_mul = q16 ? staged_q_operands<KV_DT>(a, qs, qop)
+                      : load_q_operands<KV_DT>(a, cc.b, cc.kvh, qop);
 #pragma unroll
       for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
       m_run = kNegBig;
       l_run = 0.0f;
       item_g0 = g - cc.t;
     }
+    if (lc.t == 0) load_q_stage(a, lc.b, lc.kvh, qs);  // the tile just issued starts an item
+    advance_load();
     compute_tile16<KV_DT>(cur, cc.t * kTileTok, cc.L, qop, score_mul, acc, m_run, l_run);
     const bool item_end = cc.t == cc.n - 1;
     if (item_end || g == g1 - 1) {
@@ -826,11 +927,9 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(D
     cursor_next(cc, pre, lens, a.batch, a.num_kv_heads);
   };
   for (int64_t g = g0;;) {
-    step(t0b, t2b, g);
+    step(t0b, t1b, g);
     if (++g >= g1) break;
     step(t1b, t0b, g);
-    if (++g >= g1) break;
-    step(t2b, t1b, g);
     if (++g >= g1) break;
   }
 }
@@ -845,21 +944,22 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_ke
   const int hq = (int)(wv - (int64_t)b * a.num_heads);
   const int kvh = hq / a.group, h = hq - kvh * a.group;
   const int p0 = a.sk_meta[b], n = a.sk_meta[b + 1] - p0;
-  const int per = a.sk_meta[a.batch + 1];
+  const StreamSplit sp = make_split((int64_t)a.sk_meta[a.batch] * a.num_kv_heads, a.num_waves,
+                                    a.first_waves);
   const int64_t off = (int64_t)b * a.out_stride + (int64_t)hq * kHeadDim + 2 * lane;
   float o0 = 0.0f, o1 = 0.0f, l = 0.0f;
   if (n > 0) {
     const int64_t gs = (int64_t)p0 * a.num_kv_heads + (int64_t)kvh * n;
     const int64_t ge = gs + n;
-    const int64_t wlo = gs / per, whi = (ge - 1) / per;
+    const int wlo = sp.wave_of(gs), whi = sp.wave_of(ge - 1);
     if (wlo == whi) return;  // written whole by the main kernel
     float M = kNegBig;
-    for (int64_t wp = wlo; wp <= whi; ++wp) {
-      const int64_t slot = (wp * 2 + (gs <= wp * per ? 0 : 1)) * a.group + h;
+    for (int wp = wlo; wp <= whi; ++wp) {
+      const int64_t slot = ((int64_t)wp * 2 + (gs <= sp.begin(wp) ? 0 : 1)) * a.group + h;
       M = fmaxf(M, a.ws_ml[slot * 2]);
     }
-    for (int64_t wp = wlo; wp <= whi; ++wp) {
-      const int64_t slot = (wp * 2 + (gs <= wp * per ? 0 : 1)) * a.group + h;
+    for (int wp = wlo; wp <= whi; ++wp) {
+      const int64_t slot = ((int64_t)wp * 2 + (gs <= sp.begin(wp) ? 0 : 1)) * a.group + h;
       const float wgt = __builtin_amdgcn_exp2f(a.ws_ml[slot * 2] - M);
       l += wgt * a.ws_ml[slot * 2 + 1];
       const f32x2 x = *reinterpret_cast<const f32x2*>(a.ws_acc + slot * kHeadDim + 2 * lane);
@@ -1176,16 +1276,21 @@ extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void*
     a.ws_ml = a.ws_acc + slots * kHeadDim;
     a.sk_meta = reinterpret_cast<int*>(a.ws_ml + slots * 2);
     const dim3 block(kDecWaves * kWave);
+    // Residency depends on the launch's LDS (the per-sequence prefix): query it
+    // once per device for batches up to kStreamSmallBatch and once for larger.
+    const int lds_bucket = batch <= kStreamSmallBatch ? 0 : 1;
+    const size_t lds_bound = lds_bucket ? kStreamMaxLds : kStreamSmallLds;
 #define MKV_STREAM_LAUNCH(DT)                                                              \
   {                                                                                        \
-    static int per_cu[64];                                                                 \
+    static int per_cu[64][2];                                                              \
     int dev = 0;                                                                           \
     (void)hipGetDevice(&dev);                                                              \
     const int slot = dev >= 0 && dev < 64 ? dev : 0;                                       \
-    if (per_cu[slot] == 0)                                                                 \
-      per_cu[slot] = resident_wgs_per_cu(paged_decode_stream_kernel<DT>, kStreamMaxLds);   \
-    const int wgs = device_cus() * per_cu[slot];                                           \
+    if (per_cu[slot][lds_bucket] == 0)                                                     \
+      per_cu[slot][lds_bucket] = resident_wgs_per_cu(paged_decode_stream_kernel<DT>, lds_bound); \
+    const int wgs = device_cus() * per_cu[slot][lds_bucket];                               \
     a.num_waves = wgs * kDecWaves;                                                         \
+    a.first_waves = per_cu[slot][lds_bucket] > 1 ? device_cus() * kDecWaves : a.num_waves; \
     hipLaunchKernelGGL(paged_decode_stream_kernel<DT>, dim3(wgs), block, lds, s, a);       \
   }
     switch (kv_dtype) {
