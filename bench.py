@@ -206,8 +206,13 @@ def main() -> int:
     ms = time_launches(step, args.steps, args.warmup, stream)
     t_wall = time.perf_counter() - t_wall
     gbps = nbytes / (ms * 1e-3) / 1e9
-    split = mkv._lib.query("mkv_paged_decode_split_tokens", args.batch, Hkv, meta["max_blocks"], bs,
-                           args.split_tokens)
+    if args.split_tokens > 0 or args.batch > 8192:
+        split = mkv._lib.query("mkv_paged_decode_split_tokens", args.batch, Hkv, meta["max_blocks"], bs,
+                               args.split_tokens)
+        schedule = f"split-K, {split}-token splits (paged_decode_mfma16_kernel + paged_decode_merge_kernel)"
+    else:
+        schedule = ("stream-K over 32-token tiles, persistent grid "
+                    "(paged_decode_stream_kernel + paged_decode_stream_merge_kernel)")
 
     result = {
         "metric": METRIC,
@@ -229,12 +234,15 @@ def main() -> int:
                          f"({'per-tensor e4m3fn' if args.kv == 'fp8' else 'bf16'}), bf16 q/out, "
                          f"{args.layers} rotating layer pools"),
             "batch": args.batch, "num_heads": Hq, "num_kv_heads": Hkv, "head_dim": HEAD_DIM,
-            "block_size": bs, "split_tokens": split, "algorithmic_bytes_per_step": nbytes,
+            "block_size": bs, "schedule": schedule, "algorithmic_bytes_per_step": nbytes,
         },
         "roofline": {
             "bound": "hbm", "achieved": round(gbps, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
             "frac": round(gbps / PEAK_HBM_GBPS, 4),
-            "traffic": traffic_from_profiles(f"decode_b256_{args.kv}_pmc.json"),
+            # measured for the default workload only (profiles/decode_b256_<kv>_pmc.json)
+            "traffic": (traffic_from_profiles(f"decode_b256_{args.kv}_pmc.json")
+                        if (args.batch, Hq, Hkv, args.split_tokens) == (256, 32, 8, 0) else None),
+            "timed_unit": "one decode step: main kernel + its merge kernel, HIP events on the launch stream",
         },
         "wall_s_timed_region": round(t_wall, 3),
     }

@@ -6,7 +6,8 @@
  * reference) as hand-written HIP kernels:
  *
  *   K1  slot-mapped KV append, plain copy or fused per-tensor FP8 quantisation
- *   K2  paged decode attention (GQA-shared K/V tiles, split-K + LSE merge)
+ *   K2  paged decode attention (GQA-shared K/V tiles; stream-K or split-K,
+ *       partials merged by log-sum-exp)
  *   K3  paged / contiguous causal prefill attention on MFMA
  *   K4  block-table gather (shared device functions + a standalone kernel)
  *
@@ -145,10 +146,14 @@ int mkv_fp8_calibrate_per_tensor(const void* key, int64_t key_row_stride,
  * q_batch_stride / out_batch_stride elements; out has q's dtype.
  * block_tables: int32 (batch, bt_stride) with max_blocks usable columns.
  * head_dim == 128; num_heads / num_kv_heads in 1..16; block_size a power of
- * two >= 16.  kv_dtype F32 requires q_dtype F32.
+ * two >= 16.  q_dtype is F32, BF16 or F16 with any kv_dtype.
  *
- * split_tokens: tokens per split-K work item (multiple of 32; 0 = library
- * default).  workspace: >= mkv_paged_decode_workspace_size(...) bytes.
+ * split_tokens: 0 = the library's schedule (stream-K over 32-token tiles on
+ * a persistent grid for BF16/F16/FP8 KV and batch <= 8192, else split-K with
+ * a library-chosen split); > 0 = split-K with that many tokens per work item
+ * (a multiple of 32).  workspace: >= mkv_paged_decode_workspace_size(...)
+ * bytes with the same arguments; calls that share a workspace must be
+ * ordered on one stream.
  */
 size_t mkv_paged_decode_workspace_size(int batch, int num_heads,
                                        int num_kv_heads, int max_blocks,
@@ -184,7 +189,9 @@ int mkv_paged_decode(void* out, int64_t out_batch_stride,
  * block_tables as in K2 (-1 entries skipped).
  *
  * q, out: (total_q, num_heads, head_dim) contiguous.  positions: int64
- * (total_q).  cu_seqlens_q: int32 (num_seqs + 1).
+ * (total_q).  cu_seqlens_q: int32 (num_seqs + 1).  kv_dtype BF16, F16 or
+ * FP8E4M3 (an F32 cache returns MKV_ERR_UNSUPPORTED_DTYPE); q_dtype F32,
+ * BF16 or F16.
  * workspace: >= mkv_paged_prefill_workspace_size(...) bytes (tile list).
  */
 size_t mkv_paged_prefill_workspace_size(int num_seqs, int64_t total_q,
@@ -209,7 +216,8 @@ int mkv_paged_prefill(void* out, const void* q, int q_dtype,
  * Replaces flash_attention_prefill (attention.py:446-514, kernel :336-443).
  * Row i of sequence s attends to rows cu_seqlens[s] .. i of k/v.
  * q, out: (total, num_heads, head_dim); k, v: (total, num_kv_heads,
- * head_dim); all contiguous and of one dtype (F32, BF16 or F16).
+ * head_dim); all contiguous and of one dtype (BF16 or F16; F32 returns
+ * MKV_ERR_UNSUPPORTED_DTYPE).
  */
 size_t mkv_flash_prefill_workspace_size(int num_seqs, int64_t total,
                                         int num_heads, int num_kv_heads);

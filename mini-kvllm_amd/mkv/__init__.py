@@ -6,7 +6,7 @@ with the reference engine's Python call signatures:
 * :func:`store_kvcache`, :func:`store_kvcache_fp8` — slot-mapped append
   (plain copy or fused per-tensor FP8 e4m3fn quantisation);
 * :func:`paged_attention_decode`, :func:`paged_attention_decode_quantized` —
-  paged decode attention with GQA sharing and split-K;
+  paged decode attention with GQA sharing (stream-K or split-K);
 * :func:`paged_attention_prefill_triton`, :func:`flash_attention_prefill` —
   causal prefill over the paged cache / over fresh contiguous K/V;
 * :func:`gather_kv` — block-table gather;
@@ -17,12 +17,13 @@ from .attention import (FP8_E4M3_MAX, Attention, calibrate_fp8_per_tensor,
                         flash_attention_prefill, gather_kv, paged_attention_decode,
                         paged_attention_decode_quantized, paged_attention_prefill_triton,
                         store_kvcache, store_kvcache_fp8)
-from .context import (Context, MixedAttentionSplit, get_context, reset_context, set_context,
-                      split_mixed_decode_prefill_metadata)
+from .context import (Context, MixedAttentionSplit, current_context, get_context, reset_context,
+                      set_context, split_mixed_decode_prefill_metadata, use_context_provider)
 
 __all__ = [
     "FP8_E4M3_MAX", "Attention", "Context", "MixedAttentionSplit", "calibrate_fp8_per_tensor",
     "flash_attention_prefill", "gather_kv", "get_context", "paged_attention_decode",
     "paged_attention_decode_quantized", "paged_attention_prefill_triton", "reset_context",
     "set_context", "split_mixed_decode_prefill_metadata", "store_kvcache", "store_kvcache_fp8",
+    "current_context", "use_context_provider",
 ]

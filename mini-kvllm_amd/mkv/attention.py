@@ -29,7 +29,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
-from .context import get_context
+from .context import current_context
 
 FP8_E4M3_MAX = 448.0
 INT8_MAX = 127.0
@@ -421,7 +421,7 @@ class Attention(nn.Module):
             kv_cache_dtype=self.kv_cache_dtype)
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
-        context = get_context()
+        context = current_context()
         mode = self._mode()
         if self.k_cache.numel() > 0 and self.v_cache.numel() > 0 and context.slot_mapping is not None:
             if k.dim() == 4:

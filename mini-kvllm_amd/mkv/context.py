@@ -85,10 +85,25 @@ def split_mixed_decode_prefill_metadata(cu_seqlens_q: Sequence[int], query_lens:
 
 
 _context = Context()
+_provider = None
 
 
 def get_context() -> Context:
     return _context
+
+
+def use_context_provider(provider) -> None:
+    """Make :class:`mkv.Attention` read its per-step metadata from
+    ``provider()`` instead of this module's context, e.g. the engine's own
+    ``myvllm.utils.context.get_context`` (its Context has the same field
+    names).  ``None`` restores this module's context."""
+    global _provider
+    _provider = provider
+
+
+def current_context():
+    """The context :class:`mkv.Attention` uses for this step."""
+    return _provider() if _provider is not None else _context
 
 
 def reset_context() -> None:

@@ -151,3 +151,15 @@ def test_algorithmic_bytes():
     ctx = torch.tensor([512, 1000])
     n = W.alg_bytes_decode(ctx, 256, 32, 8, kv_bytes=1)
     assert n == 1512 * 8 * 128 * 2 + 2 * 32 * 128 * 4 + (2 + 4) * 4 + 2 * 8
+
+
+def test_context_provider_hook():
+    """Attention can read an engine-owned context object (same field names)."""
+    class EngineContext:
+        is_prefill = True
+    C.use_context_provider(lambda: EngineContext)
+    try:
+        assert C.current_context() is EngineContext
+    finally:
+        C.use_context_provider(None)
+    assert C.current_context() is C.get_context()
