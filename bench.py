@@ -51,7 +51,7 @@ def parse_args():
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--num-heads", type=int, default=32)
     ap.add_argument("--num-kv-heads", type=int, default=8)
-    ap.add_argument("--cpu-seqs", type=int, default=16,
+    ap.add_argument("--cpu-seqs", type=int, default=64,
                     help="sequences in the CPU-baseline sample (0 = skip the CPU baseline)")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary measurements")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -85,6 +85,78 @@ def time_launches(fn, steps: int, warmup: int, stream) -> float:
     end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
+
+
+def step_percentiles(fn, steps: int, stream) -> dict:
+    """p10/p50/p90 of single-step times (µs), one event pair per step."""
+    import torch
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        fn(i)
+        b.record(stream)
+    torch.cuda.synchronize()
+    t = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+    pick = lambda f: round(t[min(len(t) - 1, int(f * len(t)))], 2)
+    return {"p10_us": pick(0.1), "p50_us": pick(0.5), "p90_us": pick(0.9), "steps": steps}
+
+
+def box_copy_gbps(dev, stream, mib: int = 2048) -> float:
+    """Read+write bandwidth of a plain device copy on this GPU (a measured
+    on-box reference, next to the 8 TB/s datasheet peak)."""
+    import torch
+
+    src = torch.ones(mib << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    ms = time_launches(lambda i: dst.copy_(src), 10, 2, stream)
+    del src, dst
+    return 2 * (mib << 20) / (ms * 1e-3) / 1e9
+
+
+def prefill_extra(dev, stream) -> dict:
+    """Chunked prefill over the paged cache: the 8 prefill sequences of the
+    mixed-batch workload (prior context U[0, 4096], 512-row chunks), 32 q / 8
+    kv heads, bf16 q, bf16 and FP8 KV.  FLOPs are algorithmic (4*D per
+    visible key per row and head); peak is dense fp16/bf16 MFMA."""
+    import torch
+
+    from mkv import attention as A
+    from mkv import workloads as W
+
+    pm = W.prefill_mixed(seed=4)
+    sel = [i for i, d in enumerate(pm["is_decode"]) if not d]
+    cu = pm["cu_seqlens_q"]
+    rows = torch.cat([torch.arange(int(cu[i]), int(cu[i + 1])) for i in sel])
+    ctx = pm["context_lens"][sel]
+    bt = pm["block_tables"][sel]
+    pos = pm["positions"][rows]
+    cu_p = torch.zeros(len(sel) + 1, dtype=torch.int32)
+    cu_p[1:] = torch.cumsum(torch.tensor([pm["query_lens"][i] for i in sel]), 0)
+    flops = W.alg_flops_prefill(ctx, cu_p, pos, 32)
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(rows.numel(), 32, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    dev_meta = (bt.to(dev), ctx.to(dev), cu_p.to(dev), pos.to(dev))
+    out = {"workload": (f"{len(sel)} sequences x 512 query rows, prior context "
+                        f"{[int(c) - 512 for c in ctx]}, {flops / 1e9:.1f} GFLOP")}
+    for name, dt in (("bf16", torch.bfloat16), ("fp8", torch.float8_e4m3fn)):
+        kc = torch.empty(pm["num_blocks"], pm["block_size"], 8, HEAD_DIM, dtype=dt, device=dev)
+        vc = torch.empty_like(kc)
+        ks = W.fill_pool_on_device(kc, 400)
+        vs = W.fill_pool_on_device(vc, 401)
+        kw = {}
+        if name == "fp8":
+            kw = dict(k_scale=torch.tensor([ks], device=dev), v_scale=torch.tensor([vs], device=dev),
+                      kv_cache_dtype="fp8_per_tensor")
+        args = (q, kc, vc, *dev_meta[:2], dev_meta[2], dev_meta[3], 1.0 / math.sqrt(HEAD_DIM), 32, 8,
+                HEAD_DIM, pm["block_size"])
+        ms = time_launches(lambda i: A.paged_attention_prefill_triton(*args, **kw), 20, 3, stream)
+        tf = flops / (ms * 1e-3) / 1e12
+        out[f"{name}_kv"] = {"us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1),
+                             "frac_of_2500_TFLOPs": round(tf / 2500.0, 4)}
+        del kc, vc
+    return out
 
 
 def cpu_baseline(kcs, vcs, scale_kv, q, meta, n_seqs: int) -> dict:
@@ -206,6 +278,7 @@ def main() -> int:
     ms = time_launches(step, args.steps, args.warmup, stream)
     t_wall = time.perf_counter() - t_wall
     gbps = nbytes / (ms * 1e-3) / 1e9
+    pct = step_percentiles(step, 100, stream)
     if args.split_tokens > 0 or args.batch > 8192:
         split = mkv._lib.query("mkv_paged_decode_split_tokens", args.batch, Hkv, meta["max_blocks"], bs,
                                args.split_tokens)
@@ -245,6 +318,7 @@ def main() -> int:
             "timed_unit": "one decode step: main kernel + its merge kernel, HIP events on the launch stream",
         },
         "wall_s_timed_region": round(t_wall, 3),
+        "step_time": pct,
     }
 
     if not args.no_extra:
@@ -267,6 +341,10 @@ def main() -> int:
             ab = W.alg_bytes_append(w["slot_mapping"], 8, 2, 1)
             extra[f"append_fp8_T{T}"] = {"us": round(ams * 1e3, 2), "GBps": round(ab / ams / 1e6, 1)}
             del kp, vp
+        extra["prefill_chunked"] = prefill_extra(dev, stream)
+        copy = box_copy_gbps(dev, stream)
+        extra["box_copy_GBps"] = round(copy, 1)
+        extra["decode_frac_of_box_copy"] = round(gbps / copy, 4)
         result["extra"] = extra
 
     if args.cpu_seqs > 0:

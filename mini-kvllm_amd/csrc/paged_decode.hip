@@ -553,15 +553,19 @@ struct QStage {
   u32x4 w[4];
 };
 
-// Issue the q loads of item (b, kvh) for a bf16/fp16 q (unconditional buffer
-// loads; padding heads read zeros).
-MKV_DEV void load_q_stage(const DecodeArgs& a, int b, int kvh, QStage& qs) {
+// Issue the q loads of item (b, kvh) for a bf16/fp16 q; padding heads read
+// zeros.  With need == false the same four loads are issued with an empty
+// range (nothing is read), so the stream of memory instructions is the same on
+// every pipeline step: a load issued on only some steps makes the wait-count
+// pass assume the worst at the join and wait for it, i.e. for a full memory
+// round trip, before the next tile.
+MKV_DEV void load_q_stage(const DecodeArgs& a, int b, int kvh, bool need, QStage& qs) {
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
   const char* base = reinterpret_cast<const char*>(a.q) +
                      ((int64_t)b * a.q_stride + (int64_t)kvh * a.group * kHeadDim) * 2;
-  const __amdgpu_buffer_rsrc_t r =
-      __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, a.group * kHeadDim * 2, kRsrcFlags);
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)base, (short)0, need ? a.group * kHeadDim * 2 : 0, kRsrcFlags);
   const uint32_t off = c < a.group ? (uint32_t)((c * kHeadDim + 32 * kg) * 2) : kOob;
 #pragma unroll
   for (int i = 0; i < 4; ++i) qs.w[i] = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 0);
@@ -759,6 +763,96 @@ MKV_DEV void finish_sk(const DecodeArgs& a, const Cursor& c, bool whole, int w, 
   }
 }
 
+// Finish of an item for groups of at most 4 query heads, issued as exactly
+// three buffer stores on every pipeline step (an unused store gets an empty
+// range and writes nothing), for the same reason as load_q_stage's need flag.
+// Heads live in lane group 0 (head r in acc[.][r]); four shuffles per output
+// register spread head r to lane group r, so one 16-byte store per lane covers
+// all heads.  Store A/B: the output (bf16/fp16: A only; fp32: A and B) or the
+// fp32 partial accumulator; store C: the partial's (m, l).
+struct FinishStores {
+  __amdgpu_buffer_rsrc_t ra, rc;
+  uint32_t oa, ob, oc;
+  u32x4 da, db;
+  u32x2 dc;
+};
+
+MKV_DEV void finish_none(FinishStores& f) {
+  f.ra = __builtin_amdgcn_make_buffer_rsrc(nullptr, (short)0, 0, kRsrcFlags);
+  f.rc = f.ra;
+  f.oa = f.ob = f.oc = kOob;
+}
+
+MKV_DEV void finish_small_group(const DecodeArgs& a, const Cursor& c, bool whole, int w, int k,
+                                const f32x4 (&acc)[8], float m_col, float l_col, float v_mul,
+                                FinishStores& f) {
+  const int lane = threadIdx.x & 63;
+  const int cc = lane & 15, h = lane >> 4;  // this lane's head after the spread
+  float x[8];
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm) {
+    const float t0 = __shfl(acc[mm][0], cc), t1 = __shfl(acc[mm][1], cc);
+    const float t2 = __shfl(acc[mm][2], cc), t3 = __shfl(acc[mm][3], cc);
+    x[mm] = h == 0 ? t0 : (h == 1 ? t1 : (h == 2 ? t2 : t3));
+  }
+  const float lh = __shfl(l_col, h);
+  const float mh = __shfl(m_col, h);
+  const bool valid = h < a.group;
+  if (whole) {
+    const float inv = lh > 0.0f ? v_mul / lh : 0.0f;
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm) x[mm] *= inv;
+    const int ob = a.q_dtype == MKV_DTYPE_F32 ? 4 : 2;
+    const char* base = reinterpret_cast<const char*>(a.out) +
+                       ((int64_t)c.b * a.out_stride + (int64_t)c.kvh * a.group * kHeadDim) * ob;
+    f.ra = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, a.group * kHeadDim * ob, kRsrcFlags);
+    const uint32_t off = (uint32_t)((h * kHeadDim + 8 * cc) * ob);
+    if (a.q_dtype == MKV_DTYPE_F32) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f.da[j] = __float_as_uint(x[j]);
+        f.db[j] = __float_as_uint(x[4 + j]);
+      }
+      f.oa = valid ? off : kOob;
+      f.ob = valid ? off + 16 : kOob;
+    } else {
+      const bool bf = a.q_dtype == MKV_DTYPE_BF16;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = bf ? f32_to_bf16_bits(x[2 * j]) : f32_to_f16_bits(x[2 * j]);
+        const uint32_t hi = bf ? f32_to_bf16_bits(x[2 * j + 1]) : f32_to_f16_bits(x[2 * j + 1]);
+        f.da[j] = lo | (hi << 16);
+      }
+      f.oa = valid ? off : kOob;
+      f.ob = kOob;
+    }
+    f.rc = f.ra;
+    f.oc = kOob;
+  } else {
+    const int64_t slot0 = ((int64_t)w * 2 + k) * a.group;
+    f.ra = __builtin_amdgcn_make_buffer_rsrc((void*)(a.ws_acc + slot0 * kHeadDim), (short)0,
+                                             a.group * kHeadDim * 4, kRsrcFlags);
+    f.rc = __builtin_amdgcn_make_buffer_rsrc((void*)(a.ws_ml + slot0 * 2), (short)0, a.group * 8,
+                                             kRsrcFlags);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f.da[j] = __float_as_uint(x[j]);
+      f.db[j] = __float_as_uint(x[4 + j]);
+    }
+    const uint32_t off = (uint32_t)((h * kHeadDim + 8 * cc) * 4);
+    f.oa = valid ? off : kOob;
+    f.ob = valid ? off + 16 : kOob;
+    f.dc = u32x2{__float_as_uint(mh), __float_as_uint(lh)};
+    f.oc = valid && cc == 0 ? (uint32_t)(h * 8) : kOob;
+  }
+}
+
+MKV_DEV void issue_finish(const FinishStores& f) {
+  __builtin_amdgcn_raw_buffer_store_b128(f.da, f.ra, f.oa, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(f.db, f.ra, f.ob, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b64(f.dc, f.rc, f.oc, 0, 0);
+}
+
 // Per-sequence tile counts and their prefix into LDS (every workgroup does it;
 // workgroup 0 also publishes them for the merge kernel).  Returns the total
 // number of tiles of the stream.
@@ -849,7 +943,7 @@ MKV_DEV StreamSplit make_split(int64_t total, int waves, int first_waves) {
   return p;
 }
 
-template <int KV_DT>
+template <int KV_DT, bool kSmallGroup>
 __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(DecodeArgs a) {
   constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
   extern __shared__ int sk_lds[];
@@ -893,7 +987,7 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(D
   const bool q16 = a.q_dtype != MKV_DTYPE_F32;
   ph_next = tile_phys(a, lc);
   load_tile_sk<KV_DT>(a, lc, ph_next, row_bytes, blk_bytes, k_voff, v_voff, t0b);
-  load_q_stage(a, lc.b, lc.kvh, qs);
+  load_q_stage(a, lc.b, lc.kvh, true, qs);
   advance_load();
 
   Op16<KV_DT> qop[4];
@@ -914,15 +1008,27 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(D
       l_run = 0.0f;
       item_g0 = g - cc.t;
     }
-    if (lc.t == 0) load_q_stage(a, lc.b, lc.kvh, qs);  // the tile just issued starts an item
+    // q of the item that the tile just issued starts (an empty load otherwise)
+    load_q_stage(a, lc.b, lc.kvh, lc.t == 0, qs);
     advance_load();
     compute_tile16<KV_DT>(cur, cc.t * kTileTok, cc.L, qop, score_mul, acc, m_run, l_run);
     const bool item_end = cc.t == cc.n - 1;
-    if (item_end || g == g1 - 1) {
+    const bool fin = item_end || g == g1 - 1;
+    const bool whole = item_end && item_g0 >= g0;
+    const int kslot = item_g0 <= g0 ? 0 : 1;
+    if constexpr (kSmallGroup) {
+      FinishStores fs;
+      finish_none(fs);
+      if (fin) {
+        float l_col = l_run + __shfl_xor(l_run, 16);
+        l_col += __shfl_xor(l_col, 32);
+        finish_small_group(a, cc, whole, w, kslot, acc, m_run, l_col, v_mul, fs);
+      }
+      issue_finish(fs);
+    } else if (fin) {
       float l_col = l_run + __shfl_xor(l_run, 16);
       l_col += __shfl_xor(l_col, 32);
-      const bool whole = item_end && item_g0 >= g0;
-      finish_sk(a, cc, whole, w, item_g0 <= g0 ? 0 : 1, acc, m_run, l_col, v_mul);
+      finish_sk(a, cc, whole, w, kslot, acc, m_run, l_col, v_mul);
     }
     cursor_next(cc, pre, lens, a.batch, a.num_kv_heads);
   };
@@ -1168,6 +1274,24 @@ size_t stream_ws_bytes(int batch, int group) {
   return w * 2 * group * (kHeadDim + 2) * sizeof(float) + (size_t)(batch + 2) * sizeof(int);
 }
 
+// Persistent stream-K launch: one wave per SIMD slot the kernel can hold
+// (residency cached per device and LDS bucket), the first dispatch round
+// marked for the uneven split.
+template <int DT, bool SMALL>
+void launch_stream(DecodeArgs& a, int lds_bucket, size_t lds_bound, size_t lds, hipStream_t s) {
+  static int per_cu[64][2];
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  const int slot = dev >= 0 && dev < 64 ? dev : 0;
+  if (per_cu[slot][lds_bucket] == 0)
+    per_cu[slot][lds_bucket] = resident_wgs_per_cu(paged_decode_stream_kernel<DT, SMALL>, lds_bound);
+  const int wgs = device_cus() * per_cu[slot][lds_bucket];
+  a.num_waves = wgs * kDecWaves;
+  a.first_waves = per_cu[slot][lds_bucket] > 1 ? device_cus() * kDecWaves : a.num_waves;
+  hipLaunchKernelGGL((paged_decode_stream_kernel<DT, SMALL>), dim3(wgs), dim3(kDecWaves * kWave), lds,
+                     s, a);
+}
+
 size_t split_ws_bytes(int batch, int num_heads, int max_blocks, int block_size, int st) {
   const int64_t max_splits = ((int64_t)max_blocks * block_size + st - 1) / st;
   if (max_splits <= 1) return 0;
@@ -1280,25 +1404,21 @@ extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void*
     // once per device for batches up to kStreamSmallBatch and once for larger.
     const int lds_bucket = batch <= kStreamSmallBatch ? 0 : 1;
     const size_t lds_bound = lds_bucket ? kStreamMaxLds : kStreamSmallLds;
-#define MKV_STREAM_LAUNCH(DT)                                                              \
-  {                                                                                        \
-    static int per_cu[64][2];                                                              \
-    int dev = 0;                                                                           \
-    (void)hipGetDevice(&dev);                                                              \
-    const int slot = dev >= 0 && dev < 64 ? dev : 0;                                       \
-    if (per_cu[slot][lds_bucket] == 0)                                                     \
-      per_cu[slot][lds_bucket] = resident_wgs_per_cu(paged_decode_stream_kernel<DT>, lds_bound); \
-    const int wgs = device_cus() * per_cu[slot][lds_bucket];                               \
-    a.num_waves = wgs * kDecWaves;                                                         \
-    a.first_waves = per_cu[slot][lds_bucket] > 1 ? device_cus() * kDecWaves : a.num_waves; \
-    hipLaunchKernelGGL(paged_decode_stream_kernel<DT>, dim3(wgs), block, lds, s, a);       \
-  }
+    const bool small = group <= 4;
     switch (kv_dtype) {
-      case MKV_DTYPE_FP8E4M3: MKV_STREAM_LAUNCH(MKV_DTYPE_FP8E4M3) break;
-      case MKV_DTYPE_BF16: MKV_STREAM_LAUNCH(MKV_DTYPE_BF16) break;
-      default: MKV_STREAM_LAUNCH(MKV_DTYPE_F16) break;
+      case MKV_DTYPE_FP8E4M3:
+        small ? launch_stream<MKV_DTYPE_FP8E4M3, true>(a, lds_bucket, lds_bound, lds, s)
+              : launch_stream<MKV_DTYPE_FP8E4M3, false>(a, lds_bucket, lds_bound, lds, s);
+        break;
+      case MKV_DTYPE_BF16:
+        small ? launch_stream<MKV_DTYPE_BF16, true>(a, lds_bucket, lds_bound, lds, s)
+              : launch_stream<MKV_DTYPE_BF16, false>(a, lds_bucket, lds_bound, lds, s);
+        break;
+      default:
+        small ? launch_stream<MKV_DTYPE_F16, true>(a, lds_bucket, lds_bound, lds, s)
+              : launch_stream<MKV_DTYPE_F16, false>(a, lds_bucket, lds_bound, lds, s);
+        break;
     }
-#undef MKV_STREAM_LAUNCH
     const int64_t mitems = (int64_t)batch * num_heads;
     hipLaunchKernelGGL(paged_decode_stream_merge_kernel,
                        dim3((unsigned)((mitems + kDecWaves - 1) / kDecWaves)), dim3(kDecWaves * kWave), 0,

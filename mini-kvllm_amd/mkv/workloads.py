@@ -188,6 +188,17 @@ def alg_bytes_decode(context_lens: torch.Tensor, block_size: int, num_heads: int
     return kv + qo + bt + int(L.numel()) * ctx_bytes
 
 
+def alg_flops_prefill(context_lens: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                      positions: torch.Tensor, num_heads: int) -> int:
+    """Algorithmic FLOPs of one causal paged prefill: every (query row, head)
+    attends to visible = min(context_len, position + 1) keys, 2*D for
+    S = q.K and 2*D for O += p.V per key."""
+    cu = cu_seqlens_q.to(torch.int64)
+    seq_of_row = torch.repeat_interleave(torch.arange(cu.numel() - 1), cu[1:] - cu[:-1])
+    vis = torch.minimum(context_lens.to(torch.int64)[seq_of_row], positions.to(torch.int64) + 1)
+    return int(vis.clamp(min=0).sum()) * num_heads * 4 * HEAD_DIM
+
+
 def alg_bytes_append(slot_mapping: torch.Tensor, num_kv_heads: int, in_bytes: int,
                      out_bytes: int) -> int:
     """Algorithmic bytes of one append: each valid K and V row read once and
