@@ -172,6 +172,15 @@ MKV_DEV int64_t load_index(const void* p, int64_t i, int is_i64) {
 
 MKV_DEV int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// A wave-uniform fp32 that no kernel writes (e.g. a per-tensor scale), read
+// through the constant address space so that it becomes a scalar load: a
+// vector load consumed at once would make the wave wait for every load it has
+// in flight.
+MKV_DEV float load_uniform_f32(const float* p) {
+  typedef const float __attribute__((address_space(4))) const_f32;
+  return *((const_f32*)p);
+}
+
 // ---------------------------------------------------------------------------
 // K4: block-table gather.  Logical token t of sequence b lives in physical
 // block block_tables[b, t >> log2(bs)] at offset t & (bs - 1).  An entry of -1

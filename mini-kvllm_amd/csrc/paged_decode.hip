@@ -508,9 +508,8 @@ MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const O
 // of two so q is exact and in range; k_scale (FP8) and sm_scale*log2(e) stay
 // in fp32.
 template <int KV_DT>
-MKV_DEV float q_operands(const DecodeArgs& a, float (&qf)[32], Op16<KV_DT> (&qop)[4]) {
-  float score_mul = a.sm_scale * kLog2e;
-  if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) score_mul *= *a.k_scale;
+MKV_DEV float q_operands(const DecodeArgs& a, float (&qf)[32], Op16<KV_DT> (&qop)[4], float k_mul) {
+  float score_mul = a.sm_scale * kLog2e * k_mul;
   if constexpr (KV_DT != MKV_DTYPE_BF16) {
     float qm = 0.0f;
 #pragma unroll
@@ -529,9 +528,10 @@ MKV_DEV float q_operands(const DecodeArgs& a, float (&qf)[32], Op16<KV_DT> (&qop
   return score_mul;
 }
 
-// q of item (b, kvh) loaded and converted on the spot (any q dtype).
+// q of item (b, kvh) loaded and converted on the spot (any q dtype).  k_mul:
+// the K dequantisation scale (1 for 16-bit caches).
 template <int KV_DT>
-MKV_DEV float load_q_operands(const DecodeArgs& a, int b, int kvh, Op16<KV_DT> (&qop)[4]) {
+MKV_DEV float load_q_operands(const DecodeArgs& a, int b, int kvh, Op16<KV_DT> (&qop)[4], float k_mul) {
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
   float qf[32];
@@ -543,7 +543,7 @@ MKV_DEV float load_q_operands(const DecodeArgs& a, int b, int kvh, Op16<KV_DT> (
 #pragma unroll
     for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
   }
-  return q_operands<KV_DT>(a, qf, qop);
+  return q_operands<KV_DT>(a, qf, qop, k_mul);
 }
 
 // Raw 16-bit q of one item (dims 32kg .. 32kg+31 of head c), loaded a
@@ -572,7 +572,7 @@ MKV_DEV void load_q_stage(const DecodeArgs& a, int b, int kvh, bool need, QStage
 }
 
 template <int KV_DT>
-MKV_DEV float staged_q_operands(const DecodeArgs& a, const QStage& qs, Op16<KV_DT> (&qop)[4]) {
+MKV_DEV float staged_q_operands(const DecodeArgs& a, const QStage& qs, Op16<KV_DT> (&qop)[4], float k_mul) {
   float qf[32];
   const bool bf = a.q_dtype == MKV_DTYPE_BF16;
 #pragma unroll
@@ -584,7 +584,7 @@ MKV_DEV float staged_q_operands(const DecodeArgs& a, const QStage& qs, Op16<KV_D
       qf[8 * i + 2 * j + 1] = bf ? bf16_bits_to_f32(w >> 16) : f16_bits_to_f32(w >> 16);
     }
   }
-  return q_operands<KV_DT>(a, qf, qop);
+  return q_operands<KV_DT>(a, qf, qop, k_mul);
 }
 
 template <int KV_DT>
@@ -592,7 +592,8 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(D
   WorkItem it;
   if (!decode_work_item(a, wave_work_index(), it)) return;
   Op16<KV_DT> qop[4];
-  const float score_mul = load_q_operands<KV_DT>(a, it.b, it.kvh, qop);
+  const float k_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.k_scale) : 1.0f;
+  const float score_mul = load_q_operands<KV_DT>(a, it.b, it.kvh, qop, k_mul);
 
   f32x4 acc[8];
 #pragma unroll
@@ -622,7 +623,7 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(D
   }
   float l_col = l_run + __shfl_xor(l_run, 16);
   l_col += __shfl_xor(l_col, 32);
-  const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? *a.v_scale : 1.0f;
+  const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
   finish_item(a, it, acc, m_run, l_col, v_mul);
 }
 
@@ -896,7 +897,7 @@ MKV_DEV int64_t stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
 // first round (workgroups 0 .. CUs-1).  Those first w1 waves therefore get
 // kFirstSharePct percent of the tiles and the second-round waves the rest;
 // with one workgroup per CU the split is even (w1 = W).
-constexpr int kFirstSharePct = 55;
+constexpr int kFirstSharePct = 58;
 
 struct StreamSplit {
   int64_t total;
@@ -962,7 +963,8 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(D
   const int64_t blk_bytes = (int64_t)row_bytes << a.idx.bs_log2;
   const int k_voff = c * row_bytes + 32 * kg * kEb;
   const int v_voff = 4 * kg * row_bytes + 8 * c * kEb;
-  const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? *a.v_scale : 1.0f;
+  const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
+  const float k_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.k_scale) : 1.0f;
 
   Cursor cc = cursor_at(pre, lens, a.batch, a.num_kv_heads, g0);  // tile being computed
   Cursor lc = cc;                                                  // next tile to load
@@ -1000,8 +1002,8 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(D
   auto step = [&](Tile16<KV_DT>& cur, Tile16<KV_DT>& nxt, int64_t g) {
     load_tile_sk<KV_DT>(a, lc, ph_next, row_bytes, blk_bytes, k_voff, v_voff, nxt);
     if (cc.t == 0 || g == g0) {  // a new item starts: its q, fresh softmax state
-      score_mul = q16 ? staged_q_operands<KV_DT>(a, qs, qop)
-                      : load_q_operands<KV_DT>(a, cc.b, cc.kvh, qop);
+      score_mul = q16 ? staged_q_operands<KV_DT>(a, qs, qop, k_mul)
+                      : load_q_operands<KV_DT>(a, cc.b, cc.kvh, qop, k_mul);
 #pragma unroll
       for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
       m_run = kNegBig;
@@ -1073,7 +1075,7 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_ke
       o1 += wgt * x[1];
     }
   }
-  const float inv = l > 0.0f ? (kv_fp8 ? *a.v_scale : 1.0f) / l : 0.0f;
+  const float inv = l > 0.0f ? (kv_fp8 ? load_uniform_f32(a.v_scale) : 1.0f) / l : 0.0f;
   if (a.q_dtype == MKV_DTYPE_F32) {
     *reinterpret_cast<f32x2*>(reinterpret_cast<float*>(a.out) + off) = f32x2{o0 * inv, o1 * inv};
   } else {
@@ -1204,7 +1206,7 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_merge_kernel(De
     o0 += wgt * x[0];
     o1 += wgt * x[1];
   }
-  const float inv = l > 0.0f ? (kv_fp8 ? *a.v_scale : 1.0f) / l : 0.0f;
+  const float inv = l > 0.0f ? (kv_fp8 ? load_uniform_f32(a.v_scale) : 1.0f) / l : 0.0f;
   const int64_t off = (int64_t)b * a.out_stride + (int64_t)hq * kHeadDim + 2 * lane;
   if (a.q_dtype == MKV_DTYPE_F32) {
     *reinterpret_cast<f32x2*>(reinterpret_cast<float*>(a.out) + off) = f32x2{o0 * inv, o1 * inv};

@@ -280,7 +280,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(PrefillArgs a)
     for (int i = 0; i < 32; ++i) qmax = fmaxf(qmax, fabsf(qf[rt][i]));
   }
   float score_mul = a.sm_scale * kLog2e;
-  if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) score_mul *= *a.k_scale;
+  if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) score_mul *= load_uniform_f32(a.k_scale);
   if constexpr (KV_DT != MKV_DTYPE_BF16) {
     // power-of-two normalisation so that q is exact and in range in fp16
 #pragma unroll
@@ -509,7 +509,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(PrefillArgs a)
 #undef KBUF
 #undef VBUF
   // ---- normalise and write rows 4kg + r of each row tile ----
-  const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? *a.v_scale : 1.0f;
+  const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt) {
     float l_col = l_run[rt] + __shfl_xor(l_run[rt], 16);
