@@ -27,13 +27,14 @@ namespace mkv {
 namespace {
 
 constexpr int kHeadDim = 128;
-constexpr int kPfWaves = 4;
+constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * kWave;
-constexpr int kRowTiles = 2;                       // 16-row MFMA tiles per wave
+constexpr int kRowTiles = 1;                       // 16-row MFMA tiles per wave
 constexpr int kRowsPerWg = kPfWaves * kRowTiles * 16;  // 128
 constexpr int kBN = 64;                            // keys per LDS tile
 constexpr int kXcds = 8;
 constexpr float kNegBig = -1e30f;
+constexpr float kRescaleSlack = 8.0f;
 
 struct PrefillArgs {
   void* out;
@@ -169,25 +170,6 @@ struct LdsTile {
   }
 };
 
-// Source of key rows: paged (through the block table) or contiguous.
-template <bool PAGED>
-struct KeySource {
-  const char* base;  // k or v
-  int64_t row_bytes_stride;  // bytes between consecutive token rows (contiguous)
-  int64_t head_bytes;        // byte offset of this kv head inside a token row
-  // byte offset of key t's head slice, or -1 when absent
-  MKV_DEV int64_t key_offset(const PrefillArgs& a, int seq, int64_t seq_row0, int64_t t,
-                             int eb) const {
-    if constexpr (PAGED) {
-      const int64_t phys = a.idx.physical_block(seq, t >> a.idx.bs_log2);
-      if (phys < 0) return -1;
-      return a.idx.row_offset(phys, t) * eb + head_bytes;
-    } else {
-      return (seq_row0 + t) * row_bytes_stride + head_bytes;
-    }
-  }
-};
-
 template <int KV_DT, bool PAGED>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(PrefillArgs a) {
   using LT = LdsTile<KV_DT>;
@@ -313,39 +295,93 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(PrefillArgs a)
     l_run[rt] = 0.0f;
   }
 
-  KeySource<PAGED> ksrc, vsrc;
-  ksrc.base = a.k;
-  vsrc.base = a.v;
-  ksrc.row_bytes_stride = vsrc.row_bytes_stride = (int64_t)a.num_kv_heads * kHeadDim * kEb;
-  ksrc.head_bytes = vsrc.head_bytes = (int64_t)kvh * kHeadDim * kEb;
+  // K/V staging.  A 16-key sub-tile never straddles a cache block (block
+  // size >= 16), so every 16-byte load instruction reads one sub-tile through
+  // a wave-uniform buffer descriptor (one scalar block-table lookup); the
+  // per-lane offsets are loop-invariant, and keys at or past max_vis, or in
+  // an absent block, read zeros (P is 0 there and V must stay finite).
+  // The 8 sub-tiles of a tile (K 0-3, V 4-7) are dealt to the workgroup's
+  // lanes in slots of 16 keys x kChunks chunks: slot = u * kSlotsPerLoad +
+  // tid / kLanesPerSlot for load u; lane: key tid%kLanesPerSlot/kChunks,
+  // chunk tid%kChunks.
+  constexpr int kLanesPerSlot = 16 * LT::kChunks;            // 256 (16-bit) / 128 (FP8)
+  constexpr int kSlotsPerLoad = kPfThreads / kLanesPerSlot;
+  constexpr int kLoads = 8 / kSlotsPerLoad;
+  const int64_t row_stride = (int64_t)a.num_kv_heads * kHeadDim * kEb;
+  const int64_t head_bytes = (int64_t)kvh * kHeadDim * kEb;
+  const int ld_key = (tid % kLanesPerSlot) / LT::kChunks;
+  const int ld_ch = tid % LT::kChunks;
+  const uint32_t ld_off = (uint32_t)(ld_key * row_stride + 16 * ld_ch);
+  int lds_off[kLoads];
+  int ld_slot[kLoads];  // wave-uniform
+#pragma unroll
+  for (int u = 0; u < kLoads; ++u) {
+    ld_slot[u] = __builtin_amdgcn_readfirstlane(u * kSlotsPerLoad + tid / kLanesPerSlot);
+    lds_off[u] = LT::offset(16 * (ld_slot[u] & 3) + ld_key, ld_ch);
+  }
 
-  // Global -> register staging of one K/V tile (kChunksPerThread 16-byte
-  // chunks each), then register -> LDS.
-  u32x4 kst[LT::kChunksPerThread], vst[LT::kChunksPerThread];
+  // Descriptor of rows t0 .. t0+15 of one tensor (t0 a multiple of 16).
+  auto sub_rsrc = [&](const char* base, int64_t t0) -> __amdgpu_buffer_rsrc_t {
+    const char* p = base;
+    int num = 0;
+    if constexpr (PAGED) {
+      const int64_t phys = a.idx.physical_block(seq, t0 >> a.idx.bs_log2);
+      const int64_t bmask = ((int64_t)1 << a.idx.bs_log2) - 1;
+      if (phys >= 0) {
+        p = base + (phys << a.idx.bs_log2) * row_stride + (t0 & bmask) * row_stride + head_bytes;
+        num = (int)(15 * row_stride + kHeadDim * kEb);
+      }
+    } else {
+      p = base + (q_seq0 + t0) * row_stride + head_bytes;
+      num = (int)(15 * row_stride + kHeadDim * kEb);
+    }
+    return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, num, 0x00020000);
+  };
+  u32x4 stg[kLoads];
   auto load_tile = [&](int kb) {
 #pragma unroll
-    for (int j = 0; j < LT::kChunksPerThread; ++j) {
-      const int i = tid + kPfThreads * j;
-      const int key = i / LT::kChunks, ch = i % LT::kChunks;
-      const int64_t t = kb + key;
-      int64_t ko = -1, vo = -1;
-      if (t < max_vis) {
-        ko = ksrc.key_offset(a, seq, q_seq0, t, kEb);
-        vo = ko < 0 ? -1 : vsrc.key_offset(a, seq, q_seq0, t, kEb);
-      }
-      kst[j] = ko >= 0 ? ld16(a.k + ko + 16 * ch) : u32x4{0, 0, 0, 0};
-      vst[j] = vo >= 0 ? ld16(a.v + vo + 16 * ch) : u32x4{0, 0, 0, 0};
+    for (int u = 0; u < kLoads; ++u) {
+      const int j = ld_slot[u] & 3;
+      const bool is_v = ld_slot[u] >= 4;
+      const int64_t t0 = kb + 16 * j;
+      const __amdgpu_buffer_rsrc_t r = sub_rsrc(is_v ? a.v : a.k, t0);
+      const uint32_t off = (t0 + ld_key < max_vis) ? ld_off : 0x80000000u;
+      stg[u] = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     }
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < LT::kChunksPerThread; ++j) {
-      const int i = tid + kPfThreads * j;
-      const int key = i / LT::kChunks, ch = i % LT::kChunks;
-      *reinterpret_cast<u32x4*>(KBUF(buf) + LT::offset(key, ch)) = kst[j];
-      *reinterpret_cast<u32x4*>(VBUF(buf) + LT::offset(key, ch)) = vst[j];
+    for (int u = 0; u < kLoads; ++u) {
+      const bool is_v = ld_slot[u] >= 4;
+      char* dst = is_v ? VBUF(buf) : KBUF(buf);
+      *reinterpret_cast<u32x4*>(dst + lds_off[u]) = stg[u];
     }
   };
+
+  // Transposed V reads.  ds_read_b64_tr_b16: within each 16-lane group, lane
+  // d receives element d%4 of the 8-byte reads of lanes 4i + d/4 (i = 0..3);
+  // ds_read_b64_tr_b8: byte d%8 of the reads of lanes 2i + d/8 (i = 0..7).
+  // So if lane 4i + q (16-bit) / 2i + p (FP8) of lane group kg reads key
+  // k(kg, i) at dims 16mm + 4q / 16mm + 8p, lane c receives V[k(kg, i)][16mm
+  // + c] for the lane group's MFMA k-slice, where the P operand holds keys
+  // k(kg, j) = 32ks + 16*(j/4) + 4kg + j%4.  vt_off[mm]: that address in a V
+  // tile for ks = 0 (and, 16-bit, the first half j < 4; +16 rows for j >= 4).
+  int vt_off[8];
+  {
+    const int s16 = lane & 15;
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm) {
+      if constexpr (kEb == 2) {
+        const int i = s16 >> 2, q = s16 & 3;
+        const int key = 4 * kg + i;
+        vt_off[mm] = LT::offset(key, 2 * mm + (q >> 1)) + 8 * (q & 1);
+      } else {
+        const int i = s16 >> 1, pp = s16 & 1;
+        const int key = 16 * (i >> 2) + 4 * kg + (i & 3);
+        vt_off[mm] = LT::offset(key, mm) + 8 * pp;
+      }
+    }
+  }
 
   const int n_tiles = (max_vis + kBN - 1) / kBN;
   if (n_tiles > 0) {
@@ -416,7 +452,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(PrefillArgs a)
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run[rt], mx);
+      // Lazy rescale: the running max only moves when the tile's max exceeds
+      // it by more than kRescaleSlack (log2 units), so P <= 2^kRescaleSlack,
+      // exact and in range in bf16/fp16; the output rescale below then runs
+      // only in a row's first tiles.  The result is the same softmax.
+      const float m_new = mx > m_run[rt] + kRescaleSlack ? mx : m_run[rt];
       alpha[rt] = __builtin_amdgcn_exp2f(m_run[rt] - m_new);
       m_run[rt] = m_new;
       float psum = 0.0f;
@@ -439,46 +479,13 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(PrefillArgs a)
     }
 
     // ---- O += P V, 32 keys per MFMA k-step ----
+    // B operand of output-dim tile mm (dims 16mm .. 16mm+15, lane c -> dim
+    // 16mm + c): the lane group's 8 keys of its k-slice, read transposed
+    // straight from LDS (ds_read_b64_tr_b16 / _tr_b8), see vt_off below.
+    char* vbuf = VBUF(buf);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      Op16<KV_DT> B[8];
-      if constexpr (kEb == 2) {
-        u32x4 vr[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int key = 32 * ks + 16 * (j >> 2) + 4 * kg + (j & 3);
-          vr[j] = *reinterpret_cast<const u32x4*>(VBUF(buf) + LT::offset(key, c));
-        }
-#pragma unroll
-        for (int pp = 0; pp < 4; ++pp) {
-          u32x4 lo, hi;
-#pragma unroll
-          for (int qq = 0; qq < 4; ++qq) {
-            lo[qq] = pack_lo16(vr[2 * qq][pp], vr[2 * qq + 1][pp]);
-            hi[qq] = pack_hi16(vr[2 * qq][pp], vr[2 * qq + 1][pp]);
-          }
-          B[2 * pp] = __builtin_bit_cast(Op16<KV_DT>, lo);
-          B[2 * pp + 1] = __builtin_bit_cast(Op16<KV_DT>, hi);
-        }
-      } else {
-        u32x2 vr[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int key = 32 * ks + 16 * (j >> 2) + 4 * kg + (j & 3);
-          vr[j] = *reinterpret_cast<const u32x2*>(VBUF(buf) + LT::offset(key, c >> 1) + 8 * (c & 1));
-        }
-        uint32_t X[8], Y[8];
-        transpose_bytes_4x4(vr[0][0], vr[1][0], vr[2][0], vr[3][0], X[0], X[1], X[2], X[3]);
-        transpose_bytes_4x4(vr[0][1], vr[1][1], vr[2][1], vr[3][1], X[4], X[5], X[6], X[7]);
-        transpose_bytes_4x4(vr[4][0], vr[5][0], vr[6][0], vr[7][0], Y[0], Y[1], Y[2], Y[3]);
-        transpose_bytes_4x4(vr[4][1], vr[5][1], vr[6][1], vr[7][1], Y[4], Y[5], Y[6], Y[7]);
-#pragma unroll
-        for (int mm = 0; mm < 8; ++mm) {
-          const f16x2 a0 = fp8x2_to_f16x2<false>(X[mm]), a1 = fp8x2_to_f16x2<true>(X[mm]);
-          const f16x2 a2 = fp8x2_to_f16x2<false>(Y[mm]), a3 = fp8x2_to_f16x2<true>(Y[mm]);
-          B[mm] = f16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
-        }
-      }
+      Op16<KV_DT> pop[kRowTiles], plop[kRowTiles];
 #pragma unroll
       for (int rt = 0; rt < kRowTiles; ++rt) {
         float pv[8];
@@ -487,17 +494,49 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(PrefillArgs a)
           pv[r] = p[2 * ks][rt][r];
           pv[4 + r] = p[2 * ks + 1][rt][r];
         }
-        const Op16<KV_DT> pop = to_op16<KV_DT>(pv);
-#pragma unroll
-        for (int mm = 0; mm < 8; ++mm) acc[rt][mm] = mfma16<KV_DT>(pop, B[mm], acc[rt][mm]);
+        pop[rt] = to_op16<KV_DT>(pv);
         if constexpr (KV_DT == MKV_DTYPE_BF16) {
           // second bf16 term carrying P's rounding residual (~16-bit P)
           float plo[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) plo[j] = pv[j] - (float)pop[j];
-          const Op16<KV_DT> plop = to_op16<KV_DT>(plo);
+          for (int j = 0; j < 8; ++j) plo[j] = pv[j] - (float)pop[rt][j];
+          plop[rt] = to_op16<KV_DT>(plo);
+        }
+      }
+      // all eight B operands of this k-step first, so the LDS reads overlap
+      Op16<KV_DT> Bv[8];
 #pragma unroll
-          for (int mm = 0; mm < 8; ++mm) acc[rt][mm] = mfma16<KV_DT>(plop, B[mm], acc[rt][mm]);
+      for (int mm = 0; mm < 8; ++mm) {
+        Op16<KV_DT>& B = Bv[mm];
+        if constexpr (kEb == 2) {
+          typedef short v4i16 __attribute__((ext_vector_type(4)));
+          typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+          lds_v4i16* p0 = (lds_v4i16*)(vbuf + vt_off[mm] + 32 * ks * LT::kRowBytes);
+          lds_v4i16* p1 = (lds_v4i16*)(vbuf + vt_off[mm] + (32 * ks + 16) * LT::kRowBytes);
+          const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p0);
+          const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p1);
+          const u32x4 w = {(uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16),
+                           (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16),
+                           (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16),
+                           (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16)};
+          B = __builtin_bit_cast(Op16<KV_DT>, w);
+        } else {
+          typedef int v2i32 __attribute__((ext_vector_type(2)));
+          typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
+          const v2i32 w = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              (lds_v2i32*)(vbuf + vt_off[mm] + 32 * ks * LT::kRowBytes));
+          const f16x2 a0 = fp8x2_to_f16x2<false>((uint32_t)w[0]), a1 = fp8x2_to_f16x2<true>((uint32_t)w[0]);
+          const f16x2 a2 = fp8x2_to_f16x2<false>((uint32_t)w[1]), a3 = fp8x2_to_f16x2<true>((uint32_t)w[1]);
+          B = f16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+        }
+      }
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) {
+        const Op16<KV_DT> B = Bv[mm];
+#pragma unroll
+        for (int rt = 0; rt < kRowTiles; ++rt) {
+          acc[rt][mm] = mfma16<KV_DT>(pop[rt], B, acc[rt][mm]);
+          if constexpr (KV_DT == MKV_DTYPE_BF16) acc[rt][mm] = mfma16<KV_DT>(plop[rt], B, acc[rt][mm]);
         }
       }
     }
@@ -522,10 +561,17 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(PrefillArgs a)
       if (row >= a.tok_per_wg * G || tok >= q1) continue;
       const int hq = kvh * G + row % G;
       const float inv = lh > 0.0f ? v_mul / lh : 0.0f;
-      float x[8];
+      // lane c holds dims 16mm + c
+      const int64_t o = (tok * a.num_heads + hq) * kHeadDim + c;
 #pragma unroll
-      for (int mm = 0; mm < 8; ++mm) x[mm] = acc[rt][mm][r] * inv;
-      store_out8(a.out, a.q_dtype, (tok * a.num_heads + hq) * kHeadDim + 8 * c, x);
+      for (int mm = 0; mm < 8; ++mm) {
+        const float x = acc[rt][mm][r] * inv;
+        if (a.q_dtype == MKV_DTYPE_F32)
+          reinterpret_cast<float*>(a.out)[o + 16 * mm] = x;
+        else
+          reinterpret_cast<uint16_t*>(a.out)[o + 16 * mm] =
+              (uint16_t)(a.q_dtype == MKV_DTYPE_BF16 ? f32_to_bf16_bits(x) : f32_to_f16_bits(x));
+      }
     }
   }
 }
