@@ -170,8 +170,13 @@ struct LdsTile {
   }
 };
 
+// Four waves per SIMD (two 8-wave workgroups per CU) hide the latency of each
+// wave's QK -> softmax -> PV chain, which leaves MFMA, VALU and LDS all far
+// from busy at two waves per SIMD; the compiler keeps the kernel within 128
+// registers (the bf16 variant spills a few of its registers, mostly outside
+// the tile loop).
 template <int KV_DT, bool PAGED>
-__global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4))) void prefill_mfma_kernel(PrefillArgs a) {
   using LT = LdsTile<KV_DT>;
   constexpr int kEb = LT::kEb;
   extern __shared__ __align__(16) char smem[];
@@ -503,11 +508,18 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(PrefillArgs a)
           plop[rt] = to_op16<KV_DT>(plo);
         }
       }
-      // all eight B operands of this k-step first, so the LDS reads overlap
-      Op16<KV_DT> Bv[8];
+      // B operands read in batches ahead of their MFMAs so that the LDS reads
+      // overlap: all 8 for 16-bit KV, 4 for FP8 (whose conversions need more
+      // registers; this keeps both within 128 registers without spills in the
+      // loop)
+      constexpr int kBBatch = kEb == 1 ? 4 : 8;
 #pragma unroll
-      for (int mm = 0; mm < 8; ++mm) {
-        Op16<KV_DT>& B = Bv[mm];
+      for (int half = 0; half < 8 / kBBatch; ++half) {
+      Op16<KV_DT> Bv[kBBatch];
+#pragma unroll
+      for (int m4 = 0; m4 < kBBatch; ++m4) {
+        const int mm = kBBatch * half + m4;
+        Op16<KV_DT>& B = Bv[m4];
         if constexpr (kEb == 2) {
           typedef short v4i16 __attribute__((ext_vector_type(4)));
           typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
@@ -531,13 +543,15 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(PrefillArgs a)
         }
       }
 #pragma unroll
-      for (int mm = 0; mm < 8; ++mm) {
-        const Op16<KV_DT> B = Bv[mm];
+      for (int m4 = 0; m4 < kBBatch; ++m4) {
+        const int mm = kBBatch * half + m4;
+        const Op16<KV_DT> B = Bv[m4];
 #pragma unroll
         for (int rt = 0; rt < kRowTiles; ++rt) {
           acc[rt][mm] = mfma16<KV_DT>(pop[rt], B, acc[rt][mm]);
           if constexpr (KV_DT == MKV_DTYPE_BF16) acc[rt][mm] = mfma16<KV_DT>(plop[rt], B, acc[rt][mm]);
         }
+      }
       }
     }
 
