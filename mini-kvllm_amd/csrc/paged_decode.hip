@@ -428,10 +428,21 @@ MKV_DEV void v_operands(const Tile16<KV_DT>& T, Op16<KV_DT> (&B)[8]) {
   }
 }
 
+// q as MFMA operands (dims 32kg + 8st .. +7 of head c in hi[st]).  A bf16
+// cache runs the bf16 MFMA, and bf16 holds an fp32 or fp16 q only to 8 bits:
+// then lo[st] carries the rounding residual and each QK step takes a second
+// MFMA (split), giving ~16 significant bits like the fp32 reference.
+template <int KV_DT>
+struct QOps {
+  Op16<KV_DT> hi[4];
+  Op16<KV_DT> lo[4];
+  bool split;
+};
+
 // One 32-token tile: S^T = K q^T, online softmax (log2 domain), O += P V.
 // t0: first token of the tile, t_end: end of the visible range.
 template <int KV_DT>
-MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const Op16<KV_DT> (&qop)[4],
+MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const QOps<KV_DT>& qop,
                             float score_mul, f32x4 (&acc)[8], float& m_run, float& l_run) {
   const int lane = threadIdx.x & 63;
   const int kg = lane >> 4;
@@ -448,7 +459,12 @@ MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const O
   for (int m = 0; m < 2; ++m) {
     s[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int st = 0; st < 4; ++st) s[m] = mfma16<KV_DT>(k_operand<KV_DT>(kw, m, st), qop[st], s[m]);
+    for (int st = 0; st < 4; ++st) {
+      const Op16<KV_DT> kop = k_operand<KV_DT>(kw, m, st);
+      s[m] = mfma16<KV_DT>(kop, qop.hi[st], s[m]);
+      if constexpr (KV_DT == MKV_DTYPE_BF16)
+        if (qop.split) s[m] = mfma16<KV_DT>(kop, qop.lo[st], s[m]);
+    }
   }
   float mx = kNegBig;
 #pragma unroll
@@ -508,7 +524,7 @@ MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const O
 // of two so q is exact and in range; k_scale (FP8) and sm_scale*log2(e) stay
 // in fp32.
 template <int KV_DT>
-MKV_DEV float q_operands(const DecodeArgs& a, float (&qf)[32], Op16<KV_DT> (&qop)[4], float k_mul) {
+MKV_DEV float q_operands(const DecodeArgs& a, float (&qf)[32], QOps<KV_DT>& qop, float k_mul) {
   float score_mul = a.sm_scale * kLog2e * k_mul;
   if constexpr (KV_DT != MKV_DTYPE_BF16) {
     float qm = 0.0f;
@@ -524,14 +540,25 @@ MKV_DEV float q_operands(const DecodeArgs& a, float (&qf)[32], Op16<KV_DT> (&qop
     }
   }
 #pragma unroll
-  for (int st = 0; st < 4; ++st) qop[st] = to_op16<KV_DT>(qf + 8 * st);
+  for (int st = 0; st < 4; ++st) qop.hi[st] = to_op16<KV_DT>(qf + 8 * st);
+  qop.split = false;
+  if constexpr (KV_DT == MKV_DTYPE_BF16) {
+    qop.split = a.q_dtype != MKV_DTYPE_BF16;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      float r[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r[j] = qf[8 * st + j] - (float)qop.hi[st][j];
+      qop.lo[st] = to_op16<KV_DT>(r);
+    }
+  }
   return score_mul;
 }
 
 // q of item (b, kvh) loaded and converted on the spot (any q dtype).  k_mul:
 // the K dequantisation scale (1 for 16-bit caches).
 template <int KV_DT>
-MKV_DEV float load_q_operands(const DecodeArgs& a, int b, int kvh, Op16<KV_DT> (&qop)[4], float k_mul) {
+MKV_DEV float load_q_operands(const DecodeArgs& a, int b, int kvh, QOps<KV_DT>& qop, float k_mul) {
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
   float qf[32];
@@ -572,7 +599,7 @@ MKV_DEV void load_q_stage(const DecodeArgs& a, int b, int kvh, bool need, QStage
 }
 
 template <int KV_DT>
-MKV_DEV float staged_q_operands(const DecodeArgs& a, const QStage& qs, Op16<KV_DT> (&qop)[4], float k_mul) {
+MKV_DEV float staged_q_operands(const DecodeArgs& a, const QStage& qs, QOps<KV_DT>& qop, float k_mul) {
   float qf[32];
   const bool bf = a.q_dtype == MKV_DTYPE_BF16;
 #pragma unroll
@@ -591,7 +618,7 @@ template <int KV_DT>
 __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(DecodeArgs a) {
   WorkItem it;
   if (!decode_work_item(a, wave_work_index(), it)) return;
-  Op16<KV_DT> qop[4];
+  QOps<KV_DT> qop;
   const float k_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.k_scale) : 1.0f;
   const float score_mul = load_q_operands<KV_DT>(a, it.b, it.kvh, qop, k_mul);
 
@@ -992,7 +1019,7 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(D
   load_q_stage(a, lc.b, lc.kvh, true, qs);
   advance_load();
 
-  Op16<KV_DT> qop[4];
+  QOps<KV_DT> qop;
   float score_mul = 0.0f;
   f32x4 acc[8];
   float m_run = kNegBig, l_run = 0.0f;

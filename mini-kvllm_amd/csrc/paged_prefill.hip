@@ -175,7 +175,10 @@ struct LdsTile {
 // from busy at two waves per SIMD; the compiler keeps the kernel within 128
 // registers (the bf16 variant spills a few of its registers, mostly outside
 // the tile loop).
-template <int KV_DT, bool PAGED>
+// QSPLIT (bf16 caches with an fp32 / fp16 q only): bf16 holds such a q to 8
+// bits, so q is split into bf16 hi + lo terms and each QK step takes a second
+// MFMA, giving ~16 significant bits like the fp32 reference.
+template <int KV_DT, bool PAGED, bool QSPLIT>
 __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4))) void prefill_mfma_kernel(PrefillArgs a) {
   using LT = LdsTile<KV_DT>;
   constexpr int kEb = LT::kEb;
@@ -283,10 +286,19 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     }
   }
   Op16<KV_DT> qop[kRowTiles][4];
+  Op16<KV_DT> qlo[QSPLIT ? kRowTiles : 1][4];
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt)
 #pragma unroll
-    for (int st = 0; st < 4; ++st) qop[rt][st] = to_op16<KV_DT>(qf[rt] + 8 * st);
+    for (int st = 0; st < 4; ++st) {
+      qop[rt][st] = to_op16<KV_DT>(qf[rt] + 8 * st);
+      if constexpr (QSPLIT) {
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = qf[rt][8 * st + j] - (float)qop[rt][st][j];
+        qlo[rt][st] = to_op16<KV_DT>(r);
+      }
+    }
 
   f32x4 acc[kRowTiles][8];
 #pragma unroll
@@ -432,7 +444,10 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
           kop = f16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
         }
 #pragma unroll
-        for (int rt = 0; rt < kRowTiles; ++rt) s[kt][rt] = mfma16<KV_DT>(kop, qop[rt][st], s[kt][rt]);
+        for (int rt = 0; rt < kRowTiles; ++rt) {
+          s[kt][rt] = mfma16<KV_DT>(kop, qop[rt][st], s[kt][rt]);
+          if constexpr (QSPLIT) s[kt][rt] = mfma16<KV_DT>(kop, qlo[rt][st], s[kt][rt]);
+        }
       }
     }
 
@@ -604,13 +619,13 @@ int64_t tiles_upper_bound(int num_seqs, int64_t total_q, int group) {
   return (total_q + tpw - 1) / tpw + num_seqs;
 }
 
-template <int KV_DT, bool PAGED>
+template <int KV_DT, bool PAGED, bool QSPLIT>
 int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   using LT = LdsTile<KV_DT>;
   const size_t lds = 4 * LT::kBytes + (kRowsPerWg + 2) * sizeof(int);
   int64_t nwg = a.tiles_ub * a.num_kv_heads;
   nwg = ((nwg + kXcds - 1) / kXcds) * kXcds;
-  hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED>), dim3((unsigned)nwg), dim3(kPfThreads), lds,
+  hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED, QSPLIT>), dim3((unsigned)nwg), dim3(kPfThreads), lds,
                      s, a);
   return (int)hipGetLastError();
 }
@@ -661,9 +676,11 @@ int dispatch_prefill(PrefillArgs& a, int kv_dtype, void* workspace, size_t works
   hipLaunchKernelGGL(prefill_tile_scan_kernel, dim3(1), dim3(256), 0, s, a.cu_seqlens_q, a.num_seqs,
                      a.tok_per_wg, a.tile_start);
   switch (kv_dtype) {
-    case MKV_DTYPE_FP8E4M3: return launch_prefill<MKV_DTYPE_FP8E4M3, PAGED>(a, s);
-    case MKV_DTYPE_BF16: return launch_prefill<MKV_DTYPE_BF16, PAGED>(a, s);
-    default: return launch_prefill<MKV_DTYPE_F16, PAGED>(a, s);
+    case MKV_DTYPE_FP8E4M3: return launch_prefill<MKV_DTYPE_FP8E4M3, PAGED, false>(a, s);
+    case MKV_DTYPE_BF16:
+      return a.q_dtype == MKV_DTYPE_BF16 ? launch_prefill<MKV_DTYPE_BF16, PAGED, false>(a, s)
+                                         : launch_prefill<MKV_DTYPE_BF16, PAGED, true>(a, s);
+    default: return launch_prefill<MKV_DTYPE_F16, PAGED, false>(a, s);
   }
 }
 

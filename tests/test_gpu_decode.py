@@ -222,3 +222,21 @@ def test_decode_large_batch_uses_split_k_fallback(dev):
     idx = torch.arange(0, B, 97)
     want = _oracle(q[idx], k, v, bt[idx], ctx[idx], 0.1, 8, 2)
     assert_close_out(got[idx], want, got.dtype, 2e-3)
+
+
+@pytest.mark.parametrize("kv,qdt", [(torch.bfloat16, torch.float32), (torch.bfloat16, torch.float16),
+                                    (torch.float16, torch.float32), (torch.float16, torch.bfloat16),
+                                    (torch.float8_e4m3fn, torch.float32)])
+@pytest.mark.parametrize("group", [4, 8])
+def test_decode_q_dtype_differs_from_cache(dev, kv, qdt, group):
+    """q in another dtype than the cache (the reference computes in fp32): a
+    bf16 cache with an fp32 / fp16 q takes the split (hi + lo) q path."""
+    announce(f"decode kv {kv} q {qdt} group {group}")
+    Hkv = 4
+    q, k, v, bt, ctx, ks, vs = _case(81, 12, group * Hkv, Hkv, 16, 160, 12, kv)
+    q = torch.randn(q.shape, generator=torch.Generator().manual_seed(82)).to(qdt)
+    want = _oracle(q, k, v, bt, ctx, 0.09, group * Hkv, Hkv, ks, vs)
+    for st in (0, 64):
+        got = _run(dev, q, k, v, bt, ctx, 0.09, group * Hkv, Hkv, ks, vs, split_tokens=st)
+        assert got.dtype == qdt
+        assert_close_out(got, want, got.dtype, TOL[kv])

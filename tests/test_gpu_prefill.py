@@ -249,3 +249,18 @@ def test_attention_layer_mixed_batch(dev, mode):
     vs = float(vsr) if fp8 else None
     want = R.paged_prefill_ref(q.double(), kcr, vcr, bt, ctx, cu, pos, 1 / math.sqrt(128), Hq, Hkv, ks, vs)
     assert_close_out(out, want.reshape(T, Hq * 128), out.dtype, 2e-2 if fp8 else 2e-3)
+
+
+@pytest.mark.parametrize("kv,qdt", [(torch.bfloat16, torch.float32), (torch.bfloat16, torch.float16),
+                                    (torch.float16, torch.float32)])
+def test_prefill_q_dtype_differs_from_cache(dev, kv, qdt):
+    """q in another dtype than the cache: a bf16 cache with an fp32 / fp16 q
+    takes the split (hi + lo) q path."""
+    announce(f"prefill kv {kv} q {qdt}")
+    q, k, v, bt, ctx, cu, pos, ks, vs = _make(91, [40, 0, 300], [33, 70, 5], 16, 4, 16, kv)
+    q = torch.randn(q.shape, generator=torch.Generator().manual_seed(92)).to(qdt)
+    sc = 1.0 / math.sqrt(128)
+    got = _gpu(dev, q, k, v, bt, ctx, cu, pos, sc, 16, 4, ks, vs)
+    want = R.paged_prefill_ref(q.double(), k, v, bt, ctx, cu, pos, sc, 16, 4)
+    assert got.dtype == qdt
+    assert_close_out(got, want, got.dtype, 2e-3)
