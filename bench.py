@@ -40,12 +40,19 @@ PEAK_HBM_GBPS = 8000.0
 HEAD_DIM = 128
 
 
+KV_DESC = {"fp8": "per-tensor e4m3fn", "bf16": "bf16",
+           "fp8_token": "e4m3fn codes, fp32 scale per token and kv head",
+           "int8_token": "int8 codes, fp32 scale per token and kv head"}
+
+
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--kv", choices=["fp8", "bf16"], default="fp8")
+    ap.add_argument("--kv", choices=["fp8", "bf16", "fp8_token", "int8_token"], default="fp8",
+                    help="KV format: per-tensor FP8 (the headline), bf16, or per-token-head "
+                         "FP8 / INT8 (kv_cache_dtype fp8_per_token_head / int8_per_token_head)")
     ap.add_argument("--layers", type=int, default=8, help="distinct layer pools rotated per step")
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--batch", type=int, default=256)
@@ -249,11 +256,21 @@ def main() -> int:
     meta = W.decode_b256_metadata(seed=3, batch=args.batch,
                                   num_blocks=max(4096, 16 * args.batch))
     N, bs = meta["num_blocks"], meta["block_size"]
-    kv_dtype = torch.float8_e4m3fn if args.kv == "fp8" else torch.bfloat16
+    kv_dtype = {"fp8": torch.float8_e4m3fn, "bf16": torch.bfloat16,
+                "fp8_token": torch.float8_e4m3fn, "int8_token": torch.int8}[args.kv]
+    per_token = args.kv in ("fp8_token", "int8_token")
+    token_mode = {"fp8_token": "fp8_per_token_head", "int8_token": "int8_per_token_head"}.get(args.kv)
     layers = []
     for l in range(args.layers):
         kc = torch.empty(N, bs, args.num_kv_heads, HEAD_DIM, dtype=kv_dtype, device=dev)
         vc = torch.empty_like(kc)
+        if per_token:
+            ksd = torch.empty(N, bs, args.num_kv_heads, device=dev)
+            vsd = torch.empty_like(ksd)
+            W.fill_pool_per_token_head_on_device(kc, ksd, 1000 + 2 * l, token_mode)
+            W.fill_pool_per_token_head_on_device(vc, vsd, 1001 + 2 * l, token_mode)
+            layers.append((kc, vc, (ksd, vsd), None))
+            continue
         ks = W.fill_pool_on_device(kc, 1000 + 2 * l)
         vs = W.fill_pool_on_device(vc, 1001 + 2 * l)
         sc = (torch.tensor([ks], device=dev), torch.tensor([vs], device=dev)) if ks else (None, None)
@@ -270,9 +287,10 @@ def main() -> int:
     def step(i):
         kc, vc, (ksd, vsd), _ = layers[i % len(layers)]
         A._decode(q, kc, vc, bt, ctx, sm, Hq, Hkv, HEAD_DIM, ksd, vsd,
-                  split_tokens=args.split_tokens, out=out)
+                  split_tokens=args.split_tokens, out=out, per_token_head=per_token)
 
-    nbytes = W.alg_bytes_decode(meta["context_lens"], bs, Hq, Hkv, kv_bytes=kv_dtype.itemsize)
+    nbytes = W.alg_bytes_decode(meta["context_lens"], bs, Hq, Hkv, kv_bytes=kv_dtype.itemsize,
+                                scale_bytes=4 if per_token else 0)
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
     ms = time_launches(step, args.steps, args.warmup, stream)
@@ -298,13 +316,13 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8" if args.kv == "fp8" else "bf16",
+        "dtype": {"fp8": "fp8", "bf16": "bf16", "fp8_token": "fp8", "int8_token": "int8"}[args.kv],
         "data": "synthetic (seeded N(0,1) KV pools and queries, seeded context lengths/tables)",
         "config": {
             "workload": (f"paged decode attention, batch {args.batch}, {Hq} q / {Hkv} kv heads, head_dim 128, "
                          f"block 256, ctx floor(exp(U(ln512, ln8192))) sum {int(meta['context_lens'].sum())}, "
                          f"fragmented tables over {N} blocks, {args.kv} KV "
-                         f"({'per-tensor e4m3fn' if args.kv == 'fp8' else 'bf16'}), bf16 q/out, "
+                         f"({KV_DESC[args.kv]}), bf16 q/out, "
                          f"{args.layers} rotating layer pools"),
             "batch": args.batch, "num_heads": Hq, "num_kv_heads": Hkv, "head_dim": HEAD_DIM,
             "block_size": bs, "schedule": schedule, "algorithmic_bytes_per_step": nbytes,
@@ -347,7 +365,7 @@ def main() -> int:
         extra["decode_frac_of_box_copy"] = round(gbps / copy, 4)
         result["extra"] = extra
 
-    if args.cpu_seqs > 0:
+    if args.cpu_seqs > 0 and not per_token:
         kc0, vc0, _, scales = layers[0]
         result["cpu_baseline"] = cpu_baseline(kc0, vc0, scales, q, meta, args.cpu_seqs)
     else:

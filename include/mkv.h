@@ -5,7 +5,8 @@
  * operators of the mini-kvllm engine (src/myvllm/layers/attention.py in the
  * reference) as hand-written HIP kernels:
  *
- *   K1  slot-mapped KV append, plain copy or fused per-tensor FP8 quantisation
+ *   K1  slot-mapped KV append: plain copy, or fused per-tensor FP8 /
+ *       per-token-head FP8 / per-token-head INT8 quantisation
  *   K2  paged decode attention (GQA-shared K/V tiles; stream-K or split-K,
  *       partials merged by log-sum-exp)
  *   K3  paged / contiguous causal prefill attention on MFMA
@@ -35,15 +36,29 @@
 extern "C" {
 #endif
 
-#define MKV_ABI_VERSION 1
+#define MKV_ABI_VERSION 2
 
 /* Element dtypes (torch.float32, torch.bfloat16, torch.float16,
- * torch.float8_e4m3fn).  FP8 is OCP e4m3fn: max 448, no infinities, NaN =
- * S.1111.111 (reference: model_runner.py:247, attention.py:113). */
+ * torch.float8_e4m3fn, torch.int8).  FP8 is OCP e4m3fn: max 448, no
+ * infinities, NaN = S.1111.111 (reference: model_runner.py:247,
+ * attention.py:113).  INT8 holds the symmetric per-token-head codes of
+ * kv_cache_dtype 'int8_per_token_head' (model_runner.py:242-244). */
 #define MKV_DTYPE_F32 0
 #define MKV_DTYPE_BF16 1
 #define MKV_DTYPE_F16 2
 #define MKV_DTYPE_FP8E4M3 3
+#define MKV_DTYPE_I8 4
+
+/* Granularity of the dequantisation scales of an FP8 / INT8 cache.
+ *   PER_TENSOR:     k_scale / v_scale point at one fp32 each
+ *                   (kv_cache_dtype 'fp8_per_tensor', model_runner.py:324-329).
+ *   PER_TOKEN_HEAD: k_scale / v_scale are fp32 (num_blocks, block_size,
+ *                   num_kv_heads) tensors in the pool's slot order: the scale
+ *                   of slot s, kv head h is scale[s * num_kv_heads + h]
+ *                   ('fp8_per_token_head' / 'int8_per_token_head',
+ *                   model_runner.py:330-338). */
+#define MKV_SCALE_PER_TENSOR 0
+#define MKV_SCALE_PER_TOKEN_HEAD 1
 
 /* Index dtypes for context_lens (the engine uses int64, model_runner.py:617;
  * the reference's micro-benchmarks use int32, benchmark_decoding.py:290). */
@@ -103,6 +118,36 @@ int mkv_kv_append(const void* key, int64_t key_row_stride,
                   void* stream);
 
 /*
+ * K1 with per-token-head quantisation.
+ *
+ * Replaces the per-token-head branch of store_kvcache_fp8
+ * (attention.py:281-333, kernel :118-191, branch :166-181) when cache_dtype
+ * == MKV_DTYPE_FP8E4M3 and store_kvcache_int8 (attention.py:246-276, kernel
+ * :194-243) when cache_dtype == MKV_DTYPE_I8.
+ *
+ * Rows are selected as in mkv_kv_append (slot -1 or out of pool: skipped,
+ * scales untouched).  For each written (token, kv head) with fp32 elements
+ * x[0..head_dim) and amax = max |x| (NaN elements ignored, 0 if none left):
+ *   FP8:  scale = amax > 0 ? amax / 448 : 1;  q = clamp(x / scale, +-448)
+ *         rounded to e4m3fn (RNE; NaN stays NaN), as the per-tensor mode;
+ *   INT8: scale = max(amax / 127, 1e-6);  y = x * (1 / scale);
+ *         y += (y >= 0 ? 0.5 : -0.5);  q = trunc(minNum(maxNum(y, -128), 127))
+ *         (round half away from zero; a NaN becomes -128).
+ * Divisions are IEEE-754 correctly rounded fp32.  scale is written to
+ * k_scale[slot * num_kv_heads + h] (v_scale likewise).
+ *
+ * head_dim a power of two in 16..1024; alignment as in mkv_kv_append.
+ */
+int mkv_kv_append_per_token_head(const void* key, int64_t key_row_stride,
+                                 const void* value, int64_t value_row_stride,
+                                 void* k_cache, void* v_cache,
+                                 float* k_scale, float* v_scale,
+                                 const int64_t* slot_mapping, int64_t num_tokens,
+                                 int num_kv_heads, int head_dim,
+                                 int block_size, int64_t num_blocks,
+                                 int in_dtype, int cache_dtype, void* stream);
+
+/*
  * Per-tensor FP8 calibration (attention.py:308-323), done on the device so
  * that no host synchronisation is needed.
  *
@@ -132,14 +177,18 @@ int mkv_fp8_calibrate_per_tensor(const void* key, int64_t key_row_stride,
  * K2: paged decode attention.
  *
  * Replaces paged_attention_decode (attention.py:895-950, kernel :517-646)
- * and the per-tensor FP8 path of paged_attention_decode_quantized
- * (attention.py:1213-1268, kernel :953-1121).
+ * and paged_attention_decode_quantized (attention.py:1213-1268): the
+ * per-tensor FP8 kernel (:953-1121) and the per-token-head FP8 / INT8 tile
+ * kernel (:1124-1210).
  *
  * out[b, h, :] = softmax_t(sm_scale * q[b,h,:] . K_t) @ V_t over the tokens
  * t < context_lens[b] of sequence b whose logical block
  * block_tables[b, t / block_size] is a valid pool index (entries of -1 are
  * skipped), with K_t/V_t taken from kv head h / (num_heads / num_kv_heads).
- * FP8 caches are dequantised as fp8 * (*k_scale) / fp8 * (*v_scale).
+ * Quantised caches are dequantised as code * scale: kv_scale_mode
+ * MKV_SCALE_PER_TENSOR (FP8 only) uses *k_scale / *v_scale;
+ * MKV_SCALE_PER_TOKEN_HEAD (FP8 or INT8) uses the scale of the token's slot
+ * and kv head.  kv_scale_mode is ignored for F32/BF16/F16 caches.
  * A sequence with no visible token (context_lens[b] == 0) gets zeros.
  *
  * q, out: (batch, num_heads, head_dim), rows contiguous, row stride
@@ -169,6 +218,7 @@ int mkv_paged_decode(void* out, int64_t out_batch_stride,
                      const void* k_cache, const void* v_cache, int kv_dtype,
                      int64_t num_blocks,
                      const float* k_scale, const float* v_scale,
+                     int kv_scale_mode,
                      const int32_t* block_tables, int64_t bt_stride,
                      int max_blocks,
                      const void* context_lens, int context_lens_dtype,
@@ -190,7 +240,8 @@ int mkv_paged_decode(void* out, int64_t out_batch_stride,
  *
  * q, out: (total_q, num_heads, head_dim) contiguous.  positions: int64
  * (total_q).  cu_seqlens_q: int32 (num_seqs + 1).  kv_dtype BF16, F16 or
- * FP8E4M3 (an F32 cache returns MKV_ERR_UNSUPPORTED_DTYPE); q_dtype F32,
+ * FP8E4M3 with kv_scale_mode MKV_SCALE_PER_TENSOR (an F32 or INT8 cache, or
+ * per-token-head scales, return MKV_ERR_UNSUPPORTED_DTYPE); q_dtype F32,
  * BF16 or F16.
  * workspace: >= mkv_paged_prefill_workspace_size(...) bytes (tile list).
  */
@@ -200,6 +251,7 @@ int mkv_paged_prefill(void* out, const void* q, int q_dtype,
                       const void* k_cache, const void* v_cache, int kv_dtype,
                       int64_t num_blocks,
                       const float* k_scale, const float* v_scale,
+                      int kv_scale_mode,
                       const int32_t* block_tables, int64_t bt_stride,
                       int max_blocks,
                       const void* context_lens, int context_lens_dtype,
@@ -235,7 +287,8 @@ int mkv_flash_prefill(void* out, const void* q, const void* k, const void* v,
  * dst[b, t, :, :] = cache[block_tables[b, t / bs], t % bs, :, :] for
  * t < context_lens[b]; rows t >= context_lens[b] (up to max_len) and rows
  * whose block entry is -1 are zero-filled.  dst: (batch, max_len,
- * num_kv_heads, head_dim) in the cache dtype, contiguous.
+ * num_kv_heads, head_dim) in the cache dtype (any MKV_DTYPE_*: the bytes are
+ * copied, quantised codes stay codes), contiguous.
  */
 int mkv_gather_kv(void* dst, const void* cache, int dtype, int64_t num_blocks,
                   const int32_t* block_tables, int64_t bt_stride,

@@ -59,7 +59,8 @@ extern "C" int mkv_gather_kv(void* dst, const void* cache, int dtype, int64_t nu
     case MKV_DTYPE_F32: eb = 4; break;
     case MKV_DTYPE_BF16:
     case MKV_DTYPE_F16: eb = 2; break;
-    case MKV_DTYPE_FP8E4M3: eb = 1; break;
+    case MKV_DTYPE_FP8E4M3:
+    case MKV_DTYPE_I8: eb = 1; break;
     default: return MKV_ERR_UNSUPPORTED_DTYPE;
   }
   if (context_lens_dtype != MKV_INDEX_I32 && context_lens_dtype != MKV_INDEX_I64)

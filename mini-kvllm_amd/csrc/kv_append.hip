@@ -1,9 +1,12 @@
-// K1: slot-mapped KV append with optional fused per-tensor FP8 quantisation,
-// plus the device-side per-tensor FP8 calibration.
+// K1: slot-mapped KV append with optional fused quantisation (per-tensor FP8,
+// per-token-head FP8 or INT8), plus the device-side per-tensor FP8
+// calibration.
 //
 // Reference semantics: store_kvcache (attention.py:67-108, kernel :7-64),
-// store_kvcache_fp8 per-tensor branch (attention.py:281-333, kernel
-// :118-191) and the calibrate-once rule (attention.py:308-323).
+// store_kvcache_fp8 (attention.py:281-333, kernel :118-191: per-tensor branch
+// :183-189, per-token-head branch :166-181), store_kvcache_int8
+// (attention.py:246-276, kernel :194-243) and the calibrate-once rule
+// (attention.py:308-323).
 //
 // Design: one wavefront per token row.  A row (all KV heads of one token) is
 // num_kv_heads * head_dim contiguous elements in both the input and the pool,
@@ -47,15 +50,13 @@ MKV_DEV void load16_as_f32(const void* row, int64_t e, float (&x)[16]) {
   }
 }
 
-// Quantise 16 consecutive elements of one row with a per-tensor scale.
-template <int IN_DT>
-MKV_DEV u32x4 quantize16(const void* row, int64_t e, float scale) {
-  float x[16];
-  load16_as_f32<IN_DT>(row, e, x);
+// 16 fp32 values -> 16 e4m3fn bytes: IEEE fp32 divide by the scale
+// (correctly rounded), torch.clamp to +-448 (NaN passes), RNE cast.  NaN
+// bytes keep the converter's S.1111.111 payload with the host's NaN sign.
+MKV_DEV u32x4 quantize16_fp8(const float (&x)[16], float scale) {
   u32x4 out;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    // IEEE fp32 divide (correctly rounded), then torch.clamp, then RNE cast.
     float v[4];
     uint32_t nan_bits = 0, nan_signs = 0;
 #pragma unroll
@@ -65,10 +66,17 @@ MKV_DEV u32x4 quantize16(const void* row, int64_t e, float scale) {
       nan_signs |= div_nan_sign(x[4 * i + j], scale, qv) << (8 * j + 7);
       v[j] = clamp_fp8_range(qv);
     }
-    // NaN bytes: keep the converter's S.1111.111 payload, replace its sign.
     out[i] = (pack_fp8x4(v[0], v[1], v[2], v[3]) & ~nan_bits) | nan_signs;
   }
   return out;
+}
+
+// Quantise 16 consecutive elements of one row with a per-tensor scale.
+template <int IN_DT>
+MKV_DEV u32x4 quantize16(const void* row, int64_t e, float scale) {
+  float x[16];
+  load16_as_f32<IN_DT>(row, e, x);
+  return quantize16_fp8(x, scale);
 }
 
 template <int IN_DT, bool FP8>
@@ -204,6 +212,92 @@ __global__ __launch_bounds__(kCalThreads) void fp8_calibrate_kernel(
   atomicExch(&ws[2], 0u);
 }
 
+// ---------------------------------------------------------------------------
+// Per-token-head quantisation (FP8 e4m3fn or INT8): every (token, KV head)
+// gets its own fp32 scale from the amax of its head_dim elements.  A lane
+// holds 16 consecutive elements, so one head is D/16 adjacent lanes and its
+// amax is an xor-shuffle reduction over them (D a power of two, 16..1024).
+// ---------------------------------------------------------------------------
+
+// amax of |x| over the lane's 16 elements, NaN ignored (maxNum), then over
+// the `group` lanes of the head.
+template <int IN_DT>
+MKV_DEV float head_amax(const void* row, int64_t e, int group, float (&x)[16]) {
+  load16_as_f32<IN_DT>(row, e, x);
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(x[i]));
+  for (int off = 1; off < group; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+  return m;
+}
+
+// INT8: y = x * (1 / scale), rounded half away from zero, clamped to
+// [-128, 127] with maxNum/minNum (a NaN becomes -128), truncated.
+MKV_DEV uint32_t quantize_i8(float xv, float inv) {
+  float y = xv * inv;
+  y = y >= 0.0f ? y + 0.5f : y - 0.5f;
+  y = fminf(fmaxf(y, -128.0f), 127.0f);
+  return (uint32_t)((int)y & 0xff);
+}
+
+MKV_DEV u32x4 quantize16_i8(const float (&x)[16], float inv) {
+  u32x4 out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    out[i] = quantize_i8(x[4 * i], inv) | (quantize_i8(x[4 * i + 1], inv) << 8) |
+             (quantize_i8(x[4 * i + 2], inv) << 16) | (quantize_i8(x[4 * i + 3], inv) << 24);
+  return out;
+}
+
+template <int IN_DT, bool INT8>
+MKV_DEV void quantize_head_chunk(const char* row, char* dst, float* scales, int64_t e, int group,
+                                 int head_dim, int lane) {
+  float x[16];
+  const float amax = head_amax<IN_DT>(row, e, group, x);
+  u32x4 q;
+  float scale;
+  if constexpr (INT8) {
+    scale = fmaxf(amax / 127.0f, 1e-6f);
+    q = quantize16_i8(x, 1.0f / scale);
+  } else {
+    scale = amax > 0.0f ? amax / kFp8Max : 1.0f;
+    q = quantize16_fp8(x, scale);
+  }
+  st16(dst + e, q);
+  if ((lane & (group - 1)) == 0) scales[e / head_dim] = scale;
+}
+
+template <int IN_DT, bool INT8>
+__global__ __launch_bounds__(kAppendWaves* kWave) void kv_append_per_token_head_kernel(
+    const void* __restrict__ key, int64_t key_stride,
+    const void* __restrict__ value, int64_t value_stride,
+    void* __restrict__ k_cache, void* __restrict__ v_cache,
+    float* __restrict__ k_scale, float* __restrict__ v_scale,
+    const int64_t* __restrict__ slot_mapping, int64_t num_tokens,
+    int num_kv_heads, int head_dim, int64_t num_slots) {
+  constexpr int kInBytes = DTypeInfo<IN_DT>::kBytes;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t t = (int64_t)blockIdx.x * kAppendWaves + (threadIdx.x >> 6);
+  if (t >= num_tokens) return;
+  const int64_t slot = slot_mapping[t];
+  if (slot < 0 || slot >= num_slots) return;  // -1 = padding: skip
+
+  const int64_t row_elems = (int64_t)num_kv_heads * head_dim;
+  const int group = head_dim / kElemsPerLane;  // lanes per head
+  const char* krow = reinterpret_cast<const char*>(key) + t * key_stride * kInBytes;
+  const char* vrow = reinterpret_cast<const char*>(value) + t * value_stride * kInBytes;
+  char* kdst = reinterpret_cast<char*>(k_cache) + slot * row_elems;
+  char* vdst = reinterpret_cast<char*>(v_cache) + slot * row_elems;
+  float* ks = k_scale + slot * num_kv_heads;
+  float* vs = v_scale + slot * num_kv_heads;
+  // Whole heads per iteration (a head spans group <= 64 lanes, aligned), so
+  // the lanes of one head are always active together.
+  for (int64_t e = (int64_t)lane * kElemsPerLane; e < row_elems; e += kWave * kElemsPerLane) {
+    quantize_head_chunk<IN_DT, INT8>(krow, kdst, ks, e, group, head_dim, lane);
+    quantize_head_chunk<IN_DT, INT8>(vrow, vdst, vs, e, group, head_dim, lane);
+  }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -290,5 +384,52 @@ extern "C" int mkv_fp8_calibrate_per_tensor(const void* key, int64_t key_row_str
     default: MKV_CAL_LAUNCH(MKV_DTYPE_F16); break;
   }
 #undef MKV_CAL_LAUNCH
+  return (int)hipGetLastError();
+}
+
+extern "C" int mkv_kv_append_per_token_head(const void* key, int64_t key_row_stride,
+                                            const void* value, int64_t value_row_stride,
+                                            void* k_cache, void* v_cache, float* k_scale,
+                                            float* v_scale, const int64_t* slot_mapping,
+                                            int64_t num_tokens, int num_kv_heads, int head_dim,
+                                            int block_size, int64_t num_blocks, int in_dtype,
+                                            int cache_dtype, void* stream) {
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks < 0)
+    return MKV_ERR_BAD_SHAPE;
+  if (head_dim < 16 || head_dim > 1024 || (head_dim & (head_dim - 1))) return MKV_ERR_UNSUPPORTED_HEAD_DIM;
+  if (num_tokens == 0) return MKV_OK;
+  if (!key || !value || !k_cache || !v_cache || !k_scale || !v_scale || !slot_mapping)
+    return MKV_ERR_NULL_POINTER;
+  if (in_dtype != MKV_DTYPE_F32 && in_dtype != MKV_DTYPE_BF16 && in_dtype != MKV_DTYPE_F16)
+    return MKV_ERR_UNSUPPORTED_DTYPE;
+  if (cache_dtype != MKV_DTYPE_FP8E4M3 && cache_dtype != MKV_DTYPE_I8) return MKV_ERR_UNSUPPORTED_DTYPE;
+  const int64_t row_elems = (int64_t)num_kv_heads * head_dim;
+  if (key_row_stride < row_elems || value_row_stride < row_elems) return MKV_ERR_BAD_STRIDE;
+  const int in_bytes = (in_dtype == MKV_DTYPE_F32) ? 4 : 2;
+  if (!aligned16(key) || !aligned16(value) || !aligned16(k_cache) || !aligned16(v_cache) ||
+      (key_row_stride * in_bytes) % 16 != 0 || (value_row_stride * in_bytes) % 16 != 0)
+    return MKV_ERR_MISALIGNED;
+
+  const int64_t num_slots = num_blocks * (int64_t)block_size;
+  const dim3 grid((unsigned)((num_tokens + kAppendWaves - 1) / kAppendWaves));
+  const dim3 block(kAppendWaves * kWave);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool i8 = cache_dtype == MKV_DTYPE_I8;
+#define MKV_PTH_LAUNCH(IDT, I8)                                                                  \
+  hipLaunchKernelGGL((kv_append_per_token_head_kernel<IDT, I8>), grid, block, 0, s, key,          \
+                     key_row_stride, value, value_row_stride, k_cache, v_cache, k_scale, v_scale, \
+                     slot_mapping, num_tokens, num_kv_heads, head_dim, num_slots)
+  switch (in_dtype) {
+    case MKV_DTYPE_F32:
+      if (i8) MKV_PTH_LAUNCH(MKV_DTYPE_F32, true); else MKV_PTH_LAUNCH(MKV_DTYPE_F32, false);
+      break;
+    case MKV_DTYPE_BF16:
+      if (i8) MKV_PTH_LAUNCH(MKV_DTYPE_BF16, true); else MKV_PTH_LAUNCH(MKV_DTYPE_BF16, false);
+      break;
+    default:
+      if (i8) MKV_PTH_LAUNCH(MKV_DTYPE_F16, true); else MKV_PTH_LAUNCH(MKV_DTYPE_F16, false);
+      break;
+  }
+#undef MKV_PTH_LAUNCH
   return (int)hipGetLastError();
 }

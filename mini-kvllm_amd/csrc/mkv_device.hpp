@@ -43,6 +43,26 @@ template <>
 struct DTypeInfo<MKV_DTYPE_FP8E4M3> {
   static constexpr int kBytes = 1;
 };
+template <>
+struct DTypeInfo<MKV_DTYPE_I8> {
+  static constexpr int kBytes = 1;
+};
+
+// KV formats of the attention kernels that carry one fp32 scale per (token,
+// KV head) in a tensor beside the pool.  These are template codes of the
+// kernels, not ABI values: the C ABI names them by (dtype, scale mode).
+constexpr int kKvFp8PerToken = 0x100 | MKV_DTYPE_FP8E4M3;
+constexpr int kKvI8PerToken = 0x100 | MKV_DTYPE_I8;
+template <>
+struct DTypeInfo<kKvFp8PerToken> {
+  static constexpr int kBytes = 1;
+};
+template <>
+struct DTypeInfo<kKvI8PerToken> {
+  static constexpr int kBytes = 1;
+};
+template <int KV_DT>
+constexpr bool kPerTokenScale = KV_DT == kKvFp8PerToken || KV_DT == kKvI8PerToken;
 
 // ---------------------------------------------------------------------------
 // Scalar conversions.  bf16 <-> f32 is done on the bit pattern; f32 -> bf16
@@ -116,6 +136,12 @@ MKV_DEV f16x2 fp8x2_to_f16x2(uint32_t w) {
   return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, kHi);
 }
 
+// Two e4m3fn bytes (low or high half-word of w) -> exact bf16 pair.
+template <bool kHi>
+MKV_DEV bf16x2 fp8x2_to_bf16x2(uint32_t w) {
+  return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, kHi);
+}
+
 // Two e4m3fn bytes -> exact fp32 pair.
 template <bool kHi>
 MKV_DEV f32x2 fp8x2_to_f32x2(uint32_t w) {
@@ -149,6 +175,22 @@ MKV_DEV void transpose_bytes_4x4(uint32_t r0, uint32_t r1, uint32_t r2,
 // Low half-words of (a, b) -> {a.lo, b.lo}; high half-words -> {a.hi, b.hi}.
 MKV_DEV uint32_t pack_lo16(uint32_t a, uint32_t b) { return perm(b, a, 0x05040100u); }
 MKV_DEV uint32_t pack_hi16(uint32_t a, uint32_t b) { return perm(b, a, 0x07060302u); }
+
+// Two int8 codes (bytes 0-1 of w, or bytes 2-3 with kHi) -> exact bf16 pair:
+// an integer of magnitude <= 128 has at most 8 significant bits, so the upper
+// half-word of its fp32 value is that value in bf16.
+template <bool kHi>
+MKV_DEV bf16x2 i8x2_to_bf16x2(uint32_t w) {
+  const float a = (float)(int8_t)(w >> (kHi ? 16 : 0));
+  const float b = (float)(int8_t)(w >> (kHi ? 24 : 8));
+  return __builtin_bit_cast(bf16x2, pack_hi16(__float_as_uint(a), __float_as_uint(b)));
+}
+
+// Value of lane N of this lane's 16-lane row (DPP row broadcast).
+template <int N>
+MKV_DEV float row_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + N, 0xf, 0xf, true));
+}
 
 // ---------------------------------------------------------------------------
 // Global memory access helpers.

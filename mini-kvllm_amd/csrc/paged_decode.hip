@@ -1,8 +1,9 @@
 // K2: paged decode attention for gfx950.
 //
 // Reference semantics: paged_attention_decode (attention.py:895-950, kernel
-// :517-646) and the per-tensor FP8 path of paged_attention_decode_quantized
-// (attention.py:1213-1268, kernel :953-1121, dequant :1051-1062/:1098-1107).
+// :517-646) and paged_attention_decode_quantized (attention.py:1213-1268):
+// per-tensor FP8 (kernel :953-1121, dequant :1051-1062/:1098-1107) and
+// per-token-head FP8 / INT8 (tile kernel :1124-1210).
 //
 // Work item = (sequence b, kv head g, split s): one wavefront reads the
 // split's K/V tokens of kv head g exactly once and serves all G = Hq/Hkv
@@ -24,6 +25,12 @@
 //     on the fp16 MFMA; q is normalised by a power of two so it is exact in
 //     fp16, and the per-tensor k/v scales are applied to scores / output in
 //     fp32 (legal because the scale is per tensor).
+//   * Per-token-head FP8 / INT8 codes convert exactly to bf16 and run on the
+//     bf16 MFMA.  Each lane loads one scale per tile (K or V scale of one of
+//     the 8 tokens its 16-lane row holds scores for) and DPP row broadcasts
+//     hand every lane the 16 it needs: the K scale multiplies the score, the
+//     V scale folds into P (P * v_scale, split into two bf16 terms), and the
+//     softmax denominator sums the unscaled P, as the reference does.
 // Splits that do not cover a whole sequence write (acc, m, l) partials that a
 // second kernel merges with the log-sum-exp rule.
 #include "mkv_device.hpp"
@@ -43,7 +50,7 @@ struct DecodeArgs {
   int q_dtype;
   const char* k_cache;
   const char* v_cache;
-  const float* k_scale;
+  const float* k_scale;  // per tensor: one fp32; per token head: (slots, Hkv)
   const float* v_scale;
   PagedIndex idx;
   const void* context_lens;
@@ -290,8 +297,35 @@ struct Tile16 {
   using VT = typename std::conditional<kEb == 1, u32x2, u32x4>::type;
   u32x4 k[2][kKVec];
   VT v[8];
+  float sc;    // per-token-head formats: one K or V scale (load_tile_scales)
   bool ok[2];  // sub-tile block present
 };
+
+// Per-token-head scales of the 32-token tile at t0 of KV head kvh (block
+// entries ph0 / ph1 of its two 16-token halves).  Lane (c, kg) loads the K
+// (c < 8) or V (c >= 8) scale of token t0 + 16m + 4kg + r with m = (c >> 2) & 1,
+// r = c & 3: row kg of the wave then holds exactly the 16 scales of the 8
+// tokens whose scores it computes.  An absent block reads slot 0 of block 0
+// (a valid address; the value is masked where it is used).  The load is
+// issued unconditionally, like the K/V loads.
+typedef const float __attribute__((address_space(1))) global_f32;
+template <int KV_DT>
+MKV_DEV void load_tile_scales(const DecodeArgs& a, int64_t ph0, int64_t ph1, int t0, int kvh,
+                              Tile16<KV_DT>& T) {
+  if constexpr (kPerTokenScale<KV_DT>) {
+    const int lane = threadIdx.x & 63;
+    const int c = lane & 15, kg = lane >> 4;
+    const int bs_mask = (1 << a.idx.bs_log2) - 1;
+    // scale index of the first token of each half (the host checks that the
+    // scale tensor has fewer than 2^31 entries)
+    const int s0 = (int)((((ph0 < 0 ? 0 : ph0) << a.idx.bs_log2) + (t0 & bs_mask)) * a.num_kv_heads) + kvh;
+    const int s1 =
+        (int)((((ph1 < 0 ? 0 : ph1) << a.idx.bs_log2) + ((t0 + 16) & bs_mask)) * a.num_kv_heads) + kvh;
+    const int idx = ((c & 4) ? s1 : s0) + (4 * kg + (c & 3)) * a.num_kv_heads;
+    const float* base = c < 8 ? a.k_scale : a.v_scale;
+    T.sc = *((global_f32*)(base + idx));
+  }
+}
 
 // Issue the K/V loads of one 32-token tile through the per-half descriptors
 // rk/rv (rows t0 .. t0+15 and t0+16 .. t0+31).  Rows at or past t_end read as
@@ -342,26 +376,33 @@ MKV_DEV void load_tile16(const DecodeArgs& a, const WorkItem& it, const ItemLoad
   const int c = lane & 15, kg = lane >> 4;
   const int bs_mask = (1 << a.idx.bs_log2) - 1;
   __amdgpu_buffer_rsrc_t rk[2], rv[2];
+  int64_t phys[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int th = t0 + 16 * h;
     int slot = (th >> a.idx.bs_log2) - L.blk0;
     slot = slot > 63 ? 63 : slot;
-    const int64_t phys = __builtin_amdgcn_readlane(L.my_phys, slot);
+    phys[h] = __builtin_amdgcn_readlane(L.my_phys, slot);
     const int64_t off = L.head_bytes + (int64_t)(th & bs_mask) * L.row_bytes;
-    rk[h] = rows_rsrc(a.k_cache, phys, L.blk_bytes, off);
-    rv[h] = rows_rsrc(a.v_cache, phys, L.blk_bytes, off);
-    T.ok[h] = phys >= 0;
+    rk[h] = rows_rsrc(a.k_cache, phys[h], L.blk_bytes, off);
+    rv[h] = rows_rsrc(a.v_cache, phys[h], L.blk_bytes, off);
+    T.ok[h] = phys[h] >= 0;
   }
   load_tile_rows<KV_DT>(rk, rv, t0, it.t_end, L.k_voff, L.v_voff, L.row_bytes, T);
+  load_tile_scales<KV_DT>(a, phys[0], phys[1], t0, it.kvh, T);
 }
 
+// Formats that run on the bf16 MFMA (bf16 caches and the per-token-head codes,
+// which convert to bf16 exactly); the others run on the fp16 MFMA.
 template <int KV_DT>
-using Op16 = typename std::conditional<KV_DT == MKV_DTYPE_BF16, bf16x8, f16x8>::type;
+constexpr bool kBf16Mfma = KV_DT == MKV_DTYPE_BF16 || kPerTokenScale<KV_DT>;
+
+template <int KV_DT>
+using Op16 = typename std::conditional<kBf16Mfma<KV_DT>, bf16x8, f16x8>::type;
 
 template <int KV_DT>
 MKV_DEV f32x4 mfma16(Op16<KV_DT> A, Op16<KV_DT> B, f32x4 C) {
-  if constexpr (KV_DT == MKV_DTYPE_BF16)
+  if constexpr (kBf16Mfma<KV_DT>)
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, C, 0, 0, 0);
   else
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, C, 0, 0, 0);
@@ -373,12 +414,26 @@ MKV_DEV Op16<KV_DT> to_op16(const float* x) {
   Op16<KV_DT> r;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    if constexpr (KV_DT == MKV_DTYPE_BF16)
+    if constexpr (kBf16Mfma<KV_DT>)
       r[j] = (__bf16)x[j];
     else
       r[j] = (_Float16)x[j];
   }
   return r;
+}
+
+// Eight 1-byte per-token-head codes (d0 bytes 0-3, d1 bytes 0-3) -> bf16.
+template <int KV_DT>
+MKV_DEV bf16x8 bytes8_to_bf16x8(uint32_t d0, uint32_t d1) {
+  bf16x2 a0, a1, a2, a3;
+  if constexpr (KV_DT == kKvFp8PerToken) {
+    a0 = fp8x2_to_bf16x2<false>(d0), a1 = fp8x2_to_bf16x2<true>(d0);
+    a2 = fp8x2_to_bf16x2<false>(d1), a3 = fp8x2_to_bf16x2<true>(d1);
+  } else {
+    a0 = i8x2_to_bf16x2<false>(d0), a1 = i8x2_to_bf16x2<true>(d0);
+    a2 = i8x2_to_bf16x2<false>(d1), a3 = i8x2_to_bf16x2<true>(d1);
+  }
+  return bf16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
 }
 
 // A operand of QK step st for K sub-tile m (8 dims: 32kg + 8st .. +7) from
@@ -392,6 +447,11 @@ MKV_DEV Op16<KV_DT> k_operand(const u32x4 (&K)[2][Tile16<KV_DT>::kKVec], int m, 
     const f16x2 a0 = fp8x2_to_f16x2<false>(d0), a1 = fp8x2_to_f16x2<true>(d0);
     const f16x2 a2 = fp8x2_to_f16x2<false>(d1), a3 = fp8x2_to_f16x2<true>(d1);
     return f16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+  } else if constexpr (kPerTokenScale<KV_DT>) {
+    const u32x4 w = K[m][st >> 1];
+    const uint32_t d0 = (st & 1) ? w[2] : w[0];
+    const uint32_t d1 = (st & 1) ? w[3] : w[1];
+    return bytes8_to_bf16x8<KV_DT>(d0, d1);
   } else {
     return __builtin_bit_cast(Op16<KV_DT>, K[m][st]);
   }
@@ -401,7 +461,7 @@ MKV_DEV Op16<KV_DT> k_operand(const u32x4 (&K)[2][Tile16<KV_DT>::kKVec], int m, 
 // V[token T_j][8c + mm].
 template <int KV_DT>
 MKV_DEV void v_operands(const Tile16<KV_DT>& T, Op16<KV_DT> (&B)[8]) {
-  if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) {
+  if constexpr (DTypeInfo<KV_DT>::kBytes == 1) {
     uint32_t X[8], Y[8];
     transpose_bytes_4x4(T.v[0][0], T.v[1][0], T.v[2][0], T.v[3][0], X[0], X[1], X[2], X[3]);
     transpose_bytes_4x4(T.v[0][1], T.v[1][1], T.v[2][1], T.v[3][1], X[4], X[5], X[6], X[7]);
@@ -409,9 +469,13 @@ MKV_DEV void v_operands(const Tile16<KV_DT>& T, Op16<KV_DT> (&B)[8]) {
     transpose_bytes_4x4(T.v[4][1], T.v[5][1], T.v[6][1], T.v[7][1], Y[4], Y[5], Y[6], Y[7]);
 #pragma unroll
     for (int mm = 0; mm < 8; ++mm) {
-      const f16x2 a0 = fp8x2_to_f16x2<false>(X[mm]), a1 = fp8x2_to_f16x2<true>(X[mm]);
-      const f16x2 a2 = fp8x2_to_f16x2<false>(Y[mm]), a3 = fp8x2_to_f16x2<true>(Y[mm]);
-      B[mm] = f16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+      if constexpr (kPerTokenScale<KV_DT>) {
+        B[mm] = bytes8_to_bf16x8<KV_DT>(X[mm], Y[mm]);
+      } else {
+        const f16x2 a0 = fp8x2_to_f16x2<false>(X[mm]), a1 = fp8x2_to_f16x2<true>(X[mm]);
+        const f16x2 a2 = fp8x2_to_f16x2<false>(Y[mm]), a3 = fp8x2_to_f16x2<true>(Y[mm]);
+        B[mm] = f16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+      }
     }
   } else {
 #pragma unroll
@@ -429,7 +493,7 @@ MKV_DEV void v_operands(const Tile16<KV_DT>& T, Op16<KV_DT> (&B)[8]) {
 }
 
 // q as MFMA operands (dims 32kg + 8st .. +7 of head c in hi[st]).  A bf16
-// cache runs the bf16 MFMA, and bf16 holds an fp32 or fp16 q only to 8 bits:
+// MFMA format holds an fp32 or fp16 q only to 8 bits:
 // then lo[st] carries the rounding residual and each QK step takes a second
 // MFMA (split), giving ~16 significant bits like the fp32 reference.
 template <int KV_DT>
@@ -438,6 +502,17 @@ struct QOps {
   Op16<KV_DT> lo[4];
   bool split;
 };
+
+// The 16 scales that row kg of the wave loaded (load_tile_scales): K scales
+// of its tokens 4m + r from lanes 0-7, V scales from lanes 8-15.
+MKV_DEV void row_scales(float sc, float (&ks)[8], float (&vs)[8]) {
+  ks[0] = row_bcast<0>(sc), ks[1] = row_bcast<1>(sc), ks[2] = row_bcast<2>(sc);
+  ks[3] = row_bcast<3>(sc), ks[4] = row_bcast<4>(sc), ks[5] = row_bcast<5>(sc);
+  ks[6] = row_bcast<6>(sc), ks[7] = row_bcast<7>(sc);
+  vs[0] = row_bcast<8>(sc), vs[1] = row_bcast<9>(sc), vs[2] = row_bcast<10>(sc);
+  vs[3] = row_bcast<11>(sc), vs[4] = row_bcast<12>(sc), vs[5] = row_bcast<13>(sc);
+  vs[6] = row_bcast<14>(sc), vs[7] = row_bcast<15>(sc);
+}
 
 // One 32-token tile: S^T = K q^T, online softmax (log2 domain), O += P V.
 // t0: first token of the tile, t_end: end of the visible range.
@@ -452,7 +527,7 @@ MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const Q
   for (int m = 0; m < 2; ++m) {
 #pragma unroll
     for (int i = 0; i < Tile16<KV_DT>::kKVec; ++i) kw[m][i] = cur.k[m][i];
-    if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) k_exchange(kw[m][0], kw[m][1]);
+    if constexpr (DTypeInfo<KV_DT>::kBytes == 1) k_exchange(kw[m][0], kw[m][1]);
   }
   f32x4 s[2];
 #pragma unroll
@@ -462,17 +537,25 @@ MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const Q
     for (int st = 0; st < 4; ++st) {
       const Op16<KV_DT> kop = k_operand<KV_DT>(kw, m, st);
       s[m] = mfma16<KV_DT>(kop, qop.hi[st], s[m]);
-      if constexpr (KV_DT == MKV_DTYPE_BF16)
+      if constexpr (kBf16Mfma<KV_DT>)
         if (qop.split) s[m] = mfma16<KV_DT>(kop, qop.lo[st], s[m]);
     }
   }
+  // Per-token-head formats: K scales (lanes 0-7 of the row) and V scales
+  // (lanes 8-15) of this lane's tokens 16m + 4kg + r, index 4m + r.
+  float ks[8], vs[8];
+  if constexpr (kPerTokenScale<KV_DT>) row_scales(cur.sc, ks, vs);
   float mx = kNegBig;
+  bool okt[8];
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const bool ok = t0 + 16 * m + 4 * kg + r < t_end && cur.ok[m];
-      s[m][r] = ok ? s[m][r] * score_mul : -__builtin_huge_valf();
+      okt[4 * m + r] = ok;
+      float sv = s[m][r] * score_mul;
+      if constexpr (kPerTokenScale<KV_DT>) sv *= ks[4 * m + r];
+      s[m][r] = ok ? sv : -__builtin_huge_valf();
       mx = fmaxf(mx, s[m][r]);
     }
   }
@@ -501,17 +584,27 @@ MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const Q
       for (int mm = 0; mm < 8; ++mm) acc[mm][r] *= ar;
     }
   }
-  const Op16<KV_DT> pop = to_op16<KV_DT>(p);
+  // PV weights: P, or P * v_scale of the token for per-token-head formats
+  // (zero for masked tokens, whatever scale the masked slot holds).
+  float pw[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if constexpr (kPerTokenScale<KV_DT>)
+      pw[j] = okt[j] ? p[j] * vs[j] : 0.0f;
+    else
+      pw[j] = p[j];
+  }
+  const Op16<KV_DT> pop = to_op16<KV_DT>(pw);
   Op16<KV_DT> vop[8];
   v_operands<KV_DT>(cur, vop);
 #pragma unroll
   for (int mm = 0; mm < 8; ++mm) acc[mm] = mfma16<KV_DT>(pop, vop[mm], acc[mm]);
-  if constexpr (KV_DT == MKV_DTYPE_BF16) {
-    // bf16 keeps 8 significant bits of P; add the rounding residual as a
-    // second bf16 term so P carries ~16 bits like the fp32 reference.
+  if constexpr (kBf16Mfma<KV_DT>) {
+    // bf16 keeps 8 significant bits of the weights; add the rounding residual
+    // as a second bf16 term so they carry ~16 bits like the fp32 reference.
     float plo[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) plo[j] = p[j] - (float)pop[j];
+    for (int j = 0; j < 8; ++j) plo[j] = pw[j] - (float)pop[j];
     const Op16<KV_DT> plop = to_op16<KV_DT>(plo);
 #pragma unroll
     for (int mm = 0; mm < 8; ++mm) acc[mm] = mfma16<KV_DT>(plop, vop[mm], acc[mm]);
@@ -521,12 +614,12 @@ MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const Q
 // MFMA operands of q (the lane holds dims 32kg .. 32kg+31 of head c of the
 // group, zero for padding heads); returns the fp32 factor that maps MFMA
 // scores to the log2-domain logits.  fp16 operands are normalised by a power
-// of two so q is exact and in range; k_scale (FP8) and sm_scale*log2(e) stay
-// in fp32.
+// of two so q is exact and in range; k_scale (per-tensor FP8) and
+// sm_scale*log2(e) stay in fp32.
 template <int KV_DT>
 MKV_DEV float q_operands(const DecodeArgs& a, float (&qf)[32], QOps<KV_DT>& qop, float k_mul) {
   float score_mul = a.sm_scale * kLog2e * k_mul;
-  if constexpr (KV_DT != MKV_DTYPE_BF16) {
+  if constexpr (!kBf16Mfma<KV_DT>) {
     float qm = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) qm = fmaxf(qm, fabsf(qf[i]));
@@ -542,7 +635,7 @@ MKV_DEV float q_operands(const DecodeArgs& a, float (&qf)[32], QOps<KV_DT>& qop,
 #pragma unroll
   for (int st = 0; st < 4; ++st) qop.hi[st] = to_op16<KV_DT>(qf + 8 * st);
   qop.split = false;
-  if constexpr (KV_DT == MKV_DTYPE_BF16) {
+  if constexpr (kBf16Mfma<KV_DT>) {
     qop.split = a.q_dtype != MKV_DTYPE_BF16;
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
@@ -615,7 +708,7 @@ MKV_DEV float staged_q_operands(const DecodeArgs& a, const QStage& qs, QOps<KV_D
 }
 
 template <int KV_DT>
-__global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(DecodeArgs a) {
+MKV_DEV void split_decode(const DecodeArgs& a) {
   WorkItem it;
   if (!decode_work_item(a, wave_work_index(), it)) return;
   QOps<KV_DT> qop;
@@ -652,6 +745,19 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(D
   l_col += __shfl_xor(l_col, 32);
   const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
   finish_item(a, it, acc, m_run, l_col, v_mul);
+}
+
+template <int KV_DT>
+__global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(DecodeArgs a) {
+  split_decode<KV_DT>(a);
+}
+
+// Per-token-head formats: two waves per SIMD requested explicitly (as for
+// the stream-K kernel below).
+template <int KV_DT>
+__global__ __launch_bounds__(kDecWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
+paged_decode_mfma16_2w_kernel(DecodeArgs a) {
+  split_decode<KV_DT>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -751,6 +857,7 @@ MKV_DEV void load_tile_sk(const DecodeArgs& a, const Cursor& c, const PhysPair& 
     T.ok[h] = ph.p[h] >= 0;
   }
   load_tile_rows<KV_DT>(rk, rv, t0, c.L, k_voff, v_voff, row_bytes, T);
+  load_tile_scales<KV_DT>(a, ph.p[0], ph.p[1], t0, c.kvh, T);
 }
 
 // Write the finished item of cursor c: the normalised output if the whole item
@@ -972,7 +1079,7 @@ MKV_DEV StreamSplit make_split(int64_t total, int waves, int first_waves) {
 }
 
 template <int KV_DT, bool kSmallGroup>
-__global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(DecodeArgs a) {
+MKV_DEV void stream_decode(const DecodeArgs& a) {
   constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
   extern __shared__ int sk_lds[];
   int* pre = sk_lds;                 // [batch + 1]
@@ -1067,6 +1174,28 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(D
     step(t1b, t0b, g);
     if (++g >= g1) break;
   }
+}
+
+template <int KV_DT, bool kSmallGroup>
+__global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(DecodeArgs a) {
+  stream_decode<KV_DT, kSmallGroup>(a);
+}
+
+// Per-token-head formats ask for the two-waves-per-SIMD register budget
+// explicitly: left to itself the scheduler takes a few registers more than
+// two waves can hold, and the residency halves.
+template <int KV_DT, bool kSmallGroup>
+__global__ __launch_bounds__(kDecWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
+paged_decode_stream_2w_kernel(DecodeArgs a) {
+  stream_decode<KV_DT, kSmallGroup>(a);
+}
+
+template <int KV_DT, bool kSmallGroup>
+constexpr auto stream_kernel() {
+  if constexpr (kPerTokenScale<KV_DT>)
+    return paged_decode_stream_2w_kernel<KV_DT, kSmallGroup>;
+  else
+    return paged_decode_stream_kernel<KV_DT, kSmallGroup>;
 }
 
 // Merge of stream-K partials: one wave per (sequence, query head).
@@ -1312,13 +1441,12 @@ void launch_stream(DecodeArgs& a, int lds_bucket, size_t lds_bound, size_t lds, 
   int dev = 0;
   (void)hipGetDevice(&dev);
   const int slot = dev >= 0 && dev < 64 ? dev : 0;
-  if (per_cu[slot][lds_bucket] == 0)
-    per_cu[slot][lds_bucket] = resident_wgs_per_cu(paged_decode_stream_kernel<DT, SMALL>, lds_bound);
+  constexpr auto kernel = stream_kernel<DT, SMALL>();
+  if (per_cu[slot][lds_bucket] == 0) per_cu[slot][lds_bucket] = resident_wgs_per_cu(kernel, lds_bound);
   const int wgs = device_cus() * per_cu[slot][lds_bucket];
   a.num_waves = wgs * kDecWaves;
   a.first_waves = per_cu[slot][lds_bucket] > 1 ? device_cus() * kDecWaves : a.num_waves;
-  hipLaunchKernelGGL((paged_decode_stream_kernel<DT, SMALL>), dim3(wgs), dim3(kDecWaves * kWave), lds,
-                     s, a);
+  hipLaunchKernelGGL(kernel, dim3(wgs), dim3(kDecWaves * kWave), lds, s, a);
 }
 
 size_t split_ws_bytes(int batch, int num_heads, int max_blocks, int block_size, int st) {
@@ -1355,7 +1483,7 @@ extern "C" size_t mkv_paged_decode_workspace_size(int batch, int num_heads, int 
 extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void* q,
                                 int64_t q_batch_stride, int q_dtype, const void* k_cache,
                                 const void* v_cache, int kv_dtype, int64_t num_blocks,
-                                const float* k_scale, const float* v_scale,
+                                const float* k_scale, const float* v_scale, int kv_scale_mode,
                                 const int32_t* block_tables, int64_t bt_stride, int max_blocks,
                                 const void* context_lens, int context_lens_dtype, int batch,
                                 int num_heads, int num_kv_heads, int head_dim, int block_size,
@@ -1374,9 +1502,19 @@ extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void*
   if (q_dtype != MKV_DTYPE_F32 && q_dtype != MKV_DTYPE_BF16 && q_dtype != MKV_DTYPE_F16)
     return MKV_ERR_UNSUPPORTED_DTYPE;
   if (kv_dtype != MKV_DTYPE_F32 && kv_dtype != MKV_DTYPE_BF16 && kv_dtype != MKV_DTYPE_F16 &&
-      kv_dtype != MKV_DTYPE_FP8E4M3)
+      kv_dtype != MKV_DTYPE_FP8E4M3 && kv_dtype != MKV_DTYPE_I8)
     return MKV_ERR_UNSUPPORTED_DTYPE;
-  if (kv_dtype == MKV_DTYPE_FP8E4M3 && (!k_scale || !v_scale)) return MKV_ERR_NULL_POINTER;
+  const bool quant = kv_dtype == MKV_DTYPE_FP8E4M3 || kv_dtype == MKV_DTYPE_I8;
+  if (quant && kv_scale_mode != MKV_SCALE_PER_TENSOR && kv_scale_mode != MKV_SCALE_PER_TOKEN_HEAD)
+    return MKV_ERR_UNSUPPORTED_DTYPE;
+  const bool per_token = quant && kv_scale_mode == MKV_SCALE_PER_TOKEN_HEAD;
+  if (kv_dtype == MKV_DTYPE_I8 && !per_token) return MKV_ERR_UNSUPPORTED_DTYPE;
+  if (quant && (!k_scale || !v_scale)) return MKV_ERR_NULL_POINTER;
+  // per-token-head scale indices are 32-bit
+  if (per_token && num_blocks * (int64_t)block_size * num_kv_heads >= (int64_t(1) << 31))
+    return MKV_ERR_BAD_SHAPE;
+  // kernel format: the dtype, or a per-token-head code
+  const int fmt = per_token ? (kv_dtype == MKV_DTYPE_I8 ? kKvI8PerToken : kKvFp8PerToken) : kv_dtype;
   if (context_lens_dtype != MKV_INDEX_I32 && context_lens_dtype != MKV_INDEX_I64)
     return MKV_ERR_UNSUPPORTED_DTYPE;
   if (q_batch_stride < (int64_t)num_heads * head_dim || out_batch_stride < (int64_t)num_heads * head_dim ||
@@ -1413,7 +1551,8 @@ extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void*
   a.group = group;
   a.sm_scale = sm_scale;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const bool fp8 = kv_dtype == MKV_DTYPE_FP8E4M3;
+  // the merge kernels apply the per-tensor V scale
+  const bool fp8 = fmt == MKV_DTYPE_FP8E4M3;
   if (split_tokens == 0 && kv_dtype != MKV_DTYPE_F32 && batch <= kStreamMaxBatch) {
     // stream-K path
     const size_t need = stream_ws_bytes(batch, group);
@@ -1434,10 +1573,18 @@ extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void*
     const int lds_bucket = batch <= kStreamSmallBatch ? 0 : 1;
     const size_t lds_bound = lds_bucket ? kStreamMaxLds : kStreamSmallLds;
     const bool small = group <= 4;
-    switch (kv_dtype) {
+    switch (fmt) {
       case MKV_DTYPE_FP8E4M3:
         small ? launch_stream<MKV_DTYPE_FP8E4M3, true>(a, lds_bucket, lds_bound, lds, s)
               : launch_stream<MKV_DTYPE_FP8E4M3, false>(a, lds_bucket, lds_bound, lds, s);
+        break;
+      case kKvFp8PerToken:
+        small ? launch_stream<kKvFp8PerToken, true>(a, lds_bucket, lds_bound, lds, s)
+              : launch_stream<kKvFp8PerToken, false>(a, lds_bucket, lds_bound, lds, s);
+        break;
+      case kKvI8PerToken:
+        small ? launch_stream<kKvI8PerToken, true>(a, lds_bucket, lds_bound, lds, s)
+              : launch_stream<kKvI8PerToken, false>(a, lds_bucket, lds_bound, lds, s);
         break;
       case MKV_DTYPE_BF16:
         small ? launch_stream<MKV_DTYPE_BF16, true>(a, lds_bucket, lds_bound, lds, s)
@@ -1472,9 +1619,15 @@ extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void*
   const int64_t items = (int64_t)batch * num_kv_heads * a.max_splits;
   const dim3 grid((unsigned)((items + kDecWaves - 1) / kDecWaves));
   const dim3 block(kDecWaves * kWave);
-  switch (kv_dtype) {
+  switch (fmt) {
     case MKV_DTYPE_FP8E4M3:
       hipLaunchKernelGGL(paged_decode_mfma16_kernel<MKV_DTYPE_FP8E4M3>, grid, block, 0, s, a);
+      break;
+    case kKvFp8PerToken:
+      hipLaunchKernelGGL(paged_decode_mfma16_2w_kernel<kKvFp8PerToken>, grid, block, 0, s, a);
+      break;
+    case kKvI8PerToken:
+      hipLaunchKernelGGL(paged_decode_mfma16_2w_kernel<kKvI8PerToken>, grid, block, 0, s, a);
       break;
     case MKV_DTYPE_BF16:
       hipLaunchKernelGGL(paged_decode_mfma16_kernel<MKV_DTYPE_BF16>, grid, block, 0, s, a);
@@ -1489,7 +1642,7 @@ extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void*
   if (a.max_splits > 1) {
     const int64_t mitems = (int64_t)batch * num_heads;
     hipLaunchKernelGGL(paged_decode_merge_kernel, dim3((unsigned)((mitems + kDecWaves - 1) / kDecWaves)),
-                       block, 0, s, a, (int)(kv_dtype == MKV_DTYPE_FP8E4M3));
+                       block, 0, s, a, (int)fp8);
   }
   return (int)hipGetLastError();
 }

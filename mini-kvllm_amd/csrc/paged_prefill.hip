@@ -688,7 +688,7 @@ int dispatch_prefill(PrefillArgs& a, int kv_dtype, void* workspace, size_t works
 
 extern "C" int mkv_paged_prefill(void* out, const void* q, int q_dtype, const void* k_cache,
                                  const void* v_cache, int kv_dtype, int64_t num_blocks,
-                                 const float* k_scale, const float* v_scale,
+                                 const float* k_scale, const float* v_scale, int kv_scale_mode,
                                  const int32_t* block_tables, int64_t bt_stride, int max_blocks,
                                  const void* context_lens, int context_lens_dtype,
                                  const int32_t* cu_seqlens_q, const int64_t* positions,
@@ -701,6 +701,8 @@ extern "C" int mkv_paged_prefill(void* out, const void* q, int q_dtype, const vo
   if (!out || !q || !k_cache || !v_cache || !block_tables || !context_lens || !cu_seqlens_q ||
       !positions)
     return MKV_ERR_NULL_POINTER;
+  if (kv_dtype == MKV_DTYPE_FP8E4M3 && kv_scale_mode != MKV_SCALE_PER_TENSOR)
+    return MKV_ERR_UNSUPPORTED_DTYPE;
   if (kv_dtype == MKV_DTYPE_FP8E4M3 && (!k_scale || !v_scale)) return MKV_ERR_NULL_POINTER;
   if (context_lens_dtype != MKV_INDEX_I32 && context_lens_dtype != MKV_INDEX_I64)
     return MKV_ERR_UNSUPPORTED_DTYPE;

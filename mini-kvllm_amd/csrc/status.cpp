@@ -11,7 +11,8 @@ extern "C" const char* mkv_status_string(int status) {
     case MKV_ERR_NULL_POINTER: return "a required pointer argument is NULL";
     case MKV_ERR_BAD_SHAPE: return "invalid shape or size argument";
     case MKV_ERR_UNSUPPORTED_DTYPE: return "unsupported dtype combination";
-    case MKV_ERR_UNSUPPORTED_HEAD_DIM: return "unsupported head_dim (the kernels require 128)";
+    case MKV_ERR_UNSUPPORTED_HEAD_DIM:
+      return "unsupported head_dim (attention kernels: 128; per-token-head append: a power of two in 16..1024)";
     case MKV_ERR_UNSUPPORTED_GROUP:
       return "num_heads must be a multiple of num_kv_heads with a group size in 1..16";
     case MKV_ERR_BAD_BLOCK_SIZE: return "block_size must be a power of two (>= 16 for attention)";

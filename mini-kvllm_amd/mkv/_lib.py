@@ -14,12 +14,15 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmkv.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 DTYPE_F16 = 2
 DTYPE_FP8E4M3 = 3
+DTYPE_I8 = 4
+SCALE_PER_TENSOR = 0
+SCALE_PER_TOKEN_HEAD = 1
 INDEX_I32 = 0
 INDEX_I64 = 1
 
@@ -30,6 +33,9 @@ SIGNATURES: dict[str, tuple] = {
     "mkv_kv_append": (c_int, [
         c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64,
         c_int, c_int, c_int, c_int64, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "mkv_kv_append_per_token_head": (c_int, [
+        c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+        c_int64, c_int, c_int, c_int, c_int64, c_int, c_int, c_void_p]),
     "mkv_fp8_calibrate_workspace_size": (c_size_t, []),
     "mkv_fp8_calibrate_per_tensor": (c_int, [
         c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int, c_int, c_void_p, c_void_p,
@@ -38,11 +44,11 @@ SIGNATURES: dict[str, tuple] = {
     "mkv_paged_decode_split_tokens": (c_int, [c_int, c_int, c_int, c_int, c_int]),
     "mkv_paged_decode": (c_int, [
         c_void_p, c_int64, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_int, c_int64,
-        c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p, c_int, c_int, c_int, c_int,
+        c_void_p, c_void_p, c_int, c_void_p, c_int64, c_int, c_void_p, c_int, c_int, c_int, c_int,
         c_int, c_int, c_float, c_int, c_void_p, c_size_t, c_void_p]),
     "mkv_paged_prefill_workspace_size": (c_size_t, [c_int, c_int64, c_int, c_int]),
     "mkv_paged_prefill": (c_int, [
-        c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p,
+        c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_int,
         c_void_p, c_int64, c_int, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int64,
         c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t, c_void_p]),
     "mkv_flash_prefill_workspace_size": (c_size_t, [c_int, c_int64, c_int, c_int]),

@@ -9,9 +9,12 @@ block manager can call these unchanged:
 this module                     reference
 ==============================  =========================================
 store_kvcache                   attention.py:67-108
-store_kvcache_fp8               attention.py:281-333 (per-tensor mode)
+store_kvcache_fp8               attention.py:281-333 (per-tensor and
+                                per-token-head modes)
+store_kvcache_int8              attention.py:246-276
 paged_attention_decode          attention.py:895-950
-paged_attention_decode_quantized attention.py:1213-1268 (fp8_per_tensor)
+paged_attention_decode_quantized attention.py:1213-1268 (fp8_per_tensor,
+                                fp8_per_token_head, int8_per_token_head)
 paged_attention_prefill_triton  attention.py:852-891 (+ FP8 KV keywords)
 flash_attention_prefill         attention.py:446-514
 Attention                       attention.py:1617-1807
@@ -40,7 +43,12 @@ _DTYPES = {
     torch.bfloat16: _lib.DTYPE_BF16,
     torch.float16: _lib.DTYPE_F16,
     torch.float8_e4m3fn: _lib.DTYPE_FP8E4M3,
+    torch.int8: _lib.DTYPE_I8,
 }
+
+# kv_cache_dtype strings of the reference's quantised modes and the scale
+# granularity each uses (model_runner.py:222-229, :324-338).
+PER_TOKEN_HEAD_MODES = ("fp8_per_token_head", "int8_per_token_head")
 
 _workspaces: dict[tuple[int, str], torch.Tensor] = {}
 
@@ -158,6 +166,49 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
     _append(key, value, k_cache, v_cache, slot_mapping)
 
 
+def _check_token_scales(k_scale, v_scale, k_cache):
+    """Per-token-head scales: fp32 (num_blocks, block_size, num_kv_heads)
+    tensors in slot order (model_runner.py:330-338)."""
+    want = k_cache.shape[0] * k_cache.shape[1] * k_cache.shape[2]
+    for name, sc in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if sc is None:
+            raise ValueError(f"{name} is required for per-token-head scales")
+        if sc.dtype != torch.float32 or not sc.is_contiguous() or sc.numel() < want:
+            raise ValueError(f"{name} must be a contiguous float32 (num_blocks, block_size, "
+                             f"num_kv_heads) tensor with >= {want} elements; got "
+                             f"{sc.dtype} {tuple(sc.shape)}")
+
+
+def _append_per_token_head(key, value, k_cache, v_cache, k_scale, v_scale, slot_mapping):
+    num_tokens, num_kv_heads, head_dim = key.shape
+    dev = _require_gpu(key, value, k_cache, v_cache, k_scale, v_scale, slot_mapping)
+    _check_token_scales(k_scale, v_scale, k_cache)
+    key = _token_rows(key)
+    value = _token_rows(value)
+    slots = slot_mapping if slot_mapping.dtype == torch.int64 else slot_mapping.to(torch.int64)
+    slots = slots.contiguous()
+    _lib.call(
+        "mkv_kv_append_per_token_head", key.data_ptr(), key.stride(0), value.data_ptr(),
+        value.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(),
+        v_scale.data_ptr(), slots.data_ptr(), num_tokens, num_kv_heads, head_dim,
+        k_cache.shape[1], k_cache.shape[0], _dtype_code(key, "key"),
+        _dtype_code(k_cache, "k_cache"), _stream(dev))
+
+
+def store_kvcache_int8(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                       v_cache: torch.Tensor, k_scale: torch.Tensor, v_scale: torch.Tensor,
+                       slot_mapping: torch.Tensor, block_size: int) -> None:
+    """Quantise key/value to INT8 with one scale per (token, kv head) and
+    write codes and scales to their slots.  Reference: attention.py:246-276
+    (kernel :194-243): scale = max(amax / 127, 1e-6), codes rounded half away
+    from zero and clamped to [-128, 127]."""
+    num_tokens, num_kv_heads, head_dim = key.shape
+    _check_cache(k_cache, v_cache, num_kv_heads, head_dim)
+    if k_cache.dtype != torch.int8:
+        raise TypeError(f"int8 cache expected, got {k_cache.dtype}")
+    _append_per_token_head(key, value, k_cache, v_cache, k_scale, v_scale, slot_mapping)
+
+
 def calibrate_fp8_per_tensor(key: torch.Tensor, value: torch.Tensor, k_scale: torch.Tensor,
                              v_scale: torch.Tensor) -> None:
     """Device-side form of the reference's calibrate-once rule
@@ -182,20 +233,24 @@ def calibrate_fp8_per_tensor(key: torch.Tensor, value: torch.Tensor, k_scale: to
 def store_kvcache_fp8(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
                       v_cache: torch.Tensor, k_scale: torch.Tensor, v_scale: torch.Tensor,
                       slot_mapping: torch.Tensor, block_size: int, kv_cache_dtype: str) -> None:
-    """Quantise key/value to FP8 e4m3fn with per-tensor scales and write them
-    to their cache slots.  Reference: attention.py:281-333.
+    """Quantise key/value to FP8 e4m3fn and write them to their cache slots.
+    Reference: attention.py:281-333.
 
-    The scales follow the reference's calibrate-once rule, evaluated on the
-    device; kv_cache_dtype 'fp8_per_token_head' is not implemented here.
+    'fp8_per_tensor': one scale per tensor, set by the reference's
+    calibrate-once rule evaluated on the device.  'fp8_per_token_head': one
+    scale per (token, kv head), amax / 448 (1 for an all-zero head), written
+    to k_scale/v_scale of shape (num_blocks, block_size, num_kv_heads)
+    (attention.py:166-181).
     """
-    if kv_cache_dtype == "fp8_per_token_head":
-        raise NotImplementedError("fp8_per_token_head KV scales are not implemented by mkv yet")
-    if kv_cache_dtype != "fp8_per_tensor":
+    if kv_cache_dtype not in ("fp8_per_tensor", "fp8_per_token_head"):
         raise ValueError(f"store_kvcache_fp8: unknown kv_cache_dtype {kv_cache_dtype!r}")
     num_tokens, num_kv_heads, head_dim = key.shape
     _check_cache(k_cache, v_cache, num_kv_heads, head_dim)
     if k_cache.dtype != torch.float8_e4m3fn:
         raise TypeError(f"fp8 cache expected, got {k_cache.dtype}")
+    if kv_cache_dtype == "fp8_per_token_head":
+        _append_per_token_head(key, value, k_cache, v_cache, k_scale, v_scale, slot_mapping)
+        return
     calibrate_fp8_per_tensor(key, value, k_scale, v_scale)
     _append(key, value, k_cache, v_cache, slot_mapping, k_scale, v_scale)
 
@@ -205,7 +260,7 @@ def store_kvcache_fp8(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Ten
 # ---------------------------------------------------------------------------
 def _decode(query, k_cache, v_cache, block_tables, context_lens, scale, num_heads,
             num_kv_heads, head_dim, k_scale=None, v_scale=None, split_tokens=0,
-            out=None) -> torch.Tensor:
+            out=None, per_token_head=False) -> torch.Tensor:
     dev = _require_gpu(query, k_cache, v_cache, block_tables, context_lens)
     query = query.contiguous()
     batch = query.shape[0]
@@ -220,9 +275,11 @@ def _decode(query, k_cache, v_cache, block_tables, context_lens, scale, num_head
     cl = _ctx_lens(context_lens)
     max_blocks = bt.shape[1]
     bs = k_cache.shape[1]
-    fp8 = k_cache.dtype == torch.float8_e4m3fn
-    if fp8 and (k_scale is None or v_scale is None):
-        raise ValueError("an fp8 cache needs k_scale and v_scale")
+    quant = k_cache.dtype in (torch.float8_e4m3fn, torch.int8)
+    if quant and (k_scale is None or v_scale is None):
+        raise ValueError("a quantised cache needs k_scale and v_scale")
+    if per_token_head:
+        _check_token_scales(k_scale, v_scale, k_cache)
     nbytes = _lib.query("mkv_paged_decode_workspace_size", batch, num_heads, num_kv_heads,
                         max_blocks, bs, head_dim, split_tokens)
     ws = _workspace(dev, "decode", nbytes) if nbytes else None
@@ -230,7 +287,8 @@ def _decode(query, k_cache, v_cache, block_tables, context_lens, scale, num_head
         "mkv_paged_decode", out.data_ptr(), out.stride(0), query.data_ptr(), query.stride(0),
         _dtype_code(query, "query"), k_cache.data_ptr(), v_cache.data_ptr(),
         _dtype_code(k_cache, "k_cache"), k_cache.shape[0],
-        k_scale.data_ptr() if fp8 else None, v_scale.data_ptr() if fp8 else None,
+        k_scale.data_ptr() if quant else None, v_scale.data_ptr() if quant else None,
+        _lib.SCALE_PER_TOKEN_HEAD if per_token_head else _lib.SCALE_PER_TENSOR,
         bt.data_ptr(), bt.stride(0), max_blocks, cl.data_ptr(), _index_dtype(cl), batch,
         num_heads, num_kv_heads, head_dim, bs, float(scale), split_tokens,
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
@@ -255,14 +313,26 @@ def paged_attention_decode_quantized(query: torch.Tensor, k_cache: torch.Tensor,
                                      context_lens: torch.Tensor, scale: float, num_heads: int,
                                      num_kv_heads: int, head_dim: int, block_size: int,
                                      kv_cache_dtype: str) -> torch.Tensor:
-    """Decode attention over an FP8 per-tensor cache (dequantised as
-    fp8 * scale).  Reference: attention.py:1213-1268."""
-    if kv_cache_dtype in ("fp8_per_token_head", "int8_per_token_head"):
-        raise NotImplementedError(f"{kv_cache_dtype} decode is not implemented by mkv yet")
-    if kv_cache_dtype != "fp8_per_tensor":
+    """Decode attention over a quantised cache, dequantised as code * scale.
+    Reference: attention.py:1213-1268.
+
+    'fp8_per_tensor': FP8 cache, k_scale/v_scale of one element each.
+    'fp8_per_token_head' / 'int8_per_token_head': FP8 / INT8 cache with
+    float32 (num_blocks, block_size, num_kv_heads) scales; the K scale
+    multiplies the score and the V scale the softmax weight of its token
+    (the reference's tile kernel, attention.py:1124-1210).
+    """
+    if kv_cache_dtype == "fp8_per_tensor" or kv_cache_dtype == "fp8_per_token_head":
+        if k_cache.dtype != torch.float8_e4m3fn:
+            raise TypeError(f"{kv_cache_dtype} needs an fp8 cache, got {k_cache.dtype}")
+    elif kv_cache_dtype == "int8_per_token_head":
+        if k_cache.dtype != torch.int8:
+            raise TypeError(f"{kv_cache_dtype} needs an int8 cache, got {k_cache.dtype}")
+    else:
         raise ValueError(f"unknown quantized kv_cache_dtype {kv_cache_dtype!r}")
     return _decode(query, k_cache, v_cache, block_tables, context_lens, scale, num_heads,
-                   num_kv_heads, head_dim, k_scale, v_scale)
+                   num_kv_heads, head_dim, k_scale, v_scale,
+                   per_token_head=kv_cache_dtype in PER_TOKEN_HEAD_MODES)
 
 
 # ---------------------------------------------------------------------------
@@ -282,8 +352,13 @@ def paged_attention_prefill_triton(query: torch.Tensor, k_cache: torch.Tensor,
     positions[i] + 1)).  The name is kept for drop-in compatibility with
     attention.py:852-891; the work runs on the gfx950 MFMA kernel.  With an
     FP8 cache pass k_scale/v_scale (kv_cache_dtype='fp8_per_tensor'), which
-    the reference does not implement (attention.py:1702-1708).
+    the reference does not implement (attention.py:1702-1708).  Per-token-head
+    caches raise NotImplementedError here, as in the reference.
     """
+    if kv_cache_dtype in PER_TOKEN_HEAD_MODES or k_cache.dtype == torch.int8:
+        raise NotImplementedError(
+            "chunked prefill for per-token-head quantized KV cache needs a dequantizing paged "
+            "prefill/extend attention path")
     dev = _require_gpu(query, k_cache, v_cache, block_tables, context_lens, cu_seqlens_q,
                        positions)
     query = query.contiguous()
@@ -307,8 +382,8 @@ def paged_attention_prefill_triton(query: torch.Tensor, k_cache: torch.Tensor,
     _lib.call(
         "mkv_paged_prefill", out.data_ptr(), query.data_ptr(), _dtype_code(query, "query"),
         k_cache.data_ptr(), v_cache.data_ptr(), _dtype_code(k_cache, "k_cache"), k_cache.shape[0],
-        k_scale.data_ptr() if fp8 else None, v_scale.data_ptr() if fp8 else None, bt.data_ptr(),
-        bt.stride(0), bt.shape[1], cl.data_ptr(), _index_dtype(cl), cu.data_ptr(), pos.data_ptr(),
+        k_scale.data_ptr() if fp8 else None, v_scale.data_ptr() if fp8 else None,
+        _lib.SCALE_PER_TENSOR, bt.data_ptr(), bt.stride(0), bt.shape[1], cl.data_ptr(), _index_dtype(cl), cu.data_ptr(), pos.data_ptr(),
         num_seqs, total_q, num_heads, num_kv_heads, head_dim, k_cache.shape[1], float(scale),
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
         _stream(dev))
@@ -375,9 +450,11 @@ class Attention(nn.Module):
     ``forward(q, k, v)`` contract (attention.py:1617-1807).
 
     The runner injects ``k_cache``, ``v_cache``, ``k_scale``, ``v_scale`` and
-    ``kv_cache_dtype`` ('auto' or 'fp8_per_tensor'), then sets the per-step
-    :class:`~mkv.context.Context`.  Unlike the reference, an FP8 cache also
-    works for chunked / mixed prefill.
+    ``kv_cache_dtype`` ('auto', 'fp8_per_tensor', 'fp8_per_token_head' or
+    'int8_per_token_head'), then sets the per-step
+    :class:`~mkv.context.Context`.  Unlike the reference, an FP8 per-tensor
+    cache also works for chunked / mixed prefill; per-token-head caches raise
+    there, as in the reference (attention.py:1702-1708).
     """
 
     def __init__(self, num_heads: int, head_dim: int, scale: float = 1.0,
@@ -395,19 +472,19 @@ class Attention(nn.Module):
 
     def _mode(self) -> str:
         mode = self.kv_cache_dtype
-        if mode in ("auto", "fp8_per_tensor"):
+        if mode in ("auto", "fp8_per_tensor") or mode in PER_TOKEN_HEAD_MODES:
             return mode
-        if isinstance(mode, str) and (mode.startswith("kivi") or mode in (
-                "fp8_per_token_head", "int8_per_token_head")):
+        if isinstance(mode, str) and mode.startswith("kivi"):
             raise NotImplementedError(f"kv_cache_dtype {mode!r} is not implemented by mkv")
         raise ValueError(f"unknown kv_cache_dtype {mode!r}")
 
     def _decode(self, q, block_tables, context_lens, scale):
-        if self._mode() == "fp8_per_tensor":
+        mode = self._mode()
+        if mode != "auto":
             return paged_attention_decode_quantized(
                 q, self.k_cache, self.v_cache, self.k_scale, self.v_scale, block_tables,
                 context_lens, scale, self.num_heads, self.num_kv_heads, self.head_dim,
-                self.block_size, "fp8_per_tensor")
+                self.block_size, mode)
         return paged_attention_decode(q, self.k_cache, self.v_cache, block_tables, context_lens,
                                       scale, self.num_heads, self.num_kv_heads, self.head_dim,
                                       self.block_size)
@@ -427,7 +504,10 @@ class Attention(nn.Module):
             if k.dim() == 4:
                 k = k.reshape(-1, k.shape[-2], k.shape[-1])
                 v = v.reshape(-1, v.shape[-2], v.shape[-1])
-            if mode == "fp8_per_tensor":
+            if mode == "int8_per_token_head":
+                store_kvcache_int8(k, v, self.k_cache, self.v_cache, self.k_scale, self.v_scale,
+                                   context.slot_mapping, self.block_size)
+            elif mode in ("fp8_per_tensor", "fp8_per_token_head"):
                 store_kvcache_fp8(k, v, self.k_cache, self.v_cache, self.k_scale, self.v_scale,
                                   context.slot_mapping, self.block_size, mode)
             else:
@@ -443,6 +523,10 @@ class Attention(nn.Module):
                 o = flash_attention_prefill(q, k, v, cu_seqlens, scale, self.num_heads,
                                             self.num_kv_heads, self.head_dim)
                 return o.reshape(o.shape[0], self.num_heads * self.head_dim)
+            if mode in PER_TOKEN_HEAD_MODES:  # as the reference, attention.py:1702-1708
+                raise NotImplementedError(
+                    "chunked prefill for quantized KV cache needs a dequantizing paged "
+                    "prefill/extend attention path")
             if context.positions is None or context.context_lens is None or context.block_tables is None:
                 raise ValueError("paged prefill requires positions, context_lens, and block_tables")
             split = context.mixed_attention_split

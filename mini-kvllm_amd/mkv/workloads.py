@@ -142,6 +142,31 @@ def fill_pool_on_device(pool: torch.Tensor, seed: int, scale: float | None = Non
     return scale if pool.dtype == torch.float8_e4m3fn else None
 
 
+def fill_pool_per_token_head_on_device(pool: torch.Tensor, scales: torch.Tensor, seed: int,
+                                       mode: str) -> None:
+    """Fill a (N, bs, H, D) FP8 / INT8 pool and its (N, bs, H) fp32 scales on
+    their device: seeded N(0, 1) bf16 rows, each (token, head) scaled by
+    2^U(-2, 2), quantised by the per-token-head append kernel into every slot
+    in order (mode 'fp8_per_token_head' or 'int8_per_token_head')."""
+    from . import attention as A
+
+    N, bs, H, D = pool.shape
+    rows = N * bs
+    flat_pool = pool.view(N * bs, 1, H, D).view(N, bs, H, D)
+    step = max(1, (1 << 26) // (H * D))  # ~64M elements per chunk
+    g = torch.Generator(device=pool.device).manual_seed(seed)
+    for i in range(0, rows, step):
+        n = min(step, rows - i)
+        x = torch.randn(n, H, D, generator=g, device=pool.device)
+        x = x * torch.exp2(torch.rand(n, H, 1, generator=g, device=pool.device) * 4 - 2)
+        x = x.to(torch.bfloat16)
+        slots = torch.arange(i, i + n, dtype=torch.int64, device=pool.device)
+        if mode == "int8_per_token_head":
+            A.store_kvcache_int8(x, x, flat_pool, flat_pool, scales, scales, slots, bs)
+        else:
+            A.store_kvcache_fp8(x, x, flat_pool, flat_pool, scales, scales, slots, bs, mode)
+
+
 def prefill_mixed(seed: int = 4, num_prefill: int = 8, chunk: int = 512, num_decode: int = 120,
                   block_size: int = 256, num_blocks: int = 4096) -> dict:
     """Chunked-prefill mixed batch metadata: prefill sequence s has prior
@@ -178,11 +203,12 @@ def prefill_mixed(seed: int = 4, num_prefill: int = 8, chunk: int = 512, num_dec
 
 def alg_bytes_decode(context_lens: torch.Tensor, block_size: int, num_heads: int,
                      num_kv_heads: int, kv_bytes: int, q_bytes: int = 2,
-                     ctx_bytes: int = 8) -> int:
+                     ctx_bytes: int = 8, scale_bytes: int = 0) -> int:
     """Algorithmic HBM bytes of one decode step: every visible K and V element
-    once, q and out once, the used block-table entries and context_lens."""
+    once (plus its K and V scales for per-token-head caches, scale_bytes = 4),
+    q and out once, the used block-table entries and context_lens."""
     L = context_lens.to(torch.int64)
-    kv = int(L.sum()) * num_kv_heads * HEAD_DIM * 2 * kv_bytes
+    kv = int(L.sum()) * num_kv_heads * (HEAD_DIM * kv_bytes + scale_bytes) * 2
     qo = int(L.numel()) * num_heads * HEAD_DIM * 2 * q_bytes
     bt = int(((L + block_size - 1) // block_size).sum()) * 4
     return kv + qo + bt + int(L.numel()) * ctx_bytes

@@ -70,10 +70,67 @@ def store_kvcache_fp8_ref(key, value, k_cache, v_cache, k_scale, v_scale, slot_m
     v_cache.view(-1, H, D)[slots] = fp8_quantize_ref(value[valid], float(v_scale.reshape(-1)[0]))
 
 
-def dequant_ref(cache: torch.Tensor, scale: float | None) -> torch.Tensor:
-    """fp8 -> fp32 times the per-tensor scale, in fp32 (attention.py:1051-1062,
-    :1098-1107); bf16/fp16/fp32 are upcast to fp32 exactly, fp64 is kept."""
-    if cache.dtype == torch.float8_e4m3fn:
+INT8_MAX, INT8_MIN = 127.0, -128.0
+
+
+def _amax_ignore_nan(x: torch.Tensor) -> torch.Tensor:
+    """max |x| over the last dim in fp32, NaN elements ignored (the Triton
+    max reduction of the reference kernels); 0 when nothing else is left."""
+    a = x.float().abs()
+    return torch.where(torch.isnan(a), torch.zeros_like(a), a).amax(dim=-1)
+
+
+def quantize_per_token_head_ref(x: torch.Tensor, mode: str):
+    """Per-(token, head) quantisation of x (T, H, D) -> (q, scale (T, H) fp32).
+
+    fp8 (store_kvcache_fp8_kernel, PER_TOKEN_HEAD branch, attention.py:166-191):
+      scale = amax / 448 if amax > 0 else 1.0; q = clamp(x / scale, +-448)
+      cast to e4m3fn (RNE).
+    int8 (store_kvcache_int8_kernel, attention.py:230-243):
+      scale = max(amax / 127, 1e-6); y = x * (1 / scale); y += 0.5 if y >= 0
+      else -0.5; clamp to [-128, 127] with maxNum / minNum (tl.clamp's
+      non-propagating form: a NaN becomes -128); truncate to int8.
+    amax ignores NaN elements (maxNum reduction).  All arithmetic in fp32,
+    in the reference's order, with IEEE divisions."""
+    xf = x.float()
+    amax = _amax_ignore_nan(x)
+    if mode == "fp8_per_token_head":
+        scale = torch.where(amax > 0, amax / torch.tensor(FP8_E4M3_MAX), torch.ones_like(amax))
+        q = torch.clamp(xf / scale[..., None], -FP8_E4M3_MAX, FP8_E4M3_MAX).to(torch.float8_e4m3fn)
+    elif mode == "int8_per_token_head":
+        scale = torch.maximum(amax / torch.tensor(INT8_MAX), torch.tensor(1e-6, dtype=torch.float32))
+        inv = torch.tensor(1.0, dtype=torch.float32) / scale
+        y = xf * inv[..., None]
+        y = torch.where(y >= 0, y + 0.5, y - 0.5)
+        y = torch.fmin(torch.fmax(y, torch.tensor(INT8_MIN)), torch.tensor(INT8_MAX))
+        q = y.trunc().to(torch.int8)
+    else:
+        raise ValueError(mode)
+    return q, scale
+
+
+def store_kvcache_quant_ref(key, value, k_cache, v_cache, k_scale, v_scale, slot_mapping,
+                            mode: str) -> None:
+    """Per-token-head append (attention.py:118-191 PER_TOKEN_HEAD=1, :195-276):
+    quantise every valid row and write its bytes and its (slot, head) scales;
+    k_scale/v_scale: (N, bs, H) fp32, slot -1 rows untouched."""
+    H, D = key.shape[1], key.shape[2]
+    valid = slot_mapping >= 0
+    slots = slot_mapping[valid]
+    for x, cache, sc in ((key, k_cache, k_scale), (value, v_cache, v_scale)):
+        q, s = quantize_per_token_head_ref(x[valid], mode)
+        cache.view(-1, H, D)[slots] = q
+        sc.view(-1, H)[slots] = s
+
+
+def dequant_ref(cache: torch.Tensor, scale) -> torch.Tensor:
+    """fp8 / int8 -> fp32 times the scale, in fp32 (attention.py:1051-1062,
+    :1098-1107, per-token-head :1172-1197): scale is a float (per tensor) or a
+    tensor broadcasting over the last dim (per token and head).  bf16 / fp16 /
+    fp32 are upcast to fp32 exactly, fp64 is kept."""
+    if cache.dtype in (torch.float8_e4m3fn, torch.int8):
+        if isinstance(scale, torch.Tensor):
+            return cache.to(torch.float32) * scale.to(torch.float32)[..., None]
         return cache.to(torch.float32) * scale
     if cache.dtype == torch.float64:
         return cache
@@ -109,8 +166,12 @@ def _seq_kv(k_cache, v_cache, block_tables, b, L, k_scale=None, v_scale=None):
     tbl = block_tables[b, :nb].to(torch.int64)
     ok_blk = (tbl >= 0) & (tbl < N)
     safe = torch.where(ok_blk, tbl, torch.zeros_like(tbl))
-    k = dequant_ref(k_cache[safe], k_scale).reshape(nb * bs, H, D)[:L]
-    v = dequant_ref(v_cache[safe], v_scale).reshape(nb * bs, H, D)[:L]
+    if isinstance(k_scale, torch.Tensor):  # per token and head: (N, bs, H)
+        k = dequant_ref(k_cache[safe], k_scale[safe]).reshape(nb * bs, H, D)[:L]
+        v = dequant_ref(v_cache[safe], v_scale[safe]).reshape(nb * bs, H, D)[:L]
+    else:
+        k = dequant_ref(k_cache[safe], k_scale).reshape(nb * bs, H, D)[:L]
+        v = dequant_ref(v_cache[safe], v_scale).reshape(nb * bs, H, D)[:L]
     valid = ok_blk.repeat_interleave(bs)[:L]
     return k, v, valid
 
@@ -238,6 +299,61 @@ def paged_decode_literal(query, k_cache, v_cache, block_tables, context_lens, sc
                         if p != -1:
                             acc = acc + pw[i] * vf[p, t % bs, kvh]
                             l_i += pw[i]
+                m_i = m_new
+            out[b, h] = acc / l_i if l_i > 0 else 0.0
+    return out
+
+
+def paged_decode_tile_literal(query, k_cache, v_cache, k_scale, v_scale, block_tables,
+                              context_lens, scale, num_heads, num_kv_heads) -> torch.Tensor:
+    """Step-by-step restatement of paged_attention_decode_quantized_tile_kernel
+    (attention.py:1124-1210), the per-token-head FP8 / INT8 decode, in float64
+    Python loops.  k_scale / v_scale: (N, bs, Hkv) per-slot scales.
+
+    Per 64-token chunk: qk_t = (K_raw_t . q) * k_scale_t * scale, set to -1e10
+    for t >= context_len; p_t = exp(qk_t - m) (0 past the context);
+    acc = acc * alpha + sum_t p_t * v_scale_t * V_raw_t; l = l * alpha + sum_t p_t.
+    A block entry of -1 inside the context makes the kernel's masked loads
+    return K = V = 0 and scales 0, so such a token still adds exp(0 - m) to l;
+    that is kept here as the reference has it.  Tiny inputs only."""
+    B, Hq, D = query.shape
+    G = num_heads // num_kv_heads
+    max_blocks = block_tables.shape[1]
+    bs = k_cache.shape[1]
+    BLOCK_N = 64
+    out = torch.zeros(B, Hq, D, dtype=torch.float64)
+    kr, vr = k_cache.double(), v_cache.double()
+    ksc, vsc = k_scale.double(), v_scale.double()
+    for b in range(B):
+        L = int(context_lens[b])
+        for h in range(Hq):
+            kvh = h // G
+            q = query[b, h].double()
+            acc = torch.zeros(D, dtype=torch.float64)
+            l_i, m_i = 0.0, -1e10
+            for start in range(0, max_blocks * bs, BLOCK_N):
+                if start >= L:
+                    continue
+                qk, kv_rows = [], []
+                for i in range(BLOCK_N):
+                    t = start + i
+                    p = int(block_tables[b, t // bs]) if t // bs < max_blocks else -1
+                    if t < L and p != -1:
+                        k_t, ks_t = kr[p, t % bs, kvh], float(ksc[p, t % bs, kvh])
+                        v_t, vs_t = vr[p, t % bs, kvh], float(vsc[p, t % bs, kvh])
+                    else:  # masked loads: other = 0
+                        k_t = v_t = torch.zeros(D, dtype=torch.float64)
+                        ks_t = vs_t = 0.0
+                    qk.append(float((k_t * q).sum()) * ks_t * scale if t < L else -1e10)
+                    kv_rows.append((v_t, vs_t, t < L))
+                m_new = max(m_i, max(qk))
+                alpha = math.exp(m_i - m_new)
+                acc = acc * alpha
+                l_i = l_i * alpha
+                for x, (v_t, vs_t, valid) in zip(qk, kv_rows):
+                    pw = math.exp(x - m_new) if valid else 0.0
+                    acc = acc + (pw * vs_t) * v_t
+                    l_i += pw
                 m_i = m_new
             out[b, h] = acc / l_i if l_i > 0 else 0.0
     return out

@@ -23,7 +23,8 @@ def _declared_functions() -> set[str]:
 
 def test_header_declares_expected_entry_points():
     names = _declared_functions()
-    for n in ("mkv_kv_append", "mkv_fp8_calibrate_per_tensor", "mkv_paged_decode",
+    for n in ("mkv_kv_append", "mkv_kv_append_per_token_head", "mkv_fp8_calibrate_per_tensor",
+              "mkv_paged_decode",
               "mkv_paged_prefill", "mkv_flash_prefill", "mkv_gather_kv", "mkv_abi_version",
               "mkv_status_string"):
         assert n in names
@@ -54,7 +55,7 @@ def test_argument_validation_without_launch():
                              nul, nul, nul) == -1
     # unsupported head_dim / group / block size in decode
     p = ctypes.c_void_p(16)
-    base = [p, 4096, p, 4096, 1, p, p, 1, 10, nul, nul, p, 4, 4, p, 1, 2]
+    base = [p, 4096, p, 4096, 1, p, p, 1, 10, nul, nul, 0, p, 4, 4, p, 1, 2]
     assert lib.mkv_paged_decode(*base, 32, 8, 64, 256, 0.1, 0, nul, 0, nul) == -4
     assert lib.mkv_paged_decode(*base, 32, 6, 128, 256, 0.1, 0, nul, 0, nul) == -5
     assert lib.mkv_paged_decode(*base, 32, 8, 128, 100, 0.1, 0, nul, 0, nul) == -6
@@ -64,6 +65,28 @@ def test_argument_validation_without_launch():
     # zero tokens / batch is a no-op that succeeds
     assert lib.mkv_kv_append(nul, 1024, nul, 1024, nul, nul, nul, 0, 8, 128, 16, 4, 1, 3,
                              nul, nul, nul) == 0
+    # quantised caches: INT8 needs per-token-head scales, scales must be given,
+    # and an unknown scale mode is rejected
+    q8 = [p, 4096, p, 4096, 1, p, p]
+    tail = [p, 4, 4, p, 1, 2, 32, 8, 128, 256, 0.1, 0, p, 1 << 20, nul]
+    assert lib.mkv_paged_decode(*q8, 4, 10, p, p, 0, *tail) == -3
+    assert lib.mkv_paged_decode(*q8, 4, 10, nul, p, 1, *tail) == -1
+    assert lib.mkv_paged_decode(*q8, 3, 10, p, p, 7, *tail) == -3
+    # per-token-head append: head_dim must be a power of two in 16..1024,
+    # the cache FP8 or INT8
+    assert lib.mkv_kv_append_per_token_head(p, 1024, p, 1024, p, p, p, p, p, 4, 8, 96, 16, 4,
+                                            1, 3, nul) == -4
+    assert lib.mkv_kv_append_per_token_head(p, 1024, p, 1024, p, p, p, p, p, 4, 8, 128, 16, 4,
+                                            1, 1, nul) == -3
+    assert lib.mkv_kv_append_per_token_head(p, 1024, p, 1024, p, p, nul, p, p, 4, 8, 128, 16, 4,
+                                            1, 4, nul) == -1
+    # per-token-head scales are not accepted by the prefill kernel
+    pre = [p, p, 1, p, p, 3, 10, p, p, 1, p, 4, 4, p, 1, p, p, 1, 4, 32, 8, 128, 256, 0.1,
+           p, 1 << 20, nul]
+    assert lib.mkv_paged_prefill(*pre) == -3
+    pre[2 + 3] = 4  # an INT8 cache
+    pre[9] = 0
+    assert lib.mkv_paged_prefill(*pre) == -3
 
 
 def test_decode_workspace_and_split_queries():
@@ -90,11 +113,17 @@ def test_wrappers_reject_cpu_tensors_and_unimplemented_modes():
     slots = torch.zeros(2, dtype=torch.int64)
     with pytest.raises(ValueError, match="no CPU fallback"):
         A.store_kvcache(k, k, kc, kc, slots, 16)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(TypeError, match="fp8 cache expected"):
         A.store_kvcache_fp8(k, k, kc, kc, None, None, slots, 16, "fp8_per_token_head")
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(TypeError, match="int8 cache"):
         A.paged_attention_decode_quantized(k, kc, kc, None, None, None, None, 0.1, 8, 8, 128, 16,
                                            "int8_per_token_head")
+    with pytest.raises(ValueError, match="unknown"):
+        A.paged_attention_decode_quantized(k, kc, kc, None, None, None, None, 0.1, 8, 8, 128, 16,
+                                           "fp4")
+    with pytest.raises(NotImplementedError):
+        A.paged_attention_prefill_triton(k, kc, kc, None, None, None, None, 0.1, 8, 8, 128, 16,
+                                         kv_cache_dtype="fp8_per_token_head")
     with pytest.raises(AssertionError):
         A.store_kvcache(k, k, kc, torch.zeros(2, 16, 8, 128), slots, 16)
     with pytest.raises(AssertionError):

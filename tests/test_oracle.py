@@ -339,3 +339,154 @@ def test_gather_ref():
                 assert torch.equal(out[b, t], k[int(bt[b, t // 8]), t % 8])
             else:
                 assert int(torch.count_nonzero(out[b, t])) == 0
+
+
+# ---------------------------------------------------------------------------
+# Per-token-head FP8 / INT8 quantisation (attention.py:166-181, :194-243)
+# ---------------------------------------------------------------------------
+FP8_MODE, INT8_MODE = "fp8_per_token_head", "int8_per_token_head"
+
+
+def test_per_token_fp8_known_answers():
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(5, 3, 16, generator=g) * 100
+    # amax exactly 448 -> scale exactly 1 -> the codes are torch's own cast
+    x[..., 3] = 448.0
+    q, s = R.quantize_per_token_head_ref(x, FP8_MODE)
+    assert torch.equal(s, torch.ones(5, 3))
+    assert torch.equal(q.view(torch.uint8), x.to(torch.float8_e4m3fn).view(torch.uint8))
+    # an all-zero head -> scale 1 and zero codes; NaN elements do not count
+    # towards amax and stay NaN
+    z = torch.zeros(1, 2, 16)
+    z[0, 1, 0], z[0, 1, 5] = float("nan"), -2.0
+    q, s = R.quantize_per_token_head_ref(z, FP8_MODE)
+    assert float(s[0, 0]) == 1.0 and torch.count_nonzero(q[0, 0].view(torch.uint8)) == 0
+    assert float(s[0, 1]) == np.float32(2.0) / np.float32(448.0)
+    assert int(q[0, 1, 5].view(torch.uint8)) == 0xFE  # -448
+    assert int(q[0, 1, 0].view(torch.uint8)) & 0x7F == 0x7F  # NaN
+
+
+def test_per_token_fp8_power_of_two_invariance_and_error_bound():
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(7, 4, 64, generator=g) * torch.rand(7, 4, 1, generator=g) * 10
+    q, s = R.quantize_per_token_head_ref(x, FP8_MODE)
+    for k in (-5, 3, 11):
+        q2, s2 = R.quantize_per_token_head_ref(x * 2.0 ** k, FP8_MODE)
+        assert torch.equal(s2, s * 2.0 ** k)
+        assert torch.equal(q2.view(torch.uint8), q.view(torch.uint8))
+    # the head's amax maps to +-448 and every element is within half an e4m3
+    # step (3 mantissa bits) of x / scale, or below the subnormal step
+    y = x / s[..., None]
+    deq = q.to(torch.float64)
+    amax_pos = x.abs().argmax(dim=-1, keepdim=True)
+    assert torch.equal(deq.abs().gather(-1, amax_pos), torch.full_like(deq[..., :1], 448.0))
+    step = torch.exp2(torch.floor(torch.log2(y.abs().clamp(min=2.0 ** -6))) - 3)
+    assert bool(((deq - y.double()).abs() <= step.double() / 2 + 1e-12).all())
+
+
+def test_per_token_int8_known_answers():
+    # amax 127 -> scale 1, 1 / scale 1: the rounding is half away from zero
+    x = torch.tensor([2.5, -2.5, 0.49, -0.5, 126.6, -127.0, 1.5, -1.49, 127.0, 0.5,
+                      -0.0, 3.0, -3.5, 60.5, -60.5, 0.0]).reshape(1, 1, 16)
+    q, s = R.quantize_per_token_head_ref(x, INT8_MODE)
+    assert float(s) == 1.0
+    assert q.flatten().tolist() == [3, -3, 0, -1, 127, -127, 2, -1, 127, 1, 0, 3, -4, 61, -61, 0]
+    # an all-zero head -> scale 1e-6 (fp32) and zero codes; a tiny head is
+    # floored at 1e-6 too; a NaN becomes -128 and does not count towards amax
+    z = torch.zeros(3, 1, 16)
+    z[1, 0, :2] = torch.tensor([1e-5, -4e-6])
+    z[2, 0, 0], z[2, 0, 1] = float("nan"), 63.5
+    q, s = R.quantize_per_token_head_ref(z, INT8_MODE)
+    assert float(s[0, 0]) == float(np.float32(1e-6)) and torch.count_nonzero(q[0]) == 0
+    assert float(s[1, 0]) == float(np.float32(1e-6))
+    assert q[1, 0, :2].tolist() == [10, -4]
+    assert float(s[2, 0]) == float(np.float32(63.5) / np.float32(127.0))
+    assert q[2, 0, :2].tolist() == [-128, 127]
+
+
+def test_per_token_int8_error_bound():
+    g = torch.Generator().manual_seed(33)
+    x = torch.randn(9, 8, 128, generator=g) * torch.rand(9, 8, 1, generator=g) * 50
+    q, s = R.quantize_per_token_head_ref(x, INT8_MODE)
+    deq = q.double() * s.double()[..., None]
+    assert bool(((deq - x.double()).abs() <= s.double()[..., None] * (0.5 + 1e-5)).all())
+    assert int(q.abs().amax()) == 127
+
+
+@pytest.mark.parametrize("mode", [FP8_MODE, INT8_MODE])
+def test_store_kvcache_quant_ref_matches_loop(mode):
+    g = torch.Generator().manual_seed(34)
+    T, H, D, N, bs = 11, 2, 16, 4, 4
+    k = torch.randn(T, H, D, generator=g)
+    v = torch.randn(T, H, D, generator=g)
+    slots = torch.randperm(N * bs, generator=g)[:T].to(torch.int64)
+    slots[::4] = -1
+    cdt = torch.float8_e4m3fn if mode == FP8_MODE else torch.int8
+    kc = torch.zeros(N, bs, H, D, dtype=cdt)
+    vc = torch.zeros_like(kc)
+    ks, vs = torch.ones(N, bs, H), torch.ones(N, bs, H)
+    R.store_kvcache_quant_ref(k, v, kc, vc, ks, vs, slots, mode)
+    for t in range(T):
+        sl = int(slots[t])
+        if sl == -1:
+            continue
+        for x, cache, sc in ((k, kc, ks), (v, vc, vs)):
+            qrow, srow = R.quantize_per_token_head_ref(x[t:t + 1], mode)
+            assert torch.equal(cache[sl // bs, sl % bs].view(torch.uint8), qrow[0].view(torch.uint8))
+            assert torch.equal(sc[sl // bs, sl % bs], srow[0])
+    untouched = torch.ones(N * bs, dtype=torch.bool)
+    untouched[slots[slots >= 0]] = False
+    assert bool((ks.view(-1, H)[untouched] == 1).all()) and bool((vs.view(-1, H)[untouched] == 1).all())
+    assert torch.count_nonzero(kc.view(N * bs, -1)[untouched].view(torch.uint8)) == 0
+
+
+def _tiny_token_quant(seed, mode, B=2, Hq=4, Hkv=2, D=16, N=12, bs=8, max_blocks=5):
+    q, k, v, bt, ctx, _, _ = _tiny_decode(seed, B, Hq, Hkv, D, N, bs, max_blocks)
+    k = k * torch.rand(N, bs, Hkv, 1, generator=torch.Generator().manual_seed(seed)) * 4
+    kq, ks = R.quantize_per_token_head_ref(k.reshape(-1, Hkv, D), mode)
+    vq, vs = R.quantize_per_token_head_ref(v.reshape(-1, Hkv, D), mode)
+    return (q, kq.reshape(N, bs, Hkv, D), vq.reshape(N, bs, Hkv, D), ks.reshape(N, bs, Hkv),
+            vs.reshape(N, bs, Hkv), bt, ctx)
+
+
+@pytest.mark.parametrize("seed,mode", [(40, FP8_MODE), (41, INT8_MODE), (42, INT8_MODE)])
+def test_decode_ref_per_token_matches_tile_literal(seed, mode):
+    q, kq, vq, ks, vs, bt, ctx = _tiny_token_quant(seed, mode)
+    got = R.paged_decode_ref(q, kq, vq, bt, ctx, 0.3, 4, 2, ks, vs)
+    want = R.paged_decode_tile_literal(q, kq, vq, ks, vs, bt, ctx, 0.3, 4, 2)
+    assert torch.allclose(got.double(), want, atol=1e-6, rtol=0)
+
+
+def test_decode_ref_per_token_with_uniform_scales_is_per_tensor():
+    # the same scale in every slot reduces to the per-tensor dequantisation
+    q, kq, vq, ks, vs, bt, ctx = _tiny_token_quant(43, FP8_MODE)
+    a = R.paged_decode_ref(q, kq, vq, bt, ctx, 0.3, 4, 2, torch.full_like(ks, 0.37),
+                           torch.full_like(vs, 1.9))
+    b = R.paged_decode_ref(q, kq, vq, bt, ctx, 0.3, 4, 2, 0.37, 1.9)
+    assert torch.equal(a, b)
+    # and per-token scales are per slot: scaling one slot's V scale moves the
+    # output exactly as scaling that token's V values does
+    b0, s0 = 0, int(bt[0, 0])
+    vs2 = vs.clone()
+    vs2[s0, 1] *= 3.0
+    vdeq = vq.float() * vs[..., None]
+    vdeq2 = vdeq.clone()
+    vdeq2[s0, 1] *= 3.0
+    kdeq = kq.float() * ks[..., None]
+    got = R.paged_decode_ref(q, kq, vq, bt, ctx, 0.3, 4, 2, ks, vs2)
+    want = R.paged_decode_ref(q, kdeq, vdeq2, bt, ctx, 0.3, 4, 2)
+    assert torch.allclose(got, want, atol=1e-6)
+
+
+def test_tile_literal_keeps_the_reference_hole_quirk():
+    # a -1 block inside the context: the per-tensor kernels skip its tokens,
+    # the reference's tile kernel adds exp(0 - m) per token to the denominator
+    q, kq, vq, ks, vs, bt, ctx = _tiny_token_quant(44, INT8_MODE, max_blocks=5)
+    ctx[:] = 5 * 8
+    bt[0] = torch.arange(5, dtype=torch.int32)
+    bt[1] = torch.arange(5, 10, dtype=torch.int32)
+    bt[0, 2] = -1
+    skip = R.paged_decode_ref(q, kq, vq, bt, ctx, 0.3, 4, 2, ks, vs)
+    lit = R.paged_decode_tile_literal(q, kq, vq, ks, vs, bt, ctx, 0.3, 4, 2)
+    assert torch.allclose(skip[1].double(), lit[1], atol=1e-6)
+    assert not torch.allclose(skip[0].double(), lit[0], atol=1e-3)
