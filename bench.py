@@ -267,8 +267,7 @@ def main() -> int:
         if per_token:
             ksd = torch.empty(N, bs, args.num_kv_heads, device=dev)
             vsd = torch.empty_like(ksd)
-            W.fill_pool_per_token_head_on_device(kc, ksd, 1000 + 2 * l, token_mode)
-            W.fill_pool_per_token_head_on_device(vc, vsd, 1001 + 2 * l, token_mode)
+            W.fill_pools_per_token_head_on_device(kc, vc, ksd, vsd, 1000 + l, token_mode)
             layers.append((kc, vc, (ksd, vsd), None))
             continue
         ks = W.fill_pool_on_device(kc, 1000 + 2 * l)

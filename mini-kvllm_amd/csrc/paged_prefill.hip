@@ -7,20 +7,21 @@
 // FP8 caches are dequantised exactly (e4m3fn -> fp16) in the kernel, which
 // the reference leaves unimplemented (attention.py:1702-1708).
 //
-// Work decomposition: a workgroup of 4 wavefronts owns 128 "rows" of one
+// Work decomposition: a workgroup of 8 wavefronts owns 128 "rows" of one
 // sequence and one KV head, where a row is a (query token, query head of the
 // GQA group) pair, token-major; every row of the group reads the same K/V,
 // so each K/V tile is staged in LDS once for G query heads.  Tiles of 64 keys
 // are gathered through the block table into double-buffered LDS with an XOR
 // swizzle on 16-byte chunks (conflict-free MFMA operand reads).  Each wave
-// owns 2 row tiles of 16 and computes
+// owns one row tile of 16 and computes
 //   S^T = K Q^T     (A = K from LDS, B = Q^T resident in registers)
-//   O  += P V       (A = P straight from the S^T accumulators, B = V from LDS
-//                    transposed in registers with v_perm)
-// with an online softmax in the log2 domain.  The varlen tile list is built on
-// the device by a one-workgroup scan, so the launch needs no host sync; the
-// grid is ordered so that all tiles of one KV head run on one XCD and share
-// its L2.
+//   O  += P V       (A = P straight from the S^T accumulators, B = V read
+//                    from LDS already transposed by ds_read_b64_tr_b16 / _b8)
+// with an online softmax in the log2 domain whose output rescale is deferred
+// until a row's running max grows by more than 2^8.  The varlen tile list is
+// built on the device by a one-workgroup scan, so the launch needs no host
+// sync; the grid is ordered so that all tiles of one KV head run on one XCD
+// and share its L2.
 #include "mkv_device.hpp"
 
 namespace mkv {
@@ -247,7 +248,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const int min_vis = red_lds[0];
   const int max_vis = red_lds[1];
 
-  // Query rows of this wave: row tile rt covers rows (2*wave + rt)*16 + 0..15.
+  // Query rows of this wave: row tile rt covers rows (kRowTiles*wave + rt)*16 + 0..15.
   int vis_c[kRowTiles];
   float qf[kRowTiles][32];
   float qmax = 0.0f;

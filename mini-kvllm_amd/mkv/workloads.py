@@ -142,29 +142,33 @@ def fill_pool_on_device(pool: torch.Tensor, seed: int, scale: float | None = Non
     return scale if pool.dtype == torch.float8_e4m3fn else None
 
 
-def fill_pool_per_token_head_on_device(pool: torch.Tensor, scales: torch.Tensor, seed: int,
-                                       mode: str) -> None:
-    """Fill a (N, bs, H, D) FP8 / INT8 pool and its (N, bs, H) fp32 scales on
-    their device: seeded N(0, 1) bf16 rows, each (token, head) scaled by
-    2^U(-2, 2), quantised by the per-token-head append kernel into every slot
-    in order (mode 'fp8_per_token_head' or 'int8_per_token_head')."""
+def fill_pools_per_token_head_on_device(k_pool: torch.Tensor, v_pool: torch.Tensor,
+                                        k_scale: torch.Tensor, v_scale: torch.Tensor, seed: int,
+                                        mode: str) -> None:
+    """Fill (N, bs, H, D) FP8 / INT8 K and V pools and their (N, bs, H) fp32
+    scales on their device: seeded N(0, 1) bf16 rows, each (token, head)
+    scaled by 2^U(-2, 2), quantised by the per-token-head append kernel into
+    every slot in order (mode 'fp8_per_token_head' or 'int8_per_token_head')."""
     from . import attention as A
 
-    N, bs, H, D = pool.shape
+    N, bs, H, D = k_pool.shape
     rows = N * bs
-    flat_pool = pool.view(N * bs, 1, H, D).view(N, bs, H, D)
     step = max(1, (1 << 26) // (H * D))  # ~64M elements per chunk
-    g = torch.Generator(device=pool.device).manual_seed(seed)
+    g = torch.Generator(device=k_pool.device).manual_seed(seed)
+
+    def rand_rows(n):
+        x = torch.randn(n, H, D, generator=g, device=k_pool.device)
+        x = x * torch.exp2(torch.rand(n, H, 1, generator=g, device=k_pool.device) * 4 - 2)
+        return x.to(torch.bfloat16)
+
     for i in range(0, rows, step):
         n = min(step, rows - i)
-        x = torch.randn(n, H, D, generator=g, device=pool.device)
-        x = x * torch.exp2(torch.rand(n, H, 1, generator=g, device=pool.device) * 4 - 2)
-        x = x.to(torch.bfloat16)
-        slots = torch.arange(i, i + n, dtype=torch.int64, device=pool.device)
+        kx, vx = rand_rows(n), rand_rows(n)
+        slots = torch.arange(i, i + n, dtype=torch.int64, device=k_pool.device)
         if mode == "int8_per_token_head":
-            A.store_kvcache_int8(x, x, flat_pool, flat_pool, scales, scales, slots, bs)
+            A.store_kvcache_int8(kx, vx, k_pool, v_pool, k_scale, v_scale, slots, bs)
         else:
-            A.store_kvcache_fp8(x, x, flat_pool, flat_pool, scales, scales, slots, bs, mode)
+            A.store_kvcache_fp8(kx, vx, k_pool, v_pool, k_scale, v_scale, slots, bs, mode)
 
 
 def prefill_mixed(seed: int = 4, num_prefill: int = 8, chunk: int = 512, num_decode: int = 120,

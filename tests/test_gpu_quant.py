@@ -235,8 +235,7 @@ def test_per_token_decode_batch256_full_size(dev, mode):
     vc = torch.empty_like(kc)
     ks = torch.empty(N, bs, 8, device=dev)
     vs = torch.empty_like(ks)
-    W.fill_pool_per_token_head_on_device(kc, ks, 41, mode)
-    W.fill_pool_per_token_head_on_device(vc, vs, 42, mode)
+    W.fill_pools_per_token_head_on_device(kc, vc, ks, vs, 41, mode)
     g = torch.Generator().manual_seed(33)
     q = torch.randn(256, 32, 128, generator=g).to(torch.bfloat16).to(dev)
     bt, ctx = m["block_tables"].to(dev), m["context_lens"].to(dev)
