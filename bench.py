@@ -166,6 +166,90 @@ def prefill_extra(dev, stream) -> dict:
     return out
 
 
+def decode_step_latency(dev, batches=(1, 8, 32), layers: int = 28, ctx0: int = 700,
+                        steps: int = 30) -> dict:
+    """Wall time of one decode step's attention work for a 28-layer stack
+    (16 q / 8 kv heads, head_dim 128, block 256, FP8 KV, contexts ~700
+    tokens), two ways:
+      eager: the reference runner's per-step host work (prepare_decode,
+        model_runner.py:621-640: Python lists -> pinned tensors -> device)
+        followed by every layer's append + decode launched one by one;
+      graph: the device-side metadata advance (mkv_decode_metadata) and all
+        layers captured once per batch bucket and replayed (mkv.decode_state).
+    Both synchronise at the end of each step; the attention kernels are the
+    same.  Only the attention path runs (no projections or MLP)."""
+    import torch
+
+    from mkv import attention as A
+    from mkv import decode_state as DS
+
+    Hq, Hkv, bs = 16, 8, 256
+    max_rows = max(batches)
+    # lengths ctx0 + 37 b grow by one token per step (steps + 3 warm-up)
+    max_blocks = (ctx0 + 37 * max_rows + steps + 3 + bs - 1) // bs
+    N = max_rows * max_blocks + 8
+    sm = 1.0 / math.sqrt(HEAD_DIM)
+    g = torch.Generator().manual_seed(9)
+    pools = []
+    for _ in range(layers):
+        kc = torch.zeros(N, bs, Hkv, HEAD_DIM, dtype=torch.float8_e4m3fn, device=dev)
+        pools.append((kc, torch.zeros_like(kc), torch.full((1,), 0.02, device=dev),
+                      torch.full((1,), 0.02, device=dev)))
+    q = torch.randn(max_rows, Hq, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    kv = torch.randn(max_rows, Hkv, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    out = torch.empty(layers, max_rows, Hq, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+
+    def layers_fn(rows, slot, ctx, bt):
+        for li, (kc, vc, ks, vs) in enumerate(pools):
+            A.store_kvcache_fp8(kv[:rows], kv[:rows], kc, vc, ks, vs, slot, bs, "fp8_per_tensor")
+            A._decode(q[:rows], kc, vc, bt, ctx, sm, Hq, Hkv, HEAD_DIM, ks, vs, out=out[li, :rows])
+
+    res = {"workload": (f"{layers} layers x (FP8 append + decode), {Hq} q / {Hkv} kv heads, "
+                        f"head_dim {HEAD_DIM}, block {bs}, contexts ~{ctx0} tokens; wall time per "
+                        f"step incl. host work, synchronised; median of {steps}")}
+    for B in batches:
+        tables = [[b * max_blocks + j for j in range(max_blocks)] for b in range(B)]
+        lens = [ctx0 + 37 * b for b in range(B)]
+        # eager, reference-style host metadata every step
+        times = []
+        for it in range(steps + 3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            cur = [L + it for L in lens]
+            ctx_l = list(cur)
+            slot_l = [tables[b][(L - 1) // bs] * bs + (L - 1) % bs for b, L in enumerate(cur)]
+            nb = max((L + bs - 1) // bs for L in cur)
+            bt_l = [tables[b][:nb] for b in range(B)]
+            slot = torch.tensor(slot_l, dtype=torch.long, pin_memory=True).to(dev, non_blocking=True)
+            ctx = torch.tensor(ctx_l, dtype=torch.long, pin_memory=True).to(dev, non_blocking=True)
+            bt = torch.tensor(bt_l, dtype=torch.int32, pin_memory=True).to(dev, non_blocking=True)
+            layers_fn(B, slot, ctx, bt)
+            torch.cuda.synchronize()
+            if it >= 3:
+                times.append(time.perf_counter() - t0)
+        eager_us = statistics.median(times) * 1e6
+        # device metadata + captured graph
+        meta = DS.DecodeMetadata(max_rows, max_blocks, bs, N, dev)
+        graphs = DS.DecodeGraphs(meta, layers_fn, buckets=[B])
+        graphs.capture()
+        for b in range(B):
+            meta.set_row(b, tables[b], lens[b])
+        times = []
+        for it in range(steps + 3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            graphs.run(B)
+            torch.cuda.synchronize()
+            if it >= 3:
+                times.append(time.perf_counter() - t0)
+        graph_us = statistics.median(times) * 1e6
+        res[f"batch{B}"] = {"eager_host_metadata_us": round(eager_us, 1),
+                            "graph_device_metadata_us": round(graph_us, 1),
+                            "speedup": round(eager_us / graph_us, 2)}
+        del graphs, meta
+    return res
+
+
 def cpu_baseline(kcs, vcs, scale_kv, q, meta, n_seqs: int) -> dict:
     """The reference's PyTorch decode path on the host cores, on the first
     n_seqs sequences of the workload (one micro-batch of 16 at a time)."""
@@ -359,6 +443,7 @@ def main() -> int:
             extra[f"append_fp8_T{T}"] = {"us": round(ams * 1e3, 2), "GBps": round(ab / ams / 1e6, 1)}
             del kp, vp
         extra["prefill_chunked"] = prefill_extra(dev, stream)
+        extra["decode_step_latency"] = decode_step_latency(dev)
         copy = box_copy_gbps(dev, stream)
         extra["box_copy_GBps"] = round(copy, 1)
         extra["decode_frac_of_box_copy"] = round(gbps / copy, 4)

@@ -101,12 +101,22 @@ const char* mkv_status_string(int status);
  * scalar.  The divide is the IEEE-754 correctly rounded fp32 divide and NaN
  * inputs stay NaN, so the bytes equal torch's
  *   torch.clamp(x.float() / scale, -448, 448).to(torch.float8_e4m3fn).
- * Copy mode: the bytes are copied unchanged; k_scale/v_scale are ignored.
+ * With flags & MKV_APPEND_CALIBRATE_SENTINEL, a scale that holds the 1.0
+ * "not yet calibrated" sentinel is first calibrated from all num_tokens rows
+ * and written back, exactly as mkv_fp8_calibrate_per_tensor would, so one
+ * call has store_kvcache_fp8's calibrate-once semantics
+ * (attention.py:308-333).  That fallback re-reads the whole input in every
+ * wavefront: run mkv_fp8_calibrate_per_tensor before the first append of a
+ * tensor and use the flag for the later ones, where the sentinel normally
+ * no longer occurs.  Without the flag the scales are only read.
+ * Copy mode: the bytes are copied unchanged; k_scale/v_scale and flags are
+ * ignored.
  *
  * Rows must be 16-byte aligned (base pointers and row strides).
  * in_dtype in {F32, BF16, F16}; cache_dtype == in_dtype or FP8E4M3.
  * head_dim * num_kv_heads must be a multiple of 16.
  */
+#define MKV_APPEND_CALIBRATE_SENTINEL 1
 int mkv_kv_append(const void* key, int64_t key_row_stride,
                   const void* value, int64_t value_row_stride,
                   void* k_cache, void* v_cache,
@@ -114,7 +124,7 @@ int mkv_kv_append(const void* key, int64_t key_row_stride,
                   int num_kv_heads, int head_dim,
                   int block_size, int64_t num_blocks,
                   int in_dtype, int cache_dtype,
-                  const float* k_scale, const float* v_scale,
+                  float* k_scale, float* v_scale, int flags,
                   void* stream);
 
 /*
@@ -296,6 +306,31 @@ int mkv_gather_kv(void* dst, const void* cache, int dtype, int64_t num_blocks,
                   const void* context_lens, int context_lens_dtype,
                   int batch, int max_len, int num_kv_heads, int head_dim,
                   int block_size, void* stream);
+
+/*
+ * Decode-step metadata on the device.
+ *
+ * Replaces the per-step host loop of ModelRunner.prepare_decode
+ * (model_runner.py:621-640) and the graph-buffer copies of run_model
+ * (:695-701).  The caller keeps, per batch row b < rows, the sequence length
+ * seq_lens[b] (int64; <= 0 = inactive row) and its block table row
+ * block_tables[b, 0 .. max_blocks) resident on the device.  For each row:
+ *   active (seq_lens[b] > 0):  L = seq_lens[b] + increment;
+ *       seq_lens[b] = context_lens[b] = L;
+ *       slot_mapping[b] = block_tables[b, (L-1) / block_size] * block_size
+ *                         + (L-1) % block_size
+ *       (-1 if that entry is -1, outside the pool or past max_blocks);
+ *   inactive:  seq_lens[b] = context_lens[b] = 0, slot_mapping[b] = -1
+ *       (the append skips the row and the decode writes zeros: the padded
+ *       rows of a captured batch).
+ * With increment == 1 the call advances every active sequence by the token
+ * decoded this step (len(seq) in the reference); with 0 it only derives the
+ * metadata.  context_lens may alias seq_lens.  block_size a power of two.
+ */
+int mkv_decode_metadata(int64_t* seq_lens, int64_t* context_lens,
+                        int64_t* slot_mapping, const int32_t* block_tables,
+                        int64_t bt_stride, int max_blocks, int64_t num_blocks,
+                        int block_size, int rows, int increment, void* stream);
 
 #ifdef __cplusplus
 }

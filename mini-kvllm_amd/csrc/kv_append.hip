@@ -79,46 +79,6 @@ MKV_DEV u32x4 quantize16(const void* row, int64_t e, float scale) {
   return quantize16_fp8(x, scale);
 }
 
-template <int IN_DT, bool FP8>
-__global__ __launch_bounds__(kAppendWaves* kWave) void kv_append_kernel(
-    const void* __restrict__ key, int64_t key_stride,
-    const void* __restrict__ value, int64_t value_stride,
-    void* __restrict__ k_cache, void* __restrict__ v_cache,
-    const int64_t* __restrict__ slot_mapping, int64_t num_tokens,
-    int64_t row_elems, int64_t num_slots, const float* __restrict__ k_scale,
-    const float* __restrict__ v_scale) {
-  constexpr int kInBytes = DTypeInfo<IN_DT>::kBytes;
-  constexpr int kOutBytes = FP8 ? 1 : kInBytes;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t t = (int64_t)blockIdx.x * kAppendWaves + (threadIdx.x >> 6);
-  if (t >= num_tokens) return;
-  const int64_t slot = slot_mapping[t];
-  if (slot < 0 || slot >= num_slots) return;  // -1 = padding: skip
-
-  const char* krow = reinterpret_cast<const char*>(key) + t * key_stride * kInBytes;
-  const char* vrow = reinterpret_cast<const char*>(value) + t * value_stride * kInBytes;
-  char* kdst = reinterpret_cast<char*>(k_cache) + slot * row_elems * kOutBytes;
-  char* vdst = reinterpret_cast<char*>(v_cache) + slot * row_elems * kOutBytes;
-
-  if constexpr (FP8) {
-    const float ks = *k_scale;
-    const float vs = *v_scale;
-    for (int64_t e = (int64_t)lane * kElemsPerLane; e < row_elems; e += kWave * kElemsPerLane) {
-      st16(kdst + e, quantize16<IN_DT>(krow, e, ks));
-      st16(vdst + e, quantize16<IN_DT>(vrow, e, vs));
-    }
-  } else {
-    // Plain copy in 16-byte units.
-    const int64_t row_bytes = row_elems * kInBytes;
-    for (int64_t o = (int64_t)lane * 16; o < row_bytes; o += kWave * 16) {
-      const u32x4 kv = ld16(krow + o);
-      const u32x4 vv = ld16(vrow + o);
-      st16(kdst + o, kv);
-      st16(vdst + o, vv);
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Per-tensor calibration: amax over every row (slot -1 rows included), then
 // scale = round_in(max(amax, round_in(1e-8)) / 448) for each tensor whose
@@ -152,6 +112,89 @@ MKV_DEV uint32_t block_max_u32(uint32_t v, uint32_t* smem) {
     for (int i = 1; i < kCalThreads / kWave; ++i) v = max(v, smem[i]);
   }
   return v;
+}
+
+// The calibrated scale from the amax bit pattern (a NaN amax propagates).
+template <int IN_DT>
+MKV_DEV float calibrated_scale(uint32_t amax_bits) {
+  const float lo = round_to_dtype(1e-8f, IN_DT);
+  float a = __uint_as_float(amax_bits);
+  a = (a < lo) ? lo : a;  // clamp(min=1e-8); NaN propagates
+  return round_to_dtype(a / kFp8Max, IN_DT);
+}
+
+// A scale that still holds the 1.0 sentinel when the append runs: the wave
+// reads every row (slot -1 rows included) and derives the calibrated scale
+// itself, exactly as fp8_calibrate_kernel would, and writes it back.  Every
+// wave that sees the sentinel computes the same value, so a wave that reads
+// the scale after another one wrote it quantises identically.  Only reached
+// when calibration was not run first (the Python layer runs it on a scale
+// tensor's first use) or produced exactly 1.0; it is slow (every wave reads
+// the whole input) and meant to keep the reference's semantics in those
+// cases, not to be the calibration path.
+template <int IN_DT>
+MKV_DEV float calibrate_in_wave(const void* x, int64_t stride, int64_t num_tokens, int64_t row_elems,
+                                float* scale) {
+  constexpr int kInBytes = DTypeInfo<IN_DT>::kBytes;
+  const int lane = threadIdx.x & (kWave - 1);
+  uint32_t m = 0;
+  for (int64_t t = 0; t < num_tokens; ++t) {
+    const char* row = reinterpret_cast<const char*>(x) + t * stride * kInBytes;
+    for (int64_t e = (int64_t)lane * kElemsPerLane; e < row_elems; e += kWave * kElemsPerLane)
+      m = max(m, __float_as_uint(row_chunk_absmax<IN_DT>(row, e)));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off));
+  const float sc = calibrated_scale<IN_DT>(m);
+  if (lane == 0) *scale = sc;
+  return sc;
+}
+
+template <int IN_DT, bool FP8>
+__global__ __launch_bounds__(kAppendWaves* kWave) void kv_append_kernel(
+    const void* __restrict__ key, int64_t key_stride,
+    const void* __restrict__ value, int64_t value_stride,
+    void* __restrict__ k_cache, void* __restrict__ v_cache,
+    const int64_t* __restrict__ slot_mapping, int64_t num_tokens,
+    int64_t row_elems, int64_t num_slots, float* k_scale, float* v_scale, int calibrate) {
+  constexpr int kInBytes = DTypeInfo<IN_DT>::kBytes;
+  constexpr int kOutBytes = FP8 ? 1 : kInBytes;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t t = (int64_t)blockIdx.x * kAppendWaves + (threadIdx.x >> 6);
+  if (t >= num_tokens) return;
+  float ks = 0.0f, vs = 0.0f;
+  if constexpr (FP8) {
+    ks = *k_scale;
+    vs = *v_scale;
+    // before the slot test: a padding row still calibrates (all rows count)
+    if (calibrate && ks == 1.0f)
+      ks = calibrate_in_wave<IN_DT>(key, key_stride, num_tokens, row_elems, k_scale);
+    if (calibrate && vs == 1.0f)
+      vs = calibrate_in_wave<IN_DT>(value, value_stride, num_tokens, row_elems, v_scale);
+  }
+  const int64_t slot = slot_mapping[t];
+  if (slot < 0 || slot >= num_slots) return;  // -1 = padding: skip
+
+  const char* krow = reinterpret_cast<const char*>(key) + t * key_stride * kInBytes;
+  const char* vrow = reinterpret_cast<const char*>(value) + t * value_stride * kInBytes;
+  char* kdst = reinterpret_cast<char*>(k_cache) + slot * row_elems * kOutBytes;
+  char* vdst = reinterpret_cast<char*>(v_cache) + slot * row_elems * kOutBytes;
+
+  if constexpr (FP8) {
+    for (int64_t e = (int64_t)lane * kElemsPerLane; e < row_elems; e += kWave * kElemsPerLane) {
+      st16(kdst + e, quantize16<IN_DT>(krow, e, ks));
+      st16(vdst + e, quantize16<IN_DT>(vrow, e, vs));
+    }
+  } else {
+    // Plain copy in 16-byte units.
+    const int64_t row_bytes = row_elems * kInBytes;
+    for (int64_t o = (int64_t)lane * 16; o < row_bytes; o += kWave * 16) {
+      const u32x4 kv = ld16(krow + o);
+      const u32x4 vv = ld16(vrow + o);
+      st16(kdst + o, kv);
+      st16(vdst + o, vv);
+    }
+  }
 }
 
 template <int IN_DT>
@@ -309,7 +352,7 @@ extern "C" int mkv_kv_append(const void* key, int64_t key_row_stride, const void
                              int64_t value_row_stride, void* k_cache, void* v_cache,
                              const int64_t* slot_mapping, int64_t num_tokens, int num_kv_heads,
                              int head_dim, int block_size, int64_t num_blocks, int in_dtype,
-                             int cache_dtype, const float* k_scale, const float* v_scale,
+                             int cache_dtype, float* k_scale, float* v_scale, int flags,
                              void* stream) {
   if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks < 0)
     return MKV_ERR_BAD_SHAPE;
@@ -322,6 +365,8 @@ extern "C" int mkv_kv_append(const void* key, int64_t key_row_stride, const void
   const bool fp8 = (cache_dtype == MKV_DTYPE_FP8E4M3);
   if (!fp8 && cache_dtype != in_dtype) return MKV_ERR_UNSUPPORTED_DTYPE;
   if (fp8 && (!k_scale || !v_scale)) return MKV_ERR_NULL_POINTER;
+  if (flags & ~MKV_APPEND_CALIBRATE_SENTINEL) return MKV_ERR_BAD_SHAPE;
+  const int calibrate = (flags & MKV_APPEND_CALIBRATE_SENTINEL) ? 1 : 0;
   if (key_row_stride < row_elems || value_row_stride < row_elems) return MKV_ERR_BAD_STRIDE;
   const int in_bytes = (in_dtype == MKV_DTYPE_F32) ? 4 : 2;
   if (!aligned16(key) || !aligned16(value) || !aligned16(k_cache) || !aligned16(v_cache) ||
@@ -335,7 +380,7 @@ extern "C" int mkv_kv_append(const void* key, int64_t key_row_stride, const void
 #define MKV_APPEND_LAUNCH(IDT, F8)                                                            \
   hipLaunchKernelGGL((kv_append_kernel<IDT, F8>), grid, block, 0, s, key, key_row_stride,      \
                      value, value_row_stride, k_cache, v_cache, slot_mapping, num_tokens,      \
-                     row_elems, num_slots, k_scale, v_scale)
+                     row_elems, num_slots, k_scale, v_scale, calibrate)
   switch (in_dtype) {
     case MKV_DTYPE_F32:
       if (fp8) MKV_APPEND_LAUNCH(MKV_DTYPE_F32, true); else MKV_APPEND_LAUNCH(MKV_DTYPE_F32, false);

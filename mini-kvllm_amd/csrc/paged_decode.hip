@@ -1198,7 +1198,16 @@ constexpr auto stream_kernel() {
     return paged_decode_stream_kernel<KV_DT, kSmallGroup>;
 }
 
-// Merge of stream-K partials: one wave per (sequence, query head).
+// Merge of stream-K partials: one wave per (sequence, query head).  The
+// partials of an item come from the consecutive waves wlo..whi, one slot each.
+// Lane i reads (m, l) of contributor wlo + i, so the maximum and the
+// denominator are wave reductions rather than a chain of dependent loads, and
+// the accumulator rows are read four contributors at a time (independent
+// loads in flight) with each contributor's weight taken from its lane.
+MKV_DEV int merge_slot(const DecodeArgs& a, const StreamSplit& sp, int64_t gs, int wp, int h) {
+  return ((wp * 2 + (gs <= sp.begin(wp) ? 0 : 1)) * a.group + h);
+}
+
 __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_kernel(DecodeArgs a,
                                                                                      int kv_fp8) {
   const int lane = threadIdx.x & 63;
@@ -1217,19 +1226,47 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_ke
     const int64_t ge = gs + n;
     const int wlo = sp.wave_of(gs), whi = sp.wave_of(ge - 1);
     if (wlo == whi) return;  // written whole by the main kernel
+    const int nc = whi - wlo + 1;
     float M = kNegBig;
-    for (int wp = wlo; wp <= whi; ++wp) {
-      const int64_t slot = ((int64_t)wp * 2 + (gs <= sp.begin(wp) ? 0 : 1)) * a.group + h;
-      M = fmaxf(M, a.ws_ml[slot * 2]);
+    for (int c0 = 0; c0 < nc; c0 += kWave) {
+      if (c0 + lane < nc) M = fmaxf(M, a.ws_ml[(int64_t)merge_slot(a, sp, gs, wlo + c0 + lane, h) * 2]);
     }
-    for (int wp = wlo; wp <= whi; ++wp) {
-      const int64_t slot = ((int64_t)wp * 2 + (gs <= sp.begin(wp) ? 0 : 1)) * a.group + h;
-      const float wgt = __builtin_amdgcn_exp2f(a.ws_ml[slot * 2] - M);
-      l += wgt * a.ws_ml[slot * 2 + 1];
-      const f32x2 x = *reinterpret_cast<const f32x2*>(a.ws_acc + slot * kHeadDim + 2 * lane);
-      o0 += wgt * x[0];
-      o1 += wgt * x[1];
+    M = wave_max(M);
+    for (int c0 = 0; c0 < nc; c0 += kWave) {
+      int my_slot = 0;
+      float wgt = 0.0f;
+      if (c0 + lane < nc) {
+        my_slot = merge_slot(a, sp, gs, wlo + c0 + lane, h);
+        wgt = __builtin_amdgcn_exp2f(a.ws_ml[(int64_t)my_slot * 2] - M);
+        l += wgt * a.ws_ml[(int64_t)my_slot * 2 + 1];
+      }
+      const int cnt = nc - c0 < kWave ? nc - c0 : kWave;
+      int j = 0;
+      for (; j + 4 <= cnt; j += 4) {
+        f32x2 x[4];
+        float w4[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int64_t sl = __builtin_amdgcn_readlane(my_slot, j + u);
+          w4[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), j + u));
+          x[u] = *reinterpret_cast<const f32x2*>(a.ws_acc + sl * kHeadDim + 2 * lane);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          o0 += w4[u] * x[u][0];
+          o1 += w4[u] * x[u][1];
+        }
+      }
+      for (; j < cnt; ++j) {
+        const int64_t sl = __builtin_amdgcn_readlane(my_slot, j);
+        const float w1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), j));
+        const f32x2 x = *reinterpret_cast<const f32x2*>(a.ws_acc + sl * kHeadDim + 2 * lane);
+        o0 += w1 * x[0];
+        o1 += w1 * x[1];
+      }
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
   }
   const float inv = l > 0.0f ? (kv_fp8 ? load_uniform_f32(a.v_scale) : 1.0f) / l : 0.0f;
   if (a.q_dtype == MKV_DTYPE_F32) {

@@ -23,6 +23,7 @@ DTYPE_FP8E4M3 = 3
 DTYPE_I8 = 4
 SCALE_PER_TENSOR = 0
 SCALE_PER_TOKEN_HEAD = 1
+APPEND_CALIBRATE_SENTINEL = 1
 INDEX_I32 = 0
 INDEX_I64 = 1
 
@@ -32,7 +33,7 @@ SIGNATURES: dict[str, tuple] = {
     "mkv_status_string": (ctypes.c_char_p, [c_int]),
     "mkv_kv_append": (c_int, [
         c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64,
-        c_int, c_int, c_int, c_int64, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+        c_int, c_int, c_int, c_int64, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p]),
     "mkv_kv_append_per_token_head": (c_int, [
         c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
         c_int64, c_int, c_int, c_int, c_int64, c_int, c_int, c_void_p]),
@@ -55,6 +56,9 @@ SIGNATURES: dict[str, tuple] = {
     "mkv_flash_prefill": (c_int, [
         c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int, c_int64, c_int, c_int,
         c_int, c_float, c_void_p, c_size_t, c_void_p]),
+    "mkv_decode_metadata": (c_int, [
+        c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int64, c_int, c_int, c_int,
+        c_void_p]),
     "mkv_gather_kv": (c_int, [
         c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64, c_int, c_void_p, c_int, c_int,
         c_int, c_int, c_int, c_int, c_void_p]),

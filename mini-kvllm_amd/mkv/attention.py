@@ -131,7 +131,8 @@ def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor, num_kv_heads: int
 # ---------------------------------------------------------------------------
 # K1: append
 # ---------------------------------------------------------------------------
-def _append(key, value, k_cache, v_cache, slot_mapping, k_scale=None, v_scale=None):
+def _append(key, value, k_cache, v_cache, slot_mapping, k_scale=None, v_scale=None,
+            calibrate_sentinel=False):
     num_tokens, num_kv_heads, head_dim = key.shape
     dev = _require_gpu(key, value, k_cache, v_cache, slot_mapping)
     fp8 = k_cache.dtype == torch.float8_e4m3fn
@@ -148,7 +149,8 @@ def _append(key, value, k_cache, v_cache, slot_mapping, k_scale=None, v_scale=No
         k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr(), num_tokens, num_kv_heads,
         head_dim, k_cache.shape[1], k_cache.shape[0], _dtype_code(key, "key"),
         _dtype_code(k_cache, "k_cache"), k_scale.data_ptr() if fp8 else None,
-        v_scale.data_ptr() if fp8 else None, _stream(dev))
+        v_scale.data_ptr() if fp8 else None,
+        _lib.APPEND_CALIBRATE_SENTINEL if (fp8 and calibrate_sentinel) else 0, _stream(dev))
 
 
 def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
@@ -237,7 +239,11 @@ def store_kvcache_fp8(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Ten
     Reference: attention.py:281-333.
 
     'fp8_per_tensor': one scale per tensor, set by the reference's
-    calibrate-once rule evaluated on the device.  'fp8_per_token_head': one
+    calibrate-once rule evaluated on the device: the first call on a scale
+    tensor runs the calibration kernel; later calls pass the sentinel test to
+    the append kernel itself, which calibrates in the rare case that the
+    scale still holds 1.0, so the rule holds on every call with one launch
+    instead of two.  'fp8_per_token_head': one
     scale per (token, kv head), amax / 448 (1 for an all-zero head), written
     to k_scale/v_scale of shape (num_blocks, block_size, num_kv_heads)
     (attention.py:166-181).
@@ -251,8 +257,11 @@ def store_kvcache_fp8(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Ten
     if kv_cache_dtype == "fp8_per_token_head":
         _append_per_token_head(key, value, k_cache, v_cache, k_scale, v_scale, slot_mapping)
         return
-    calibrate_fp8_per_tensor(key, value, k_scale, v_scale)
-    _append(key, value, k_cache, v_cache, slot_mapping, k_scale, v_scale)
+    if not (getattr(k_scale, "_mkv_calibrated", False) and getattr(v_scale, "_mkv_calibrated", False)):
+        calibrate_fp8_per_tensor(key, value, k_scale, v_scale)
+        k_scale._mkv_calibrated = True
+        v_scale._mkv_calibrated = True
+    _append(key, value, k_cache, v_cache, slot_mapping, k_scale, v_scale, calibrate_sentinel=True)
 
 
 # ---------------------------------------------------------------------------

@@ -360,6 +360,43 @@ def paged_decode_tile_literal(query, k_cache, v_cache, k_scale, v_scale, block_t
 
 
 # ---------------------------------------------------------------------------
+# Decode-step metadata (the runner side of the decode path)
+# ---------------------------------------------------------------------------
+def decode_metadata_ref(block_tables: list, seq_lens: list, block_size: int):
+    """Decode metadata of one step for sequences with block tables
+    ``block_tables[i]`` (lists of block ids) and lengths ``seq_lens[i]`` =
+    len(seq) including the token being decoded: context_lens = len(seq), and
+    the slot of token len(seq) - 1 as prepare_mixed computes it for a decode
+    item (model_runner.py:530-553: start = num_tokens - 1,
+    slot = block_table[t // bs] * bs + t % bs).  A length <= 0 is an inactive
+    (padding) row: context 0, slot -1.
+
+    prepare_decode (model_runner.py:621-629) writes the same slot as
+    block_table[-1] * bs + last_block_num_tokens - 1, except when len(seq) is a
+    multiple of bs: last_block_num_tokens is then 0 (sequence.py:80-82) and
+    its slot, block_table[-1] * bs - 1, lies in another block."""
+    ctx, slots = [], []
+    for bt, L in zip(block_tables, seq_lens):
+        if L <= 0:
+            ctx.append(0)
+            slots.append(-1)
+            continue
+        t = L - 1
+        blk = t // block_size
+        ctx.append(L)
+        slots.append(bt[blk] * block_size + t % block_size if blk < len(bt) and bt[blk] >= 0 else -1)
+    return ctx, slots
+
+
+def prepare_decode_slot_literal(block_table: list, num_tokens: int, block_size: int) -> int:
+    """prepare_decode's slot formula, literally (model_runner.py:628 with
+    Sequence.last_block_num_tokens, sequence.py:80-82)."""
+    full_blocks = num_tokens // block_size
+    last_block_num_tokens = num_tokens - full_blocks * block_size
+    return block_table[-1] * block_size + last_block_num_tokens - 1
+
+
+# ---------------------------------------------------------------------------
 # a6: chunked prefill over the paged cache; a7: full prefill on fresh K/V
 # ---------------------------------------------------------------------------
 def paged_prefill_ref(query, k_cache, v_cache, block_tables, context_lens, cu_seqlens_q,

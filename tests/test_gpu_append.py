@@ -160,3 +160,46 @@ def test_calibration_sentinel_and_zero_input(dev):
     A.calibrate_fp8_per_tensor(z.to(dev), z.to(dev), ks, vs)
     assert float(ks) == R.calibrate_scale_ref(z) == 0.0
 
+
+
+@pytest.mark.parametrize("in_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_fp8_append_sentinel_fallback_calibrates_like_the_kernel(dev, in_dtype):
+    """The append's own sentinel path (used after a scale tensor's first
+    store_kvcache_fp8) gives the calibrate-once result: a scale reset to 1.0
+    on an already-used tensor is calibrated from all rows (slot -1 included)
+    and written back; a scale that is not 1.0 is left alone."""
+    announce(f"fp8 append sentinel fallback, {in_dtype}")
+    g = torch.Generator().manual_seed(71)
+    T, H, N, bs = 96, 8, 16, 16
+    key = (torch.randn(T, H, 128, generator=g) * 3).to(in_dtype)
+    value = (torch.randn(T, H, 128, generator=g) * 0.5).to(in_dtype)
+    key[5, 2, 9] = 40.0  # the amax sits in a padding row
+    slots = torch.randperm(N * bs, generator=g)[:T].to(torch.int64)
+    slots[5] = -1
+    kc = torch.zeros(N, bs, H, 128, dtype=FP8, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.ones(1, device=dev)
+    vs = torch.ones(1, device=dev)
+    kd, vd, sd = key.to(dev), value.to(dev), slots.to(dev)
+    A.store_kvcache_fp8(kd, vd, kc, vc, ks, vs, sd, bs, "fp8_per_tensor")  # calibrates
+    assert ks._mkv_calibrated
+    first = float(ks), float(vs)
+    # reset only k_scale: the next call goes straight to the append kernel
+    ks.fill_(1.0)
+    kc.zero_()
+    vc.zero_()
+    A.store_kvcache_fp8(kd, vd, kc, vc, ks, vs, sd, bs, "fp8_per_tensor")
+    kr = torch.zeros(N, bs, H, 128, dtype=FP8)
+    vr = torch.zeros_like(kr)
+    ksr, vsr = torch.ones(1), torch.tensor([first[1]])
+    R.store_kvcache_fp8_ref(key, value, kr, vr, ksr, vsr, slots)
+    assert float(ks) == float(ksr) == first[0]
+    assert float(vs) == first[1]
+    assert torch.equal(_u8(kc), kr.view(torch.uint8))
+    assert torch.equal(_u8(vc), vr.view(torch.uint8))
+    # every slot -1: nothing is written, but the sentinel is still calibrated
+    ks.fill_(1.0)
+    kc.zero_()
+    A.store_kvcache_fp8(kd, vd, kc, vc, ks, vs, torch.full_like(sd, -1), bs, "fp8_per_tensor")
+    assert float(ks) == first[0]
+    assert torch.count_nonzero(_u8(kc)) == 0

@@ -24,7 +24,7 @@ def _declared_functions() -> set[str]:
 def test_header_declares_expected_entry_points():
     names = _declared_functions()
     for n in ("mkv_kv_append", "mkv_kv_append_per_token_head", "mkv_fp8_calibrate_per_tensor",
-              "mkv_paged_decode",
+              "mkv_paged_decode", "mkv_decode_metadata",
               "mkv_paged_prefill", "mkv_flash_prefill", "mkv_gather_kv", "mkv_abi_version",
               "mkv_status_string"):
         assert n in names
@@ -52,7 +52,7 @@ def test_argument_validation_without_launch():
     nul = None
     # null pointers
     assert lib.mkv_kv_append(nul, 1024, nul, 1024, nul, nul, nul, 4, 8, 128, 16, 4, 1, 3,
-                             nul, nul, nul) == -1
+                             nul, nul, 0, nul) == -1
     # unsupported head_dim / group / block size in decode
     p = ctypes.c_void_p(16)
     base = [p, 4096, p, 4096, 1, p, p, 1, 10, nul, nul, 0, p, 4, 4, p, 1, 2]
@@ -64,7 +64,10 @@ def test_argument_validation_without_launch():
     assert lib.mkv_paged_decode(*base, 32, 8, 128, 256, 0.1, 32, p, 16, nul) == -7
     # zero tokens / batch is a no-op that succeeds
     assert lib.mkv_kv_append(nul, 1024, nul, 1024, nul, nul, nul, 0, 8, 128, 16, 4, 1, 3,
-                             nul, nul, nul) == 0
+                             nul, nul, 0, nul) == 0
+    # unknown append flags are rejected
+    assert lib.mkv_kv_append(p, 1024, p, 1024, p, p, p, 4, 8, 128, 16, 4, 1, 3, p, p, 6,
+                             nul) == -2
     # quantised caches: INT8 needs per-token-head scales, scales must be given,
     # and an unknown scale mode is rejected
     q8 = [p, 4096, p, 4096, 1, p, p]
@@ -80,6 +83,11 @@ def test_argument_validation_without_launch():
                                             1, 1, nul) == -3
     assert lib.mkv_kv_append_per_token_head(p, 1024, p, 1024, p, p, nul, p, p, 4, 8, 128, 16, 4,
                                             1, 4, nul) == -1
+    # decode metadata: nothing to do for zero rows; bad block size / pointers
+    assert lib.mkv_decode_metadata(nul, nul, nul, nul, 8, 8, 10, 16, 0, 1, nul) == 0
+    assert lib.mkv_decode_metadata(p, p, p, p, 8, 8, 10, 24, 4, 1, nul) == -6
+    assert lib.mkv_decode_metadata(p, nul, p, p, 8, 8, 10, 16, 4, 1, nul) == -1
+    assert lib.mkv_decode_metadata(p, p, p, p, 4, 8, 10, 16, 4, 1, nul) == -9
     # per-token-head scales are not accepted by the prefill kernel
     pre = [p, p, 1, p, p, 3, 10, p, p, 1, p, 4, 4, p, 1, p, p, 1, 4, 32, 8, 128, 256, 0.1,
            p, 1 << 20, nul]

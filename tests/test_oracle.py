@@ -490,3 +490,32 @@ def test_tile_literal_keeps_the_reference_hole_quirk():
     lit = R.paged_decode_tile_literal(q, kq, vq, ks, vs, bt, ctx, 0.3, 4, 2)
     assert torch.allclose(skip[1].double(), lit[1], atol=1e-6)
     assert not torch.allclose(skip[0].double(), lit[0], atol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# Decode-step metadata (model_runner.py:530-553, :621-640)
+# ---------------------------------------------------------------------------
+def test_decode_metadata_ref_matches_prepare_decode_except_at_block_ends():
+    g = torch.Generator().manual_seed(50)
+    bs = 16
+    perm = torch.randperm(200, generator=g).tolist()
+    for L in range(2, 120):
+        nb = (L + bs - 1) // bs
+        bt = perm[:nb]
+        ctx, slots = R.decode_metadata_ref([bt], [L], bs)
+        assert ctx == [L]
+        literal = R.prepare_decode_slot_literal(bt, L, bs)
+        if L % bs:
+            assert slots == [literal]
+        else:
+            # the reference's formula lands on the last slot of block bt[-1] - 1
+            assert literal == bt[-1] * bs - 1 and slots == [bt[-1] * bs + bs - 1]
+        # the slot is where the prefill path would have written token L - 1
+        assert slots[0] == bt[(L - 1) // bs] * bs + (L - 1) % bs
+
+
+def test_decode_metadata_ref_padding_and_absent_blocks():
+    ctx, slots = R.decode_metadata_ref([[3, 4], [7], [0, 0]], [20, 5, 0], 16)
+    assert ctx == [20, 5, 0] and slots == [4 * 16 + 3, 7 * 16 + 4, -1]
+    ctx, slots = R.decode_metadata_ref([[3, -1]], [20], 16)
+    assert slots == [-1]
