@@ -166,6 +166,71 @@ def prefill_extra(dev, stream) -> dict:
     return out
 
 
+def producer_extra(dev, stream) -> dict:
+    """The fused producer (q/k RMSNorm + rotary + FP8 per-tensor append) for
+    one layer, 16 q / 8 kv heads, head_dim 128, bf16 qkv, fp32 cos/sin table,
+    at 256 tokens (a decode batch) and 4096 tokens (a prefill chunk), against
+    the reference's sequence of operations on the same GPU: the q/k/v split,
+    LayerNorm.rms_forward on q and k, apply_rotary_pos_emb, the contiguous
+    copies of k and v (qwen3.py:85-118, attention.py:1664-1665) in eager torch,
+    then the FP8 append.  Bytes are algorithmic: qkv rows, positions, cos/sin
+    rows and slots read once, q and the FP8 K/V rows written once."""
+    import torch
+
+    from mkv import attention as A
+    from mkv import producer as P
+
+    Hq, Hkv, D, bs = 16, 8, HEAD_DIM, 256
+    res = {"workload": "one layer, 16 q / 8 kv heads, head_dim 128, bf16 qkv, FP8 per-tensor KV"}
+    g = torch.Generator().manual_seed(12)
+    cs = (torch.arange(4096, dtype=torch.float32)[:, None] *
+          (1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float32) / D)))[None, :])
+    cs = torch.cat([cs.cos(), cs.sin()], dim=-1).to(dev)
+    qw = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16).to(dev)
+    kw = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16).to(dev)
+    for T in (256, 4096):
+        qkv = torch.randn(T, (Hq + 2 * Hkv) * D, generator=g).to(torch.bfloat16).to(dev)
+        pos = torch.randint(0, 4096, (T,), generator=g).to(dev)
+        slots = torch.randperm(1024 * bs, generator=g)[:T].to(torch.int64).to(dev)
+        kc = torch.zeros(1024, bs, Hkv, D, dtype=torch.float8_e4m3fn, device=dev)
+        vc = torch.zeros_like(kc)
+        ks, vs = torch.ones(1, device=dev), torch.ones(1, device=dev)
+        fused = lambda i: P.qkv_norm_rope_append(qkv, pos, Hq, Hkv, D, cs, kc, vc, slots, bs,
+                                                 q_norm_weight=qw, k_norm_weight=kw,
+                                                 kv_cache_dtype="fp8_per_tensor", k_scale=ks,
+                                                 v_scale=vs)
+        fused(0)  # first use: calibrates the scales
+
+        def unfused(i):
+            q, k, v = qkv.split([Hq * D, Hkv * D, Hkv * D], dim=-1)
+            q, k, v = q.view(-1, Hq, D), k.view(-1, Hkv, D), v.view(-1, Hkv, D)
+
+            def rms(x, w):
+                var = x.pow(2).mean(dim=-1, keepdim=True) + 1e-5
+                return x / var.sqrt() * w
+
+            def rope(x, c, s_):
+                x1, x2 = x.chunk(2, dim=-1)
+                return torch.cat([x1 * c - x2 * s_, x1 * s_ + x2 * c], dim=-1)
+
+            q, k = rms(q, qw), rms(k, kw)
+            c, s_ = cs[pos].chunk(2, dim=-1)
+            c, s_ = c.unsqueeze(1), s_.unsqueeze(1)
+            q, k = rope(q, c, s_), rope(k, c, s_)
+            A.store_kvcache_fp8(k.contiguous(), v.contiguous(), kc, vc, ks, vs, slots, bs,
+                                "fp8_per_tensor")
+            return q
+
+        ms_f = time_launches(fused, 50, 5, stream)
+        ms_u = time_launches(unfused, 20, 3, stream)
+        nbytes = T * ((Hq + 2 * Hkv) * D * 2 + 8 + D * 4 + 8) + T * Hq * D * 2 + T * 2 * Hkv * D
+        res[f"T{T}"] = {"fused_us": round(ms_f * 1e3, 2), "fused_GBps": round(nbytes / ms_f / 1e6, 1),
+                        "reference_ops_us": round(ms_u * 1e3, 2), "speedup": round(ms_u / ms_f, 2),
+                        "algorithmic_bytes": nbytes}
+        del kc, vc
+    return res
+
+
 def decode_step_latency(dev, batches=(1, 8, 32), layers: int = 28, ctx0: int = 700,
                         steps: int = 30) -> dict:
     """Wall time of one decode step's attention work for a 28-layer stack
@@ -444,6 +509,7 @@ def main() -> int:
             del kp, vp
         extra["prefill_chunked"] = prefill_extra(dev, stream)
         extra["decode_step_latency"] = decode_step_latency(dev)
+        extra["producer_fused"] = producer_extra(dev, stream)
         copy = box_copy_gbps(dev, stream)
         extra["box_copy_GBps"] = round(copy, 1)
         extra["decode_frac_of_box_copy"] = round(gbps / copy, 4)

@@ -308,6 +308,56 @@ int mkv_gather_kv(void* dst, const void* cache, int dtype, int64_t num_blocks,
                   int block_size, void* stream);
 
 /*
+ * K6: fused producer — q/k RMSNorm + rotary embedding + KV append.
+ *
+ * Replaces, for one attention layer, the steps between the qkv projection
+ * and the attention kernels: the q/k/v split and q_norm / k_norm of
+ * Qwen3Attention.forward (qwen3.py:73-118; LayerNorm.rms_forward,
+ * layernorm.py:16-24), the rotary embedding (rotary_embedding.py:100-109,
+ * apply_rotary_pos_emb :4-26) and Attention.forward's contiguous copies and
+ * append (attention.py:1654-1691: store_kvcache / store_kvcache_fp8 /
+ * store_kvcache_int8).
+ *
+ * qkv: (num_tokens, qkv_row_stride) rows holding q (num_heads * head_dim),
+ * then k and v (num_kv_heads * head_dim each), in in_dtype.  For each token t
+ * and q / k head, with x the head's elements in fp32:
+ *   norm (if the weight pointer is non-null):
+ *     y = round_in(x / sqrt(sum(x^2) / head_dim + eps) * weight)
+ *   rotary at p = positions[t], c = cos_sin_cache[p, i], s =
+ *     cos_sin_cache[p, head_dim/2 + i] for i < head_dim/2 (NeoX halves):
+ *     out[i] = y[i]*c - y[i + D/2]*s,  out[i + D/2] = y[i]*s + y[i + D/2]*c
+ *   rounded to out_dtype (fp32 products and sums, no fused multiply-add).
+ * q_out (num_tokens, num_heads, head_dim) and, if non-null, k_out
+ * (num_tokens, num_kv_heads, head_dim) receive the rotated q / k in
+ * out_dtype.  The rotated k and the raw v of every token with slot =
+ * slot_mapping[t] in [0, num_blocks * block_size) are appended as
+ * mkv_kv_append (cache_dtype = a float type: cast on store; FP8E4M3 with
+ * kv_scale_mode PER_TENSOR, honouring flags as mkv_kv_append, where the
+ * 1.0-sentinel calibration uses this call's rotated k / raw v) or
+ * mkv_kv_append_per_token_head (FP8E4M3 or I8 with PER_TOKEN_HEAD) would
+ * append them.  slot_mapping NULL: nothing is appended (the caches and
+ * scales may be NULL then).  A position outside [0, max_position) gives NaN
+ * outputs.
+ *
+ * head_dim a power of two in 32..1024; in / out / cos_sin / weight dtypes
+ * F32, BF16 or F16; 16-byte aligned pointers and qkv row stride.
+ */
+int mkv_qkv_norm_rope_append(const void* qkv, int64_t qkv_row_stride,
+                             int in_dtype, int64_t num_tokens,
+                             int num_heads, int num_kv_heads, int head_dim,
+                             const void* q_norm_weight,
+                             const void* k_norm_weight,
+                             int norm_weight_dtype, float eps,
+                             const void* cos_sin_cache, int cos_sin_dtype,
+                             int64_t max_position, const int64_t* positions,
+                             void* q_out, void* k_out, int out_dtype,
+                             void* k_cache, void* v_cache, int cache_dtype,
+                             int kv_scale_mode, float* k_scale, float* v_scale,
+                             const int64_t* slot_mapping, int block_size,
+                             int64_t num_blocks, int flags, void* stream);
+
+/*
+ * Decode-step metadata on the device./*
  * Decode-step metadata on the device.
  *
  * Replaces the per-step host loop of ModelRunner.prepare_decode

@@ -50,27 +50,6 @@ MKV_DEV void load16_as_f32(const void* row, int64_t e, float (&x)[16]) {
   }
 }
 
-// 16 fp32 values -> 16 e4m3fn bytes: IEEE fp32 divide by the scale
-// (correctly rounded), torch.clamp to +-448 (NaN passes), RNE cast.  NaN
-// bytes keep the converter's S.1111.111 payload with the host's NaN sign.
-MKV_DEV u32x4 quantize16_fp8(const float (&x)[16], float scale) {
-  u32x4 out;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float v[4];
-    uint32_t nan_bits = 0, nan_signs = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float qv = x[4 * i + j] / scale;
-      nan_bits |= (qv != qv ? 0x80u : 0u) << (8 * j);
-      nan_signs |= div_nan_sign(x[4 * i + j], scale, qv) << (8 * j + 7);
-      v[j] = clamp_fp8_range(qv);
-    }
-    out[i] = (pack_fp8x4(v[0], v[1], v[2], v[3]) & ~nan_bits) | nan_signs;
-  }
-  return out;
-}
-
 // Quantise 16 consecutive elements of one row with a per-tensor scale.
 template <int IN_DT>
 MKV_DEV u32x4 quantize16(const void* row, int64_t e, float scale) {
@@ -274,24 +253,6 @@ MKV_DEV float head_amax(const void* row, int64_t e, int group, float (&x)[16]) {
   return m;
 }
 
-// INT8: y = x * (1 / scale), rounded half away from zero, clamped to
-// [-128, 127] with maxNum/minNum (a NaN becomes -128), truncated.
-MKV_DEV uint32_t quantize_i8(float xv, float inv) {
-  float y = xv * inv;
-  y = y >= 0.0f ? y + 0.5f : y - 0.5f;
-  y = fminf(fmaxf(y, -128.0f), 127.0f);
-  return (uint32_t)((int)y & 0xff);
-}
-
-MKV_DEV u32x4 quantize16_i8(const float (&x)[16], float inv) {
-  u32x4 out;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    out[i] = quantize_i8(x[4 * i], inv) | (quantize_i8(x[4 * i + 1], inv) << 8) |
-             (quantize_i8(x[4 * i + 2], inv) << 16) | (quantize_i8(x[4 * i + 3], inv) << 24);
-  return out;
-}
-
 template <int IN_DT, bool INT8>
 MKV_DEV void quantize_head_chunk(const char* row, char* dst, float* scales, int64_t e, int group,
                                  int head_dim, int lane) {
@@ -300,10 +261,10 @@ MKV_DEV void quantize_head_chunk(const char* row, char* dst, float* scales, int6
   u32x4 q;
   float scale;
   if constexpr (INT8) {
-    scale = fmaxf(amax / 127.0f, 1e-6f);
+    scale = i8_head_scale(amax);
     q = quantize16_i8(x, 1.0f / scale);
   } else {
-    scale = amax > 0.0f ? amax / kFp8Max : 1.0f;
+    scale = fp8_head_scale(amax);
     q = quantize16_fp8(x, scale);
   }
   st16(dst + e, q);

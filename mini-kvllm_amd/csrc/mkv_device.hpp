@@ -130,7 +130,55 @@ MKV_DEV uint32_t div_nan_sign(float x, float s, float q) {
   return 1u;
 }
 
-// Two e4m3fn bytes (low or high half-word of w) -> exact fp16 pair.
+// Four fp32 values -> four e4m3fn bytes with the per-tensor quantiser's
+// semantics: IEEE fp32 divide by the scale (correctly rounded), torch.clamp
+// to +-448 (NaN passes), round to nearest even.  NaN bytes keep the
+// converter's S.1111.111 payload with the sign of the host's NaN
+// (div_nan_sign), so the bytes equal torch's CPU cast.
+MKV_DEV uint32_t quantize4_fp8(const float* x, float scale) {
+  float v[4];
+  uint32_t nan_bits = 0, nan_signs = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float qv = x[j] / scale;
+    nan_bits |= (qv != qv ? 0x80u : 0u) << (8 * j);
+    nan_signs |= div_nan_sign(x[j], scale, qv) << (8 * j + 7);
+    v[j] = clamp_fp8_range(qv);
+  }
+  return (pack_fp8x4(v[0], v[1], v[2], v[3]) & ~nan_bits) | nan_signs;
+}
+
+MKV_DEV u32x4 quantize16_fp8(const float (&x)[16], float scale) {
+  return u32x4{quantize4_fp8(x, scale), quantize4_fp8(x + 4, scale), quantize4_fp8(x + 8, scale),
+               quantize4_fp8(x + 12, scale)};
+}
+
+// INT8 code of x for the per-token-head quantiser: y = x * inv (inv =
+// 1 / scale), rounded half away from zero, clamped to [-128, 127] with
+// maxNum / minNum (a NaN becomes -128), truncated.
+MKV_DEV uint32_t quantize_i8(float xv, float inv) {
+  float y = xv * inv;
+  y = y >= 0.0f ? y + 0.5f : y - 0.5f;
+  y = fminf(fmaxf(y, -128.0f), 127.0f);
+  return (uint32_t)((int)y & 0xff);
+}
+
+MKV_DEV uint32_t quantize4_i8(const float* x, float inv) {
+  return quantize_i8(x[0], inv) | (quantize_i8(x[1], inv) << 8) | (quantize_i8(x[2], inv) << 16) |
+         (quantize_i8(x[3], inv) << 24);
+}
+
+MKV_DEV u32x4 quantize16_i8(const float (&x)[16], float inv) {
+  return u32x4{quantize4_i8(x, inv), quantize4_i8(x + 4, inv), quantize4_i8(x + 8, inv),
+               quantize4_i8(x + 12, inv)};
+}
+
+// Per-token-head scales from a head's amax (NaN elements excluded):
+// FP8 amax / 448, or 1 for an all-zero head; INT8 max(amax / 127, 1e-6).
+MKV_DEV float fp8_head_scale(float amax) { return amax > 0.0f ? amax / kFp8Max : 1.0f; }
+MKV_DEV float i8_head_scale(float amax) { return fmaxf(amax / 127.0f, 1e-6f); }
+
+// Two e4m3fn bytes (low or high half-word of w) -> exact fp16 pair.// Two e4m3fn bytes (low or high half-word of w) -> exact fp16 pair.
 template <bool kHi>
 MKV_DEV f16x2 fp8x2_to_f16x2(uint32_t w) {
   return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, kHi);

@@ -56,6 +56,10 @@ SIGNATURES: dict[str, tuple] = {
     "mkv_flash_prefill": (c_int, [
         c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int, c_int64, c_int, c_int,
         c_int, c_float, c_void_p, c_size_t, c_void_p]),
+    "mkv_qkv_norm_rope_append": (c_int, [
+        c_void_p, c_int64, c_int, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_int, c_float,
+        c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int,
+        c_int, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int, c_void_p]),
     "mkv_decode_metadata": (c_int, [
         c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int64, c_int, c_int, c_int,
         c_void_p]),

@@ -118,7 +118,25 @@ def _ctx_lens(cl: torch.Tensor) -> torch.Tensor:
     return cl.contiguous()
 
 
+def _check_kv_rows(key: torch.Tensor, value: torch.Tensor) -> None:
+    if key.dim() != 3 or key.shape != value.shape:
+        raise ValueError("key and value must both be (num_tokens, num_kv_heads, head_dim); got "
+                         f"{tuple(key.shape)} and {tuple(value.shape)}")
+
+
+def _one_dtype(key: torch.Tensor, value: torch.Tensor):
+    """The C ABI reads key and value with one element dtype.  A pair whose
+    dtypes differ (e.g. a rotated k promoted to fp32 next to a bf16 v) is
+    widened to fp32, which is exact; the reference's kernels load both as
+    fp32 (attention.py:163-164, :225-226)."""
+    if key.dtype != value.dtype:
+        return key.float(), value.float()
+    return key, value
+
+
 def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor, num_kv_heads: int, head_dim: int):
+    if k_cache.dtype != v_cache.dtype:
+        raise TypeError(f"k_cache and v_cache must share a dtype; got {k_cache.dtype} and {v_cache.dtype}")
     if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
         raise ValueError("k_cache/v_cache must both be (num_blocks, block_size, num_kv_heads, "
                          f"head_dim); got {tuple(k_cache.shape)} and {tuple(v_cache.shape)}")
@@ -133,13 +151,23 @@ def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor, num_kv_heads: int
 # ---------------------------------------------------------------------------
 def _append(key, value, k_cache, v_cache, slot_mapping, k_scale=None, v_scale=None,
             calibrate_sentinel=False):
+    _check_kv_rows(key, value)
     num_tokens, num_kv_heads, head_dim = key.shape
     dev = _require_gpu(key, value, k_cache, v_cache, slot_mapping)
+    if k_cache.dtype != v_cache.dtype:
+        raise TypeError("k_cache and v_cache must share a dtype")
     fp8 = k_cache.dtype == torch.float8_e4m3fn
-    if not fp8 and key.dtype != k_cache.dtype:
+    if not fp8:
         # The reference's kernel casts on store; do the same cast on the GPU.
-        key = key.to(k_cache.dtype)
-        value = value.to(k_cache.dtype)
+        if key.dtype != k_cache.dtype:
+            key = key.to(k_cache.dtype)
+        if value.dtype != v_cache.dtype:
+            value = value.to(v_cache.dtype)
+    elif key.dtype != value.dtype:
+        key, value = _one_dtype(key, value)
+        # the in-kernel calibration would round both amax values in fp32; the
+        # callers calibrate such pairs per tensor beforehand
+        calibrate_sentinel = False
     key = _token_rows(key)
     value = _token_rows(value)
     slots = slot_mapping if slot_mapping.dtype == torch.int64 else slot_mapping.to(torch.int64)
@@ -182,9 +210,13 @@ def _check_token_scales(k_scale, v_scale, k_cache):
 
 
 def _append_per_token_head(key, value, k_cache, v_cache, k_scale, v_scale, slot_mapping):
+    _check_kv_rows(key, value)
     num_tokens, num_kv_heads, head_dim = key.shape
     dev = _require_gpu(key, value, k_cache, v_cache, k_scale, v_scale, slot_mapping)
     _check_token_scales(k_scale, v_scale, k_cache)
+    if k_cache.dtype != v_cache.dtype:
+        raise TypeError("k_cache and v_cache must share a dtype")
+    key, value = _one_dtype(key, value)
     key = _token_rows(key)
     value = _token_rows(value)
     slots = slot_mapping if slot_mapping.dtype == torch.int64 else slot_mapping.to(torch.int64)
@@ -220,16 +252,27 @@ def calibrate_fp8_per_tensor(key: torch.Tensor, value: torch.Tensor, k_scale: to
     dev = _require_gpu(key, value, k_scale, v_scale)
     if k_scale.dtype != torch.float32 or v_scale.dtype != torch.float32:
         raise TypeError("k_scale/v_scale must be float32 tensors")
+    _check_kv_rows(key, value)
     if key.shape[0] == 0:
         raise RuntimeError("amax of an empty key/value tensor is undefined")
+    if key.dtype != value.dtype:
+        # the rule rounds in each tensor's own dtype: one launch per tensor,
+        # the other scale pointing at a zero that is never the sentinel
+        zero = _workspace(dev, "fp8_calibrate_zero", 4, zeroed=True)
+        _calibrate_launch(dev, key, key, k_scale.data_ptr(), zero.data_ptr())
+        _calibrate_launch(dev, value, value, zero.data_ptr(), v_scale.data_ptr())
+        return
+    _calibrate_launch(dev, key, value, k_scale.data_ptr(), v_scale.data_ptr())
+
+
+def _calibrate_launch(dev, key, value, k_scale_ptr, v_scale_ptr) -> None:
     key = _token_rows(key)
     value = _token_rows(value)
     ws = _workspace(dev, "fp8_calibrate", _lib.query("mkv_fp8_calibrate_workspace_size"),
                     zeroed=True)
     _lib.call("mkv_fp8_calibrate_per_tensor", key.data_ptr(), key.stride(0), value.data_ptr(),
               value.stride(0), key.shape[0], key.shape[1] * key.shape[2],
-              _dtype_code(key, "key"), k_scale.data_ptr(), v_scale.data_ptr(), ws.data_ptr(),
-              _stream(dev))
+              _dtype_code(key, "key"), k_scale_ptr, v_scale_ptr, ws.data_ptr(), _stream(dev))
 
 
 def store_kvcache_fp8(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
@@ -257,10 +300,12 @@ def store_kvcache_fp8(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Ten
     if kv_cache_dtype == "fp8_per_token_head":
         _append_per_token_head(key, value, k_cache, v_cache, k_scale, v_scale, slot_mapping)
         return
-    if not (getattr(k_scale, "_mkv_calibrated", False) and getattr(v_scale, "_mkv_calibrated", False)):
+    mixed = key.dtype != value.dtype  # calibrated per tensor on every call (see _append)
+    if mixed or not (getattr(k_scale, "_mkv_calibrated", False) and getattr(v_scale, "_mkv_calibrated", False)):
         calibrate_fp8_per_tensor(key, value, k_scale, v_scale)
-        k_scale._mkv_calibrated = True
-        v_scale._mkv_calibrated = True
+        if not mixed:
+            k_scale._mkv_calibrated = True
+            v_scale._mkv_calibrated = True
     _append(key, value, k_cache, v_cache, slot_mapping, k_scale, v_scale, calibrate_sentinel=True)
 
 

@@ -360,6 +360,58 @@ def paged_decode_tile_literal(query, k_cache, v_cache, k_scale, v_scale, block_t
 
 
 # ---------------------------------------------------------------------------
+# Producer: q/k RMSNorm + rotary embedding (the values the append receives)
+# ---------------------------------------------------------------------------
+def rms_norm_ref(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """LayerNorm.rms_forward (layernorm.py:16-24): x / sqrt(mean(x^2) + eps)
+    * weight over the last dim, computed in fp32 and returned in x's dtype
+    (the reference's normed tensor has x's dtype)."""
+    xf = x.float()
+    var = xf.pow(2).mean(dim=-1, keepdim=True) + eps
+    return (xf / var.sqrt() * weight.float()).to(x.dtype)
+
+
+def rope_ref(x: torch.Tensor, positions: torch.Tensor, cos_sin_cache: torch.Tensor) -> torch.Tensor:
+    """apply_rotary_pos_emb (rotary_embedding.py:4-26) with cos, sin =
+    cos_sin_cache[positions].chunk(2, -1) (:100-109), NeoX halves, in fp32:
+    out1 = x1 * cos - x2 * sin, out2 = x1 * sin + x2 * cos.  x: (T, H, D)."""
+    cs = cos_sin_cache[positions].float()
+    cos, sin = cs.chunk(2, dim=-1)
+    cos, sin = cos[:, None, :], sin[:, None, :]
+    x1, x2 = x.float().chunk(2, dim=-1)
+    return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=-1)
+
+
+def qkv_norm_rope_ref(qkv, positions, num_heads, num_kv_heads, head_dim, cos_sin_cache,
+                      q_norm_weight=None, k_norm_weight=None, eps=1e-5, out_dtype=None):
+    """Qwen3Attention.forward up to the attention call (qwen3.py:85-118):
+    split the qkv rows into q, k, v, q_norm / k_norm if weights are given,
+    rotary embedding; q and k rounded to out_dtype (default qkv's dtype), v
+    the raw view.  Returns (q, k, v)."""
+    T = qkv.shape[0]
+    qs, ks = num_heads * head_dim, num_kv_heads * head_dim
+    q = qkv[:, :qs].reshape(T, num_heads, head_dim)
+    k = qkv[:, qs:qs + ks].reshape(T, num_kv_heads, head_dim)
+    v = qkv[:, qs + ks:qs + 2 * ks].reshape(T, num_kv_heads, head_dim)
+    if q_norm_weight is not None:
+        q = rms_norm_ref(q, q_norm_weight, eps)
+    if k_norm_weight is not None:
+        k = rms_norm_ref(k, k_norm_weight, eps)
+    out_dtype = out_dtype or qkv.dtype
+    return (rope_ref(q, positions, cos_sin_cache).to(out_dtype),
+            rope_ref(k, positions, cos_sin_cache).to(out_dtype), v)
+
+
+def rope_cos_sin_cache(base: float, head_dim: int, max_position: int) -> torch.Tensor:
+    """RotaryEmbedding's cos_sin_cache (rotary_embedding.py:37-90, no llama3
+    scaling): inv_freq = 1 / base^(2i/D), freqs = position x inv_freq,
+    [cos | sin], fp32."""
+    inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    freqs = torch.arange(max_position, dtype=torch.float32)[:, None] * inv_freq[None, :]
+    return torch.cat([freqs.cos(), freqs.sin()], dim=-1)
+
+
+# ---------------------------------------------------------------------------
 # Decode-step metadata (the runner side of the decode path)
 # ---------------------------------------------------------------------------
 def decode_metadata_ref(block_tables: list, seq_lens: list, block_size: int):

@@ -203,3 +203,48 @@ def test_fp8_append_sentinel_fallback_calibrates_like_the_kernel(dev, in_dtype):
     A.store_kvcache_fp8(kd, vd, kc, vc, ks, vs, torch.full_like(sd, -1), bs, "fp8_per_tensor")
     assert float(ks) == first[0]
     assert torch.count_nonzero(_u8(kc)) == 0
+
+
+@pytest.mark.parametrize("mode", ["fp8_per_tensor", "fp8_per_token_head", "copy"])
+def test_append_key_and_value_of_different_dtypes(dev, mode):
+    """Regression: an fp32 key (a rotated k promoted by an fp32 cos/sin table)
+    next to a bf16 value.  Both are widened to fp32 before the ABI call (it
+    reads both with one dtype); the per-tensor scales are calibrated each in
+    its own tensor's dtype, as the reference does."""
+    announce(f"append, fp32 key + bf16 value, {mode}")
+    g = torch.Generator().manual_seed(73)
+    T, H, N, bs = 80, 8, 12, 16
+    key = torch.randn(T, H, 128, generator=g) * 3
+    value = (torch.randn(T, H, 128, generator=g) * 0.7).to(torch.bfloat16)
+    slots = torch.randperm(N * bs, generator=g)[:T].to(torch.int64)
+    slots[::6] = -1
+    kd, vd, sd = key.to(dev), value.to(dev), slots.to(dev)
+    if mode == "copy":
+        kc = torch.zeros(N, bs, H, 128, dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        A.store_kvcache(kd, vd, kc, vc, sd, bs)
+        kr, vr = torch.zeros(N, bs, H, 128, dtype=torch.bfloat16), torch.zeros(N, bs, H, 128, dtype=torch.bfloat16)
+        R.store_kvcache_ref(key, value, kr, vr, slots)
+        assert torch.equal(kc.cpu().view(torch.int16), kr.view(torch.int16))
+        assert torch.equal(vc.cpu().view(torch.int16), vr.view(torch.int16))
+        return
+    kc = torch.zeros(N, bs, H, 128, dtype=FP8, device=dev)
+    vc = torch.zeros_like(kc)
+    if mode == "fp8_per_tensor":
+        ks, vs = torch.ones(1, device=dev), torch.ones(1, device=dev)
+        for _ in range(2):  # the second call takes the calibrated path
+            A.store_kvcache_fp8(kd, vd, kc, vc, ks, vs, sd, bs, mode)
+        kr, vr = torch.zeros(N, bs, H, 128, dtype=FP8), torch.zeros(N, bs, H, 128, dtype=FP8)
+        ksr, vsr = torch.ones(1), torch.ones(1)
+        R.store_kvcache_fp8_ref(key, value, kr, vr, ksr, vsr, slots)
+        assert float(ks) == float(ksr) and float(vs) == float(vsr)
+    else:
+        ks = torch.ones(N, bs, H, device=dev)
+        vs = torch.ones_like(ks)
+        A.store_kvcache_fp8(kd, vd, kc, vc, ks, vs, sd, bs, mode)
+        kr, vr = torch.zeros(N, bs, H, 128, dtype=FP8), torch.zeros(N, bs, H, 128, dtype=FP8)
+        ksr, vsr = torch.ones(N, bs, H), torch.ones(N, bs, H)
+        R.store_kvcache_quant_ref(key, value.float(), kr, vr, ksr, vsr, slots, mode)
+        assert torch.equal(ks.cpu(), ksr) and torch.equal(vs.cpu(), vsr)
+    assert torch.equal(_u8(kc), kr.view(torch.uint8))
+    assert torch.equal(_u8(vc), vr.view(torch.uint8))

@@ -24,7 +24,7 @@ def _declared_functions() -> set[str]:
 def test_header_declares_expected_entry_points():
     names = _declared_functions()
     for n in ("mkv_kv_append", "mkv_kv_append_per_token_head", "mkv_fp8_calibrate_per_tensor",
-              "mkv_paged_decode", "mkv_decode_metadata",
+              "mkv_paged_decode", "mkv_decode_metadata", "mkv_qkv_norm_rope_append",
               "mkv_paged_prefill", "mkv_flash_prefill", "mkv_gather_kv", "mkv_abi_version",
               "mkv_status_string"):
         assert n in names
@@ -88,6 +88,19 @@ def test_argument_validation_without_launch():
     assert lib.mkv_decode_metadata(p, p, p, p, 8, 8, 10, 24, 4, 1, nul) == -6
     assert lib.mkv_decode_metadata(p, nul, p, p, 8, 8, 10, 16, 4, 1, nul) == -1
     assert lib.mkv_decode_metadata(p, p, p, p, 4, 8, 10, 16, 4, 1, nul) == -9
+    # fused producer: head_dim must be a power of two >= 32; INT8 needs
+    # per-token-head scales; unknown flags are rejected
+    prod = [p, 4096, 1, 4, 16, 8, 128, nul, nul, 1, 1e-5, p, 0, 64, p, p, nul, 1, p, p, 3, 0, p, p,
+            p, 16, 8, 0, nul]
+    bad = list(prod)
+    bad[6] = 96
+    assert lib.mkv_qkv_norm_rope_append(*bad) == -4
+    bad = list(prod)
+    bad[20], bad[21] = 4, 0
+    assert lib.mkv_qkv_norm_rope_append(*bad) == -3
+    bad = list(prod)
+    bad[27] = 4
+    assert lib.mkv_qkv_norm_rope_append(*bad) == -2
     # per-token-head scales are not accepted by the prefill kernel
     pre = [p, p, 1, p, p, 3, 10, p, p, 1, p, 4, 4, p, 1, p, p, 1, 4, 32, 8, 128, 256, 0.1,
            p, 1 << 20, nul]
@@ -200,3 +213,61 @@ def test_context_provider_hook():
     finally:
         C.use_context_provider(None)
     assert C.current_context() is C.get_context()
+
+
+def test_key_and_value_reach_the_abi_in_one_dtype(monkeypatch):
+    """The C ABI reads key and value with one element dtype.  A rotated k
+    promoted to fp32 (an fp32 cos/sin table) next to a bf16 v once reached it
+    with the key's dtype, so the kernel read the v buffer at twice its size.
+    Every wrapper must now pass rows of one dtype (widened to fp32, exact),
+    cast both to the cache dtype in copy mode, and calibrate per tensor."""
+    seen, calls = [], []
+    real_rows = A._token_rows
+
+    def rows(x):
+        out = real_rows(x)
+        seen.append(out)
+        return out
+
+    monkeypatch.setattr(A, "_token_rows", rows)
+    monkeypatch.setattr(A, "_require_gpu", lambda *t: torch.device("cpu"))
+    monkeypatch.setattr(A, "_stream", lambda dev: 0)
+    monkeypatch.setattr(A, "_workspace", lambda dev, name, n, zeroed=False: torch.zeros(max(n, 256), dtype=torch.uint8))
+    monkeypatch.setattr(A._lib, "call", lambda name, *args: calls.append((name, args)))
+    monkeypatch.setattr(A._lib, "query", lambda name, *args: 16)
+    key = torch.randn(4, 8, 128)  # fp32
+    value = torch.randn(4, 8, 128).to(torch.bfloat16)
+    slots = torch.arange(4)
+
+    def last_pair():
+        k, v = seen[-2], seen[-1]
+        assert k.dtype == v.dtype and k.shape == v.shape
+        return k, v
+
+    # FP8 per tensor: widened to fp32, in-kernel calibration off for the pair
+    kc = torch.zeros(2, 16, 8, 128, dtype=torch.float8_e4m3fn)
+    A._append(key, value, kc, kc.clone(), slots, torch.ones(1), torch.ones(1), calibrate_sentinel=True)
+    k, v = last_pair()
+    assert k.dtype == torch.float32 and torch.equal(v, value.float())
+    name, args = calls[-1]
+    assert name == "mkv_kv_append" and args[12] == _lib.DTYPE_F32 and args[16] == 0
+    # copy mode: each cast to the cache dtype
+    kb = torch.zeros(2, 16, 8, 128, dtype=torch.bfloat16)
+    A._append(key, value, kb, kb.clone(), slots)
+    k, v = last_pair()
+    assert k.dtype == torch.bfloat16 and calls[-1][1][12] == _lib.DTYPE_BF16
+    # per-token-head
+    kq = torch.zeros(2, 16, 8, 128, dtype=torch.int8)
+    A._append_per_token_head(key, value, kq, kq.clone(), torch.ones(2, 16, 8), torch.ones(2, 16, 8), slots)
+    k, v = last_pair()
+    assert k.dtype == torch.float32 and calls[-1][1][14] == _lib.DTYPE_F32
+    # calibration: one launch per tensor, each in its own dtype
+    calls.clear()
+    A.calibrate_fp8_per_tensor(key, value, torch.ones(1), torch.ones(1))
+    assert [c[0] for c in calls] == ["mkv_fp8_calibrate_per_tensor"] * 2
+    assert calls[0][1][6] == _lib.DTYPE_F32 and calls[1][1][6] == _lib.DTYPE_BF16
+    # mismatched shapes or cache dtypes are refused before any launch
+    with pytest.raises(ValueError):
+        A._append(key, value[:3], kc, kc.clone(), slots, torch.ones(1), torch.ones(1))
+    with pytest.raises(TypeError):
+        A._append(key, value, kc, kb, slots, torch.ones(1), torch.ones(1))

@@ -519,3 +519,65 @@ def test_decode_metadata_ref_padding_and_absent_blocks():
     assert ctx == [20, 5, 0] and slots == [4 * 16 + 3, 7 * 16 + 4, -1]
     ctx, slots = R.decode_metadata_ref([[3, -1]], [20], 16)
     assert slots == [-1]
+
+
+# ---------------------------------------------------------------------------
+# Producer: RMSNorm + rotary embedding (layernorm.py:16-24,
+# rotary_embedding.py:4-26, :100-109)
+# ---------------------------------------------------------------------------
+def _angles_cache(theta: torch.Tensor) -> torch.Tensor:
+    """cos_sin rows for explicit angles (P, D/2) in float64."""
+    return torch.cat([theta.cos(), theta.sin()], dim=-1)
+
+
+def test_rope_ref_is_complex_rotation():
+    g = torch.Generator().manual_seed(80)
+    T, H, D = 9, 3, 16
+    x = torch.randn(T, H, D, generator=g, dtype=torch.float64)
+    theta = torch.rand(20, D // 2, generator=g, dtype=torch.float64) * 6.3
+    pos = torch.randint(0, 20, (T,), generator=g)
+    got = R.rope_ref(x, pos, _angles_cache(theta)).double()
+    z = torch.complex(x[..., :D // 2], x[..., D // 2:]) * torch.exp(1j * theta[pos])[:, None, :]
+    want = torch.cat([z.real, z.imag], dim=-1)
+    assert torch.allclose(got, want, atol=1e-5)
+    # position with zero angle is the identity; pair norms are preserved
+    zero = _angles_cache(torch.zeros(1, D // 2, dtype=torch.float64))
+    assert torch.allclose(R.rope_ref(x, torch.zeros(T, dtype=torch.int64), zero).double(), x, atol=1e-6)
+    n_in = x[..., :D // 2] ** 2 + x[..., D // 2:] ** 2
+    n_out = got[..., :D // 2] ** 2 + got[..., D // 2:] ** 2
+    assert torch.allclose(n_in, n_out, atol=1e-4)
+
+
+def test_rope_cache_composes_rotations():
+    cs = R.rope_cos_sin_cache(10000.0, 32, 64).double()
+    x = torch.randn(1, 2, 32, generator=torch.Generator().manual_seed(81), dtype=torch.float64)
+    a, b = 17, 23
+    ab = R.rope_ref(R.rope_ref(x, torch.tensor([a]), cs).double(), torch.tensor([b]), cs).double()
+    direct = R.rope_ref(x, torch.tensor([a + b]), cs).double()
+    assert torch.allclose(ab, direct, atol=2e-5)
+
+
+def test_rms_norm_ref_invariants():
+    g = torch.Generator().manual_seed(82)
+    x = torch.randn(5, 4, 64, generator=g) * 7
+    y = R.rms_norm_ref(x, torch.ones(64), 0.0).double()
+    assert torch.allclose(y.pow(2).mean(-1), torch.ones(5, 4, dtype=torch.float64), atol=1e-5)
+    w = torch.rand(64, generator=g) + 0.5
+    assert torch.allclose(R.rms_norm_ref(x, w, 0.0).double(), y * w.double(), atol=1e-5)
+    c = torch.full((1, 1, 64), -3.0)
+    assert torch.allclose(R.rms_norm_ref(c, w, 0.0), -w[None, None], atol=1e-6)
+    # the result has x's dtype, rounded once
+    xb = x.to(torch.bfloat16)
+    assert R.rms_norm_ref(xb, w, 1e-5).dtype == torch.bfloat16
+
+
+def test_qkv_norm_rope_ref_splits_columns():
+    g = torch.Generator().manual_seed(83)
+    Hq, Hkv, D, T = 4, 2, 16, 6
+    qkv = torch.randn(T, (Hq + 2 * Hkv) * D, generator=g)
+    cs = R.rope_cos_sin_cache(10000.0, D, 32)
+    pos = torch.arange(T)
+    q, k, v = R.qkv_norm_rope_ref(qkv, pos, Hq, Hkv, D, cs)
+    assert torch.equal(v, qkv[:, (Hq + Hkv) * D:].reshape(T, Hkv, D))
+    assert torch.allclose(q, R.rope_ref(qkv[:, :Hq * D].reshape(T, Hq, D), pos, cs))
+    assert torch.allclose(k, R.rope_ref(qkv[:, Hq * D:(Hq + Hkv) * D].reshape(T, Hkv, D), pos, cs))
