@@ -357,7 +357,6 @@ int mkv_qkv_norm_rope_append(const void* qkv, int64_t qkv_row_stride,
                              int64_t num_blocks, int flags, void* stream);
 
 /*
- * Decode-step metadata on the device./*
  * Decode-step metadata on the device.
  *
  * Replaces the per-step host loop of ModelRunner.prepare_decode

@@ -9,10 +9,10 @@
 // copies k and v to contiguous tensors and appends them
 // (attention.py:1654-1691: store_kvcache / store_kvcache_fp8 /
 // store_kvcache_int8).  That is six or more launches that each read and
-// write the rows again.  Here one wavefront per token row reads the row once
-// and writes q (normed, rotated), the row's K and V in the cache's format
-// (copy, FP8 per tensor, FP8 or INT8 per token and head) and, optionally, the
-// rotated k for a full-prefill attention over fresh K/V.
+// write the rows again.  Here the rows are read once and the kernel writes q
+// (normed, rotated), the rows' K and V in the cache's format (copy, FP8 per
+// tensor, FP8 or INT8 per token and head) and, optionally, the rotated k for
+// a full-prefill attention over fresh K/V.
 //
 // Lane layout: a head of D elements is D/16 lanes; lane m of a head holds
 // elements [8m, 8m+8) and [D/2 + 8m, D/2 + 8m + 8), i.e. 8 rotary pairs, so
@@ -241,74 +241,85 @@ MKV_DEV float producer_calibrate(const ProducerArgs& a, bool is_k, float* scale,
   return sc;
 }
 
+// Work item = (token row, group of heads): the q heads, the k heads and the
+// v heads of a row are cut into groups of 64 / (D/16) heads (8 at D = 128),
+// one wavefront each, so a row's groups run in parallel and every wave does
+// one round of loads, math and stores.
+MKV_DEV int head_groups(int heads, int hpi) { return (heads + hpi - 1) / hpi; }
+
 template <int IN_DT, int MODE>
 __global__ __launch_bounds__(kProdWaves* kWave) void qkv_producer_kernel(ProducerArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t t = (int64_t)blockIdx.x * kProdWaves + (threadIdx.x >> 6);
-  if (t >= a.num_tokens) return;
   const int lanes = a.head_dim / 16, hpi = kWave / lanes;
   const int m = lane % lanes, hi = lane / lanes;
   const int half = a.head_dim / 2;
+  const int gq = head_groups(a.num_heads, hpi), gk = head_groups(a.num_kv_heads, hpi);
+  const int groups = gq + 2 * gk;
+  const int64_t w = (int64_t)blockIdx.x * kProdWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t t = w / groups;
+  if (t >= a.num_tokens) return;
+  const int g = (int)(w - t * groups);
+  // region of this wave: 0 = q heads, 1 = k heads, 2 = v heads
+  const int region = g < gq ? 0 : (g < gq + gk ? 1 : 2);
+  const int h = (region == 0 ? g : (region == 1 ? g - gq : g - gq - gk)) * hpi + hi;
+  const int region_heads = region == 0 ? a.num_heads : a.num_kv_heads;
 
-  // norm weights of the lane's elements (the same for every head)
-  float wql[8], wqh[8], wkl[8], wkh[8];
-  if (a.q_w) {
-    const int eb = dtype_bytes(a.w_dtype);
-    load8_f32(reinterpret_cast<const char*>(a.q_w) + (8 * m) * eb, a.w_dtype, wql);
-    load8_f32(reinterpret_cast<const char*>(a.q_w) + (half + 8 * m) * eb, a.w_dtype, wqh);
-  }
-  if (a.k_w) {
-    const int eb = dtype_bytes(a.w_dtype);
-    load8_f32(reinterpret_cast<const char*>(a.k_w) + (8 * m) * eb, a.w_dtype, wkl);
-    load8_f32(reinterpret_cast<const char*>(a.k_w) + (half + 8 * m) * eb, a.w_dtype, wkh);
-  }
   float ks = 0.0f, vs = 0.0f;
-  if (MODE == kCacheFp8Tensor && a.slot_mapping) {
-    ks = *a.k_scale;
-    vs = *a.v_scale;
-    // before the slot test: padding rows count for the calibration
-    if (a.calibrate && ks == 1.0f) ks = producer_calibrate(a, true, a.k_scale, IN_DT, wkl, wkh);
-    if (a.calibrate && vs == 1.0f) vs = producer_calibrate(a, false, a.v_scale, IN_DT, wkl, wkh);
+  if (MODE == kCacheFp8Tensor && a.slot_mapping && region != 0) {
+    // the scale's 1.0 sentinel is handled before the slot test: padding rows
+    // count for the calibration
+    float wkl[8], wkh[8];
+    if (region == 1 && a.k_w) {
+      const int eb = dtype_bytes(a.w_dtype);
+      load8_f32(reinterpret_cast<const char*>(a.k_w) + (8 * m) * eb, a.w_dtype, wkl);
+      load8_f32(reinterpret_cast<const char*>(a.k_w) + (half + 8 * m) * eb, a.w_dtype, wkh);
+    }
+    if (region == 1) {
+      ks = *a.k_scale;
+      if (a.calibrate && ks == 1.0f) ks = producer_calibrate(a, true, a.k_scale, IN_DT, wkl, wkh);
+    } else {
+      vs = *a.v_scale;
+      if (a.calibrate && vs == 1.0f) vs = producer_calibrate(a, false, a.v_scale, IN_DT, wkl, wkh);
+    }
   }
-
+  if (h >= region_heads) return;  // the last group of a region may be partial
   const char* row = a.qkv + t * a.qkv_stride * DTypeInfo<IN_DT>::kBytes;
+  const int ob = dtype_bytes(a.out_dtype);
+  const int64_t slot = a.slot_mapping ? a.slot_mapping[t] : -1;
+  const bool append = slot >= 0 && slot < a.num_slots;
+
+  if (region == 2) {
+    if (!append) return;
+    float o1[8], o2[8];
+    load_v(a, row, h, m, IN_DT, o1, o2);
+    store_kv<MODE>(a, a.v_cache, a.v_scale, slot, h, m, o1, o2, vs);
+    return;
+  }
+  // q or k: norm weights of the lane's elements, cos / sin of the position
+  const void* wptr = region == 0 ? a.q_w : a.k_w;
+  float wl[8], wh[8];
+  if (wptr) {
+    const int eb = dtype_bytes(a.w_dtype);
+    load8_f32(reinterpret_cast<const char*>(wptr) + (8 * m) * eb, a.w_dtype, wl);
+    load8_f32(reinterpret_cast<const char*>(wptr) + (half + 8 * m) * eb, a.w_dtype, wh);
+  }
   float c[8], s[8];
   rotary_row(a, a.positions[t], m, c, s);
-  const int ob = dtype_bytes(a.out_dtype);
-
-  // q heads
-  for (int hb = 0; hb < a.num_heads; hb += hpi) {
-    const int h = hb + hi;
-    if (h >= a.num_heads) break;
-    float o1[8], o2[8];
-    produce_qk(a, row, (int64_t)h * a.head_dim, a.q_w, wql, wqh, c, s, m, IN_DT, o1, o2);
+  float o1[8], o2[8];
+  const int64_t head_off = (int64_t)(region == 0 ? h : a.num_heads + h) * a.head_dim;
+  produce_qk(a, row, head_off, wptr, wl, wh, c, s, m, IN_DT, o1, o2);
+  if (region == 0) {
     char* q = reinterpret_cast<char*>(a.q_out) + ((t * a.num_heads + h) * a.head_dim) * ob;
     store8(q + (8 * m) * ob, a.out_dtype, o1);
     store8(q + (half + 8 * m) * ob, a.out_dtype, o2);
+    return;
   }
-  const int64_t slot = a.slot_mapping ? a.slot_mapping[t] : -1;
-  const bool append = slot >= 0 && slot < a.num_slots;
-  // k heads: rotated, optionally written out, appended
-  for (int hb = 0; hb < a.num_kv_heads; hb += hpi) {
-    const int kvh = hb + hi;
-    if (kvh >= a.num_kv_heads) break;
-    float o1[8], o2[8];
-    produce_qk(a, row, (int64_t)(a.num_heads + kvh) * a.head_dim, a.k_w, wkl, wkh, c, s, m, IN_DT, o1, o2);
-    if (a.k_out) {
-      char* k = reinterpret_cast<char*>(a.k_out) + ((t * a.num_kv_heads + kvh) * a.head_dim) * ob;
-      store8(k + (8 * m) * ob, a.out_dtype, o1);
-      store8(k + (half + 8 * m) * ob, a.out_dtype, o2);
-    }
-    if (append) store_kv<MODE>(a, a.k_cache, a.k_scale, slot, kvh, m, o1, o2, ks);
+  if (a.k_out) {
+    char* k = reinterpret_cast<char*>(a.k_out) + ((t * a.num_kv_heads + h) * a.head_dim) * ob;
+    store8(k + (8 * m) * ob, a.out_dtype, o1);
+    store8(k + (half + 8 * m) * ob, a.out_dtype, o2);
   }
-  if (!append) return;
-  for (int hb = 0; hb < a.num_kv_heads; hb += hpi) {
-    const int kvh = hb + hi;
-    if (kvh >= a.num_kv_heads) break;
-    float o1[8], o2[8];
-    load_v(a, row, kvh, m, IN_DT, o1, o2);
-    store_kv<MODE>(a, a.v_cache, a.v_scale, slot, kvh, m, o1, o2, vs);
-  }
+  if (append) store_kv<MODE>(a, a.k_cache, a.k_scale, slot, h, m, o1, o2, ks);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -388,7 +399,9 @@ extern "C" int mkv_qkv_norm_rope_append(
   a.slot_mapping = slot_mapping;
   a.num_slots = num_blocks * (int64_t)block_size;
 
-  const dim3 grid((unsigned)((num_tokens + kProdWaves - 1) / kProdWaves));
+  const int hpi = kWave / (head_dim / 16);
+  const int64_t items = num_tokens * (int64_t)((num_heads + hpi - 1) / hpi + 2 * ((num_kv_heads + hpi - 1) / hpi));
+  const dim3 grid((unsigned)((items + kProdWaves - 1) / kProdWaves));
   const dim3 block(kProdWaves * kWave);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 #define MKV_PROD(IDT, MODE) hipLaunchKernelGGL((qkv_producer_kernel<IDT, MODE>), grid, block, 0, s, a)
