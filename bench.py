@@ -166,6 +166,62 @@ def prefill_extra(dev, stream) -> dict:
     return out
 
 
+def mixed_batch_extra(dev, stream) -> dict:
+    """Attention over the mixed-batch workload (8 prefill chunks of 512 rows
+    after priors U[0, 4096] and 120 decode rows with contexts U[256, 4096],
+    shuffled; 32 q / 8 kv heads, bf16 q), K/V already appended, two routes
+    of mkv.Attention: "split" (the reference's index_select -> decode kernel
+    + prefill kernel -> index_copy_, attention.py:1711-1760), "unified"
+    (one prefill launch over every row) and "overlap" (split, with the decode
+    rows on a second stream beside the prefill kernel)."""
+    import torch
+
+    from mkv import attention as A
+    from mkv import context as C
+    from mkv import workloads as W
+
+    m = W.prefill_mixed(seed=4)
+    T = int(m["cu_seqlens_q"][-1])
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(T, 32, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    split = C.split_mixed_decode_prefill_metadata(m["cu_seqlens_q"].tolist(), m["query_lens"],
+                                                   m["is_decode"])
+    split.decode_token_indices_tensor = torch.tensor(split.decode_token_indices, device=dev)
+    split.decode_seq_indices_tensor = torch.tensor(split.decode_seq_indices, device=dev)
+    split.prefill_token_indices_tensor = torch.tensor(split.prefill_token_indices, device=dev)
+    split.prefill_seq_indices_tensor = torch.tensor(split.prefill_seq_indices, device=dev)
+    split.prefill_cu_seqlens_q_tensor = torch.tensor(split.prefill_cu_seqlens_q, dtype=torch.int32,
+                                                     device=dev)
+    res = {"workload": f"{T} rows: 8 x 512-row prefill chunks + 120 decode rows, 32 q / 8 kv heads"}
+    for name, dt in (("bf16", torch.bfloat16), ("fp8", torch.float8_e4m3fn)):
+        kc = torch.empty(m["num_blocks"], m["block_size"], 8, HEAD_DIM, dtype=dt, device=dev)
+        vc = torch.empty_like(kc)
+        ks = W.fill_pool_on_device(kc, 500)
+        vs = W.fill_pool_on_device(vc, 501)
+        layer = A.Attention(32, HEAD_DIM, num_kv_heads=8, block_size=m["block_size"])
+        layer.k_cache, layer.v_cache = kc, vc
+        if name == "fp8":
+            layer.kv_cache_dtype = "fp8_per_tensor"
+            layer.k_scale = torch.tensor([ks], device=dev)
+            layer.v_scale = torch.tensor([vs], device=dev)
+        C.set_context(True, cu_seqlens_q=m["cu_seqlens_q"].to(dev), max_seqlen_q=512,
+                      slot_mapping=None, context_lens=m["context_lens"].to(dev),
+                      block_tables=m["block_tables"].to(dev), positions=m["positions"].to(dev),
+                      mixed_attention_split=split, is_full_prefill=False)
+        try:
+            row = {}
+            for route in ("split", "unified", "overlap"):
+                layer.mixed_batch = route
+                ms = time_launches(lambda i: layer(q, q, q, kv_appended=True), 20, 3, stream)
+                row[f"{route}_us"] = round(ms * 1e3, 1)
+            row["best_speedup_vs_split"] = round(row["split_us"] / min(row["unified_us"], row["overlap_us"]), 2)
+        finally:
+            C.reset_context()
+        res[f"{name}_kv"] = row
+        del kc, vc
+    return res
+
+
 def producer_extra(dev, stream) -> dict:
     """The fused producer (q/k RMSNorm + rotary + FP8 per-tensor append) for
     one layer, 16 q / 8 kv heads, head_dim 128, bf16 qkv, fp32 cos/sin table,
@@ -510,6 +566,7 @@ def main() -> int:
         extra["prefill_chunked"] = prefill_extra(dev, stream)
         extra["decode_step_latency"] = decode_step_latency(dev)
         extra["producer_fused"] = producer_extra(dev, stream)
+        extra["mixed_batch"] = mixed_batch_extra(dev, stream)
         copy = box_copy_gbps(dev, stream)
         extra["box_copy_GBps"] = round(copy, 1)
         extra["decode_frac_of_box_copy"] = round(gbps / copy, 4)

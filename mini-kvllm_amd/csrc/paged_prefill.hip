@@ -402,6 +402,14 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   }
 
   const int n_tiles = (max_vis + kBN - 1) / kBN;
+  // A wave whose rows see no key (padding rows: the workgroup of a short
+  // chunk, e.g. a decode row of a mixed batch, whose G rows sit in wave 0)
+  // still loads its share of every tile and meets every barrier, but skips
+  // the math.
+  bool wave_rows = false;
+#pragma unroll
+  for (int rt = 0; rt < kRowTiles; ++rt) wave_rows |= vis_c[rt] > 0;
+  const bool wave_active = __builtin_amdgcn_ballot_w64(wave_rows) != 0;
   if (n_tiles > 0) {
     load_tile(0);
     store_tile(0);
@@ -411,6 +419,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     const int buf = it & 1;
     const int kb = it * kBN;
     if (it + 1 < n_tiles) load_tile(kb + kBN);
+    if (wave_active) {
 
     // Key sub-tile validity (16 keys never straddle a block: bs >= 16).
     bool kvalid[4];
@@ -570,6 +579,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       }
       }
     }
+    }  // wave_active
 
     if (it + 1 < n_tiles) store_tile(buf ^ 1);
     __syncthreads();

@@ -75,6 +75,19 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+_side_streams: dict[int, torch.cuda.Stream] = {}
+
+
+def _side_stream(dev: torch.device) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for work that can run
+    beside the current stream's."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    st = _side_streams.get(idx)
+    if st is None:
+        st = _side_streams[idx] = torch.cuda.Stream(device=dev)
+    return st
+
+
 def _workspace(dev: torch.device, name: str, nbytes: int, zeroed: bool = False) -> torch.Tensor:
     """Per-device scratch tensor, grown on demand and then reused."""
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), name)
@@ -523,6 +536,14 @@ class Attention(nn.Module):
         self.kv_cache_dtype = "auto"
         self.k_scale = None
         self.v_scale = None
+        # Mixed decode + prefill batches: "unified" runs every row through the
+        # prefill kernel in one launch (a decode row is a chunk of one token:
+        # visible = min(context_len, position + 1) = context_len); "split" is
+        # the reference's route (attention.py:1711-1760): index_select the
+        # decode and prefill rows, two kernels, index_copy_ back; "overlap"
+        # is "split" with the decode rows on a second stream, concurrent with
+        # the prefill kernel.
+        self.mixed_batch = "overlap"
 
     def _mode(self) -> str:
         mode = self.kv_cache_dtype
@@ -551,10 +572,16 @@ class Attention(nn.Module):
             k_scale=self.k_scale if fp8 else None, v_scale=self.v_scale if fp8 else None,
             kv_cache_dtype=self.kv_cache_dtype)
 
-    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+                kv_appended: bool = False) -> torch.Tensor:
+        """The reference's forward (store, then attend).  kv_appended=True:
+        the step's K/V are already in the cache (mkv.producer's fused
+        norm + rotary + append), so the store is skipped; k and v are still
+        used by a full prefill."""
         context = current_context()
         mode = self._mode()
-        if self.k_cache.numel() > 0 and self.v_cache.numel() > 0 and context.slot_mapping is not None:
+        if (not kv_appended and self.k_cache.numel() > 0 and self.v_cache.numel() > 0
+                and context.slot_mapping is not None):
             if k.dim() == 4:
                 k = k.reshape(-1, k.shape[-2], k.shape[-1])
                 v = v.reshape(-1, v.shape[-2], v.shape[-1])
@@ -584,7 +611,8 @@ class Attention(nn.Module):
             if context.positions is None or context.context_lens is None or context.block_tables is None:
                 raise ValueError("paged prefill requires positions, context_lens, and block_tables")
             split = context.mixed_attention_split
-            if split is not None and split.decode_token_indices and split.prefill_token_indices:
+            if (self.mixed_batch in ("split", "overlap") and split is not None
+                    and split.decode_token_indices and split.prefill_token_indices):
                 if (split.decode_token_indices_tensor is None or split.decode_seq_indices_tensor is None
                         or split.prefill_token_indices_tensor is None
                         or split.prefill_seq_indices_tensor is None
@@ -593,15 +621,30 @@ class Attention(nn.Module):
                 o = torch.empty_like(q)
                 dti = split.decode_token_indices_tensor
                 dsi = split.decode_seq_indices_tensor
-                o.index_copy_(0, dti, self._decode(
-                    q.index_select(0, dti), context.block_tables.index_select(0, dsi),
-                    context.context_lens.index_select(0, dsi), scale))
                 pti = split.prefill_token_indices_tensor
                 psi = split.prefill_seq_indices_tensor
+
+                def decode_rows():
+                    o.index_copy_(0, dti, self._decode(
+                        q.index_select(0, dti), context.block_tables.index_select(0, dsi),
+                        context.context_lens.index_select(0, dsi), scale))
+
+                if self.mixed_batch == "overlap":
+                    # the memory-bound decode rows run on a second stream while
+                    # the MFMA-bound prefill rows run on this one
+                    main = torch.cuda.current_stream(q.device)
+                    side = _side_stream(q.device)
+                    side.wait_stream(main)
+                    with torch.cuda.stream(side):
+                        decode_rows()
+                else:
+                    decode_rows()
                 o.index_copy_(0, pti, self._prefill(
                     q.index_select(0, pti), context.block_tables.index_select(0, psi),
                     context.context_lens.index_select(0, psi), split.prefill_cu_seqlens_q_tensor,
                     context.positions.index_select(0, pti), scale))
+                if self.mixed_batch == "overlap":
+                    main.wait_stream(side)
                 return o.reshape(o.shape[0], self.num_heads * self.head_dim)
             o = self._prefill(q, context.block_tables, context.context_lens, cu_seqlens,
                               context.positions, scale)

@@ -184,10 +184,12 @@ def test_chunked_equals_one_shot_and_append_path(dev):
 
 
 @pytest.mark.parametrize("mode", ["auto", "fp8_per_tensor"])
-def test_attention_layer_mixed_batch(dev, mode):
-    """The Attention layer stores the step's K/V, then routes decode rows to
-    the decode kernel and prefill rows to the prefill kernel."""
-    announce(f"Attention layer mixed batch {mode}")
+@pytest.mark.parametrize("route", ["unified", "split", "overlap"])
+def test_attention_layer_mixed_batch(dev, mode, route):
+    """The Attention layer stores the step's K/V, then attends: all rows in
+    one prefill launch ("unified"), or decode rows to the decode kernel and
+    prefill rows to the prefill kernel ("split", the reference's route)."""
+    announce(f"Attention layer mixed batch {mode} {route}")
     g = torch.Generator().manual_seed(17)
     Hq, Hkv, bs, N = 8, 2, 16, 64
     prior = [40, 0, 99, 7]
@@ -208,6 +210,7 @@ def test_attention_layer_mixed_batch(dev, mode):
     hist_v = torch.randn(N, bs, Hkv, 128, generator=g).to(torch.bfloat16)
     layer = A.Attention(Hq, 128, scale=1.0, num_kv_heads=Hkv, block_size=bs)
     layer.kv_cache_dtype = mode
+    layer.mixed_batch = route
     fp8 = mode == "fp8_per_tensor"
     cdt = torch.float8_e4m3fn if fp8 else torch.bfloat16
     kcr = torch.zeros(N, bs, Hkv, 128, dtype=cdt)

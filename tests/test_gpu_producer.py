@@ -168,3 +168,49 @@ def test_producer_strided_rows_and_out_of_range_position(dev):
     # the normed values are rounded to the bf16 input dtype before the rotation
     _close_scaled(q[ok.to(dev)], qr, torch.bfloat16, "q")
     _close_scaled(k[ok.to(dev)], kr, torch.bfloat16, "k")
+
+
+def test_attention_layer_after_the_fused_producer(dev):
+    """Producer + Attention(kv_appended=True) equals the reference's order:
+    norm + rotary in torch-on-GPU, then Attention.forward storing and
+    attending (decode step, FP8 per-tensor cache)."""
+    announce("producer + Attention(kv_appended=True) decode step")
+    from mkv import context as C
+    g = torch.Generator().manual_seed(97)
+    B, Hq, Hkv, D, bs, N = 6, 16, 8, 128, 16, 48
+    ctx = torch.tensor([5, 17, 33, 48, 70, 100], dtype=torch.int64)
+    bt = torch.arange(N, dtype=torch.int32)[:42].view(B, 7)
+    slots = torch.tensor([int(bt[b, (int(ctx[b]) - 1) // bs]) * bs + (int(ctx[b]) - 1) % bs
+                          for b in range(B)], dtype=torch.int64)
+    qkv, pos, cs, qw, kw = _inputs(98, B, Hq, Hkv, D, torch.bfloat16, torch.bfloat16, True)
+    pos = ctx - 1
+    prior = torch.randn(N * bs, Hkv, D, generator=g).to(torch.bfloat16).to(dev)
+    outs = []
+    for fused in (True, False):
+        kc = torch.zeros(N, bs, Hkv, D, dtype=torch.float8_e4m3fn, device=dev)
+        vc = torch.zeros_like(kc)
+        ks, vs = torch.full((1,), 0.03, device=dev), torch.full((1,), 0.03, device=dev)
+        A._append(prior, prior, kc, vc, torch.arange(N * bs, device=dev), ks, vs)
+        layer = A.Attention(Hq, D, scale=1.0, num_kv_heads=Hkv, block_size=bs)
+        layer.k_cache, layer.v_cache, layer.k_scale, layer.v_scale = kc, vc, ks, vs
+        layer.kv_cache_dtype = "fp8_per_tensor"
+        C.set_context(False, slot_mapping=slots.to(dev), context_lens=ctx.to(dev), block_tables=bt.to(dev))
+        try:
+            if fused:
+                q, k, v = P.qkv_norm_rope_append(
+                    qkv.to(dev), pos.to(dev), Hq, Hkv, D, cs.to(dev), kc, vc, slots.to(dev), bs,
+                    q_norm_weight=qw.to(dev), k_norm_weight=kw.to(dev), kv_cache_dtype="fp8_per_tensor",
+                    k_scale=ks, v_scale=vs)
+                o = layer(q, k, v, kv_appended=True)
+            else:
+                q, k, v = P.qkv_norm_rope_append(
+                    qkv.to(dev), pos.to(dev), Hq, Hkv, D, cs.to(dev), None, None, None, bs,
+                    q_norm_weight=qw.to(dev), k_norm_weight=kw.to(dev), return_k=True)
+                o = layer(q, k, v.contiguous())
+        finally:
+            C.reset_context()
+        outs.append((o, kc.clone(), vc.clone()))
+    (o1, k1, v1), (o2, k2, v2) = outs
+    assert torch.equal(k1.view(torch.uint8), k2.view(torch.uint8))
+    assert torch.equal(v1.view(torch.uint8), v2.view(torch.uint8))
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
