@@ -158,7 +158,39 @@ MKV_DEV void store_out8(void* out, int dt, int64_t off, const float* x) {
 }
 
 // LDS geometry of one K or V tile: kBN key rows of kRowBytes, 16-byte chunks
-// XOR-swizzled by the key index.
+// XOR-swizzled by the key index.  A key row starts at a bank-cycle boundary
+// (128 or 256 bytes), so only the chunk position mod 8 picks the banks.  The
+// swizzle is a bijection on 8 aligned consecutive keys (the K operand reads:
+// 8 lanes, 8 keys, one chunk) and gives the transposed V reads of a 16-lane
+// group 8 distinct positions:
+//   16-bit: keys 4kg + i (i < 4) at chunks 2mm and 2mm + 1;
+//           s(key) = ((key & 3) << 1) | ((key >> 2) & 1);
+//   FP8:    keys 4kg + j and 16 + 4kg + j (j < 4) at one chunk;
+//           s(key) = ((key & 3) << 1) | (((key >> 2) ^ (key >> 4)) & 1).
+// The V read offsets are computed for the first keys and reused 16 (16-bit)
+// and 32 rows further, so s is invariant under those shifts.  Every LDS
+// access of the tile is then free of bank conflicts.
+// max(x, x of lane ^ 16) and max(x, x of lane ^ 32): VALU lane swaps
+// (v_permlane16_swap / v_permlane32_swap) that leave each lane the pair of
+// its own and its partner's value, with no LDS round trip or address
+// register.
+MKV_DEV float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+MKV_DEV float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// The lane index, computed where it is used: a volatile asm pair that the
+// compiler can neither hoist out of a loop nor keep in a register across it.
+MKV_DEV int lane_id_volatile() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 template <int KV_DT>
 struct LdsTile {
   static constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
@@ -166,16 +198,17 @@ struct LdsTile {
   static constexpr int kChunks = kRowBytes / 16;        // 16 or 8
   static constexpr int kBytes = kBN * kRowBytes;
   static constexpr int kChunksPerThread = kBN * kChunks / kPfThreads;  // 4 or 2
-  MKV_DEV static int offset(int key, int chunk) {
-    return key * kRowBytes + ((chunk ^ (key & (kChunks - 1))) << 4);
+  MKV_DEV static int swz(int key) {
+    return kEb == 2 ? ((key & 3) << 1) | ((key >> 2) & 1) : ((key & 3) << 1) | (((key >> 2) ^ (key >> 4)) & 1);
   }
+  MKV_DEV static int offset(int key, int chunk) { return key * kRowBytes + ((chunk ^ swz(key)) << 4); }
 };
 
 // Four waves per SIMD (two 8-wave workgroups per CU) hide the latency of each
 // wave's QK -> softmax -> PV chain, which leaves MFMA, VALU and LDS all far
 // from busy at two waves per SIMD; the compiler keeps the kernel within 128
-// registers (the bf16 variant spills a few of its registers, mostly outside
-// the tile loop).
+// registers, and the paged variants hold nothing in scratch inside the key
+// loop (a reload there waits for the tile prefetch as well).
 // QSPLIT (bf16 caches with an fp32 / fp16 q only): bf16 holds such a q to 8
 // bits, so q is split into bf16 hi + lo terms and each QK step takes a second
 // MFMA, giving ~16 significant bits like the fp32 reference.
@@ -286,6 +319,17 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       score_mul *= ldexpf(1.0f, e - 8);
     }
   }
+  // The loop keeps raw scores and needs score_mul > 0: a negative scale
+  // moves its sign into q (exact), a zero scale is q = 0 with scale 1 (every
+  // visible key weighs the same, as with 0 * score); NaN propagates.
+  if (!(score_mul > 0.0f) && score_mul == score_mul) {
+    const float f = score_mul < 0.0f ? -1.0f : 0.0f;
+#pragma unroll
+    for (int rt = 0; rt < kRowTiles; ++rt)
+#pragma unroll
+      for (int i = 0; i < 32; ++i) qf[rt][i] *= f;
+    score_mul = score_mul < 0.0f ? -score_mul : 1.0f;
+  }
   Op16<KV_DT> qop[kRowTiles][4];
   Op16<KV_DT> qlo[QSPLIT ? kRowTiles : 1][4];
 #pragma unroll
@@ -330,23 +374,43 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const int ld_key = (tid % kLanesPerSlot) / LT::kChunks;
   const int ld_ch = tid % LT::kChunks;
   const uint32_t ld_off = (uint32_t)(ld_key * row_stride + 16 * ld_ch);
-  int lds_off[kLoads];
   int ld_slot[kLoads];  // wave-uniform
 #pragma unroll
-  for (int u = 0; u < kLoads; ++u) {
+  for (int u = 0; u < kLoads; ++u)
     ld_slot[u] = __builtin_amdgcn_readfirstlane(u * kSlotsPerLoad + tid / kLanesPerSlot);
-    lds_off[u] = LT::offset(16 * (ld_slot[u] & 3) + ld_key, ld_ch);
-  }
+  // LDS offsets of the loads: one per-lane base plus a wave-uniform row
+  // shift.  Load u's sub-tile is (ld_slot[u] & 3) = (ld_slot[0] & 3) + 2u'
+  // (16-bit: shifts of 0 or 32 keys; FP8: 0), and the swizzle is invariant
+  // under a 32-key shift, so only one offset register lives through the loop.
+  static_assert(kSlotsPerLoad == 2 || kSlotsPerLoad == 4, "load slot layout");
+  const int lds_base = LT::offset(16 * (ld_slot[0] & 3) + ld_key, ld_ch);
+  auto lds_off = [&](int u) { return lds_base + ((ld_slot[u] & 3) - (ld_slot[0] & 3)) * 16 * LT::kRowBytes; };
 
-  // Descriptor of rows t0 .. t0+15 of one tensor (t0 a multiple of 16).
-  auto sub_rsrc = [&](const char* base, int64_t t0) -> __amdgpu_buffer_rsrc_t {
+  // Block-table entries of the four 16-key sub-tiles of the tile at kb: one
+  // table read when a tile lies inside one block (block_size >= kBN), shared
+  // by the K and V descriptors and the key-validity test of that tile.
+  auto tile_blocks = [&](int kb, int64_t (&ph)[4]) {
+    if constexpr (PAGED) {
+      if (a.idx.bs_log2 >= 6) {
+        const int64_t p = a.idx.physical_block(seq, (int64_t)kb >> a.idx.bs_log2);
+        ph[0] = ph[1] = ph[2] = ph[3] = p;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ph[j] = a.idx.physical_block(seq, (int64_t)(kb + 16 * j) >> a.idx.bs_log2);
+      }
+    } else {
+      ph[0] = ph[1] = ph[2] = ph[3] = 0;
+    }
+  };
+  // Descriptor of rows t0 .. t0+15 of one tensor (t0 a multiple of 16) whose
+  // block entry is phys.
+  auto sub_rsrc = [&](const char* base, int64_t t0, int64_t phys) -> __amdgpu_buffer_rsrc_t {
     const char* p = base;
     int num = 0;
     if constexpr (PAGED) {
-      const int64_t phys = a.idx.physical_block(seq, t0 >> a.idx.bs_log2);
       const int64_t bmask = ((int64_t)1 << a.idx.bs_log2) - 1;
       if (phys >= 0) {
-        p = base + (phys << a.idx.bs_log2) * row_stride + (t0 & bmask) * row_stride + head_bytes;
+        p = base + ((phys << a.idx.bs_log2) + (t0 & bmask)) * row_stride + head_bytes;
         num = (int)(15 * row_stride + kHeadDim * kEb);
       }
     } else {
@@ -356,13 +420,14 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, num, 0x00020000);
   };
   u32x4 stg[kLoads];
-  auto load_tile = [&](int kb) {
+  auto load_tile = [&](int kb, const int64_t (&ph)[4]) {
 #pragma unroll
     for (int u = 0; u < kLoads; ++u) {
       const int j = ld_slot[u] & 3;
       const bool is_v = ld_slot[u] >= 4;
       const int64_t t0 = kb + 16 * j;
-      const __amdgpu_buffer_rsrc_t r = sub_rsrc(is_v ? a.v : a.k, t0);
+      const int64_t phys = j == 0 ? ph[0] : (j == 1 ? ph[1] : (j == 2 ? ph[2] : ph[3]));
+      const __amdgpu_buffer_rsrc_t r = sub_rsrc(is_v ? a.v : a.k, t0, phys);
       const uint32_t off = (t0 + ld_key < max_vis) ? ld_off : 0x80000000u;
       stg[u] = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     }
@@ -372,7 +437,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     for (int u = 0; u < kLoads; ++u) {
       const bool is_v = ld_slot[u] >= 4;
       char* dst = is_v ? VBUF(buf) : KBUF(buf);
-      *reinterpret_cast<u32x4*>(dst + lds_off[u]) = stg[u];
+      *reinterpret_cast<u32x4*>(dst + lds_off(u)) = stg[u];
     }
   };
 
@@ -384,16 +449,23 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   // + c] for the lane group's MFMA k-slice, where the P operand holds keys
   // k(kg, j) = 32ks + 16*(j/4) + 4kg + j%4.  vt_off[mm]: that address in a V
   // tile for ks = 0 (and, 16-bit, the first half j < 4; +16 rows for j >= 4).
+  // 16-bit: the offsets follow from two per-lane values (computed where they
+  // are used, so they do not hold eight registers through the key loop):
+  // chunk (2mm + x) ^ s = ((mm ^ (s >> 1)) << 1) | (x ^ (s & 1)), hence
+  // offset(mm) = vt_base + ((mm << 5) ^ vt_swh).
   int vt_off[8];
+  int vt_base = 0, vt_swh = 0;
   {
     const int s16 = lane & 15;
+    if constexpr (kEb == 2) {
+      const int i = s16 >> 2, q = s16 & 3;
+      const int key = 4 * kg + i;
+      const int sw = LT::swz(key);
+      vt_base = key * LT::kRowBytes + ((((q >> 1) ^ sw) & 1) << 4) + 8 * (q & 1);
+      vt_swh = (sw >> 1) << 5;
+    } else {
 #pragma unroll
-    for (int mm = 0; mm < 8; ++mm) {
-      if constexpr (kEb == 2) {
-        const int i = s16 >> 2, q = s16 & 3;
-        const int key = 4 * kg + i;
-        vt_off[mm] = LT::offset(key, 2 * mm + (q >> 1)) + 8 * (q & 1);
-      } else {
+      for (int mm = 0; mm < 8; ++mm) {
         const int i = s16 >> 1, pp = s16 & 1;
         const int key = 16 * (i >> 2) + 4 * kg + (i & 3);
         vt_off[mm] = LT::offset(key, mm) + 8 * pp;
@@ -410,35 +482,39 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt) wave_rows |= vis_c[rt] > 0;
   const bool wave_active = __builtin_amdgcn_ballot_w64(wave_rows) != 0;
+  int64_t ph_cur[4], ph_nxt[4];
   if (n_tiles > 0) {
-    load_tile(0);
+    tile_blocks(0, ph_cur);
+    load_tile(0, ph_cur);
     store_tile(0);
   }
   __syncthreads();
   for (int it = 0; it < n_tiles; ++it) {
     const int buf = it & 1;
     const int kb = it * kBN;
-    if (it + 1 < n_tiles) load_tile(kb + kBN);
+    if (it + 1 < n_tiles) {
+      tile_blocks(kb + kBN, ph_nxt);
+      load_tile(kb + kBN, ph_nxt);
+    }
     if (wave_active) {
 
     // Key sub-tile validity (16 keys never straddle a block: bs >= 16).
     bool kvalid[4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      if constexpr (PAGED)
-        kvalid[kt] = a.idx.physical_block(seq, (int64_t)(kb + 16 * kt) >> a.idx.bs_log2) >= 0;
-      else
-        kvalid[kt] = true;
-    }
+    for (int kt = 0; kt < 4; ++kt) kvalid[kt] = ph_cur[kt] >= 0;
     const bool full = kb + kBN <= min_vis && kvalid[0] && kvalid[1] && kvalid[2] && kvalid[3];
 
     // ---- S^T = K Q^T ----
+    // 16-bit: the lane's key row, recomputed here: held across the loop it
+    // is the register the allocator spills first, and its reload would wait
+    // for the tile prefetch issued just above.
+    const int c_k = kEb == 2 ? lane_id_volatile() & 15 : c;
     f32x4 s[4][kRowTiles];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
       for (int rt = 0; rt < kRowTiles; ++rt) s[kt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int key = 16 * kt + c;
+      const int key = 16 * kt + c_k;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         Op16<KV_DT> kop;
@@ -462,26 +538,29 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     }
 
     // ---- online softmax (log2 domain), per row = lane column c ----
+    // The scores stay unscaled (score_mul > 0): the max of the scaled scores
+    // is the scaled max of the raw ones (rounding a product by a positive
+    // constant is monotonic), and each P takes one FMA.
     float p[4][kRowTiles][4];
     float alpha[kRowTiles];
 #pragma unroll
     for (int rt = 0; rt < kRowTiles; ++rt) {
-      float mx = kNegBig;
+      if (!full) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float x = s[kt][rt][r] * score_mul;
-          if (!full) {
+          for (int r = 0; r < 4; ++r) {
             const int t = kb + 16 * kt + 4 * kg + r;
-            x = (t < vis_c[rt] && kvalid[kt]) ? x : -__builtin_huge_valf();
+            if (!(t < vis_c[rt] && kvalid[kt])) s[kt][rt][r] = -__builtin_huge_valf();
           }
-          s[kt][rt][r] = x;
-          mx = fmaxf(mx, x);
-        }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      float mx = -__builtin_huge_valf();
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][rt][r]);
+      mx = max_xor32(max_xor16(mx));
+      mx = fmaxf(mx * score_mul, kNegBig);
       // Lazy rescale: the running max only moves when the tile's max exceeds
       // it by more than kRescaleSlack (log2 units), so P <= 2^kRescaleSlack,
       // exact and in range in bf16/fp16; the output rescale below then runs
@@ -494,7 +573,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          p[kt][rt][r] = __builtin_amdgcn_exp2f(s[kt][rt][r] - m_new);
+          p[kt][rt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][rt][r], score_mul, -m_new));
           psum += p[kt][rt][r];
         }
       l_run[rt] = l_run[rt] * alpha[rt] + psum;
@@ -526,10 +605,22 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
         }
         pop[rt] = to_op16<KV_DT>(pv);
         if constexpr (KV_DT == MKV_DTYPE_BF16) {
-          // second bf16 term carrying P's rounding residual (~16-bit P)
+          // second bf16 term carrying P's rounding residual (~16-bit P);
+          // p - hi is exact in fp32 and one dot2 forms it: hi_pair . (-1, 0)
+          // + p for the even element, . (0, -1) + p for the odd one.  The
+          // two constants are bit patterns held in scalar registers (an
+          // inline float constant is not a bf16 pair).
+          typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+          uint32_t nl_bits = 0x0000bf80u, nh_bits = 0xbf800000u;
+          asm volatile("" : "+s"(nl_bits), "+s"(nh_bits));
+          const bf16x2 neg_lo = __builtin_bit_cast(bf16x2, nl_bits), neg_hi = __builtin_bit_cast(bf16x2, nh_bits);
           float plo[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) plo[j] = pv[j] - (float)pop[rt][j];
+          for (int j = 0; j < 8; j += 2) {
+            const bf16x2 h = {pop[rt][j], pop[rt][j + 1]};
+            plo[j] = __builtin_amdgcn_fdot2_f32_bf16(h, neg_lo, pv[j], false);
+            plo[j + 1] = __builtin_amdgcn_fdot2_f32_bf16(h, neg_hi, pv[j + 1], false);
+          }
           plop[rt] = to_op16<KV_DT>(plo);
         }
       }
@@ -548,8 +639,9 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
         if constexpr (kEb == 2) {
           typedef short v4i16 __attribute__((ext_vector_type(4)));
           typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-          lds_v4i16* p0 = (lds_v4i16*)(vbuf + vt_off[mm] + 32 * ks * LT::kRowBytes);
-          lds_v4i16* p1 = (lds_v4i16*)(vbuf + vt_off[mm] + (32 * ks + 16) * LT::kRowBytes);
+          const int vo = vt_base + ((mm << 5) ^ vt_swh);
+          lds_v4i16* p0 = (lds_v4i16*)(vbuf + vo + 32 * ks * LT::kRowBytes);
+          lds_v4i16* p1 = (lds_v4i16*)(vbuf + vo + (32 * ks + 16) * LT::kRowBytes);
           const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p0);
           const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p1);
           const u32x4 w = {(uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16),
@@ -582,6 +674,8 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     }  // wave_active
 
     if (it + 1 < n_tiles) store_tile(buf ^ 1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ph_cur[j] = ph_nxt[j];
     __syncthreads();
   }
 

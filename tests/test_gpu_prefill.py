@@ -74,6 +74,21 @@ def test_prefill_small_groups(dev, dtype, group):
     assert_close_out(got, want, got.dtype, TOL[dtype])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("scale", [0.0, -0.09])
+def test_prefill_zero_and_negative_scale(dev, dtype, scale):
+    """The kernel keeps raw scores and scales them once: a zero scale (every
+    visible key weighs the same) and a negative one (the softmax of the
+    negated scores) must still match the oracle."""
+    announce(f"prefill {dtype} scale {scale}")
+    prior = [0, 40, 3]
+    qlen = [90, 24, 70]
+    q, k, v, bt, ctx, cu, pos, ks, vs = _make(7, prior, qlen, 8, 2, 16, dtype)
+    got = _gpu(dev, q, k, v, bt, ctx, cu, pos, scale, 8, 2, ks, vs)
+    want = R.paged_prefill_ref(q.double(), k, v, bt, ctx, cu, pos, scale, 8, 2, ks, vs)
+    assert_close_out(got, want, got.dtype, TOL[dtype])
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
 @pytest.mark.parametrize("bs", [16, 256])
 def test_prefill_block_sizes_holes_and_context_caps(dev, dtype, bs):
