@@ -57,38 +57,91 @@ struct PrefillArgs {
   int group;
   int tok_per_wg;
   float sm_scale;
-  int32_t* tile_start;  // [num_seqs + 1]
+  int32_t* tile_start;  // [num_seqs + 1], over the visiting order
+  const int32_t* order; // [num_seqs]: sequence visited at position k
   int64_t tiles_ub;     // upper bound of tiles per KV head (grid rows)
 };
 
 // ---------------------------------------------------------------------------
-// Tile list: tile_start[s] = sum_{s' < s} ceil(qlen_s' / tok_per_wg).
+// Tile list.  Sequences are visited longest first (by context length, paged;
+// by query length, contiguous), and each sequence's tiles from its last (the
+// rows that see the most keys) to its first: the grid then hands out the
+// workgroups roughly longest-processing-time first, which keeps the last
+// workgroups of a launch short.  order[k] = the sequence at position k,
+// tile_start[k] = sum_{k' < k} ceil(qlen(order[k']) / tok_per_wg).  Batches
+// of more than 256 sequences keep their own order.  The order changes which
+// workgroup computes a tile, never the tile's result.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void prefill_tile_scan_kernel(const int32_t* __restrict__ cu,
-                                                                int num_seqs, int tok_per_wg,
-                                                                int32_t* __restrict__ tile_start) {
+                                                                const void* context_lens, int ctx_i64,
+                                                                int64_t ctx_cap, int num_seqs,
+                                                                int tok_per_wg,
+                                                                int32_t* __restrict__ tile_start,
+                                                                int32_t* __restrict__ order) {
   __shared__ int32_t part[256];
+  __shared__ int64_t key[256];
+  __shared__ int32_t ord[256];
+  const int t = threadIdx.x;
+  auto tiles_of = [&](int s) {
+    const int32_t len = cu[s + 1] - cu[s];
+    return len > 0 ? (len + tok_per_wg - 1) / tok_per_wg : 0;
+  };
+  auto scan = [&](int32_t n) {  // Hillis-Steele inclusive scan of part[]
+    part[t] = n;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+      const int32_t add = t >= off ? part[t - off] : 0;
+      __syncthreads();
+      part[t] += add;
+      __syncthreads();
+    }
+  };
+  if (num_seqs <= 256) {
+    int64_t kk = -1;
+    if (t < num_seqs) {
+      if (cu[t + 1] > cu[t]) {
+        if (context_lens) {
+          const int64_t c = load_index(context_lens, t, ctx_i64);
+          kk = c < 0 ? 0 : (c > ctx_cap ? ctx_cap : c);
+        } else {
+          kk = cu[t + 1] - cu[t];
+        }
+      }
+      key[t] = kk;
+    }
+    __syncthreads();
+    if (t < num_seqs) {  // stable rank, longest first
+      int r = 0;
+      for (int j = 0; j < num_seqs; ++j) {
+        const int64_t kj = key[j];
+        r += (kj > kk) || (kj == kk && j < t);
+      }
+      ord[r] = t;
+    }
+    __syncthreads();
+    const int s = t < num_seqs ? ord[t] : 0;
+    const int32_t n = t < num_seqs ? tiles_of(s) : 0;
+    scan(n);
+    if (t < num_seqs) {
+      tile_start[t] = part[t] - n;
+      order[t] = s;
+    }
+    if (t == 0) tile_start[num_seqs] = part[255];
+    return;
+  }
   int32_t running = 0;
   for (int base = 0; base < num_seqs; base += 256) {
-    const int s = base + threadIdx.x;
-    int32_t n = 0;
+    const int s = base + t;
+    const int32_t n = s < num_seqs ? tiles_of(s) : 0;
+    scan(n);
     if (s < num_seqs) {
-      const int32_t len = cu[s + 1] - cu[s];
-      n = len > 0 ? (len + tok_per_wg - 1) / tok_per_wg : 0;
+      tile_start[s] = running + part[t] - n;
+      order[s] = s;
     }
-    part[threadIdx.x] = n;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {  // Hillis-Steele inclusive scan
-      const int32_t add = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
-      __syncthreads();
-      part[threadIdx.x] += add;
-      __syncthreads();
-    }
-    if (s < num_seqs) tile_start[s] = running + part[threadIdx.x] - n;
     running += part[255];
     __syncthreads();
   }
-  if (threadIdx.x == 0) tile_start[num_seqs] = running;
+  if (t == 0) tile_start[num_seqs] = running;
 }
 
 template <int KV_DT>
@@ -227,24 +280,30 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const int lane = tid & 63, wave = tid >> 6;
   const int c = lane & 15, kg = lane >> 4;
 
-  // XCD-aware order: consecutive logical tiles (same KV head) share an XCD.
+  // XCD-aware order: with a multiple of 8 KV heads every XCD takes whole
+  // heads (consecutive logical tiles share an XCD and its L2, and each XCD
+  // sees the same longest-first mix); otherwise the tiles are dealt round
+  // robin, so that the longest ones spread over all XCDs.
   const int64_t nwg = gridDim.x;
-  const int64_t per_xcd = nwg / kXcds;
-  const int64_t logical = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  const int64_t logical = a.num_kv_heads % kXcds == 0
+                              ? (int64_t)(blockIdx.x % kXcds) * (nwg / kXcds) + blockIdx.x / kXcds
+                              : (int64_t)blockIdx.x;
   const int kvh = (int)(logical / a.tiles_ub);
   const int64_t tau = logical - (int64_t)kvh * a.tiles_ub;
   if (kvh >= a.num_kv_heads) return;
   const int32_t total_tiles = a.tile_start[a.num_seqs];
   if (tau >= total_tiles) return;
-  int lo = 0, hi = a.num_seqs;  // largest s with tile_start[s] <= tau
+  int lo = 0, hi = a.num_seqs;  // largest k with tile_start[k] <= tau
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
     if (a.tile_start[mid] <= tau) lo = mid; else hi = mid;
   }
-  const int seq = lo;
+  const int seq = a.order[lo];
   const int64_t q_seq0 = a.cu_seqlens_q[seq];
   const int64_t q_seq1 = a.cu_seqlens_q[seq + 1];
-  const int64_t q0 = q_seq0 + (tau - a.tile_start[seq]) * (int64_t)a.tok_per_wg;
+  // the sequence's last tile first
+  const int64_t tile = (int64_t)(a.tile_start[lo + 1] - 1) - tau;
+  const int64_t q0 = q_seq0 + tile * (int64_t)a.tok_per_wg;
   const int64_t q1 = q0 + a.tok_per_wg < q_seq1 ? q0 + a.tok_per_wg : q_seq1;
   const int G = a.group;
 
@@ -735,7 +794,7 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   return (int)hipGetLastError();
 }
 
-size_t prefill_ws_bytes(int num_seqs) { return ((size_t)(num_seqs + 1) * sizeof(int32_t) + 255) / 256 * 256; }
+size_t prefill_ws_bytes(int num_seqs) { return ((size_t)(2 * num_seqs + 1) * sizeof(int32_t) + 255) / 256 * 256; }
 
 }  // namespace
 }  // namespace mkv
@@ -776,10 +835,14 @@ int dispatch_prefill(PrefillArgs& a, int kv_dtype, void* workspace, size_t works
                      hipStream_t s) {
   if (workspace_bytes < prefill_ws_bytes(a.num_seqs) || !workspace) return MKV_ERR_WORKSPACE_TOO_SMALL;
   a.tile_start = reinterpret_cast<int32_t*>(workspace);
+  int32_t* order = a.tile_start + a.num_seqs + 1;
+  a.order = order;
   a.tok_per_wg = tok_per_wg_for(a.group);
   a.tiles_ub = tiles_upper_bound(a.num_seqs, a.total_q, a.group);
-  hipLaunchKernelGGL(prefill_tile_scan_kernel, dim3(1), dim3(256), 0, s, a.cu_seqlens_q, a.num_seqs,
-                     a.tok_per_wg, a.tile_start);
+  const int64_t ctx_cap = PAGED ? ((int64_t)a.idx.max_blocks << a.idx.bs_log2) : 0;
+  hipLaunchKernelGGL(prefill_tile_scan_kernel, dim3(1), dim3(256), 0, s, a.cu_seqlens_q,
+                     PAGED ? a.context_lens : nullptr, a.ctx_i64, ctx_cap, a.num_seqs, a.tok_per_wg,
+                     a.tile_start, order);
   switch (kv_dtype) {
     case MKV_DTYPE_FP8E4M3: return launch_prefill<MKV_DTYPE_FP8E4M3, PAGED, false>(a, s);
     case MKV_DTYPE_BF16:

@@ -89,6 +89,23 @@ def test_prefill_zero_and_negative_scale(dev, dtype, scale):
     assert_close_out(got, want, got.dtype, TOL[dtype])
 
 
+@pytest.mark.parametrize("nseq,Hkv", [(40, 2), (40, 8), (300, 2)])
+def test_prefill_visit_order_many_tied_and_empty_sequences(dev, nseq, Hkv):
+    """The tile list visits sequences longest first (ranked on the device for
+    up to 256 sequences, in batch order beyond) and each sequence's tiles last
+    first; ties, empty sequences and both grid mappings (KV heads a multiple
+    of 8 or not) must leave every row's result unchanged."""
+    announce(f"prefill visit order: {nseq} sequences, {Hkv} kv heads")
+    g = torch.Generator().manual_seed(500 + nseq + Hkv)
+    prior = [int(x) for x in torch.tensor([0, 16, 50, 97])[torch.randint(0, 4, (nseq,), generator=g)]]
+    qlen = [int(x) for x in torch.randint(0, 7, (nseq,), generator=g)]
+    qlen[3] = 70  # one sequence of several tiles
+    q, k, v, bt, ctx, cu, pos, ks, vs = _make(nseq, prior, qlen, 2 * Hkv, Hkv, 16, torch.bfloat16)
+    got = _gpu(dev, q, k, v, bt, ctx, cu, pos, 0.09, 2 * Hkv, Hkv, ks, vs)
+    want = R.paged_prefill_ref(q.double(), k, v, bt, ctx, cu, pos, 0.09, 2 * Hkv, Hkv, ks, vs)
+    assert_close_out(got, want, got.dtype, TOL[torch.bfloat16])
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
 @pytest.mark.parametrize("bs", [16, 256])
 def test_prefill_block_sizes_holes_and_context_caps(dev, dtype, bs):
