@@ -210,19 +210,6 @@ MKV_DEV void store_out8(void* out, int dt, int64_t off, const float* x) {
   }
 }
 
-// LDS geometry of one K or V tile: kBN key rows of kRowBytes, 16-byte chunks
-// XOR-swizzled by the key index.  A key row starts at a bank-cycle boundary
-// (128 or 256 bytes), so only the chunk position mod 8 picks the banks.  The
-// swizzle is a bijection on 8 aligned consecutive keys (the K operand reads:
-// 8 lanes, 8 keys, one chunk) and gives the transposed V reads of a 16-lane
-// group 8 distinct positions:
-//   16-bit: keys 4kg + i (i < 4) at chunks 2mm and 2mm + 1;
-//           s(key) = ((key & 3) << 1) | ((key >> 2) & 1);
-//   FP8:    keys 4kg + j and 16 + 4kg + j (j < 4) at one chunk;
-//           s(key) = ((key & 3) << 1) | (((key >> 2) ^ (key >> 4)) & 1).
-// The V read offsets are computed for the first keys and reused 16 (16-bit)
-// and 32 rows further, so s is invariant under those shifts.  Every LDS
-// access of the tile is then free of bank conflicts.
 // max(x, x of lane ^ 16) and max(x, x of lane ^ 32): VALU lane swaps
 // (v_permlane16_swap / v_permlane32_swap) that leave each lane the pair of
 // its own and its partner's value, with no LDS round trip or address
@@ -244,6 +231,24 @@ MKV_DEV int lane_id_volatile() {
   return l;
 }
 
+// LDS geometry of one K or V tile: kBN key rows of kRowBytes, 16-byte chunks
+// XOR-swizzled by the key index.  The LDS serves 256 bytes per clock from 64
+// four-byte banks: 16 lanes of a 16-byte access, or 32 lanes of an 8-byte
+// one, go together, and they are conflict-free when they touch 16 distinct
+// 16-byte positions modulo 256 bytes.  A key row starts at a 128- or 256-byte
+// boundary, so that position is the chunk (and, FP8, the key's parity).
+//   16-bit: s(key) = ((key & 7) << 1) | ((key >> 3) & 1) (4 bits), a
+//     bijection on key mod 16 (K operand reads: 16 lanes, keys 16kt + c, one
+//     chunk), whose upper 3 bits are a bijection on 8 consecutive keys (V
+//     transposed reads: 32 lanes, keys 4kg + i, chunk pairs 2mm, 2mm + 1).
+//   FP8: s(key) = ((key >> 1) & 3) | ((((key >> 3) ^ (key >> 4)) & 1) << 2),
+//     a bijection on the same-parity keys among 16 consecutive ones (K
+//     reads) and among keys 4kg + j, 16 + 4kg + j for two lane groups (V
+//     reads).
+// Staging writes put 16 chunks of one 16-bit key (two FP8 keys) in one go,
+// distinct under any s.  The V read offsets are computed for the first keys
+// and reused 16 (16-bit) and 32 rows further, and the staging offsets 16-48
+// (16-bit) or 32 (FP8) rows further: s is invariant under those shifts.
 template <int KV_DT>
 struct LdsTile {
   static constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
@@ -252,7 +257,8 @@ struct LdsTile {
   static constexpr int kBytes = kBN * kRowBytes;
   static constexpr int kChunksPerThread = kBN * kChunks / kPfThreads;  // 4 or 2
   MKV_DEV static int swz(int key) {
-    return kEb == 2 ? ((key & 3) << 1) | ((key >> 2) & 1) : ((key & 3) << 1) | (((key >> 2) ^ (key >> 4)) & 1);
+    return kEb == 2 ? ((key & 7) << 1) | ((key >> 3) & 1)
+                    : ((key >> 1) & 3) | ((((key >> 3) ^ (key >> 4)) & 1) << 2);
   }
   MKV_DEV static int offset(int key, int chunk) { return key * kRowBytes + ((chunk ^ swz(key)) << 4); }
 };
@@ -564,6 +570,11 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     const bool full = kb + kBN <= min_vis && kvalid[0] && kvalid[1] && kvalid[2] && kvalid[3];
 
     // ---- S^T = K Q^T ----
+    // The MFMA blocks run at raised wave priority: a SIMD's waves reach the
+    // same phase together (one barrier per tile), and issuing the MFMAs of
+    // whichever waves have them first keeps the matrix pipe fed while the
+    // other waves' softmax fills the gaps.
+    __builtin_amdgcn_s_setprio(1);
     // 16-bit: the lane's key row, recomputed here: held across the loop it
     // is the register the allocator spills first, and its reload would wait
     // for the tile prefetch issued just above.
@@ -596,6 +607,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       }
     }
 
+    __builtin_amdgcn_s_setprio(0);
     // ---- online softmax (log2 domain), per row = lane column c ----
     // The scores stay unscaled (score_mul > 0): the max of the scaled scores
     // is the scaled max of the raw ones (rounding a product by a positive
@@ -647,6 +659,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     }
 
     // ---- O += P V, 32 keys per MFMA k-step ----
+    __builtin_amdgcn_s_setprio(1);
     // B operand of output-dim tile mm (dims 16mm .. 16mm+15, lane c -> dim
     // 16mm + c): the lane group's 8 keys of its k-slice, read transposed
     // straight from LDS (ds_read_b64_tr_b16 / _tr_b8), see vt_off below.
@@ -730,6 +743,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     }  // wave_active
 
     if (it + 1 < n_tiles) store_tile(buf ^ 1);
