@@ -231,35 +231,27 @@ MKV_DEV int lane_id_volatile() {
   return l;
 }
 
-// LDS geometry of one K or V tile: kBN key rows of kRowBytes, 16-byte chunks
-// XOR-swizzled by the key index.  The LDS serves 256 bytes per clock from 64
-// four-byte banks: 16 lanes of a 16-byte access, or 32 lanes of an 8-byte
-// one, go together, and they are conflict-free when they touch 16 distinct
-// 16-byte positions modulo 256 bytes.  A key row starts at a 128- or 256-byte
-// boundary, so that position is the chunk (and, FP8, the key's parity).
-//   16-bit: s(key) = ((key & 7) << 1) | ((key >> 3) & 1) (4 bits), a
-//     bijection on key mod 16 (K operand reads: 16 lanes, keys 16kt + c, one
-//     chunk), whose upper 3 bits are a bijection on 8 consecutive keys (V
-//     transposed reads: 32 lanes, keys 4kg + i, chunk pairs 2mm, 2mm + 1).
-//   FP8: s(key) = ((key >> 1) & 3) | ((((key >> 3) ^ (key >> 4)) & 1) << 2),
-//     a bijection on the same-parity keys among 16 consecutive ones (K
-//     reads) and among keys 4kg + j, 16 + 4kg + j for two lane groups (V
-//     reads).
-// Staging writes put 16 chunks of one 16-bit key (two FP8 keys) in one go,
-// distinct under any s.  The V read offsets are computed for the first keys
-// and reused 16 (16-bit) and 32 rows further, and the staging offsets 16-48
-// (16-bit) or 32 (FP8) rows further: s is invariant under those shifts.
+// LDS geometry of one K or V tile: kBN key rows of 256 bytes (128 16-bit
+// elements; FP8 caches are converted to fp16 as they are staged), 16-byte
+// chunks XOR-swizzled by the key index.  The LDS serves 256 bytes per clock
+// from 64 four-byte banks: 16 lanes of a 16-byte access, or 32 lanes of an
+// 8-byte one, go together, and they are conflict-free when they touch 16
+// distinct 16-byte positions of a 256-byte row (a row's chunk index).
+// s(key) = ((key & 7) << 1) | ((key >> 3) & 1) is a bijection on key mod 16
+// (K operand reads: 16 lanes, keys 16kt + c, one chunk) whose upper 3 bits
+// are a bijection on 8 consecutive keys (V transposed reads: 32 lanes, keys
+// 4kg + i, chunk pairs 2mm, 2mm + 1).  Staging writes of a 16-bit cache put
+// 16 chunks of one key in one go; an FP8 cache's writes put 8 chunks of each
+// of two keys, the even chunks of one and the odd chunks of the other.  The V
+// read offsets are computed for the first keys and reused 16 and 32 rows
+// further, the staging offsets 16-48 rows further: s has period 16.
 template <int KV_DT>
 struct LdsTile {
-  static constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
-  static constexpr int kRowBytes = kHeadDim * kEb;      // 256 (16-bit) or 128 (fp8)
-  static constexpr int kChunks = kRowBytes / 16;        // 16 or 8
+  static constexpr int kEb = 2;
+  static constexpr int kRowBytes = kHeadDim * kEb;  // 256
+  static constexpr int kChunks = kRowBytes / 16;    // 16
   static constexpr int kBytes = kBN * kRowBytes;
-  static constexpr int kChunksPerThread = kBN * kChunks / kPfThreads;  // 4 or 2
-  MKV_DEV static int swz(int key) {
-    return kEb == 2 ? ((key & 7) << 1) | ((key >> 3) & 1)
-                    : ((key >> 1) & 3) | ((((key >> 3) ^ (key >> 4)) & 1) << 2);
-  }
+  MKV_DEV static int swz(int key) { return ((key & 7) << 1) | ((key >> 3) & 1); }
   MKV_DEV static int offset(int key, int chunk) { return key * kRowBytes + ((chunk ^ swz(key)) << 4); }
 };
 
@@ -274,7 +266,11 @@ struct LdsTile {
 template <int KV_DT, bool PAGED, bool QSPLIT>
 __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4))) void prefill_mfma_kernel(PrefillArgs a) {
   using LT = LdsTile<KV_DT>;
-  constexpr int kEb = LT::kEb;
+  // CT: the element type of the LDS tiles and the MFMA operands (fp16 for
+  // an FP8 cache, converted exactly while staging).
+  constexpr int CT = KV_DT == MKV_DTYPE_FP8E4M3 ? MKV_DTYPE_F16 : KV_DT;
+  constexpr int kEbG = DTypeInfo<KV_DT>::kBytes;  // cache element bytes
+  constexpr int kChunksG = kHeadDim * kEbG / 16;   // 16-byte chunks per cache row
   extern __shared__ __align__(16) char smem[];
   // buffer b: K tile at smem + 2b*kBytes, V tile right after it
 #define KBUF(b) (smem + (b) * 2 * LT::kBytes)
@@ -395,18 +391,18 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       for (int i = 0; i < 32; ++i) qf[rt][i] *= f;
     score_mul = score_mul < 0.0f ? -score_mul : 1.0f;
   }
-  Op16<KV_DT> qop[kRowTiles][4];
-  Op16<KV_DT> qlo[QSPLIT ? kRowTiles : 1][4];
+  Op16<CT> qop[kRowTiles][4];
+  Op16<CT> qlo[QSPLIT ? kRowTiles : 1][4];
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt)
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      qop[rt][st] = to_op16<KV_DT>(qf[rt] + 8 * st);
+      qop[rt][st] = to_op16<CT>(qf[rt] + 8 * st);
       if constexpr (QSPLIT) {
         float r[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) r[j] = qf[rt][8 * st + j] - (float)qop[rt][st][j];
-        qlo[rt][st] = to_op16<KV_DT>(r);
+        qlo[rt][st] = to_op16<CT>(r);
       }
     }
 
@@ -431,25 +427,27 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   // lanes in slots of 16 keys x kChunks chunks: slot = u * kSlotsPerLoad +
   // tid / kLanesPerSlot for load u; lane: key tid%kLanesPerSlot/kChunks,
   // chunk tid%kChunks.
-  constexpr int kLanesPerSlot = 16 * LT::kChunks;            // 256 (16-bit) / 128 (FP8)
+  constexpr int kLanesPerSlot = 16 * kChunksG;               // 256 (16-bit) / 128 (FP8)
   constexpr int kSlotsPerLoad = kPfThreads / kLanesPerSlot;
   constexpr int kLoads = 8 / kSlotsPerLoad;
-  const int64_t row_stride = (int64_t)a.num_kv_heads * kHeadDim * kEb;
-  const int64_t head_bytes = (int64_t)kvh * kHeadDim * kEb;
-  const int ld_key = (tid % kLanesPerSlot) / LT::kChunks;
-  const int ld_ch = tid % LT::kChunks;
+  const int64_t row_stride = (int64_t)a.num_kv_heads * kHeadDim * kEbG;
+  const int64_t head_bytes = (int64_t)kvh * kHeadDim * kEbG;
+  const int ld_key = (tid % kLanesPerSlot) / kChunksG;
+  const int ld_ch = tid % kChunksG;
   const uint32_t ld_off = (uint32_t)(ld_key * row_stride + 16 * ld_ch);
   int ld_slot[kLoads];  // wave-uniform
 #pragma unroll
   for (int u = 0; u < kLoads; ++u)
     ld_slot[u] = __builtin_amdgcn_readfirstlane(u * kSlotsPerLoad + tid / kLanesPerSlot);
   // LDS offsets of the loads: one per-lane base plus a wave-uniform row
-  // shift.  Load u's sub-tile is (ld_slot[u] & 3) = (ld_slot[0] & 3) + 2u'
-  // (16-bit: shifts of 0 or 32 keys; FP8: 0), and the swizzle is invariant
-  // under a 32-key shift, so only one offset register lives through the loop.
-  static_assert(kSlotsPerLoad == 2 || kSlotsPerLoad == 4, "load slot layout");
-  const int lds_base = LT::offset(16 * (ld_slot[0] & 3) + ld_key, ld_ch);
-  auto lds_off = [&](int u) { return lds_base + ((ld_slot[u] & 3) - (ld_slot[0] & 3)) * 16 * LT::kRowBytes; };
+  // shift of 16 (ld_slot[u] & 3) - (ld_slot[0] & 3) keys (the swizzle has
+  // period 16), so only the base lives through the loop.  An FP8 chunk
+  // (16 elements) becomes two fp16 chunks, 2ch + b and 2ch + 1 - b with
+  // b = key parity.
+  const int lds_key0 = 16 * (ld_slot[0] & 3) + ld_key;
+  const int lds_base = kEbG == 2 ? LT::offset(lds_key0, ld_ch) : LT::offset(lds_key0, 2 * ld_ch + (ld_key & 1));
+  const int lds_base2 = kEbG == 2 ? 0 : LT::offset(lds_key0, 2 * ld_ch + 1 - (ld_key & 1));
+  auto lds_shift = [&](int u) { return ((ld_slot[u] & 3) - (ld_slot[0] & 3)) * 16 * LT::kRowBytes; };
 
   // Block-table entries of the four 16-key sub-tiles of the tile at kb: one
   // table read when a tile lies inside one block (block_size >= kBN), shared
@@ -476,11 +474,11 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       const int64_t bmask = ((int64_t)1 << a.idx.bs_log2) - 1;
       if (phys >= 0) {
         p = base + ((phys << a.idx.bs_log2) + (t0 & bmask)) * row_stride + head_bytes;
-        num = (int)(15 * row_stride + kHeadDim * kEb);
+        num = (int)(15 * row_stride + kHeadDim * kEbG);
       }
     } else {
       p = base + (q_seq0 + t0) * row_stride + head_bytes;
-      num = (int)(15 * row_stride + kHeadDim * kEb);
+      num = (int)(15 * row_stride + kHeadDim * kEbG);
     }
     return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, num, 0x00020000);
   };
@@ -501,41 +499,43 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
 #pragma unroll
     for (int u = 0; u < kLoads; ++u) {
       const bool is_v = ld_slot[u] >= 4;
-      char* dst = is_v ? VBUF(buf) : KBUF(buf);
-      *reinterpret_cast<u32x4*>(dst + lds_off(u)) = stg[u];
+      char* dst = (is_v ? VBUF(buf) : KBUF(buf)) + lds_shift(u);
+      if constexpr (kEbG == 2) {
+        *reinterpret_cast<u32x4*>(dst + lds_base) = stg[u];
+      } else {
+        // e4m3 -> fp16 is exact; elements 8h .. 8h+7 of the chunk from dwords 2h, 2h+1
+        auto half = [&](int h) {
+          const uint32_t d0 = stg[u][2 * h], d1 = stg[u][2 * h + 1];
+          const f16x2 a0 = fp8x2_to_f16x2<false>(d0), a1 = fp8x2_to_f16x2<true>(d0);
+          const f16x2 a2 = fp8x2_to_f16x2<false>(d1), a3 = fp8x2_to_f16x2<true>(d1);
+          return u32x4{__builtin_bit_cast(uint32_t, a0), __builtin_bit_cast(uint32_t, a1),
+                       __builtin_bit_cast(uint32_t, a2), __builtin_bit_cast(uint32_t, a3)};
+        };
+        const bool odd = ld_key & 1;
+        *reinterpret_cast<u32x4*>(dst + lds_base) = half(odd ? 1 : 0);
+        *reinterpret_cast<u32x4*>(dst + lds_base2) = half(odd ? 0 : 1);
+      }
     }
   };
 
   // Transposed V reads.  ds_read_b64_tr_b16: within each 16-lane group, lane
-  // d receives element d%4 of the 8-byte reads of lanes 4i + d/4 (i = 0..3);
-  // ds_read_b64_tr_b8: byte d%8 of the reads of lanes 2i + d/8 (i = 0..7).
-  // So if lane 4i + q (16-bit) / 2i + p (FP8) of lane group kg reads key
-  // k(kg, i) at dims 16mm + 4q / 16mm + 8p, lane c receives V[k(kg, i)][16mm
-  // + c] for the lane group's MFMA k-slice, where the P operand holds keys
-  // k(kg, j) = 32ks + 16*(j/4) + 4kg + j%4.  vt_off[mm]: that address in a V
-  // tile for ks = 0 (and, 16-bit, the first half j < 4; +16 rows for j >= 4).
-  // 16-bit: the offsets follow from two per-lane values (computed where they
-  // are used, so they do not hold eight registers through the key loop):
-  // chunk (2mm + x) ^ s = ((mm ^ (s >> 1)) << 1) | (x ^ (s & 1)), hence
-  // offset(mm) = vt_base + ((mm << 5) ^ vt_swh).
-  int vt_off[8];
-  int vt_base = 0, vt_swh = 0;
+  // d receives element d%4 of the 8-byte reads of lanes 4i + d/4 (i = 0..3).
+  // So if lane 4i + q of lane group kg reads key 4kg + i at dims 16mm + 4q,
+  // lane c receives V[4kg + i][16mm + c] for the lane group's MFMA k-slice,
+  // where the P operand holds keys 32ks + 16*(j/4) + 4kg + j%4 (the second
+  // half j >= 4 reads 16 rows further).  The offsets follow from two
+  // per-lane values (computed where they are used, so they do not hold eight
+  // registers through the key loop): chunk (2mm + x) ^ s =
+  // ((mm ^ (s >> 1)) << 1) | (x ^ (s & 1)), hence offset(mm) = vt_base +
+  // ((mm << 5) ^ vt_swh).
+  int vt_base, vt_swh;
   {
     const int s16 = lane & 15;
-    if constexpr (kEb == 2) {
-      const int i = s16 >> 2, q = s16 & 3;
-      const int key = 4 * kg + i;
-      const int sw = LT::swz(key);
-      vt_base = key * LT::kRowBytes + ((((q >> 1) ^ sw) & 1) << 4) + 8 * (q & 1);
-      vt_swh = (sw >> 1) << 5;
-    } else {
-#pragma unroll
-      for (int mm = 0; mm < 8; ++mm) {
-        const int i = s16 >> 1, pp = s16 & 1;
-        const int key = 16 * (i >> 2) + 4 * kg + (i & 3);
-        vt_off[mm] = LT::offset(key, mm) + 8 * pp;
-      }
-    }
+    const int i = s16 >> 2, q = s16 & 3;
+    const int key = 4 * kg + i;
+    const int sw = LT::swz(key);
+    vt_base = key * LT::kRowBytes + ((((q >> 1) ^ sw) & 1) << 4) + 8 * (q & 1);
+    vt_swh = (sw >> 1) << 5;
   }
 
   const int n_tiles = (max_vis + kBN - 1) / kBN;
@@ -578,7 +578,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     // 16-bit: the lane's key row, recomputed here: held across the loop it
     // is the register the allocator spills first, and its reload would wait
     // for the tile prefetch issued just above.
-    const int c_k = kEb == 2 ? lane_id_volatile() & 15 : c;
+    const int c_k = lane_id_volatile() & 15;
     f32x4 s[4][kRowTiles];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
@@ -587,22 +587,12 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       const int key = 16 * kt + c_k;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        Op16<KV_DT> kop;
-        if constexpr (kEb == 2) {
-          const u32x4 w = *reinterpret_cast<const u32x4*>(KBUF(buf) + LT::offset(key, 4 * kg + st));
-          kop = __builtin_bit_cast(Op16<KV_DT>, w);
-        } else {
-          const u32x4 w = *reinterpret_cast<const u32x4*>(KBUF(buf) + LT::offset(key, 2 * kg + (st >> 1)));
-          const uint32_t d0 = (st & 1) ? w[2] : w[0];
-          const uint32_t d1 = (st & 1) ? w[3] : w[1];
-          const f16x2 a0 = fp8x2_to_f16x2<false>(d0), a1 = fp8x2_to_f16x2<true>(d0);
-          const f16x2 a2 = fp8x2_to_f16x2<false>(d1), a3 = fp8x2_to_f16x2<true>(d1);
-          kop = f16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
-        }
+        const u32x4 w = *reinterpret_cast<const u32x4*>(KBUF(buf) + LT::offset(key, 4 * kg + st));
+        const Op16<CT> kop = __builtin_bit_cast(Op16<CT>, w);
 #pragma unroll
         for (int rt = 0; rt < kRowTiles; ++rt) {
-          s[kt][rt] = mfma16<KV_DT>(kop, qop[rt][st], s[kt][rt]);
-          if constexpr (QSPLIT) s[kt][rt] = mfma16<KV_DT>(kop, qlo[rt][st], s[kt][rt]);
+          s[kt][rt] = mfma16<CT>(kop, qop[rt][st], s[kt][rt]);
+          if constexpr (QSPLIT) s[kt][rt] = mfma16<CT>(kop, qlo[rt][st], s[kt][rt]);
         }
       }
     }
@@ -662,11 +652,11 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     __builtin_amdgcn_s_setprio(1);
     // B operand of output-dim tile mm (dims 16mm .. 16mm+15, lane c -> dim
     // 16mm + c): the lane group's 8 keys of its k-slice, read transposed
-    // straight from LDS (ds_read_b64_tr_b16 / _tr_b8), see vt_off below.
+    // straight from LDS (ds_read_b64_tr_b16, see vt_base above).
     char* vbuf = VBUF(buf);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      Op16<KV_DT> pop[kRowTiles], plop[kRowTiles];
+      Op16<CT> pop[kRowTiles], plop[kRowTiles];
 #pragma unroll
       for (int rt = 0; rt < kRowTiles; ++rt) {
         float pv[8];
@@ -675,7 +665,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
           pv[r] = p[2 * ks][rt][r];
           pv[4 + r] = p[2 * ks + 1][rt][r];
         }
-        pop[rt] = to_op16<KV_DT>(pv);
+        pop[rt] = to_op16<CT>(pv);
         if constexpr (KV_DT == MKV_DTYPE_BF16) {
           // second bf16 term carrying P's rounding residual (~16-bit P);
           // p - hi is exact in fp32 and one dot2 forms it: hi_pair . (-1, 0)
@@ -693,54 +683,33 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
             plo[j] = __builtin_amdgcn_fdot2_f32_bf16(h, neg_lo, pv[j], false);
             plo[j + 1] = __builtin_amdgcn_fdot2_f32_bf16(h, neg_hi, pv[j + 1], false);
           }
-          plop[rt] = to_op16<KV_DT>(plo);
+          plop[rt] = to_op16<CT>(plo);
         }
       }
-      // B operands read in batches ahead of their MFMAs so that the LDS reads
-      // overlap: all 8 for 16-bit KV, 4 for FP8 (whose conversions need more
-      // registers; this keeps both within 128 registers without spills in the
-      // loop)
-      constexpr int kBBatch = kEb == 1 ? 4 : 8;
+      // all 8 B operands read ahead of their MFMAs so that the LDS reads overlap
+      Op16<CT> Bv[8];
 #pragma unroll
-      for (int half = 0; half < 8 / kBBatch; ++half) {
-      Op16<KV_DT> Bv[kBBatch];
-#pragma unroll
-      for (int m4 = 0; m4 < kBBatch; ++m4) {
-        const int mm = kBBatch * half + m4;
-        Op16<KV_DT>& B = Bv[m4];
-        if constexpr (kEb == 2) {
-          typedef short v4i16 __attribute__((ext_vector_type(4)));
-          typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-          const int vo = vt_base + ((mm << 5) ^ vt_swh);
-          lds_v4i16* p0 = (lds_v4i16*)(vbuf + vo + 32 * ks * LT::kRowBytes);
-          lds_v4i16* p1 = (lds_v4i16*)(vbuf + vo + (32 * ks + 16) * LT::kRowBytes);
-          const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p0);
-          const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p1);
-          const u32x4 w = {(uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16),
-                           (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16),
-                           (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16),
-                           (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16)};
-          B = __builtin_bit_cast(Op16<KV_DT>, w);
-        } else {
-          typedef int v2i32 __attribute__((ext_vector_type(2)));
-          typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
-          const v2i32 w = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-              (lds_v2i32*)(vbuf + vt_off[mm] + 32 * ks * LT::kRowBytes));
-          const f16x2 a0 = fp8x2_to_f16x2<false>((uint32_t)w[0]), a1 = fp8x2_to_f16x2<true>((uint32_t)w[0]);
-          const f16x2 a2 = fp8x2_to_f16x2<false>((uint32_t)w[1]), a3 = fp8x2_to_f16x2<true>((uint32_t)w[1]);
-          B = f16x8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
-        }
+      for (int mm = 0; mm < 8; ++mm) {
+        typedef short v4i16 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+        const int vo = vt_base + ((mm << 5) ^ vt_swh);
+        lds_v4i16* p0 = (lds_v4i16*)(vbuf + vo + 32 * ks * LT::kRowBytes);
+        lds_v4i16* p1 = (lds_v4i16*)(vbuf + vo + (32 * ks + 16) * LT::kRowBytes);
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p0);
+        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p1);
+        const u32x4 w = {(uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16),
+                         (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16),
+                         (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16),
+                         (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16)};
+        Bv[mm] = __builtin_bit_cast(Op16<CT>, w);
       }
 #pragma unroll
-      for (int m4 = 0; m4 < kBBatch; ++m4) {
-        const int mm = kBBatch * half + m4;
-        const Op16<KV_DT> B = Bv[m4];
+      for (int mm = 0; mm < 8; ++mm) {
 #pragma unroll
         for (int rt = 0; rt < kRowTiles; ++rt) {
-          acc[rt][mm] = mfma16<KV_DT>(pop[rt], B, acc[rt][mm]);
-          if constexpr (KV_DT == MKV_DTYPE_BF16) acc[rt][mm] = mfma16<KV_DT>(plop[rt], B, acc[rt][mm]);
+          acc[rt][mm] = mfma16<CT>(pop[rt], Bv[mm], acc[rt][mm]);
+          if constexpr (CT == MKV_DTYPE_BF16) acc[rt][mm] = mfma16<CT>(plop[rt], Bv[mm], acc[rt][mm]);
         }
-      }
       }
     }
     __builtin_amdgcn_s_setprio(0);
