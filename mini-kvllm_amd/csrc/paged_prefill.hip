@@ -241,8 +241,9 @@ MKV_DEV int lane_id_volatile() {
 // (K operand reads: 16 lanes, keys 16kt + c, one chunk) whose upper 3 bits
 // are a bijection on 8 consecutive keys (V transposed reads: 32 lanes, keys
 // 4kg + i, chunk pairs 2mm, 2mm + 1).  Staging writes of a 16-bit cache put
-// 16 chunks of one key in one go; an FP8 cache's writes put 8 chunks of each
-// of two keys, the even chunks of one and the odd chunks of the other.  The V
+// 16 chunks of one key in one go (writes go 8 lanes at a time, over 32
+// banks: 8 distinct chunks mod 8 under any s); an FP8 cache's chunk pairs are
+// split so that each write touches 8 distinct positions too.  The V
 // read offsets are computed for the first keys and reused 16 and 32 rows
 // further, the staging offsets 16-48 rows further: s has period 16.
 template <int KV_DT>
@@ -442,11 +443,14 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   // LDS offsets of the loads: one per-lane base plus a wave-uniform row
   // shift of 16 (ld_slot[u] & 3) - (ld_slot[0] & 3) keys (the swizzle has
   // period 16), so only the base lives through the loop.  An FP8 chunk
-  // (16 elements) becomes two fp16 chunks, 2ch + b and 2ch + 1 - b with
-  // b = key parity.
+  // (16 elements) becomes two fp16 chunks, written as 2ch + b, then
+  // 2ch + 1 - b, with b = ((ch >> 2) ^ key) & 1: LDS writes go 8 lanes (one
+  // key) at a time over 32 banks, and b gives those lanes 8 distinct chunk
+  // positions mod 8 (and a 16-lane pair of keys all 16).
   const int lds_key0 = 16 * (ld_slot[0] & 3) + ld_key;
-  const int lds_base = kEbG == 2 ? LT::offset(lds_key0, ld_ch) : LT::offset(lds_key0, 2 * ld_ch + (ld_key & 1));
-  const int lds_base2 = kEbG == 2 ? 0 : LT::offset(lds_key0, 2 * ld_ch + 1 - (ld_key & 1));
+  const int ld_b = ((ld_ch >> 2) ^ ld_key) & 1;
+  const int lds_base = kEbG == 2 ? LT::offset(lds_key0, ld_ch) : LT::offset(lds_key0, 2 * ld_ch + ld_b);
+  const int lds_base2 = kEbG == 2 ? 0 : LT::offset(lds_key0, 2 * ld_ch + 1 - ld_b);
   auto lds_shift = [&](int u) { return ((ld_slot[u] & 3) - (ld_slot[0] & 3)) * 16 * LT::kRowBytes; };
 
   // Block-table entries of the four 16-key sub-tiles of the tile at kb: one
@@ -511,9 +515,8 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
           return u32x4{__builtin_bit_cast(uint32_t, a0), __builtin_bit_cast(uint32_t, a1),
                        __builtin_bit_cast(uint32_t, a2), __builtin_bit_cast(uint32_t, a3)};
         };
-        const bool odd = ld_key & 1;
-        *reinterpret_cast<u32x4*>(dst + lds_base) = half(odd ? 1 : 0);
-        *reinterpret_cast<u32x4*>(dst + lds_base2) = half(odd ? 0 : 1);
+        *reinterpret_cast<u32x4*>(dst + lds_base) = half(ld_b);
+        *reinterpret_cast<u32x4*>(dst + lds_base2) = half(1 - ld_b);
       }
     }
   };
