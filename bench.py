@@ -45,7 +45,10 @@ KV_DESC = {"fp8": "per-tensor e4m3fn", "bf16": "bf16",
            "int8_token": "int8 codes, fp32 scale per token and kv head"}
 
 
-def parse_args():
+EXTRAS = ("append", "prefill", "latency", "producer", "mixed", "copy")
+
+
+def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
@@ -61,10 +64,23 @@ def parse_args():
     ap.add_argument("--cpu-seqs", type=int, default=64,
                     help="sequences in the CPU-baseline sample (0 = skip the CPU baseline)")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary measurements")
+    ap.add_argument("--extra", default="all",
+                    help="secondary measurements to run: 'all' or a comma list of "
+                         "append, prefill, latency, producer, mixed, copy")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (5 times) and exit; "
                          "its rocprofv3 FETCH_SIZE/WRITE_SIZE calibrate the PMC byte counts")
-    return ap.parse_args()
+    args = ap.parse_args(argv)
+    if args.no_extra:
+        args.extra_set = set()
+    elif args.extra == "all":
+        args.extra_set = set(EXTRAS)
+    else:
+        args.extra_set = {x.strip() for x in args.extra.split(",") if x.strip()}
+        unknown = args.extra_set - set(EXTRAS)
+        if unknown:
+            ap.error(f"--extra: unknown measurement(s) {sorted(unknown)}; choose from {list(EXTRAS)}")
+    return args
 
 
 def cpu_model() -> str:
@@ -543,10 +559,11 @@ def main() -> int:
         "step_time": pct,
     }
 
-    if not args.no_extra:
+    wanted = args.extra_set
+    if wanted:
         extra = {}
         # KV append + FP8 quantisation: 4096 tokens (5% padding) and 65536 tokens
-        for T in (4096, 65536):
+        for T in ((4096, 65536) if "append" in wanted else ()):
             w = W.append_fp8(seed=2, num_tokens=T) if T == 4096 else None
             if w is None:
                 gg = torch.Generator().manual_seed(20)
@@ -563,13 +580,18 @@ def main() -> int:
             ab = W.alg_bytes_append(w["slot_mapping"], 8, 2, 1)
             extra[f"append_fp8_T{T}"] = {"us": round(ams * 1e3, 2), "GBps": round(ab / ams / 1e6, 1)}
             del kp, vp
-        extra["prefill_chunked"] = prefill_extra(dev, stream)
-        extra["decode_step_latency"] = decode_step_latency(dev)
-        extra["producer_fused"] = producer_extra(dev, stream)
-        extra["mixed_batch"] = mixed_batch_extra(dev, stream)
-        copy = box_copy_gbps(dev, stream)
-        extra["box_copy_GBps"] = round(copy, 1)
-        extra["decode_frac_of_box_copy"] = round(gbps / copy, 4)
+        if "prefill" in wanted:
+            extra["prefill_chunked"] = prefill_extra(dev, stream)
+        if "latency" in wanted:
+            extra["decode_step_latency"] = decode_step_latency(dev)
+        if "producer" in wanted:
+            extra["producer_fused"] = producer_extra(dev, stream)
+        if "mixed" in wanted:
+            extra["mixed_batch"] = mixed_batch_extra(dev, stream)
+        if "copy" in wanted:
+            copy = box_copy_gbps(dev, stream)
+            extra["box_copy_GBps"] = round(copy, 1)
+            extra["decode_frac_of_box_copy"] = round(gbps / copy, 4)
         result["extra"] = extra
 
     if args.cpu_seqs > 0 and not per_token:

@@ -542,8 +542,12 @@ class Attention(nn.Module):
         # the reference's route (attention.py:1711-1760): index_select the
         # decode and prefill rows, two kernels, index_copy_ back; "overlap"
         # is "split" with the decode rows on a second stream, concurrent with
-        # the prefill kernel.
-        self.mixed_batch = "overlap"
+        # the prefill kernel.  "unified" is the default: the prefill kernel
+        # reads a decode row's K/V once per KV head, as the decode kernel
+        # does, and its longest-first tile order runs the long decode rows
+        # first and fills in around them, with no gathers and no second
+        # launch.
+        self.mixed_batch = "unified"
 
     def _mode(self) -> str:
         mode = self.kv_cache_dtype

@@ -271,3 +271,16 @@ def test_key_and_value_reach_the_abi_in_one_dtype(monkeypatch):
         A._append(key, value[:3], kc, kc.clone(), slots, torch.ones(1), torch.ones(1))
     with pytest.raises(TypeError):
         A._append(key, value, kc, kb, slots, torch.ones(1), torch.ones(1))
+
+
+def test_bench_extra_selection():
+    """bench.py's --extra picks secondary measurements by name (for profiling
+    one workload at a time) and refuses unknown names before any GPU work."""
+    import sys
+    sys.path.insert(0, str(REPO))
+    import bench
+    assert bench.parse_args([]).extra_set == set(bench.EXTRAS)
+    assert bench.parse_args(["--extra", "prefill, mixed"]).extra_set == {"prefill", "mixed"}
+    assert bench.parse_args(["--no-extra", "--extra", "prefill"]).extra_set == set()
+    with pytest.raises(SystemExit):
+        bench.parse_args(["--extra", "prefil"])
