@@ -138,7 +138,7 @@ def box_copy_gbps(dev, stream, mib: int = 2048) -> float:
     return 2 * (mib << 20) / (ms * 1e-3) / 1e9
 
 
-def prefill_extra(dev, stream) -> dict:
+def prefill_extra(dev, stream, cpu: bool = True) -> dict:
     """Chunked prefill over the paged cache: the 8 prefill sequences of the
     mixed-batch workload (prior context U[0, 4096], 512-row chunks), 32 q / 8
     kv heads, bf16 q, bf16 and FP8 KV.  FLOPs are algorithmic (4*D per
@@ -178,8 +178,79 @@ def prefill_extra(dev, stream) -> dict:
         tf = flops / (ms * 1e-3) / 1e12
         out[f"{name}_kv"] = {"us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1),
                              "frac_of_2500_TFLOPs": round(tf / 2500.0, 4)}
+        if name == "bf16" and cpu:
+            out["cpu_baseline"] = cpu_prefill_baseline(q, kc, vc, bt, ctx, cu_p, pos, pm["block_size"])
         del kc, vc
     return out
+
+
+def _cpu_threads() -> int:
+    import torch
+
+    threads = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit():
+        threads = min(threads, int(env))
+    torch.set_num_threads(threads)
+    return threads
+
+
+def _median_time(fn, reps: int = 3) -> float:
+    fn()  # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def cpu_prefill_baseline(q, kc, vc, bt, ctx, cu_p, pos, bs) -> dict:
+    """The reference's CPU prefill semantics (oracle paged_prefill_ref in
+    fp32: per-sequence gather, causal masked matmul / softmax, the paged
+    prefix included) on the first sequence of the chunked-prefill workload,
+    all 32 query heads."""
+    import torch
+
+    from mkv import workloads as W
+    from oracle import reference as R
+
+    threads = _cpu_threads()
+    n = int(cu_p[1])
+    blocks = bt[0][bt[0] >= 0].to(torch.int64)
+    idx = blocks.to(kc.device)
+    kh, vh = kc.index_select(0, idx).cpu(), vc.index_select(0, idx).cpu()
+    bt_h = torch.arange(blocks.numel(), dtype=torch.int32).view(1, -1)
+    qh = q[:n].cpu()
+    cu_h = torch.tensor([0, n], dtype=torch.int32)
+    ctx_h, pos_h = ctx[:1], pos[:n]
+    sm = 1.0 / math.sqrt(HEAD_DIM)
+    t = _median_time(lambda: R.paged_prefill_ref(qh, kh, vh, bt_h, ctx_h, cu_h, pos_h, sm, 32, 8,
+                                                  compute_dtype=torch.float32))
+    fl = W.alg_flops_prefill(ctx_h, cu_h, pos_h, 32)
+    return {"value": round(fl / t / 1e9, 2), "unit": "GFLOP/s", "cores": threads, "kind": "port",
+            "sample": (f"sequence 0: {n} rows after a prior of {int(ctx[0]) - n} tokens, 32 q / 8 kv "
+                       f"heads, bf16 KV, paged_prefill_ref in fp32, median of 3: {t:.3f} s "
+                       f"({fl / 1e9:.1f} GFLOP)")}
+
+
+def cpu_append_baseline(key, value, slots, ks: float, vs: float) -> dict:
+    """The reference's FP8 append semantics on the host cores (oracle
+    store_kvcache_fp8_ref: fp32 divide, clamp, e4m3fn cast, scatter into the
+    pool) for the 4096-token append workload."""
+    import torch
+
+    from mkv import workloads as W
+    from oracle import reference as R
+
+    threads = _cpu_threads()
+    kp = torch.zeros(1024, 256, 8, HEAD_DIM, dtype=torch.float8_e4m3fn)
+    vp = torch.zeros_like(kp)
+    kst, vst = torch.tensor([ks]), torch.tensor([vs])
+    t = _median_time(lambda: R.store_kvcache_fp8_ref(key, value, kp, vp, kst, vst, slots))
+    ab = W.alg_bytes_append(slots, 8, 2, 1)
+    return {"value": round(ab / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the whole workload ({slots.numel()} tokens), median of 3: {t * 1e3:.1f} ms"}
 
 
 def mixed_batch_extra(dev, stream) -> dict:
@@ -208,7 +279,15 @@ def mixed_batch_extra(dev, stream) -> dict:
     split.prefill_seq_indices_tensor = torch.tensor(split.prefill_seq_indices, device=dev)
     split.prefill_cu_seqlens_q_tensor = torch.tensor(split.prefill_cu_seqlens_q, dtype=torch.int32,
                                                      device=dev)
-    res = {"workload": f"{T} rows: 8 x 512-row prefill chunks + 120 decode rows, 32 q / 8 kv heads"}
+    res = {"workload": f"{T} rows: 8 x 512-row prefill chunks + 120 decode rows, 32 q / 8 kv heads; "
+                       "*_with_append_us: each row's own K/V (bf16) appended in the timed step first"}
+    # each row's slot: its position through its sequence's block table
+    bs_m = m["block_size"]
+    seq_of_row = torch.repeat_interleave(torch.arange(len(m["query_lens"])), torch.tensor(m["query_lens"]))
+    pos = m["positions"]
+    slots = (m["block_tables"][seq_of_row, pos // bs_m].to(torch.int64) * bs_m + pos % bs_m).to(dev)
+    k_new = torch.randn(T, 8, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    v_new = torch.randn(T, 8, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
     for name, dt in (("bf16", torch.bfloat16), ("fp8", torch.float8_e4m3fn)):
         kc = torch.empty(m["num_blocks"], m["block_size"], 8, HEAD_DIM, dtype=dt, device=dev)
         vc = torch.empty_like(kc)
@@ -231,6 +310,15 @@ def mixed_batch_extra(dev, stream) -> dict:
                 ms = time_launches(lambda i: layer(q, q, q, kv_appended=True), 20, 3, stream)
                 row[f"{route}_us"] = round(ms * 1e3, 1)
             row["best_speedup_vs_split"] = round(row["split_us"] / min(row["unified_us"], row["overlap_us"]), 2)
+            # the engine's step: the rows' own K/V appended first (store, then attend)
+            C.set_context(True, cu_seqlens_q=m["cu_seqlens_q"].to(dev), max_seqlen_q=512,
+                          slot_mapping=slots, context_lens=m["context_lens"].to(dev),
+                          block_tables=m["block_tables"].to(dev), positions=m["positions"].to(dev),
+                          mixed_attention_split=split, is_full_prefill=False)
+            for route in ("split", "unified"):
+                layer.mixed_batch = route
+                ms = time_launches(lambda i: layer(q, k_new, v_new), 20, 3, stream)
+                row[f"{route}_with_append_us"] = round(ms * 1e3, 1)
         finally:
             C.reset_context()
         res[f"{name}_kv"] = row
@@ -579,9 +667,12 @@ def main() -> int:
             ams = time_launches(lambda i: A._append(kd, vd, kp, vp, sd, ksd, vsd), 50, 5, stream)
             ab = W.alg_bytes_append(w["slot_mapping"], 8, 2, 1)
             extra[f"append_fp8_T{T}"] = {"us": round(ams * 1e3, 2), "GBps": round(ab / ams / 1e6, 1)}
+            if T == 4096 and args.cpu_seqs > 0:
+                extra[f"append_fp8_T{T}"]["cpu_baseline"] = cpu_append_baseline(
+                    w["key"], w["value"], w["slot_mapping"], 0.05, 0.05)
             del kp, vp
         if "prefill" in wanted:
-            extra["prefill_chunked"] = prefill_extra(dev, stream)
+            extra["prefill_chunked"] = prefill_extra(dev, stream, cpu=args.cpu_seqs > 0)
         if "latency" in wanted:
             extra["decode_step_latency"] = decode_step_latency(dev)
         if "producer" in wanted:
