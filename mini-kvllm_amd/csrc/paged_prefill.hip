@@ -4,24 +4,26 @@
 // Reference semantics: paged_attention_prefill_kernel (attention.py:704-847,
 // wrapper :852-891; visible = min(context_len, position + 1) at :747) and
 // flash_attention_varlen_kernel (attention.py:336-443, wrapper :446-514).
-// FP8 caches are dequantised exactly (e4m3fn -> fp16) in the kernel, which
-// the reference leaves unimplemented (attention.py:1702-1708).
+// FP8 caches are dequantised exactly (e4m3fn -> fp16) as their tiles are
+// staged into LDS, which the reference leaves unimplemented
+// (attention.py:1702-1708).
 //
 // Work decomposition: a workgroup of 8 wavefronts owns 128 "rows" of one
 // sequence and one KV head, where a row is a (query token, query head of the
 // GQA group) pair, token-major; every row of the group reads the same K/V,
 // so each K/V tile is staged in LDS once for G query heads.  Tiles of 64 keys
 // are gathered through the block table into double-buffered LDS with an XOR
-// swizzle on 16-byte chunks (conflict-free MFMA operand reads).  Each wave
+// swizzle on 16-byte chunks (every LDS access conflict-free).  Each wave
 // owns one row tile of 16 and computes
 //   S^T = K Q^T     (A = K from LDS, B = Q^T resident in registers)
 //   O  += P V       (A = P straight from the S^T accumulators, B = V read
-//                    from LDS already transposed by ds_read_b64_tr_b16 / _b8)
+//                    from LDS already transposed by ds_read_b64_tr_b16)
 // with an online softmax in the log2 domain whose output rescale is deferred
 // until a row's running max grows by more than 2^8.  The varlen tile list is
-// built on the device by a one-workgroup scan, so the launch needs no host
-// sync; the grid is ordered so that all tiles of one KV head run on one XCD
-// and share its L2.
+// built on the device by a one-workgroup scan (longest sequences first, each
+// sequence's last tile first), so the launch needs no host sync; with a
+// multiple of 8 KV heads the grid is ordered so that all tiles of one KV head
+// run on one XCD and share its L2.
 #include "mkv_device.hpp"
 
 namespace mkv {
