@@ -141,7 +141,7 @@ def box_copy_gbps(dev, stream, mib: int = 2048) -> float:
 def prefill_extra(dev, stream, cpu: bool = True) -> dict:
     """Chunked prefill over the paged cache: the 8 prefill sequences of the
     mixed-batch workload (prior context U[0, 4096], 512-row chunks), 32 q / 8
-    kv heads, bf16 q, bf16 and FP8 KV.  FLOPs are algorithmic (4*D per
+    kv heads, bf16 q; bf16, per-tensor FP8, per-token-head FP8 and INT8 KV.  FLOPs are algorithmic (4*D per
     visible key per row and head); peak is dense fp16/bf16 MFMA."""
     import torch
 
@@ -163,15 +163,23 @@ def prefill_extra(dev, stream, cpu: bool = True) -> dict:
     dev_meta = (bt.to(dev), ctx.to(dev), cu_p.to(dev), pos.to(dev))
     out = {"workload": (f"{len(sel)} sequences x 512 query rows, prior context "
                         f"{[int(c) - 512 for c in ctx]}, {flops / 1e9:.1f} GFLOP")}
-    for name, dt in (("bf16", torch.bfloat16), ("fp8", torch.float8_e4m3fn)):
+    for name, dt in (("bf16", torch.bfloat16), ("fp8", torch.float8_e4m3fn),
+                     ("fp8_token", torch.float8_e4m3fn), ("int8_token", torch.int8)):
         kc = torch.empty(pm["num_blocks"], pm["block_size"], 8, HEAD_DIM, dtype=dt, device=dev)
         vc = torch.empty_like(kc)
-        ks = W.fill_pool_on_device(kc, 400)
-        vs = W.fill_pool_on_device(vc, 401)
         kw = {}
-        if name == "fp8":
-            kw = dict(k_scale=torch.tensor([ks], device=dev), v_scale=torch.tensor([vs], device=dev),
-                      kv_cache_dtype="fp8_per_tensor")
+        if name.endswith("_token"):
+            mode = "fp8_per_token_head" if name == "fp8_token" else "int8_per_token_head"
+            kst = torch.empty(pm["num_blocks"], pm["block_size"], 8, dtype=torch.float32, device=dev)
+            vst = torch.empty_like(kst)
+            W.fill_pools_per_token_head_on_device(kc, vc, kst, vst, 400, mode)
+            kw = dict(k_scale=kst, v_scale=vst, kv_cache_dtype=mode)
+        else:
+            ks = W.fill_pool_on_device(kc, 400)
+            vs = W.fill_pool_on_device(vc, 401)
+            if name == "fp8":
+                kw = dict(k_scale=torch.tensor([ks], device=dev), v_scale=torch.tensor([vs], device=dev),
+                          kv_cache_dtype="fp8_per_tensor")
         args = (q, kc, vc, *dev_meta[:2], dev_meta[2], dev_meta[3], 1.0 / math.sqrt(HEAD_DIM), 32, 8,
                 HEAD_DIM, pm["block_size"])
         ms = time_launches(lambda i: A.paged_attention_prefill_triton(*args, **kw), 20, 3, stream)

@@ -178,7 +178,7 @@ MKV_DEV u32x4 quantize16_i8(const float (&x)[16], float inv) {
 MKV_DEV float fp8_head_scale(float amax) { return amax > 0.0f ? amax / kFp8Max : 1.0f; }
 MKV_DEV float i8_head_scale(float amax) { return fmaxf(amax / 127.0f, 1e-6f); }
 
-// Two e4m3fn bytes (low or high half-word of w) -> exact fp16 pair.// Two e4m3fn bytes (low or high half-word of w) -> exact fp16 pair.
+// Two e4m3fn bytes (low or high half-word of w) -> exact fp16 pair.
 template <bool kHi>
 MKV_DEV f16x2 fp8x2_to_f16x2(uint32_t w) {
   return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, kHi);

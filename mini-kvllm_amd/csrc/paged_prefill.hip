@@ -24,6 +24,8 @@
 // sequence's last tile first), so the launch needs no host sync; with a
 // multiple of 8 KV heads the grid is ordered so that all tiles of one KV head
 // run on one XCD and share its L2.
+#include <type_traits>
+
 #include "mkv_device.hpp"
 
 namespace mkv {
@@ -271,7 +273,10 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   using LT = LdsTile<KV_DT>;
   // CT: the element type of the LDS tiles and the MFMA operands (fp16 for
   // an FP8 cache, converted exactly while staging).
-  constexpr int CT = KV_DT == MKV_DTYPE_FP8E4M3 ? MKV_DTYPE_F16 : KV_DT;
+  // Per-token-head FP8 / INT8 caches: codes staged as exact bf16, scales
+  // applied per key (K scale to the score, V scale to P).
+  constexpr bool kTokScale = kPerTokenScale<KV_DT>;
+  constexpr int CT = kTokScale ? MKV_DTYPE_BF16 : (KV_DT == MKV_DTYPE_FP8E4M3 ? MKV_DTYPE_F16 : KV_DT);
   constexpr int kEbG = DTypeInfo<KV_DT>::kBytes;  // cache element bytes
   constexpr int kChunksG = kHeadDim * kEbG / 16;   // 16-byte chunks per cache row
   extern __shared__ __align__(16) char smem[];
@@ -280,6 +285,8 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
 #define VBUF(b) (smem + (b) * 2 * LT::kBytes + LT::kBytes)
   int* vis_lds = reinterpret_cast<int*>(smem + 4 * LT::kBytes);  // [kRowsPerWg]
   int* red_lds = vis_lds + kRowsPerWg;                             // [2]
+  // per-token-head scales of the staged tiles: [buffer][K keys 0..63, V keys 0..63]
+  float* sc_lds = reinterpret_cast<float*>(red_lds + 4);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -369,7 +376,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   }
   float score_mul = a.sm_scale * kLog2e;
   if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) score_mul *= load_uniform_f32(a.k_scale);
-  if constexpr (KV_DT != MKV_DTYPE_BF16) {
+  if constexpr (CT != MKV_DTYPE_BF16) {
     // power-of-two normalisation so that q is exact and in range in fp16
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) qmax = fmaxf(qmax, __shfl_xor(qmax, off));
@@ -489,6 +496,23 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, num, 0x00020000);
   };
   u32x4 stg[kLoads];
+  // Per-token-head scales of a tile: lane tid < 128 loads the K (tid < 64) or
+  // V scale of key tid % 64 (0 for keys past max_vis or in absent blocks;
+  // every lane loads, the others from index 0, so the load is unconditional).
+  float stg_sc = 0.0f;
+  auto load_scales = [&](int kb, const int64_t (&ph)[4]) {
+    if constexpr (kTokScale && PAGED) {
+      const int key = tid & 63;
+      const int j = key >> 4;
+      const int64_t phys = j == 0 ? ph[0] : (j == 1 ? ph[1] : (j == 2 ? ph[2] : ph[3]));
+      const int64_t t = (int64_t)kb + key;
+      const bool valid = tid < 128 && phys >= 0 && t < max_vis;
+      const int64_t slot = (phys << a.idx.bs_log2) + (t & (((int64_t)1 << a.idx.bs_log2) - 1));
+      const float* base = tid >= 64 ? a.v_scale : a.k_scale;
+      const float x = base[valid ? slot * a.num_kv_heads + kvh : 0];
+      stg_sc = valid ? x : 0.0f;
+    }
+  };
   auto load_tile = [&](int kb, const int64_t (&ph)[4]) {
 #pragma unroll
     for (int u = 0; u < kLoads; ++u) {
@@ -500,6 +524,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       const uint32_t off = (t0 + ld_key < max_vis) ? ld_off : 0x80000000u;
       stg[u] = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     }
+    load_scales(kb, ph);
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
@@ -509,18 +534,28 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       if constexpr (kEbG == 2) {
         *reinterpret_cast<u32x4*>(dst + lds_base) = stg[u];
       } else {
-        // e4m3 -> fp16 is exact; elements 8h .. 8h+7 of the chunk from dwords 2h, 2h+1
+        // e4m3 -> fp16 (per tensor) or e4m3 / int8 -> bf16 (per token and
+        // head) is exact; elements 8h .. 8h+7 of the chunk from dwords 2h, 2h+1
+        auto pair = [&](uint32_t d, auto hi_tag) -> uint32_t {
+          constexpr bool kHi = decltype(hi_tag)::value;
+          if constexpr (KV_DT == kKvI8PerToken)
+            return __builtin_bit_cast(uint32_t, i8x2_to_bf16x2<kHi>(d));
+          else if constexpr (KV_DT == kKvFp8PerToken)
+            return __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<kHi>(d));
+          else
+            return __builtin_bit_cast(uint32_t, fp8x2_to_f16x2<kHi>(d));
+        };
         auto half = [&](int h) {
           const uint32_t d0 = stg[u][2 * h], d1 = stg[u][2 * h + 1];
-          const f16x2 a0 = fp8x2_to_f16x2<false>(d0), a1 = fp8x2_to_f16x2<true>(d0);
-          const f16x2 a2 = fp8x2_to_f16x2<false>(d1), a3 = fp8x2_to_f16x2<true>(d1);
-          return u32x4{__builtin_bit_cast(uint32_t, a0), __builtin_bit_cast(uint32_t, a1),
-                       __builtin_bit_cast(uint32_t, a2), __builtin_bit_cast(uint32_t, a3)};
+          return u32x4{pair(d0, std::false_type{}), pair(d0, std::true_type{}),
+                       pair(d1, std::false_type{}), pair(d1, std::true_type{})};
         };
         *reinterpret_cast<u32x4*>(dst + lds_base) = half(ld_b);
         *reinterpret_cast<u32x4*>(dst + lds_base2) = half(1 - ld_b);
       }
     }
+    if constexpr (kTokScale)
+      if (tid < 128) sc_lds[buf * 128 + tid] = stg_sc;
   };
 
   // Transposed V reads.  ds_read_b64_tr_b16: within each 16-lane group, lane
@@ -609,6 +644,17 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     // constant is monotonic), and each P takes one FMA.
     float p[4][kRowTiles][4];
     float alpha[kRowTiles];
+    // per-token-head K scales of this lane's keys 16kt + 4kg + r
+    if constexpr (kTokScale) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const f32x4 ksc = *reinterpret_cast<const f32x4*>(sc_lds + buf * 128 + 16 * kt + 4 * kg);
+#pragma unroll
+        for (int rt = 0; rt < kRowTiles; ++rt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[kt][rt][r] *= ksc[r];
+      }
+    }
 #pragma unroll
     for (int rt = 0; rt < kRowTiles; ++rt) {
       if (!full) {
@@ -659,6 +705,12 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     // 16mm + c): the lane group's 8 keys of its k-slice, read transposed
     // straight from LDS (ds_read_b64_tr_b16, see vt_base above).
     char* vbuf = VBUF(buf);
+    f32x4 vsc[4];  // per-token-head V scales of keys 16kt + 4kg + r (P * v_scale)
+    if constexpr (kTokScale) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+        vsc[kt] = *reinterpret_cast<const f32x4*>(sc_lds + buf * 128 + 64 + 16 * kt + 4 * kg);
+    }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       Op16<CT> pop[kRowTiles], plop[kRowTiles];
@@ -669,9 +721,13 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
         for (int r = 0; r < 4; ++r) {
           pv[r] = p[2 * ks][rt][r];
           pv[4 + r] = p[2 * ks + 1][rt][r];
+          if constexpr (kTokScale) {
+            pv[r] *= vsc[2 * ks][r];
+            pv[4 + r] *= vsc[2 * ks + 1][r];
+          }
         }
         pop[rt] = to_op16<CT>(pv);
-        if constexpr (KV_DT == MKV_DTYPE_BF16) {
+        if constexpr (CT == MKV_DTYPE_BF16) {
           // second bf16 term carrying P's rounding residual (~16-bit P);
           // p - hi is exact in fp32 and one dot2 forms it: hi_pair . (-1, 0)
           // + p for the even element, . (0, -1) + p for the odd one.  The
@@ -774,7 +830,7 @@ int64_t tiles_upper_bound(int num_seqs, int64_t total_q, int group) {
 template <int KV_DT, bool PAGED, bool QSPLIT>
 int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   using LT = LdsTile<KV_DT>;
-  const size_t lds = 4 * LT::kBytes + (kRowsPerWg + 2) * sizeof(int);
+  const size_t lds = 4 * LT::kBytes + (kRowsPerWg + 4) * sizeof(int) + 2 * 128 * sizeof(float);
   int64_t nwg = a.tiles_ub * a.num_kv_heads;
   nwg = ((nwg + kXcds - 1) / kXcds) * kXcds;
   hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED, QSPLIT>), dim3((unsigned)nwg), dim3(kPfThreads), lds,
@@ -813,7 +869,8 @@ int check_common(int num_seqs, int64_t total_q, int num_heads, int num_kv_heads,
   if (g < 1 || g > 16) return MKV_ERR_UNSUPPORTED_GROUP;
   if (q_dtype != MKV_DTYPE_F32 && q_dtype != MKV_DTYPE_BF16 && q_dtype != MKV_DTYPE_F16)
     return MKV_ERR_UNSUPPORTED_DTYPE;
-  if (kv_dtype != MKV_DTYPE_BF16 && kv_dtype != MKV_DTYPE_F16 && kv_dtype != MKV_DTYPE_FP8E4M3)
+  if (kv_dtype != MKV_DTYPE_BF16 && kv_dtype != MKV_DTYPE_F16 && kv_dtype != MKV_DTYPE_FP8E4M3 &&
+      kv_dtype != MKV_DTYPE_I8)
     return MKV_ERR_UNSUPPORTED_DTYPE;
   return MKV_OK;
 }
@@ -831,8 +888,17 @@ int dispatch_prefill(PrefillArgs& a, int kv_dtype, void* workspace, size_t works
   hipLaunchKernelGGL(prefill_tile_scan_kernel, dim3(1), dim3(256), 0, s, a.cu_seqlens_q,
                      PAGED ? a.context_lens : nullptr, a.ctx_i64, ctx_cap, a.num_seqs, a.tok_per_wg,
                      a.tile_start, order);
+  const bool q16 = a.q_dtype == MKV_DTYPE_BF16;
   switch (kv_dtype) {
     case MKV_DTYPE_FP8E4M3: return launch_prefill<MKV_DTYPE_FP8E4M3, PAGED, false>(a, s);
+    case kKvFp8PerToken:
+      if constexpr (PAGED)
+        return q16 ? launch_prefill<kKvFp8PerToken, true, false>(a, s) : launch_prefill<kKvFp8PerToken, true, true>(a, s);
+      return MKV_ERR_UNSUPPORTED_DTYPE;
+    case kKvI8PerToken:
+      if constexpr (PAGED)
+        return q16 ? launch_prefill<kKvI8PerToken, true, false>(a, s) : launch_prefill<kKvI8PerToken, true, true>(a, s);
+      return MKV_ERR_UNSUPPORTED_DTYPE;
     case MKV_DTYPE_BF16:
       return a.q_dtype == MKV_DTYPE_BF16 ? launch_prefill<MKV_DTYPE_BF16, PAGED, false>(a, s)
                                          : launch_prefill<MKV_DTYPE_BF16, PAGED, true>(a, s);
@@ -857,9 +923,14 @@ extern "C" int mkv_paged_prefill(void* out, const void* q, int q_dtype, const vo
   if (!out || !q || !k_cache || !v_cache || !block_tables || !context_lens || !cu_seqlens_q ||
       !positions)
     return MKV_ERR_NULL_POINTER;
-  if (kv_dtype == MKV_DTYPE_FP8E4M3 && kv_scale_mode != MKV_SCALE_PER_TENSOR)
+  // FP8: per-tensor or per-token-head scales; INT8: per-token-head only
+  int fmt = kv_dtype;
+  if (kv_scale_mode == MKV_SCALE_PER_TOKEN_HEAD && (kv_dtype == MKV_DTYPE_FP8E4M3 || kv_dtype == MKV_DTYPE_I8))
+    fmt = kv_dtype == MKV_DTYPE_I8 ? kKvI8PerToken : kKvFp8PerToken;
+  else if (kv_dtype == MKV_DTYPE_I8 || (kv_dtype == MKV_DTYPE_FP8E4M3 && kv_scale_mode != MKV_SCALE_PER_TENSOR))
     return MKV_ERR_UNSUPPORTED_DTYPE;
-  if (kv_dtype == MKV_DTYPE_FP8E4M3 && (!k_scale || !v_scale)) return MKV_ERR_NULL_POINTER;
+  if ((kv_dtype == MKV_DTYPE_FP8E4M3 || kv_dtype == MKV_DTYPE_I8) && (!k_scale || !v_scale))
+    return MKV_ERR_NULL_POINTER;
   if (context_lens_dtype != MKV_INDEX_I32 && context_lens_dtype != MKV_INDEX_I64)
     return MKV_ERR_UNSUPPORTED_DTYPE;
   const int bs_log2 = ilog2_exact(block_size);
@@ -892,7 +963,7 @@ extern "C" int mkv_paged_prefill(void* out, const void* q, int q_dtype, const vo
   a.num_kv_heads = num_kv_heads;
   a.group = num_heads / num_kv_heads;
   a.sm_scale = sm_scale;
-  return dispatch_prefill<true>(a, kv_dtype, workspace, workspace_bytes,
+  return dispatch_prefill<true>(a, fmt, workspace, workspace_bytes,
                                 reinterpret_cast<hipStream_t>(stream));
 }
 

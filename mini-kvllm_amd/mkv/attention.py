@@ -417,15 +417,13 @@ def paged_attention_prefill_triton(query: torch.Tensor, k_cache: torch.Tensor,
 
     Row i of sequence s attends to logical tokens [0, min(context_lens[s],
     positions[i] + 1)).  The name is kept for drop-in compatibility with
-    attention.py:852-891; the work runs on the gfx950 MFMA kernel.  With an
-    FP8 cache pass k_scale/v_scale (kv_cache_dtype='fp8_per_tensor'), which
-    the reference does not implement (attention.py:1702-1708).  Per-token-head
-    caches raise NotImplementedError here, as in the reference.
+    attention.py:852-891; the work runs on the gfx950 MFMA kernel.  Quantised
+    caches, which the reference's prefill does not implement
+    (attention.py:1702-1708), take k_scale/v_scale: kv_cache_dtype
+    'fp8_per_tensor' with (1,) scales, or 'fp8_per_token_head' /
+    'int8_per_token_head' with (num_blocks, block_size, num_kv_heads) scales
+    (the decode path's formats, attention.py:1124-1210).
     """
-    if kv_cache_dtype in PER_TOKEN_HEAD_MODES or k_cache.dtype == torch.int8:
-        raise NotImplementedError(
-            "chunked prefill for per-token-head quantized KV cache needs a dequantizing paged "
-            "prefill/extend attention path")
     dev = _require_gpu(query, k_cache, v_cache, block_tables, context_lens, cu_seqlens_q,
                        positions)
     query = query.contiguous()
@@ -434,8 +432,16 @@ def paged_attention_prefill_triton(query: torch.Tensor, k_cache: torch.Tensor,
     if total_q == 0:
         return out
     _check_cache(k_cache, v_cache, num_kv_heads, head_dim)
-    fp8 = k_cache.dtype == torch.float8_e4m3fn
-    if fp8:
+    quant = k_cache.dtype in (torch.float8_e4m3fn, torch.int8)
+    per_token = kv_cache_dtype in PER_TOKEN_HEAD_MODES
+    if per_token:
+        want = torch.int8 if kv_cache_dtype == "int8_per_token_head" else torch.float8_e4m3fn
+        if k_cache.dtype != want:
+            raise TypeError(f"{kv_cache_dtype} needs a {want} cache, got {k_cache.dtype}")
+        _check_token_scales(k_scale, v_scale, k_cache)
+    elif k_cache.dtype == torch.int8:
+        raise ValueError("an int8 cache needs kv_cache_dtype='int8_per_token_head' and its scales")
+    elif quant:
         if kv_cache_dtype not in ("fp8_per_tensor", "auto") or k_scale is None or v_scale is None:
             raise ValueError("an fp8 cache needs kv_cache_dtype='fp8_per_tensor' and k_scale/v_scale")
     bt = _block_table(block_tables)
@@ -449,8 +455,9 @@ def paged_attention_prefill_triton(query: torch.Tensor, k_cache: torch.Tensor,
     _lib.call(
         "mkv_paged_prefill", out.data_ptr(), query.data_ptr(), _dtype_code(query, "query"),
         k_cache.data_ptr(), v_cache.data_ptr(), _dtype_code(k_cache, "k_cache"), k_cache.shape[0],
-        k_scale.data_ptr() if fp8 else None, v_scale.data_ptr() if fp8 else None,
-        _lib.SCALE_PER_TENSOR, bt.data_ptr(), bt.stride(0), bt.shape[1], cl.data_ptr(), _index_dtype(cl), cu.data_ptr(), pos.data_ptr(),
+        k_scale.data_ptr() if quant else None, v_scale.data_ptr() if quant else None,
+        _lib.SCALE_PER_TOKEN_HEAD if per_token else _lib.SCALE_PER_TENSOR,
+        bt.data_ptr(), bt.stride(0), bt.shape[1], cl.data_ptr(), _index_dtype(cl), cu.data_ptr(), pos.data_ptr(),
         num_seqs, total_q, num_heads, num_kv_heads, head_dim, k_cache.shape[1], float(scale),
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
         _stream(dev))
@@ -569,11 +576,11 @@ class Attention(nn.Module):
                                       self.block_size)
 
     def _prefill(self, q, block_tables, context_lens, cu_seqlens_q, positions, scale):
-        fp8 = self._mode() == "fp8_per_tensor"
+        quant = self._mode() != "auto"
         return paged_attention_prefill_triton(
             q, self.k_cache, self.v_cache, block_tables, context_lens, cu_seqlens_q, positions,
             scale, self.num_heads, self.num_kv_heads, self.head_dim, self.block_size,
-            k_scale=self.k_scale if fp8 else None, v_scale=self.v_scale if fp8 else None,
+            k_scale=self.k_scale if quant else None, v_scale=self.v_scale if quant else None,
             kv_cache_dtype=self.kv_cache_dtype)
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
@@ -608,10 +615,6 @@ class Attention(nn.Module):
                 o = flash_attention_prefill(q, k, v, cu_seqlens, scale, self.num_heads,
                                             self.num_kv_heads, self.head_dim)
                 return o.reshape(o.shape[0], self.num_heads * self.head_dim)
-            if mode in PER_TOKEN_HEAD_MODES:  # as the reference, attention.py:1702-1708
-                raise NotImplementedError(
-                    "chunked prefill for quantized KV cache needs a dequantizing paged "
-                    "prefill/extend attention path")
             if context.positions is None or context.context_lens is None or context.block_tables is None:
                 raise ValueError("paged prefill requires positions, context_lens, and block_tables")
             split = context.mixed_attention_split

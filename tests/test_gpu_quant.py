@@ -9,6 +9,10 @@ Decode (reference tile kernel attention.py:1124-1210): the oracle runs on the
 very codes and scales the kernel reads, so the only difference is arithmetic:
 2e-3 absolute plus half an output ulp (tighter than the 2e-2 allowed for FP8
 KV against unquantised values).
+
+Chunked prefill over the same caches (an extension; the reference's prefill
+raises for quantised caches): the operator and the Attention layer's mixed
+batch, against the oracle on the same codes and scales, with the same bound.
 """
 from __future__ import annotations
 
@@ -284,3 +288,93 @@ def test_attention_layer_per_token_decode_step(dev, mode):
                                               1 / math.sqrt(128), Hq, Hkv, 128, bs, mode)
     assert torch.equal(out, want.reshape(B, Hq * 128))
     assert torch.equal(_u8(layer.k_cache), _u8(kc2)) and torch.equal(_u8(layer.v_scale), _u8(vs2))
+
+
+# ---------------------------------------------------------------------------
+# Chunked prefill over per-token-head caches (an extension: the reference's
+# prefill raises for quantised caches, attention.py:1702-1708; the decode
+# path's per-token arithmetic, attention.py:1124-1210, applied per key).
+# ---------------------------------------------------------------------------
+def _prefill_case(seed, mode, prior, qlen, Hq, Hkv, bs, qdt=torch.bfloat16, holes=()):
+    g = torch.Generator().manual_seed(seed)
+    ctx = torch.tensor([p + n for p, n in zip(prior, qlen)], dtype=torch.int64)
+    N = sum((int(c) + bs - 1) // bs for c in ctx) + 3
+    bt = W.fragmented_block_tables(ctx, bs, N, g)
+    for s, j in holes:
+        bt[s, j] = -1
+    cu = torch.zeros(len(qlen) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(qlen), 0).to(torch.int32)
+    pos = torch.tensor([p + j for p, n in zip(prior, qlen) for j in range(n)], dtype=torch.int64)
+    q = torch.randn(int(cu[-1]), Hq, 128, generator=g).to(qdt)
+    kq, vq, ks, vs = _quant_pool(g, mode, N, bs, Hkv)
+    return q, kq, vq, ks, vs, bt, ctx, cu, pos
+
+
+def _prefill_gpu(dev, mode, q, kq, vq, ks, vs, bt, ctx, cu, pos, scale, Hq, Hkv):
+    out = A.paged_attention_prefill_triton(
+        q.to(dev), kq.to(dev), vq.to(dev), bt.to(dev), ctx.to(dev), cu.to(dev), pos.to(dev), scale,
+        Hq, Hkv, 128, kq.shape[1], k_scale=ks.to(dev), v_scale=vs.to(dev), kv_cache_dtype=mode)
+    return out.cpu()
+
+
+@pytest.mark.parametrize("mode", [FP8_MODE, INT8_MODE])
+@pytest.mark.parametrize("group", [1, 4, 16])
+@pytest.mark.parametrize("qdt", [torch.bfloat16, torch.float32])
+def test_per_token_prefill_matches_oracle(dev, mode, group, qdt):
+    announce(f"per-token prefill {mode} group {group} q {qdt}")
+    Hkv = 2
+    q, kq, vq, ks, vs, bt, ctx, cu, pos = _prefill_case(30 + group, mode, [0, 37, 130, 5],
+                                                        [70, 33, 1, 200], Hkv * group, Hkv, 32, qdt)
+    sc = 1 / math.sqrt(128)
+    got = _prefill_gpu(dev, mode, q, kq, vq, ks, vs, bt, ctx, cu, pos, sc, Hkv * group, Hkv)
+    want = R.paged_prefill_ref(q.double(), kq, vq, bt, ctx, cu, pos, sc, Hkv * group, Hkv, ks, vs)
+    assert_close_out(got, want, got.dtype, TOL)
+
+
+@pytest.mark.parametrize("mode", [FP8_MODE, INT8_MODE])
+@pytest.mark.parametrize("bs", [16, 256])
+def test_per_token_prefill_block_sizes_holes_and_context_caps(dev, mode, bs):
+    announce(f"per-token prefill {mode} bs {bs} holes")
+    q, kq, vq, ks, vs, bt, ctx, cu, pos = _prefill_case(40 + bs, mode, [3, 0, 300], [129, 64, 17],
+                                                        8, 2, bs, holes=[(2, 0)])
+    ctx2 = ctx.clone()
+    ctx2[0] = 50  # context shorter than some positions: visible = min(ctx, pos + 1)
+    got = _prefill_gpu(dev, mode, q, kq, vq, ks, vs, bt, ctx2, cu, pos, 0.1, 8, 2)
+    want = R.paged_prefill_ref(q.double(), kq, vq, bt, ctx2, cu, pos, 0.1, 8, 2, ks, vs)
+    assert_close_out(got, want, got.dtype, TOL)
+
+
+@pytest.mark.parametrize("mode", [FP8_MODE, INT8_MODE])
+@pytest.mark.parametrize("route", ["unified", "split"])
+def test_attention_layer_per_token_mixed_batch(dev, mode, route):
+    """Attention.forward on a mixed batch (prefill chunks and decode rows,
+    K/V already in the cache) in a per-token-head mode, both routes, against
+    the oracle over every row."""
+    announce(f"Attention layer per-token mixed batch, {mode}, {route}")
+    from mkv import context as C
+    Hq, Hkv, bs = 16, 4, 16
+    prior, qlen = [40, 200, 7, 0, 120, 33], [1, 48, 1, 90, 1, 1]
+    q, kq, vq, ks, vs, bt, ctx, cu, pos = _prefill_case(50, mode, prior, qlen, Hq, Hkv, bs)
+    is_dec = [n == 1 for n in qlen]
+    split = C.split_mixed_decode_prefill_metadata(cu.tolist(), qlen, is_dec)
+    for name in ("decode_token_indices", "decode_seq_indices", "prefill_token_indices",
+                 "prefill_seq_indices"):
+        setattr(split, name + "_tensor", torch.tensor(getattr(split, name), device=dev))
+    split.prefill_cu_seqlens_q_tensor = torch.tensor(split.prefill_cu_seqlens_q, dtype=torch.int32,
+                                                     device=dev)
+    layer = A.Attention(Hq, 128, scale=1.0, num_kv_heads=Hkv, block_size=bs)
+    layer.k_cache, layer.v_cache = kq.to(dev), vq.to(dev)
+    layer.k_scale, layer.v_scale = ks.to(dev), vs.to(dev)
+    layer.kv_cache_dtype = mode
+    layer.mixed_batch = route
+    C.set_context(True, cu_seqlens_q=cu.to(dev), max_seqlen_q=max(qlen), slot_mapping=None,
+                  context_lens=ctx.to(dev), block_tables=bt.to(dev), positions=pos.to(dev),
+                  mixed_attention_split=split, is_full_prefill=False)
+    try:
+        qd = q.to(dev)
+        out = layer(qd, qd, qd, kv_appended=True).cpu().view(-1, Hq, 128)
+    finally:
+        C.reset_context()
+    want = R.paged_prefill_ref(q.double(), kq, vq, bt, ctx, cu, pos, 1 / math.sqrt(128), Hq, Hkv,
+                               ks, vs)
+    assert_close_out(out, want, out.dtype, TOL)

@@ -142,9 +142,10 @@ def test_wrappers_reject_cpu_tensors_and_unimplemented_modes():
     with pytest.raises(ValueError, match="unknown"):
         A.paged_attention_decode_quantized(k, kc, kc, None, None, None, None, 0.1, 8, 8, 128, 16,
                                            "fp4")
-    with pytest.raises(NotImplementedError):
-        A.paged_attention_prefill_triton(k, kc, kc, None, None, None, None, 0.1, 8, 8, 128, 16,
-                                         kv_cache_dtype="fp8_per_token_head")
+    bt, cl, cu = torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.int64), torch.tensor([0, 2])
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        A.paged_attention_prefill_triton(k, kc, kc, bt, cl, cu, torch.zeros(2, dtype=torch.int64), 0.1,
+                                         8, 8, 128, 16, kv_cache_dtype="fp8_per_token_head")
     with pytest.raises(AssertionError):
         A.store_kvcache(k, k, kc, torch.zeros(2, 16, 8, 128), slots, 16)
     with pytest.raises(AssertionError):
