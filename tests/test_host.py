@@ -101,13 +101,17 @@ def test_argument_validation_without_launch():
     bad = list(prod)
     bad[27] = 4
     assert lib.mkv_qkv_norm_rope_append(*bad) == -2
-    # per-token-head scales are not accepted by the prefill kernel
-    pre = [p, p, 1, p, p, 3, 10, p, p, 1, p, 4, 4, p, 1, p, p, 1, 4, 32, 8, 128, 256, 0.1,
+    # prefill scale modes: FP8 takes per-tensor or per-token-head scales,
+    # INT8 only per-token-head ones, and a quantised cache needs both scales
+    pre = [p, p, 1, p, p, 3, 10, p, p, 7, p, 4, 4, p, 1, p, p, 1, 4, 32, 8, 128, 256, 0.1,
            p, 1 << 20, nul]
+    assert lib.mkv_paged_prefill(*pre) == -3  # unknown scale mode
+    pre[5], pre[9] = 4, 0  # INT8 with a per-tensor scale
     assert lib.mkv_paged_prefill(*pre) == -3
-    pre[2 + 3] = 4  # an INT8 cache
-    pre[9] = 0
-    assert lib.mkv_paged_prefill(*pre) == -3
+    pre[9], pre[7] = 1, nul  # INT8 per token and head without its K scales
+    assert lib.mkv_paged_prefill(*pre) == -1
+    pre[5] = 3  # FP8 per token and head without its K scales
+    assert lib.mkv_paged_prefill(*pre) == -1
 
 
 def test_decode_workspace_and_split_queries():
