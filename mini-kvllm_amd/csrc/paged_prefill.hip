@@ -37,6 +37,9 @@ constexpr int kPfThreads = kPfWaves * kWave;
 constexpr int kRowTiles = 1;                       // 16-row MFMA tiles per wave
 constexpr int kRowsPerWg = kPfWaves * kRowTiles * 16;  // 128
 constexpr int kBN = 64;                            // keys per LDS tile
+// dynamic LDS: 4 tiles of 64 keys x 256 bytes, row visibility [128] + 4
+// ints, per-token scales [2][128], then the inline tile list (8-aligned)
+constexpr int kTileListOffset = 4 * kBN * 256 + (128 + 4) * 4 + 2 * 128 * 4;
 constexpr int kXcds = 8;
 constexpr float kNegBig = -1e30f;
 constexpr float kRescaleSlack = 8.0f;
@@ -63,6 +66,7 @@ struct PrefillArgs {
   float sm_scale;
   int32_t* tile_start;  // [num_seqs + 1], over the visiting order
   const int32_t* order; // [num_seqs]: sequence visited at position k
+  int inline_list;      // num_seqs <= kInlineSeqs: each workgroup builds the list in LDS
   int64_t tiles_ub;     // upper bound of tiles per KV head (grid rows)
 };
 
@@ -76,73 +80,107 @@ struct PrefillArgs {
 // of more than 256 sequences keep their own order.  The order changes which
 // workgroup computes a tile, never the tile's result.
 // ---------------------------------------------------------------------------
+// Up to kInlineSeqs sequences: the list is built in LDS (by the scan kernel,
+// or by every prefill workgroup itself, which saves the scan launch and the
+// global lookups of the tile's sequence).
+constexpr int kInlineSeqs = 256;
+struct TileListLds {
+  int32_t part[kInlineSeqs];
+  int64_t key[kInlineSeqs];
+  int32_t ord[kInlineSeqs];
+  int32_t ts[kInlineSeqs + 1];   // tile prefix over the visiting order
+  int32_t cu[kInlineSeqs + 1];   // cu_seqlens_q
+  int32_t ctx[kInlineSeqs];      // clamped context lengths (paged)
+};
+
+// Builds the list of n <= kInlineSeqs sequences in L with one coalesced
+// round trip for cu_seqlens_q and context_lens; the first kInlineSeqs
+// threads do the per-sequence work, and every thread of the workgroup must
+// call it (it holds barriers).
+MKV_DEV void build_tile_list(TileListLds& L, const int32_t* __restrict__ cu, const void* context_lens,
+                             int ctx_i64, int64_t ctx_cap, int n, int tok_per_wg) {
+  const int t = threadIdx.x;
+  if (t <= n) L.cu[t] = cu[t];
+  if (t < n) {
+    int64_t c = context_lens ? load_index(context_lens, t, ctx_i64) : 0;
+    c = c < 0 ? 0 : (c > ctx_cap ? ctx_cap : c);
+    L.ctx[t] = (int32_t)(c < 0x7fffffff ? c : 0x7fffffff);
+  }
+  __syncthreads();
+  int64_t kk = -1;
+  if (t < n) {
+    const int32_t len = L.cu[t + 1] - L.cu[t];
+    if (len > 0) kk = context_lens ? L.ctx[t] : len;
+    L.key[t] = kk;
+  }
+  __syncthreads();
+  if (t < n) {  // stable rank, longest first
+    int r = 0;
+    for (int j = 0; j < n; ++j) {
+      const int64_t kj = L.key[j];
+      r += (kj > kk) || (kj == kk && j < t);
+    }
+    L.ord[r] = t;
+  }
+  __syncthreads();
+  const int s = t < n ? L.ord[t] : 0;
+  const int32_t len = t < n ? L.cu[s + 1] - L.cu[s] : 0;
+  const int32_t nt = len > 0 ? (len + tok_per_wg - 1) / tok_per_wg : 0;
+  if (t < kInlineSeqs) L.part[t] = nt;
+  __syncthreads();
+  for (int off = 1; off < kInlineSeqs; off <<= 1) {  // Hillis-Steele inclusive scan
+    const int32_t add = t < kInlineSeqs && t >= off ? L.part[t - off] : 0;
+    __syncthreads();
+    if (t < kInlineSeqs) L.part[t] += add;
+    __syncthreads();
+  }
+  if (t < n) L.ts[t] = L.part[t] - nt;
+  if (t == 0) L.ts[n] = L.part[kInlineSeqs - 1];
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Tile list kernel (batches of more than kInlineSeqs sequences, in batch
+// order; smaller ones only when a caller asks for the global list).
+// ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void prefill_tile_scan_kernel(const int32_t* __restrict__ cu,
                                                                 const void* context_lens, int ctx_i64,
                                                                 int64_t ctx_cap, int num_seqs,
                                                                 int tok_per_wg,
                                                                 int32_t* __restrict__ tile_start,
                                                                 int32_t* __restrict__ order) {
-  __shared__ int32_t part[256];
-  __shared__ int64_t key[256];
-  __shared__ int32_t ord[256];
+  __shared__ TileListLds L;
   const int t = threadIdx.x;
-  auto tiles_of = [&](int s) {
-    const int32_t len = cu[s + 1] - cu[s];
-    return len > 0 ? (len + tok_per_wg - 1) / tok_per_wg : 0;
-  };
-  auto scan = [&](int32_t n) {  // Hillis-Steele inclusive scan of part[]
-    part[t] = n;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-      const int32_t add = t >= off ? part[t - off] : 0;
-      __syncthreads();
-      part[t] += add;
-      __syncthreads();
-    }
-  };
-  if (num_seqs <= 256) {
-    int64_t kk = -1;
+  if (num_seqs <= kInlineSeqs) {
+    build_tile_list(L, cu, context_lens, ctx_i64, ctx_cap, num_seqs, tok_per_wg);
     if (t < num_seqs) {
-      if (cu[t + 1] > cu[t]) {
-        if (context_lens) {
-          const int64_t c = load_index(context_lens, t, ctx_i64);
-          kk = c < 0 ? 0 : (c > ctx_cap ? ctx_cap : c);
-        } else {
-          kk = cu[t + 1] - cu[t];
-        }
-      }
-      key[t] = kk;
+      tile_start[t] = L.ts[t];
+      order[t] = L.ord[t];
     }
-    __syncthreads();
-    if (t < num_seqs) {  // stable rank, longest first
-      int r = 0;
-      for (int j = 0; j < num_seqs; ++j) {
-        const int64_t kj = key[j];
-        r += (kj > kk) || (kj == kk && j < t);
-      }
-      ord[r] = t;
-    }
-    __syncthreads();
-    const int s = t < num_seqs ? ord[t] : 0;
-    const int32_t n = t < num_seqs ? tiles_of(s) : 0;
-    scan(n);
-    if (t < num_seqs) {
-      tile_start[t] = part[t] - n;
-      order[t] = s;
-    }
-    if (t == 0) tile_start[num_seqs] = part[255];
+    if (t == 0) tile_start[num_seqs] = L.ts[num_seqs];
     return;
   }
   int32_t running = 0;
   for (int base = 0; base < num_seqs; base += 256) {
     const int s = base + t;
-    const int32_t n = s < num_seqs ? tiles_of(s) : 0;
-    scan(n);
+    int32_t n = 0;
     if (s < num_seqs) {
-      tile_start[s] = running + part[t] - n;
+      const int32_t len = cu[s + 1] - cu[s];
+      n = len > 0 ? (len + tok_per_wg - 1) / tok_per_wg : 0;
+    }
+    L.part[t] = n;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {  // Hillis-Steele inclusive scan
+      const int32_t add = t >= off ? L.part[t - off] : 0;
+      __syncthreads();
+      L.part[t] += add;
+      __syncthreads();
+    }
+    if (s < num_seqs) {
+      tile_start[s] = running + L.part[t] - n;
       order[s] = s;
     }
-    running += part[255];
+    running += L.part[255];
     __syncthreads();
   }
   if (t == 0) tile_start[num_seqs] = running;
@@ -287,6 +325,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   int* red_lds = vis_lds + kRowsPerWg;                             // [2]
   // per-token-head scales of the staged tiles: [buffer][K keys 0..63, V keys 0..63]
   float* sc_lds = reinterpret_cast<float*>(red_lds + 4);
+  static_assert(kTileListOffset == 4 * LT::kBytes + (kRowsPerWg + 4) * 4 + 2 * 128 * 4, "LDS layout");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -303,30 +342,45 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const int kvh = (int)(logical / a.tiles_ub);
   const int64_t tau = logical - (int64_t)kvh * a.tiles_ub;
   if (kvh >= a.num_kv_heads) return;
-  const int32_t total_tiles = a.tile_start[a.num_seqs];
-  if (tau >= total_tiles) return;
-  int lo = 0, hi = a.num_seqs;  // largest k with tile_start[k] <= tau
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (a.tile_start[mid] <= tau) lo = mid; else hi = mid;
+  const int64_t cap = PAGED ? (int64_t)a.idx.max_blocks << a.idx.bs_log2 : 0;
+  int seq;
+  int64_t q_seq0, q_seq1, tile, ctx;
+  if (a.inline_list) {
+    TileListLds& L = *reinterpret_cast<TileListLds*>(smem + kTileListOffset);
+    build_tile_list(L, a.cu_seqlens_q, PAGED ? a.context_lens : nullptr, a.ctx_i64, cap, a.num_seqs,
+                    a.tok_per_wg);
+    if (tau >= L.ts[a.num_seqs]) return;
+    int lo = 0, hi = a.num_seqs;  // largest k with ts[k] <= tau
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (L.ts[mid] <= tau) lo = mid; else hi = mid;
+    }
+    seq = L.ord[lo];
+    q_seq0 = L.cu[seq];
+    q_seq1 = L.cu[seq + 1];
+    tile = (int64_t)(L.ts[lo + 1] - 1) - tau;  // the sequence's last tile first
+    ctx = PAGED ? (int64_t)L.ctx[seq] : q_seq1 - q_seq0;
+  } else {
+    if (tau >= a.tile_start[a.num_seqs]) return;
+    int lo = 0, hi = a.num_seqs;  // largest k with tile_start[k] <= tau
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (a.tile_start[mid] <= tau) lo = mid; else hi = mid;
+    }
+    seq = a.order[lo];
+    q_seq0 = a.cu_seqlens_q[seq];
+    q_seq1 = a.cu_seqlens_q[seq + 1];
+    tile = (int64_t)(a.tile_start[lo + 1] - 1) - tau;  // the sequence's last tile first
+    if constexpr (PAGED) {
+      ctx = load_index(a.context_lens, seq, a.ctx_i64);
+      ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+    } else {
+      ctx = q_seq1 - q_seq0;
+    }
   }
-  const int seq = a.order[lo];
-  const int64_t q_seq0 = a.cu_seqlens_q[seq];
-  const int64_t q_seq1 = a.cu_seqlens_q[seq + 1];
-  // the sequence's last tile first
-  const int64_t tile = (int64_t)(a.tile_start[lo + 1] - 1) - tau;
   const int64_t q0 = q_seq0 + tile * (int64_t)a.tok_per_wg;
   const int64_t q1 = q0 + a.tok_per_wg < q_seq1 ? q0 + a.tok_per_wg : q_seq1;
   const int G = a.group;
-
-  int64_t ctx;
-  if constexpr (PAGED) {
-    ctx = load_index(a.context_lens, seq, a.ctx_i64);
-    const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
-    ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
-  } else {
-    ctx = q_seq1 - q_seq0;
-  }
 
   // Visible length of every row (0 for padding rows), and the WG's min / max.
   if (tid < kRowsPerWg) {
@@ -830,7 +884,7 @@ int64_t tiles_upper_bound(int num_seqs, int64_t total_q, int group) {
 template <int KV_DT, bool PAGED, bool QSPLIT>
 int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   using LT = LdsTile<KV_DT>;
-  const size_t lds = 4 * LT::kBytes + (kRowsPerWg + 4) * sizeof(int) + 2 * 128 * sizeof(float);
+  const size_t lds = kTileListOffset + (a.inline_list ? sizeof(TileListLds) : 0);
   int64_t nwg = a.tiles_ub * a.num_kv_heads;
   nwg = ((nwg + kXcds - 1) / kXcds) * kXcds;
   hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED, QSPLIT>), dim3((unsigned)nwg), dim3(kPfThreads), lds,
@@ -884,10 +938,13 @@ int dispatch_prefill(PrefillArgs& a, int kv_dtype, void* workspace, size_t works
   a.order = order;
   a.tok_per_wg = tok_per_wg_for(a.group);
   a.tiles_ub = tiles_upper_bound(a.num_seqs, a.total_q, a.group);
-  const int64_t ctx_cap = PAGED ? ((int64_t)a.idx.max_blocks << a.idx.bs_log2) : 0;
-  hipLaunchKernelGGL(prefill_tile_scan_kernel, dim3(1), dim3(256), 0, s, a.cu_seqlens_q,
-                     PAGED ? a.context_lens : nullptr, a.ctx_i64, ctx_cap, a.num_seqs, a.tok_per_wg,
-                     a.tile_start, order);
+  a.inline_list = a.num_seqs <= kInlineSeqs;
+  if (!a.inline_list) {
+    const int64_t ctx_cap = PAGED ? ((int64_t)a.idx.max_blocks << a.idx.bs_log2) : 0;
+    hipLaunchKernelGGL(prefill_tile_scan_kernel, dim3(1), dim3(256), 0, s, a.cu_seqlens_q,
+                       PAGED ? a.context_lens : nullptr, a.ctx_i64, ctx_cap, a.num_seqs, a.tok_per_wg,
+                       a.tile_start, order);
+  }
   const bool q16 = a.q_dtype == MKV_DTYPE_BF16;
   switch (kv_dtype) {
     case MKV_DTYPE_FP8E4M3: return launch_prefill<MKV_DTYPE_FP8E4M3, PAGED, false>(a, s);
