@@ -19,9 +19,10 @@
 //   O  += P V       (A = P straight from the S^T accumulators, B = V read
 //                    from LDS already transposed by ds_read_b64_tr_b16)
 // with an online softmax in the log2 domain whose output rescale is deferred
-// until a row's running max grows by more than 2^8.  The varlen tile list is
-// built on the device by a one-workgroup scan (longest sequences first, each
-// sequence's last tile first), so the launch needs no host sync; with a
+// until a row's running max grows by more than 2^8.  The varlen tile list
+// (longest sequences first, each sequence's last tile first) is built on the
+// device — by every workgroup in LDS for up to 256 sequences, else by a
+// one-workgroup scan kernel — so the launch needs no host sync; with a
 // multiple of 8 KV heads the grid is ordered so that all tiles of one KV head
 // run on one XCD and share its L2.
 #include <type_traits>
