@@ -526,9 +526,9 @@ class Attention(nn.Module):
     The runner injects ``k_cache``, ``v_cache``, ``k_scale``, ``v_scale`` and
     ``kv_cache_dtype`` ('auto', 'fp8_per_tensor', 'fp8_per_token_head' or
     'int8_per_token_head'), then sets the per-step
-    :class:`~mkv.context.Context`.  Unlike the reference, an FP8 per-tensor
-    cache also works for chunked / mixed prefill; per-token-head caches raise
-    there, as in the reference (attention.py:1702-1708).
+    :class:`~mkv.context.Context`.  Unlike the reference, which raises for
+    any quantised cache there (attention.py:1702-1708), FP8 per-tensor and
+    FP8 / INT8 per-token-head caches also work for chunked / mixed prefill.
     """
 
     def __init__(self, num_heads: int, head_dim: int, scale: float = 1.0,
