@@ -38,9 +38,10 @@ constexpr int kPfThreads = kPfWaves * kWave;
 constexpr int kRowTiles = 1;                       // 16-row MFMA tiles per wave
 constexpr int kRowsPerWg = kPfWaves * kRowTiles * 16;  // 128
 constexpr int kBN = 64;                            // keys per LDS tile
-// dynamic LDS: 4 tiles of 64 keys x 256 bytes, row visibility [128] + 4
-// ints, per-token scales [2][128], then the inline tile list (8-aligned)
-constexpr int kTileListOffset = 4 * kBN * 256 + (128 + 4) * 4 + 2 * 128 * 4;
+// static LDS: 4 tiles of 64 keys x 256 bytes (K and V, double-buffered);
+// dynamic LDS: row visibility [128] + 4 ints, per-token scales [2][128],
+// then the inline tile list (8-aligned)
+constexpr int kTileListOffset = (128 + 4) * 4 + 2 * 128 * 4;
 constexpr int kXcds = 8;
 constexpr float kNegBig = -1e30f;
 constexpr float kRescaleSlack = 8.0f;
@@ -319,14 +320,22 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   constexpr int kEbG = DTypeInfo<KV_DT>::kBytes;  // cache element bytes
   constexpr int kChunksG = kHeadDim * kEbG / 16;   // 16-byte chunks per cache row
   extern __shared__ __align__(16) char smem[];
-  // buffer b: K tile at smem + 2b*kBytes, V tile right after it
-#define KBUF(b) (smem + (b) * 2 * LT::kBytes)
-#define VBUF(b) (smem + (b) * 2 * LT::kBytes + LT::kBytes)
-  int* vis_lds = reinterpret_cast<int*>(smem + 4 * LT::kBytes);  // [kRowsPerWg]
+  // 16-bit caches stage tiles by LDS DMA into four distinct static buffers,
+  // indexed by compile-time constants (below): the compiler's wait-count pass
+  // then tells a read of one buffer from a pending DMA into the other and
+  // lets the DMA run on under the reads.  Converting formats index one array
+  // (buffer b: K at 2b tiles, V after it).
+  constexpr bool kDma = DTypeInfo<KV_DT>::kBytes == 2;
+  constexpr int kSplitBytes = kDma ? LT::kBytes : 16, kOneBytes = kDma ? 16 : 4 * LT::kBytes;
+  __shared__ __align__(16) char lds_k0[kSplitBytes], lds_v0[kSplitBytes], lds_k1[kSplitBytes], lds_v1[kSplitBytes];
+  __shared__ __align__(16) char lds_kv[kOneBytes];
+#define KBUF(b) (kDma ? ((b) ? lds_k1 : lds_k0) : lds_kv + (b) * 2 * LT::kBytes)
+#define VBUF(b) (kDma ? ((b) ? lds_v1 : lds_v0) : lds_kv + (b) * 2 * LT::kBytes + LT::kBytes)
+  int* vis_lds = reinterpret_cast<int*>(smem);  // [kRowsPerWg]
   int* red_lds = vis_lds + kRowsPerWg;                             // [2]
   // per-token-head scales of the staged tiles: [buffer][K keys 0..63, V keys 0..63]
   float* sc_lds = reinterpret_cast<float*>(red_lds + 4);
-  static_assert(kTileListOffset == 4 * LT::kBytes + (kRowsPerWg + 4) * 4 + 2 * 128 * 4, "LDS layout");
+  static_assert(kTileListOffset == (kRowsPerWg + 4) * 4 + 2 * 128 * 4, "LDS layout");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -550,6 +559,27 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     }
     return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, num, 0x00020000);
   };
+  // 16-bit caches: tiles go straight from HBM into LDS (buffer_load ... lds,
+  // 16 bytes per lane, no registers, no LDS write instructions).  One wave's
+  // load fills 1 KB = 4 key rows contiguously, lane l at byte 16l (key row
+  // l / 16, stored chunk l % 16), so lane l reads logical chunk
+  // (l % 16) ^ s(key) of its key; s has period 16 and each load's 4 rows
+  // start at a multiple of 4, so the offset is the same for every load.
+  static_assert(!kDma || (kSlotsPerLoad == 2 && kLoads == 4), "DMA slot layout");
+  const uint32_t ld_off_dma = (uint32_t)(ld_key * row_stride + 16 * (ld_ch ^ LT::swz(ld_key)));
+  const int dma_row = __builtin_amdgcn_readfirstlane(4 * (wave & 3) * LT::kRowBytes);
+  auto dma_tile = [&](int kb, const int64_t (&ph)[4], int buf) {
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+      const int j = ld_slot[u] & 3;  // slot = 2u + wave / 4: K for u < 2, V for u >= 2
+      const int64_t t0 = kb + 16 * j;
+      const int64_t phys = j == 0 ? ph[0] : (j == 1 ? ph[1] : (j == 2 ? ph[2] : ph[3]));
+      const __amdgpu_buffer_rsrc_t r = sub_rsrc(u >= 2 ? a.v : a.k, t0, phys);
+      const uint32_t off = (t0 + ld_key < max_vis) ? ld_off_dma : 0x80000000u;
+      char* dst = (u >= 2 ? VBUF(buf) : KBUF(buf)) + 16 * j * LT::kRowBytes + dma_row;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, off, 0, 0, 0);
+    }
+  };
   u32x4 stg[kLoads];
   // Per-token-head scales of a tile: lane tid < 128 loads the K (tid < 64) or
   // V scale of key tid % 64 (0 for keys past max_vis or in absent blocks;
@@ -631,6 +661,10 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     const int sw = LT::swz(key);
     vt_base = key * LT::kRowBytes + ((((q >> 1) ^ sw) & 1) << 4) + 8 * (q & 1);
     vt_swh = (sw >> 1) << 5;
+    // one opaque value: split into its terms, the address of a V read became
+    // a chain of GEPs too deep for the LDS alias-scope annotation, and a read
+    // without it waits for every pending LDS DMA
+    if constexpr (kDma) asm volatile("" : "+v"(vt_base));
   }
 
   const int n_tiles = (max_vis + kBN - 1) / kBN;
@@ -645,16 +679,31 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   int64_t ph_cur[4], ph_nxt[4];
   if (n_tiles > 0) {
     tile_blocks(0, ph_cur);
-    load_tile(0, ph_cur);
-    store_tile(0);
+    if constexpr (kDma) {
+      dma_tile(0, ph_cur, 0);
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    } else {
+      load_tile(0, ph_cur);
+      store_tile(0);
+    }
   }
   __syncthreads();
-  for (int it = 0; it < n_tiles; ++it) {
-    const int buf = it & 1;
+  // The DMA path takes two tiles per trip (the inner loop unrolls fully), so
+  // each buffer index is a compile-time constant.
+  constexpr int kPerTrip = kDma ? 2 : 1;
+  for (int it0 = 0; it0 < n_tiles; it0 += kPerTrip) {
+#pragma unroll
+  for (int h = 0; h < kPerTrip; ++h) {
+    const int it = it0 + h;
+    if (kDma && it >= n_tiles) break;
+    const int buf = kDma ? h : (it & 1);
     const int kb = it * kBN;
     if (it + 1 < n_tiles) {
       tile_blocks(kb + kBN, ph_nxt);
-      load_tile(kb + kBN, ph_nxt);
+      if constexpr (kDma)
+        dma_tile(kb + kBN, ph_nxt, buf ^ 1);
+      else
+        load_tile(kb + kBN, ph_nxt);
     }
     if (wave_active) {
 
@@ -831,10 +880,14 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     __builtin_amdgcn_s_setprio(0);
     }  // wave_active
 
-    if (it + 1 < n_tiles) store_tile(buf ^ 1);
+    if constexpr (kDma)
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's DMA has landed
+    else if (it + 1 < n_tiles)
+      store_tile(buf ^ 1);
 #pragma unroll
     for (int j = 0; j < 4; ++j) ph_cur[j] = ph_nxt[j];
     __syncthreads();
+  }
   }
 
 #undef KBUF
