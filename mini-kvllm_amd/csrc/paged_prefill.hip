@@ -13,7 +13,9 @@
 // GQA group) pair, token-major; every row of the group reads the same K/V,
 // so each K/V tile is staged in LDS once for G query heads.  Tiles of 64 keys
 // are gathered through the block table into double-buffered LDS with an XOR
-// swizzle on 16-byte chunks (every LDS access conflict-free).  Each wave
+// swizzle on 16-byte chunks (every LDS access conflict-free): 16-bit caches
+// by LDS DMA (buffer_load ... lds), FP8 / INT8 caches through registers,
+// converted on the way.  Each wave
 // owns one row tile of 16 and computes
 //   S^T = K Q^T     (A = K from LDS, B = Q^T resident in registers)
 //   O  += P V       (A = P straight from the S^T accumulators, B = V read
@@ -284,10 +286,11 @@ MKV_DEV int lane_id_volatile() {
 // s(key) = ((key & 7) << 1) | ((key >> 3) & 1) is a bijection on key mod 16
 // (K operand reads: 16 lanes, keys 16kt + c, one chunk) whose upper 3 bits
 // are a bijection on 8 consecutive keys (V transposed reads: 32 lanes, keys
-// 4kg + i, chunk pairs 2mm, 2mm + 1).  Staging writes of a 16-bit cache put
-// 16 chunks of one key in one go (writes go 8 lanes at a time, over 32
-// banks: 8 distinct chunks mod 8 under any s); an FP8 cache's chunk pairs are
-// split so that each write touches 8 distinct positions too.  The V
+// 4kg + i, chunk pairs 2mm, 2mm + 1).  A 16-bit cache's LDS DMA writes whole
+// 256-byte rows (the swizzle is applied to the global addresses instead); an
+// FP8 / INT8 cache's staging writes go 8 lanes at a time over 32 banks, and
+// its chunk pairs are split so that each write touches 8 distinct positions
+// mod 8.  The V
 // read offsets are computed for the first keys and reused 16 and 32 rows
 // further, the staging offsets 16-48 rows further: s has period 16.
 template <int KV_DT>
