@@ -763,16 +763,22 @@ paged_decode_mfma16_2w_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 // Stream-K decode (16-bit MFMA path, the default).
 //
-// The work is one global stream of 32-token tiles: sequence by sequence, KV
-// head by KV head, the ceil(L/32) tiles of every (sequence, KV head) item.
-// A persistent grid of W waves splits the stream into W equal contiguous
-// ranges, so every wave streams the same number of bytes whatever the
-// context-length skew, and its load pipeline runs across item boundaries
-// (the next tile's block-table entry and K/V are always in flight).  An item
-// cut by a range boundary writes (acc, m, l) partials to slot (wave, 0) if it
-// began at or before the wave's range, else (wave, 1); the merge kernel
-// combines them.  Sequences with no visible token are written as zeros by
-// the merge kernel.
+// The work is one global stream of columns: sequence by sequence, the
+// ceil(L/32) 32-token tiles of every sequence, each column standing for that
+// tile of all Hkv KV heads.  The persistent grid's W waves form W / Hkv
+// groups of Hkv consecutive waves; the groups split the column stream into
+// equal contiguous ranges, and wave k of a group computes KV head k of every
+// column in its group's range.  So every wave streams the same number of
+// bytes whatever the context-length skew, its load pipeline runs across item
+// boundaries (the next tile's block-table entry and K/V are always in
+// flight), and the Hkv heads' 128-byte slices of each 1 KB token row are read
+// by the Hkv waves of one group at about the same time (walking one head over
+// a long token range while the other heads of the same rows come much later
+// measured 4% slower on a pure read of the pool layout).  An item (sequence,
+// KV head) cut by a range boundary writes (acc, m, l) partials to slot
+// (wave, 0) if it began at or before the range, else (wave, 1); the merge
+// kernel combines them.  Sequences with no visible token are written as
+// zeros by the merge kernel.
 // ---------------------------------------------------------------------------
 constexpr int kTileTok = 32;
 constexpr int kStreamMaxBatch = 8192;
@@ -787,29 +793,28 @@ struct Cursor {
 
 MKV_DEV int lds_uniform(const int* p, int i) { return __builtin_amdgcn_readfirstlane(p[i]); }
 
-// Position of global tile g (pre: per-sequence tile prefix, lens: lengths).
-MKV_DEV Cursor cursor_at(const int* pre, const int* lens, int B, int Hkv, int64_t g) {
-  int lo = 0, hi = B;  // largest b with pre[b] * Hkv <= g; that b has tiles
+// Tile of KV head kvh at column g (pre: per-sequence tile prefix, lens:
+// lengths; g < pre[B]).
+MKV_DEV Cursor cursor_at(const int* pre, const int* lens, int B, int kvh, int64_t g) {
+  int lo = 0, hi = B;  // largest b with pre[b] <= g; that b has tiles
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
-    if ((int64_t)lds_uniform(pre, mid) * Hkv <= g) lo = mid; else hi = mid;
+    if (lds_uniform(pre, mid) <= g) lo = mid; else hi = mid;
   }
   Cursor c;
   c.b = lo;
+  c.kvh = kvh;
   const int p0 = lds_uniform(pre, lo);
   c.n = lds_uniform(pre, lo + 1) - p0;
-  const int64_t r = g - (int64_t)p0 * Hkv;
-  c.kvh = (int)(r / c.n);
-  c.t = (int)(r - (int64_t)c.kvh * c.n);
+  c.t = (int)(g - p0);
   c.L = lds_uniform(lens, lo);
   return c;
 }
 
-MKV_DEV void cursor_next(Cursor& c, const int* pre, const int* lens, int B, int Hkv) {
+// The next column of the same KV head.
+MKV_DEV void cursor_next(Cursor& c, const int* pre, const int* lens, int B) {
   if (++c.t < c.n) return;
   c.t = 0;
-  if (++c.kvh < Hkv) return;
-  c.kvh = 0;
   do {
     ++c.b;
   } while (c.b < B && lds_uniform(pre, c.b + 1) == lds_uniform(pre, c.b));
@@ -990,7 +995,7 @@ MKV_DEV void issue_finish(const FinishStores& f) {
 
 // Per-sequence tile counts and their prefix into LDS (every workgroup does it;
 // workgroup 0 also publishes them for the merge kernel).  Returns the total
-// number of tiles of the stream.
+// number of columns of the stream.
 MKV_DEV int64_t stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
   __shared__ int part[kDecWaves * kWave];
   const int tid = threadIdx.x;
@@ -1021,16 +1026,17 @@ MKV_DEV int64_t stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
   __syncthreads();
   if (blockIdx.x == 0)
     for (int i = tid; i <= a.batch; i += kDecWaves * kWave) a.sk_meta[i] = pre[i];
-  return (int64_t)running * a.num_kv_heads;
+  return running;
 }
 
-// Static split of the T tiles of the stream over the W waves: wave w runs the
-// contiguous range [begin(w), end(w)).  When two workgroups share each CU, the
-// two waves on a SIMD do not progress at the same rate: issue arbitration
-// favours the older wave, i.e. the one whose workgroup was dispatched in the
-// first round (workgroups 0 .. CUs-1).  Those first w1 waves therefore get
-// kFirstSharePct percent of the tiles and the second-round waves the rest;
-// with one workgroup per CU the split is even (w1 = W).
+// Static split of the T columns of the stream over the W / Hkv wave groups:
+// group w runs the contiguous range [begin(w), end(w)).  When two workgroups
+// share each CU, the two waves on a SIMD do not progress at the same rate:
+// issue arbitration favours the older wave, i.e. the one whose workgroup was
+// dispatched in the first round (workgroups 0 .. CUs-1).  The groups of those
+// waves (w1 of them) therefore get kFirstSharePct percent of the columns and
+// the second-round groups the rest; with one workgroup per CU the split is
+// even (w1 = W / Hkv).
 constexpr int kFirstSharePct = 58;
 
 struct StreamSplit {
@@ -1053,6 +1059,10 @@ struct StreamSplit {
     return g < base ? (int)(g / per1) : w1 + (int)((g - base) / per2);
   }
 };
+
+// The group split of a launch: groups of Hkv consecutive waves (waves past
+// the last whole group stay idle).
+MKV_DEV StreamSplit stream_split(const DecodeArgs& a, int64_t columns);
 
 MKV_DEV StreamSplit make_split(int64_t total, int waves, int first_waves) {
   StreamSplit p;
@@ -1078,19 +1088,28 @@ MKV_DEV StreamSplit make_split(int64_t total, int waves, int first_waves) {
   return p;
 }
 
+MKV_DEV StreamSplit stream_split(const DecodeArgs& a, int64_t columns) {
+  const int groups = a.num_waves / a.num_kv_heads;
+  const int first = a.first_waves >= a.num_waves ? groups : a.first_waves / a.num_kv_heads;
+  return make_split(columns, groups, first);
+}
+
 template <int KV_DT, bool kSmallGroup>
 MKV_DEV void stream_decode(const DecodeArgs& a) {
   constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
   extern __shared__ int sk_lds[];
   int* pre = sk_lds;                 // [batch + 1]
   int* lens = sk_lds + a.batch + 1;  // [batch]
-  const StreamSplit sp = make_split(stream_prefix(a, pre, lens), a.num_waves, a.first_waves);
+  const StreamSplit sp = stream_split(a, stream_prefix(a, pre, lens));
 
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
   const int w = blockIdx.x * kDecWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t g0 = sp.begin(w);
-  const int64_t g1 = sp.end(w);
+  const int grp = w / a.num_kv_heads;  // this wave: KV head w % Hkv of its group's columns
+  const int kvh = w - grp * a.num_kv_heads;
+  if (grp >= sp.waves) return;
+  const int64_t g0 = sp.begin(grp);
+  const int64_t g1 = sp.end(grp);
   if (g0 >= g1) return;
 
   const int row_bytes = (int)(a.idx.row_elems * kEb);
@@ -1100,7 +1119,7 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
   const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
   const float k_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.k_scale) : 1.0f;
 
-  Cursor cc = cursor_at(pre, lens, a.batch, a.num_kv_heads, g0);  // tile being computed
+  Cursor cc = cursor_at(pre, lens, a.batch, kvh, g0);  // tile being computed
   Cursor lc = cc;                                                  // next tile to load
   int64_t lg = g0;                                                 // its global index
   PhysPair ph_next;
@@ -1108,7 +1127,7 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
   // (L = 0: no bytes move), selected without a branch so that the load
   // stream stays unconditional and the wait-count pass never drains it.
   auto advance_load = [&]() {
-    cursor_next(lc, pre, lens, a.batch, a.num_kv_heads);
+    cursor_next(lc, pre, lens, a.batch);
     ++lg;
     lc.L = lg < g1 ? lc.L : 0;
     ph_next = tile_phys(a, lc);
@@ -1130,7 +1149,7 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
   float score_mul = 0.0f;
   f32x4 acc[8];
   float m_run = kNegBig, l_run = 0.0f;
-  int64_t item_g0 = g0 - cc.t;  // global index of the current item's first tile
+  int64_t item_g0 = g0 - cc.t;  // column of the current item's first tile
 
   // One pipeline step: prefetch tile g+1 into `nxt`, compute tile g in `cur`.
   auto step = [&](Tile16<KV_DT>& cur, Tile16<KV_DT>& nxt, int64_t g) {
@@ -1166,7 +1185,7 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
       l_col += __shfl_xor(l_col, 32);
       finish_sk(a, cc, whole, w, kslot, acc, m_run, l_col, v_mul);
     }
-    cursor_next(cc, pre, lens, a.batch, a.num_kv_heads);
+    cursor_next(cc, pre, lens, a.batch);
   };
   for (int64_t g = g0;;) {
     step(t0b, t1b, g);
@@ -1181,9 +1200,10 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(D
   stream_decode<KV_DT, kSmallGroup>(a);
 }
 
-// Per-token-head formats ask for the two-waves-per-SIMD register budget
-// explicitly: left to itself the scheduler takes a few registers more than
-// two waves can hold, and the residency halves.
+// Per-token-head formats (and per-tensor FP8 with groups above 4) ask for
+// the two-waves-per-SIMD register budget explicitly: left to itself the
+// scheduler takes a few registers more than two waves can hold, and the
+// residency halves.
 template <int KV_DT, bool kSmallGroup>
 __global__ __launch_bounds__(kDecWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
 paged_decode_stream_2w_kernel(DecodeArgs a) {
@@ -1192,20 +1212,23 @@ paged_decode_stream_2w_kernel(DecodeArgs a) {
 
 template <int KV_DT, bool kSmallGroup>
 constexpr auto stream_kernel() {
-  if constexpr (kPerTokenScale<KV_DT>)
+  // (per-tensor FP8 with groups above 4 lands a few registers past 256 on its own)
+  if constexpr (kPerTokenScale<KV_DT> || (KV_DT == MKV_DTYPE_FP8E4M3 && !kSmallGroup))
     return paged_decode_stream_2w_kernel<KV_DT, kSmallGroup>;
   else
     return paged_decode_stream_kernel<KV_DT, kSmallGroup>;
 }
 
 // Merge of stream-K partials: one wave per (sequence, query head).  The
-// partials of an item come from the consecutive waves wlo..whi, one slot each.
+// partials of an item (sequence, KV head kvh) come from wave kvh of the
+// consecutive groups glo..ghi, one slot each.
 // Lane i reads (m, l) of contributor wlo + i, so the maximum and the
 // denominator are wave reductions rather than a chain of dependent loads, and
 // the accumulator rows are read four contributors at a time (independent
 // loads in flight) with each contributor's weight taken from its lane.
-MKV_DEV int merge_slot(const DecodeArgs& a, const StreamSplit& sp, int64_t gs, int wp, int h) {
-  return ((wp * 2 + (gs <= sp.begin(wp) ? 0 : 1)) * a.group + h);
+MKV_DEV int merge_slot(const DecodeArgs& a, const StreamSplit& sp, int64_t gs, int grp, int kvh, int h) {
+  const int wp = grp * a.num_kv_heads + kvh;
+  return ((wp * 2 + (gs <= sp.begin(grp) ? 0 : 1)) * a.group + h);
 }
 
 __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_kernel(DecodeArgs a,
@@ -1217,26 +1240,25 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_ke
   const int hq = (int)(wv - (int64_t)b * a.num_heads);
   const int kvh = hq / a.group, h = hq - kvh * a.group;
   const int p0 = a.sk_meta[b], n = a.sk_meta[b + 1] - p0;
-  const StreamSplit sp = make_split((int64_t)a.sk_meta[a.batch] * a.num_kv_heads, a.num_waves,
-                                    a.first_waves);
+  const StreamSplit sp = stream_split(a, (int64_t)a.sk_meta[a.batch]);
   const int64_t off = (int64_t)b * a.out_stride + (int64_t)hq * kHeadDim + 2 * lane;
   float o0 = 0.0f, o1 = 0.0f, l = 0.0f;
   if (n > 0) {
-    const int64_t gs = (int64_t)p0 * a.num_kv_heads + (int64_t)kvh * n;
+    const int64_t gs = p0;  // the item's columns
     const int64_t ge = gs + n;
-    const int wlo = sp.wave_of(gs), whi = sp.wave_of(ge - 1);
-    if (wlo == whi) return;  // written whole by the main kernel
-    const int nc = whi - wlo + 1;
+    const int glo = sp.wave_of(gs), ghi = sp.wave_of(ge - 1);
+    if (glo == ghi) return;  // written whole by the main kernel
+    const int nc = ghi - glo + 1;
     float M = kNegBig;
     for (int c0 = 0; c0 < nc; c0 += kWave) {
-      if (c0 + lane < nc) M = fmaxf(M, a.ws_ml[(int64_t)merge_slot(a, sp, gs, wlo + c0 + lane, h) * 2]);
+      if (c0 + lane < nc) M = fmaxf(M, a.ws_ml[(int64_t)merge_slot(a, sp, gs, glo + c0 + lane, kvh, h) * 2]);
     }
     M = wave_max(M);
     for (int c0 = 0; c0 < nc; c0 += kWave) {
       int my_slot = 0;
       float wgt = 0.0f;
       if (c0 + lane < nc) {
-        my_slot = merge_slot(a, sp, gs, wlo + c0 + lane, h);
+        my_slot = merge_slot(a, sp, gs, glo + c0 + lane, kvh, h);
         wgt = __builtin_amdgcn_exp2f(a.ws_ml[(int64_t)my_slot * 2] - M);
         l += wgt * a.ws_ml[(int64_t)my_slot * 2 + 1];
       }
@@ -1590,7 +1612,10 @@ extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void*
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // the merge kernels apply the per-tensor V scale
   const bool fp8 = fmt == MKV_DTYPE_FP8E4M3;
-  if (split_tokens == 0 && kv_dtype != MKV_DTYPE_F32 && batch <= kStreamMaxBatch) {
+  // (stream-K needs a group of num_kv_heads waves, and a grid holds at least
+  // CUs x kDecWaves waves)
+  if (split_tokens == 0 && kv_dtype != MKV_DTYPE_F32 && batch <= kStreamMaxBatch &&
+      num_kv_heads <= device_cus() * kDecWaves) {
     // stream-K path
     const size_t need = stream_ws_bytes(batch, group);
     if (!workspace) return MKV_ERR_NULL_POINTER;
