@@ -618,8 +618,8 @@ def main() -> int:
                                args.split_tokens)
         schedule = f"split-K, {split}-token splits (paged_decode_mfma16_kernel + paged_decode_merge_kernel)"
     else:
-        schedule = ("stream-K over 32-token tiles, persistent grid "
-                    "(paged_decode_stream_kernel + paged_decode_stream_merge_kernel)")
+        schedule = ("stream-K over 32-token tile columns, persistent grid, groups of Hkv waves "
+                    "with one KV head per wave (paged_decode_stream_kernel + paged_decode_stream_merge_kernel)")
 
     result = {
         "metric": METRIC,
