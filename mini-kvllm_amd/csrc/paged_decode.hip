@@ -1249,42 +1249,82 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_ke
     const int glo = sp.wave_of(gs), ghi = sp.wave_of(ge - 1);
     if (glo == ghi) return;  // written whole by the main kernel
     const int nc = ghi - glo + 1;
-    float M = kNegBig;
-    for (int c0 = 0; c0 < nc; c0 += kWave) {
-      if (c0 + lane < nc) M = fmaxf(M, a.ws_ml[(int64_t)merge_slot(a, sp, gs, glo + c0 + lane, kvh, h) * 2]);
-    }
-    M = wave_max(M);
-    for (int c0 = 0; c0 < nc; c0 += kWave) {
-      int my_slot = 0;
-      float wgt = 0.0f;
-      if (c0 + lane < nc) {
-        my_slot = merge_slot(a, sp, gs, glo + c0 + lane, kvh, h);
-        wgt = __builtin_amdgcn_exp2f(a.ws_ml[(int64_t)my_slot * 2] - M);
-        l += wgt * a.ws_ml[(int64_t)my_slot * 2 + 1];
+    if (nc <= kWave) {
+      // One round trip for the common case: every contributor's (m, l),
+      // lane-parallel, and the first four accumulator rows are loaded
+      // together (the rows' slots do not depend on (m, l)); the weights
+      // follow from the maximum, the remaining rows four at a time.
+      const int my_slot = lane < nc ? merge_slot(a, sp, gs, glo + lane, kvh, h) : 0;
+      f32x2 x[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {  // nc >= 2; rows u >= nc repeat row 0 with weight 0
+        const int64_t sl = __builtin_amdgcn_readlane(my_slot, u);
+        x[u] = *reinterpret_cast<const f32x2*>(a.ws_acc + (u < nc ? sl : 0) * kHeadDim + 2 * lane);
       }
-      const int cnt = nc - c0 < kWave ? nc - c0 : kWave;
-      int j = 0;
-      for (; j + 4 <= cnt; j += 4) {
-        f32x2 x[4];
+      const f32x2 ml = lane < nc ? *reinterpret_cast<const f32x2*>(a.ws_ml + (int64_t)my_slot * 2)
+                                 : f32x2{kNegBig, 0.0f};
+      const float M = wave_max(ml[0]);
+      const float wgt = lane < nc ? __builtin_amdgcn_exp2f(ml[0] - M) : 0.0f;
+      l = wgt * ml[1];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float w1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), u));
+        o0 += w1 * x[u][0];
+        o1 += w1 * x[u][1];
+      }
+      for (int j = 4; j < nc; j += 4) {
+        f32x2 y[4];
         float w4[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          const int64_t sl = __builtin_amdgcn_readlane(my_slot, j + u);
-          w4[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), j + u));
-          x[u] = *reinterpret_cast<const f32x2*>(a.ws_acc + sl * kHeadDim + 2 * lane);
+          const int64_t sl = __builtin_amdgcn_readlane(my_slot, j + u < nc ? j + u : 0);
+          w4[u] = j + u < nc ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), j + u)) : 0.0f;
+          y[u] = *reinterpret_cast<const f32x2*>(a.ws_acc + sl * kHeadDim + 2 * lane);
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          o0 += w4[u] * x[u][0];
-          o1 += w4[u] * x[u][1];
+          o0 += w4[u] * y[u][0];
+          o1 += w4[u] * y[u][1];
         }
       }
-      for (; j < cnt; ++j) {
-        const int64_t sl = __builtin_amdgcn_readlane(my_slot, j);
-        const float w1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), j));
-        const f32x2 x = *reinterpret_cast<const f32x2*>(a.ws_acc + sl * kHeadDim + 2 * lane);
-        o0 += w1 * x[0];
-        o1 += w1 * x[1];
+    } else {
+      float M = kNegBig;
+      for (int c0 = 0; c0 < nc; c0 += kWave) {
+        if (c0 + lane < nc) M = fmaxf(M, a.ws_ml[(int64_t)merge_slot(a, sp, gs, glo + c0 + lane, kvh, h) * 2]);
+      }
+      M = wave_max(M);
+      for (int c0 = 0; c0 < nc; c0 += kWave) {
+        int my_slot = 0;
+        float wgt = 0.0f;
+        if (c0 + lane < nc) {
+          my_slot = merge_slot(a, sp, gs, glo + c0 + lane, kvh, h);
+          wgt = __builtin_amdgcn_exp2f(a.ws_ml[(int64_t)my_slot * 2] - M);
+          l += wgt * a.ws_ml[(int64_t)my_slot * 2 + 1];
+        }
+        const int cnt = nc - c0 < kWave ? nc - c0 : kWave;
+        int j = 0;
+        for (; j + 4 <= cnt; j += 4) {
+          f32x2 x[4];
+          float w4[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int64_t sl = __builtin_amdgcn_readlane(my_slot, j + u);
+            w4[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), j + u));
+            x[u] = *reinterpret_cast<const f32x2*>(a.ws_acc + sl * kHeadDim + 2 * lane);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            o0 += w4[u] * x[u][0];
+            o1 += w4[u] * x[u][1];
+          }
+        }
+        for (; j < cnt; ++j) {
+          const int64_t sl = __builtin_amdgcn_readlane(my_slot, j);
+          const float w1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), j));
+          const f32x2 x = *reinterpret_cast<const f32x2*>(a.ws_acc + sl * kHeadDim + 2 * lane);
+          o0 += w1 * x[0];
+          o1 += w1 * x[1];
+        }
       }
     }
 #pragma unroll

@@ -212,6 +212,20 @@ def test_decode_stream_k_vs_split_k_and_empty_rows(dev, dtype):
     assert torch.count_nonzero(sk[[0, 7, 8, 39]]) == 0
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
+def test_decode_stream_k_item_over_many_groups(dev, dtype):
+    """One long sequence beside a short one, 8 KV heads: the long sequence's
+    columns are cut over ~190 wave groups, so its items take the merge
+    kernel's general path (more than 64 contributors); the short one's take
+    the one-round-trip path."""
+    announce(f"decode {dtype} stream-K, one item over ~190 wave groups")
+    ctx = torch.tensor([6000, 300])
+    q, k, v, bt, ctx, ks, vs = _case(91, 2, 32, 8, 256, 64, 24, dtype, ctx=ctx)
+    want = _oracle(q, k, v, bt, ctx, 0.08, 32, 8, ks, vs)
+    got = _run(dev, q, k, v, bt, ctx, 0.08, 32, 8, ks, vs)
+    assert_close_out(got, want, got.dtype, TOL[dtype])
+
+
 def test_decode_large_batch_uses_split_k_fallback(dev):
     announce("decode batch 9000 (beyond the stream-K batch cap)")
     g = torch.Generator().manual_seed(73)
