@@ -208,8 +208,9 @@ int mkv_fp8_calibrate_per_tensor(const void* key, int64_t key_row_stride,
  * two >= 16.  q_dtype is F32, BF16 or F16 with any kv_dtype.
  *
  * split_tokens: 0 = the library's schedule (stream-K over 32-token tiles on
- * a persistent grid for BF16/F16/FP8 KV and batch <= 8192, else split-K with
- * a library-chosen split); > 0 = split-K with that many tokens per work item
+ * a persistent grid, groups of num_kv_heads waves sharing each tile range,
+ * for BF16/F16/FP8/INT8 KV and batch <= 8192, else split-K with a
+ * library-chosen split); > 0 = split-K with that many tokens per work item
  * (a multiple of 32).  workspace: >= mkv_paged_decode_workspace_size(...)
  * bytes with the same arguments; calls that share a workspace must be
  * ordered on one stream.
