@@ -213,6 +213,22 @@ def test_decode_stream_k_vs_split_k_and_empty_rows(dev, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("Hkv", [1, 3, 5, 12, 40])
+def test_decode_stream_k_kv_head_counts(dev, dtype, Hkv):
+    """The stream-K grid forms groups of Hkv waves (one KV head each) and
+    leaves the waves past the last whole group idle: KV head counts that do
+    not divide the grid, and large ones, give the oracle's result."""
+    announce(f"decode {dtype} stream-K with {Hkv} KV heads")
+    g = torch.Generator().manual_seed(93 + Hkv)
+    ctx = torch.randint(1, 2049, (5,), generator=g)
+    ctx[2] = 0
+    q, k, v, bt, ctx, ks, vs = _case(94 + Hkv, 5, 2 * Hkv, Hkv, 128, 96, 16, dtype, ctx=ctx)
+    want = _oracle(q, k, v, bt, ctx, 0.09, 2 * Hkv, Hkv, ks, vs)
+    got = _run(dev, q, k, v, bt, ctx, 0.09, 2 * Hkv, Hkv, ks, vs)
+    assert_close_out(got, want, got.dtype, TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
 def test_decode_stream_k_item_over_many_groups(dev, dtype):
     """One long sequence beside a short one, 8 KV heads: the long sequence's
     columns are cut over ~190 wave groups, so its items take the merge
