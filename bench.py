@@ -45,7 +45,7 @@ KV_DESC = {"fp8": "per-tensor e4m3fn", "bf16": "bf16",
            "int8_token": "int8 codes, fp32 scale per token and kv head"}
 
 
-EXTRAS = ("append", "prefill", "latency", "producer", "mixed", "copy")
+EXTRAS = ("append", "prefill", "latency", "producer", "mixed", "copy", "gather")
 
 
 def parse_args(argv=None):
@@ -259,6 +259,51 @@ def cpu_append_baseline(key, value, slots, ks: float, vs: float) -> dict:
     ab = W.alg_bytes_append(slots, 8, 2, 1)
     return {"value": round(ab / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"the whole workload ({slots.numel()} tokens), median of 3: {t * 1e3:.1f} ms"}
+
+
+def gather_extra(kc, meta, dev, stream, cpu: bool = True) -> dict:
+    """Block-table gather (mkv.gather_kv; the reference's torch form is
+    benchmark_decoding.py:166-178) of one layer's K pool of the decode
+    workload into a zero-padded (batch, max_len, Hkv, D) tensor, max_len =
+    the longest context rounded up to a block.  Algorithmic bytes: the
+    visible rows read once, every output row written once, the table
+    entries read once."""
+    from mkv import attention as A
+
+    bs = meta["block_size"]
+    lens = meta["context_lens"]
+    max_len = (int(lens.max()) + bs - 1) // bs * bs
+    row = kc.shape[2] * kc.shape[3] * kc.element_size()
+    nblk = (lens + bs - 1) // bs
+    alg = int(lens.sum()) * row + lens.numel() * max_len * row + int(nblk.sum()) * 4
+    bt, ctx = meta["block_tables"].to(dev), meta["context_lens"].to(dev)
+    ms = time_launches(lambda i: A.gather_kv(kc, bt, ctx, max_len), 20, 3, stream)
+    res = {"workload": f"{lens.numel()} sequences, context sum {int(lens.sum())}, max_len {max_len}, "
+                       f"{row}-byte rows ({kc.dtype}), block {bs}",
+           "us": round(ms * 1e3, 1), "GBps": round(alg / ms / 1e6, 1),
+           "frac_of_8000_GBps": round(alg / ms / 1e6 / 8000.0, 4)}
+    if cpu:
+        # the reference's torch form on the host cores, per sequence: the
+        # blocks' rows by index, cut to the context, zero-padded to max_len
+        import torch
+        n = 32
+        pool = kc.view(torch.uint8).cpu()
+        tbl, cl = meta["block_tables"][:n], lens[:n]
+        threads = _cpu_threads()
+
+        def host_gather():
+            outh = torch.zeros(n, max_len, *pool.shape[2:], dtype=pool.dtype)
+            for b in range(n):
+                L = int(cl[b])
+                nb = (L + bs - 1) // bs
+                idx = tbl[b, :nb].to(torch.int64)
+                outh[b, :L] = pool[idx].reshape(nb * bs, *pool.shape[2:])[:L]
+            return outh
+        t = _median_time(host_gather)
+        cab = int(cl.sum()) * row + n * max_len * row + int(nblk[:n].sum()) * 4
+        res["cpu_baseline"] = {"value": round(cab / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+                               "kind": "port", "sample": f"first {n} sequences, median of 3: {t * 1e3:.1f} ms"}
+    return res
 
 
 def mixed_batch_extra(dev, stream) -> dict:
@@ -687,6 +732,8 @@ def main() -> int:
             extra["producer_fused"] = producer_extra(dev, stream)
         if "mixed" in wanted:
             extra["mixed_batch"] = mixed_batch_extra(dev, stream)
+        if "gather" in wanted:
+            extra["gather_kv"] = gather_extra(layers[0][0], meta, dev, stream, cpu=args.cpu_seqs > 0)
         if "copy" in wanted:
             copy = box_copy_gbps(dev, stream)
             extra["box_copy_GBps"] = round(copy, 1)
