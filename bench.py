@@ -306,6 +306,24 @@ def gather_extra(kc, meta, dev, stream, cpu: bool = True) -> dict:
     return res
 
 
+def cpu_copy_append_baseline(key, value, slots) -> dict:
+    """The reference's copy append semantics on the host cores (oracle
+    store_kvcache_ref: index-assign of every valid row into the pool) for
+    the 4096-token append workload."""
+    import torch
+
+    from mkv import workloads as W
+    from oracle import reference as R
+
+    threads = _cpu_threads()
+    kp = torch.zeros(1024, 256, 8, HEAD_DIM, dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    t = _median_time(lambda: R.store_kvcache_ref(key, value, kp, vp, slots))
+    ab = W.alg_bytes_append(slots, 8, 2, 2)
+    return {"value": round(ab / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the whole workload ({slots.numel()} tokens), median of 3: {t * 1e3:.1f} ms"}
+
+
 def mixed_batch_extra(dev, stream) -> dict:
     """Attention over the mixed-batch workload (8 prefill chunks of 512 rows
     after priors U[0, 4096] and 120 decode rows with contexts U[256, 4096],
@@ -723,6 +741,16 @@ def main() -> int:
             if T == 4096 and args.cpu_seqs > 0:
                 extra[f"append_fp8_T{T}"]["cpu_baseline"] = cpu_append_baseline(
                     w["key"], w["value"], w["slot_mapping"], 0.05, 0.05)
+            del kp, vp
+            # the copy append (bf16 rows into a bf16 pool) on the same tokens
+            kp = torch.zeros(1024, 256, 8, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+            vp = torch.zeros_like(kp)
+            cms = time_launches(lambda i: A._append(kd, vd, kp, vp, sd), 50, 5, stream)
+            cab = W.alg_bytes_append(w["slot_mapping"], 8, 2, 2)
+            extra[f"append_copy_T{T}"] = {"us": round(cms * 1e3, 2), "GBps": round(cab / cms / 1e6, 1)}
+            if T == 4096 and args.cpu_seqs > 0:
+                extra[f"append_copy_T{T}"]["cpu_baseline"] = cpu_copy_append_baseline(
+                    w["key"], w["value"], w["slot_mapping"])
             del kp, vp
         if "prefill" in wanted:
             extra["prefill_chunked"] = prefill_extra(dev, stream, cpu=args.cpu_seqs > 0)
