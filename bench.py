@@ -189,7 +189,52 @@ def prefill_extra(dev, stream, cpu: bool = True) -> dict:
         if name == "bf16" and cpu:
             out["cpu_baseline"] = cpu_prefill_baseline(q, kc, vc, bt, ctx, cu_p, pos, pm["block_size"])
         del kc, vc
+    out["full_prefill"] = full_prefill_extra(dev, stream, cpu)
     return out
+
+
+def full_prefill_extra(dev, stream, cpu: bool = True) -> dict:
+    """Causal varlen prefill over fresh contiguous bf16 q/k/v
+    (mkv.flash_attention_prefill, the reference's flash_attention_prefill):
+    the end-to-end workload's prompts (60, lengths U[32, 512], 16 q / 8 kv
+    heads) and 8 prompts of 4096 tokens (32 q / 8 kv heads).  FLOPs are
+    algorithmic (4*D per visible key per row and head)."""
+    import torch
+
+    from mkv import attention as A
+
+    res = {}
+    for name, lens, hq in (("prompts60_16q", None, 16), ("8x4096_32q", [4096] * 8, 32)):
+        g = torch.Generator().manual_seed(5)
+        if lens is None:
+            lens = torch.randint(32, 513, (60,), generator=g).tolist()
+        cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
+        cu[1:] = torch.cumsum(torch.tensor(lens), 0)
+        T = int(cu[-1])
+        q = torch.randn(T, hq, HEAD_DIM, generator=g).to(torch.bfloat16)
+        k = torch.randn(T, 8, HEAD_DIM, generator=g).to(torch.bfloat16)
+        v = torch.randn(T, 8, HEAD_DIM, generator=g).to(torch.bfloat16)
+        qd, kd, vd, cud = q.to(dev), k.to(dev), v.to(dev), cu.to(dev)
+        flops = sum(n * (n + 1) // 2 for n in lens) * hq * 4 * HEAD_DIM
+        sm = 1.0 / math.sqrt(HEAD_DIM)
+        ms = time_launches(lambda i: A.flash_attention_prefill(qd, kd, vd, cud, sm, hq, 8, HEAD_DIM),
+                           20, 3, stream)
+        tf = flops / (ms * 1e-3) / 1e12
+        res[name] = {"tokens": T, "GFLOP": round(flops / 1e9, 1), "us": round(ms * 1e3, 1),
+                     "TFLOPs": round(tf, 1), "frac_of_2500_TFLOPs": round(tf / 2500.0, 4)}
+        if cpu and name == "prompts60_16q":
+            # the reference's torch form (pytorch_standard_attention semantics, fp32) on 8 prompts
+            from oracle import reference as R
+            n = 8
+            cu8 = cu[: n + 1]
+            t8 = int(cu8[-1])
+            t = _median_time(lambda: R.flash_prefill_ref(q[:t8], k[:t8], v[:t8], cu8, sm, hq, 8,
+                                                           compute_dtype=torch.float32))
+            f8 = sum(x * (x + 1) // 2 for x in lens[:n]) * hq * 4 * HEAD_DIM
+            res[name]["cpu_baseline"] = {"value": round(f8 / t / 1e9, 2), "unit": "GFLOP/s",
+                                         "cores": _cpu_threads(), "kind": "port",
+                                         "sample": f"first {n} prompts ({t8} tokens), median of 3: {t * 1e3:.1f} ms"}
+    return res
 
 
 def _cpu_threads() -> int:
