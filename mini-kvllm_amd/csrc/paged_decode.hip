@@ -1039,55 +1039,57 @@ MKV_DEV int64_t stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
 // even (w1 = W / Hkv).
 constexpr int kFirstSharePct = 58;
 
+// Contiguous split of `total` units (columns) over `parts` parts (wave
+// groups); the first `parts1` parts (the first dispatch round) take
+// kFirstSharePct percent of the units.
 struct StreamSplit {
   int64_t total;
-  int64_t base;  // tiles of the first group
+  int64_t base;  // units of the first-round parts
   int64_t per1, per2;
-  int w1, waves;
+  int parts1, parts;
 
-  MKV_DEV int64_t begin(int w) const {
-    const int64_t b = w < w1 ? (int64_t)w * per1 : base + (int64_t)(w - w1) * per2;
-    const int64_t cap = w < w1 ? base : total;
+  MKV_DEV int64_t begin(int p) const {
+    const int64_t b = p < parts1 ? (int64_t)p * per1 : base + (int64_t)(p - parts1) * per2;
+    const int64_t cap = p < parts1 ? base : total;
     return b < cap ? b : cap;
   }
-  MKV_DEV int64_t end(int w) const {
-    const int64_t e = w < w1 ? (int64_t)(w + 1) * per1 : base + (int64_t)(w - w1 + 1) * per2;
-    const int64_t cap = w < w1 ? base : total;
+  MKV_DEV int64_t end(int p) const {
+    const int64_t e = p < parts1 ? (int64_t)(p + 1) * per1 : base + (int64_t)(p - parts1 + 1) * per2;
+    const int64_t cap = p < parts1 ? base : total;
     return e < cap ? e : cap;
   }
-  MKV_DEV int wave_of(int64_t g) const {
-    return g < base ? (int)(g / per1) : w1 + (int)((g - base) / per2);
+  // the part whose range holds unit g
+  MKV_DEV int part_of(int64_t g) const {
+    return g < base ? (int)(g / per1) : parts1 + (int)((g - base) / per2);
   }
 };
 
-// The group split of a launch: groups of Hkv consecutive waves (waves past
-// the last whole group stay idle).
-MKV_DEV StreamSplit stream_split(const DecodeArgs& a, int64_t columns);
-
-MKV_DEV StreamSplit make_split(int64_t total, int waves, int first_waves) {
+MKV_DEV StreamSplit make_split(int64_t total, int parts, int first_parts) {
   StreamSplit p;
   p.total = total;
-  p.waves = waves;
-  if (first_waves <= 0 || first_waves >= waves) {
-    p.w1 = waves;
-    p.per1 = (total + waves - 1) / waves;
+  p.parts = parts;
+  if (first_parts <= 0 || first_parts >= parts) {
+    p.parts1 = parts;
+    p.per1 = (total + parts - 1) / parts;
     p.per1 = p.per1 < 1 ? 1 : p.per1;
     p.base = total;
     p.per2 = 1;
     return p;
   }
-  p.w1 = first_waves;
+  p.parts1 = first_parts;
   const int64_t t1 = total * kFirstSharePct / 100;
-  p.per1 = (t1 + first_waves - 1) / first_waves;
+  p.per1 = (t1 + first_parts - 1) / first_parts;
   p.per1 = p.per1 < 1 ? 1 : p.per1;
-  const int64_t head = (int64_t)first_waves * p.per1;
+  const int64_t head = (int64_t)first_parts * p.per1;
   p.base = head < total ? head : total;
-  const int w2 = waves - first_waves;
-  p.per2 = (total - p.base + w2 - 1) / w2;
+  const int p2 = parts - first_parts;
+  p.per2 = (total - p.base + p2 - 1) / p2;
   p.per2 = p.per2 < 1 ? 1 : p.per2;
   return p;
 }
 
+// The group split of a launch: groups of Hkv consecutive waves (waves past
+// the last whole group stay idle).
 MKV_DEV StreamSplit stream_split(const DecodeArgs& a, int64_t columns) {
   const int groups = a.num_waves / a.num_kv_heads;
   const int first = a.first_waves >= a.num_waves ? groups : a.first_waves / a.num_kv_heads;
@@ -1107,7 +1109,7 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
   const int w = blockIdx.x * kDecWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = w / a.num_kv_heads;  // this wave: KV head w % Hkv of its group's columns
   const int kvh = w - grp * a.num_kv_heads;
-  if (grp >= sp.waves) return;
+  if (grp >= sp.parts) return;
   const int64_t g0 = sp.begin(grp);
   const int64_t g1 = sp.end(grp);
   if (g0 >= g1) return;
@@ -1246,7 +1248,7 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_ke
   if (n > 0) {
     const int64_t gs = p0;  // the item's columns
     const int64_t ge = gs + n;
-    const int glo = sp.wave_of(gs), ghi = sp.wave_of(ge - 1);
+    const int glo = sp.part_of(gs), ghi = sp.part_of(ge - 1);
     if (glo == ghi) return;  // written whole by the main kernel
     const int nc = ghi - glo + 1;
     if (nc <= kWave) {
