@@ -1,7 +1,7 @@
 """Seeded synthetic workloads for the KV-cache hot path.
 
 Each generator draws from ``torch.Generator(device='cpu').manual_seed(seed)``
-in a fixed, documented order, so a CPU checker, a CPU baseline and the GPU
+in a fixed, documented order, so the oracle, a CPU baseline and the GPU
 kernels can all see identical bytes.  Large KV pools (the batch-256 decode
 workload) are filled on the GPU with a seeded CUDA generator instead, which
 keeps setup time to seconds; their parity is checked through properties
