@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MKV_ABI_VERSION 2
+#define MKV_ABI_VERSION 3
 
 /* Element dtypes (torch.float32, torch.bfloat16, torch.float16,
  * torch.float8_e4m3fn, torch.int8).  FP8 is OCP e4m3fn: max 448, no
@@ -212,13 +212,14 @@ int mkv_fp8_calibrate_per_tensor(const void* key, int64_t key_row_stride,
  * for BF16/F16/FP8/INT8 KV and batch <= 8192, else split-K with a
  * library-chosen split); > 0 = split-K with that many tokens per work item
  * (a multiple of 32).  workspace: >= mkv_paged_decode_workspace_size(...)
- * bytes with the same arguments; calls that share a workspace must be
- * ordered on one stream.
+ * bytes with the same arguments (the size of the route those arguments
+ * select: stream-K partial slots for the persistent grid, or split-K
+ * partials); calls that share a workspace must be ordered on one stream.
  */
 size_t mkv_paged_decode_workspace_size(int batch, int num_heads,
                                        int num_kv_heads, int max_blocks,
                                        int block_size, int head_dim,
-                                       int split_tokens);
+                                       int kv_dtype, int split_tokens);
 
 /* Tokens per split-K work item that mkv_paged_decode uses for these sizes
  * (split_tokens itself when it is > 0). */

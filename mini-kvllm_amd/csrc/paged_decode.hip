@@ -1556,6 +1556,23 @@ size_t split_ws_bytes(int batch, int num_heads, int max_blocks, int block_size, 
   return (size_t)batch * num_heads * max_splits * (kHeadDim + 2) * sizeof(float);
 }
 
+// The route mkv_paged_decode takes: stream-K (library schedule, 16-bit / FP8
+// / INT8 KV, batch <= kStreamMaxBatch; it needs a group of num_kv_heads
+// waves, and a grid holds at least CUs x kDecWaves waves), else split-K.
+bool use_stream(int split_tokens, int kv_dtype, int batch, int num_kv_heads) {
+  return split_tokens == 0 && kv_dtype != MKV_DTYPE_F32 && batch <= kStreamMaxBatch &&
+         num_kv_heads <= device_cus() * kDecWaves;
+}
+
+// Workspace bytes of the route that these arguments select.
+size_t decode_ws_bytes(int batch, int num_heads, int num_kv_heads, int max_blocks, int block_size,
+                       int kv_dtype, int split_tokens) {
+  if (use_stream(split_tokens, kv_dtype, batch, num_kv_heads))
+    return stream_ws_bytes(batch, num_heads / num_kv_heads);
+  const int st = resolve_split(split_tokens, batch, num_kv_heads, max_blocks, block_size);
+  return split_ws_bytes(batch, num_heads, max_blocks, block_size, st);
+}
+
 }  // namespace
 }  // namespace mkv
 
@@ -1568,17 +1585,11 @@ extern "C" int mkv_paged_decode_split_tokens(int batch, int num_kv_heads, int ma
 
 extern "C" size_t mkv_paged_decode_workspace_size(int batch, int num_heads, int num_kv_heads,
                                                   int max_blocks, int block_size, int head_dim,
-                                                  int split_tokens) {
+                                                  int kv_dtype, int split_tokens) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks <= 0 || block_size <= 0 ||
       head_dim <= 0 || num_heads % num_kv_heads)
     return 0;
-  const int st = resolve_split(split_tokens, batch, num_kv_heads, max_blocks, block_size);
-  size_t n = split_ws_bytes(batch, num_heads, max_blocks, block_size, st);
-  if (split_tokens <= 0 && batch <= kStreamMaxBatch) {
-    const size_t sk = stream_ws_bytes(batch, num_heads / num_kv_heads);
-    n = sk > n ? sk : n;
-  }
-  return n;
+  return decode_ws_bytes(batch, num_heads, num_kv_heads, max_blocks, block_size, kv_dtype, split_tokens);
 }
 
 extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void* q,
@@ -1654,10 +1665,7 @@ extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void*
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // the merge kernels apply the per-tensor V scale
   const bool fp8 = fmt == MKV_DTYPE_FP8E4M3;
-  // (stream-K needs a group of num_kv_heads waves, and a grid holds at least
-  // CUs x kDecWaves waves)
-  if (split_tokens == 0 && kv_dtype != MKV_DTYPE_F32 && batch <= kStreamMaxBatch &&
-      num_kv_heads <= device_cus() * kDecWaves) {
+  if (use_stream(split_tokens, kv_dtype, batch, num_kv_heads)) {
     // stream-K path
     const size_t need = stream_ws_bytes(batch, group);
     if (!workspace) return MKV_ERR_NULL_POINTER;

@@ -14,7 +14,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmkv.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -41,7 +41,7 @@ SIGNATURES: dict[str, tuple] = {
     "mkv_fp8_calibrate_per_tensor": (c_int, [
         c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int, c_int, c_void_p, c_void_p,
         c_void_p, c_void_p]),
-    "mkv_paged_decode_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
+    "mkv_paged_decode_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
     "mkv_paged_decode_split_tokens": (c_int, [c_int, c_int, c_int, c_int, c_int]),
     "mkv_paged_decode": (c_int, [
         c_void_p, c_int64, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_int, c_int64,

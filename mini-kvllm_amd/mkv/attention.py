@@ -51,6 +51,11 @@ _DTYPES = {
 PER_TOKEN_HEAD_MODES = ("fp8_per_token_head", "int8_per_token_head")
 
 _workspaces: dict[tuple[int, str], torch.Tensor] = {}
+# Workspaces replaced by larger ones.  A captured graph keeps the device
+# address of the workspace it was captured with, so a replaced workspace is
+# never handed back to the allocator (growth is geometric, so these hold at
+# most as many bytes as the live ones).
+_retired_workspaces: list[torch.Tensor] = []
 
 
 def _dtype_code(t: torch.Tensor, what: str) -> int:
@@ -89,11 +94,15 @@ def _side_stream(dev: torch.device) -> torch.cuda.Stream:
 
 
 def _workspace(dev: torch.device, name: str, nbytes: int, zeroed: bool = False) -> torch.Tensor:
-    """Per-device scratch tensor, grown on demand and then reused."""
+    """Per-device scratch tensor, grown on demand (at least doubling) and then
+    reused; a replaced one stays allocated for the life of the process."""
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), name)
     t = _workspaces.get(key)
     if t is None or t.numel() < nbytes:
         n = max(256, (nbytes + 255) // 256 * 256)
+        if t is not None:
+            n = max(n, 2 * t.numel())
+            _retired_workspaces.append(t)
         t = (torch.zeros if zeroed else torch.empty)(n, dtype=torch.uint8, device=dev)
         _workspaces[key] = t
     return t
@@ -348,7 +357,7 @@ def _decode(query, k_cache, v_cache, block_tables, context_lens, scale, num_head
     if per_token_head:
         _check_token_scales(k_scale, v_scale, k_cache)
     nbytes = _lib.query("mkv_paged_decode_workspace_size", batch, num_heads, num_kv_heads,
-                        max_blocks, bs, head_dim, split_tokens)
+                        max_blocks, bs, head_dim, _dtype_code(k_cache, "k_cache"), split_tokens)
     ws = _workspace(dev, "decode", nbytes) if nbytes else None
     _lib.call(
         "mkv_paged_decode", out.data_ptr(), out.stride(0), query.data_ptr(), query.stride(0),

@@ -137,11 +137,23 @@ class DecodeGraphs:
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.pool = None
 
-    def capture(self) -> None:
+    def capture(self, scales: Iterable[torch.Tensor] = ()) -> None:
         """Capture one graph per bucket, largest first, sharing one memory
         pool.  The state is saved, every row deactivated for the warm-up and
-        the capture (so no K/V is written anywhere), and then restored."""
+        the capture (so no K/V is written anywhere), and then restored.
+
+        ``scales``: the per-tensor FP8 scale tensors that ``step_fn``'s
+        appends use.  The warm-up runs the appends eagerly on the inactive
+        rows, and a scale that still holds the 1.0 "not yet calibrated"
+        sentinel would be calibrated there from those rows' dummy K/V and
+        then frozen (the reference's capture has the same hazard,
+        model_runner.py:769-794).  Their values and calibration flags are
+        saved before the warm-up and restored after the capture, so a scale
+        that held 1.0 is calibrated by the first real step (eager, or a
+        replay: the captured append keeps the sentinel test)."""
         m = self.meta
+        scales = list(scales)
+        saved_scales = [(s, s.clone(), getattr(s, "_mkv_calibrated", None)) for s in scales]
         saved = (m.seq_lens.clone(), m.context_lens.clone(), m.slot_mapping.clone())
         m.seq_lens.zero_()
         side = torch.cuda.Stream(m.device)
@@ -162,6 +174,14 @@ class DecodeGraphs:
         m.seq_lens.copy_(saved[0])
         m.context_lens.copy_(saved[1])
         m.slot_mapping.copy_(saved[2])
+        for s, value, flag in saved_scales:
+            s.copy_(value)
+            if flag is None:
+                if hasattr(s, "_mkv_calibrated"):
+                    del s._mkv_calibrated
+            else:
+                s._mkv_calibrated = flag
+        torch.cuda.synchronize(m.device)
 
     def bucket(self, batch: int) -> int:
         for b in self.buckets:

@@ -97,17 +97,23 @@ def test_decode_metadata_matches_oracle_over_a_run(dev):
             join()
 
 
-def _make_layers(dev, n_layers, N, bs, Hkv):
+def _make_layers(dev, n_layers, N, bs, Hkv, scale=0.02):
     layers = []
     for _ in range(n_layers):
         kc = torch.zeros(N, bs, Hkv, 128, dtype=torch.float8_e4m3fn, device=dev)
-        layers.append((kc, torch.zeros_like(kc), torch.full((1,), 0.02, device=dev),
-                       torch.full((1,), 0.02, device=dev)))
+        layers.append((kc, torch.zeros_like(kc), torch.full((1,), scale, device=dev),
+                       torch.full((1,), scale, device=dev)))
     return layers
 
 
-def test_captured_decode_steps_match_eager(dev):
-    announce("decode graphs: buckets 1/2/4/8/16, 2 layers fp8 append+decode, 30 steps")
+@pytest.mark.parametrize("sentinel", [False, True], ids=["calibrated", "sentinel"])
+def test_captured_decode_steps_match_eager(dev, sentinel):
+    """sentinel: the scales start at the runner's 1.0 "not yet calibrated"
+    value (model_runner.py:327).  The capture must leave them at 1.0, and the
+    first replay must calibrate them from its own K/V exactly as the eager
+    store_kvcache_fp8 does."""
+    announce(f"decode graphs: buckets 1/2/4/8/16, 2 layers fp8 append+decode, 30 steps, "
+             f"scales {'1.0 sentinel' if sentinel else 'preset'}")
     g = torch.Generator().manual_seed(62)
     bs, max_rows, max_blocks, N, Hq, Hkv, L = 16, 16, 16, 300, 16, 4, 2
     sm = 1.0 / math.sqrt(128)
@@ -120,7 +126,7 @@ def test_captured_decode_steps_match_eager(dev):
         v = torch.zeros_like(k)
         out = torch.zeros(L, max_rows, Hq, 128, dtype=torch.bfloat16, device=dev)
         sides.append(dict(meta=meta, q=q, k=k, v=v, out=out,
-                          layers=_make_layers(dev, L, N, bs, Hkv)))
+                          layers=_make_layers(dev, L, N, bs, Hkv, 1.0 if sentinel else 0.02)))
 
     def make_step(sd):
         def step_fn(rows, slot, ctx, bt):
@@ -132,10 +138,14 @@ def test_captured_decode_steps_match_eager(dev):
         return step_fn
 
     graphs = DS.DecodeGraphs(sides[0]["meta"], make_step(sides[0]), buckets=[1, 2, 4, 8, 16])
-    graphs.capture()
+    scales = [x for lay in sides[0]["layers"] for x in lay[2:]]
+    graphs.capture(scales=scales)
     for sd in sides:  # capture wrote nothing: pools still zero
         for kc, vc, _, _ in sd["layers"]:
             assert torch.count_nonzero(kc.view(torch.uint8)) == 0
+    for x in scales:  # and left the scales (and their calibration state) alone
+        assert float(x) == (1.0 if sentinel else 0.02)
+        assert not getattr(x, "_mkv_calibrated", False)
     eager_step = make_step(sides[1])
     blocks = _Blocks(N, g)
     rows: list[dict] = []
@@ -174,7 +184,10 @@ def test_captured_decode_steps_match_eager(dev):
         assert torch.equal(ga["out"][:, :n].view(torch.int16), eb["out"][:, :n].view(torch.int16)), \
             f"step {step} (batch {n}, bucket {rows_run}): outputs"
         assert torch.count_nonzero(ga["out"][:, n:rows_run].float()) == 0, "padded rows must be zero"
-        for (kc, vc, _, _), (kc2, vc2, _, _) in zip(ga["layers"], eb["layers"]):
+        for (kc, vc, ks, vs), (kc2, vc2, ks2, vs2) in zip(ga["layers"], eb["layers"]):
+            assert torch.equal(ks, ks2) and torch.equal(vs, vs2), f"step {step}: scales"
+            if sentinel:
+                assert float(ks) != 1.0 and float(vs) != 1.0, f"step {step}: scale not calibrated"
             assert torch.equal(kc.view(torch.uint8), kc2.view(torch.uint8)), f"step {step}: K pool"
             assert torch.equal(vc.view(torch.uint8), vc2.view(torch.uint8)), f"step {step}: V pool"
         # grow to 11, shrink to 2, grow again: buckets change in both directions
@@ -188,3 +201,46 @@ def test_captured_decode_steps_match_eager(dev):
                 sd["meta"].move_row(len(rows) - 1, victim)
             rows[victim] = rows.pop()
     assert max(batches) == 11 and min(batches) == 2
+
+
+def test_replay_after_workspace_growth(dev):
+    """A captured decode keeps the device address of the decode workspace.
+    A later eager decode that needs a larger workspace must not hand the
+    captured one back to the allocator: tensors allocated afterwards would
+    share its memory and the replay would write partials into them."""
+    announce("decode graph replay after a larger eager decode grew the workspace")
+    g = torch.Generator().manual_seed(63)
+    bs, rows, max_blocks, N, Hq, Hkv = 16, 4, 8, 200, 16, 4
+    sm = 1.0 / math.sqrt(128)
+    kc = (torch.randn(N, bs, Hkv, 128, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    vc = torch.randn(N, bs, Hkv, 128, generator=g).to(torch.bfloat16).to(dev)
+    meta = DS.DecodeMetadata(rows, max_blocks, bs, N, dev)
+    perm = torch.randperm(N, generator=g).tolist()
+    for r in range(rows):
+        meta.set_row(r, perm[r * max_blocks:(r + 1) * max_blocks], 40 + 17 * r)
+    q = torch.randn(rows, Hq, 128, generator=g).to(torch.bfloat16).to(dev)
+    out = torch.zeros(rows, Hq, 128, dtype=torch.bfloat16, device=dev)
+
+    def step_fn(n, slot, ctx, bt):
+        A._decode(q[:n], kc, vc, bt, ctx, sm, Hq, Hkv, 128, out=out[:n])
+
+    graphs = DS.DecodeGraphs(meta, step_fn, buckets=[rows])
+    graphs.capture()
+    # an eager decode with a much larger batch and table: its workspace is larger
+    B2, mb2 = 2048, 12
+    ctx2 = torch.randint(1, mb2 * bs, (B2,), generator=g)
+    bt2 = torch.randint(0, N, (B2, mb2), generator=g, dtype=torch.int32)
+    q2 = torch.randn(B2, Hq, 128, generator=g).to(torch.bfloat16).to(dev)
+    A.paged_attention_decode(q2, kc, vc, bt2.to(dev), ctx2.to(dev), sm, Hq, Hkv, 128, bs)
+    # tensors allocated now may take any memory the allocator got back
+    fillers = [torch.full((n,), 7, dtype=torch.uint8, device=dev) for n in (1 << 20, 4 << 20, 8 << 20)]
+    torch.cuda.synchronize()
+    for step in range(3):
+        graphs.run(rows)
+        torch.cuda.synchronize()
+        slot, ctx, bt = meta.slot_mapping, meta.context_lens, meta.block_tables
+        want = A.paged_attention_decode(q, kc, vc, bt, ctx, sm, Hq, Hkv, 128, bs)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"replay {step}"
+        for f in fillers:
+            assert int((f != 7).sum()) == 0, f"replay {step} wrote into memory it does not own"

@@ -116,18 +116,31 @@ def test_argument_validation_without_launch():
 
 def test_decode_workspace_and_split_queries():
     lib = _lib.load()
+    F32, BF16, FP8 = _lib.DTYPE_F32, _lib.DTYPE_BF16, _lib.DTYPE_FP8E4M3
     st = lib.mkv_paged_decode_split_tokens(256, 8, 32, 256, 0)
     assert st % 32 == 0 and 64 <= st <= 512
-    n = lib.mkv_paged_decode_workspace_size(256, 32, 8, 32, 256, 128, 0)
+    # an fp32 cache always takes split-K: its partials
+    n = lib.mkv_paged_decode_workspace_size(256, 32, 8, 32, 256, 128, F32, 0)
     splits = (32 * 256 + st - 1) // st
-    assert n >= 256 * 32 * splits * 130 * 4  # split-K partials
+    assert n == 256 * 32 * splits * 130 * 4
     # explicit split sizes select the split-K path only
-    n512 = lib.mkv_paged_decode_workspace_size(256, 32, 8, 32, 256, 128, 512)
+    n512 = lib.mkv_paged_decode_workspace_size(256, 32, 8, 32, 256, 128, FP8, 512)
     assert n512 == 256 * 32 * 16 * 130 * 4
     # one split covers the table: no workspace on the split-K path
-    assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 1, 256, 128, 512) == 0
-    # the default (stream-K) path always needs its partial slots
-    assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 1, 256, 128, 0) > 0
+    assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 1, 256, 128, FP8, 512) == 0
+    st4 = lib.mkv_paged_decode_split_tokens(4, 8, 1, 256, 0)
+    splits4 = (256 + st4 - 1) // st4
+    assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 1, 256, 128, F32, 0) == (
+        4 * 16 * splits4 * 130 * 4 if splits4 > 1 else 0)
+    # the default stream-K route needs its partial slots for the persistent
+    # grid and the tile prefix only, not the split-K partials: without a GPU
+    # the CU count query falls back to 512 CUs, i.e. 4096 waves
+    nsk = lib.mkv_paged_decode_workspace_size(256, 32, 8, 32, 256, 128, FP8, 0)
+    assert lib.mkv_paged_decode_workspace_size(256, 32, 8, 32, 256, 128, BF16, 0) == nsk
+    assert nsk % (2 * 4 * 130 * 4) == (256 + 2) * 4
+    waves = (nsk - (256 + 2) * 4) // (2 * 4 * 130 * 4)
+    assert waves in (4096, 2048) and nsk < n
+    assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 1, 256, 128, FP8, 0) > 0
     # small batches split finer
     assert lib.mkv_paged_decode_split_tokens(4, 8, 8, 256, 0) < st or st == 64
 
