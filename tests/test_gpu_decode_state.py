@@ -144,7 +144,7 @@ def test_captured_decode_steps_match_eager(dev, sentinel):
         for kc, vc, _, _ in sd["layers"]:
             assert torch.count_nonzero(kc.view(torch.uint8)) == 0
     for x in scales:  # and left the scales (and their calibration state) alone
-        assert float(x) == (1.0 if sentinel else 0.02)
+        assert float(x) == float(torch.tensor(1.0 if sentinel else 0.02, dtype=torch.float32))
         assert not getattr(x, "_mkv_calibrated", False)
     eager_step = make_step(sides[1])
     blocks = _Blocks(N, g)
