@@ -75,6 +75,7 @@ extern "C" {
 #define MKV_ERR_WORKSPACE_TOO_SMALL (-7)
 #define MKV_ERR_MISALIGNED (-8)
 #define MKV_ERR_BAD_STRIDE (-9)
+#define MKV_ERR_SCRATCH_LIMIT (-10)
 
 /* ABI version of the loaded library (MKV_ABI_VERSION at build time). */
 int mkv_abi_version(void);
@@ -237,6 +238,38 @@ int mkv_paged_decode(void* out, int64_t out_batch_stride,
                      int batch, int num_heads, int num_kv_heads, int head_dim,
                      int block_size, float sm_scale, int split_tokens,
                      void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * K2 without a caller workspace, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  It has no counterpart in the reference.
+ *
+ * Same arguments and results as mkv_paged_decode (the same kernels and
+ * schedule, so the outputs are bit-identical), minus workspace and
+ * workspace_bytes: the partials live in a static per-device scratch array of
+ * MKV_NOALLOC_SCRATCH_BYTES (32 MiB) that the library holds on each GPU it
+ * runs on until the process ends.  The call allocates
+ * and frees nothing.  A call whose route needs more than that (see
+ * mkv_paged_decode_workspace_size) returns MKV_ERR_SCRATCH_LIMIT before any
+ * launch.  Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (different streams, or different host threads without
+ * ordering) race and must be ordered by the caller.  The first call on a
+ * device resolves the array's address on that device (make it outside graph
+ * capture).
+ */
+#define MKV_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int mkv_paged_decode_noalloc(void* out, int64_t out_batch_stride,
+                             const void* q, int64_t q_batch_stride, int q_dtype,
+                             const void* k_cache, const void* v_cache, int kv_dtype,
+                             int64_t num_blocks,
+                             const float* k_scale, const float* v_scale,
+                             int kv_scale_mode,
+                             const int32_t* block_tables, int64_t bt_stride,
+                             int max_blocks,
+                             const void* context_lens, int context_lens_dtype,
+                             int batch, int num_heads, int num_kv_heads, int head_dim,
+                             int block_size, float sm_scale, int split_tokens,
+                             void* stream);
 
 /*
  * K3: causal prefill / extend attention over the paged cache.

@@ -33,6 +33,8 @@
 //     softmax denominator sums the unscaled P, as the reference does.
 // Splits that do not cover a whole sequence write (acc, m, l) partials that a
 // second kernel merges with the log-sum-exp rule.
+#include <mutex>
+
 #include "mkv_device.hpp"
 
 namespace mkv {
@@ -1592,15 +1594,16 @@ extern "C" size_t mkv_paged_decode_workspace_size(int batch, int num_heads, int 
   return decode_ws_bytes(batch, num_heads, num_kv_heads, max_blocks, block_size, kv_dtype, split_tokens);
 }
 
-extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void* q,
-                                int64_t q_batch_stride, int q_dtype, const void* k_cache,
-                                const void* v_cache, int kv_dtype, int64_t num_blocks,
-                                const float* k_scale, const float* v_scale, int kv_scale_mode,
-                                const int32_t* block_tables, int64_t bt_stride, int max_blocks,
-                                const void* context_lens, int context_lens_dtype, int batch,
-                                int num_heads, int num_kv_heads, int head_dim, int block_size,
-                                float sm_scale, int split_tokens, void* workspace,
-                                size_t workspace_bytes, void* stream) {
+namespace {
+
+int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_t q_batch_stride,
+                      int q_dtype, const void* k_cache, const void* v_cache, int kv_dtype,
+                      int64_t num_blocks, const float* k_scale, const float* v_scale,
+                      int kv_scale_mode, const int32_t* block_tables, int64_t bt_stride,
+                      int max_blocks, const void* context_lens, int context_lens_dtype, int batch,
+                      int num_heads, int num_kv_heads, int head_dim, int block_size,
+                      float sm_scale, int split_tokens, void* workspace, size_t workspace_bytes,
+                      void* stream) {
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks < 0 || num_blocks < 0)
     return MKV_ERR_BAD_SHAPE;
   if (batch == 0) return MKV_OK;
@@ -1757,4 +1760,81 @@ extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void*
                        block, 0, s, a, (int)fp8);
   }
   return (int)hipGetLastError();
+}
+
+}  // namespace
+
+// Scratch of mkv_paged_decode_noalloc: one array per GPU, held from the
+// library's first use on that GPU until the process ends.  It is sized for
+// the stream-K partial slots of group sizes up to 8 on 256 CUs (2048 waves x
+// 2 slots x 8 heads x 130 floats = 16.3 MiB, plus the per-sequence tile
+// prefix) with room for moderate split-K requests; larger requests are
+// refused.  Host code must not pass the array's name to a kernel: in host
+// code it is a stand-in, not a device address.  The per-device address comes
+// from hipGetSymbolAddress, taken once per device with that device current.
+constexpr size_t kScratchBytes = MKV_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// Device address of the current device's scratch array (resolved on the
+// first call on that device).
+int scratch_address(void** out) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return MKV_ERR_BAD_SHAPE;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (r != hipSuccess) return (int)r;
+    if (!p) return MKV_ERR_NULL_POINTER;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MKV_OK;
+}
+
+}  // namespace
+
+extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void* q,
+                                int64_t q_batch_stride, int q_dtype, const void* k_cache,
+                                const void* v_cache, int kv_dtype, int64_t num_blocks,
+                                const float* k_scale, const float* v_scale, int kv_scale_mode,
+                                const int32_t* block_tables, int64_t bt_stride, int max_blocks,
+                                const void* context_lens, int context_lens_dtype, int batch,
+                                int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                float sm_scale, int split_tokens, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  return paged_decode_impl(out, out_batch_stride, q, q_batch_stride, q_dtype, k_cache, v_cache, kv_dtype,
+                           num_blocks, k_scale, v_scale, kv_scale_mode, block_tables, bt_stride, max_blocks,
+                           context_lens, context_lens_dtype, batch, num_heads, num_kv_heads, head_dim,
+                           block_size, sm_scale, split_tokens, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mkv_paged_decode_noalloc(void* out, int64_t out_batch_stride, const void* q,
+                                        int64_t q_batch_stride, int q_dtype, const void* k_cache,
+                                        const void* v_cache, int kv_dtype, int64_t num_blocks,
+                                        const float* k_scale, const float* v_scale, int kv_scale_mode,
+                                        const int32_t* block_tables, int64_t bt_stride, int max_blocks,
+                                        const void* context_lens, int context_lens_dtype, int batch,
+                                        int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                        float sm_scale, int split_tokens, void* stream) {
+  if (batch > 0 && num_heads > 0 && num_kv_heads > 0 && max_blocks > 0 && block_size > 0 &&
+      num_heads % num_kv_heads == 0 && split_tokens >= 0 &&
+      decode_ws_bytes(batch, num_heads, num_kv_heads, max_blocks, block_size, kv_dtype, split_tokens) >
+          kScratchBytes)
+    return MKV_ERR_SCRATCH_LIMIT;
+  void* ws = nullptr;
+  const int st = scratch_address(&ws);
+  if (st != MKV_OK) return st;
+  return paged_decode_impl(out, out_batch_stride, q, q_batch_stride, q_dtype, k_cache, v_cache, kv_dtype,
+                           num_blocks, k_scale, v_scale, kv_scale_mode, block_tables, bt_stride, max_blocks,
+                           context_lens, context_lens_dtype, batch, num_heads, num_kv_heads, head_dim,
+                           block_size, sm_scale, split_tokens, ws, kScratchBytes, stream);
 }

@@ -19,6 +19,9 @@ extern "C" const char* mkv_status_string(int status) {
     case MKV_ERR_WORKSPACE_TOO_SMALL: return "workspace is smaller than the size query reported";
     case MKV_ERR_MISALIGNED: return "pointer or row stride is not 16-byte aligned";
     case MKV_ERR_BAD_STRIDE: return "row stride is smaller than the row it must hold";
+    case MKV_ERR_SCRATCH_LIMIT:
+      return "the call needs more than the library's static per-device scratch "
+             "(MKV_NOALLOC_SCRATCH_BYTES); use mkv_paged_decode with a workspace";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

@@ -24,6 +24,7 @@ DTYPE_I8 = 4
 SCALE_PER_TENSOR = 0
 SCALE_PER_TOKEN_HEAD = 1
 APPEND_CALIBRATE_SENTINEL = 1
+NOALLOC_SCRATCH_BYTES = 32 << 20  # MKV_NOALLOC_SCRATCH_BYTES
 INDEX_I32 = 0
 INDEX_I64 = 1
 
@@ -47,6 +48,10 @@ SIGNATURES: dict[str, tuple] = {
         c_void_p, c_int64, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_int, c_int64,
         c_void_p, c_void_p, c_int, c_void_p, c_int64, c_int, c_void_p, c_int, c_int, c_int, c_int,
         c_int, c_int, c_float, c_int, c_void_p, c_size_t, c_void_p]),
+    "mkv_paged_decode_noalloc": (c_int, [
+        c_void_p, c_int64, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_int, c_int64,
+        c_void_p, c_void_p, c_int, c_void_p, c_int64, c_int, c_void_p, c_int, c_int, c_int, c_int,
+        c_int, c_int, c_float, c_int, c_void_p]),
     "mkv_paged_prefill_workspace_size": (c_size_t, [c_int, c_int64, c_int, c_int]),
     "mkv_paged_prefill": (c_int, [
         c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_int,

@@ -40,10 +40,24 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 def test_status_strings():
     lib = _lib.load()
-    for code in range(0, -10, -1):
+    for code in range(0, -11, -1):
         s = lib.mkv_status_string(code).decode()
         assert s and s != "unknown mkv status"
     assert lib.mkv_status_string(-1234).decode() == "unknown mkv status"
+
+
+def test_noalloc_decode_refuses_requests_beyond_its_scratch():
+    """The allocation-free decode checks its scratch limit on the host,
+    before it touches the device."""
+    lib = _lib.load()
+    args = [None, 32 * 128, None, 32 * 128, _lib.DTYPE_BF16, None, None, _lib.DTYPE_F32, 4096,
+            None, None, 0, None, 32, 32, None, _lib.INDEX_I64, 1024, 32, 8, 128, 256, 0.088, 32,
+            None]
+    # split-K partials of 1024 x 32 heads x 256 splits: 4.4 GB > 32 MiB
+    assert lib.mkv_paged_decode_noalloc(*args) == -10
+    assert lib.mkv_paged_decode_workspace_size(1024, 32, 8, 32, 256, 128, _lib.DTYPE_F32, 32) \
+        > _lib.NOALLOC_SCRATCH_BYTES
+    assert "scratch" in lib.mkv_status_string(-10).decode()
 
 
 def test_argument_validation_without_launch():
