@@ -284,14 +284,15 @@ int mkv_paged_decode_noalloc(void* out, int64_t out_batch_stride,
  * block_tables as in K2 (-1 entries skipped).
  *
  * q, out: (total_q, num_heads, head_dim) contiguous.  positions: int64
- * (total_q).  cu_seqlens_q: int32 (num_seqs + 1).  kv_dtype BF16 or F16;
+ * (total_q).  cu_seqlens_q: int32 (num_seqs + 1).  kv_dtype F32 (the
+ * reference engine's default, computed on the fp32 MFMA), BF16 or F16;
  * FP8E4M3 with kv_scale_mode MKV_SCALE_PER_TENSOR (k_scale / v_scale: one
  * fp32 each) or MKV_SCALE_PER_TOKEN_HEAD; INT8 with MKV_SCALE_PER_TOKEN_HEAD
  * (k_scale / v_scale: fp32 (num_blocks, block_size, num_kv_heads), as in
  * K2).  Per-token-head caches are an extension as well: the reference's
  * decode-path arithmetic (K scale on the score, V scale on P, the
- * denominator over the unscaled P) applied per key.  An F32 cache returns
- * MKV_ERR_UNSUPPORTED_DTYPE; q_dtype F32, BF16 or F16.
+ * denominator over the unscaled P) applied per key.  q_dtype F32, BF16 or
+ * F16 with any kv_dtype; out has q's dtype.
  * workspace: >= mkv_paged_prefill_workspace_size(...) bytes (tile list).
  */
 size_t mkv_paged_prefill_workspace_size(int num_seqs, int64_t total_q,
@@ -317,8 +318,7 @@ int mkv_paged_prefill(void* out, const void* q, int q_dtype,
  * Replaces flash_attention_prefill (attention.py:446-514, kernel :336-443).
  * Row i of sequence s attends to rows cu_seqlens[s] .. i of k/v.
  * q, out: (total, num_heads, head_dim); k, v: (total, num_kv_heads,
- * head_dim); all contiguous and of one dtype (BF16 or F16; F32 returns
- * MKV_ERR_UNSUPPORTED_DTYPE).
+ * head_dim); all contiguous and of one dtype (F32, BF16 or F16).
  */
 size_t mkv_flash_prefill_workspace_size(int num_seqs, int64_t total,
                                         int num_heads, int num_kv_heads);

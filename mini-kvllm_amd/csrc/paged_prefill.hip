@@ -277,6 +277,105 @@ MKV_DEV int lane_id_volatile() {
   return l;
 }
 
+// The workgroup's share of a prefill launch: its KV head, sequence and
+// query rows, and the number of keys each of its kRowsPerWg rows sees.
+struct WgWork {
+  int kvh;
+  int seq;
+  int64_t q_seq0;  // first query row of the sequence
+  int64_t q0, q1;  // the workgroup's query rows [q0, q1)
+  int min_vis, max_vis;
+};
+
+// Looks up the workgroup's tile (XCD-aware order over the longest-first
+// tile list) and fills vis_lds[row] (0 for padding rows).  Returns false,
+// uniformly over the workgroup, when it has no tile.  Holds barriers: every
+// thread of the workgroup must call it.
+template <bool PAGED>
+MKV_DEV bool wg_work(const PrefillArgs& a, char* smem, int* vis_lds, int* red_lds, WgWork& w) {
+  const int tid = threadIdx.x;
+  // XCD-aware order: with a multiple of 8 KV heads every XCD takes whole
+  // heads (consecutive logical tiles share an XCD and its L2, and each XCD
+  // sees the same longest-first mix); otherwise the tiles are dealt round
+  // robin, so that the longest ones spread over all XCDs.
+  const int64_t nwg = gridDim.x;
+  const int64_t logical = a.num_kv_heads % kXcds == 0
+                              ? (int64_t)(blockIdx.x % kXcds) * (nwg / kXcds) + blockIdx.x / kXcds
+                              : (int64_t)blockIdx.x;
+  const int kvh = (int)(logical / a.tiles_ub);
+  const int64_t tau = logical - (int64_t)kvh * a.tiles_ub;
+  if (kvh >= a.num_kv_heads) return false;
+  const int64_t cap = PAGED ? (int64_t)a.idx.max_blocks << a.idx.bs_log2 : 0;
+  int seq;
+  int64_t q_seq0, q_seq1, tile, ctx;
+  if (a.inline_list) {
+    TileListLds& L = *reinterpret_cast<TileListLds*>(smem + kTileListOffset);
+    build_tile_list(L, a.cu_seqlens_q, PAGED ? a.context_lens : nullptr, a.ctx_i64, cap, a.num_seqs,
+                    a.tok_per_wg);
+    if (tau >= L.ts[a.num_seqs]) return false;
+    int lo = 0, hi = a.num_seqs;  // largest k with ts[k] <= tau
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (L.ts[mid] <= tau) lo = mid; else hi = mid;
+    }
+    seq = L.ord[lo];
+    q_seq0 = L.cu[seq];
+    q_seq1 = L.cu[seq + 1];
+    tile = (int64_t)(L.ts[lo + 1] - 1) - tau;  // the sequence's last tile first
+    ctx = PAGED ? (int64_t)L.ctx[seq] : q_seq1 - q_seq0;
+  } else {
+    if (tau >= a.tile_start[a.num_seqs]) return false;
+    int lo = 0, hi = a.num_seqs;  // largest k with tile_start[k] <= tau
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (a.tile_start[mid] <= tau) lo = mid; else hi = mid;
+    }
+    seq = a.order[lo];
+    q_seq0 = a.cu_seqlens_q[seq];
+    q_seq1 = a.cu_seqlens_q[seq + 1];
+    tile = (int64_t)(a.tile_start[lo + 1] - 1) - tau;  // the sequence's last tile first
+    if constexpr (PAGED) {
+      ctx = load_index(a.context_lens, seq, a.ctx_i64);
+      ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+    } else {
+      ctx = q_seq1 - q_seq0;
+    }
+  }
+  const int64_t q0 = q_seq0 + tile * (int64_t)a.tok_per_wg;
+  const int64_t q1 = q0 + a.tok_per_wg < q_seq1 ? q0 + a.tok_per_wg : q_seq1;
+  const int G = a.group;
+
+  // Visible length of every row (0 for padding rows), and the WG's min / max.
+  if (tid < kRowsPerWg) {
+    const int64_t tok = q0 + tid / G;
+    int vis = 0;
+    if (tid < a.tok_per_wg * G && tok < q1) {
+      const int64_t pos = PAGED ? a.positions[tok] : tok - q_seq0;
+      const int64_t v = pos + 1 < ctx ? pos + 1 : ctx;
+      vis = v < 0 ? 0 : (int)v;
+    }
+    vis_lds[tid] = vis;
+  }
+  if (tid == 0) {
+    red_lds[0] = 0x7fffffff;
+    red_lds[1] = 0;
+  }
+  __syncthreads();
+  if (tid < kRowsPerWg && tid < a.tok_per_wg * G && q0 + tid / G < q1) {
+    atomicMin(&red_lds[0], vis_lds[tid]);
+    atomicMax(&red_lds[1], vis_lds[tid]);
+  }
+  __syncthreads();
+  w.kvh = kvh;
+  w.seq = seq;
+  w.q_seq0 = q_seq0;
+  w.q0 = q0;
+  w.q1 = q1;
+  w.min_vis = red_lds[0];
+  w.max_vis = red_lds[1];
+  return true;
+}
+
 // LDS geometry of one K or V tile: kBN key rows of 256 bytes (128 16-bit
 // elements; FP8 caches are converted to fp16 as they are staged), 16-byte
 // chunks XOR-swizzled by the key index.  The LDS serves 256 bytes per clock
@@ -344,80 +443,12 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const int lane = tid & 63, wave = tid >> 6;
   const int c = lane & 15, kg = lane >> 4;
 
-  // XCD-aware order: with a multiple of 8 KV heads every XCD takes whole
-  // heads (consecutive logical tiles share an XCD and its L2, and each XCD
-  // sees the same longest-first mix); otherwise the tiles are dealt round
-  // robin, so that the longest ones spread over all XCDs.
-  const int64_t nwg = gridDim.x;
-  const int64_t logical = a.num_kv_heads % kXcds == 0
-                              ? (int64_t)(blockIdx.x % kXcds) * (nwg / kXcds) + blockIdx.x / kXcds
-                              : (int64_t)blockIdx.x;
-  const int kvh = (int)(logical / a.tiles_ub);
-  const int64_t tau = logical - (int64_t)kvh * a.tiles_ub;
-  if (kvh >= a.num_kv_heads) return;
-  const int64_t cap = PAGED ? (int64_t)a.idx.max_blocks << a.idx.bs_log2 : 0;
-  int seq;
-  int64_t q_seq0, q_seq1, tile, ctx;
-  if (a.inline_list) {
-    TileListLds& L = *reinterpret_cast<TileListLds*>(smem + kTileListOffset);
-    build_tile_list(L, a.cu_seqlens_q, PAGED ? a.context_lens : nullptr, a.ctx_i64, cap, a.num_seqs,
-                    a.tok_per_wg);
-    if (tau >= L.ts[a.num_seqs]) return;
-    int lo = 0, hi = a.num_seqs;  // largest k with ts[k] <= tau
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (L.ts[mid] <= tau) lo = mid; else hi = mid;
-    }
-    seq = L.ord[lo];
-    q_seq0 = L.cu[seq];
-    q_seq1 = L.cu[seq + 1];
-    tile = (int64_t)(L.ts[lo + 1] - 1) - tau;  // the sequence's last tile first
-    ctx = PAGED ? (int64_t)L.ctx[seq] : q_seq1 - q_seq0;
-  } else {
-    if (tau >= a.tile_start[a.num_seqs]) return;
-    int lo = 0, hi = a.num_seqs;  // largest k with tile_start[k] <= tau
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (a.tile_start[mid] <= tau) lo = mid; else hi = mid;
-    }
-    seq = a.order[lo];
-    q_seq0 = a.cu_seqlens_q[seq];
-    q_seq1 = a.cu_seqlens_q[seq + 1];
-    tile = (int64_t)(a.tile_start[lo + 1] - 1) - tau;  // the sequence's last tile first
-    if constexpr (PAGED) {
-      ctx = load_index(a.context_lens, seq, a.ctx_i64);
-      ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
-    } else {
-      ctx = q_seq1 - q_seq0;
-    }
-  }
-  const int64_t q0 = q_seq0 + tile * (int64_t)a.tok_per_wg;
-  const int64_t q1 = q0 + a.tok_per_wg < q_seq1 ? q0 + a.tok_per_wg : q_seq1;
+  WgWork wk;
+  if (!wg_work<PAGED>(a, smem, vis_lds, red_lds, wk)) return;
+  const int kvh = wk.kvh, seq = wk.seq;
+  const int64_t q_seq0 = wk.q_seq0, q0 = wk.q0, q1 = wk.q1;
+  const int min_vis = wk.min_vis, max_vis = wk.max_vis;
   const int G = a.group;
-
-  // Visible length of every row (0 for padding rows), and the WG's min / max.
-  if (tid < kRowsPerWg) {
-    const int64_t tok = q0 + tid / G;
-    int vis = 0;
-    if (tid < a.tok_per_wg * G && tok < q1) {
-      const int64_t pos = PAGED ? a.positions[tok] : tok - q_seq0;
-      const int64_t v = pos + 1 < ctx ? pos + 1 : ctx;
-      vis = v < 0 ? 0 : (int)v;
-    }
-    vis_lds[tid] = vis;
-  }
-  if (tid == 0) {
-    red_lds[0] = 0x7fffffff;
-    red_lds[1] = 0;
-  }
-  __syncthreads();
-  if (tid < kRowsPerWg && tid < a.tok_per_wg * G && q0 + tid / G < q1) {
-    atomicMin(&red_lds[0], vis_lds[tid]);
-    atomicMax(&red_lds[1], vis_lds[tid]);
-  }
-  __syncthreads();
-  const int min_vis = red_lds[0];
-  const int max_vis = red_lds[1];
 
   // Query rows of this wave: row tile rt covers rows (kRowTiles*wave + rt)*16 + 0..15.
   int vis_c[kRowTiles];
@@ -924,6 +955,262 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp32 caches (the reference engine's default precision, model_runner.py:87,
+// :249; flash_attention_prefill / paged_attention_prefill_triton take fp32,
+// attention.py:446-514, :852-891).  The same work decomposition as
+// prefill_mfma_kernel (128 rows of one sequence and KV head per workgroup,
+// the same tile list), on the fp32 MFMA (v_mfma_f32_16x16x4_f32: products
+// and sums in fp32, no rounding of K, V, q or P below fp32).
+//
+// Tiles of kBN32 = 32 keys x 512 bytes go from HBM straight into LDS by DMA
+// (buffer_load ... lds), double-buffered.  Wave w loads 8 consecutive keys
+// of one 16-key sub-tile: K (w < 4) or V, sub-tile (w % 4) / 2, keys
+// 8 (w % 2) .. +7, two key rows per instruction.  K rows are stored with
+// 16-byte chunk p holding logical chunk p ^ (key & 15) (the swizzle moves to
+// the global side of the DMA), so that the 16 lanes of a QK operand read
+// (16 keys, one logical chunk) hit 16 distinct chunk positions mod 16; V rows
+// are stored as they are (the 16 lanes of a PV operand read take one key's
+// chunks c and 16 + c).
+//
+// Per wave (16 rows), per 16-key sub-tile kt:
+//   S^T = K Q^T: 32 MFMAs; lane (c, kg) supplies K[key c][32 kg + st] and
+//     q[row c][32 kg + st] at step st (the contraction order over head_dim
+//     is free), and receives S^T[key 4 kg + r][row c].
+//   O += P V: 4 x 8 MFMAs; step r takes P[row c][key 4 kg + r] (from the
+//     lane's own scores) and V[key 4 kg + r][dim], where output tile mm and
+//     lane column c hold dim 4c + mm (mm < 4) or 64 + 4c + mm - 4.
+// ---------------------------------------------------------------------------
+constexpr int kBN32 = 32;
+constexpr int kRowBytes32 = kHeadDim * 4;          // 512
+constexpr int kTileBytes32 = kBN32 * kRowBytes32;  // 16 KB per K or V tile
+
+template <bool PAGED>
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4))) void prefill_f32_kernel(PrefillArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  __shared__ __align__(16) char lds_k0[kTileBytes32], lds_v0[kTileBytes32], lds_k1[kTileBytes32],
+      lds_v1[kTileBytes32];
+  int* vis_lds = reinterpret_cast<int*>(smem);
+  int* red_lds = vis_lds + kRowsPerWg;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 15, kg = lane >> 4;
+
+  WgWork wk;
+  if (!wg_work<PAGED>(a, smem, vis_lds, red_lds, wk)) return;
+  const int kvh = wk.kvh, seq = wk.seq;
+  const int64_t q0 = wk.q0, q1 = wk.q1;
+  const int min_vis = wk.min_vis, max_vis = wk.max_vis;
+  const int G = a.group;
+
+  // q of row c (dims 32 kg .. 32 kg + 31), fp32
+  const int my_row = 16 * wave + c;
+  const int vis_row = vis_lds[my_row];
+  float qf[32];
+  {
+    const int64_t tok = q0 + my_row / G;
+    if (my_row < a.tok_per_wg * G && tok < q1) {
+      const int hq = kvh * G + my_row % G;
+      const int64_t off = (tok * a.num_heads + hq) * kHeadDim + 32 * kg;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) load_q8(a.q, a.q_dtype, off + 8 * i, qf + 8 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
+    }
+  }
+  // The loop keeps raw scores and needs score_mul > 0 (as prefill_mfma_kernel).
+  float score_mul = a.sm_scale * kLog2e;
+  if (!(score_mul > 0.0f) && score_mul == score_mul) {
+    const float f = score_mul < 0.0f ? -1.0f : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) qf[i] *= f;
+    score_mul = score_mul < 0.0f ? -score_mul : 1.0f;
+  }
+
+  f32x4 acc[8];
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegBig, l_run = 0.0f;
+
+  // DMA geometry of this wave: tensor (K for waves 0-3), sub-tile j, first
+  // key kw of its 8; lane l fills key kw + 2u + l / 32 at chunk position
+  // l % 32 in instruction u.
+  const int64_t row_stride = (int64_t)a.num_kv_heads * kRowBytes32;
+  const int64_t head_bytes = (int64_t)kvh * kRowBytes32;
+  const bool w_is_v = wave >= 4;
+  const int w_sub = (wave & 3) >> 1;
+  const int w_key = 8 * (wave & 1);
+  uint32_t dma_off[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int key = w_key + 2 * u + (lane >> 5);  // within the sub-tile (== key & 15)
+    const int p = lane & 31;
+    const int gch = w_is_v ? p : (p ^ key);
+    dma_off[u] = (uint32_t)(key * row_stride + 16 * gch);
+  }
+  auto dma_tile = [&](int kb, char* kbuf, char* vbuf) {
+    const int64_t t0 = kb + 16 * w_sub;
+    const char* base = w_is_v ? a.v : a.k;
+    const char* ptr = base;
+    int num = 0;
+    if constexpr (PAGED) {
+      const int64_t phys = a.idx.physical_block(seq, t0 >> a.idx.bs_log2);
+      if (phys >= 0) {
+        const int64_t bmask = ((int64_t)1 << a.idx.bs_log2) - 1;
+        ptr = base + ((phys << a.idx.bs_log2) + (t0 & bmask)) * row_stride + head_bytes;
+        num = (int)(15 * row_stride + kRowBytes32);
+      }
+    } else {
+      ptr = base + (wk.q_seq0 + t0) * row_stride + head_bytes;
+      num = (int)(15 * row_stride + kRowBytes32);
+    }
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)ptr, (short)0, num, 0x00020000);
+    char* dst0 = (w_is_v ? vbuf : kbuf) + (16 * w_sub + w_key) * kRowBytes32;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t key = t0 + w_key + 2 * u + (lane >> 5);
+      const uint32_t off = key < max_vis ? dma_off[u] : 0x80000000u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r, (__attribute__((address_space(3))) void*)(dst0 + 2 * u * kRowBytes32), 16, off, 0, 0, 0);
+    }
+  };
+  // validity of the two 16-key sub-tiles of the tile at kb (absent blocks)
+  auto sub_valid = [&](int kb, int kt) -> bool {
+    if constexpr (PAGED) return a.idx.physical_block(seq, (int64_t)(kb + 16 * kt) >> a.idx.bs_log2) >= 0;
+    return true;
+  };
+
+  const int n_tiles = (max_vis + kBN32 - 1) / kBN32;
+  const bool wave_active = __builtin_amdgcn_ballot_w64(vis_row > 0) != 0;
+  if (n_tiles > 0) {
+    dma_tile(0, lds_k0, lds_v0);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  }
+  __syncthreads();
+  for (int it0 = 0; it0 < n_tiles; it0 += 2) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int it = it0 + h;
+      if (it >= n_tiles) break;
+      char* kbuf = h ? lds_k1 : lds_k0;
+      char* vbuf = h ? lds_v1 : lds_v0;
+      const int kb = it * kBN32;
+      if (it + 1 < n_tiles) dma_tile(kb + kBN32, h ? lds_k0 : lds_k1, h ? lds_v0 : lds_v1);
+      if (wave_active) {
+        bool kvalid[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) kvalid[kt] = sub_valid(kb, kt);
+        const bool full = kb + kBN32 <= min_vis && kvalid[0] && kvalid[1];
+        // ---- S^T = K Q^T ----
+        f32x4 s[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          const char* krow = kbuf + (16 * kt + c) * kRowBytes32;
+#pragma unroll
+          for (int qd = 0; qd < 8; ++qd) {
+            const f32x4 kv4 = *reinterpret_cast<const f32x4*>(krow + 16 * ((8 * kg + qd) ^ c));
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv4[e], qf[4 * qd + e], s[kt], 0, 0, 0);
+          }
+        }
+        // ---- online softmax (log2 domain) for row c ----
+        if (!full) {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int t = kb + 16 * kt + 4 * kg + r;
+              if (!(t < vis_row && kvalid[kt])) s[kt][r] = -__builtin_huge_valf();
+            }
+        }
+        float mx = -__builtin_huge_valf();
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][r]);
+        mx = max_xor32(max_xor16(mx));
+        mx = fmaxf(mx * score_mul, kNegBig);
+        const float m_new = mx > m_run + kRescaleSlack ? mx : m_run;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        float psum = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            s[kt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], score_mul, -m_new));
+            psum += s[kt][r];
+          }
+        l_run = l_run * alpha + psum;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float ar = __shfl(alpha, 4 * kg + r);
+#pragma unroll
+            for (int mm = 0; mm < 8; ++mm) acc[mm][r] *= ar;
+          }
+        }
+        // ---- O += P V ----
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const char* vrow = vbuf + (16 * kt + 4 * kg + r) * kRowBytes32;
+            const f32x4 v_lo = *reinterpret_cast<const f32x4*>(vrow + 16 * c);
+            const f32x4 v_hi = *reinterpret_cast<const f32x4*>(vrow + 256 + 16 * c);
+#pragma unroll
+            for (int mm = 0; mm < 4; ++mm) {
+              acc[mm] = __builtin_amdgcn_mfma_f32_16x16x4f32(s[kt][r], v_lo[mm], acc[mm], 0, 0, 0);
+              acc[4 + mm] = __builtin_amdgcn_mfma_f32_16x16x4f32(s[kt][r], v_hi[mm], acc[4 + mm], 0, 0, 0);
+            }
+          }
+      }  // wave_active
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's DMA has landed
+      __syncthreads();
+    }
+  }
+
+  // ---- normalise and write rows 4 kg + r ----
+  float l_col = l_run + __shfl_xor(l_run, 16);
+  l_col += __shfl_xor(l_col, 32);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float lh = __shfl(l_col, 4 * kg + r);
+    const int row = 16 * wave + 4 * kg + r;
+    const int64_t tok = q0 + row / G;
+    if (row >= a.tok_per_wg * G || tok >= q1) continue;
+    const int hq = kvh * G + row % G;
+    const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
+    float lo[8], hi[8];
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+      lo[mm] = acc[mm][r] * inv;
+      hi[mm] = acc[4 + mm][r] * inv;
+    }
+    const int64_t o = (tok * a.num_heads + hq) * kHeadDim;
+    if (a.q_dtype == MKV_DTYPE_F32) {
+      float* po = reinterpret_cast<float*>(a.out) + o;
+      *reinterpret_cast<f32x4*>(po + 4 * c) = f32x4{lo[0], lo[1], lo[2], lo[3]};
+      *reinterpret_cast<f32x4*>(po + 64 + 4 * c) = f32x4{hi[0], hi[1], hi[2], hi[3]};
+    } else {
+      const bool bf = a.q_dtype == MKV_DTYPE_BF16;
+      auto pack = [&](float x, float y) -> uint32_t {
+        const uint32_t bx = bf ? f32_to_bf16_bits(x) : f32_to_f16_bits(x);
+        const uint32_t by = bf ? f32_to_bf16_bits(y) : f32_to_f16_bits(y);
+        return bx | (by << 16);
+      };
+      uint16_t* po = reinterpret_cast<uint16_t*>(a.out) + o;
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<u32x2*>(po + 4 * c) = u32x2{pack(lo[0], lo[1]), pack(lo[2], lo[3])};
+      *reinterpret_cast<u32x2*>(po + 64 + 4 * c) = u32x2{pack(hi[0], hi[1]), pack(hi[2], hi[3])};
+    }
+  }
+}
+
 int ilog2_exact(int v) {
   if (v <= 0 || (v & (v - 1))) return -1;
   int l = 0;
@@ -946,6 +1233,15 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   nwg = ((nwg + kXcds - 1) / kXcds) * kXcds;
   hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED, QSPLIT>), dim3((unsigned)nwg), dim3(kPfThreads), lds,
                      s, a);
+  return (int)hipGetLastError();
+}
+
+template <bool PAGED>
+int launch_prefill_f32(const PrefillArgs& a, hipStream_t s) {
+  const size_t lds = kTileListOffset + (a.inline_list ? sizeof(TileListLds) : 0);
+  int64_t nwg = a.tiles_ub * a.num_kv_heads;
+  nwg = ((nwg + kXcds - 1) / kXcds) * kXcds;
+  hipLaunchKernelGGL((prefill_f32_kernel<PAGED>), dim3((unsigned)nwg), dim3(kPfThreads), lds, s, a);
   return (int)hipGetLastError();
 }
 
@@ -980,8 +1276,8 @@ int check_common(int num_seqs, int64_t total_q, int num_heads, int num_kv_heads,
   if (g < 1 || g > 16) return MKV_ERR_UNSUPPORTED_GROUP;
   if (q_dtype != MKV_DTYPE_F32 && q_dtype != MKV_DTYPE_BF16 && q_dtype != MKV_DTYPE_F16)
     return MKV_ERR_UNSUPPORTED_DTYPE;
-  if (kv_dtype != MKV_DTYPE_BF16 && kv_dtype != MKV_DTYPE_F16 && kv_dtype != MKV_DTYPE_FP8E4M3 &&
-      kv_dtype != MKV_DTYPE_I8)
+  if (kv_dtype != MKV_DTYPE_F32 && kv_dtype != MKV_DTYPE_BF16 && kv_dtype != MKV_DTYPE_F16 &&
+      kv_dtype != MKV_DTYPE_FP8E4M3 && kv_dtype != MKV_DTYPE_I8)
     return MKV_ERR_UNSUPPORTED_DTYPE;
   return MKV_OK;
 }
@@ -1004,6 +1300,7 @@ int dispatch_prefill(PrefillArgs& a, int kv_dtype, void* workspace, size_t works
   }
   const bool q16 = a.q_dtype == MKV_DTYPE_BF16;
   switch (kv_dtype) {
+    case MKV_DTYPE_F32: return launch_prefill_f32<PAGED>(a, s);
     case MKV_DTYPE_FP8E4M3: return launch_prefill<MKV_DTYPE_FP8E4M3, PAGED, false>(a, s);
     case kKvFp8PerToken:
       if constexpr (PAGED)

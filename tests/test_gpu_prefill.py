@@ -21,7 +21,7 @@ from mkv import workloads as W
 from oracle import reference as R
 
 pytestmark = pytest.mark.gpu
-TOL = {torch.bfloat16: 2e-3, torch.float16: 2e-3, torch.float8_e4m3fn: 2e-2}
+TOL = {torch.float32: 2e-3, torch.bfloat16: 2e-3, torch.float16: 2e-3, torch.float8_e4m3fn: 2e-2}
 
 
 def _make(seed, prior, qlen, Hq, Hkv, bs, dtype, N=None, holes=()):
@@ -60,7 +60,7 @@ def _gpu(dev, q, k, v, bt, ctx, cu, pos, scale, Hq, Hkv, ks, vs):
     return out.cpu()
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float8_e4m3fn])
 @pytest.mark.parametrize("group", [1, 2, 4, 8, 16])
 def test_prefill_small_groups(dev, dtype, group):
     announce(f"prefill {dtype} group {group}")
@@ -74,7 +74,7 @@ def test_prefill_small_groups(dev, dtype, group):
     assert_close_out(got, want, got.dtype, TOL[dtype])
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float8_e4m3fn])
 @pytest.mark.parametrize("scale", [0.0, -0.09])
 def test_prefill_zero_and_negative_scale(dev, dtype, scale):
     """The kernel keeps raw scores and scales them once: a zero scale (every
@@ -89,25 +89,26 @@ def test_prefill_zero_and_negative_scale(dev, dtype, scale):
     assert_close_out(got, want, got.dtype, TOL[dtype])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("nseq,Hkv", [(40, 2), (40, 8), (300, 2)])
-def test_prefill_visit_order_many_tied_and_empty_sequences(dev, nseq, Hkv):
+def test_prefill_visit_order_many_tied_and_empty_sequences(dev, nseq, Hkv, dtype):
     """The tile list visits sequences longest first (ranked on the device for
     up to 256 sequences, in batch order beyond) and each sequence's tiles last
     first; ties, empty sequences and both grid mappings (KV heads a multiple
     of 8 or not) must leave every row's result unchanged."""
-    announce(f"prefill visit order: {nseq} sequences, {Hkv} kv heads")
+    announce(f"prefill visit order: {nseq} sequences, {Hkv} kv heads, {dtype}")
     g = torch.Generator().manual_seed(500 + nseq + Hkv)
     prior = [int(x) for x in torch.tensor([0, 16, 50, 97])[torch.randint(0, 4, (nseq,), generator=g)]]
     qlen = [int(x) for x in torch.randint(0, 7, (nseq,), generator=g)]
     qlen[3] = 70  # one sequence of several tiles
-    q, k, v, bt, ctx, cu, pos, ks, vs = _make(nseq, prior, qlen, 2 * Hkv, Hkv, 16, torch.bfloat16)
+    q, k, v, bt, ctx, cu, pos, ks, vs = _make(nseq, prior, qlen, 2 * Hkv, Hkv, 16, dtype)
     got = _gpu(dev, q, k, v, bt, ctx, cu, pos, 0.09, 2 * Hkv, Hkv, ks, vs)
     want = R.paged_prefill_ref(q.double(), k, v, bt, ctx, cu, pos, 0.09, 2 * Hkv, Hkv, ks, vs)
-    assert_close_out(got, want, got.dtype, TOL[torch.bfloat16])
+    assert_close_out(got, want, got.dtype, TOL[dtype])
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
-@pytest.mark.parametrize("bs", [16, 256])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("bs", [16, 64, 256])
 def test_prefill_block_sizes_holes_and_context_caps(dev, dtype, bs):
     announce(f"prefill {dtype} bs {bs} holes")
     prior = [3, 0, 300]
@@ -145,12 +146,12 @@ def _torch_prefill_gpu(q, kc, vc, bt, ctx, cu, pos, scale, Hq, Hkv, ks=None, vs=
     return out
 
 
-@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+@pytest.mark.parametrize("kv", ["bf16", "fp8", "f32"])
 def test_prefill_chunk_workload_full_size(dev, kv):
     announce(f"prefill 8 x 512-row chunks, prior U[0,4096], 32/8 heads, {kv} KV")
     m = W.prefill_mixed(seed=4, num_decode=0)
     N, bs = m["num_blocks"], m["block_size"]
-    dtype = torch.bfloat16 if kv == "bf16" else torch.float8_e4m3fn
+    dtype = {"bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn, "f32": torch.float32}[kv]
     kc = torch.empty(N, bs, 8, 128, dtype=dtype, device=dev)
     vc = torch.empty_like(kc)
     ks = W.fill_pool_on_device(kc, 41)
@@ -169,8 +170,8 @@ def test_prefill_chunk_workload_full_size(dev, kv):
     assert_close_out(got, want, got.dtype, 2e-2 if ks else 2e-3)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("group", [1, 4])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("group", [1, 4, 16])
 def test_flash_prefill_contiguous(dev, dtype, group):
     announce(f"flash prefill contiguous {dtype} group {group}")
     g = torch.Generator().manual_seed(90 + group)
@@ -287,7 +288,8 @@ def test_attention_layer_mixed_batch(dev, mode, route):
 
 
 @pytest.mark.parametrize("kv,qdt", [(torch.bfloat16, torch.float32), (torch.bfloat16, torch.float16),
-                                    (torch.float16, torch.float32)])
+                                    (torch.float16, torch.float32), (torch.float32, torch.bfloat16),
+                                    (torch.float32, torch.float16)])
 def test_prefill_q_dtype_differs_from_cache(dev, kv, qdt):
     """q in another dtype than the cache: a bf16 cache with an fp32 / fp16 q
     takes the split (hi + lo) q path."""
@@ -299,3 +301,135 @@ def test_prefill_q_dtype_differs_from_cache(dev, kv, qdt):
     want = R.paged_prefill_ref(q.double(), k, v, bt, ctx, cu, pos, sc, 16, 4)
     assert got.dtype == qdt
     assert_close_out(got, want, got.dtype, 2e-3)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+@pytest.mark.parametrize("route", ["unified", "split", "overlap"])
+def test_attention_layer_mixed_batch_full_size(dev, kv, route):
+    """The chunked-prefill mixed batch at full size through Attention.forward:
+    8 chunks of 512 rows after priors U[0, 4096] plus 120 decode rows with
+    contexts U[256, 4096], shuffled, 32 q / 8 kv heads, block 256.  The
+    layer appends every row's own K/V (store, then attend, as the reference's
+    forward does, attention.py:1654-1760) and the output is checked against a
+    float32 torch reference over the appended cache; the appended rows are
+    checked byte for byte against the oracle's append."""
+    announce(f"Attention layer mixed batch, full size (8x512 + 120 decode), {kv} KV, {route}")
+    m = W.prefill_mixed(seed=4)
+    N, bs, Hq, Hkv = m["num_blocks"], m["block_size"], 32, 8
+    cu, pos, ctx, bt = m["cu_seqlens_q"], m["positions"], m["context_lens"], m["block_tables"]
+    qlen, is_dec = m["query_lens"], m["is_decode"]
+    T = int(cu[-1])
+    seq_of_row = torch.repeat_interleave(torch.arange(len(qlen)), torch.tensor(qlen))
+    slots = bt[seq_of_row, pos // bs].long() * bs + pos % bs
+    fp8 = kv == "fp8"
+    cdt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+    layer = A.Attention(Hq, 128, scale=1.0, num_kv_heads=Hkv, block_size=bs)
+    layer.kv_cache_dtype = "fp8_per_tensor" if fp8 else "auto"
+    layer.mixed_batch = route
+    layer.k_cache = torch.empty(N, bs, Hkv, 128, dtype=cdt, device=dev)
+    layer.v_cache = torch.empty_like(layer.k_cache)
+    ks = W.fill_pool_on_device(layer.k_cache, 51)
+    vs = W.fill_pool_on_device(layer.v_cache, 52)
+    if fp8:
+        layer.k_scale = torch.tensor([ks], device=dev)
+        layer.v_scale = torch.tensor([vs], device=dev)
+    g = torch.Generator().manual_seed(53)
+    q = torch.randn(T, Hq, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(T, Hkv, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(T, Hkv, 128, generator=g).to(torch.bfloat16)
+    split = C.split_mixed_decode_prefill_metadata(cu.tolist(), qlen, is_dec)
+    split.decode_token_indices_tensor = torch.tensor(split.decode_token_indices, device=dev)
+    split.decode_seq_indices_tensor = torch.tensor(split.decode_seq_indices, device=dev)
+    split.prefill_token_indices_tensor = torch.tensor(split.prefill_token_indices, device=dev)
+    split.prefill_seq_indices_tensor = torch.tensor(split.prefill_seq_indices, device=dev)
+    split.prefill_cu_seqlens_q_tensor = torch.tensor(split.prefill_cu_seqlens_q, dtype=torch.int32,
+                                                     device=dev)
+    assert len(split.decode_token_indices) == 120 and len(split.prefill_token_indices) == 8 * 512
+    C.set_context(True, cu_seqlens_q=cu.to(dev), max_seqlen_q=max(qlen), slot_mapping=slots.to(dev),
+                  context_lens=ctx.to(dev), block_tables=bt.to(dev), positions=pos.to(dev),
+                  mixed_attention_split=split, is_full_prefill=False)
+    try:
+        out = layer(q.to(dev), k.to(dev), v.to(dev))
+    finally:
+        C.reset_context()
+    torch.cuda.synchronize()
+    # the step's own rows landed in their slots, bytes as the oracle's append
+    sd = slots.to(dev)
+    got_k = layer.k_cache.view(-1, Hkv, 128).index_select(0, sd).cpu()
+    got_v = layer.v_cache.view(-1, Hkv, 128).index_select(0, sd).cpu()
+    if fp8:
+        assert torch.equal(got_k.view(torch.uint8), R.fp8_quantize_ref(k, ks).view(torch.uint8))
+        assert torch.equal(got_v.view(torch.uint8), R.fp8_quantize_ref(v, vs).view(torch.uint8))
+    else:
+        assert torch.equal(got_k.view(torch.int16), k.view(torch.int16))
+        assert torch.equal(got_v.view(torch.int16), v.view(torch.int16))
+    want = _torch_prefill_gpu(q.to(dev), layer.k_cache, layer.v_cache, bt.to(dev), ctx.to(dev), cu,
+                              pos.to(dev), 1 / math.sqrt(128), Hq, Hkv, ks, vs)
+    assert out.shape == (T, Hq * 128)
+    assert_close_out(out.reshape(T, Hq, 128), want, out.dtype, 2e-2 if fp8 else 2e-3)
+
+
+def test_attention_layer_fp32_auto_full_then_chunked_then_decode(dev):
+    """The reference engine's default precision: an fp32 model with 'auto'
+    (fp32) caches (model_runner.py:87, :249).  Three sequences go through a
+    full prefill (flash_attention_prefill on the fresh k/v, after the
+    append), a chunked prefill of further tokens over the cache, then two
+    decode steps, all through Attention.forward; each step's output is
+    checked against the float64 oracle on the oracle's own cache."""
+    announce("Attention layer, fp32 'auto' caches: full prefill -> chunked prefill -> decode")
+    g = torch.Generator().manual_seed(71)
+    Hq, Hkv, bs, N = 8, 2, 16, 64
+    sm = 1.0 / math.sqrt(128)
+    layer = A.Attention(Hq, 128, scale=1.0, num_kv_heads=Hkv, block_size=bs)
+    layer.k_cache = torch.zeros(N, bs, Hkv, 128, dtype=torch.float32, device=dev)
+    layer.v_cache = torch.zeros_like(layer.k_cache)
+    kcr = torch.zeros(N, bs, Hkv, 128, dtype=torch.float32)
+    vcr = torch.zeros_like(kcr)
+    tables = [torch.randperm(N, generator=g)[i * 20:(i + 1) * 20].tolist() for i in range(3)]
+    bt = torch.tensor(tables, dtype=torch.int32)
+    lens = [0, 0, 0]
+
+    def step(new_tokens, full):
+        """new_tokens[s] rows for sequence s (0 = not scheduled)."""
+        seqs = [s for s in range(3) if new_tokens[s] > 0]
+        qlen = [new_tokens[s] for s in seqs]
+        pos = torch.tensor([lens[s] + j for s in seqs for j in range(new_tokens[s])], dtype=torch.int64)
+        slots = torch.tensor([tables[s][(lens[s] + j) // bs] * bs + (lens[s] + j) % bs
+                              for s in seqs for j in range(new_tokens[s])], dtype=torch.int64)
+        for s in seqs:
+            lens[s] += new_tokens[s]
+        ctx = torch.tensor([lens[s] for s in seqs], dtype=torch.int64)
+        cu = torch.zeros(len(seqs) + 1, dtype=torch.int32)
+        cu[1:] = torch.cumsum(torch.tensor(qlen), 0).to(torch.int32)
+        T = int(cu[-1])
+        q = torch.randn(T, Hq, 128, generator=g)
+        k = torch.randn(T, Hkv, 128, generator=g)
+        v = torch.randn(T, Hkv, 128, generator=g)
+        R.store_kvcache_ref(k, v, kcr, vcr, slots)
+        btd = bt[seqs]
+        decode = all(n == 1 for n in qlen) and not full
+        if decode:
+            C.set_context(False, slot_mapping=slots.to(dev), context_lens=ctx.to(dev),
+                          block_tables=btd.to(dev))
+        else:
+            C.set_context(True, cu_seqlens_q=cu.to(dev), max_seqlen_q=max(qlen),
+                          slot_mapping=slots.to(dev), context_lens=ctx.to(dev),
+                          block_tables=btd.to(dev), positions=pos.to(dev), is_full_prefill=full)
+        try:
+            out = layer(q.to(dev), k.to(dev), v.to(dev)).cpu()
+        finally:
+            C.reset_context()
+        assert out.dtype == torch.float32
+        assert torch.equal(layer.k_cache.cpu(), kcr) and torch.equal(layer.v_cache.cpu(), vcr)
+        if decode:
+            want = R.paged_decode_ref(q.double(), kcr, vcr, btd, ctx, sm, Hq, Hkv)
+        elif full:
+            want = R.flash_prefill_ref(q.double(), k.double(), v.double(), cu, sm, Hq, Hkv)
+        else:
+            want = R.paged_prefill_ref(q.double(), kcr, vcr, btd, ctx, cu, pos, sm, Hq, Hkv)
+        assert_close_out(out.reshape(T, Hq, 128), want, torch.float32, 2e-3)
+
+    step([37, 100, 5], full=True)
+    step([20, 1, 64], full=False)
+    step([1, 1, 1], full=False)
+    step([1, 0, 1], full=False)
