@@ -45,7 +45,7 @@ KV_DESC = {"fp8": "per-tensor e4m3fn", "bf16": "bf16",
            "int8_token": "int8 codes, fp32 scale per token and kv head"}
 
 
-EXTRAS = ("append", "prefill", "latency", "producer", "mixed", "copy", "gather")
+EXTRAS = ("e2e", "append", "prefill", "latency", "producer", "mixed", "copy", "gather")
 
 
 def parse_args(argv=None):
@@ -66,7 +66,7 @@ def parse_args(argv=None):
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary measurements")
     ap.add_argument("--extra", default="all",
                     help="secondary measurements to run: 'all' or a comma list of "
-                         "append, prefill, latency, producer, mixed, copy")
+                         "e2e, append, prefill, latency, producer, mixed, copy, gather")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (5 times) and exit; "
                          "its rocprofv3 FETCH_SIZE/WRITE_SIZE calibrate the PMC byte counts")
@@ -475,6 +475,44 @@ def mixed_batch_extra(dev, stream) -> dict:
     return res
 
 
+def e2e_extra(dev) -> dict:
+    """The end-to-end engine workload: a random-init Qwen3-0.6B-shaped model
+    (28 layers, hidden 1024, 16 q / 8 kv heads, head_dim 128, intermediate
+    3072, vocab 151936, bf16 weights N(0, 0.02), seed 5) generating 256
+    tokens (temperature 1.0, EOS ignored) for each of 60 prompts of uniform
+    random token ids with lengths U[32, 512], through mkv.engine: continuous
+    batching of up to 64 sequences, chunked prefill under a 1024-token budget,
+    FP8 per-tensor KV in 256-token blocks, decode steps replayed from
+    captured graphs.  One untimed run first (graph capture, GEMM
+    heuristics), then the timed run; e2e decode tok/s = generated tokens /
+    wall time of the whole generate."""
+    import torch
+
+    from mkv import engine as E
+
+    g = torch.Generator().manual_seed(5)
+    lens = torch.randint(32, 513, (60,), generator=g).tolist()
+    prompts = [torch.randint(0, 151936, (L,), generator=g).tolist() for L in lens]
+    cfg = E.ModelConfig()
+    model = E.Qwen3Model(cfg, dev, seed=5, block_size=256)
+    eng = E.Engine(model, num_blocks=512, max_num_seqs=64, max_num_batched_tokens=1024,
+                   kv_cache_dtype="fp8_per_tensor", max_model_len=4096, seed=0)
+    eng.generate(prompts, max_tokens=256)  # warm-up: captures the decode graphs
+    eng.stats.clear()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    outs = eng.generate(prompts, max_tokens=256)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    res = eng.summary(wall)
+    assert res["generated_tokens"] == 60 * 256 and all(len(o) == 256 for o in outs)
+    res["workload"] = (f"Qwen3-0.6B shape (28 layers, hidden 1024, 16/8 heads, D 128, I 3072, vocab "
+                       f"151936), bf16 random weights; 60 prompts of {sum(lens)} tokens (32-512), "
+                       "256 output tokens each, T 1.0; max_num_seqs 64, max_num_batched_tokens "
+                       "1024, FP8 per-tensor KV, block 256, chunked prefill, captured decode")
+    return res
+
+
 def producer_extra(dev, stream) -> dict:
     """The fused producer (q/k RMSNorm + rotary + FP8 per-tensor append) for
     one layer, 16 q / 8 kv heads, head_dim 128, bf16 qkv, fp32 cos/sin table,
@@ -832,6 +870,8 @@ def main() -> int:
                 extra[f"append_copy_T{T}"]["cpu_baseline"] = cpu_copy_append_baseline(
                     w["key"], w["value"], w["slot_mapping"])
             del kp, vp
+        if "e2e" in wanted:
+            extra["e2e_engine"] = e2e_extra(dev)
         if "prefill" in wanted:
             extra["prefill_chunked"] = prefill_extra(dev, stream, cpu=args.cpu_seqs > 0)
         if "latency" in wanted:

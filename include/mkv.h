@@ -420,6 +420,30 @@ int mkv_decode_metadata(int64_t* seq_lens, int64_t* context_lens,
                         int64_t bt_stride, int max_blocks, int64_t num_blocks,
                         int block_size, int rows, int increment, void* stream);
 
+/*
+ * Decoder-layer row operations of the end-to-end engine (mkv.engine), one
+ * HBM pass each.
+ *
+ * mkv_rmsnorm replaces LayerNorm.rms_forward / residual_rms_forward
+ * (layernorm.py:16-33).  x, out: (rows, hidden) contiguous; weight:
+ * (hidden,).  If residual is non-NULL it is updated in place to
+ * round(x + residual) and normalised; otherwise x is.  With h the row being
+ * normalised: out = round(h * weight / sqrt(sum(h^2) / hidden + eps)), fp32
+ * arithmetic, one rounding to dtype.  hidden a multiple of 8, <= 2048;
+ * 16-byte aligned pointers.
+ *
+ * mkv_silu_mul replaces SiluAndMul (activation.py:16-19): x rows of
+ * 2 * inter elements (row stride x_row_stride >= 2 * inter), out (rows,
+ * inter) contiguous, out = round(silu(x[:, :inter]) * x[:, inter:]) with
+ * silu(a) = a / (1 + exp(-a)) in fp32.  inter a multiple of 8.
+ *
+ * dtype F32, BF16 or F16.
+ */
+int mkv_rmsnorm(void* out, void* residual, const void* x, const void* weight,
+                int64_t rows, int hidden, float eps, int dtype, void* stream);
+int mkv_silu_mul(void* out, const void* x, int64_t x_row_stride, int64_t rows,
+                 int inter, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

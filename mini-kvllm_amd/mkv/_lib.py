@@ -68,6 +68,9 @@ SIGNATURES: dict[str, tuple] = {
     "mkv_decode_metadata": (c_int, [
         c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int64, c_int, c_int, c_int,
         c_void_p]),
+    "mkv_rmsnorm": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_float, c_int,
+                            c_void_p]),
+    "mkv_silu_mul": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_void_p]),
     "mkv_gather_kv": (c_int, [
         c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64, c_int, c_void_p, c_int, c_int,
         c_int, c_int, c_int, c_int, c_void_p]),

@@ -1,0 +1,127 @@
+"""GPU tests of the engine slice (mkv.engine) on a 2-layer, small-vocabulary
+copy of the Qwen3 shape (head_dim 128, 4 q / 2 kv heads), FP8 per-tensor KV,
+block size 16, a token budget and a sequence cap that force chunked prefill,
+queueing and mixed decode + prefill steps.
+
+* The captured decode steps generate exactly the tokens of the same steps run
+  eagerly (same kernels on the same bucket shapes).
+* Step by step, the engine's logits match the same engine whose attention is
+  the oracle's float64 restatement of the reference's attention
+  (paged_prefill_ref / paged_decode_ref / flash_prefill_ref) on the same
+  cache, with the sampled tokens forced equal so that both see the same
+  inputs.
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from conftest import announce
+from mkv import context as C
+from mkv import engine as E
+from oracle import reference as R
+
+pytestmark = pytest.mark.gpu
+
+CFG = E.ModelConfig(vocab_size=512, hidden_size=256, num_layers=2, num_heads=4, num_kv_heads=2,
+                    head_dim=128, intermediate_size=512, max_position=4096)
+
+
+def _prompts(seed, n=6):
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(5, 101, (n,), generator=g).tolist()
+    return [torch.randint(0, CFG.vocab_size, (L,), generator=g).tolist() for L in lens]
+
+
+def _engine(dev, use_graphs=True, model_cls=E.Qwen3Model, kv="fp8_per_tensor"):
+    model = model_cls(CFG, dev, seed=5, block_size=16)
+    return E.Engine(model, num_blocks=96, max_num_seqs=4, max_num_batched_tokens=64,
+                    kv_cache_dtype=kv, max_model_len=256, seed=0, use_graphs=use_graphs)
+
+
+@pytest.mark.parametrize("kv", ["fp8_per_tensor", "auto"])
+def test_captured_decode_generates_the_eager_tokens(dev, kv):
+    announce(f"engine: captured vs eager decode, 2-layer model, {kv} KV")
+    prompts = _prompts(11)
+    outs = []
+    for graphs in (True, False):
+        eng = _engine(dev, graphs, kv=kv)
+        outs.append(eng.generate(prompts, max_tokens=12))
+        kinds = {s.kind for s in eng.stats}
+        assert kinds == {"mixed", "decode"}, kinds
+        assert all(len(o) == 12 for o in outs[-1])
+        if kv == "fp8_per_tensor":
+            assert all(float(s) != 1.0 for s in eng.model.scales()), "scales calibrated"
+    assert outs[0] == outs[1]
+
+
+class OracleAttentionModel(E.Qwen3Model):
+    """The same model with the oracle's attention on the CPU in float64 over
+    the layer's own (dequantised) cache."""
+
+    def attention(self, li, q, k, v):
+        ctx = C.current_context()
+        att = self.layers[li]["attn"]
+        Hq, Hkv = self.cfg.num_heads, self.cfg.num_kv_heads
+        sm = 1.0 / math.sqrt(self.cfg.head_dim)
+        fp8 = att.kv_cache_dtype == "fp8_per_tensor"
+        ks = float(att.k_scale) if fp8 else None
+        vs = float(att.v_scale) if fp8 else None
+        kc, vc = att.k_cache.cpu(), att.v_cache.cpu()
+        if ctx.is_prefill and ctx.is_full_prefill:
+            out = R.flash_prefill_ref(q.cpu().double(), k.cpu().double(), v.cpu().double(),
+                                      ctx.cu_seqlens_q.cpu(), sm, Hq, Hkv)
+        elif ctx.is_prefill:
+            out = R.paged_prefill_ref(q.cpu().double(), kc, vc, ctx.block_tables.cpu(),
+                                      ctx.context_lens.cpu(), ctx.cu_seqlens_q.cpu(),
+                                      ctx.positions.cpu(), sm, Hq, Hkv, ks, vs)
+        else:
+            out = R.paged_decode_ref(q.cpu().double(), kc, vc, ctx.block_tables.cpu(),
+                                     ctx.context_lens.cpu(), sm, Hq, Hkv, ks, vs)
+        return out.to(q.dtype).to(q.device).reshape(q.shape[0], Hq * self.cfg.head_dim)
+
+
+def test_engine_logits_match_the_oracle_attention_engine(dev, monkeypatch):
+    announce("engine: logits vs the same engine with oracle attention, every step")
+    prompts = _prompts(12)
+    eng = _engine(dev, True)
+    ref = _engine(dev, False, model_cls=OracleAttentionModel)
+    for e in (eng, ref):
+        for p in prompts:
+            e.add_request(p, max_tokens=6)
+    forced = {}
+    real_sample = E.sample
+
+    def sample_forced(logits, temperature, gen):
+        if "tok" in forced:
+            return forced.pop("tok")
+        return real_sample(logits, temperature, gen)
+
+    monkeypatch.setattr(E, "sample", sample_forced)
+    kinds = []
+    worst = 0.0
+    compared = 0
+    for step in range(60):
+        if eng.sched.done():
+            break
+        eng.step()
+        kinds.append(eng.stats[-1].kind)
+        sampled = eng.last_sampled
+        if sampled:  # the reference engine samples exactly the engine's tokens
+            forced["tok"] = torch.tensor(sampled, dtype=torch.int64, device=dev)
+        ref.step()
+        assert "tok" not in forced
+        assert [r.tokens for r in eng.sched.running] == [r.tokens for r in ref.sched.running]
+        if not sampled:
+            continue
+        got, want = eng.last_logits.float(), ref.last_logits.float()
+        assert got.shape == want.shape == (len(sampled), CFG.vocab_size)
+        err = float((got - want).abs().max())
+        worst = max(worst, err)
+        compared += 1
+        assert err <= 3e-2, f"step {step} ({kinds[-1]}): max logit difference {err:.3e}"
+    assert eng.sched.done() and ref.sched.done()
+    assert "mixed" in kinds and "decode" in kinds and compared >= 6, kinds
+    print(f"max logit difference over {compared} steps: {worst:.2e}")
