@@ -45,7 +45,7 @@ KV_DESC = {"fp8": "per-tensor e4m3fn", "bf16": "bf16",
            "int8_token": "int8 codes, fp32 scale per token and kv head"}
 
 
-EXTRAS = ("e2e", "append", "prefill", "latency", "producer", "mixed", "copy", "gather")
+EXTRAS = ("configs", "e2e", "append", "prefill", "latency", "producer", "mixed", "copy", "gather")
 
 
 def parse_args(argv=None):
@@ -66,7 +66,7 @@ def parse_args(argv=None):
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary measurements")
     ap.add_argument("--extra", default="all",
                     help="secondary measurements to run: 'all' or a comma list of "
-                         "e2e, append, prefill, latency, producer, mixed, copy, gather")
+                         "configs, e2e, append, prefill, latency, producer, mixed, copy, gather")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (5 times) and exit; "
                          "its rocprofv3 FETCH_SIZE/WRITE_SIZE calibrate the PMC byte counts")
@@ -402,7 +402,52 @@ def cpu_copy_append_baseline(key, value, slots) -> dict:
             "sample": f"the whole workload ({slots.numel()} tokens), median of 3: {t * 1e3:.1f} ms"}
 
 
-def mixed_batch_extra(dev, stream) -> dict:
+def cpu_mixed_baseline(q, kc, vc, m, n_decode: int = 16) -> dict:
+    """The reference's CPU path for the mixed batch on a bounded sample: its
+    first prefill chunk (paged_prefill_ref in fp32, the paged prefix
+    included) and its first n_decode decode rows (decode_torch_optimized
+    semantics, micro-batch 16), all 32 query heads; GFLOP/s of the sample's
+    algorithmic FLOPs."""
+    import torch
+
+    from mkv import workloads as W
+    from oracle import reference as R
+
+    threads = _cpu_threads()
+    cu = m["cu_seqlens_q"].tolist()
+    pre = [i for i, d in enumerate(m["is_decode"]) if not d][0]
+    dec = [i for i, d in enumerate(m["is_decode"]) if d][:n_decode]
+    seqs = [pre] + dec
+    bt = m["block_tables"][seqs]
+    used = sorted({int(x) for x in bt.flatten() if x >= 0})
+    remap = {p: i for i, p in enumerate(used)}
+    bt_c = bt.clone()
+    bt_c.apply_(lambda x: remap[x] if x >= 0 else -1)
+    idx = torch.tensor(used, device=kc.device)
+    kh, vh = kc.index_select(0, idx).cpu(), vc.index_select(0, idx).cpu()
+    ctx = m["context_lens"][seqs]
+    a, b = cu[pre], cu[pre + 1]
+    qp = q[a:b].float().cpu()
+    cu_p = torch.tensor([0, b - a], dtype=torch.int32)
+    pos_p = m["positions"][a:b]
+    qd = q[torch.tensor([cu[i] for i in dec], device=q.device)].float().cpu()
+    sm = 1.0 / math.sqrt(HEAD_DIM)
+
+    def run():
+        R.paged_prefill_ref(qp, kh, vh, bt_c[:1], ctx[:1], cu_p, pos_p, sm, 32, 8,
+                            compute_dtype=torch.float32)
+        R.decode_torch_optimized_ref(qd, kh, vh, bt_c[1:], ctx[1:], sm, 32, 8, HEAD_DIM,
+                                     m["block_size"], micro_batch=16)
+
+    t = _median_time(run)
+    fl = W.alg_flops_prefill(ctx[:1], cu_p, pos_p, 32) + int(ctx[1:].sum()) * 32 * 4 * HEAD_DIM
+    return {"value": round(fl / t / 1e9, 2), "unit": "GFLOP/s", "cores": threads, "kind": "port",
+            "sample": (f"the first prefill chunk ({b - a} rows after {int(ctx[0]) - (b - a)} tokens) and the "
+                       f"first {len(dec)} decode rows, bf16 KV upcast to fp32, median of 3: {t:.3f} s "
+                       f"({fl / 1e9:.1f} GFLOP); CPU {cpu_model()}")}
+
+
+def mixed_batch_extra(dev, stream, cpu: bool = True) -> dict:
     """Attention over the mixed-batch workload (8 prefill chunks of 512 rows
     after priors U[0, 4096] and 120 decode rows with contexts U[256, 4096],
     shuffled; 32 q / 8 kv heads, bf16 q), K/V already appended, two routes
@@ -418,6 +463,7 @@ def mixed_batch_extra(dev, stream) -> dict:
 
     m = W.prefill_mixed(seed=4)
     T = int(m["cu_seqlens_q"][-1])
+    flops = W.alg_flops_prefill(m["context_lens"], m["cu_seqlens_q"], m["positions"], 32)
     g = torch.Generator().manual_seed(5)
     q = torch.randn(T, 32, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
     split = C.split_mixed_decode_prefill_metadata(m["cu_seqlens_q"].tolist(), m["query_lens"],
@@ -459,6 +505,19 @@ def mixed_batch_extra(dev, stream) -> dict:
                 ms = time_launches(lambda i: layer(q, q, q, kv_appended=True), 20, 3, stream)
                 row[f"{route}_us"] = round(ms * 1e3, 1)
             row["best_speedup_vs_split"] = round(row["split_us"] / min(row["unified_us"], row["overlap_us"]), 2)
+            # rooflines of the default (unified) launch: the prefill rows are
+            # MFMA work, the decode rows HBM reads; both fractions are given
+            us = row["unified_us"]
+            ekv = 2 if name == "bf16" else 1
+            kv_bytes = int(m["context_lens"].sum()) * 8 * HEAD_DIM * 2 * ekv + T * 32 * HEAD_DIM * 4
+            row["roofline"] = {
+                "alg_flops": flops, "alg_kv_bytes": kv_bytes,
+                "TFLOPs": round(flops / us / 1e6, 1), "frac_of_2500_TFLOPs": round(flops / us / 1e6 / 2500, 4),
+                "GBps": round(kv_bytes / us / 1e3, 1),
+                "frac_of_8000_GBps": round(kv_bytes / us / 1e3 / PEAK_HBM_GBPS, 4),
+                "bound": "mfma" if flops / 2.5e15 > kv_bytes / 8e12 else "hbm"}
+            if name == "bf16" and cpu:
+                row["cpu_baseline"] = cpu_mixed_baseline(q, kc, vc, m)
             # the engine's step: the rows' own K/V appended first (store, then attend)
             C.set_context(True, cu_seqlens_q=m["cu_seqlens_q"].to(dev), max_seqlen_q=512,
                           slot_mapping=slots, context_lens=m["context_lens"].to(dev),
@@ -472,6 +531,170 @@ def mixed_batch_extra(dev, stream) -> dict:
             C.reset_context()
         res[f"{name}_kv"] = row
         del kc, vc
+    return res
+
+
+def graph_time_us(fn, reps: int = 20, replays: int = 10) -> float:
+    """Device time per call of fn (µs), from replays of a HIP graph that
+    holds `reps` back-to-back calls: for launches shorter than the host's
+    enqueue time, where an eager loop would time the host."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(replays):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / (reps * replays)
+
+
+def cpu_decode_baseline(q, kc, vc, bt, ctx, scale, num_heads, num_kv_heads, bs, ks, vs,
+                        nbytes: int, what: str):
+    """The reference's PyTorch decode path (decode_torch_optimized semantics,
+    benchmark_decoding.py:145-198, restated in the oracle) on host tensors,
+    micro-batches of 16 sequences, median of 3.  Returns (record, output)."""
+    from oracle import reference as R
+
+    threads = _cpu_threads()
+    out = {}
+
+    def run():
+        out["o"] = R.decode_torch_optimized_ref(q, kc, vc, bt, ctx, scale, num_heads, num_kv_heads,
+                                                HEAD_DIM, bs, ks, vs, micro_batch=16)
+
+    t = _median_time(run)
+    return ({"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+             "sample": f"{what}; median of 3: {t:.3f} s; CPU {cpu_model()}, os.cpu_count {os.cpu_count()}"},
+            out["o"])
+
+
+def configs_extra(dev, stream, cpu: bool = True) -> dict:
+    """The other decode configurations of the workload set, each with its
+    algorithmic bytes, HBM roofline fraction, the reference's CPU decode path
+    timed on the same inputs, and the largest difference from it:
+    fp32 decode at batch 4 (16 q / 8 kv heads, pool of 64 blocks, contexts
+    U[64, 2048]); FP8 decode at batch 32 (32 q / 8 kv heads) over the pool the
+    4096-token FP8 append workload leaves (every slot filled first, then the
+    append); the batch-256 decode workload with a bf16 cache."""
+    import torch
+
+    from mkv import attention as A
+    from mkv import workloads as W
+
+    res = {}
+    # fp32 decode, batch 4
+    w = W.decode_small(seed=1)
+    q, kc, vc = w["q"].to(dev), w["k_cache"].to(dev), w["v_cache"].to(dev)
+    bt, ctx = w["block_tables"].to(dev), w["context_lens"].to(dev)
+    out = torch.empty_like(q)
+    fn = lambda: A._decode(q, kc, vc, bt, ctx, w["scale"], 16, 8, HEAD_DIM, out=out)
+    us = graph_time_us(fn)
+    nb = W.alg_bytes_decode(w["context_lens"], 256, 16, 8, kv_bytes=4, q_bytes=4)
+    row = {"workload": f"fp32 KV and q, batch 4, 16 q / 8 kv heads, contexts {w['context_lens'].tolist()}",
+           "us": round(us, 2), "algorithmic_bytes": nb, "GBps": round(nb / us / 1e3, 1),
+           "frac_of_8000_GBps": round(nb / us / 1e3 / PEAK_HBM_GBPS, 4),
+           "note": "35 MB of KV: the step is launch- and latency-bound and the bytes fit the "
+                   "256 MB Infinity Cache, so this is not an HBM rate"}
+    if cpu:
+        rec, o = cpu_decode_baseline(w["q"], w["k_cache"], w["v_cache"], w["block_tables"],
+                                     w["context_lens"], w["scale"], 16, 8, 256, None, None, nb,
+                                     "the whole workload, fp32")
+        row["cpu_baseline"] = rec
+        row["max_abs_err_vs_cpu"] = float((out.cpu() - o).abs().max())
+    res["fp32_decode_b4"] = row
+    del q, kc, vc
+
+    # FP8 decode, batch 32, over the appended pool
+    w = W.decode_fp8_b32(seed=2)
+    N, bs = w["num_blocks"], w["block_size"]
+    kp = torch.zeros(N, bs, 8, HEAD_DIM, dtype=torch.float8_e4m3fn, device=dev)
+    vp = torch.zeros_like(kp)
+    ks, vs = torch.ones(1, device=dev), torch.ones(1, device=dev)
+    A.store_kvcache_fp8(w["fill_key"].to(dev), w["fill_value"].to(dev), kp, vp, ks, vs,
+                        w["fill_slots"].to(dev), bs, "fp8_per_tensor")
+    A.store_kvcache_fp8(w["key"].to(dev), w["value"].to(dev), kp, vp, ks, vs,
+                        w["slot_mapping"].to(dev), bs, "fp8_per_tensor")
+    q = w["q"].to(dev)
+    bt, ctx = w["block_tables"].to(dev), w["context_lens"].to(dev)
+    out = torch.empty_like(q)
+    fn = lambda: A._decode(q, kp, vp, bt, ctx, w["scale"], 32, 8, HEAD_DIM, ks, vs, out=out)
+    us = graph_time_us(fn)
+    nb = W.alg_bytes_decode(w["context_lens"], bs, 32, 8, kv_bytes=1)
+    row = {"workload": f"FP8 per-tensor KV (scales {float(ks):.6g} / {float(vs):.6g}), bf16 q, batch 32, "
+                       f"32 q / 8 kv heads, contexts U[256, 4096] sum {int(w['context_lens'].sum())}",
+           "us": round(us, 2), "algorithmic_bytes": nb, "GBps": round(nb / us / 1e3, 1),
+           "frac_of_8000_GBps": round(nb / us / 1e3 / PEAK_HBM_GBPS, 4)}
+    if cpu:
+        rec, o = cpu_decode_baseline(w["q"].float(), kp.cpu(), vp.cpu(), w["block_tables"],
+                                     w["context_lens"], w["scale"], 32, 8, bs, float(ks), float(vs),
+                                     nb, "the whole batch, fp32 on the dequantised cache")
+        row["cpu_baseline"] = rec
+        row["max_abs_err_vs_cpu"] = float((out.float().cpu() - o).abs().max())
+    res["fp8_decode_b32"] = row
+    del kp, vp
+
+    # bf16 decode, the batch-256 workload
+    meta = W.decode_b256_metadata(seed=3)
+    N, bs = meta["num_blocks"], meta["block_size"]
+    pools = []
+    for l in range(4):
+        kc = torch.empty(N, bs, 8, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+        vc = torch.empty_like(kc)
+        W.fill_pool_on_device(kc, 2000 + 2 * l)
+        W.fill_pool_on_device(vc, 2001 + 2 * l)
+        pools.append((kc, vc))
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(256, 32, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    bt, ctx = meta["block_tables"].to(dev), meta["context_lens"].to(dev)
+    out = torch.empty_like(q)
+    sm = 1.0 / math.sqrt(HEAD_DIM)
+
+    def step(i):
+        kc, vc = pools[i % len(pools)]
+        A._decode(q, kc, vc, bt, ctx, sm, 32, 8, HEAD_DIM, out=out)
+
+    ms, rec_settle = time_launches(step, 40, 5, stream, settle_first=True)
+    nb = W.alg_bytes_decode(meta["context_lens"], bs, 32, 8, kv_bytes=2)
+    row = {"workload": "the batch-256 decode workload (32 q / 8 kv heads, contexts log-U[512, 8192]) "
+                       "with bf16 KV, 4 rotating layer pools (16 GiB)",
+           "us": round(ms * 1e3, 2), "algorithmic_bytes": nb, "GBps": round(nb / ms / 1e6, 1),
+           "frac_of_8000_GBps": round(nb / ms / 1e6 / PEAK_HBM_GBPS, 4), "settle": rec_settle}
+    if cpu:
+        step(0)
+        torch.cuda.synchronize()
+        kc, vc = pools[0]
+        n = 32
+        used = sorted({int(x) for x in meta["block_tables"][:n].flatten() if x >= 0})
+        remap = {p: i for i, p in enumerate(used)}
+        idx = torch.tensor(used, device=dev)
+        bt_c = meta["block_tables"][:n].clone()
+        bt_c.apply_(lambda x: remap[x] if x >= 0 else -1)
+        nbs = W.alg_bytes_decode(meta["context_lens"][:n], bs, 32, 8, kv_bytes=2)
+        rec, o = cpu_decode_baseline(q[:n].float().cpu(), kc.index_select(0, idx).cpu(),
+                                     vc.index_select(0, idx).cpu(), bt_c, meta["context_lens"][:n],
+                                     sm, 32, 8, bs, None, None, nbs,
+                                     f"first {n} of 256 sequences, fp32 on the upcast bf16 cache")
+        row["cpu_baseline"] = rec
+        row["max_abs_err_vs_cpu"] = float((out[:n].float().cpu() - o).abs().max())
+    res["bf16_decode_b256"] = row
+    del pools
     return res
 
 
@@ -870,6 +1093,8 @@ def main() -> int:
                 extra[f"append_copy_T{T}"]["cpu_baseline"] = cpu_copy_append_baseline(
                     w["key"], w["value"], w["slot_mapping"])
             del kp, vp
+        if "configs" in wanted:
+            extra["decode_configs"] = configs_extra(dev, stream, cpu=args.cpu_seqs > 0)
         if "e2e" in wanted:
             extra["e2e_engine"] = e2e_extra(dev)
         if "prefill" in wanted:
@@ -879,13 +1104,11 @@ def main() -> int:
         if "producer" in wanted:
             extra["producer_fused"] = producer_extra(dev, stream)
         if "mixed" in wanted:
-            extra["mixed_batch"] = mixed_batch_extra(dev, stream)
+            extra["mixed_batch"] = mixed_batch_extra(dev, stream, cpu=args.cpu_seqs > 0)
         if "gather" in wanted:
             extra["gather_kv"] = gather_extra(layers[0][0], meta, dev, stream, cpu=args.cpu_seqs > 0)
         if "copy" in wanted:
-            copy = box_copy_gbps(dev, stream)
-            extra["box_copy_GBps"] = round(copy, 1)
-            extra["decode_frac_of_box_copy"] = round(gbps / copy, 4)
+            extra["box_copy_GBps"] = round(box_copy_gbps(dev, stream), 1)
         result["extra"] = extra
 
     if args.cpu_seqs > 0 and not per_token:

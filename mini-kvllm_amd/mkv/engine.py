@@ -45,10 +45,12 @@ from .producer import qkv_norm_rope_append
 # ---------------------------------------------------------------------------
 # Requests and scheduling (host only)
 # ---------------------------------------------------------------------------
-@dataclass
+@dataclass(eq=False)
 class Request:
     """One generation request.  ``tokens`` holds the prompt followed by the
-    generated tokens; ``num_cached`` of them have their K/V in the cache."""
+    generated tokens; ``num_cached`` of them have their K/V in the cache.
+    Requests compare by identity (membership tests on the running list must
+    not compare token lists)."""
 
     req_id: int
     prompt_len: int
