@@ -39,6 +39,7 @@ constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * kWave;
 constexpr int kRowTiles = 1;                       // 16-row MFMA tiles per wave
 constexpr int kRowsPerWg = kPfWaves * kRowTiles * 16;  // 128
+static_assert(kRowsPerWg == 2 * kWave, "the row visibility reduction assumes the rows fill waves 0 and 1");
 constexpr int kBN = 64;                            // keys per LDS tile
 // static LDS: 4 tiles of 64 keys x 256 bytes (K and V, double-buffered);
 // dynamic LDS: row visibility [128] + 4 ints, per-token scales [2][128],
@@ -90,7 +91,7 @@ struct PrefillArgs {
 constexpr int kInlineSeqs = 256;
 struct TileListLds {
   int32_t part[kInlineSeqs];
-  int64_t key[kInlineSeqs];
+  int32_t key[kInlineSeqs];
   int32_t ord[kInlineSeqs];
   int32_t ts[kInlineSeqs + 1];   // tile prefix over the visiting order
   int32_t cu[kInlineSeqs + 1];   // cu_seqlens_q
@@ -111,7 +112,7 @@ MKV_DEV void build_tile_list(TileListLds& L, const int32_t* __restrict__ cu, con
     L.ctx[t] = (int32_t)(c < 0x7fffffff ? c : 0x7fffffff);
   }
   __syncthreads();
-  int64_t kk = -1;
+  int32_t kk = -1;
   if (t < n) {
     const int32_t len = L.cu[t + 1] - L.cu[t];
     if (len > 0) kk = context_lens ? L.ctx[t] : len;
@@ -121,7 +122,7 @@ MKV_DEV void build_tile_list(TileListLds& L, const int32_t* __restrict__ cu, con
   if (t < n) {  // stable rank, longest first
     int r = 0;
     for (int j = 0; j < n; ++j) {
-      const int64_t kj = L.key[j];
+      const int32_t kj = L.key[j];
       r += (kj > kk) || (kj == kk && j < t);
     }
     L.ord[r] = t;
@@ -130,16 +131,30 @@ MKV_DEV void build_tile_list(TileListLds& L, const int32_t* __restrict__ cu, con
   const int s = t < n ? L.ord[t] : 0;
   const int32_t len = t < n ? L.cu[s + 1] - L.cu[s] : 0;
   const int32_t nt = len > 0 ? (len + tok_per_wg - 1) / tok_per_wg : 0;
-  if (t < kInlineSeqs) L.part[t] = nt;
-  __syncthreads();
-  for (int off = 1; off < kInlineSeqs; off <<= 1) {  // Hillis-Steele inclusive scan
-    const int32_t add = t < kInlineSeqs && t >= off ? L.part[t - off] : 0;
-    __syncthreads();
-    if (t < kInlineSeqs) L.part[t] += add;
-    __syncthreads();
+  // Inclusive scan of nt over the kInlineSeqs entries: each of the first
+  // kInlineSeqs / 64 waves scans its 64 entries with lane shuffles, then adds
+  // the totals of the waves before it (one barrier, where a workgroup-wide
+  // Hillis-Steele scan takes two per step).
+  const int lane = t & 63;
+  int32_t incl = nt;
+  if (t < kInlineSeqs) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int32_t y = __shfl_up(incl, off);
+      if (lane >= off) incl += y;
+    }
+    if (lane == 63) L.part[t >> 6] = incl;
   }
-  if (t < n) L.ts[t] = L.part[t] - nt;
-  if (t == 0) L.ts[n] = L.part[kInlineSeqs - 1];
+  __syncthreads();
+  int32_t total = 0;
+#pragma unroll
+  for (int w = 0; w < kInlineSeqs / 64; ++w) {
+    const int32_t p = L.part[w];
+    if (w < (t >> 6)) incl += p;
+    total += p;
+  }
+  if (t < n) L.ts[t] = incl - nt;
+  if (t == 0) L.ts[n] = total;
   __syncthreads();
 }
 
@@ -284,16 +299,15 @@ struct WgWork {
   int seq;
   int64_t q_seq0;  // first query row of the sequence
   int64_t q0, q1;  // the workgroup's query rows [q0, q1)
+  int64_t ctx;     // keys of the sequence (paged: its clamped context length)
   int min_vis, max_vis;
 };
 
 // Looks up the workgroup's tile (XCD-aware order over the longest-first
-// tile list) and fills vis_lds[row] (0 for padding rows).  Returns false,
-// uniformly over the workgroup, when it has no tile.  Holds barriers: every
-// thread of the workgroup must call it.
+// tile list).  Returns false, uniformly over the workgroup, when it has no
+// tile.  Holds barriers: every thread of the workgroup must call it.
 template <bool PAGED>
-MKV_DEV bool wg_work(const PrefillArgs& a, char* smem, int* vis_lds, int* red_lds, WgWork& w) {
-  const int tid = threadIdx.x;
+MKV_DEV bool wg_tile(const PrefillArgs& a, char* smem, WgWork& w) {
   // XCD-aware order: with a multiple of 8 KV heads every XCD takes whole
   // heads (consecutive logical tiles share an XCD and its L2, and each XCD
   // sees the same longest-first mix); otherwise the tiles are dealt round
@@ -341,11 +355,23 @@ MKV_DEV bool wg_work(const PrefillArgs& a, char* smem, int* vis_lds, int* red_ld
       ctx = q_seq1 - q_seq0;
     }
   }
-  const int64_t q0 = q_seq0 + tile * (int64_t)a.tok_per_wg;
-  const int64_t q1 = q0 + a.tok_per_wg < q_seq1 ? q0 + a.tok_per_wg : q_seq1;
-  const int G = a.group;
+  w.kvh = kvh;
+  w.seq = seq;
+  w.q_seq0 = q_seq0;
+  w.q0 = q_seq0 + tile * (int64_t)a.tok_per_wg;
+  w.q1 = w.q0 + a.tok_per_wg < q_seq1 ? w.q0 + a.tok_per_wg : q_seq1;
+  w.ctx = ctx;
+  return true;
+}
 
-  // Visible length of every row (0 for padding rows), and the WG's min / max.
+// The number of keys each of the workgroup's kRowsPerWg rows sees, in
+// vis_lds[row] (0 for padding rows), and their min / max over the real rows.
+// Holds a barrier: every thread of the workgroup must call it.
+template <bool PAGED>
+MKV_DEV void wg_rows(const PrefillArgs& a, int* vis_lds, int* red_lds, WgWork& w) {
+  const int tid = threadIdx.x;
+  const int64_t q0 = w.q0, q1 = w.q1, q_seq0 = w.q_seq0, ctx = w.ctx;
+  const int G = a.group;
   if (tid < kRowsPerWg) {
     const int64_t tok = q0 + tid / G;
     int vis = 0;
@@ -355,25 +381,24 @@ MKV_DEV bool wg_work(const PrefillArgs& a, char* smem, int* vis_lds, int* red_ld
       vis = v < 0 ? 0 : (int)v;
     }
     vis_lds[tid] = vis;
-  }
-  if (tid == 0) {
-    red_lds[0] = 0x7fffffff;
-    red_lds[1] = 0;
+    // min / max over the real rows: the rows are waves 0 and 1; each reduces
+    // its 64 with lane shuffles and writes one pair (LDS atomics from every
+    // row to one address serialise: ~7 us per workgroup)
+    const bool real = tid < a.tok_per_wg * G && tok < q1;
+    int mn = real ? vis : 0x7fffffff, mx = real ? vis : 0;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      mn = min(mn, __shfl_xor(mn, off));
+      mx = max(mx, __shfl_xor(mx, off));
+    }
+    if ((tid & 63) == 0) {
+      red_lds[2 * (tid >> 6)] = mn;
+      red_lds[2 * (tid >> 6) + 1] = mx;
+    }
   }
   __syncthreads();
-  if (tid < kRowsPerWg && tid < a.tok_per_wg * G && q0 + tid / G < q1) {
-    atomicMin(&red_lds[0], vis_lds[tid]);
-    atomicMax(&red_lds[1], vis_lds[tid]);
-  }
-  __syncthreads();
-  w.kvh = kvh;
-  w.seq = seq;
-  w.q_seq0 = q_seq0;
-  w.q0 = q0;
-  w.q1 = q1;
-  w.min_vis = red_lds[0];
-  w.max_vis = red_lds[1];
-  return true;
+  w.min_vis = min(red_lds[0], red_lds[2]);
+  w.max_vis = max(red_lds[1], red_lds[3]);
 }
 
 // LDS geometry of one K or V tile: kBN key rows of 256 bytes (128 16-bit
@@ -444,20 +469,19 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const int c = lane & 15, kg = lane >> 4;
 
   WgWork wk;
-  if (!wg_work<PAGED>(a, smem, vis_lds, red_lds, wk)) return;
+  if (!wg_tile<PAGED>(a, smem, wk)) return;
   const int kvh = wk.kvh, seq = wk.seq;
   const int64_t q_seq0 = wk.q_seq0, q0 = wk.q0, q1 = wk.q1;
-  const int min_vis = wk.min_vis, max_vis = wk.max_vis;
   const int G = a.group;
 
   // Query rows of this wave: row tile rt covers rows (kRowTiles*wave + rt)*16 + 0..15.
-  int vis_c[kRowTiles];
+  // q is loaded before the rows' visibility is worked out, so that its
+  // latency overlaps that phase.
   float qf[kRowTiles][32];
   float qmax = 0.0f;
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt) {
     const int row = (kRowTiles * wave + rt) * 16 + c;
-    vis_c[rt] = vis_lds[row];
     const int64_t tok = q0 + row / G;
     const bool ok = row < a.tok_per_wg * G && tok < q1;
     if (ok) {
@@ -472,6 +496,11 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
 #pragma unroll
     for (int i = 0; i < 32; ++i) qmax = fmaxf(qmax, fabsf(qf[rt][i]));
   }
+  wg_rows<PAGED>(a, vis_lds, red_lds, wk);
+  const int min_vis = wk.min_vis, max_vis = wk.max_vis;
+  int vis_c[kRowTiles];
+#pragma unroll
+  for (int rt = 0; rt < kRowTiles; ++rt) vis_c[rt] = vis_lds[(kRowTiles * wave + rt) * 16 + c];
   float score_mul = a.sm_scale * kLog2e;
   if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) score_mul *= load_uniform_f32(a.k_scale);
   if constexpr (CT != MKV_DTYPE_BF16) {
@@ -928,6 +957,46 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
 #undef VBUF
   // ---- normalise and write rows 4kg + r of each row tile ----
   const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
+  static_assert(kRowTiles == 1, "the staged epilogue holds one 16-row tile per wave");
+  if (a.q_dtype != MKV_DTYPE_F32) {
+    // 16-bit outputs: the wave's 16 x 128 tile is staged in LDS (free after
+    // the last tile's barrier; 4 KB per wave, 256-byte rows with 16-byte
+    // chunk ch of row rr stored at position ch ^ rr, so that the four rows of
+    // a write are on distinct banks) and written as whole 16-byte chunks, 4
+    // stores per lane instead of 32 two-byte ones.
+    char* stage = (kDma ? (wave < 4 ? lds_k0 : lds_v0) : lds_kv) + (kDma ? (wave & 3) : wave) * 4096;
+    const bool bf = a.q_dtype == MKV_DTYPE_BF16;
+    float l_col = l_run[0] + __shfl_xor(l_run[0], 16);
+    l_col += __shfl_xor(l_col, 32);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float lh = __shfl(l_col, 4 * kg + r);
+      const float inv = lh > 0.0f ? v_mul / lh : 0.0f;
+      const int rr = 4 * kg + r;
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) {
+        const float x = acc[0][mm][r] * inv;
+        const uint16_t h = (uint16_t)(bf ? f32_to_bf16_bits(x) : f32_to_f16_bits(x));
+        const int ch = 2 * mm + (c >> 3);
+        *reinterpret_cast<uint16_t*>(stage + rr * 256 + ((ch ^ rr) << 4) + 2 * (c & 7)) = h;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's staging writes are done
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int ci = 64 * u + lane;
+      const int rr = ci >> 4, ch = ci & 15;
+      const int row = 16 * wave + rr;
+      const int64_t tok = q0 + row / G;
+      const u32x4 d = *reinterpret_cast<const u32x4*>(stage + rr * 256 + ((ch ^ rr) << 4));
+      if (row < a.tok_per_wg * G && tok < q1) {
+        const int hq = kvh * G + row % G;
+        st16(reinterpret_cast<uint16_t*>(a.out) + (tok * a.num_heads + hq) * kHeadDim + 8 * ch, d);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt) {
     float l_col = l_run[rt] + __shfl_xor(l_run[rt], 16);
@@ -943,14 +1012,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       // lane c holds dims 16mm + c
       const int64_t o = (tok * a.num_heads + hq) * kHeadDim + c;
 #pragma unroll
-      for (int mm = 0; mm < 8; ++mm) {
-        const float x = acc[rt][mm][r] * inv;
-        if (a.q_dtype == MKV_DTYPE_F32)
-          reinterpret_cast<float*>(a.out)[o + 16 * mm] = x;
-        else
-          reinterpret_cast<uint16_t*>(a.out)[o + 16 * mm] =
-              (uint16_t)(a.q_dtype == MKV_DTYPE_BF16 ? f32_to_bf16_bits(x) : f32_to_f16_bits(x));
-      }
+      for (int mm = 0; mm < 8; ++mm) reinterpret_cast<float*>(a.out)[o + 16 * mm] = acc[rt][mm][r] * inv;
     }
   }
 }
@@ -998,15 +1060,14 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const int c = lane & 15, kg = lane >> 4;
 
   WgWork wk;
-  if (!wg_work<PAGED>(a, smem, vis_lds, red_lds, wk)) return;
+  if (!wg_tile<PAGED>(a, smem, wk)) return;
   const int kvh = wk.kvh, seq = wk.seq;
   const int64_t q0 = wk.q0, q1 = wk.q1;
-  const int min_vis = wk.min_vis, max_vis = wk.max_vis;
   const int G = a.group;
 
-  // q of row c (dims 32 kg .. 32 kg + 31), fp32
+  // q of row c (dims 32 kg .. 32 kg + 31), fp32, loaded before the rows'
+  // visibility is worked out
   const int my_row = 16 * wave + c;
-  const int vis_row = vis_lds[my_row];
   float qf[32];
   {
     const int64_t tok = q0 + my_row / G;
@@ -1020,6 +1081,9 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
     }
   }
+  wg_rows<PAGED>(a, vis_lds, red_lds, wk);
+  const int min_vis = wk.min_vis, max_vis = wk.max_vis;
+  const int vis_row = vis_lds[my_row];
   // The loop keeps raw scores and needs score_mul > 0 (as prefill_mfma_kernel).
   float score_mul = a.sm_scale * kLog2e;
   if (!(score_mul > 0.0f) && score_mul == score_mul) {
