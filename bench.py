@@ -67,6 +67,9 @@ def parse_args(argv=None):
     ap.add_argument("--extra", default="all",
                     help="secondary measurements to run: 'all' or a comma list of "
                          "configs, e2e, append, prefill, latency, producer, mixed, copy, gather")
+    ap.add_argument("--skip-headline", action="store_true",
+                    help="run only the secondary measurements (for profiling them); the printed "
+                         "line then has no headline value")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (5 times) and exit; "
                          "its rocprofv3 FETCH_SIZE/WRITE_SIZE calibrate the PMC byte counts")
@@ -1009,55 +1012,59 @@ def main() -> int:
 
     nbytes = W.alg_bytes_decode(meta["context_lens"], bs, Hq, Hkv, kv_bytes=kv_dtype.itemsize,
                                 scale_bytes=4 if per_token else 0)
-    torch.cuda.synchronize()
-    t_wall = time.perf_counter()
-    ms, settle_rec = time_launches(step, args.steps, args.warmup, stream, settle_first=True)
-    t_wall = time.perf_counter() - t_wall
-    gbps = nbytes / (ms * 1e-3) / 1e9
-    pct = step_percentiles(step, 100, stream)
-    if args.split_tokens > 0 or args.batch > 8192:
-        split = mkv._lib.query("mkv_paged_decode_split_tokens", args.batch, Hkv, meta["max_blocks"], bs,
-                               args.split_tokens)
-        schedule = f"split-K, {split}-token splits (paged_decode_mfma16_kernel + paged_decode_merge_kernel)"
+    if args.skip_headline:
+        # a profiling run of the extras: the headline step is not timed
+        result = {"headline": "skipped (--skip-headline)"}
     else:
-        schedule = ("stream-K over 32-token tile columns, persistent grid, groups of Hkv waves "
-                    "with one KV head per wave (paged_decode_stream_kernel + paged_decode_stream_merge_kernel)")
+        torch.cuda.synchronize()
+        t_wall = time.perf_counter()
+        ms, settle_rec = time_launches(step, args.steps, args.warmup, stream, settle_first=True)
+        t_wall = time.perf_counter() - t_wall
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        pct = step_percentiles(step, 100, stream)
+        if args.split_tokens > 0 or args.batch > 8192:
+            split = mkv._lib.query("mkv_paged_decode_split_tokens", args.batch, Hkv, meta["max_blocks"], bs,
+                                   args.split_tokens)
+            schedule = f"split-K, {split}-token splits (paged_decode_mfma16_kernel + paged_decode_merge_kernel)"
+        else:
+            schedule = ("stream-K over 32-token tile columns, persistent grid, groups of Hkv waves "
+                        "with one KV head per wave (paged_decode_stream_kernel + paged_decode_stream_merge_kernel)")
 
-    result = {
-        "metric": METRIC,
-        "value": round(gbps, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": {"fp8": "fp8", "bf16": "bf16", "fp8_token": "fp8", "int8_token": "int8"}[args.kv],
-        "data": "synthetic (seeded N(0,1) KV pools and queries, seeded context lengths/tables)",
-        "config": {
-            "workload": (f"paged decode attention, batch {args.batch}, {Hq} q / {Hkv} kv heads, head_dim 128, "
-                         f"block 256, ctx floor(exp(U(ln512, ln8192))) sum {int(meta['context_lens'].sum())}, "
-                         f"fragmented tables over {N} blocks, {args.kv} KV "
-                         f"({KV_DESC[args.kv]}), bf16 q/out, "
-                         f"{args.layers} rotating layer pools"),
-            "batch": args.batch, "num_heads": Hq, "num_kv_heads": Hkv, "head_dim": HEAD_DIM,
-            "block_size": bs, "schedule": schedule, "algorithmic_bytes_per_step": nbytes,
-        },
-        "roofline": {
-            "bound": "hbm", "achieved": round(gbps, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-            "frac": round(gbps / PEAK_HBM_GBPS, 4),
-            # measured for the default workload only (profiles/decode_b256_<kv>_pmc.json)
-            "traffic": (traffic_from_profiles(f"decode_b256_{args.kv}_pmc.json")
-                        if (args.batch, Hq, Hkv, args.split_tokens) == (256, 32, 8, 0) else None),
-            "timed_unit": "one decode step: main kernel + its merge kernel, HIP events on the launch stream",
-        },
-        "wall_s_timed_region": round(t_wall, 3),
-        # untimed steps after the warm-up, run until the step time is steady
-        "settle": settle_rec,
-        "step_time": pct,
-    }
+        result = {
+            "metric": METRIC,
+            "value": round(gbps, 2),
+            "unit": "GB/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms, 5),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": {"fp8": "fp8", "bf16": "bf16", "fp8_token": "fp8", "int8_token": "int8"}[args.kv],
+            "data": "synthetic (seeded N(0,1) KV pools and queries, seeded context lengths/tables)",
+            "config": {
+                "workload": (f"paged decode attention, batch {args.batch}, {Hq} q / {Hkv} kv heads, head_dim 128, "
+                             f"block 256, ctx floor(exp(U(ln512, ln8192))) sum {int(meta['context_lens'].sum())}, "
+                             f"fragmented tables over {N} blocks, {args.kv} KV "
+                             f"({KV_DESC[args.kv]}), bf16 q/out, "
+                             f"{args.layers} rotating layer pools"),
+                "batch": args.batch, "num_heads": Hq, "num_kv_heads": Hkv, "head_dim": HEAD_DIM,
+                "block_size": bs, "schedule": schedule, "algorithmic_bytes_per_step": nbytes,
+            },
+            "roofline": {
+                "bound": "hbm", "achieved": round(gbps, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                # measured for the default workload only (profiles/decode_b256_<kv>_pmc.json)
+                "traffic": (traffic_from_profiles(f"decode_b256_{args.kv}_pmc.json")
+                            if (args.batch, Hq, Hkv, args.split_tokens) == (256, 32, 8, 0) else None),
+                "timed_unit": "one decode step: main kernel + its merge kernel, HIP events on the launch stream",
+            },
+            "wall_s_timed_region": round(t_wall, 3),
+            # untimed steps after the warm-up, run until the step time is steady
+            "settle": settle_rec,
+            "step_time": pct,
+        }
 
     wanted = args.extra_set
     if wanted:
@@ -1076,7 +1083,8 @@ def main() -> int:
             vp = torch.zeros_like(kp)
             ksd = torch.tensor([0.05], device=dev)
             vsd = torch.tensor([0.05], device=dev)
-            ams = time_launches(lambda i: A._append(kd, vd, kp, vp, sd, ksd, vsd), 50, 5, stream)
+            ams, _ = time_launches(lambda i: A._append(kd, vd, kp, vp, sd, ksd, vsd), 50, 5, stream,
+                                   settle_first=True)
             ab = W.alg_bytes_append(w["slot_mapping"], 8, 2, 1)
             extra[f"append_fp8_T{T}"] = {"us": round(ams * 1e3, 2), "GBps": round(ab / ams / 1e6, 1)}
             if T == 4096 and args.cpu_seqs > 0:
@@ -1086,7 +1094,8 @@ def main() -> int:
             # the copy append (bf16 rows into a bf16 pool) on the same tokens
             kp = torch.zeros(1024, 256, 8, HEAD_DIM, dtype=torch.bfloat16, device=dev)
             vp = torch.zeros_like(kp)
-            cms = time_launches(lambda i: A._append(kd, vd, kp, vp, sd), 50, 5, stream)
+            cms, _ = time_launches(lambda i: A._append(kd, vd, kp, vp, sd), 50, 5, stream,
+                                   settle_first=True)
             cab = W.alg_bytes_append(w["slot_mapping"], 8, 2, 2)
             extra[f"append_copy_T{T}"] = {"us": round(cms * 1e3, 2), "GBps": round(cab / cms / 1e6, 1)}
             if T == 4096 and args.cpu_seqs > 0:
@@ -1111,7 +1120,7 @@ def main() -> int:
             extra["box_copy_GBps"] = round(box_copy_gbps(dev, stream), 1)
         result["extra"] = extra
 
-    if args.cpu_seqs > 0 and not per_token:
+    if args.cpu_seqs > 0 and not per_token and not args.skip_headline:
         kc0, vc0, _, scales = layers[0]
         result["cpu_baseline"] = cpu_baseline(kc0, vc0, scales, q, meta, args.cpu_seqs)
     else:

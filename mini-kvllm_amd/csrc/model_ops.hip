@@ -83,8 +83,12 @@ __global__ __launch_bounds__(kRowWaves* kWave) void rmsnorm_kernel(
   if (row >= rows) return;
   const int64_t base = row * hidden;
   const int chunks = hidden / 8;
-  float h[kMaxChunks][8];
+  float h[kMaxChunks][8], w[kMaxChunks][8];
   float ss = 0.0f;
+  // the weight is loaded with the row (one memory round trip, not two)
+#pragma unroll
+  for (int u = 0; u < kMaxChunks; ++u)
+    if (lane + 64 * u < chunks) load8<DT>(weight, 8 * (lane + 64 * u), w[u]);
 #pragma unroll
   for (int u = 0; u < kMaxChunks; ++u) {
     const int c = lane + 64 * u;
@@ -108,10 +112,9 @@ __global__ __launch_bounds__(kRowWaves* kWave) void rmsnorm_kernel(
   for (int u = 0; u < kMaxChunks; ++u) {
     const int c = lane + 64 * u;
     if (c < chunks) {
-      float w[8], y[8];
-      load8<DT>(weight, 8 * c, w);
+      float y[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) y[j] = h[u][j] * inv * w[j];
+      for (int j = 0; j < 8; ++j) y[j] = h[u][j] * inv * w[u][j];
       store8<DT>(out, base + 8 * c, y);
     }
   }
