@@ -242,6 +242,25 @@ def test_decode_stream_k_item_over_many_groups(dev, dtype):
     assert_close_out(got, want, got.dtype, TOL[dtype])
 
 
+@pytest.mark.parametrize("B,dtype", [(2048, torch.float8_e4m3fn), (4096, torch.bfloat16),
+                                     (8192, torch.float8_e4m3fn)])
+def test_decode_stream_k_large_batches(dev, B, dtype):
+    """Batches of 2048-8192 take the stream-K route with the larger
+    per-sequence prefix in LDS (above 2047 sequences the launch is sized for
+    up to 8192); short contexts with some empty rows, checked against the
+    oracle on every 61st row, and the empty rows exactly zero."""
+    announce(f"decode {dtype} stream-K batch {B}")
+    g = torch.Generator().manual_seed(75 + B)
+    ctx = torch.randint(0, 70, (B,), generator=g)
+    ctx[::37] = 0
+    q, k, v, bt, ctx, ks, vs = _case(76 + B, B, 8, 2, 16, 3 * B, 5, dtype, ctx=ctx)
+    got = _run(dev, q, k, v, bt, ctx, 0.1, 8, 2, ks, vs)
+    idx = torch.arange(0, B, 61)
+    want = _oracle(q[idx], k, v, bt[idx], ctx[idx], 0.1, 8, 2, ks, vs)
+    assert_close_out(got[idx], want, got.dtype, TOL[dtype])
+    assert torch.count_nonzero(got[ctx == 0].float()) == 0
+
+
 def test_decode_large_batch_uses_split_k_fallback(dev):
     announce("decode batch 9000 (beyond the stream-K batch cap)")
     g = torch.Generator().manual_seed(73)
