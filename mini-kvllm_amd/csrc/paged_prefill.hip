@@ -48,6 +48,17 @@ constexpr int kTileListOffset = (128 + 4) * 4 + 2 * 128 * 4;
 constexpr int kXcds = 8;
 constexpr float kNegBig = -1e30f;
 constexpr float kRescaleSlack = 8.0f;
+// bf16 P·V operands (bf16 caches): P (fp32) is split into bf16 hi + lo terms
+// (~16-bit P, two MFMAs per step) for keys below kSplitPKeys, and rounded once
+// to bf16 beyond, as the reference's flash kernel rounds it (p.to(v.dtype),
+// attention.py:432), with the row sum taken over the rounded weights.  The
+// output is then a convex combination of V rows whose weights w_i carry
+// independent relative errors |d_i| <= 2^-9: o - o* = sum_i w_i (d_i - d) v_i,
+// at most 2^-9 sum_i w_i |v_i - o*| and averaging down over many keys (a row
+// whose weight sits on one key gets that key's V exactly).  Keys past
+// kSplitPKeys are only visible to rows that see more than kSplitPKeys keys,
+// so rows with few keys, where the averaging is weakest, keep the split.
+constexpr int kSplitPKeys = 256;
 
 struct PrefillArgs {
   void* out;
@@ -589,38 +600,60 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const int lds_base2 = kEbG == 2 ? 0 : LT::offset(lds_key0, 2 * ld_ch + 1 - ld_b);
   auto lds_shift = [&](int u) { return ((ld_slot[u] & 3) - (ld_slot[0] & 3)) * 16 * LT::kRowBytes; };
 
-  // Block-table entries of the four 16-key sub-tiles of the tile at kb: one
-  // table read when a tile lies inside one block (block_size >= kBN), shared
-  // by the K and V descriptors and the key-validity test of that tile.
-  auto tile_blocks = [&](int kb, int64_t (&ph)[4]) {
+  // Block-table entries of a tile, read one tile ahead of their use by a
+  // vector load: lane l of every wave reads the entry of sub-tile l / 16
+  // (keys kb + 16 (l / 16) .. +15; a 16-key sub-tile never straddles a block,
+  // bs >= 16).  A scalar load would share its wait counter with the LDS reads
+  // of the key loop; this one is covered by the wait for the tile's DMA.
+  const int64_t bmask = PAGED ? ((int64_t)1 << a.idx.bs_log2) - 1 : 0;
+  const int32_t* bt_row = PAGED ? a.idx.block_tables + (int64_t)seq * a.idx.bt_stride : nullptr;
+  const int num_blocks32 = PAGED ? (int)min(a.idx.num_blocks, (int64_t)0x7fffffff) : 0;
+  auto entry_load = [&](int kb) -> int32_t {
     if constexpr (PAGED) {
-      if (a.idx.bs_log2 >= 6) {
-        const int64_t p = a.idx.physical_block(seq, (int64_t)kb >> a.idx.bs_log2);
-        ph[0] = ph[1] = ph[2] = ph[3] = p;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ph[j] = a.idx.physical_block(seq, (int64_t)(kb + 16 * j) >> a.idx.bs_log2);
-      }
+      const int blk = (kb + 16 * kg) >> a.idx.bs_log2;
+      return bt_row[blk < a.idx.max_blocks ? blk : 0];
     } else {
-      ph[0] = ph[1] = ph[2] = ph[3] = 0;
+      return 0;
     }
   };
-  // Descriptor of rows t0 .. t0+15 of one tensor (t0 a multiple of 16) whose
-  // block entry is phys.
-  auto sub_rsrc = [&](const char* base, int64_t t0, int64_t phys) -> __amdgpu_buffer_rsrc_t {
-    const char* p = base;
-    int num = 0;
+  // The entries of the tile at kb, validated: per lane (sub-tile l / 16) the
+  // physical block (-1 if absent), the byte offset of the sub-tile's first
+  // row in this KV head and the per-token-head scale index of key
+  // kb + l % 64; per wave the tile's present sub-tiles as bits.
+  struct SubTiles {
+    int32_t phys;
+    int64_t off;
+    int64_t sidx;
+    uint32_t present;
+  };
+  auto entry_use = [&](int kb, int32_t e) -> SubTiles {
+    const int t0 = kb + 16 * kg;
+    SubTiles st;
     if constexpr (PAGED) {
-      const int64_t bmask = ((int64_t)1 << a.idx.bs_log2) - 1;
-      if (phys >= 0) {
-        p = base + ((phys << a.idx.bs_log2) + (t0 & bmask)) * row_stride + head_bytes;
-        num = (int)(15 * row_stride + kHeadDim * kEbG);
-      }
+      const bool ok = (t0 >> a.idx.bs_log2) < a.idx.max_blocks && e >= 0 && e < num_blocks32;
+      st.phys = ok ? e : -1;
+      // token slot of the sub-tile's first key (the pool holds at most 2^32)
+      const uint32_t row = ((uint32_t)e << a.idx.bs_log2) + (uint32_t)(t0 & (int)bmask);
+      st.off = (int64_t)((uint64_t)row * (uint64_t)row_stride) + head_bytes;
+      st.sidx = (int64_t)((uint64_t)(row + (uint32_t)(lane & 15)) * (uint64_t)a.num_kv_heads) + kvh;
+      const uint64_t b = __builtin_amdgcn_ballot_w64(ok);  // bits 16j: sub-tile j
+      st.present = (uint32_t)((b & 1u) | ((b >> 15) & 2u) | ((b >> 30) & 4u) | ((b >> 45) & 8u));
     } else {
-      p = base + (q_seq0 + t0) * row_stride + head_bytes;
-      num = (int)(15 * row_stride + kHeadDim * kEbG);
+      st.phys = 0;
+      st.off = (q_seq0 + t0) * row_stride + head_bytes;
+      st.sidx = 0;
+      st.present = 0xfu;
     }
-    return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, num, 0x00020000);
+    return st;
+  };
+  // Descriptor of rows 16j .. 16j+15 of one tensor's tile (no records when
+  // the sub-tile's block is absent: its loads read zeros).
+  auto sub_rsrc = [&](const char* base, const SubTiles& st, int j) -> __amdgpu_buffer_rsrc_t {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)st.off, 16 * j);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)st.off >> 32), 16 * j);
+    const int64_t off = (int64_t)(((uint64_t)hi << 32) | lo);
+    const int num = (st.present >> j) & 1u ? (int)(15 * row_stride + kHeadDim * kEbG) : 0;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + off), (short)0, num, 0x00020000);
   };
   // 16-bit caches: tiles go straight from HBM into LDS (buffer_load ... lds,
   // 16 bytes per lane, no registers, no LDS write instructions).  One wave's
@@ -631,13 +664,12 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   static_assert(!kDma || (kSlotsPerLoad == 2 && kLoads == 4), "DMA slot layout");
   const uint32_t ld_off_dma = (uint32_t)(ld_key * row_stride + 16 * (ld_ch ^ LT::swz(ld_key)));
   const int dma_row = __builtin_amdgcn_readfirstlane(4 * (wave & 3) * LT::kRowBytes);
-  auto dma_tile = [&](int kb, const int64_t (&ph)[4], int buf) {
+  auto dma_tile = [&](int kb, const SubTiles& st, int buf) {
 #pragma unroll
     for (int u = 0; u < kLoads; ++u) {
       const int j = ld_slot[u] & 3;  // slot = 2u + wave / 4: K for u < 2, V for u >= 2
       const int64_t t0 = kb + 16 * j;
-      const int64_t phys = j == 0 ? ph[0] : (j == 1 ? ph[1] : (j == 2 ? ph[2] : ph[3]));
-      const __amdgpu_buffer_rsrc_t r = sub_rsrc(u >= 2 ? a.v : a.k, t0, phys);
+      const __amdgpu_buffer_rsrc_t r = sub_rsrc(u >= 2 ? a.v : a.k, st, j);
       const uint32_t off = (t0 + ld_key < max_vis) ? ld_off_dma : 0x80000000u;
       char* dst = (u >= 2 ? VBUF(buf) : KBUF(buf)) + 16 * j * LT::kRowBytes + dma_row;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, off, 0, 0, 0);
@@ -648,31 +680,26 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   // V scale of key tid % 64 (0 for keys past max_vis or in absent blocks;
   // every lane loads, the others from index 0, so the load is unconditional).
   float stg_sc = 0.0f;
-  auto load_scales = [&](int kb, const int64_t (&ph)[4]) {
+  auto load_scales = [&](int kb, const SubTiles& st) {
     if constexpr (kTokScale && PAGED) {
-      const int key = tid & 63;
-      const int j = key >> 4;
-      const int64_t phys = j == 0 ? ph[0] : (j == 1 ? ph[1] : (j == 2 ? ph[2] : ph[3]));
-      const int64_t t = (int64_t)kb + key;
-      const bool valid = tid < 128 && phys >= 0 && t < max_vis;
-      const int64_t slot = (phys << a.idx.bs_log2) + (t & (((int64_t)1 << a.idx.bs_log2) - 1));
+      // lane tid % 64 holds key kb + tid % 64 (sub-tile (tid % 64) / 16)
+      const bool valid = tid < 128 && st.phys >= 0 && kb + (tid & 63) < max_vis;
       const float* base = tid >= 64 ? a.v_scale : a.k_scale;
-      const float x = base[valid ? slot * a.num_kv_heads + kvh : 0];
+      const float x = base[valid ? st.sidx : 0];
       stg_sc = valid ? x : 0.0f;
     }
   };
-  auto load_tile = [&](int kb, const int64_t (&ph)[4]) {
+  auto load_tile = [&](int kb, const SubTiles& st) {
 #pragma unroll
     for (int u = 0; u < kLoads; ++u) {
       const int j = ld_slot[u] & 3;
       const bool is_v = ld_slot[u] >= 4;
       const int64_t t0 = kb + 16 * j;
-      const int64_t phys = j == 0 ? ph[0] : (j == 1 ? ph[1] : (j == 2 ? ph[2] : ph[3]));
-      const __amdgpu_buffer_rsrc_t r = sub_rsrc(is_v ? a.v : a.k, t0, phys);
+      const __amdgpu_buffer_rsrc_t r = sub_rsrc(is_v ? a.v : a.k, st, j);
       const uint32_t off = (t0 + ld_key < max_vis) ? ld_off : 0x80000000u;
       stg[u] = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     }
-    load_scales(kb, ph);
+    load_scales(kb, st);
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
@@ -739,22 +766,31 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt) wave_rows |= vis_c[rt] > 0;
   const bool wave_active = __builtin_amdgcn_ballot_w64(wave_rows) != 0;
-  int64_t ph_cur[4], ph_nxt[4];
+  // present sub-tiles of the current and the next tile; raw entries of the
+  // tile after the next (in flight)
+  uint32_t present_cur = 0xfu, present_nxt = 0xfu;
+  int32_t e_ahead = 0;
   if (n_tiles > 0) {
-    tile_blocks(0, ph_cur);
+    const SubTiles st0 = entry_use(0, entry_load(0));
+    present_cur = st0.present;
+    e_ahead = entry_load(kBN);
     if constexpr (kDma) {
-      dma_tile(0, ph_cur, 0);
+      dma_tile(0, st0, 0);
       __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     } else {
-      load_tile(0, ph_cur);
+      load_tile(0, st0);
       store_tile(0);
     }
   }
   __syncthreads();
   // The DMA path takes two tiles per trip (the inner loop unrolls fully), so
-  // each buffer index is a compile-time constant.
+  // each buffer index is a compile-time constant.  A trip is instantiated
+  // twice for bf16 operands: keys below kSplitPKeys split P into hi + lo
+  // terms, later keys take one bf16 term (see the PV step).
   constexpr int kPerTrip = kDma ? 2 : 1;
-  for (int it0 = 0; it0 < n_tiles; it0 += kPerTrip) {
+  auto trip = [&](auto split_tag, const int it0) {
+    constexpr bool kSplitP = decltype(split_tag)::value;
+    constexpr bool kRoundedSum = CT == MKV_DTYPE_BF16 && !kSplitP;
 #pragma unroll
   for (int h = 0; h < kPerTrip; ++h) {
     const int it = it0 + h;
@@ -762,18 +798,20 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     const int buf = kDma ? h : (it & 1);
     const int kb = it * kBN;
     if (it + 1 < n_tiles) {
-      tile_blocks(kb + kBN, ph_nxt);
+      const SubTiles st1 = entry_use(kb + kBN, e_ahead);
+      present_nxt = st1.present;
       if constexpr (kDma)
-        dma_tile(kb + kBN, ph_nxt, buf ^ 1);
+        dma_tile(kb + kBN, st1, buf ^ 1);
       else
-        load_tile(kb + kBN, ph_nxt);
+        load_tile(kb + kBN, st1);
+      e_ahead = entry_load(kb + 2 * kBN);
     }
     if (wave_active) {
 
     // Key sub-tile validity (16 keys never straddle a block: bs >= 16).
     bool kvalid[4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) kvalid[kt] = ph_cur[kt] >= 0;
+    for (int kt = 0; kt < 4; ++kt) kvalid[kt] = (present_cur >> kt) & 1u;
     const bool full = kb + kBN <= min_vis && kvalid[0] && kvalid[1] && kvalid[2] && kvalid[3];
 
     // ---- S^T = K Q^T ----
@@ -847,15 +885,26 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       const float m_new = mx > m_run[rt] + kRescaleSlack ? mx : m_run[rt];
       alpha[rt] = __builtin_amdgcn_exp2f(m_run[rt] - m_new);
       m_run[rt] = m_new;
+      // (a tile whose P is rounded once to bf16 adds the rounded weights to
+      // l_run in the PV step instead)
       float psum = 0.0f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           p[kt][rt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][rt][r], score_mul, -m_new));
-          psum += p[kt][rt][r];
+          if constexpr (!kRoundedSum) psum += p[kt][rt][r];
         }
       l_run[rt] = l_run[rt] * alpha[rt] + psum;
+      if constexpr (kTokScale) {
+        // per-token-head V scales of keys 16kt + 4kg + r, folded into P
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          const f32x4 vs = *reinterpret_cast<const f32x4*>(sc_lds + buf * 128 + 64 + 16 * kt + 4 * kg);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) p[kt][rt][r] *= vs[r];
+        }
+      }
       if (__builtin_amdgcn_ballot_w64(alpha[rt] != 1.0f)) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -872,12 +921,6 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     // 16mm + c): the lane group's 8 keys of its k-slice, read transposed
     // straight from LDS (ds_read_b64_tr_b16, see vt_base above).
     char* vbuf = VBUF(buf);
-    f32x4 vsc[4];  // per-token-head V scales of keys 16kt + 4kg + r (P * v_scale)
-    if constexpr (kTokScale) {
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-        vsc[kt] = *reinterpret_cast<const f32x4*>(sc_lds + buf * 128 + 64 + 16 * kt + 4 * kg);
-    }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       Op16<CT> pop[kRowTiles], plop[kRowTiles];
@@ -888,13 +931,10 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
         for (int r = 0; r < 4; ++r) {
           pv[r] = p[2 * ks][rt][r];
           pv[4 + r] = p[2 * ks + 1][rt][r];
-          if constexpr (kTokScale) {
-            pv[r] *= vsc[2 * ks][r];
-            pv[4 + r] *= vsc[2 * ks + 1][r];
-          }
         }
         pop[rt] = to_op16<CT>(pv);
         if constexpr (CT == MKV_DTYPE_BF16) {
+        if constexpr (kSplitP) {
           // second bf16 term carrying P's rounding residual (~16-bit P);
           // p - hi is exact in fp32 and one dot2 forms it: hi_pair . (-1, 0)
           // + p for the even element, . (0, -1) + p for the odd one.  The
@@ -912,6 +952,21 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
             plo[j + 1] = __builtin_amdgcn_fdot2_f32_bf16(h, neg_hi, pv[j + 1], false);
           }
           plop[rt] = to_op16<CT>(plo);
+        } else {
+          // one bf16 term: the row sum is taken over the rounded weights, so
+          // that the output is an exact convex combination of V rows whose
+          // weights are off by at most 2^-8 relative (a row whose weight sits
+          // on one key gets that key's V exactly)
+          typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+          uint32_t one_bits = 0x3f803f80u;
+          asm volatile("" : "+s"(one_bits));
+          const bf16x2 ones = __builtin_bit_cast(bf16x2, one_bits);
+          float sum = l_run[rt];
+#pragma unroll
+          for (int j = 0; j < 8; j += 2)
+            sum = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pop[rt][j], pop[rt][j + 1]}, ones, sum, false);
+          l_run[rt] = sum;
+        }
         }
       }
       // all 8 B operands read ahead of their MFMAs so that the LDS reads overlap
@@ -936,7 +991,9 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
 #pragma unroll
         for (int rt = 0; rt < kRowTiles; ++rt) {
           acc[rt][mm] = mfma16<CT>(pop[rt], Bv[mm], acc[rt][mm]);
-          if constexpr (CT == MKV_DTYPE_BF16) acc[rt][mm] = mfma16<CT>(plop[rt], Bv[mm], acc[rt][mm]);
+          if constexpr (CT == MKV_DTYPE_BF16) {
+            if constexpr (kSplitP) acc[rt][mm] = mfma16<CT>(plop[rt], Bv[mm], acc[rt][mm]);
+          }
         }
       }
     }
@@ -947,10 +1004,20 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's DMA has landed
     else if (it + 1 < n_tiles)
       store_tile(buf ^ 1);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ph_cur[j] = ph_nxt[j];
+    present_cur = present_nxt;
     __syncthreads();
   }
+  };
+  static_assert(kSplitPKeys % (2 * kBN) == 0, "the split-P tiles fill whole trips");
+  int it0 = 0;
+  if constexpr (CT == MKV_DTYPE_BF16 && !kTokScale) {
+    const int split_end = min(n_tiles, kSplitPKeys / kBN);
+    for (; it0 < split_end; it0 += kPerTrip) trip(std::true_type{}, it0);
+    for (; it0 < n_tiles; it0 += kPerTrip) trip(std::false_type{}, it0);
+  } else {
+    // fp16 operands (FP8 caches) take one term (an 11-bit P); per-token-head
+    // caches fold each key's V scale into P and keep the split on every key
+    for (; it0 < n_tiles; it0 += kPerTrip) trip(std::bool_constant<CT == MKV_DTYPE_BF16>{}, it0);
   }
 
 #undef KBUF
@@ -1411,6 +1478,9 @@ extern "C" int mkv_paged_prefill(void* out, const void* q, int q_dtype, const vo
   const int bs_log2 = ilog2_exact(block_size);
   if (bs_log2 < 4) return MKV_ERR_BAD_BLOCK_SIZE;
   if (bt_stride < max_blocks || max_blocks < 0 || num_blocks < 0) return MKV_ERR_BAD_STRIDE;
+  // token slots of the pool are indexed in 32 bits (a pool of 2^32 slots is
+  // 512 GiB per cache at one byte per element and head_dim 128)
+  if (num_blocks > ((int64_t)1 << (32 - bs_log2))) return MKV_ERR_BAD_SHAPE;
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u)
     return MKV_ERR_MISALIGNED;

@@ -170,6 +170,31 @@ def test_prefill_chunk_workload_full_size(dev, kv):
     assert_close_out(got, want, got.dtype, 2e-2 if ks else 2e-3)
 
 
+@pytest.mark.parametrize("scale", [0.3, 1.0])
+def test_prefill_peaked_attention_past_split_keys(dev, scale):
+    """bf16 caches: keys past the first 256 take one bf16 P term, with the row
+    sum over the rounded weights.  Peaked softmaxes (scale 0.3 and 1.0 on
+    N(0,1) q and k: the weight of a row sits on a few keys) over 290-1500
+    keys, paged and contiguous, stay within 2e-3 of the float64 oracle."""
+    announce(f"prefill peaked attention past 256 keys, scale {scale}")
+    q, k, v, bt, ctx, cu, pos, _, _ = _make(77, [250, 700, 1400], [64, 40, 100], 8, 2, 64,
+                                            torch.bfloat16)
+    got = _gpu(dev, q, k, v, bt, ctx, cu, pos, scale, 8, 2, None, None)
+    want = R.paged_prefill_ref(q.double(), k, v, bt, ctx, cu, pos, scale, 8, 2)
+    assert_close_out(got, want, got.dtype, 2e-3)
+    g = torch.Generator().manual_seed(78)
+    lens = [600, 1100, 300]
+    cuf = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    T = int(cuf[-1])
+    qf = torch.randn(T, 8, 128, generator=g).to(torch.bfloat16)
+    kf = torch.randn(T, 2, 128, generator=g).to(torch.bfloat16)
+    vf = torch.randn(T, 2, 128, generator=g).to(torch.bfloat16)
+    gotf = mkv.flash_attention_prefill(qf.to(dev), kf.to(dev), vf.to(dev), cuf.to(dev), scale, 8, 2,
+                                       128).cpu()
+    wantf = R.flash_prefill_ref(qf.double(), kf.double(), vf.double(), cuf, scale, 8, 2)
+    assert_close_out(gotf, wantf, gotf.dtype, 2e-3)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("group", [1, 4, 16])
 def test_flash_prefill_contiguous(dev, dtype, group):
