@@ -48,17 +48,12 @@ constexpr int kTileListOffset = (128 + 4) * 4 + 2 * 128 * 4;
 constexpr int kXcds = 8;
 constexpr float kNegBig = -1e30f;
 constexpr float kRescaleSlack = 8.0f;
-// bf16 P·V operands (bf16 caches): P (fp32) is split into bf16 hi + lo terms
-// (~16-bit P, two MFMAs per step) for keys below kSplitPKeys, and rounded once
-// to bf16 beyond, as the reference's flash kernel rounds it (p.to(v.dtype),
-// attention.py:432), with the row sum taken over the rounded weights.  The
-// output is then a convex combination of V rows whose weights w_i carry
-// independent relative errors |d_i| <= 2^-9: o - o* = sum_i w_i (d_i - d) v_i,
-// at most 2^-9 sum_i w_i |v_i - o*| and averaging down over many keys (a row
-// whose weight sits on one key gets that key's V exactly).  Keys past
-// kSplitPKeys are only visible to rows that see more than kSplitPKeys keys,
-// so rows with few keys, where the averaging is weakest, keep the split.
-constexpr int kSplitPKeys = 256;
+// bf16 P·V operands: bf16 holds P to 8 bits, so P (fp32) is split into bf16
+// hi + lo terms (~16-bit P, two MFMAs per step) on every key.  One term (the
+// reference's flash kernel rounds P once, p.to(v.dtype), attention.py:432)
+// misses 2e-3 where a row's weight sits on two or three keys: the error is
+// ~2^-9 * w_i w_j |v_i - v_j|.  fp16 operands (FP8 caches) take one term, an
+// 11-bit P.
 
 struct PrefillArgs {
   void* out;
@@ -784,13 +779,9 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   }
   __syncthreads();
   // The DMA path takes two tiles per trip (the inner loop unrolls fully), so
-  // each buffer index is a compile-time constant.  A trip is instantiated
-  // twice for bf16 operands: keys below kSplitPKeys split P into hi + lo
-  // terms, later keys take one bf16 term (see the PV step).
+  // each buffer index is a compile-time constant.
   constexpr int kPerTrip = kDma ? 2 : 1;
-  auto trip = [&](auto split_tag, const int it0) {
-    constexpr bool kSplitP = decltype(split_tag)::value;
-    constexpr bool kRoundedSum = CT == MKV_DTYPE_BF16 && !kSplitP;
+  for (int it0 = 0; it0 < n_tiles; it0 += kPerTrip) {
 #pragma unroll
   for (int h = 0; h < kPerTrip; ++h) {
     const int it = it0 + h;
@@ -847,8 +838,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     // The scores stay unscaled (score_mul > 0): the max of the scaled scores
     // is the scaled max of the raw ones (rounding a product by a positive
     // constant is monotonic), and each P takes one FMA.
-    float p[4][kRowTiles][4];
-    float alpha[kRowTiles];
+    float l_scaled[kRowTiles];
     // per-token-head K scales of this lane's keys 16kt + 4kg + r
     if constexpr (kTokScale) {
 #pragma unroll
@@ -883,19 +873,41 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       // exact and in range in bf16/fp16; the output rescale below then runs
       // only in a row's first tiles.  The result is the same softmax.
       const float m_new = mx > m_run[rt] + kRescaleSlack ? mx : m_run[rt];
-      alpha[rt] = __builtin_amdgcn_exp2f(m_run[rt] - m_new);
+      const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_new);
       m_run[rt] = m_new;
-      // (a tile whose P is rounded once to bf16 adds the rounded weights to
-      // l_run in the PV step instead)
+      l_scaled[rt] = l_run[rt] * alpha;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float ar = __shfl(alpha, 4 * kg + r);
+#pragma unroll
+          for (int mm = 0; mm < 8; ++mm) acc[rt][mm][r] *= ar;
+        }
+      }
+    }
+
+    // ---- P = exp2(score - m) and O += P V, 32 keys per MFMA k-step ----
+    // B operand of output-dim tile mm (dims 16mm .. 16mm+15, lane c -> dim
+    // 16mm + c): the lane group's 8 keys of its k-slice, read transposed
+    // straight from LDS (ds_read_b64_tr_b16, see vt_base above).
+    char* vbuf = VBUF(buf);
+    // (a lambda: written inline, the same step leaves the compiler's register
+    // allocation spilling in the per-token-head variants)
+    auto pv_step = [&](auto split_tag) {
+    constexpr bool kSplitP = decltype(split_tag)::value;
+    float p[4][kRowTiles][4];
+#pragma unroll
+    for (int rt = 0; rt < kRowTiles; ++rt) {
+      const float m_new = m_run[rt];
       float psum = 0.0f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           p[kt][rt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][rt][r], score_mul, -m_new));
-          if constexpr (!kRoundedSum) psum += p[kt][rt][r];
+          psum += p[kt][rt][r];
         }
-      l_run[rt] = l_run[rt] * alpha[rt] + psum;
+      l_run[rt] = l_scaled[rt] + psum;
       if constexpr (kTokScale) {
         // per-token-head V scales of keys 16kt + 4kg + r, folded into P
 #pragma unroll
@@ -905,22 +917,8 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
           for (int r = 0; r < 4; ++r) p[kt][rt][r] *= vs[r];
         }
       }
-      if (__builtin_amdgcn_ballot_w64(alpha[rt] != 1.0f)) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float ar = __shfl(alpha[rt], 4 * kg + r);
-#pragma unroll
-          for (int mm = 0; mm < 8; ++mm) acc[rt][mm][r] *= ar;
-        }
-      }
     }
-
-    // ---- O += P V, 32 keys per MFMA k-step ----
     __builtin_amdgcn_s_setprio(1);
-    // B operand of output-dim tile mm (dims 16mm .. 16mm+15, lane c -> dim
-    // 16mm + c): the lane group's 8 keys of its k-slice, read transposed
-    // straight from LDS (ds_read_b64_tr_b16, see vt_base above).
-    char* vbuf = VBUF(buf);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       Op16<CT> pop[kRowTiles], plop[kRowTiles];
@@ -952,20 +950,6 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
             plo[j + 1] = __builtin_amdgcn_fdot2_f32_bf16(h, neg_hi, pv[j + 1], false);
           }
           plop[rt] = to_op16<CT>(plo);
-        } else {
-          // one bf16 term: the row sum is taken over the rounded weights, so
-          // that the output is an exact convex combination of V rows whose
-          // weights are off by at most 2^-8 relative (a row whose weight sits
-          // on one key gets that key's V exactly)
-          typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-          uint32_t one_bits = 0x3f803f80u;
-          asm volatile("" : "+s"(one_bits));
-          const bf16x2 ones = __builtin_bit_cast(bf16x2, one_bits);
-          float sum = l_run[rt];
-#pragma unroll
-          for (int j = 0; j < 8; j += 2)
-            sum = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pop[rt][j], pop[rt][j + 1]}, ones, sum, false);
-          l_run[rt] = sum;
         }
         }
       }
@@ -998,6 +982,8 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       }
     }
     __builtin_amdgcn_s_setprio(0);
+    };
+    pv_step(std::bool_constant<CT == MKV_DTYPE_BF16>{});
     }  // wave_active
 
     if constexpr (kDma)
@@ -1007,17 +993,6 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     present_cur = present_nxt;
     __syncthreads();
   }
-  };
-  static_assert(kSplitPKeys % (2 * kBN) == 0, "the split-P tiles fill whole trips");
-  int it0 = 0;
-  if constexpr (CT == MKV_DTYPE_BF16 && !kTokScale) {
-    const int split_end = min(n_tiles, kSplitPKeys / kBN);
-    for (; it0 < split_end; it0 += kPerTrip) trip(std::true_type{}, it0);
-    for (; it0 < n_tiles; it0 += kPerTrip) trip(std::false_type{}, it0);
-  } else {
-    // fp16 operands (FP8 caches) take one term (an 11-bit P); per-token-head
-    // caches fold each key's V scale into P and keep the split on every key
-    for (; it0 < n_tiles; it0 += kPerTrip) trip(std::bool_constant<CT == MKV_DTYPE_BF16>{}, it0);
   }
 
 #undef KBUF

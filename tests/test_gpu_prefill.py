@@ -171,12 +171,12 @@ def test_prefill_chunk_workload_full_size(dev, kv):
 
 
 @pytest.mark.parametrize("scale", [0.3, 1.0])
-def test_prefill_peaked_attention_past_split_keys(dev, scale):
-    """bf16 caches: keys past the first 256 take one bf16 P term, with the row
-    sum over the rounded weights.  Peaked softmaxes (scale 0.3 and 1.0 on
-    N(0,1) q and k: the weight of a row sits on a few keys) over 290-1500
-    keys, paged and contiguous, stay within 2e-3 of the float64 oracle."""
-    announce(f"prefill peaked attention past 256 keys, scale {scale}")
+def test_prefill_peaked_attention_long_context(dev, scale):
+    """Peaked softmaxes (scale 0.3 and 1.0 on N(0,1) q and k: a row's weight
+    sits on two or three keys, where a P rounded once to bf16 would miss 2e-3)
+    over 290-1500 keys, paged and contiguous, bf16, within 2e-3 of the float64
+    oracle."""
+    announce(f"prefill peaked attention, long context, scale {scale}")
     q, k, v, bt, ctx, cu, pos, _, _ = _make(77, [250, 700, 1400], [64, 40, 100], 8, 2, 64,
                                             torch.bfloat16)
     got = _gpu(dev, q, k, v, bt, ctx, cu, pos, scale, 8, 2, None, None)
