@@ -474,6 +474,11 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const int lane = tid & 63, wave = tid >> 6;
   const int c = lane & 15, kg = lane >> 4;
 
+  // The prologue (tile list, q, row visibility, first tile) and the epilogue
+  // are chains of memory round trips that need few issue slots: they run at
+  // the highest wave priority, so that the MFMA phases of the other
+  // workgroup on the CU (raised to 1 below) do not hold them back.
+  __builtin_amdgcn_s_setprio(3);
   WgWork wk;
   if (!wg_tile<PAGED>(a, smem, wk)) return;
   const int kvh = wk.kvh, seq = wk.seq;
@@ -778,6 +783,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     }
   }
   __syncthreads();
+  __builtin_amdgcn_s_setprio(0);
   // The DMA path takes two tiles per trip (the inner loop unrolls fully), so
   // each buffer index is a compile-time constant.
   constexpr int kPerTrip = kDma ? 2 : 1;
@@ -997,6 +1003,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
 
 #undef KBUF
 #undef VBUF
+  __builtin_amdgcn_s_setprio(3);
   // ---- normalise and write rows 4kg + r of each row tile ----
   const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
   static_assert(kRowTiles == 1, "the staged epilogue holds one 16-row tile per wave");
