@@ -130,27 +130,46 @@ MKV_DEV uint32_t div_nan_sign(float x, float s, float q) {
   return 1u;
 }
 
+// The quantiser's scale with its reciprocal in fp64.  x / s correctly
+// rounded to fp32 equals x * (1/s in fp64) rounded to fp32 for every fp32 x
+// and s whose quotient is a normal fp32 number (smaller quotients become
+// e4m3fn zero either way): the fp64 product is within 2^-52 (relative) of
+// x / s, while a quotient of two 24-bit numbers is either an fp32 number or
+// at least 2^-49 (relative) away from every midpoint between fp32 numbers
+// (x - m s is a nonzero multiple of 2^-49 m s for a 25-bit midpoint m), so
+// both round to the same fp32 value.  One fp64 product replaces the fp32
+// division's refinement sequence.
+struct Fp8Quant {
+  float scale;
+  double rcp;
+};
+MKV_DEV Fp8Quant fp8_quant(float scale) { return Fp8Quant{scale, 1.0 / (double)scale}; }
+
 // Four fp32 values -> four e4m3fn bytes with the per-tensor quantiser's
-// semantics: IEEE fp32 divide by the scale (correctly rounded), torch.clamp
-// to +-448 (NaN passes), round to nearest even.  NaN bytes keep the
-// converter's S.1111.111 payload with the sign of the host's NaN
+// semantics: IEEE fp32 divide by the scale (correctly rounded, as above),
+// torch.clamp to +-448 (NaN passes), round to nearest even.  NaN bytes keep
+// the converter's S.1111.111 payload with the sign of the host's NaN
 // (div_nan_sign), so the bytes equal torch's CPU cast.
-MKV_DEV uint32_t quantize4_fp8(const float* x, float scale) {
+MKV_DEV uint32_t quantize4_fp8(const float* x, const Fp8Quant& q) {
   float v[4];
-  uint32_t nan_bits = 0, nan_signs = 0;
+  bool nan = false;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const float qv = x[j] / scale;
-    nan_bits |= (qv != qv ? 0x80u : 0u) << (8 * j);
-    nan_signs |= div_nan_sign(x[j], scale, qv) << (8 * j + 7);
+    const float qv = (float)((double)x[j] * q.rcp);
+    nan |= qv != qv;
     v[j] = clamp_fp8_range(qv);
   }
-  return (pack_fp8x4(v[0], v[1], v[2], v[3]) & ~nan_bits) | nan_signs;
+  uint32_t w = pack_fp8x4(v[0], v[1], v[2], v[3]);
+  if (nan) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (v[j] != v[j]) w = (w & ~(0x80u << (8 * j))) | (div_nan_sign(x[j], q.scale, v[j]) << (8 * j + 7));
+  }
+  return w;
 }
 
-MKV_DEV u32x4 quantize16_fp8(const float (&x)[16], float scale) {
-  return u32x4{quantize4_fp8(x, scale), quantize4_fp8(x + 4, scale), quantize4_fp8(x + 8, scale),
-               quantize4_fp8(x + 12, scale)};
+MKV_DEV u32x4 quantize16_fp8(const float (&x)[16], const Fp8Quant& q) {
+  return u32x4{quantize4_fp8(x, q), quantize4_fp8(x + 4, q), quantize4_fp8(x + 8, q), quantize4_fp8(x + 12, q)};
 }
 
 // INT8 code of x for the per-token-head quantiser: y = x * inv (inv =

@@ -167,8 +167,9 @@ MKV_DEV void store_kv(const ProducerArgs& a, char* cache, float* scales, int64_t
       w1 = u32x2{quantize4_i8(o1, inv), quantize4_i8(o1 + 4, inv)};
       w2 = u32x2{quantize4_i8(o2, inv), quantize4_i8(o2 + 4, inv)};
     } else {
-      w1 = u32x2{quantize4_fp8(o1, sc), quantize4_fp8(o1 + 4, sc)};
-      w2 = u32x2{quantize4_fp8(o2, sc), quantize4_fp8(o2 + 4, sc)};
+      const Fp8Quant q = fp8_quant(sc);
+      w1 = u32x2{quantize4_fp8(o1, q), quantize4_fp8(o1 + 4, q)};
+      w2 = u32x2{quantize4_fp8(o2, q), quantize4_fp8(o2 + 4, q)};
     }
     *reinterpret_cast<u32x2*>(base + e1) = w1;
     *reinterpret_cast<u32x2*>(base + e2) = w2;

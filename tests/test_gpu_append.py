@@ -64,8 +64,33 @@ def test_fp8_encoding_exhaustive_bf16(dev, scale):
     assert np.array_equal(got, want), detail
 
 
-def test_fp8_encoding_random_fp32_inputs(dev):
-    announce("fp8 encode of random fp32 inputs over 2^-20..2^12")
+def test_fp8_encoding_exhaustive_bf16_many_scales(dev):
+    """All 65,536 bf16 patterns against torch's cast for 40 scales at once:
+    log-uniform over 2^-40..2^40, powers of two, the calibration floor
+    (bf16(1e-8) / 448), a subnormal fp32 scale and ratios near 448."""
+    announce("fp8 encode of all 65536 bf16 patterns, 40 scales")
+    g = torch.Generator().manual_seed(12)
+    scales = torch.exp2(torch.rand(28, generator=g, dtype=torch.float64) * 80 - 40).float().tolist()
+    scales += [2.0 ** -20, 2.0 ** 7, 1.0 / 448, 3.0, 1.0 / 3, 448.0 / 3, 0.1,
+               float(torch.tensor(1e-8).to(torch.bfloat16).float() / 448), 1e-40, 6.5e4, 1.17e-38, 2.0 ** 60]
+    bits = torch.from_numpy(np.arange(65536, dtype=np.uint16).view(np.int16))
+    x = bits.view(torch.bfloat16).reshape(64, 8, 128)
+    slots = torch.arange(64, dtype=torch.int64)
+    xd = x.to(dev)
+    for scale in scales:
+        kc = torch.zeros(1, 64, 8, 128, dtype=FP8, device=dev)
+        vc = torch.zeros_like(kc)
+        s = torch.full((1,), scale, device=dev)
+        A._append(xd, xd, kc, vc, slots.to(dev), s, s)
+        got = _u8(kc).reshape(-1).numpy()
+        want = R.fp8_quantize_ref(x, float(s)).view(torch.uint8).reshape(-1).numpy()
+        bad = np.nonzero(got != want)[0]
+        assert bad.size == 0, (scale, [(hex(int(bits[i]) & 0xFFFF), hex(got[i]), hex(want[i])) for i in bad[:8]])
+
+
+@pytest.mark.parametrize("scale", [0.37, 3.0e-3, 1.0 / 3])
+def test_fp8_encoding_random_fp32_inputs(dev, scale):
+    announce(f"fp8 encode of random fp32 inputs over 2^-20..2^12, scale {scale}")
     g = torch.Generator().manual_seed(11)
     T, H, D = 512, 8, 128
     mag = torch.exp2(torch.randint(-20, 12, (T, H, D), generator=g).float())
@@ -73,14 +98,14 @@ def test_fp8_encoding_random_fp32_inputs(dev):
     slots = torch.randperm(T, generator=g).to(torch.int64)
     kc = torch.zeros(2, 256, H, D, dtype=FP8, device=dev)
     vc = torch.zeros_like(kc)
-    s = torch.full((1,), 0.37, device=dev)
+    s = torch.full((1,), scale, device=dev)
     A._append(x.to(dev), x.to(dev), kc, vc, slots.to(dev), s, s)
     want = torch.zeros(2 * 256, H, D, dtype=FP8)
-    want[slots] = R.fp8_quantize_ref(x, 0.37)
+    want[slots] = R.fp8_quantize_ref(x, float(s))
     assert torch.equal(_u8(kc).reshape(-1), want.view(torch.uint8).reshape(-1))
     # the independent codec agrees on the same bytes
     assert np.array_equal(_u8(kc).reshape(-1, H, D)[slots].reshape(-1).numpy(),
-                          fp8_codec.quantize_per_tensor(x.reshape(-1).numpy(), 0.37))
+                          fp8_codec.quantize_per_tensor(x.reshape(-1).numpy(), float(s)))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
