@@ -736,7 +736,113 @@ def e2e_extra(dev) -> dict:
                        f"151936), bf16 random weights; 60 prompts of {sum(lens)} tokens (32-512), "
                        "256 output tokens each, T 1.0; max_num_seqs 64, max_num_batched_tokens "
                        "1024, FP8 per-tensor KV, block 256, chunked prefill, captured decode")
+    # the same engine with eager decode steps (no captured graphs)
+    eager = E.Engine(model, num_blocks=512, max_num_seqs=64, max_num_batched_tokens=1024,
+                     kv_cache_dtype="fp8_per_tensor", max_model_len=4096, seed=0, use_graphs=False)
+    eager.generate(prompts[:4], max_tokens=4)  # warm-up
+    eager.stats.clear()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    eager.generate(prompts, max_tokens=256)
+    torch.cuda.synchronize()
+    eres = eager.summary(time.perf_counter() - t0)
+    res["mkv_eager_engine"] = {k: eres[k] for k in ("e2e_decode_tok_s", "decode_only_tok_s", "wall_s")}
+    del eng, eager, model
+    torch.cuda.empty_cache()
+    # the same engine and workload with the reference's PyTorch attention on the GPU
+    base_model = _torch_attention_model()(cfg, dev, seed=5, block_size=256)
+    base = E.Engine(base_model, num_blocks=512, max_num_seqs=64, max_num_batched_tokens=1024,
+                    kv_cache_dtype="fp8_per_tensor", max_model_len=4096, seed=0, use_graphs=False)
+    base.generate(prompts[:4], max_tokens=4)  # warm-up
+    base.stats.clear()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    bouts = base.generate(prompts, max_tokens=256)
+    torch.cuda.synchronize()
+    bwall = time.perf_counter() - t0
+    assert all(len(o) == 256 for o in bouts)
+    bres = base.summary(bwall)
+    res["torch_attention_engine"] = {
+        "e2e_decode_tok_s": bres["e2e_decode_tok_s"], "decode_only_tok_s": bres["decode_only_tok_s"],
+        "wall_s": bres["wall_s"], "speedup_of_mkv": round(res["e2e_decode_tok_s"] / bres["e2e_decode_tok_s"], 2),
+        "speedup_of_mkv_eager": round(res["mkv_eager_engine"]["e2e_decode_tok_s"] / bres["e2e_decode_tok_s"], 2),
+        "what": "the same engine, producer, FP8 append, GEMMs and workload (eager decode steps); attention by "
+                "the reference's PyTorch semantics in fp32 on the dequantised cache on the GPU "
+                "(decode_torch_optimized, pytorch_standard_attention over the paged prefix)"}
+    del base, base_model
+    torch.cuda.empty_cache()
     return res
+
+
+def _torch_attention_model():
+    """mkv.engine's model with its attention computed by the reference's
+    PyTorch semantics on the GPU, in fp32 on dequantised K/V: decode as
+    decode_torch_optimized (benchmark_decoding.py:145-198: the batch's blocks
+    gathered into a zero-padded (B, Lmax, Hkv, D), GQA by repeat_interleave,
+    matmul, mask, softmax, matmul), prefill chunks and mixed items per
+    sequence as pytorch_standard_attention (benchmark_prefilling.py:9-52)
+    over the paged prefix with visible = min(context, position + 1)
+    (attention.py:747).  It reads the layer's own cache after the same
+    producer and append, so only the attention differs.  A baseline for the
+    end-to-end workload, which the reference's engine cannot run (FP8 KV
+    with chunked prefill raises, attention.py:1704-1708)."""
+    import torch
+
+    from mkv import context as C
+    from mkv import engine as E
+
+    class TorchAttentionModel(E.Qwen3Model):
+        def attention(self, li, q, k, v):
+            ctx = C.current_context()
+            att = self.layers[li]["attn"]
+            cfg = self.cfg
+            Hq, Hkv, D, bs = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, self.block_size
+            G = Hq // Hkv
+            sm = 1.0 / math.sqrt(D)
+            fp8 = att.kv_cache_dtype == "fp8_per_tensor"
+            kc, vc = att.k_cache, att.v_cache
+
+            def gather(idx, n_tok):  # (..., nb) block ids -> fp32 K, V (..., n_tok, Hkv, D)
+                shp = idx.shape[:-1] + (idx.shape[-1] * bs, Hkv, D)
+                kk = kc[idx].reshape(shp)[..., :n_tok, :, :].float()
+                vv = vc[idx].reshape(shp)[..., :n_tok, :, :].float()
+                if fp8:
+                    kk, vv = kk * att.k_scale, vv * att.v_scale
+                return kk, vv
+
+            out = torch.empty(q.shape[0], Hq, D, dtype=torch.float32, device=q.device)
+            qf = q.float().view(-1, Hq, D)
+            if not ctx.is_prefill:
+                lens = ctx.context_lens
+                B = lens.shape[0]
+                L = max(int(lens.max()), 1)
+                idx = ctx.block_tables[:, :(L + bs - 1) // bs].long().clamp_min(0)
+                kk, vv = gather(idx, L)
+                kk = kk.repeat_interleave(G, dim=2).permute(0, 2, 3, 1).contiguous()  # (B, Hq, D, L)
+                vv = vv.repeat_interleave(G, dim=2).permute(0, 2, 1, 3).contiguous()  # (B, Hq, L, D)
+                sc = torch.matmul(qf[:B].unsqueeze(2), kk).squeeze(2) * sm
+                mask = torch.arange(L, device=q.device)[None, :] >= lens[:, None]
+                p = torch.softmax(sc.masked_fill(mask[:, None, :], float("-inf")), -1).nan_to_num_(0.0)
+                out[:B] = torch.matmul(p.unsqueeze(2), vv).squeeze(2)
+            else:
+                cu = ctx.cu_seqlens_q.tolist()
+                lens = ctx.context_lens.tolist()
+                for si in range(len(cu) - 1):
+                    a, b, c = cu[si], cu[si + 1], int(lens[si])
+                    if b == a:
+                        continue
+                    idx = ctx.block_tables[si, :(c + bs - 1) // bs].long().clamp_min(0)
+                    kk, vv = gather(idx, c)
+                    kk = kk.repeat_interleave(G, dim=1).permute(1, 2, 0).contiguous()  # (Hq, D, c)
+                    vv = vv.repeat_interleave(G, dim=1).permute(1, 0, 2).contiguous()  # (Hq, c, D)
+                    sc = torch.matmul(qf[a:b].permute(1, 0, 2).contiguous(), kk) * sm  # (Hq, n, c)
+                    vis = torch.clamp(ctx.positions[a:b] + 1, max=c)
+                    mask = torch.arange(c, device=q.device)[None, :] >= vis[:, None]
+                    p = torch.softmax(sc.masked_fill(mask[None], float("-inf")), -1)
+                    out[a:b] = torch.matmul(p, vv).permute(1, 0, 2)
+            return out.to(q.dtype).reshape(q.shape[0], Hq * D)
+
+    return TorchAttentionModel
 
 
 def producer_extra(dev, stream) -> dict:
