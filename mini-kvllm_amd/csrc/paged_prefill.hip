@@ -370,11 +370,30 @@ MKV_DEV bool wg_tile(const PrefillArgs& a, char* smem, WgWork& w) {
   return true;
 }
 
+// Keys seen by row `row` of a workgroup over contiguous K/V (0 for padding
+// rows): visible = min(ctx, position + 1), the position counted from the
+// sequence's first query token.
+MKV_DEV int row_vis_contiguous(const PrefillArgs& a, const WgWork& w, int row) {
+  const int64_t tok = w.q0 + row / a.group;
+  if (row >= a.tok_per_wg * a.group || tok >= w.q1) return 0;
+  const int64_t v = tok - w.q_seq0 + 1;
+  return (int)(v < w.ctx ? v : w.ctx);
+}
+
 // The number of keys each of the workgroup's kRowsPerWg rows sees, in
-// vis_lds[row] (0 for padding rows), and their min / max over the real rows.
-// Holds a barrier: every thread of the workgroup must call it.
+// vis_lds[row] (0 for padding rows; paged), and their min / max over the real
+// rows.  Holds a barrier when paged: every thread of the workgroup must call
+// it.
 template <bool PAGED>
 MKV_DEV void wg_rows(const PrefillArgs& a, int* vis_lds, int* red_lds, WgWork& w) {
+  if constexpr (!PAGED) {
+    // contiguous K/V: a row's visibility grows with its token, so the real
+    // rows' min / max are those of the first and the last token, and each
+    // row's own comes from row_vis_contiguous (no LDS, no barrier)
+    w.min_vis = (int)(w.q0 - w.q_seq0 + 1 < w.ctx ? w.q0 - w.q_seq0 + 1 : w.ctx);
+    w.max_vis = (int)(w.q1 - w.q_seq0 < w.ctx ? w.q1 - w.q_seq0 : w.ctx);
+    return;
+  }
   const int tid = threadIdx.x;
   const int64_t q0 = w.q0, q1 = w.q1, q_seq0 = w.q_seq0, ctx = w.ctx;
   const int G = a.group;
@@ -511,7 +530,10 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const int min_vis = wk.min_vis, max_vis = wk.max_vis;
   int vis_c[kRowTiles];
 #pragma unroll
-  for (int rt = 0; rt < kRowTiles; ++rt) vis_c[rt] = vis_lds[(kRowTiles * wave + rt) * 16 + c];
+  for (int rt = 0; rt < kRowTiles; ++rt) {
+    const int row = (kRowTiles * wave + rt) * 16 + c;
+    vis_c[rt] = PAGED ? vis_lds[row] : row_vis_contiguous(a, wk, row);
+  }
   float score_mul = a.sm_scale * kLog2e;
   if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) score_mul *= load_uniform_f32(a.k_scale);
   if constexpr (CT != MKV_DTYPE_BF16) {
@@ -1132,7 +1154,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   }
   wg_rows<PAGED>(a, vis_lds, red_lds, wk);
   const int min_vis = wk.min_vis, max_vis = wk.max_vis;
-  const int vis_row = vis_lds[my_row];
+  const int vis_row = PAGED ? vis_lds[my_row] : row_vis_contiguous(a, wk, my_row);
   // The loop keeps raw scores and needs score_mul > 0 (as prefill_mfma_kernel).
   float score_mul = a.sm_scale * kLog2e;
   if (!(score_mul > 0.0f) && score_mul == score_mul) {

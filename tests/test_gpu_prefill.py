@@ -90,12 +90,12 @@ def test_prefill_zero_and_negative_scale(dev, dtype, scale):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("nseq,Hkv", [(40, 2), (40, 8), (300, 2)])
+@pytest.mark.parametrize("nseq,Hkv", [(40, 2), (40, 8), (64, 2), (65, 8), (100, 2), (300, 2)])
 def test_prefill_visit_order_many_tied_and_empty_sequences(dev, nseq, Hkv, dtype):
     """The tile list visits sequences longest first (ranked on the device for
-    up to 256 sequences, in batch order beyond) and each sequence's tiles last
-    first; ties, empty sequences and both grid mappings (KV heads a multiple
-    of 8 or not) must leave every row's result unchanged."""
+    up to 256 sequences, in batch order beyond) and each sequence's tiles
+    last first; ties, empty sequences and both grid mappings (KV heads a
+    multiple of 8 or not) must leave every row's result unchanged."""
     announce(f"prefill visit order: {nseq} sequences, {Hkv} kv heads, {dtype}")
     g = torch.Generator().manual_seed(500 + nseq + Hkv)
     prior = [int(x) for x in torch.tensor([0, 16, 50, 97])[torch.randint(0, 4, (nseq,), generator=g)]]
@@ -206,6 +206,27 @@ def test_flash_prefill_contiguous(dev, dtype, group):
     q = torch.randn(T, Hkv * group, 128, generator=g).to(dtype)
     k = torch.randn(T, Hkv, 128, generator=g).to(dtype)
     v = torch.randn(T, Hkv, 128, generator=g).to(dtype)
+    got = mkv.flash_attention_prefill(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), 0.08,
+                                      Hkv * group, Hkv, 128).cpu()
+    want = R.flash_prefill_ref(q.double(), k.double(), v.double(), cu, 0.08, Hkv * group, Hkv)
+    assert_close_out(got, want, got.dtype, 2e-3)
+
+
+@pytest.mark.parametrize("nseq", [60, 64, 65, 120])
+def test_flash_prefill_many_ragged_prompts(dev, nseq):
+    """Full prefill of many short prompts (the end-to-end workload's shape:
+    prompt lengths 0-200 with ties on a tile boundary and an empty prompt),
+    each row's visibility taken from its token's position."""
+    announce(f"flash prefill {nseq} ragged prompts")
+    g = torch.Generator().manual_seed(700 + nseq)
+    lens = [int(x) for x in torch.randint(0, 201, (nseq,), generator=g)]
+    lens[1] = 0
+    lens[2] = lens[5] = lens[7] = 64  # ties on a tile boundary
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    T, Hkv, group = int(cu[-1]), 2, 2
+    q = torch.randn(T, Hkv * group, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(T, Hkv, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(T, Hkv, 128, generator=g).to(torch.bfloat16)
     got = mkv.flash_attention_prefill(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), 0.08,
                                       Hkv * group, Hkv, 128).cpu()
     want = R.flash_prefill_ref(q.double(), k.double(), v.double(), cu, 0.08, Hkv * group, Hkv)
