@@ -361,6 +361,13 @@ MKV_DEV bool wg_tile(const PrefillArgs& a, char* smem, WgWork& w) {
       ctx = q_seq1 - q_seq0;
     }
   }
+  // The sequence's rows are clamped to [0, total_q): a cu_seqlens_q whose
+  // entries leave that range (the kernel cannot check them on the host
+  // without a sync) loses those rows instead of reading or writing past q
+  // and out.
+  q_seq0 = q_seq0 < 0 ? 0 : (q_seq0 > a.total_q ? a.total_q : q_seq0);
+  q_seq1 = q_seq1 < q_seq0 ? q_seq0 : (q_seq1 > a.total_q ? a.total_q : q_seq1);
+  if constexpr (!PAGED) ctx = q_seq1 - q_seq0;
   w.kvh = kvh;
   w.seq = seq;
   w.q_seq0 = q_seq0;

@@ -179,6 +179,10 @@ def _append(key, value, k_cache, v_cache, slot_mapping, k_scale=None, v_scale=No
     if k_cache.dtype != v_cache.dtype:
         raise TypeError("k_cache and v_cache must share a dtype")
     fp8 = k_cache.dtype == torch.float8_e4m3fn
+    if fp8 and (k_scale is None or v_scale is None):
+        raise ValueError("an fp8 cache needs k_scale/v_scale (store_kvcache_fp8)")
+    if slot_mapping.numel() != num_tokens:
+        raise ValueError(f"slot_mapping has {slot_mapping.numel()} entries for {num_tokens} tokens")
     if not fp8:
         # The reference's kernel casts on store; do the same cast on the GPU.
         if key.dtype != k_cache.dtype:
@@ -238,6 +242,8 @@ def _append_per_token_head(key, value, k_cache, v_cache, k_scale, v_scale, slot_
     _check_token_scales(k_scale, v_scale, k_cache)
     if k_cache.dtype != v_cache.dtype:
         raise TypeError("k_cache and v_cache must share a dtype")
+    if slot_mapping.numel() != num_tokens:
+        raise ValueError(f"slot_mapping has {slot_mapping.numel()} entries for {num_tokens} tokens")
     key, value = _one_dtype(key, value)
     key = _token_rows(key)
     value = _token_rows(value)
@@ -349,6 +355,9 @@ def _decode(query, k_cache, v_cache, block_tables, context_lens, scale, num_head
         return out
     bt = _block_table(block_tables)
     cl = _ctx_lens(context_lens)
+    if bt.dim() != 2 or bt.shape[0] < batch or cl.numel() < batch:
+        raise ValueError(f"block_tables {tuple(bt.shape)} / context_lens {tuple(cl.shape)} cover fewer "
+                         f"than the batch's {batch} sequences")
     max_blocks = bt.shape[1]
     bs = k_cache.shape[1]
     quant = k_cache.dtype in (torch.float8_e4m3fn, torch.int8)
@@ -458,6 +467,11 @@ def paged_attention_prefill_triton(query: torch.Tensor, k_cache: torch.Tensor,
     cu = cu_seqlens_q.to(torch.int32).contiguous()
     pos = positions.to(torch.int64).contiguous()
     num_seqs = cl.shape[0]
+    # (num_seqs comes from context_lens, as in attention.py:869; extra
+    # cu_seqlens_q entries are ignored, missing ones would be read past its end)
+    if cu.numel() < num_seqs + 1 or bt.dim() != 2 or bt.shape[0] < num_seqs or pos.numel() < total_q:
+        raise ValueError(f"cu_seqlens_q {tuple(cu.shape)}, block_tables {tuple(bt.shape)} and positions "
+                         f"{tuple(pos.shape)} must cover {num_seqs} sequences and {total_q} query rows")
     nbytes = _lib.query("mkv_paged_prefill_workspace_size", num_seqs, total_q, num_heads,
                         num_kv_heads)
     ws = _workspace(dev, "prefill", nbytes) if nbytes else None
@@ -489,6 +503,10 @@ def flash_attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         return out
     if not (q.dtype == k.dtype == v.dtype):
         raise TypeError("q, k and v must share one dtype")
+    if (q.dim() != 3 or tuple(q.shape[1:]) != (num_heads, head_dim) or k.shape != v.shape
+            or tuple(k.shape) != (total, num_kv_heads, head_dim)):
+        raise ValueError(f"q {tuple(q.shape)} and k/v {tuple(k.shape)} / {tuple(v.shape)} must be "
+                         f"(total, {num_heads} / {num_kv_heads}, {head_dim}) with one total")
     cu = cu_seqlens.to(torch.int32).contiguous()
     num_seqs = cu.shape[0] - 1
     nbytes = _lib.query("mkv_flash_prefill_workspace_size", num_seqs, total, num_heads,
