@@ -59,6 +59,8 @@ def qkv_norm_rope_append(qkv: torch.Tensor, positions: torch.Tensor, num_heads: 
     if T == 0:
         return q, k, v
     pos = positions.to(torch.int64).contiguous()
+    if pos.numel() < T:
+        raise ValueError(f"positions has {pos.numel()} entries for {T} tokens")
     cs = cos_sin_cache.contiguous()
     if cs.shape[-1] != head_dim:
         raise ValueError(f"cos_sin_cache must be (max_position, {head_dim})")
@@ -78,6 +80,8 @@ def qkv_norm_rope_append(qkv: torch.Tensor, positions: torch.Tensor, num_heads: 
     if append:
         _check_cache(k_cache, v_cache, num_kv_heads, head_dim)
         slots = slot_mapping.to(torch.int64).contiguous()
+        if slots.numel() != T:
+            raise ValueError(f"slot_mapping has {slots.numel()} entries for {T} tokens")
         if kv_cache_dtype in PER_TOKEN_HEAD_MODES:
             want = torch.int8 if kv_cache_dtype == "int8_per_token_head" else torch.float8_e4m3fn
             if k_cache.dtype != want:
