@@ -281,13 +281,21 @@ MKV_DEV void store_out8(void* out, int dt, int64_t off, const float* x) {
 // (v_permlane16_swap / v_permlane32_swap) that leave each lane the pair of
 // its own and its partner's value, with no LDS round trip or address
 // register.
+// The max is one v_max_f32: through fmaxf the compiler first quiets each
+// swapped operand (v_max_f32 x, x, x) since it cannot see that they hold no
+// signalling NaN; the scores, MFMA results and their maxima, never do.
+MKV_DEV float vmax_quiet(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 MKV_DEV float max_xor16(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return vmax_quiet(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 MKV_DEV float max_xor32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return vmax_quiet(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // The lane index, computed where it is used: a volatile asm pair that the
@@ -647,40 +655,48 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   };
   // The entries of the tile at kb, validated: per lane (sub-tile l / 16) the
   // physical block (-1 if absent), the byte offset of the sub-tile's first
-  // row in this KV head and the per-token-head scale index of key
-  // kb + l % 64; per wave the tile's present sub-tiles as bits.
+  // token slot of the sub-tile's first key (paged) and the per-token-head
+  // scale index of key kb + l % 64; per wave the tile's first key and its
+  // present sub-tiles as bits.
   struct SubTiles {
     int32_t phys;
-    int64_t off;
+    uint32_t row;
     int64_t sidx;
+    int kb;
     uint32_t present;
   };
   auto entry_use = [&](int kb, int32_t e) -> SubTiles {
     const int t0 = kb + 16 * kg;
     SubTiles st;
+    st.kb = kb;
     if constexpr (PAGED) {
       const bool ok = (t0 >> a.idx.bs_log2) < a.idx.max_blocks && e >= 0 && e < num_blocks32;
       st.phys = ok ? e : -1;
-      // token slot of the sub-tile's first key (the pool holds at most 2^32)
-      const uint32_t row = ((uint32_t)e << a.idx.bs_log2) + (uint32_t)(t0 & (int)bmask);
-      st.off = (int64_t)((uint64_t)row * (uint64_t)row_stride) + head_bytes;
-      st.sidx = (int64_t)((uint64_t)(row + (uint32_t)(lane & 15)) * (uint64_t)a.num_kv_heads) + kvh;
+      // (the pool holds at most 2^32 token slots)
+      st.row = ((uint32_t)e << a.idx.bs_log2) + (uint32_t)(t0 & (int)bmask);
+      st.sidx = (int64_t)((uint64_t)(st.row + (uint32_t)(lane & 15)) * (uint64_t)a.num_kv_heads) + kvh;
       const uint64_t b = __builtin_amdgcn_ballot_w64(ok);  // bits 16j: sub-tile j
       st.present = (uint32_t)((b & 1u) | ((b >> 15) & 2u) | ((b >> 30) & 4u) | ((b >> 45) & 8u));
     } else {
       st.phys = 0;
-      st.off = (q_seq0 + t0) * row_stride + head_bytes;
+      st.row = 0;
       st.sidx = 0;
       st.present = 0xfu;
     }
     return st;
   };
   // Descriptor of rows 16j .. 16j+15 of one tensor's tile (no records when
-  // the sub-tile's block is absent: its loads read zeros).
+  // the sub-tile's block is absent: its loads read zeros).  The byte offset
+  // is formed in scalar registers from the sub-tile's first row (lane 16j's
+  // slot, or the sequence's row for contiguous K/V), only in the waves that
+  // issue loads.
   auto sub_rsrc = [&](const char* base, const SubTiles& st, int j) -> __amdgpu_buffer_rsrc_t {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)st.off, 16 * j);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)st.off >> 32), 16 * j);
-    const int64_t off = (int64_t)(((uint64_t)hi << 32) | lo);
+    int64_t r64;
+    if constexpr (PAGED)
+      r64 = (uint32_t)__builtin_amdgcn_readlane((int)st.row, 16 * j);
+    else
+      r64 = q_seq0 + st.kb + 16 * j;
+    const int64_t off = r64 * row_stride + head_bytes;
     const int num = (st.present >> j) & 1u ? (int)(15 * row_stride + kHeadDim * kEbG) : 0;
     return __builtin_amdgcn_make_buffer_rsrc((void*)(base + off), (short)0, num, 0x00020000);
   };
@@ -945,7 +961,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           p[kt][rt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][rt][r], score_mul, -m_new));
-          psum += p[kt][rt][r];
+          psum = (kt | r) ? psum + p[kt][rt][r] : p[kt][rt][r];
         }
       l_run[rt] = l_scaled[rt] + psum;
       if constexpr (kTokScale) {
