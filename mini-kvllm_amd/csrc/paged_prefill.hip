@@ -298,6 +298,14 @@ MKV_DEV float max_xor32(float x) {
   return vmax_quiet(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// mask bit of the lane set ? b : a, as one v_cndmask_b32 (opaque to LLVM,
+// which folds two such selects of one vector into a dynamic index)
+MKV_DEV uint32_t lane_select(uint32_t a, uint32_t b, uint64_t mask) {
+  uint32_t r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
+  return r;
+}
+
 // The lane index, computed where it is used: a volatile asm pair that the
 // compiler can neither hoist out of a loop nor keep in a register across it.
 MKV_DEV int lane_id_volatile() {
@@ -635,6 +643,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const int ld_b = ((ld_ch >> 2) ^ ld_key) & 1;
   const int lds_base = kEbG == 2 ? LT::offset(lds_key0, ld_ch) : LT::offset(lds_key0, 2 * ld_ch + ld_b);
   const int lds_base2 = kEbG == 2 ? 0 : LT::offset(lds_key0, 2 * ld_ch + 1 - ld_b);
+  const uint64_t ld_b_mask = __builtin_amdgcn_ballot_w64(ld_b != 0);  // lanes whose first write is half 1
   auto lds_shift = [&](int u) { return ((ld_slot[u] & 3) - (ld_slot[0] & 3)) * 16 * LT::kRowBytes; };
 
   // Block-table entries of a tile, read one tile ahead of their use by a
@@ -770,13 +779,17 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
           else
             return __builtin_bit_cast(uint32_t, fp8x2_to_f16x2<kHi>(d));
         };
-        auto half = [&](int h) {
-          const uint32_t d0 = stg[u][2 * h], d1 = stg[u][2 * h + 1];
+        // (the lane's first write takes half ld_b: one v_cndmask per dword
+        // on the lanes' ld_b mask; written as selects in C++, LLVM turns them
+        // into an index 2 * ld_b, a 4-way select per dword)
+        auto half = [&](uint32_t d0, uint32_t d1) {
           return u32x4{pair(d0, std::false_type{}), pair(d0, std::true_type{}),
                        pair(d1, std::false_type{}), pair(d1, std::true_type{})};
         };
-        *reinterpret_cast<u32x4*>(dst + lds_base) = half(ld_b);
-        *reinterpret_cast<u32x4*>(dst + lds_base2) = half(1 - ld_b);
+        *reinterpret_cast<u32x4*>(dst + lds_base) =
+            half(lane_select(stg[u][0], stg[u][2], ld_b_mask), lane_select(stg[u][1], stg[u][3], ld_b_mask));
+        *reinterpret_cast<u32x4*>(dst + lds_base2) =
+            half(lane_select(stg[u][2], stg[u][0], ld_b_mask), lane_select(stg[u][3], stg[u][1], ld_b_mask));
       }
     }
     if constexpr (kTokScale)
@@ -834,15 +847,16 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   }
   __syncthreads();
   __builtin_amdgcn_s_setprio(0);
-  // The DMA path takes two tiles per trip (the inner loop unrolls fully), so
-  // each buffer index is a compile-time constant.
-  constexpr int kPerTrip = kDma ? 2 : 1;
+  // Two tiles per trip (the inner loop unrolls fully), so that each buffer
+  // index is a compile-time constant (LDS addresses fold into the read and
+  // write offsets).
+  constexpr int kPerTrip = 2;
   for (int it0 = 0; it0 < n_tiles; it0 += kPerTrip) {
 #pragma unroll
   for (int h = 0; h < kPerTrip; ++h) {
     const int it = it0 + h;
-    if (kDma && it >= n_tiles) break;
-    const int buf = kDma ? h : (it & 1);
+    if (it >= n_tiles) break;
+    const int buf = h;
     const int kb = it * kBN;
     if (it + 1 < n_tiles) {
       const SubTiles st1 = entry_use(kb + kBN, e_ahead);
