@@ -45,6 +45,7 @@ constexpr int kBN = 64;                            // keys per LDS tile
 // dynamic LDS: row visibility [128] + 4 ints, per-token scales [2][128],
 // then the inline tile list (8-aligned)
 constexpr int kTileListOffset = (128 + 4) * 4 + 2 * 128 * 4;
+static_assert(kTileListOffset % 8 == 0, "TilePick holds 64-bit fields");
 constexpr int kXcds = 8;
 constexpr float kNegBig = -1e30f;
 constexpr float kRescaleSlack = 8.0f;
@@ -91,9 +92,10 @@ struct PrefillArgs {
 // of more than 256 sequences keep their own order.  The order changes which
 // workgroup computes a tile, never the tile's result.
 // ---------------------------------------------------------------------------
-// Up to kInlineSeqs sequences: the list is built in LDS (by the scan kernel,
-// or by every prefill workgroup itself, which saves the scan launch and the
-// global lookups of the tile's sequence).
+// Up to kInlineSeqs sequences: every prefill workgroup finds its own tile
+// (pick_tile_inline: no scan launch, no global lookups of the tile's
+// sequence); the scan kernel builds the list in LDS when a caller asks for
+// the global list.
 constexpr int kInlineSeqs = 256;
 struct TileListLds {
   int32_t part[kInlineSeqs];
@@ -161,6 +163,80 @@ MKV_DEV void build_tile_list(TileListLds& L, const int32_t* __restrict__ cu, con
   }
   if (t < n) L.ts[t] = incl - nt;
   if (t == 0) L.ts[n] = total;
+  __syncthreads();
+}
+
+// The tile `tau` of the longest-first list of n <= kInlineSeqs sequences,
+// found without building the list: a sequence's first tile in that order is
+// the sum of the tile counts of the sequences before it (longer key first,
+// ties in batch order), which one pass over the n sequences gives.  Waves
+// w < ceil(n / 64) own sequences 64w + lane: each lane writes its sequence's
+// order value and tile count to LDS once, then reads all n entries with
+// uniform-address reads (LDS broadcasts, 8 entries per step, no scan, no
+// search); the one lane whose sequence holds tile tau writes it out, and
+// P.seq stays -1 when no sequence does.  ~1.7 us per workgroup less than
+// the LDS list (a rank loop waiting on one LDS read per sequence, a scan
+// and a binary search: ~3.9 us for 60 prompts).  Every thread of the
+// workgroup must call it (one barrier; two for more than 64 sequences).
+struct TilePick {
+  int32_t seq;    // -1: no tile
+  int32_t tile;   // the tile's index within its sequence's tiles
+  int64_t q_seq0, q_seq1;
+  int64_t ctx;    // clamped context length (paged)
+  uint2 ent[kInlineSeqs];  // order value, tile count (0, 0 past n)
+};
+template <bool PAGED>
+MKV_DEV void pick_tile_inline(const PrefillArgs& a, TilePick& P, int64_t tau, int64_t ctx_cap) {
+  const int t = threadIdx.x;
+  const int n = a.num_seqs;
+  const int nw = (n + 63) >> 6;
+  const bool active = t < 64 * nw;
+  // Sequence t's order value: (key + 1) * 256 + 255 - t, with the key capped
+  // at 2^23 - 2 (the cap only reorders sequences longer than 8M tokens among
+  // themselves) and key -1 for an empty sequence; sequence j comes before
+  // sequence t when its value is larger (longer key, or the same key and
+  // j < t).  n <= 256 keeps t in the low byte.
+  uint32_t ov = 0;
+  int32_t nt = 0, c0 = 0, c1 = 0, cx = 0;
+  if (active) {
+    if (t < n) {
+      c0 = a.cu_seqlens_q[t];
+      c1 = a.cu_seqlens_q[t + 1];
+      if (PAGED && a.context_lens != nullptr) {
+        int64_t c = load_index(a.context_lens, t, a.ctx_i64);
+        c = c < 0 ? 0 : (c > ctx_cap ? ctx_cap : c);
+        cx = (int32_t)(c < 0x7fffffff ? c : 0x7fffffff);
+      }
+      const int32_t len = c1 - c0;
+      if (len > 0) {
+        const int32_t key = (PAGED && a.context_lens != nullptr) ? cx : len;
+        ov = ((uint32_t)(key < (1 << 23) - 2 ? key : (1 << 23) - 2) + 1u) << 8;
+        nt = (len + a.tok_per_wg - 1) / a.tok_per_wg;
+      }
+      ov |= 255u - (uint32_t)t;
+    }
+    if (t == 0) P.seq = -1;
+    P.ent[t] = make_uint2(ov, (uint32_t)nt);
+  }
+  // (one wave: its LDS writes complete before its reads, in order)
+  if (nw > 1) __syncthreads();
+  if (active) {
+    int32_t ts = 0;
+    for (int j0 = 0; j0 < n; j0 += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const uint2 e = P.ent[j0 + u];
+        ts += e.x > ov ? (int32_t)e.y : 0;
+      }
+    }
+    if (nt > 0 && (int64_t)ts <= tau && tau < (int64_t)ts + nt) {
+      P.seq = t;
+      P.tile = ts + nt - 1 - (int32_t)tau;  // the sequence's last tile first
+      P.q_seq0 = c0;
+      P.q_seq1 = c1;
+      P.ctx = cx;
+    }
+  }
   __syncthreads();
 }
 
@@ -345,20 +421,14 @@ MKV_DEV bool wg_tile(const PrefillArgs& a, char* smem, WgWork& w) {
   int seq;
   int64_t q_seq0, q_seq1, tile, ctx;
   if (a.inline_list) {
-    TileListLds& L = *reinterpret_cast<TileListLds*>(smem + kTileListOffset);
-    build_tile_list(L, a.cu_seqlens_q, PAGED ? a.context_lens : nullptr, a.ctx_i64, cap, a.num_seqs,
-                    a.tok_per_wg);
-    if (tau >= L.ts[a.num_seqs]) return false;
-    int lo = 0, hi = a.num_seqs;  // largest k with ts[k] <= tau
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (L.ts[mid] <= tau) lo = mid; else hi = mid;
-    }
-    seq = L.ord[lo];
-    q_seq0 = L.cu[seq];
-    q_seq1 = L.cu[seq + 1];
-    tile = (int64_t)(L.ts[lo + 1] - 1) - tau;  // the sequence's last tile first
-    ctx = PAGED ? (int64_t)L.ctx[seq] : q_seq1 - q_seq0;
+    TilePick& P = *reinterpret_cast<TilePick*>(smem + kTileListOffset);
+    pick_tile_inline<PAGED>(a, P, tau, cap);
+    if (P.seq < 0) return false;
+    seq = P.seq;
+    q_seq0 = P.q_seq0;
+    q_seq1 = P.q_seq1;
+    tile = P.tile;
+    ctx = PAGED ? P.ctx : q_seq1 - q_seq0;
   } else {
     if (tau >= a.tile_start[a.num_seqs]) return false;
     int lo = 0, hi = a.num_seqs;  // largest k with tile_start[k] <= tau
@@ -1434,7 +1504,7 @@ int64_t tiles_upper_bound(int num_seqs, int64_t total_q, int group) {
 template <int KV_DT, bool PAGED, bool QSPLIT>
 int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   using LT = LdsTile<KV_DT>;
-  const size_t lds = kTileListOffset + (a.inline_list ? sizeof(TileListLds) : 0);
+  const size_t lds = kTileListOffset + (a.inline_list ? sizeof(TilePick) : 0);
   int64_t nwg = a.tiles_ub * a.num_kv_heads;
   nwg = ((nwg + kXcds - 1) / kXcds) * kXcds;
   hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED, QSPLIT>), dim3((unsigned)nwg), dim3(kPfThreads), lds,
@@ -1444,7 +1514,7 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
 
 template <bool PAGED>
 int launch_prefill_f32(const PrefillArgs& a, hipStream_t s) {
-  const size_t lds = kTileListOffset + (a.inline_list ? sizeof(TileListLds) : 0);
+  const size_t lds = kTileListOffset + (a.inline_list ? sizeof(TilePick) : 0);
   int64_t nwg = a.tiles_ub * a.num_kv_heads;
   nwg = ((nwg + kXcds - 1) / kXcds) * kXcds;
   hipLaunchKernelGGL((prefill_f32_kernel<PAGED>), dim3((unsigned)nwg), dim3(kPfThreads), lds, s, a);

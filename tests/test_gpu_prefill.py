@@ -90,12 +90,14 @@ def test_prefill_zero_and_negative_scale(dev, dtype, scale):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("nseq,Hkv", [(40, 2), (40, 8), (64, 2), (65, 8), (100, 2), (300, 2)])
+@pytest.mark.parametrize("nseq,Hkv", [(40, 2), (40, 8), (64, 2), (65, 8), (100, 2), (193, 8), (256, 2),
+                                      (300, 2)])
 def test_prefill_visit_order_many_tied_and_empty_sequences(dev, nseq, Hkv, dtype):
     """The tile list visits sequences longest first (ranked on the device for
-    up to 256 sequences, in batch order beyond) and each sequence's tiles
-    last first; ties, empty sequences and both grid mappings (KV heads a
-    multiple of 8 or not) must leave every row's result unchanged."""
+    up to 256 sequences, one to four waves of them, in batch order beyond)
+    and each sequence's tiles last first; ties, empty sequences and both grid
+    mappings (KV heads a multiple of 8 or not) must leave every row's result
+    unchanged."""
     announce(f"prefill visit order: {nseq} sequences, {Hkv} kv heads, {dtype}")
     g = torch.Generator().manual_seed(500 + nseq + Hkv)
     prior = [int(x) for x in torch.tensor([0, 16, 50, 97])[torch.randint(0, 4, (nseq,), generator=g)]]
@@ -212,7 +214,7 @@ def test_flash_prefill_contiguous(dev, dtype, group):
     assert_close_out(got, want, got.dtype, 2e-3)
 
 
-@pytest.mark.parametrize("nseq", [60, 64, 65, 120])
+@pytest.mark.parametrize("nseq", [60, 64, 65, 120, 256])
 def test_flash_prefill_many_ragged_prompts(dev, nseq):
     """Full prefill of many short prompts (the end-to-end workload's shape:
     prompt lengths 0-200 with ties on a tile boundary and an empty prompt),
