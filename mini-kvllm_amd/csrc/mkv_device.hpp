@@ -266,6 +266,56 @@ MKV_DEV u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 MKV_DEV u32x2 ld8(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
 MKV_DEV void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
+// 32 consecutive q elements (fp32, bf16 or fp16; element offset off a
+// multiple of 8) as fp32, in two steps: q32_issue issues every load of the
+// slice (4 for 16-bit q, 8 for fp32) and q32_convert, called once they are
+// needed, converts them, so the loads share one round trip and other loads
+// can go out in between (a load, wait and convert per 8 elements took four
+// round trips in a row).
+struct Q32Raw {
+  u32x4 r[8];
+};
+MKV_DEV void q32_issue(const void* q, int dt, int64_t off, Q32Raw& w) {
+  if (dt == MKV_DTYPE_F32) {
+    const float* p = reinterpret_cast<const float*>(q) + off;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w.r[i] = ld16(p + 4 * i);
+  } else {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(q) + off;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w.r[i] = ld16(p + 8 * i);
+  }
+}
+MKV_DEV void q32_convert(int dt, const Q32Raw& w, float* x) {
+  if (dt == MKV_DTYPE_F32) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[4 * i + j] = __uint_as_float(w.r[i][j]);
+  } else if (dt == MKV_DTYPE_BF16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x[8 * i + 2 * j] = bf16_bits_to_f32(w.r[i][j] & 0xffffu);
+        x[8 * i + 2 * j + 1] = bf16_bits_to_f32(w.r[i][j] >> 16);
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x[8 * i + 2 * j] = f16_bits_to_f32(w.r[i][j] & 0xffffu);
+        x[8 * i + 2 * j + 1] = f16_bits_to_f32(w.r[i][j] >> 16);
+      }
+  }
+}
+MKV_DEV void load_q32(const void* q, int dt, int64_t off, float* x) {
+  Q32Raw w;
+  q32_issue(q, dt, off, w);
+  q32_convert(dt, w, x);
+}
+
 // Non-temporal 16-byte load for streamed-once KV bytes.
 MKV_DEV u32x4 ld16_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));

@@ -78,31 +78,6 @@ MKV_DEV float wave_max(float v) {
   return v;
 }
 
-// Load 8 consecutive q elements (any q dtype) as fp32.
-MKV_DEV void load_q8(const void* q, int dt, int64_t off, float* x) {
-  if (dt == MKV_DTYPE_F32) {
-    const float* p = reinterpret_cast<const float*>(q) + off;
-    const u32x4 a = ld16(p), b = ld16(p + 4);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      x[j] = __uint_as_float(a[j]);
-      x[4 + j] = __uint_as_float(b[j]);
-    }
-  } else {
-    const u32x4 a = ld16(reinterpret_cast<const uint16_t*>(q) + off);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (dt == MKV_DTYPE_BF16) {
-        x[2 * j] = bf16_bits_to_f32(a[j] & 0xffffu);
-        x[2 * j + 1] = bf16_bits_to_f32(a[j] >> 16);
-      } else {
-        x[2 * j] = f16_bits_to_f32(a[j] & 0xffffu);
-        x[2 * j + 1] = f16_bits_to_f32(a[j] >> 16);
-      }
-    }
-  }
-}
-
 // Store 8 consecutive fp32 values in the output dtype.
 MKV_DEV void store_out8(void* out, int dt, int64_t off, const float* x) {
   if (dt == MKV_DTYPE_F32) {
@@ -659,8 +634,7 @@ MKV_DEV float load_q_operands(const DecodeArgs& a, int b, int kvh, QOps<KV_DT>& 
   float qf[32];
   if (c < a.group) {
     const int64_t qoff = (int64_t)b * a.q_stride + (int64_t)(kvh * a.group + c) * kHeadDim + 32 * kg;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) load_q8(a.q, a.q_dtype, qoff + 8 * i, qf + 8 * i);
+    load_q32(a.q, a.q_dtype, qoff, qf);
   } else {
 #pragma unroll
     for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
@@ -1357,8 +1331,7 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma32_kernel(D
   const int hq = it.kvh * a.group + c;
   if (c < a.group) {
     const int64_t qoff = (int64_t)it.b * a.q_stride + (int64_t)hq * kHeadDim + 32 * kg;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) load_q8(a.q, a.q_dtype, qoff + 8 * i, qf + 8 * i);
+    load_q32(a.q, a.q_dtype, qoff, qf);
   } else {
 #pragma unroll
     for (int i = 0; i < 32; ++i) qf[i] = 0.0f;

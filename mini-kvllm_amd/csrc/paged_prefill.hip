@@ -311,25 +311,6 @@ MKV_DEV Op16<KV_DT> to_op16(const float* x) {
   return r;
 }
 
-MKV_DEV void load_q8(const void* q, int dt, int64_t off, float* x) {
-  if (dt == MKV_DTYPE_F32) {
-    const float* p = reinterpret_cast<const float*>(q) + off;
-    const u32x4 a = ld16(p), b = ld16(p + 4);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      x[j] = __uint_as_float(a[j]);
-      x[4 + j] = __uint_as_float(b[j]);
-    }
-  } else {
-    const u32x4 a = ld16(reinterpret_cast<const uint16_t*>(q) + off);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      x[2 * j] = dt == MKV_DTYPE_BF16 ? bf16_bits_to_f32(a[j] & 0xffffu) : f16_bits_to_f32(a[j] & 0xffffu);
-      x[2 * j + 1] = dt == MKV_DTYPE_BF16 ? bf16_bits_to_f32(a[j] >> 16) : f16_bits_to_f32(a[j] >> 16);
-    }
-  }
-}
-
 MKV_DEV void store_out8(void* out, int dt, int64_t off, const float* x) {
   if (dt == MKV_DTYPE_F32) {
     float* p = reinterpret_cast<float*>(out) + off;
@@ -597,28 +578,59 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const int64_t q_seq0 = wk.q_seq0, q0 = wk.q0, q1 = wk.q1;
   const int G = a.group;
 
+  // Block-table entries of a tile, read one tile ahead of their use by a
+  // vector load: lane l of every wave reads the entry of sub-tile l / 16
+  // (keys kb + 16 (l / 16) .. +15; a 16-key sub-tile never straddles a block,
+  // bs >= 16).  A scalar load would share its wait counter with the LDS reads
+  // of the key loop; this one is covered by the wait for the tile's DMA.
+  const int64_t bmask = PAGED ? ((int64_t)1 << a.idx.bs_log2) - 1 : 0;
+  const int32_t* bt_row = PAGED ? a.idx.block_tables + (int64_t)seq * a.idx.bt_stride : nullptr;
+  const int num_blocks32 = PAGED ? (int)min(a.idx.num_blocks, (int64_t)0x7fffffff) : 0;
+  auto entry_load = [&](int kb) -> int32_t {
+    if constexpr (PAGED) {
+      const int blk = (kb + 16 * kg) >> a.idx.bs_log2;
+      return bt_row[blk < a.idx.max_blocks ? blk : 0];
+    } else {
+      return 0;
+    }
+  };
+  // (the entries of the first two tiles go out first, with q's loads; the
+  // block index is clamped to the row, so the loads stay in the table)
+  const int32_t e_tile0 = entry_load(0), e_tile1 = entry_load(kBN);
+
   // Query rows of this wave: row tile rt covers rows (kRowTiles*wave + rt)*16 + 0..15.
-  // q is loaded before the rows' visibility is worked out, so that its
-  // latency overlaps that phase.
+  // q's loads go out before the rows' visibility is worked out and the
+  // first tile is requested; q is converted after both (one round trip),
+  // except where q is split (QSPLIT: fp32 q held raw across the first
+  // tile's set-up spilled), which converts it at once.
+  Q32Raw qraw[kRowTiles];
+  bool q_ok[kRowTiles];
   float qf[kRowTiles][32];
   float qmax = 0.0f;
+  auto convert_q = [&]() {
+#pragma unroll
+    for (int rt = 0; rt < kRowTiles; ++rt) {
+      if (q_ok[rt]) {
+        q32_convert(a.q_dtype, qraw[rt], qf[rt]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) qf[rt][i] = 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < 32; ++i) qmax = fmaxf(qmax, fabsf(qf[rt][i]));
+    }
+  };
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt) {
     const int row = (kRowTiles * wave + rt) * 16 + c;
     const int64_t tok = q0 + row / G;
-    const bool ok = row < a.tok_per_wg * G && tok < q1;
-    if (ok) {
+    q_ok[rt] = row < a.tok_per_wg * G && tok < q1;
+    if (q_ok[rt]) {
       const int hq = kvh * G + row % G;
-      const int64_t off = (tok * a.num_heads + hq) * kHeadDim + 32 * kg;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) load_q8(a.q, a.q_dtype, off + 8 * i, qf[rt] + 8 * i);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 32; ++i) qf[rt][i] = 0.0f;
+      q32_issue(a.q, a.q_dtype, (tok * a.num_heads + hq) * kHeadDim + 32 * kg, qraw[rt]);
     }
-#pragma unroll
-    for (int i = 0; i < 32; ++i) qmax = fmaxf(qmax, fabsf(qf[rt][i]));
   }
+  if constexpr (QSPLIT) convert_q();
   wg_rows<PAGED>(a, vis_lds, red_lds, wk);
   const int min_vis = wk.min_vis, max_vis = wk.max_vis;
   int vis_c[kRowTiles];
@@ -627,48 +639,6 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     const int row = (kRowTiles * wave + rt) * 16 + c;
     vis_c[rt] = PAGED ? vis_lds[row] : row_vis_contiguous(a, wk, row);
   }
-  float score_mul = a.sm_scale * kLog2e;
-  if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) score_mul *= load_uniform_f32(a.k_scale);
-  if constexpr (CT != MKV_DTYPE_BF16) {
-    // power-of-two normalisation so that q is exact and in range in fp16
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) qmax = fmaxf(qmax, __shfl_xor(qmax, off));
-    if (qmax > 0.0f && qmax < __builtin_huge_valf()) {
-      const int e = ilogbf(qmax);
-      const float f = ldexpf(1.0f, 8 - e);
-#pragma unroll
-      for (int rt = 0; rt < kRowTiles; ++rt)
-#pragma unroll
-        for (int i = 0; i < 32; ++i) qf[rt][i] *= f;
-      score_mul *= ldexpf(1.0f, e - 8);
-    }
-  }
-  // The loop keeps raw scores and needs score_mul > 0: a negative scale
-  // moves its sign into q (exact), a zero scale is q = 0 with scale 1 (every
-  // visible key weighs the same, as with 0 * score); NaN propagates.
-  if (!(score_mul > 0.0f) && score_mul == score_mul) {
-    const float f = score_mul < 0.0f ? -1.0f : 0.0f;
-#pragma unroll
-    for (int rt = 0; rt < kRowTiles; ++rt)
-#pragma unroll
-      for (int i = 0; i < 32; ++i) qf[rt][i] *= f;
-    score_mul = score_mul < 0.0f ? -score_mul : 1.0f;
-  }
-  Op16<CT> qop[kRowTiles][4];
-  Op16<CT> qlo[QSPLIT ? kRowTiles : 1][4];
-#pragma unroll
-  for (int rt = 0; rt < kRowTiles; ++rt)
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      qop[rt][st] = to_op16<CT>(qf[rt] + 8 * st);
-      if constexpr (QSPLIT) {
-        float r[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] = qf[rt][8 * st + j] - (float)qop[rt][st][j];
-        qlo[rt][st] = to_op16<CT>(r);
-      }
-    }
-
   f32x4 acc[kRowTiles][8];
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt)
@@ -734,22 +704,6 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const uint64_t ld_b_mask = __builtin_amdgcn_ballot_w64(ld_b != 0);  // lanes whose first write is half 1
   auto lds_shift = [&](int u) { return ((ld_slot[u] & 3) - (ld_slot[0] & 3)) * 16 * LT::kRowBytes; };
 
-  // Block-table entries of a tile, read one tile ahead of their use by a
-  // vector load: lane l of every wave reads the entry of sub-tile l / 16
-  // (keys kb + 16 (l / 16) .. +15; a 16-key sub-tile never straddles a block,
-  // bs >= 16).  A scalar load would share its wait counter with the LDS reads
-  // of the key loop; this one is covered by the wait for the tile's DMA.
-  const int64_t bmask = PAGED ? ((int64_t)1 << a.idx.bs_log2) - 1 : 0;
-  const int32_t* bt_row = PAGED ? a.idx.block_tables + (int64_t)seq * a.idx.bt_stride : nullptr;
-  const int num_blocks32 = PAGED ? (int)min(a.idx.num_blocks, (int64_t)0x7fffffff) : 0;
-  auto entry_load = [&](int kb) -> int32_t {
-    if constexpr (PAGED) {
-      const int blk = (kb + 16 * kg) >> a.idx.bs_log2;
-      return bt_row[blk < a.idx.max_blocks ? blk : 0];
-    } else {
-      return 0;
-    }
-  };
   // The entries of the tile at kb, validated: per lane (sub-tile l / 16) the
   // physical block (-1 if absent), the byte offset of the sub-tile's first
   // token slot of the sub-tile's first key (paged) and the per-token-head
@@ -921,17 +875,66 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   // tile after the next (in flight)
   uint32_t present_cur = 0xfu, present_nxt = 0xfu;
   int32_t e_ahead = 0;
+  // The first tile's loads go out before q is waited for and converted
+  // below, so that the two round trips overlap (q waited for first, then the
+  // tile, took ~0.6 us more per workgroup).
   if (n_tiles > 0) {
-    const SubTiles st0 = entry_use(0, entry_load(0));
+    const SubTiles st0 = entry_use(0, e_tile0);
     present_cur = st0.present;
-    e_ahead = entry_load(kBN);
-    if constexpr (kDma) {
+    e_ahead = e_tile1;
+    if constexpr (kDma)
       dma_tile(0, st0, 0);
-      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    } else {
+    else
       load_tile(0, st0);
-      store_tile(0);
+  }
+  if constexpr (!QSPLIT) convert_q();
+  float score_mul = a.sm_scale * kLog2e;
+  if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) score_mul *= load_uniform_f32(a.k_scale);
+  if constexpr (CT != MKV_DTYPE_BF16) {
+    // power-of-two normalisation so that q is exact and in range in fp16
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) qmax = fmaxf(qmax, __shfl_xor(qmax, off));
+    if (qmax > 0.0f && qmax < __builtin_huge_valf()) {
+      const int e = ilogbf(qmax);
+      const float f = ldexpf(1.0f, 8 - e);
+#pragma unroll
+      for (int rt = 0; rt < kRowTiles; ++rt)
+#pragma unroll
+        for (int i = 0; i < 32; ++i) qf[rt][i] *= f;
+      score_mul *= ldexpf(1.0f, e - 8);
     }
+  }
+  // The loop keeps raw scores and needs score_mul > 0: a negative scale
+  // moves its sign into q (exact), a zero scale is q = 0 with scale 1 (every
+  // visible key weighs the same, as with 0 * score); NaN propagates.
+  if (!(score_mul > 0.0f) && score_mul == score_mul) {
+    const float f = score_mul < 0.0f ? -1.0f : 0.0f;
+#pragma unroll
+    for (int rt = 0; rt < kRowTiles; ++rt)
+#pragma unroll
+      for (int i = 0; i < 32; ++i) qf[rt][i] *= f;
+    score_mul = score_mul < 0.0f ? -score_mul : 1.0f;
+  }
+  Op16<CT> qop[kRowTiles][4];
+  Op16<CT> qlo[QSPLIT ? kRowTiles : 1][4];
+#pragma unroll
+  for (int rt = 0; rt < kRowTiles; ++rt)
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      qop[rt][st] = to_op16<CT>(qf[rt] + 8 * st);
+      if constexpr (QSPLIT) {
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = qf[rt][8 * st + j] - (float)qop[rt][st][j];
+        qlo[rt][st] = to_op16<CT>(r);
+      }
+    }
+
+  if (n_tiles > 0) {
+    if constexpr (kDma)
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    else
+      store_tile(0);
   }
   __syncthreads();
   __builtin_amdgcn_s_setprio(0);
@@ -1286,8 +1289,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     if (my_row < a.tok_per_wg * G && tok < q1) {
       const int hq = kvh * G + my_row % G;
       const int64_t off = (tok * a.num_heads + hq) * kHeadDim + 32 * kg;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) load_q8(a.q, a.q_dtype, off + 8 * i, qf + 8 * i);
+      load_q32(a.q, a.q_dtype, off, qf);
     } else {
 #pragma unroll
       for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
