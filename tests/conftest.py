@@ -50,7 +50,10 @@ def assert_close_out(got: torch.Tensor, want: torch.Tensor, out_dtype: torch.dty
         e = torch.floor(torch.log2(want.abs().clamp(min=2.0 ** -14)))
         tol = abs_tol + 0.5 * torch.exp2(e - (mant - 1))
     err = (got - want).abs()
-    bad = err > tol
+    # a NaN (or inf - inf) difference is a failure unless both sides are NaN
+    # there; `err > tol` alone is False for NaN and would let it pass
+    both_nan = torch.isnan(got) & torch.isnan(want)
+    bad = ~(err <= tol) & ~both_nan
     assert not bool(bad.any()), (
         f"{int(bad.sum())} of {err.numel()} elements out of tolerance; max abs err "
         f"{float(err.max()):.3e}, max excess {float((err - tol).max()):.3e} (abs_tol {abs_tol})")

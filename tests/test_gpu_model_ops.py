@@ -24,7 +24,8 @@ def _check(got, want, dtype):
     got, want = got.double().cpu(), want.double().cpu()
     e = torch.floor(torch.log2(want.abs().clamp(min=2.0 ** -149))).clamp(min=EMIN[dtype])
     tol = 0.5 * torch.exp2(e - (MANT[dtype] - 1)) + 2e-6 * want.abs() + 1e-30
-    bad = (got - want).abs() > tol
+    # (a NaN difference fails unless both sides are NaN; `> tol` alone passes it)
+    bad = ~((got - want).abs() <= tol) & ~(torch.isnan(got) & torch.isnan(want))
     assert not bool(bad.any()), f"{int(bad.sum())} elements off; max err {float((got - want).abs().max()):.3e}"
 
 

@@ -35,7 +35,8 @@ def _close_scaled(got, want, dtype, what):
     scale = want.abs().amax(-1, keepdim=True).clamp(min=1e-3)
     tol = 4.0 * 2.0 ** (1 - MANT[dtype]) * scale + 1e-6
     err = (got - want).abs()
-    bad = err > tol
+    # (a NaN difference fails unless both sides are NaN; `> tol` alone passes it)
+    bad = ~(err <= tol) & ~(torch.isnan(got) & torch.isnan(want))
     assert not bool(bad.any()), f"{what}: {int(bad.sum())} of {err.numel()} out of tolerance, max err {float(err.max()):.3e}"
 
 

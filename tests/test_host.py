@@ -316,3 +316,15 @@ def test_bench_extra_selection():
     assert bench.parse_args(["--no-extra", "--extra", "prefill"]).extra_set == set()
     with pytest.raises(SystemExit):
         bench.parse_args(["--extra", "prefil"])
+
+
+def test_assert_close_out_rejects_nan_differences():
+    """The GPU tests' tolerance check fails a NaN on one side only (a bare
+    `err > tol` is False for NaN and would pass it) and accepts NaN on both."""
+    from conftest import assert_close_out
+    want = torch.tensor([1.0, float("nan"), 2.0])
+    assert_close_out(torch.tensor([1.0, float("nan"), 2.0]), want, torch.float32, 1e-3)
+    for got in (torch.tensor([float("nan"), float("nan"), 2.0]), torch.tensor([1.0, 1.0, 2.0]),
+                torch.tensor([1.0, float("nan"), float("inf")])):
+        with pytest.raises(AssertionError):
+            assert_close_out(got, want, torch.float32, 1e-3)
