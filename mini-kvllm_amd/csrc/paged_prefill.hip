@@ -1174,39 +1174,71 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   static_assert(kRowTiles == 1, "the staged epilogue holds one 16-row tile per wave");
   if (a.q_dtype != MKV_DTYPE_F32) {
     // 16-bit outputs: the wave's 16 x 128 tile is staged in LDS (free after
-    // the last tile's barrier; 4 KB per wave, 256-byte rows with 16-byte
-    // chunk ch of row rr stored at position ch ^ rr, so that the four rows of
-    // a write are on distinct banks) and written as whole 16-byte chunks, 4
-    // stores per lane instead of 32 two-byte ones.
-    char* stage = (kDma ? (wave < 4 ? lds_k0 : lds_v0) : lds_kv) + (kDma ? (wave & 3) : wave) * 4096;
-    const bool bf = a.q_dtype == MKV_DTYPE_BF16;
-    float l_col = l_run[0] + __shfl_xor(l_run[0], 16);
-    l_col += __shfl_xor(l_col, 32);
+    // the last tile's barrier; 16 rows of 272 bytes per wave, two waves per
+    // 16 KB tile buffer: the 16-byte row padding puts the four rows of a
+    // write on distinct banks and makes each element's address the row's
+    // base plus an immediate) and written as whole 16-byte chunks, 4 stores
+    // per lane instead of 32 two-byte ones.
+    constexpr int kStageRow = 272;
+    static_assert(!kDma || 2 * 16 * kStageRow <= kSplitBytes, "two waves' staging per tile buffer");
+    static_assert(kDma || kPfWaves * 16 * kStageRow <= kOneBytes, "every wave's staging in the tile array");
+    static_assert(kRowsPerWg <= 128, "row / G by multiply-shift holds for rows below 128");
+    char* stage;
+    if constexpr (kDma) {
+      char* const half = wave < 4 ? (wave < 2 ? lds_k0 : lds_v0) : (wave < 6 ? lds_k1 : lds_v1);
+      stage = half + (wave & 1) * 16 * kStageRow;
+    } else {
+      stage = lds_kv + wave * 16 * kStageRow;
+    }
+    // 1 / l of rows 4kg + r: one division per lane (its own row c, then
+    // moved) where the sums are on the VALU; the MFMA row sums hold row
+    // 4kg + r in every lane of the group.
+    float inv_r[4];
+    if constexpr (kSumMfma) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      // (the MFMA row sums hold row 4kg + r in every lane of the group)
-      const float lh = kSumMfma ? acc_sum[0][r] : __shfl(l_col, 4 * kg + r);
-      const float inv = lh > 0.0f ? v_mul / lh : 0.0f;
-      const int rr = 4 * kg + r;
+      for (int r = 0; r < 4; ++r) inv_r[r] = acc_sum[0][r] > 0.0f ? v_mul / acc_sum[0][r] : 0.0f;
+    } else {
+      float l_col = l_run[0] + __shfl_xor(l_run[0], 16);
+      l_col += __shfl_xor(l_col, 32);
+      const float inv_c = l_col > 0.0f ? v_mul / l_col : 0.0f;
 #pragma unroll
-      for (int mm = 0; mm < 8; ++mm) {
-        const float x = acc[0][mm][r] * inv;
-        const uint16_t h = (uint16_t)(bf ? f32_to_bf16_bits(x) : f32_to_f16_bits(x));
-        const int ch = 2 * mm + (c >> 3);
-        *reinterpret_cast<uint16_t*>(stage + rr * 256 + ((ch ^ rr) << 4) + 2 * (c & 7)) = h;
-      }
+      for (int r = 0; r < 4; ++r) inv_r[r] = __shfl(inv_c, 4 * kg + r);
+    }
+    char* const wbase = stage + 4 * kg * kStageRow + 2 * c;  // + r rows + 32 bytes per output tile
+    if (a.q_dtype == MKV_DTYPE_BF16) {
+      typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int mm = 0; mm < 8; mm += 2) {
+          // round to nearest even, two elements per conversion
+          const bf16x2_t h = {(__bf16)(acc[0][mm][r] * inv_r[r]), (__bf16)(acc[0][mm + 1][r] * inv_r[r])};
+          const uint32_t pk = __builtin_bit_cast(uint32_t, h);
+          *reinterpret_cast<uint16_t*>(wbase + r * kStageRow + 32 * mm) = (uint16_t)pk;
+          *reinterpret_cast<uint16_t*>(wbase + r * kStageRow + 32 * (mm + 1)) = (uint16_t)(pk >> 16);
+        }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int mm = 0; mm < 8; ++mm)
+          *reinterpret_cast<uint16_t*>(wbase + r * kStageRow + 32 * mm) =
+              (uint16_t)f32_to_f16_bits(acc[0][mm][r] * inv_r[r]);
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's staging writes are done
     __builtin_amdgcn_wave_barrier();
+    // row / G for row < 128 and G <= 128: (row * gm) >> 16 with
+    // gm = 65536 / G + 1 (the excess, below 128 / 65536, stays under 1 / G)
+    const uint32_t gm = 65536u / (uint32_t)G + 1u;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int ci = 64 * u + lane;
-      const int rr = ci >> 4, ch = ci & 15;
+      const int rr = 4 * u + kg, ch = c;  // chunk 64u + lane: row rr, 16-byte chunk ch
       const int row = 16 * wave + rr;
-      const int64_t tok = q0 + row / G;
-      const u32x4 d = *reinterpret_cast<const u32x4*>(stage + rr * 256 + ((ch ^ rr) << 4));
+      const int rq = (int)(((uint32_t)row * gm) >> 16);
+      const int64_t tok = q0 + rq;
+      const u32x4 d = *reinterpret_cast<const u32x4*>(stage + rr * kStageRow + 16 * ch);
       if (row < a.tok_per_wg * G && tok < q1) {
-        const int hq = kvh * G + row % G;
+        const int hq = kvh * G + (row - rq * G);
         st16(reinterpret_cast<uint16_t*>(a.out) + (tok * a.num_heads + hq) * kHeadDim + 8 * ch, d);
       }
     }
