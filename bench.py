@@ -174,6 +174,32 @@ def box_copy_gbps(dev, stream, mib: int = 2048) -> float:
     return 2 * (mib << 20) / (ms * 1e-3) / 1e9
 
 
+def box_read_gbps(dev, stream, mib: int = 2048) -> dict:
+    """Read rate of a plain streaming kernel on this GPU (mkv_stream_read_probe:
+    non-temporal 16-byte loads, the decode's KV load type, over a 2 GiB buffer
+    read once per launch, no writes but one checksum dword per wave); the best
+    of a few grid sizes.  The measured ceiling for the decode's HBM reads."""
+    import torch
+
+    import mkv
+
+    nbytes = mib << 20
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    best = None
+    for grid in (2048, 4096, 8192, 16384, 32768):
+        sink = torch.empty(int(mkv._lib.query("mkv_stream_read_probe_sink_words", grid)),
+                           dtype=torch.int32, device=dev)
+        ms = time_launches(lambda i: mkv._lib.call("mkv_stream_read_probe", buf.data_ptr(), nbytes,
+                                                    sink.data_ptr(), grid, stream.cuda_stream),
+                           10, 2, stream)
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        if best is None or gbps > best["GBps"]:
+            best = {"GBps": round(gbps, 1), "grid": grid, "bytes": nbytes, "us": round(ms * 1e3, 1)}
+        del sink
+    del buf
+    return best
+
+
 def prefill_extra(dev, stream, cpu: bool = True) -> dict:
     """Chunked prefill over the paged cache: the 8 prefill sequences of the
     mixed-batch workload (prior context U[0, 4096], 512-row chunks), 32 q / 8
@@ -1235,6 +1261,10 @@ def main() -> int:
             extra["gather_kv"] = gather_extra(layers[0][0], meta, dev, stream, cpu=args.cpu_seqs > 0)
         if "copy" in wanted:
             extra["box_copy_GBps"] = round(box_copy_gbps(dev, stream), 1)
+            extra["box_read"] = box_read_gbps(dev, stream)
+            if "value" in result:
+                extra["box_read"]["headline_frac_of_box_read"] = round(
+                    result["value"] / extra["box_read"]["GBps"], 4)
         result["extra"] = extra
 
     if args.cpu_seqs > 0 and not per_token and not args.skip_headline:

@@ -444,6 +444,21 @@ int mkv_rmsnorm(void* out, void* residual, const void* x, const void* weight,
 int mkv_silu_mul(void* out, const void* x, int64_t x_row_stride, int64_t rows,
                  int inter, int dtype, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Measurement helper (no counterpart in the reference; for benchmarks).
+ *
+ * mkv_stream_read_probe reads `bytes` (a multiple of 16) from the 16-byte
+ * aligned device buffer `buf` once, with the non-temporal 16-byte loads the
+ * decode kernels use for KV, in `grid` workgroups of 256 threads
+ * (grid-stride, 4 loads in flight per lane), and writes one XOR checksum
+ * dword per wavefront to `sink` (mkv_stream_read_probe_sink_words(grid)
+ * words).  Its time gives the read rate a plain streaming kernel reaches on
+ * the GPU, the measured ceiling next to the datasheet peak.
+ */
+size_t mkv_stream_read_probe_sink_words(int grid);
+int mkv_stream_read_probe(const void* buf, int64_t bytes, uint32_t* sink, int grid,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,8 @@ SIGNATURES: dict[str, tuple] = {
     "mkv_gather_kv": (c_int, [
         c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64, c_int, c_void_p, c_int, c_int,
         c_int, c_int, c_int, c_int, c_void_p]),
+    "mkv_stream_read_probe_sink_words": (c_size_t, [c_int]),
+    "mkv_stream_read_probe": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_void_p]),
 }
 
 _lock = threading.Lock()

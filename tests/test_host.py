@@ -328,3 +328,16 @@ def test_assert_close_out_rejects_nan_differences():
                 torch.tensor([1.0, float("nan"), float("inf")])):
         with pytest.raises(AssertionError):
             assert_close_out(got, want, torch.float32, 1e-3)
+
+
+def test_stream_read_probe_checks_arguments_on_the_host():
+    """The read probe (a measurement helper) refuses bad sizes, null and
+    misaligned buffers before it launches anything."""
+    lib = _lib.load()
+    assert lib.mkv_stream_read_probe_sink_words(2048) == 2048 * 4
+    assert lib.mkv_stream_read_probe_sink_words(0) == 0
+    assert lib.mkv_stream_read_probe(16, 100, 16, 64, None) == -2      # bytes not a multiple of 16
+    assert lib.mkv_stream_read_probe(16, 4096, 16, 0, None) == -2      # empty grid
+    assert lib.mkv_stream_read_probe(16, 4096, 16, 70000, None) == -2  # grid too large
+    assert lib.mkv_stream_read_probe(None, 4096, 16, 64, None) == -1
+    assert lib.mkv_stream_read_probe(24, 4096, 16, 64, None) == -8     # misaligned buffer
