@@ -1244,22 +1244,30 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     }
     return;
   }
+  // fp32 outputs: 1 / l as above
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt) {
-    float l_col = l_run[rt] + __shfl_xor(l_run[rt], 16);
-    l_col += __shfl_xor(l_col, 32);
+    float inv_r[4];
+    if constexpr (kSumMfma) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) inv_r[r] = acc_sum[rt][r] > 0.0f ? v_mul / acc_sum[rt][r] : 0.0f;
+    } else {
+      float l_col = l_run[rt] + __shfl_xor(l_run[rt], 16);
+      l_col += __shfl_xor(l_col, 32);
+      const float inv_c = l_col > 0.0f ? v_mul / l_col : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) inv_r[r] = __shfl(inv_c, 4 * kg + r);
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float lh = kSumMfma ? acc_sum[rt][r] : __shfl(l_col, 4 * kg + r);
       const int row = (kRowTiles * wave + rt) * 16 + 4 * kg + r;
       const int64_t tok = q0 + row / G;
       if (row >= a.tok_per_wg * G || tok >= q1) continue;
       const int hq = kvh * G + row % G;
-      const float inv = lh > 0.0f ? v_mul / lh : 0.0f;
       // lane c holds dims 16mm + c
       const int64_t o = (tok * a.num_heads + hq) * kHeadDim + c;
 #pragma unroll
-      for (int mm = 0; mm < 8; ++mm) reinterpret_cast<float*>(a.out)[o + 16 * mm] = acc[rt][mm][r] * inv;
+      for (int mm = 0; mm < 8; ++mm) reinterpret_cast<float*>(a.out)[o + 16 * mm] = acc[rt][mm][r] * inv_r[r];
     }
   }
 }
