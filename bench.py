@@ -747,8 +747,11 @@ def e2e_extra(dev) -> dict:
     prompts = [torch.randint(0, 151936, (L,), generator=g).tolist() for L in lens]
     cfg = E.ModelConfig()
     model = E.Qwen3Model(cfg, dev, seed=5, block_size=256)
+    # decode in 256-token split-K: with 60 rows of 300-800 tokens it beats
+    # the stream-K default (e2e 17.9k -> 18.4k tok/s, two runs each)
     eng = E.Engine(model, num_blocks=512, max_num_seqs=64, max_num_batched_tokens=1024,
-                   kv_cache_dtype="fp8_per_tensor", max_model_len=4096, seed=0)
+                   kv_cache_dtype="fp8_per_tensor", max_model_len=4096, seed=0,
+                   decode_split_tokens=256)
     eng.generate(prompts, max_tokens=256)  # warm-up: captures the decode graphs
     eng.stats.clear()
     torch.cuda.synchronize()
@@ -764,7 +767,8 @@ def e2e_extra(dev) -> dict:
                        "1024, FP8 per-tensor KV, block 256, chunked prefill, captured decode")
     # the same engine with eager decode steps (no captured graphs)
     eager = E.Engine(model, num_blocks=512, max_num_seqs=64, max_num_batched_tokens=1024,
-                     kv_cache_dtype="fp8_per_tensor", max_model_len=4096, seed=0, use_graphs=False)
+                     kv_cache_dtype="fp8_per_tensor", max_model_len=4096, seed=0, use_graphs=False,
+                     decode_split_tokens=256)
     eager.generate(prompts[:4], max_tokens=4)  # warm-up
     eager.stats.clear()
     torch.cuda.synchronize()

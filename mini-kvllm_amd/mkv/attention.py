@@ -384,12 +384,14 @@ def _decode(query, k_cache, v_cache, block_tables, context_lens, scale, num_head
 def paged_attention_decode(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                            block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float,
                            num_heads: int, num_kv_heads: int, head_dim: int,
-                           block_size: int) -> torch.Tensor:
+                           block_size: int, split_tokens: int = 0) -> torch.Tensor:
     """Decode attention over the paged cache: query (batch, num_heads,
     head_dim) -> output of the same shape and dtype.  Reference:
-    attention.py:895-950.  Rows with context_lens == 0 yield zeros."""
+    attention.py:895-950.  Rows with context_lens == 0 yield zeros.
+    split_tokens (an addition; 0 by default) selects the schedule:
+    0 = stream-K over the whole batch, n > 0 = split-K in n-token splits."""
     return _decode(query, k_cache, v_cache, block_tables, context_lens, scale, num_heads,
-                   num_kv_heads, head_dim)
+                   num_kv_heads, head_dim, split_tokens=split_tokens)
 
 
 def paged_attention_decode_quantized(query: torch.Tensor, k_cache: torch.Tensor,
@@ -397,7 +399,7 @@ def paged_attention_decode_quantized(query: torch.Tensor, k_cache: torch.Tensor,
                                      v_scale: torch.Tensor, block_tables: torch.Tensor,
                                      context_lens: torch.Tensor, scale: float, num_heads: int,
                                      num_kv_heads: int, head_dim: int, block_size: int,
-                                     kv_cache_dtype: str) -> torch.Tensor:
+                                     kv_cache_dtype: str, split_tokens: int = 0) -> torch.Tensor:
     """Decode attention over a quantised cache, dequantised as code * scale.
     Reference: attention.py:1213-1268.
 
@@ -406,6 +408,7 @@ def paged_attention_decode_quantized(query: torch.Tensor, k_cache: torch.Tensor,
     float32 (num_blocks, block_size, num_kv_heads) scales; the K scale
     multiplies the score and the V scale the softmax weight of its token
     (the reference's tile kernel, attention.py:1124-1210).
+    split_tokens as for paged_attention_decode.
     """
     if kv_cache_dtype == "fp8_per_tensor" or kv_cache_dtype == "fp8_per_token_head":
         if k_cache.dtype != torch.float8_e4m3fn:
@@ -416,7 +419,7 @@ def paged_attention_decode_quantized(query: torch.Tensor, k_cache: torch.Tensor,
     else:
         raise ValueError(f"unknown quantized kv_cache_dtype {kv_cache_dtype!r}")
     return _decode(query, k_cache, v_cache, block_tables, context_lens, scale, num_heads,
-                   num_kv_heads, head_dim, k_scale, v_scale,
+                   num_kv_heads, head_dim, k_scale, v_scale, split_tokens=split_tokens,
                    per_token_head=kv_cache_dtype in PER_TOKEN_HEAD_MODES)
 
 
@@ -582,6 +585,9 @@ class Attention(nn.Module):
         # first and fills in around them, with no gathers and no second
         # launch.
         self.mixed_batch = "unified"
+        # decode schedule (0: stream-K, the default; n > 0: n-token split-K,
+        # faster for batches of short contexts, e.g. 60 rows of 300-800 tokens)
+        self.decode_split_tokens = 0
 
     def _mode(self) -> str:
         mode = self.kv_cache_dtype
@@ -597,10 +603,10 @@ class Attention(nn.Module):
             return paged_attention_decode_quantized(
                 q, self.k_cache, self.v_cache, self.k_scale, self.v_scale, block_tables,
                 context_lens, scale, self.num_heads, self.num_kv_heads, self.head_dim,
-                self.block_size, mode)
+                self.block_size, mode, split_tokens=self.decode_split_tokens)
         return paged_attention_decode(q, self.k_cache, self.v_cache, block_tables, context_lens,
                                       scale, self.num_heads, self.num_kv_heads, self.head_dim,
-                                      self.block_size)
+                                      self.block_size, split_tokens=self.decode_split_tokens)
 
     def _prefill(self, q, block_tables, context_lens, cu_seqlens_q, positions, scale):
         quant = self._mode() != "auto"

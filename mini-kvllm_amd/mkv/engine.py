@@ -412,8 +412,10 @@ class Engine:
     def __init__(self, model: Qwen3Model, num_blocks: int, max_num_seqs: int = 64,
                  max_num_batched_tokens: int = 1024, kv_cache_dtype: str = "fp8_per_tensor",
                  max_model_len: int = 4096, eos: int | None = None, seed: int = 0,
-                 use_graphs: bool = True):
+                 use_graphs: bool = True, decode_split_tokens: int = 0):
         self.model = model
+        for layer in model.layers:
+            layer["attn"].decode_split_tokens = decode_split_tokens
         self.dev = model.embed.device
         self.bs = model.block_size
         model.attach_kv_cache(num_blocks, kv_cache_dtype)

@@ -35,10 +35,11 @@ def _prompts(seed, n=6):
     return [torch.randint(0, CFG.vocab_size, (L,), generator=g).tolist() for L in lens]
 
 
-def _engine(dev, use_graphs=True, model_cls=E.Qwen3Model, kv="fp8_per_tensor"):
+def _engine(dev, use_graphs=True, model_cls=E.Qwen3Model, kv="fp8_per_tensor", split=0):
     model = model_cls(CFG, dev, seed=5, block_size=16)
     return E.Engine(model, num_blocks=96, max_num_seqs=4, max_num_batched_tokens=64,
-                    kv_cache_dtype=kv, max_model_len=256, seed=0, use_graphs=use_graphs)
+                    kv_cache_dtype=kv, max_model_len=256, seed=0, use_graphs=use_graphs,
+                    decode_split_tokens=split)
 
 
 @pytest.mark.parametrize("kv", ["fp8_per_tensor", "auto"])
@@ -83,10 +84,13 @@ class OracleAttentionModel(E.Qwen3Model):
         return out.to(q.dtype).to(q.device).reshape(q.shape[0], Hq * self.cfg.head_dim)
 
 
-def test_engine_logits_match_the_oracle_attention_engine(dev, monkeypatch):
-    announce("engine: logits vs the same engine with oracle attention, every step")
+@pytest.mark.parametrize("split", [0, 32])
+def test_engine_logits_match_the_oracle_attention_engine(dev, monkeypatch, split):
+    """Every step's logits against the same engine with the oracle's
+    attention; decode by stream-K (split 0) and by 32-token split-K."""
+    announce(f"engine: logits vs the same engine with oracle attention, every step, split {split}")
     prompts = _prompts(12)
-    eng = _engine(dev, True)
+    eng = _engine(dev, True, split=split)
     ref = _engine(dev, False, model_cls=OracleAttentionModel)
     for e in (eng, ref):
         for p in prompts:
