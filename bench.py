@@ -178,7 +178,8 @@ def box_read_gbps(dev, stream, mib: int = 2048) -> dict:
     """Read rate of a plain streaming kernel on this GPU (mkv_stream_read_probe:
     non-temporal 16-byte loads, the decode's KV load type, over a 2 GiB buffer
     read once per launch, no writes but one checksum dword per wave); the best
-    of a few grid sizes.  The measured ceiling for the decode's HBM reads."""
+    of a few grid sizes (many waves with a few loads each read fastest).  The
+    measured ceiling for the decode's HBM reads."""
     import torch
 
     import mkv
@@ -186,7 +187,7 @@ def box_read_gbps(dev, stream, mib: int = 2048) -> dict:
     nbytes = mib << 20
     buf = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
     best = None
-    for grid in (2048, 4096, 8192, 16384, 32768):
+    for grid in (32768, 65536, 131072, 262144):
         sink = torch.empty(int(mkv._lib.query("mkv_stream_read_probe_sink_words", grid)),
                            dtype=torch.int32, device=dev)
         ms = time_launches(lambda i: mkv._lib.call("mkv_stream_read_probe", buf.data_ptr(), nbytes,

@@ -449,8 +449,8 @@ int mkv_silu_mul(void* out, const void* x, int64_t x_row_stride, int64_t rows,
  *
  * mkv_stream_read_probe reads `bytes` (a multiple of 16) from the 16-byte
  * aligned device buffer `buf` once, with the non-temporal 16-byte loads the
- * decode kernels use for KV, in `grid` workgroups of 256 threads
- * (grid-stride, 4 loads in flight per lane), and writes one XOR checksum
+ * decode kernels use for KV, in `grid` (<= 2^20) workgroups of 256 threads
+ * (grid-stride, up to 16 loads in flight per lane), and writes one XOR checksum
  * dword per wavefront to `sink` (mkv_stream_read_probe_sink_words(grid)
  * words).  Its time gives the read rate a plain streaming kernel reaches on
  * the GPU, the measured ceiling next to the datasheet peak.

@@ -4,7 +4,7 @@
 // No reference counterpart: measurement only.
 //
 // Every lane reads 16-byte chunks with non-temporal loads (the decode's KV
-// load type), kProbeUnroll of them in flight, grid-stride over the buffer; a
+// load type), up to kProbeUnroll of them in flight, grid-stride over the buffer; a
 // wave folds what it read into one dword (XOR) written to its sink word, so
 // the loads cannot be dropped.  Nothing else is written.
 #include "mkv_device.hpp"
@@ -13,7 +13,7 @@ namespace mkv {
 namespace {
 
 constexpr int kProbeThreads = 256;
-constexpr int kProbeUnroll = 4;
+constexpr int kProbeUnroll = 16;
 
 __global__ __launch_bounds__(kProbeThreads) void stream_read_kernel(const u32x4* __restrict__ p,
                                                                     int64_t n16,
@@ -44,7 +44,7 @@ extern "C" size_t mkv_stream_read_probe_sink_words(int grid) {
 
 extern "C" int mkv_stream_read_probe(const void* buf, int64_t bytes, uint32_t* sink, int grid,
                                      void* stream) {
-  if (bytes < 0 || grid <= 0 || grid > 65536) return MKV_ERR_BAD_SHAPE;
+  if (bytes < 0 || grid <= 0 || grid > (1 << 20)) return MKV_ERR_BAD_SHAPE;
   if (bytes % 16) return MKV_ERR_BAD_SHAPE;
   if (!buf || !sink) return MKV_ERR_NULL_POINTER;
   if (reinterpret_cast<uintptr_t>(buf) & 15u) return MKV_ERR_MISALIGNED;

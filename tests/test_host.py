@@ -338,6 +338,6 @@ def test_stream_read_probe_checks_arguments_on_the_host():
     assert lib.mkv_stream_read_probe_sink_words(0) == 0
     assert lib.mkv_stream_read_probe(16, 100, 16, 64, None) == -2      # bytes not a multiple of 16
     assert lib.mkv_stream_read_probe(16, 4096, 16, 0, None) == -2      # empty grid
-    assert lib.mkv_stream_read_probe(16, 4096, 16, 70000, None) == -2  # grid too large
+    assert lib.mkv_stream_read_probe(16, 4096, 16, (1 << 20) + 1, None) == -2  # grid too large (above 2^20)
     assert lib.mkv_stream_read_probe(None, 4096, 16, 64, None) == -1
     assert lib.mkv_stream_read_probe(24, 4096, 16, 64, None) == -8     # misaligned buffer
