@@ -212,11 +212,16 @@ int mkv_fp8_calibrate_per_tensor(const void* key, int64_t key_row_stride,
  * a persistent grid, groups of num_kv_heads waves sharing each tile range,
  * for BF16/F16/FP8/INT8 KV and batch <= 8192, else split-K with a
  * library-chosen split); > 0 = split-K with that many tokens per work item
- * (a multiple of 32).  workspace: >= mkv_paged_decode_workspace_size(...)
+ * (a multiple of 32); MKV_DECODE_WORKGROUP = one workgroup per (sequence,
+ * KV head) whose waves split the sequence and merge in LDS (BF16/F16/FP8/
+ * INT8 KV; no workspace, one launch; MKV_ERR_BAD_SHAPE when a wave's share
+ * of the widest block table would span more than 62 blocks).
+ * workspace: >= mkv_paged_decode_workspace_size(...)
  * bytes with the same arguments (the size of the route those arguments
  * select: stream-K partial slots for the persistent grid, or split-K
  * partials); calls that share a workspace must be ordered on one stream.
  */
+#define MKV_DECODE_WORKGROUP (-1)
 size_t mkv_paged_decode_workspace_size(int batch, int num_heads,
                                        int num_kv_heads, int max_blocks,
                                        int block_size, int head_dim,

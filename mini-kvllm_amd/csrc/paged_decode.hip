@@ -737,6 +737,118 @@ paged_decode_mfma16_2w_kernel(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Workgroup split (small batches): one workgroup per (sequence, KV head).
+// Its nw waves take consecutive tile ranges of the sequence, run the split-K
+// tile pipeline above, and merge their (acc, m, l) through LDS with the
+// log-sum-exp rule; one pass writes the output.  No workspace, no second
+// kernel: a batch of a few dozen sequences is bound by the latency of each
+// wave's tile chain, and this shortens the chain by nw without the partial
+// round trip through HBM and the merge launch.
+// LDS (dynamic): acc [nw][group][head_dim] fp32, then m [nw][group], l [nw][group].
+// ---------------------------------------------------------------------------
+constexpr int kWgMaxWaves = 8;
+
+template <int KV_DT>
+MKV_DEV void wg_decode(const DecodeArgs& a) {
+  extern __shared__ float wg_lds[];
+  const int nw = blockDim.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+  const int G = a.group;
+  WorkItem it;
+  it.b = (int)(blockIdx.x / (unsigned)a.num_kv_heads);
+  it.kvh = (int)blockIdx.x - it.b * a.num_kv_heads;
+  int64_t L = load_index(a.context_lens, it.b, a.ctx_i64);
+  const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
+  L = L < 0 ? 0 : (L > cap ? cap : L);
+  const int tiles = (int)((L + 31) >> 5);
+  const int per = (tiles + nw - 1) / nw;  // tiles per wave
+  const int64_t tb = (int64_t)wv * per * 32, te = tb + (int64_t)per * 32;
+  it.t_begin = (int)(tb < L ? tb : L);
+  it.t_end = (int)(te < L ? te : L);
+  it.split = wv;
+  it.num_splits = nw;
+
+  QOps<KV_DT> qop;
+  const float k_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.k_scale) : 1.0f;
+  const float score_mul = load_q_operands<KV_DT>(a, it.b, it.kvh, qop, k_mul);
+  f32x4 acc[8];
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegBig, l_run = 0.0f;
+  if (it.t_begin < it.t_end) {
+    const ItemLoad Ld = item_load_setup<KV_DT>(a, it);
+    Tile16<KV_DT> ta, tb2;
+    load_tile16<KV_DT>(a, it, Ld, it.t_begin, ta);
+    for (int t0 = it.t_begin;;) {
+      load_tile16<KV_DT>(a, it, Ld, t0 + 32, tb2);
+      compute_tile16<KV_DT>(ta, t0, it.t_end, qop, score_mul, acc, m_run, l_run);
+      t0 += 32;
+      if (t0 >= it.t_end) break;
+      load_tile16<KV_DT>(a, it, Ld, t0 + 32, ta);
+      compute_tile16<KV_DT>(tb2, t0, it.t_end, qop, score_mul, acc, m_run, l_run);
+      t0 += 32;
+      if (t0 >= it.t_end) break;
+    }
+  }
+  float l_col = l_run + __shfl_xor(l_run, 16);
+  l_col += __shfl_xor(l_col, 32);
+
+  // this wave's partial: O[head 4kg + r][dim 8c + mm] = acc[mm][r]
+  float* acc_l = wg_lds;
+  float* m_l = wg_lds + nw * G * kHeadDim;
+  float* l_l = m_l + nw * G;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * kg + r;
+    if (h < G) {
+      float* p = acc_l + (wv * G + h) * kHeadDim + 8 * c;
+      *reinterpret_cast<f32x4*>(p) = f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+      *reinterpret_cast<f32x4*>(p + 4) = f32x4{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
+    }
+  }
+  if (kg == 0 && c < G) {
+    m_l[wv * G + c] = m_run;
+    l_l[wv * G + c] = l_col;
+  }
+  __syncthreads();
+
+  const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
+  for (int u = threadIdx.x; u < G * 16; u += blockDim.x) {
+    const int h = u >> 4, d0 = (u & 15) * 8;
+    float M = kNegBig;
+    for (int w = 0; w < nw; ++w) M = fmaxf(M, m_l[w * G + h]);
+    float lsum = 0.0f, o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = 0.0f;
+    for (int w = 0; w < nw; ++w) {
+      const float e = __builtin_amdgcn_exp2f(m_l[w * G + h] - M);
+      lsum += e * l_l[w * G + h];
+      const float* p = acc_l + (w * G + h) * kHeadDim + d0;
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(p);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        o[j] += e * x0[j];
+        o[4 + j] += e * x1[j];
+      }
+    }
+    const float inv = lsum > 0.0f ? v_mul / lsum : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] *= inv;
+    store_out8(a.out, a.q_dtype,
+               (int64_t)it.b * a.out_stride + (int64_t)(it.kvh * G + h) * kHeadDim + d0, o);
+  }
+}
+
+template <int KV_DT>
+__global__ __launch_bounds__(kWgMaxWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
+paged_decode_wg_kernel(DecodeArgs a) {
+  wg_decode<KV_DT>(a);
+}
+
+// ---------------------------------------------------------------------------
 // Stream-K decode (16-bit MFMA path, the default).
 //
 // The work is one global stream of columns: sequence by sequence, the
@@ -1539,9 +1651,25 @@ bool use_stream(int split_tokens, int kv_dtype, int batch, int num_kv_heads) {
          num_kv_heads <= device_cus() * kDecWaves;
 }
 
+// Waves per workgroup of the workgroup-split route: as many as fill the
+// chip's two-waves-per-SIMD slots once (at most kWgMaxWaves), no more than
+// the widest sequence's tiles, and few enough that the LDS merge buffers fit
+// in 64 KiB.
+int wg_waves(int batch, int num_kv_heads, int group, int max_blocks, int block_size) {
+  const int64_t items = (int64_t)batch * num_kv_heads;
+  const int64_t slots = (int64_t)device_cus() * 8;
+  const int64_t max_tiles = ((int64_t)max_blocks * block_size + 31) / 32;
+  int nw = kWgMaxWaves;
+  while (nw > 1 && (items * nw > slots || nw > max_tiles ||
+                    (size_t)nw * group * (kHeadDim + 2) * sizeof(float) > 65536))
+    nw >>= 1;
+  return nw;
+}
+
 // Workspace bytes of the route that these arguments select.
 size_t decode_ws_bytes(int batch, int num_heads, int num_kv_heads, int max_blocks, int block_size,
                        int kv_dtype, int split_tokens) {
+  if (split_tokens == MKV_DECODE_WORKGROUP) return 0;
   if (use_stream(split_tokens, kv_dtype, batch, num_kv_heads))
     return stream_ws_bytes(batch, num_heads / num_kv_heads);
   const int st = resolve_split(split_tokens, batch, num_kv_heads, max_blocks, block_size);
@@ -1608,7 +1736,9 @@ int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_
   if (q_batch_stride < (int64_t)num_heads * head_dim || out_batch_stride < (int64_t)num_heads * head_dim ||
       bt_stride < max_blocks)
     return MKV_ERR_BAD_STRIDE;
-  if (split_tokens < 0 || split_tokens % 32 != 0) return MKV_ERR_BAD_SHAPE;
+  if (split_tokens != MKV_DECODE_WORKGROUP && (split_tokens < 0 || split_tokens % 32 != 0))
+    return MKV_ERR_BAD_SHAPE;
+  if (split_tokens == MKV_DECODE_WORKGROUP && kv_dtype == MKV_DTYPE_F32) return MKV_ERR_UNSUPPORTED_DTYPE;
   const int qb = q_dtype == MKV_DTYPE_F32 ? 4 : 2;
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u)
@@ -1641,6 +1771,37 @@ int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // the merge kernels apply the per-tensor V scale
   const bool fp8 = fmt == MKV_DTYPE_FP8E4M3;
+  if (split_tokens == MKV_DECODE_WORKGROUP) {
+    const int nw = wg_waves(batch, num_kv_heads, group, max_blocks, block_size);
+    // a wave's tile range must span at most 64 blocks (one lane each)
+    const int64_t max_tiles = ((int64_t)max_blocks * block_size + 31) / 32;
+    const int64_t wave_tokens = ((max_tiles + nw - 1) / nw) * 32;
+    if ((wave_tokens >> bs_log2) + 2 > 64) return MKV_ERR_BAD_SHAPE;
+    const size_t lds = (size_t)nw * group * (kHeadDim + 2) * sizeof(float);
+    a.split_tokens = 0;
+    a.max_splits = 0;
+    a.ws_acc = nullptr;
+    a.ws_ml = nullptr;
+    const dim3 grid((unsigned)((int64_t)batch * num_kv_heads)), block(nw * kWave);
+    switch (fmt) {
+      case MKV_DTYPE_FP8E4M3:
+        hipLaunchKernelGGL(paged_decode_wg_kernel<MKV_DTYPE_FP8E4M3>, grid, block, lds, s, a);
+        break;
+      case kKvFp8PerToken:
+        hipLaunchKernelGGL(paged_decode_wg_kernel<kKvFp8PerToken>, grid, block, lds, s, a);
+        break;
+      case kKvI8PerToken:
+        hipLaunchKernelGGL(paged_decode_wg_kernel<kKvI8PerToken>, grid, block, lds, s, a);
+        break;
+      case MKV_DTYPE_BF16:
+        hipLaunchKernelGGL(paged_decode_wg_kernel<MKV_DTYPE_BF16>, grid, block, lds, s, a);
+        break;
+      default:
+        hipLaunchKernelGGL(paged_decode_wg_kernel<MKV_DTYPE_F16>, grid, block, lds, s, a);
+        break;
+    }
+    return (int)hipGetLastError();
+  }
   if (use_stream(split_tokens, kv_dtype, batch, num_kv_heads)) {
     // stream-K path
     const size_t need = stream_ws_bytes(batch, group);

@@ -27,6 +27,7 @@ APPEND_CALIBRATE_SENTINEL = 1
 NOALLOC_SCRATCH_BYTES = 32 << 20  # MKV_NOALLOC_SCRATCH_BYTES
 INDEX_I32 = 0
 INDEX_I64 = 1
+DECODE_WORKGROUP = -1  # MKV_DECODE_WORKGROUP: split_tokens value of the workgroup route
 
 # name -> (restype, argtypes); mirrors include/mkv.h one to one.
 SIGNATURES: dict[str, tuple] = {

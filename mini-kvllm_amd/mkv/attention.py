@@ -34,6 +34,8 @@ import torch.nn as nn
 from . import _lib
 from .context import current_context
 
+DECODE_WORKGROUP = _lib.DECODE_WORKGROUP
+
 FP8_E4M3_MAX = 448.0
 INT8_MAX = 127.0
 INT8_MIN = -128.0
@@ -389,7 +391,9 @@ def paged_attention_decode(query: torch.Tensor, k_cache: torch.Tensor, v_cache: 
     head_dim) -> output of the same shape and dtype.  Reference:
     attention.py:895-950.  Rows with context_lens == 0 yield zeros.
     split_tokens (an addition; 0 by default) selects the schedule:
-    0 = stream-K over the whole batch, n > 0 = split-K in n-token splits."""
+    0 = stream-K over the whole batch, n > 0 = split-K in n-token splits,
+    DECODE_WORKGROUP (-1) = one workgroup per (sequence, KV head) whose
+    waves split the sequence and merge in LDS (16-bit and quantised caches)."""
     return _decode(query, k_cache, v_cache, block_tables, context_lens, scale, num_heads,
                    num_kv_heads, head_dim, split_tokens=split_tokens)
 
@@ -585,8 +589,9 @@ class Attention(nn.Module):
         # first and fills in around them, with no gathers and no second
         # launch.
         self.mixed_batch = "unified"
-        # decode schedule (0: stream-K, the default; n > 0: n-token split-K,
-        # faster for batches of short contexts, e.g. 60 rows of 300-800 tokens)
+        # decode schedule (0: stream-K, the default; n > 0: n-token split-K;
+        # DECODE_WORKGROUP: one workgroup per sequence and KV head, fastest for
+        # batches of a few dozen short contexts, e.g. 60 rows of 300-800 tokens)
         self.decode_split_tokens = 0
 
     def _mode(self) -> str:

@@ -37,7 +37,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from . import context as C
-from .attention import Attention, _dtype_code, _stream
+from .attention import DECODE_WORKGROUP, Attention, _dtype_code, _stream
 from .decode_state import DecodeGraphs, DecodeMetadata
 from .producer import qkv_norm_rope_append
 

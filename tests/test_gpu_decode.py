@@ -98,29 +98,38 @@ def _case(seed, B, Hq, Hkv, bs, N, max_blocks, dtype, ctx=None):
     return q, k, v, bt, ctx.to(torch.int64), ks, vs
 
 
+WG = A.DECODE_WORKGROUP
+
+
+@pytest.mark.parametrize("route", [0, WG])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn, torch.float32])
 @pytest.mark.parametrize("group", [1, 2, 4, 8, 16])
-def test_decode_group_sizes(dev, dtype, group):
-    announce(f"decode {dtype} group {group}")
+def test_decode_group_sizes(dev, dtype, group, route):
+    if route == WG and dtype == torch.float32:
+        pytest.skip("the workgroup route serves 16-bit and quantised caches")
+    announce(f"decode {dtype} group {group} route {route}")
     Hkv = 2
     q, k, v, bt, ctx, ks, vs = _case(100 + group, 6, Hkv * group, Hkv, 32, 64, 10, dtype)
-    got = _run(dev, q, k, v, bt, ctx, 1 / math.sqrt(128), Hkv * group, Hkv, ks, vs)
+    got = _run(dev, q, k, v, bt, ctx, 1 / math.sqrt(128), Hkv * group, Hkv, ks, vs, split_tokens=route)
     want = _oracle(q, k, v, bt, ctx, 1 / math.sqrt(128), Hkv * group, Hkv, ks, vs)
     assert_close_out(got, want, got.dtype, TOL[dtype])
 
 
+@pytest.mark.parametrize("route", [0, WG])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn, torch.float32])
 @pytest.mark.parametrize("bs", [16, 32, 128])
-def test_decode_block_sizes_and_edges(dev, dtype, bs):
-    announce(f"decode {dtype} bs {bs} with ctx 0/1/holes")
+def test_decode_block_sizes_and_edges(dev, dtype, bs, route):
+    if route == WG and dtype == torch.float32:
+        pytest.skip("the workgroup route serves 16-bit and quantised caches")
+    announce(f"decode {dtype} bs {bs} with ctx 0/1/holes, route {route}")
     ctx = torch.tensor([0, 1, 2, bs - 1, bs, bs + 1, 5 * bs + 7, 31], dtype=torch.int64)
     q, k, v, bt, ctx, ks, vs = _case(7 * bs, 8, 8, 2, bs, 80, 6, dtype, ctx=ctx)
     bt[6, 2] = -1  # an absent block inside a context: its tokens are skipped
-    got = _run(dev, q, k, v, bt, ctx, 0.09, 8, 2, ks, vs)
+    got = _run(dev, q, k, v, bt, ctx, 0.09, 8, 2, ks, vs, split_tokens=route)
     want = _oracle(q, k, v, bt, ctx, 0.09, 8, 2, ks, vs)
     assert_close_out(got, want, got.dtype, TOL[dtype])
     assert torch.count_nonzero(got[0]) == 0  # context 0 -> zeros
-    got32 = _run(dev, q, k, v, bt, ctx.to(torch.int32), 0.09, 8, 2, ks, vs)
+    got32 = _run(dev, q, k, v, bt, ctx.to(torch.int32), 0.09, 8, 2, ks, vs, split_tokens=route)
     assert torch.equal(got, got32)
 
 
@@ -285,7 +294,40 @@ def test_decode_q_dtype_differs_from_cache(dev, kv, qdt, group):
     q, k, v, bt, ctx, ks, vs = _case(81, 12, group * Hkv, Hkv, 16, 160, 12, kv)
     q = torch.randn(q.shape, generator=torch.Generator().manual_seed(82)).to(qdt)
     want = _oracle(q, k, v, bt, ctx, 0.09, group * Hkv, Hkv, ks, vs)
-    for st in (0, 64):
+    for st in (0, 64, WG):
         got = _run(dev, q, k, v, bt, ctx, 0.09, group * Hkv, Hkv, ks, vs, split_tokens=st)
         assert got.dtype == qdt
         assert_close_out(got, want, got.dtype, TOL[kv])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
+def test_decode_workgroup_route_small_batches(dev, dtype):
+    """The workgroup route (one workgroup per sequence and KV head, waves
+    merged in LDS) on the shapes it serves: 32 sequences of up to 4096 tokens
+    (8 waves per workgroup) and 60 of 300-800 (4 waves), with empty rows, each
+    against the oracle and against stream-K."""
+    for B, Hq, lo, hi in ((32, 32, 256, 4096), (60, 16, 300, 800)):
+        announce(f"decode {dtype} workgroup route, batch {B}, contexts [{lo}, {hi}]")
+        g = torch.Generator().manual_seed(500 + B)
+        ctx = torch.randint(lo, hi + 1, (B,), generator=g)
+        ctx[[1, B - 1]] = 0
+        mb = (hi + 255) // 256
+        q, k, v, bt, ctx, ks, vs = _case(501 + B, B, Hq, 8, 256, B * mb + 8, mb, dtype, ctx=ctx)
+        want = _oracle(q, k, v, bt, ctx, 0.088, Hq, 8, ks, vs)
+        got = _run(dev, q, k, v, bt, ctx, 0.088, Hq, 8, ks, vs, split_tokens=WG)
+        assert_close_out(got, want, got.dtype, TOL[dtype])
+        assert torch.count_nonzero(got[[1, B - 1]].float()) == 0
+        sk = _run(dev, q, k, v, bt, ctx, 0.088, Hq, 8, ks, vs)
+        assert_close_out(got, sk.double(), got.dtype, TOL[dtype])
+
+
+def test_decode_workgroup_route_refusals(dev):
+    """fp32 caches and block tables whose per-wave share spans more than 62
+    blocks are refused before any launch."""
+    from mkv._lib import MkvError
+    q, k, v, bt, ctx, ks, vs = _case(9, 2, 8, 2, 16, 64, 4, torch.float32)
+    with pytest.raises(MkvError, match="dtype"):
+        _run(dev, q, k, v, bt, ctx, 0.1, 8, 2, split_tokens=WG)
+    q, k, v, bt, ctx, ks, vs = _case(10, 1, 8, 2, 16, 600, 600, torch.bfloat16)
+    with pytest.raises(MkvError):
+        _run(dev, q, k, v, bt, ctx, 0.1, 8, 2, split_tokens=WG)

@@ -84,10 +84,11 @@ class OracleAttentionModel(E.Qwen3Model):
         return out.to(q.dtype).to(q.device).reshape(q.shape[0], Hq * self.cfg.head_dim)
 
 
-@pytest.mark.parametrize("split", [0, 32])
+@pytest.mark.parametrize("split", [0, 32, -1])
 def test_engine_logits_match_the_oracle_attention_engine(dev, monkeypatch, split):
     """Every step's logits against the same engine with the oracle's
-    attention; decode by stream-K (split 0) and by 32-token split-K."""
+    attention; decode by stream-K (split 0), by 32-token split-K and by the
+    workgroup route (-1, one workgroup per sequence and KV head)."""
     announce(f"engine: logits vs the same engine with oracle attention, every step, split {split}")
     prompts = _prompts(12)
     eng = _engine(dev, True, split=split)
