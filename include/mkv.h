@@ -213,9 +213,9 @@ int mkv_fp8_calibrate_per_tensor(const void* key, int64_t key_row_stride,
  * for BF16/F16/FP8/INT8 KV and batch <= 8192, else split-K with a
  * library-chosen split); > 0 = split-K with that many tokens per work item
  * (a multiple of 32); MKV_DECODE_WORKGROUP = one workgroup per (sequence,
- * KV head) whose waves split the sequence and merge in LDS (BF16/F16/FP8/
- * INT8 KV; no workspace, one launch; MKV_ERR_BAD_SHAPE when a wave's share
- * of the widest block table would span more than 62 blocks).
+ * KV head) whose waves split the sequence and merge in LDS (every KV
+ * format; no workspace, one launch; MKV_ERR_BAD_SHAPE when a wave's share of
+ * the widest block table would span more than 62 blocks).
  * workspace: >= mkv_paged_decode_workspace_size(...)
  * bytes with the same arguments (the size of the route those arguments
  * select: stream-K partial slots for the persistent grid, or split-K

@@ -748,54 +748,19 @@ paged_decode_mfma16_2w_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kWgMaxWaves = 8;
 
-template <int KV_DT>
-MKV_DEV void wg_decode(const DecodeArgs& a) {
+// The LDS merge of the workgroup route: every wave writes its (acc, m, l)
+// (lane (kg, c) holds O[head 4kg + r][dim 8c + mm] in acc[mm][r], m and l of
+// head c), then the workgroup combines the nw partials of each (head, 8-dim
+// chunk) with the log-sum-exp rule and writes the output row.  v_mul: the
+// per-tensor V scale (1 otherwise).
+MKV_DEV void wg_merge_store(const DecodeArgs& a, const WorkItem& it, const f32x4 (&acc)[8], float m_run,
+                            float l_col, float v_mul) {
   extern __shared__ float wg_lds[];
   const int nw = blockDim.x >> 6;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
   const int G = a.group;
-  WorkItem it;
-  it.b = (int)(blockIdx.x / (unsigned)a.num_kv_heads);
-  it.kvh = (int)blockIdx.x - it.b * a.num_kv_heads;
-  int64_t L = load_index(a.context_lens, it.b, a.ctx_i64);
-  const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
-  L = L < 0 ? 0 : (L > cap ? cap : L);
-  const int tiles = (int)((L + 31) >> 5);
-  const int per = (tiles + nw - 1) / nw;  // tiles per wave
-  const int64_t tb = (int64_t)wv * per * 32, te = tb + (int64_t)per * 32;
-  it.t_begin = (int)(tb < L ? tb : L);
-  it.t_end = (int)(te < L ? te : L);
-  it.split = wv;
-  it.num_splits = nw;
-
-  QOps<KV_DT> qop;
-  const float k_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.k_scale) : 1.0f;
-  const float score_mul = load_q_operands<KV_DT>(a, it.b, it.kvh, qop, k_mul);
-  f32x4 acc[8];
-#pragma unroll
-  for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = kNegBig, l_run = 0.0f;
-  if (it.t_begin < it.t_end) {
-    const ItemLoad Ld = item_load_setup<KV_DT>(a, it);
-    Tile16<KV_DT> ta, tb2;
-    load_tile16<KV_DT>(a, it, Ld, it.t_begin, ta);
-    for (int t0 = it.t_begin;;) {
-      load_tile16<KV_DT>(a, it, Ld, t0 + 32, tb2);
-      compute_tile16<KV_DT>(ta, t0, it.t_end, qop, score_mul, acc, m_run, l_run);
-      t0 += 32;
-      if (t0 >= it.t_end) break;
-      load_tile16<KV_DT>(a, it, Ld, t0 + 32, ta);
-      compute_tile16<KV_DT>(tb2, t0, it.t_end, qop, score_mul, acc, m_run, l_run);
-      t0 += 32;
-      if (t0 >= it.t_end) break;
-    }
-  }
-  float l_col = l_run + __shfl_xor(l_run, 16);
-  l_col += __shfl_xor(l_col, 32);
-
-  // this wave's partial: O[head 4kg + r][dim 8c + mm] = acc[mm][r]
   float* acc_l = wg_lds;
   float* m_l = wg_lds + nw * G * kHeadDim;
   float* l_l = m_l + nw * G;
@@ -813,8 +778,6 @@ MKV_DEV void wg_decode(const DecodeArgs& a) {
     l_l[wv * G + c] = l_col;
   }
   __syncthreads();
-
-  const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
   for (int u = threadIdx.x; u < G * 16; u += blockDim.x) {
     const int h = u >> 4, d0 = (u & 15) * 8;
     float M = kNegBig;
@@ -842,10 +805,175 @@ MKV_DEV void wg_decode(const DecodeArgs& a) {
   }
 }
 
+// Work item of wave wv of the workgroup route: the sequence's 32-token tiles
+// cut into nw consecutive ranges.
+MKV_DEV WorkItem wg_item(const DecodeArgs& a) {
+  const int nw = blockDim.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  WorkItem it;
+  it.b = (int)(blockIdx.x / (unsigned)a.num_kv_heads);
+  it.kvh = (int)blockIdx.x - it.b * a.num_kv_heads;
+  int64_t L = load_index(a.context_lens, it.b, a.ctx_i64);
+  const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
+  L = L < 0 ? 0 : (L > cap ? cap : L);
+  const int tiles = (int)((L + 31) >> 5);
+  const int per = (tiles + nw - 1) / nw;
+  const int64_t tb = (int64_t)wv * per * 32, te = tb + (int64_t)per * 32;
+  it.t_begin = (int)(tb < L ? tb : L);
+  it.t_end = (int)(te < L ? te : L);
+  it.split = wv;
+  it.num_splits = nw;
+  return it;
+}
+
+template <int KV_DT>
+MKV_DEV void wg_decode(const DecodeArgs& a) {
+  const WorkItem it = wg_item(a);
+
+  QOps<KV_DT> qop;
+  const float k_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.k_scale) : 1.0f;
+  const float score_mul = load_q_operands<KV_DT>(a, it.b, it.kvh, qop, k_mul);
+  f32x4 acc[8];
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegBig, l_run = 0.0f;
+  if (it.t_begin < it.t_end) {
+    const ItemLoad Ld = item_load_setup<KV_DT>(a, it);
+    Tile16<KV_DT> ta, tb2;
+    load_tile16<KV_DT>(a, it, Ld, it.t_begin, ta);
+    for (int t0 = it.t_begin;;) {
+      load_tile16<KV_DT>(a, it, Ld, t0 + 32, tb2);
+      compute_tile16<KV_DT>(ta, t0, it.t_end, qop, score_mul, acc, m_run, l_run);
+      t0 += 32;
+      if (t0 >= it.t_end) break;
+      load_tile16<KV_DT>(a, it, Ld, t0 + 32, ta);
+      compute_tile16<KV_DT>(tb2, t0, it.t_end, qop, score_mul, acc, m_run, l_run);
+      t0 += 32;
+      if (t0 >= it.t_end) break;
+    }
+  }
+  float l_col = l_run + __shfl_xor(l_run, 16);
+  l_col += __shfl_xor(l_col, 32);
+  const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
+  wg_merge_store(a, it, acc, m_run, l_col, v_mul);
+}
+
 template <int KV_DT>
 __global__ __launch_bounds__(kWgMaxWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
 paged_decode_wg_kernel(DecodeArgs a) {
   wg_decode<KV_DT>(a);
+}
+
+// fp32 caches on the workgroup route: 16-token tiles on v_mfma_f32_16x16x4_f32
+// (the split-K fp32 kernel's arithmetic), loaded through per-tile buffer
+// descriptors one tile ahead of the math.
+struct TileF32 {
+  u32x4 k[8];     // K row of token t0 + c, dims 32kg .. 32kg+31
+  u32x4 v[4][2];  // V rows of tokens t0 + 4kg + r, dims 8c .. 8c+7
+  bool ok;        // block present
+};
+
+MKV_DEV void load_tile_f32(const DecodeArgs& a, const WorkItem& it, const ItemLoad& L, int t0, TileF32& T) {
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+  const int bs_mask = (1 << a.idx.bs_log2) - 1;
+  int slot = (t0 >> a.idx.bs_log2) - L.blk0;
+  slot = slot > 63 ? 63 : slot;
+  const int64_t phys = __builtin_amdgcn_readlane(L.my_phys, slot);
+  const int64_t off = L.head_bytes + (int64_t)(t0 & bs_mask) * L.row_bytes;
+  const __amdgpu_buffer_rsrc_t rk = rows_rsrc(a.k_cache, phys, L.blk_bytes, off);
+  const __amdgpu_buffer_rsrc_t rv = rows_rsrc(a.v_cache, phys, L.blk_bytes, off);
+  T.ok = phys >= 0;
+  const uint32_t ko = (t0 + c < it.t_end) ? (uint32_t)L.k_voff : kOob;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) T.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 16 * i, 0, kAuxNt);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t vo = (t0 + 4 * kg + r < it.t_end) ? (uint32_t)(L.v_voff + r * L.row_bytes) : kOob;
+    T.v[r][0] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, kAuxNt);
+    T.v[r][1] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo + 16, 0, kAuxNt);
+  }
+}
+
+MKV_DEV void compute_tile_f32(const TileF32& T, int t0, int t_end, const float (&qf)[32], float score_mul,
+                              f32x4 (&acc)[8], float& m_run, float& l_run) {
+  const int kg = (threadIdx.x & 63) >> 4;
+  f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < 32; ++st)
+    s = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(T.k[st >> 2][st & 3]), qf[st], s, 0, 0, 0);
+  float mx = kNegBig;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const bool ok = t0 + 4 * kg + r < t_end && T.ok;
+    s[r] = ok ? s[r] * score_mul : -__builtin_huge_valf();
+    mx = fmaxf(mx, s[r]);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float m_new = fmaxf(m_run, mx);
+  const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+  m_run = m_new;
+  float p[4], psum = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    p[r] = __builtin_amdgcn_exp2f(s[r] - m_new);
+    psum += p[r];
+  }
+  l_run = l_run * alpha + psum;
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float ar = __shfl(alpha, 4 * kg + r);
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) acc[mm][r] *= ar;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm)
+      acc[mm] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], __uint_as_float(T.v[r][mm >> 2][mm & 3]), acc[mm],
+                                                      0, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(kWgMaxWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
+paged_decode_wg_f32_kernel(DecodeArgs a) {
+  const WorkItem it = wg_item(a);
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+  float qf[32];
+  if (c < a.group) {
+    const int64_t qoff = (int64_t)it.b * a.q_stride + (int64_t)(it.kvh * a.group + c) * kHeadDim + 32 * kg;
+    load_q32(a.q, a.q_dtype, qoff, qf);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
+  }
+  const float score_mul = a.sm_scale * kLog2e;
+  f32x4 acc[8];
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegBig, l_run = 0.0f;
+  if (it.t_begin < it.t_end) {
+    const ItemLoad Ld = item_load_setup<MKV_DTYPE_F32>(a, it);
+    TileF32 ta, tb;
+    load_tile_f32(a, it, Ld, it.t_begin, ta);
+    for (int t0 = it.t_begin;;) {
+      load_tile_f32(a, it, Ld, t0 + 16, tb);
+      compute_tile_f32(ta, t0, it.t_end, qf, score_mul, acc, m_run, l_run);
+      t0 += 16;
+      if (t0 >= it.t_end) break;
+      load_tile_f32(a, it, Ld, t0 + 16, ta);
+      compute_tile_f32(tb, t0, it.t_end, qf, score_mul, acc, m_run, l_run);
+      t0 += 16;
+      if (t0 >= it.t_end) break;
+    }
+  }
+  float l_col = l_run + __shfl_xor(l_run, 16);
+  l_col += __shfl_xor(l_col, 32);
+  wg_merge_store(a, it, acc, m_run, l_col, 1.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -1738,7 +1866,6 @@ int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_
     return MKV_ERR_BAD_STRIDE;
   if (split_tokens != MKV_DECODE_WORKGROUP && (split_tokens < 0 || split_tokens % 32 != 0))
     return MKV_ERR_BAD_SHAPE;
-  if (split_tokens == MKV_DECODE_WORKGROUP && kv_dtype == MKV_DTYPE_F32) return MKV_ERR_UNSUPPORTED_DTYPE;
   const int qb = q_dtype == MKV_DTYPE_F32 ? 4 : 2;
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u)
@@ -1784,6 +1911,9 @@ int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_
     a.ws_ml = nullptr;
     const dim3 grid((unsigned)((int64_t)batch * num_kv_heads)), block(nw * kWave);
     switch (fmt) {
+      case MKV_DTYPE_F32:
+        hipLaunchKernelGGL(paged_decode_wg_f32_kernel, grid, block, lds, s, a);
+        break;
       case MKV_DTYPE_FP8E4M3:
         hipLaunchKernelGGL(paged_decode_wg_kernel<MKV_DTYPE_FP8E4M3>, grid, block, lds, s, a);
         break;

@@ -393,7 +393,7 @@ def paged_attention_decode(query: torch.Tensor, k_cache: torch.Tensor, v_cache: 
     split_tokens (an addition; 0 by default) selects the schedule:
     0 = stream-K over the whole batch, n > 0 = split-K in n-token splits,
     DECODE_WORKGROUP (-1) = one workgroup per (sequence, KV head) whose
-    waves split the sequence and merge in LDS (16-bit and quantised caches)."""
+    waves split the sequence and merge in LDS (one launch, no workspace)."""
     return _decode(query, k_cache, v_cache, block_tables, context_lens, scale, num_heads,
                    num_kv_heads, head_dim, split_tokens=split_tokens)
 

@@ -32,12 +32,13 @@ def _oracle(q, k, v, bt, ctx, scale, Hq, Hkv, ks=None, vs=None):
     return R.paged_decode_ref(q.double(), k, v, bt, ctx, scale, Hq, Hkv, ks, vs)
 
 
-def test_decode_small_fp32(dev):
-    announce("decode: batch 4, 16/8 heads, fp32, bs 256, pool 64")
+@pytest.mark.parametrize("route", [0, -1])
+def test_decode_small_fp32(dev, route):
+    announce(f"decode: batch 4, 16/8 heads, fp32, bs 256, pool 64, route {route}")
     w = W.decode_small(seed=1)
     args = (w["q"], w["k_cache"], w["v_cache"], w["block_tables"], w["context_lens"], w["scale"],
             w["num_heads"], w["num_kv_heads"])
-    got = _run(dev, *args)
+    got = _run(dev, *args, split_tokens=route)
     want = _oracle(*args)
     assert_close_out(got, want, got.dtype, 2e-3)
 
@@ -105,8 +106,6 @@ WG = A.DECODE_WORKGROUP
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn, torch.float32])
 @pytest.mark.parametrize("group", [1, 2, 4, 8, 16])
 def test_decode_group_sizes(dev, dtype, group, route):
-    if route == WG and dtype == torch.float32:
-        pytest.skip("the workgroup route serves 16-bit and quantised caches")
     announce(f"decode {dtype} group {group} route {route}")
     Hkv = 2
     q, k, v, bt, ctx, ks, vs = _case(100 + group, 6, Hkv * group, Hkv, 32, 64, 10, dtype)
@@ -119,8 +118,6 @@ def test_decode_group_sizes(dev, dtype, group, route):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn, torch.float32])
 @pytest.mark.parametrize("bs", [16, 32, 128])
 def test_decode_block_sizes_and_edges(dev, dtype, bs, route):
-    if route == WG and dtype == torch.float32:
-        pytest.skip("the workgroup route serves 16-bit and quantised caches")
     announce(f"decode {dtype} bs {bs} with ctx 0/1/holes, route {route}")
     ctx = torch.tensor([0, 1, 2, bs - 1, bs, bs + 1, 5 * bs + 7, 31], dtype=torch.int64)
     q, k, v, bt, ctx, ks, vs = _case(7 * bs, 8, 8, 2, bs, 80, 6, dtype, ctx=ctx)
@@ -300,7 +297,7 @@ def test_decode_q_dtype_differs_from_cache(dev, kv, qdt, group):
         assert_close_out(got, want, got.dtype, TOL[kv])
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn, torch.float32])
 def test_decode_workgroup_route_small_batches(dev, dtype):
     """The workgroup route (one workgroup per sequence and KV head, waves
     merged in LDS) on the shapes it serves: 32 sequences of up to 4096 tokens
@@ -321,13 +318,10 @@ def test_decode_workgroup_route_small_batches(dev, dtype):
         assert_close_out(got, sk.double(), got.dtype, TOL[dtype])
 
 
-def test_decode_workgroup_route_refusals(dev):
-    """fp32 caches and block tables whose per-wave share spans more than 62
-    blocks are refused before any launch."""
+def test_decode_workgroup_route_refusal(dev):
+    """A block table whose per-wave share would span more than 62 blocks is
+    refused before any launch."""
     from mkv._lib import MkvError
-    q, k, v, bt, ctx, ks, vs = _case(9, 2, 8, 2, 16, 64, 4, torch.float32)
-    with pytest.raises(MkvError, match="dtype"):
-        _run(dev, q, k, v, bt, ctx, 0.1, 8, 2, split_tokens=WG)
     q, k, v, bt, ctx, ks, vs = _case(10, 1, 8, 2, 16, 600, 600, torch.bfloat16)
     with pytest.raises(MkvError):
         _run(dev, q, k, v, bt, ctx, 0.1, 8, 2, split_tokens=WG)
