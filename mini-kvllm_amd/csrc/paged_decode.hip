@@ -67,7 +67,9 @@ struct DecodeArgs {
   float* ws_acc;  // [batch * num_heads][max_splits][head_dim]
   float* ws_ml;   // [batch * num_heads][max_splits][2]  (m, l), log2 domain
   // stream-K decomposition (16-bit KV): partial slots per wave and metadata
-  int* sk_meta;     // [batch + 1] tile prefix per sequence
+  int* sk_meta;     // [batch + 1] tile prefix per sequence, then [batch] x 3 merge
+                    // metadata (first / last contributing group, slot of the first)
+  int seq_cost;     // split cost of entering a sequence, in quarter columns
   int num_waves;    // persistent waves in the grid
   int first_waves;  // waves of the first dispatch round (== num_waves: even split)
 };
@@ -1240,8 +1242,6 @@ MKV_DEV int64_t stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
   }
   if (tid == 0) pre[0] = 0;
   __syncthreads();
-  if (blockIdx.x == 0)
-    for (int i = tid; i <= a.batch; i += kDecWaves * kWave) a.sk_meta[i] = pre[i];
   return running;
 }
 
@@ -1254,6 +1254,14 @@ MKV_DEV int64_t stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
 // the second-round groups the rest; with one workgroup per CU the split is
 // even (w1 = W / Hkv).
 constexpr int kFirstSharePct = 58;
+// Split units per column (the cost-balanced split below).  Every range is at
+// least kColCost units wide, so a range inside an item holds at least one of
+// its columns: the merge kernel reads every group between an item's first and
+// last contributor.
+constexpr int kColCost = 4;
+// Split units for entering a sequence: 1.25 columns (against 0, 0.75 and 2
+// columns: +0.9% at the batch-256 FP8 step, +1-4% at batches 8-128).
+constexpr int kSeqCost = 5;
 
 // Contiguous split of `total` units (columns) over `parts` parts (wave
 // groups); the first `parts1` parts (the first dispatch round) take
@@ -1287,7 +1295,7 @@ MKV_DEV StreamSplit make_split(int64_t total, int parts, int first_parts) {
   if (first_parts <= 0 || first_parts >= parts) {
     p.parts1 = parts;
     p.per1 = (total + parts - 1) / parts;
-    p.per1 = p.per1 < 1 ? 1 : p.per1;
+    p.per1 = p.per1 < kColCost ? kColCost : p.per1;
     p.base = total;
     p.per2 = 1;
     return p;
@@ -1295,12 +1303,12 @@ MKV_DEV StreamSplit make_split(int64_t total, int parts, int first_parts) {
   p.parts1 = first_parts;
   const int64_t t1 = total * kFirstSharePct / 100;
   p.per1 = (t1 + first_parts - 1) / first_parts;
-  p.per1 = p.per1 < 1 ? 1 : p.per1;
+  p.per1 = p.per1 < kColCost ? kColCost : p.per1;
   const int64_t head = (int64_t)first_parts * p.per1;
   p.base = head < total ? head : total;
   const int p2 = parts - first_parts;
   p.per2 = (total - p.base + p2 - 1) / p2;
-  p.per2 = p.per2 < 1 ? 1 : p.per2;
+  p.per2 = p.per2 < kColCost ? kColCost : p.per2;
   return p;
 }
 
@@ -1312,13 +1320,70 @@ MKV_DEV StreamSplit stream_split(const DecodeArgs& a, int64_t columns) {
   return make_split(columns, groups, first);
 }
 
+// Cost-balanced split.  A wave's time is its tiles plus a fixed cost for
+// every sequence its range enters (the item's q, its finish stores and its
+// partial last tile: ~1.25 tiles measured per sequence), so the groups split
+// a cost stream, not the column stream: column g of sequence b costs
+// kColCost units and stands at cost(g) = kColCost * g + a.seq_cost * b
+// (kColCost is defined with the split above).
+
+MKV_DEV int64_t stream_cost_total(const DecodeArgs& a, int64_t columns) {
+  return kColCost * columns + (int64_t)a.seq_cost * a.batch;
+}
+
+// The first column whose cost is at least x (the column count past the end).
+MKV_DEV int64_t cost_to_col(const DecodeArgs& a, const int* pre, int64_t x) {
+  int lo = 0, hi = a.batch;  // largest b whose first column costs <= x
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (kColCost * (int64_t)lds_uniform(pre, mid) + (int64_t)a.seq_cost * mid <= x) lo = mid; else hi = mid;
+  }
+  const int64_t p0 = lds_uniform(pre, lo), p1 = lds_uniform(pre, lo + 1);
+  const int64_t rem = x - kColCost * p0 - (int64_t)a.seq_cost * lo;
+  const int64_t g = p0 + (rem <= 0 ? 0 : (rem + kColCost - 1) / kColCost);
+  return g < p1 ? g : p1;
+}
+
+// Workgroup 0 publishes, per sequence, the groups whose ranges hold its
+// first and last columns and the partial slot the first of them used (0 when
+// its range starts exactly at the sequence), for the merge kernel.
+MKV_DEV void publish_merge_meta(const DecodeArgs& a, const StreamSplit& sp, const int* pre) {
+  int* meta = a.sk_meta + a.batch + 1;
+  for (int b = threadIdx.x; b < a.batch; b += blockDim.x) {
+    const int64_t p0 = pre[b], p1 = pre[b + 1];
+    int glo = 0, ghi = 0, s0 = 0;
+    if (p1 > p0) {
+      const int64_t base = (int64_t)a.seq_cost * b;
+      glo = sp.part_of(kColCost * p0 + base);
+      ghi = sp.part_of(kColCost * (p1 - 1) + base);
+      // first column of glo's range, by the same rule as cost_to_col
+      const int64_t x = sp.begin(glo);
+      int lo = 0, hi = a.batch;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (kColCost * (int64_t)pre[mid] + (int64_t)a.seq_cost * mid <= x) lo = mid; else hi = mid;
+      }
+      const int64_t q0 = pre[lo], q1 = pre[lo + 1];
+      const int64_t rem = x - kColCost * q0 - (int64_t)a.seq_cost * lo;
+      int64_t g0 = q0 + (rem <= 0 ? 0 : (rem + kColCost - 1) / kColCost);
+      g0 = g0 < q1 ? g0 : q1;
+      s0 = p0 <= g0 ? 0 : 1;
+    }
+    meta[3 * b] = glo;
+    meta[3 * b + 1] = ghi;
+    meta[3 * b + 2] = s0;
+  }
+  for (int i = threadIdx.x; i <= a.batch; i += blockDim.x) a.sk_meta[i] = pre[i];
+}
+
 template <int KV_DT, bool kSmallGroup>
 MKV_DEV void stream_decode(const DecodeArgs& a) {
   constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
   extern __shared__ int sk_lds[];
   int* pre = sk_lds;                 // [batch + 1]
   int* lens = sk_lds + a.batch + 1;  // [batch]
-  const StreamSplit sp = stream_split(a, stream_prefix(a, pre, lens));
+  const StreamSplit sp = stream_split(a, stream_cost_total(a, stream_prefix(a, pre, lens)));
+  if (blockIdx.x == 0) publish_merge_meta(a, sp, pre);
 
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
@@ -1326,8 +1391,8 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
   const int grp = w / a.num_kv_heads;  // this wave: KV head w % Hkv of its group's columns
   const int kvh = w - grp * a.num_kv_heads;
   if (grp >= sp.parts) return;
-  const int64_t g0 = sp.begin(grp);
-  const int64_t g1 = sp.end(grp);
+  const int64_t g0 = cost_to_col(a, pre, sp.begin(grp));
+  const int64_t g1 = cost_to_col(a, pre, sp.end(grp));
   if (g0 >= g1) return;
 
   const int row_bytes = (int)(a.idx.row_elems * kEb);
@@ -1444,9 +1509,9 @@ constexpr auto stream_kernel() {
 // denominator are wave reductions rather than a chain of dependent loads, and
 // the accumulator rows are read four contributors at a time (independent
 // loads in flight) with each contributor's weight taken from its lane.
-MKV_DEV int merge_slot(const DecodeArgs& a, const StreamSplit& sp, int64_t gs, int grp, int kvh, int h) {
+MKV_DEV int merge_slot(const DecodeArgs& a, int glo, int s0, int grp, int kvh, int h) {
   const int wp = grp * a.num_kv_heads + kvh;
-  return ((wp * 2 + (gs <= sp.begin(grp) ? 0 : 1)) * a.group + h);
+  return ((wp * 2 + (grp == glo ? s0 : 0)) * a.group + h);
 }
 
 __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_kernel(DecodeArgs a,
@@ -1458,13 +1523,11 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_ke
   const int hq = (int)(wv - (int64_t)b * a.num_heads);
   const int kvh = hq / a.group, h = hq - kvh * a.group;
   const int p0 = a.sk_meta[b], n = a.sk_meta[b + 1] - p0;
-  const StreamSplit sp = stream_split(a, (int64_t)a.sk_meta[a.batch]);
+  const int* meta = a.sk_meta + a.batch + 1 + 3 * b;
   const int64_t off = (int64_t)b * a.out_stride + (int64_t)hq * kHeadDim + 2 * lane;
   float o0 = 0.0f, o1 = 0.0f, l = 0.0f;
   if (n > 0) {
-    const int64_t gs = p0;  // the item's columns
-    const int64_t ge = gs + n;
-    const int glo = sp.part_of(gs), ghi = sp.part_of(ge - 1);
+    const int glo = meta[0], ghi = meta[1], s0 = meta[2];
     if (glo == ghi) return;  // written whole by the main kernel
     const int nc = ghi - glo + 1;
     if (nc <= kWave) {
@@ -1472,7 +1535,7 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_ke
       // lane-parallel, and the first four accumulator rows are loaded
       // together (the rows' slots do not depend on (m, l)); the weights
       // follow from the maximum, the remaining rows four at a time.
-      const int my_slot = lane < nc ? merge_slot(a, sp, gs, glo + lane, kvh, h) : 0;
+      const int my_slot = lane < nc ? merge_slot(a, glo, s0, glo + lane, kvh, h) : 0;
       f32x2 x[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {  // nc >= 2; rows u >= nc repeat row 0 with weight 0
@@ -1508,14 +1571,14 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_ke
     } else {
       float M = kNegBig;
       for (int c0 = 0; c0 < nc; c0 += kWave) {
-        if (c0 + lane < nc) M = fmaxf(M, a.ws_ml[(int64_t)merge_slot(a, sp, gs, glo + c0 + lane, kvh, h) * 2]);
+        if (c0 + lane < nc) M = fmaxf(M, a.ws_ml[(int64_t)merge_slot(a, glo, s0, glo + c0 + lane, kvh, h) * 2]);
       }
       M = wave_max(M);
       for (int c0 = 0; c0 < nc; c0 += kWave) {
         int my_slot = 0;
         float wgt = 0.0f;
         if (c0 + lane < nc) {
-          my_slot = merge_slot(a, sp, gs, glo + c0 + lane, kvh, h);
+          my_slot = merge_slot(a, glo, s0, glo + c0 + lane, kvh, h);
           wgt = __builtin_amdgcn_exp2f(a.ws_ml[(int64_t)my_slot * 2] - M);
           l += wgt * a.ws_ml[(int64_t)my_slot * 2 + 1];
         }
@@ -1745,7 +1808,7 @@ int stream_waves() { return device_cus() * kStreamWgPerCu * kDecWaves; }
 
 size_t stream_ws_bytes(int batch, int group) {
   const size_t w = (size_t)stream_waves();
-  return w * 2 * group * (kHeadDim + 2) * sizeof(float) + (size_t)(batch + 2) * sizeof(int);
+  return w * 2 * group * (kHeadDim + 2) * sizeof(float) + (size_t)(4 * batch + 2) * sizeof(int);
 }
 
 // Persistent stream-K launch: one wave per SIMD slot the kernel can hold
@@ -1946,6 +2009,7 @@ int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_
     a.ws_acc = reinterpret_cast<float*>(workspace);
     a.ws_ml = a.ws_acc + slots * kHeadDim;
     a.sk_meta = reinterpret_cast<int*>(a.ws_ml + slots * 2);
+    a.seq_cost = kSeqCost;
     const dim3 block(kDecWaves * kWave);
     // Residency depends on the launch's LDS (the per-sequence prefix): query it
     // once per device for batches up to kStreamSmallBatch and once for larger.

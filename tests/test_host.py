@@ -147,12 +147,13 @@ def test_decode_workspace_and_split_queries():
     assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 1, 256, 128, F32, 0) == (
         4 * 16 * splits4 * 130 * 4 if splits4 > 1 else 0)
     # the default stream-K route needs its partial slots for the persistent
-    # grid and the tile prefix only, not the split-K partials: without a GPU
+    # grid and the per-sequence metadata only, not the split-K partials: without a GPU
     # the CU count query falls back to 512 CUs, i.e. 4096 waves
     nsk = lib.mkv_paged_decode_workspace_size(256, 32, 8, 32, 256, 128, FP8, 0)
     assert lib.mkv_paged_decode_workspace_size(256, 32, 8, 32, 256, 128, BF16, 0) == nsk
-    assert nsk % (2 * 4 * 130 * 4) == (256 + 2) * 4
-    waves = (nsk - (256 + 2) * 4) // (2 * 4 * 130 * 4)
+    # (per sequence: the tile prefix and three merge-metadata words)
+    assert nsk % (2 * 4 * 130 * 4) == (4 * 256 + 2) * 4
+    waves = (nsk - (4 * 256 + 2) * 4) // (2 * 4 * 130 * 4)
     assert waves in (4096, 2048) and nsk < n
     assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 1, 256, 128, FP8, 0) > 0
     # small batches split finer
