@@ -70,6 +70,7 @@ struct DecodeArgs {
   int* sk_meta;     // [batch + 1] tile prefix per sequence, then [batch] x 3 merge
                     // metadata (first / last contributing group, slot of the first)
   int seq_cost;     // split cost of entering a sequence, in quarter columns
+  int first_pct;    // percent of the split that the first dispatch round's groups take
   int num_waves;    // persistent waves in the grid
   int first_waves;  // waves of the first dispatch round (== num_waves: even split)
 };
@@ -1215,8 +1216,8 @@ MKV_DEV void issue_finish(const FinishStores& f) {
 // workgroup 0 also publishes them for the merge kernel).  Returns the total
 // number of columns of the stream.
 MKV_DEV int64_t stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
-  __shared__ int part[kDecWaves * kWave];
-  const int tid = threadIdx.x;
+  __shared__ int wave_tot[kDecWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
   int running = 0;
   for (int base = 0; base < a.batch; base += kDecWaves * kWave) {
@@ -1228,16 +1229,24 @@ MKV_DEV int64_t stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
       lens[b] = (int)L;
       n = (int)((L + kTileTok - 1) / kTileTok);
     }
-    part[tid] = n;
-    __syncthreads();
-    for (int off = 1; off < kDecWaves * kWave; off <<= 1) {
-      const int add = tid >= off ? part[tid - off] : 0;
-      __syncthreads();
-      part[tid] += add;
-      __syncthreads();
+    // inclusive scan inside the wave (shuffles), then across the waves
+    int incl = n;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int y = __shfl_up(incl, off);
+      incl += lane >= off ? y : 0;
     }
-    if (b < a.batch) pre[b + 1] = running + part[tid];
-    running += part[kDecWaves * kWave - 1];
+    if (lane == kWave - 1) wave_tot[wv] = incl;
+    __syncthreads();
+    int before = running, total = running;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) {
+      const int t = wave_tot[w];
+      before += w < wv ? t : 0;
+      total += t;
+    }
+    if (b < a.batch) pre[b + 1] = before + incl;
+    running = total;
     __syncthreads();
   }
   if (tid == 0) pre[0] = 0;
@@ -1253,7 +1262,7 @@ MKV_DEV int64_t stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
 // waves (w1 of them) therefore get kFirstSharePct percent of the columns and
 // the second-round groups the rest; with one workgroup per CU the split is
 // even (w1 = W / Hkv).
-constexpr int kFirstSharePct = 58;
+constexpr int kFirstSharePct = 58;  // (55 / 61 / 64 with the cost-balanced ranges: -0.6% / +0.2% / -0.8%)
 // Split units per column (the cost-balanced split below).  Every range is at
 // least kColCost units wide, so a range inside an item holds at least one of
 // its columns: the merge kernel reads every group between an item's first and
@@ -1288,7 +1297,7 @@ struct StreamSplit {
   }
 };
 
-MKV_DEV StreamSplit make_split(int64_t total, int parts, int first_parts) {
+MKV_DEV StreamSplit make_split(int64_t total, int parts, int first_parts, int first_pct) {
   StreamSplit p;
   p.total = total;
   p.parts = parts;
@@ -1301,7 +1310,7 @@ MKV_DEV StreamSplit make_split(int64_t total, int parts, int first_parts) {
     return p;
   }
   p.parts1 = first_parts;
-  const int64_t t1 = total * kFirstSharePct / 100;
+  const int64_t t1 = total * first_pct / 100;
   p.per1 = (t1 + first_parts - 1) / first_parts;
   p.per1 = p.per1 < kColCost ? kColCost : p.per1;
   const int64_t head = (int64_t)first_parts * p.per1;
@@ -1317,7 +1326,7 @@ MKV_DEV StreamSplit make_split(int64_t total, int parts, int first_parts) {
 MKV_DEV StreamSplit stream_split(const DecodeArgs& a, int64_t columns) {
   const int groups = a.num_waves / a.num_kv_heads;
   const int first = a.first_waves >= a.num_waves ? groups : a.first_waves / a.num_kv_heads;
-  return make_split(columns, groups, first);
+  return make_split(columns, groups, first, a.first_pct);
 }
 
 // Cost-balanced split.  A wave's time is its tiles plus a fixed cost for
@@ -1644,6 +1653,30 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma32_kernel(D
 #pragma unroll
   for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegBig, l_run = 0.0f;
+  // Splits that span at most 64 blocks (every default split): the K/V of
+  // the next 16-token tile are in flight while this one is computed.
+  const int nblk = it.t_end > it.t_begin
+                       ? ((it.t_end - 1) >> a.idx.bs_log2) - (it.t_begin >> a.idx.bs_log2) + 1
+                       : 0;
+  if (nblk > 0 && nblk <= 64) {
+    const ItemLoad Ld = item_load_setup<MKV_DTYPE_F32>(a, it);
+    TileF32 ta, tb;
+    load_tile_f32(a, it, Ld, it.t_begin, ta);
+    for (int t0 = it.t_begin;;) {
+      load_tile_f32(a, it, Ld, t0 + 16, tb);
+      compute_tile_f32(ta, t0, it.t_end, qf, score_mul, acc, m_run, l_run);
+      t0 += 16;
+      if (t0 >= it.t_end) break;
+      load_tile_f32(a, it, Ld, t0 + 16, ta);
+      compute_tile_f32(tb, t0, it.t_end, qf, score_mul, acc, m_run, l_run);
+      t0 += 16;
+      if (t0 >= it.t_end) break;
+    }
+    float l_col = l_run + __shfl_xor(l_run, 16);
+    l_col += __shfl_xor(l_col, 32);
+    finish_item(a, it, acc, m_run, l_col, 1.0f);
+    return;
+  }
   const int64_t bs_mask = (int64_t(1) << a.idx.bs_log2) - 1;
   const int64_t head_off = (int64_t)it.kvh * kHeadDim;
   const float* kc = reinterpret_cast<const float*>(a.k_cache);
@@ -2010,6 +2043,7 @@ int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_
     a.ws_ml = a.ws_acc + slots * kHeadDim;
     a.sk_meta = reinterpret_cast<int*>(a.ws_ml + slots * 2);
     a.seq_cost = kSeqCost;
+    a.first_pct = kFirstSharePct;
     const dim3 block(kDecWaves * kWave);
     // Residency depends on the launch's LDS (the per-sequence prefix): query it
     // once per device for batches up to kStreamSmallBatch and once for larger.
