@@ -70,6 +70,9 @@ def parse_args(argv=None):
     ap.add_argument("--skip-headline", action="store_true",
                     help="run only the secondary measurements (for profiling them); the printed "
                          "line then has no headline value")
+    ap.add_argument("--e2e-no-baselines", action="store_true",
+                    help="e2e extra: time only the mkv engine with captured decode (for profiling "
+                         "it), not the eager and PyTorch-attention engines beside it")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (5 times) and exit; "
                          "its rocprofv3 FETCH_SIZE/WRITE_SIZE calibrate the PMC byte counts")
@@ -728,7 +731,7 @@ def configs_extra(dev, stream, cpu: bool = True) -> dict:
     return res
 
 
-def e2e_extra(dev) -> dict:
+def e2e_extra(dev, baselines: bool = True) -> dict:
     """The end-to-end engine workload: a random-init Qwen3-0.6B-shaped model
     (28 layers, hidden 1024, 16 q / 8 kv heads, head_dim 128, intermediate
     3072, vocab 151936, bf16 weights N(0, 0.02), seed 5) generating 256
@@ -767,6 +770,8 @@ def e2e_extra(dev) -> dict:
                        f"151936), bf16 random weights; 60 prompts of {sum(lens)} tokens (32-512), "
                        "256 output tokens each, T 1.0; max_num_seqs 64, max_num_batched_tokens "
                        "1024, FP8 per-tensor KV, block 256, chunked prefill, captured decode")
+    if not baselines:  # (--e2e-no-baselines: a profile of this engine alone)
+        return res
     # the same engine with eager decode steps (no captured graphs)
     eager = E.Engine(model, num_blocks=512, max_num_seqs=64, max_num_batched_tokens=1024,
                      kv_cache_dtype="fp8_per_tensor", max_model_len=4096, seed=0, use_graphs=False,
@@ -1254,7 +1259,7 @@ def main() -> int:
                     w["key"], w["value"], w["slot_mapping"])
             del kp, vp
         if "e2e" in wanted:
-            extra["e2e_engine"] = e2e_extra(dev)
+            extra["e2e_engine"] = e2e_extra(dev, baselines=not args.e2e_no_baselines)
         if "prefill" in wanted:
             extra["prefill_chunked"] = prefill_extra(dev, stream, cpu=args.cpu_seqs > 0)
         if "latency" in wanted:
