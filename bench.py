@@ -683,6 +683,34 @@ def configs_extra(dev, stream, cpu: bool = True) -> dict:
     res["fp8_decode_b32"] = row
     del kp, vp
 
+    # FP8 decode at the end-to-end engine's decode shape (60 rows of 300-800
+    # tokens, 16 q / 8 kv heads, 16-block tables as the engine's): the three
+    # schedules, the workgroup route being the one the engine uses
+    g = torch.Generator().manual_seed(11)
+    ctx = torch.randint(300, 801, (60,), generator=g)
+    N = 60 * 4 + 16
+    bt = W.fragmented_block_tables(ctx, 256, N, g, max_blocks=16).to(dev)
+    kp = torch.empty(N, 256, 8, HEAD_DIM, dtype=torch.float8_e4m3fn, device=dev)
+    vp = torch.empty_like(kp)
+    W.fill_pool_on_device(kp, 3001)
+    W.fill_pool_on_device(vp, 3002)
+    qd = torch.randn(60, 16, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    sc = torch.full((1,), 0.0125, device=dev)
+    ctxd = ctx.to(dev)
+    out = torch.empty_like(qd)
+    nb = W.alg_bytes_decode(ctx, 256, 16, 8, kv_bytes=1, q_bytes=2)
+    row = {"workload": f"FP8 per-tensor KV, bf16 q, batch 60, 16 q / 8 kv heads, contexts U[300, 800] "
+                       f"sum {int(ctx.sum())}, 16-block tables (the end-to-end engine's decode shape)",
+           "algorithmic_bytes": nb}
+    for name, st in (("stream_k", 0), ("split_k_256", 256), ("workgroup", A.DECODE_WORKGROUP)):
+        fn = lambda st=st: A._decode(qd, kp, vp, bt, ctxd, 0.088, 16, 8, HEAD_DIM, sc, sc,
+                                     split_tokens=st, out=out)
+        us = graph_time_us(fn)
+        row[name] = {"us": round(us, 2), "GBps": round(nb / us / 1e3, 1),
+                     "frac_of_8000_GBps": round(nb / us / 1e3 / PEAK_HBM_GBPS, 4)}
+    res["fp8_decode_b60_engine_shape"] = row
+    del kp, vp
+
     # bf16 decode, the batch-256 workload
     meta = W.decode_b256_metadata(seed=3)
     N, bs = meta["num_blocks"], meta["block_size"]
