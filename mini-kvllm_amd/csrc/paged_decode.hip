@@ -70,6 +70,7 @@ struct DecodeArgs {
   int* sk_meta;     // [batch + 1] tile prefix per sequence, then [batch] x 3 merge
                     // metadata (first / last contributing group, slot of the first)
   int seq_cost;     // split cost of entering a sequence, in quarter columns
+  int defer;        // finishes a stream-K wave may hold in LDS until its range ends
   int first_pct;    // percent of the split that the first dispatch round's groups take
   int num_waves;    // persistent waves in the grid
   int first_waves;  // waves of the first dispatch round (== num_waves: even split)
@@ -1003,7 +1004,21 @@ constexpr int kTileTok = 32;
 constexpr int kStreamMaxBatch = 8192;
 constexpr size_t kStreamMaxLds = (2 * kStreamMaxBatch + 1) * sizeof(int);
 constexpr int kStreamSmallBatch = 2047;
-constexpr size_t kStreamSmallLds = (2 * kStreamSmallBatch + 1) * sizeof(int);
+// Finishes a wave may hold in LDS (batches up to kStreamDeferMaxBatch): each
+// takes 64 lanes x 64 bytes plus 16 bytes per wave.  Holding the finishes
+// before a range's last tile and storing them after it took the batch-256
+// FP8 step from 6188 to 6304-6310 GB/s (one held: 6291).
+constexpr int kStreamDefer = 3;
+constexpr int kStreamDeferMaxBatch = 1024;
+constexpr size_t stream_lds_bytes(int batch, int defer) {
+  return ((size_t)(2 * batch + 1) * sizeof(int) + 15) / 16 * 16 +
+         (size_t)defer * kDecWaves * (kWave * 64 + 16);
+}
+constexpr size_t kStreamSmallLds =
+    stream_lds_bytes(kStreamSmallBatch, 0) > stream_lds_bytes(kStreamDeferMaxBatch, kStreamDefer)
+        ? stream_lds_bytes(kStreamSmallBatch, 0)
+        : stream_lds_bytes(kStreamDeferMaxBatch, kStreamDefer);
+static_assert(kStreamSmallLds <= 65536, "stream-K dynamic LDS");
 
 struct Cursor {
   int b, kvh, t;  // item (sequence, KV head) and tile index inside the item
@@ -1142,6 +1157,24 @@ MKV_DEV void finish_none(FinishStores& f) {
   f.oa = f.ob = f.oc = kOob;
 }
 
+// Store descriptors of an item's finish: its output row (whole) or its
+// partial slot k of wave w (acc, then (m, l)).  All inputs wave-uniform.
+MKV_DEV void finish_rsrc(const DecodeArgs& a, bool whole, int b, int kvh, int w, int k, FinishStores& f) {
+  if (whole) {
+    const int ob = a.q_dtype == MKV_DTYPE_F32 ? 4 : 2;
+    const char* base = reinterpret_cast<const char*>(a.out) +
+                       ((int64_t)b * a.out_stride + (int64_t)kvh * a.group * kHeadDim) * ob;
+    f.ra = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, a.group * kHeadDim * ob, kRsrcFlags);
+    f.rc = f.ra;
+  } else {
+    const int64_t slot0 = ((int64_t)w * 2 + k) * a.group;
+    f.ra = __builtin_amdgcn_make_buffer_rsrc((void*)(a.ws_acc + slot0 * kHeadDim), (short)0,
+                                             a.group * kHeadDim * 4, kRsrcFlags);
+    f.rc = __builtin_amdgcn_make_buffer_rsrc((void*)(a.ws_ml + slot0 * 2), (short)0, a.group * 8,
+                                             kRsrcFlags);
+  }
+}
+
 MKV_DEV void finish_small_group(const DecodeArgs& a, const Cursor& c, bool whole, int w, int k,
                                 const f32x4 (&acc)[8], float m_col, float l_col, float v_mul,
                                 FinishStores& f) {
@@ -1162,9 +1195,7 @@ MKV_DEV void finish_small_group(const DecodeArgs& a, const Cursor& c, bool whole
 #pragma unroll
     for (int mm = 0; mm < 8; ++mm) x[mm] *= inv;
     const int ob = a.q_dtype == MKV_DTYPE_F32 ? 4 : 2;
-    const char* base = reinterpret_cast<const char*>(a.out) +
-                       ((int64_t)c.b * a.out_stride + (int64_t)c.kvh * a.group * kHeadDim) * ob;
-    f.ra = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, a.group * kHeadDim * ob, kRsrcFlags);
+    finish_rsrc(a, true, c.b, c.kvh, w, k, f);
     const uint32_t off = (uint32_t)((h * kHeadDim + 8 * cc) * ob);
     if (a.q_dtype == MKV_DTYPE_F32) {
 #pragma unroll
@@ -1185,14 +1216,9 @@ MKV_DEV void finish_small_group(const DecodeArgs& a, const Cursor& c, bool whole
       f.oa = valid ? off : kOob;
       f.ob = kOob;
     }
-    f.rc = f.ra;
     f.oc = kOob;
   } else {
-    const int64_t slot0 = ((int64_t)w * 2 + k) * a.group;
-    f.ra = __builtin_amdgcn_make_buffer_rsrc((void*)(a.ws_acc + slot0 * kHeadDim), (short)0,
-                                             a.group * kHeadDim * 4, kRsrcFlags);
-    f.rc = __builtin_amdgcn_make_buffer_rsrc((void*)(a.ws_ml + slot0 * 2), (short)0, a.group * 8,
-                                             kRsrcFlags);
+    finish_rsrc(a, false, c.b, c.kvh, w, k, f);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       f.da[j] = __float_as_uint(x[j]);
@@ -1391,6 +1417,13 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
   extern __shared__ int sk_lds[];
   int* pre = sk_lds;                 // [batch + 1]
   int* lens = sk_lds + a.batch + 1;  // [batch]
+  // deferred finishes of this wave: a.defer records of 64 lanes x 64 bytes,
+  // then 4 ints each (whole, sequence, KV head, slot)
+  const int wl = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  u32x4* dq = reinterpret_cast<u32x4*>(sk_lds + ((2 * a.batch + 1 + 3) & ~3)) + wl * a.defer * kWave * 4;
+  int* dqu = reinterpret_cast<int*>(reinterpret_cast<u32x4*>(sk_lds + ((2 * a.batch + 1 + 3) & ~3)) +
+                                    kDecWaves * a.defer * kWave * 4) + wl * a.defer * 4;
+  int ndef = 0;
   const StreamSplit sp = stream_split(a, stream_cost_total(a, stream_prefix(a, pre, lens)));
   if (blockIdx.x == 0) publish_merge_meta(a, sp, pre);
 
@@ -1470,6 +1503,25 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
         float l_col = l_run + __shfl_xor(l_run, 16);
         l_col += __shfl_xor(l_col, 32);
         finish_small_group(a, cc, whole, w, kslot, acc, m_run, l_col, v_mul, fs);
+        // Finishes before the range's last tile wait in LDS (up to
+        // a.defer of them) and go out after it, so that their stores do not
+        // sit between the tile loads of the read stream.
+        if (g != g1 - 1 && ndef < a.defer) {
+          u32x4* rec = dq + (ndef * kWave + lane) * 4;
+          rec[0] = fs.da;
+          rec[1] = fs.db;
+          rec[2] = u32x4{fs.dc[0], fs.dc[1], fs.oa, fs.ob};
+          rec[3] = u32x4{fs.oc, 0u, 0u, 0u};
+          if (lane == 0) {
+            int* u = dqu + 4 * ndef;
+            u[0] = whole ? 1 : 0;
+            u[1] = cc.b;
+            u[2] = cc.kvh;
+            u[3] = kslot;
+          }
+          ++ndef;
+          finish_none(fs);
+        }
       }
       issue_finish(fs);
     } else if (fin) {
@@ -1484,6 +1536,22 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
     if (++g >= g1) break;
     step(t1b, t0b, g);
     if (++g >= g1) break;
+  }
+  if constexpr (kSmallGroup) {
+    for (int i = 0; i < ndef; ++i) {
+      const int* u = dqu + 4 * i;
+      FinishStores fs;
+      finish_rsrc(a, lds_uniform(u, 0) != 0, lds_uniform(u, 1), lds_uniform(u, 2), w, lds_uniform(u, 3), fs);
+      const u32x4* rec = dq + (i * kWave + lane) * 4;
+      fs.da = rec[0];
+      fs.db = rec[1];
+      const u32x4 r2 = rec[2];
+      fs.dc = u32x2{r2[0], r2[1]};
+      fs.oa = r2[2];
+      fs.ob = r2[3];
+      fs.oc = rec[3][0];
+      issue_finish(fs);
+    }
   }
 }
 
@@ -2034,7 +2102,9 @@ int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_
     if (!workspace) return MKV_ERR_NULL_POINTER;
     if (workspace_bytes < need) return MKV_ERR_WORKSPACE_TOO_SMALL;
     if (reinterpret_cast<uintptr_t>(workspace) & 15u) return MKV_ERR_MISALIGNED;
-    const size_t lds = (size_t)(2 * batch + 1) * sizeof(int);
+    a.defer = batch <= kStreamDeferMaxBatch ? kStreamDefer : 0;
+
+    const size_t lds = stream_lds_bytes(batch, a.defer);
     // Workspace slots are laid out for the largest grid (stream_waves()).
     const size_t slots = (size_t)stream_waves() * 2 * group;
     a.split_tokens = kTileTok;
