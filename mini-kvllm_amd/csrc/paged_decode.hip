@@ -2102,7 +2102,8 @@ int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_
     if (!workspace) return MKV_ERR_NULL_POINTER;
     if (workspace_bytes < need) return MKV_ERR_WORKSPACE_TOO_SMALL;
     if (reinterpret_cast<uintptr_t>(workspace) & 15u) return MKV_ERR_MISALIGNED;
-    a.defer = batch <= kStreamDeferMaxBatch ? kStreamDefer : 0;
+    // (held finishes: the kernels for groups of at most 4 query heads)
+    a.defer = batch <= kStreamDeferMaxBatch && group <= 4 ? kStreamDefer : 0;
 
     const size_t lds = stream_lds_bytes(batch, a.defer);
     // Workspace slots are laid out for the largest grid (stream_waves()).
