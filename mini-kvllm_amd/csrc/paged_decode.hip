@@ -2200,8 +2200,9 @@ int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_
 // Scratch of mkv_paged_decode_noalloc: one array per GPU, held from the
 // library's first use on that GPU until the process ends.  It is sized for
 // the stream-K partial slots of group sizes up to 8 on 256 CUs (2048 waves x
-// 2 slots x 8 heads x 130 floats = 16.3 MiB, plus the per-sequence tile
-// prefix) with room for moderate split-K requests; larger requests are
+// 2 slots x 8 heads x 130 floats = 16.3 MiB, plus four ints per sequence:
+// the tile prefix and the merge metadata) with room for moderate split-K
+// requests (the workgroup route needs none); larger requests are
 // refused.  Host code must not pass the array's name to a kernel: in host
 // code it is a stand-in, not a device address.  The per-device address comes
 // from hipGetSymbolAddress, taken once per device with that device current.
