@@ -138,7 +138,7 @@ def _oracle(q, kq, vq, ks, vs, bt, ctx, scale, Hq, Hkv):
 
 @pytest.mark.parametrize("mode", [FP8_MODE, INT8_MODE])
 @pytest.mark.parametrize("group", [1, 4, 8, 16])
-@pytest.mark.parametrize("split_tokens", [0, 64])
+@pytest.mark.parametrize("split_tokens", [0, 64, -1])
 def test_per_token_decode_groups(dev, mode, group, split_tokens):
     announce(f"decode {mode}: group {group}, split_tokens {split_tokens}")
     Hkv = 2
@@ -167,9 +167,12 @@ def test_per_token_decode_edges(dev, mode, bs):
     assert torch.count_nonzero(got[0]) == 0
     got32 = _run(dev, mode, q, kq, vq, ks, vs, bt, ctx.to(torch.int32), 0.09, 8, 2)
     assert torch.equal(got, got32)
-    # the same through the split-K kernel
+    # the same through the split-K kernel and the workgroup route
     got_sk = _run(dev, mode, q, kq, vq, ks, vs, bt, ctx, 0.09, 8, 2, split_tokens=32)
     assert_close_out(got_sk, want, got.dtype, TOL)
+    got_wg = _run(dev, mode, q, kq, vq, ks, vs, bt, ctx, 0.09, 8, 2, split_tokens=-1)
+    assert_close_out(got_wg, want, got.dtype, TOL)
+    assert torch.count_nonzero(got_wg[0]) == 0
 
 
 @pytest.mark.parametrize("mode", [FP8_MODE, INT8_MODE])
