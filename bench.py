@@ -45,6 +45,7 @@ KV_DESC = {"fp8": "per-tensor e4m3fn", "bf16": "bf16",
            "int8_token": "int8 codes, fp32 scale per token and kv head"}
 
 
+DECODE_CONFIGS = ("fp32_decode_b4", "fp8_decode_b32", "fp8_decode_b60_engine_shape", "bf16_decode_b256")
 EXTRAS = ("configs", "e2e", "append", "prefill", "latency", "producer", "mixed", "copy", "gather")
 
 
@@ -67,6 +68,8 @@ def parse_args(argv=None):
     ap.add_argument("--extra", default="all",
                     help="secondary measurements to run: 'all' or a comma list of "
                          "configs, e2e, append, prefill, latency, producer, mixed, copy, gather")
+    ap.add_argument("--decode-configs", default="all",
+                    help="configs extra: 'all' or a comma list of " + ", ".join(DECODE_CONFIGS))
     ap.add_argument("--skip-headline", action="store_true",
                     help="run only the secondary measurements (for profiling them); the printed "
                          "line then has no headline value")
@@ -86,6 +89,13 @@ def parse_args(argv=None):
         unknown = args.extra_set - set(EXTRAS)
         if unknown:
             ap.error(f"--extra: unknown measurement(s) {sorted(unknown)}; choose from {list(EXTRAS)}")
+    if args.decode_configs == "all":
+        args.decode_config_set = set(DECODE_CONFIGS)
+    else:
+        args.decode_config_set = {x.strip() for x in args.decode_configs.split(",") if x.strip()}
+        unknown = args.decode_config_set - set(DECODE_CONFIGS)
+        if unknown:
+            ap.error(f"--decode-configs: unknown {sorted(unknown)}; choose from {list(DECODE_CONFIGS)}")
     return args
 
 
@@ -618,7 +628,7 @@ def cpu_decode_baseline(q, kc, vc, bt, ctx, scale, num_heads, num_kv_heads, bs, 
             out["o"])
 
 
-def configs_extra(dev, stream, cpu: bool = True) -> dict:
+def configs_extra(dev, stream, cpu: bool = True, which=DECODE_CONFIGS) -> dict:
     """The other decode configurations of the workload set, each with its
     algorithmic bytes, HBM roofline fraction, the reference's CPU decode path
     timed on the same inputs, and the largest difference from it:
@@ -633,129 +643,133 @@ def configs_extra(dev, stream, cpu: bool = True) -> dict:
 
     res = {}
     # fp32 decode, batch 4
-    w = W.decode_small(seed=1)
-    q, kc, vc = w["q"].to(dev), w["k_cache"].to(dev), w["v_cache"].to(dev)
-    bt, ctx = w["block_tables"].to(dev), w["context_lens"].to(dev)
-    out = torch.empty_like(q)
-    fn = lambda: A._decode(q, kc, vc, bt, ctx, w["scale"], 16, 8, HEAD_DIM, out=out)
-    us = graph_time_us(fn)
-    nb = W.alg_bytes_decode(w["context_lens"], 256, 16, 8, kv_bytes=4, q_bytes=4)
-    row = {"workload": f"fp32 KV and q, batch 4, 16 q / 8 kv heads, contexts {w['context_lens'].tolist()}",
-           "us": round(us, 2), "algorithmic_bytes": nb, "GBps": round(nb / us / 1e3, 1),
-           "frac_of_8000_GBps": round(nb / us / 1e3 / PEAK_HBM_GBPS, 4),
-           "note": "35 MB of KV: the step is launch- and latency-bound and the bytes fit the "
-                   "256 MB Infinity Cache, so this is not an HBM rate"}
-    if cpu:
-        rec, o = cpu_decode_baseline(w["q"], w["k_cache"], w["v_cache"], w["block_tables"],
-                                     w["context_lens"], w["scale"], 16, 8, 256, None, None, nb,
-                                     "the whole workload, fp32")
-        row["cpu_baseline"] = rec
-        row["max_abs_err_vs_cpu"] = float((out.cpu() - o).abs().max())
-    res["fp32_decode_b4"] = row
-    del q, kc, vc
+    if "fp32_decode_b4" in which:
+        w = W.decode_small(seed=1)
+        q, kc, vc = w["q"].to(dev), w["k_cache"].to(dev), w["v_cache"].to(dev)
+        bt, ctx = w["block_tables"].to(dev), w["context_lens"].to(dev)
+        out = torch.empty_like(q)
+        fn = lambda: A._decode(q, kc, vc, bt, ctx, w["scale"], 16, 8, HEAD_DIM, out=out)
+        us = graph_time_us(fn)
+        nb = W.alg_bytes_decode(w["context_lens"], 256, 16, 8, kv_bytes=4, q_bytes=4)
+        row = {"workload": f"fp32 KV and q, batch 4, 16 q / 8 kv heads, contexts {w['context_lens'].tolist()}",
+               "us": round(us, 2), "algorithmic_bytes": nb, "GBps": round(nb / us / 1e3, 1),
+               "frac_of_8000_GBps": round(nb / us / 1e3 / PEAK_HBM_GBPS, 4),
+               "note": "35 MB of KV: the step is launch- and latency-bound and the bytes fit the "
+                       "256 MB Infinity Cache, so this is not an HBM rate"}
+        if cpu:
+            rec, o = cpu_decode_baseline(w["q"], w["k_cache"], w["v_cache"], w["block_tables"],
+                                         w["context_lens"], w["scale"], 16, 8, 256, None, None, nb,
+                                         "the whole workload, fp32")
+            row["cpu_baseline"] = rec
+            row["max_abs_err_vs_cpu"] = float((out.cpu() - o).abs().max())
+        res["fp32_decode_b4"] = row
+        del q, kc, vc
 
     # FP8 decode, batch 32, over the appended pool
-    w = W.decode_fp8_b32(seed=2)
-    N, bs = w["num_blocks"], w["block_size"]
-    kp = torch.zeros(N, bs, 8, HEAD_DIM, dtype=torch.float8_e4m3fn, device=dev)
-    vp = torch.zeros_like(kp)
-    ks, vs = torch.ones(1, device=dev), torch.ones(1, device=dev)
-    A.store_kvcache_fp8(w["fill_key"].to(dev), w["fill_value"].to(dev), kp, vp, ks, vs,
-                        w["fill_slots"].to(dev), bs, "fp8_per_tensor")
-    A.store_kvcache_fp8(w["key"].to(dev), w["value"].to(dev), kp, vp, ks, vs,
-                        w["slot_mapping"].to(dev), bs, "fp8_per_tensor")
-    q = w["q"].to(dev)
-    bt, ctx = w["block_tables"].to(dev), w["context_lens"].to(dev)
-    out = torch.empty_like(q)
-    fn = lambda: A._decode(q, kp, vp, bt, ctx, w["scale"], 32, 8, HEAD_DIM, ks, vs, out=out)
-    us = graph_time_us(fn)
-    nb = W.alg_bytes_decode(w["context_lens"], bs, 32, 8, kv_bytes=1)
-    row = {"workload": f"FP8 per-tensor KV (scales {float(ks):.6g} / {float(vs):.6g}), bf16 q, batch 32, "
-                       f"32 q / 8 kv heads, contexts U[256, 4096] sum {int(w['context_lens'].sum())}",
-           "us": round(us, 2), "algorithmic_bytes": nb, "GBps": round(nb / us / 1e3, 1),
-           "frac_of_8000_GBps": round(nb / us / 1e3 / PEAK_HBM_GBPS, 4)}
-    if cpu:
-        rec, o = cpu_decode_baseline(w["q"].float(), kp.cpu(), vp.cpu(), w["block_tables"],
-                                     w["context_lens"], w["scale"], 32, 8, bs, float(ks), float(vs),
-                                     nb, "the whole batch, fp32 on the dequantised cache")
-        row["cpu_baseline"] = rec
-        row["max_abs_err_vs_cpu"] = float((out.float().cpu() - o).abs().max())
-    res["fp8_decode_b32"] = row
-    del kp, vp
+    if "fp8_decode_b32" in which:
+        w = W.decode_fp8_b32(seed=2)
+        N, bs = w["num_blocks"], w["block_size"]
+        kp = torch.zeros(N, bs, 8, HEAD_DIM, dtype=torch.float8_e4m3fn, device=dev)
+        vp = torch.zeros_like(kp)
+        ks, vs = torch.ones(1, device=dev), torch.ones(1, device=dev)
+        A.store_kvcache_fp8(w["fill_key"].to(dev), w["fill_value"].to(dev), kp, vp, ks, vs,
+                            w["fill_slots"].to(dev), bs, "fp8_per_tensor")
+        A.store_kvcache_fp8(w["key"].to(dev), w["value"].to(dev), kp, vp, ks, vs,
+                            w["slot_mapping"].to(dev), bs, "fp8_per_tensor")
+        q = w["q"].to(dev)
+        bt, ctx = w["block_tables"].to(dev), w["context_lens"].to(dev)
+        out = torch.empty_like(q)
+        fn = lambda: A._decode(q, kp, vp, bt, ctx, w["scale"], 32, 8, HEAD_DIM, ks, vs, out=out)
+        us = graph_time_us(fn)
+        nb = W.alg_bytes_decode(w["context_lens"], bs, 32, 8, kv_bytes=1)
+        row = {"workload": f"FP8 per-tensor KV (scales {float(ks):.6g} / {float(vs):.6g}), bf16 q, batch 32, "
+                           f"32 q / 8 kv heads, contexts U[256, 4096] sum {int(w['context_lens'].sum())}",
+               "us": round(us, 2), "algorithmic_bytes": nb, "GBps": round(nb / us / 1e3, 1),
+               "frac_of_8000_GBps": round(nb / us / 1e3 / PEAK_HBM_GBPS, 4)}
+        if cpu:
+            rec, o = cpu_decode_baseline(w["q"].float(), kp.cpu(), vp.cpu(), w["block_tables"],
+                                         w["context_lens"], w["scale"], 32, 8, bs, float(ks), float(vs),
+                                         nb, "the whole batch, fp32 on the dequantised cache")
+            row["cpu_baseline"] = rec
+            row["max_abs_err_vs_cpu"] = float((out.float().cpu() - o).abs().max())
+        res["fp8_decode_b32"] = row
+        del kp, vp
 
     # FP8 decode at the end-to-end engine's decode shape (60 rows of 300-800
     # tokens, 16 q / 8 kv heads, 16-block tables as the engine's): the three
     # schedules, the workgroup route being the one the engine uses
-    g = torch.Generator().manual_seed(11)
-    ctx = torch.randint(300, 801, (60,), generator=g)
-    N = 60 * 4 + 16
-    bt = W.fragmented_block_tables(ctx, 256, N, g, max_blocks=16).to(dev)
-    kp = torch.empty(N, 256, 8, HEAD_DIM, dtype=torch.float8_e4m3fn, device=dev)
-    vp = torch.empty_like(kp)
-    W.fill_pool_on_device(kp, 3001)
-    W.fill_pool_on_device(vp, 3002)
-    qd = torch.randn(60, 16, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
-    sc = torch.full((1,), 0.0125, device=dev)
-    ctxd = ctx.to(dev)
-    out = torch.empty_like(qd)
-    nb = W.alg_bytes_decode(ctx, 256, 16, 8, kv_bytes=1, q_bytes=2)
-    row = {"workload": f"FP8 per-tensor KV, bf16 q, batch 60, 16 q / 8 kv heads, contexts U[300, 800] "
-                       f"sum {int(ctx.sum())}, 16-block tables (the end-to-end engine's decode shape)",
-           "algorithmic_bytes": nb}
-    for name, st in (("stream_k", 0), ("split_k_256", 256), ("workgroup", A.DECODE_WORKGROUP)):
-        fn = lambda st=st: A._decode(qd, kp, vp, bt, ctxd, 0.088, 16, 8, HEAD_DIM, sc, sc,
-                                     split_tokens=st, out=out)
-        us = graph_time_us(fn)
-        row[name] = {"us": round(us, 2), "GBps": round(nb / us / 1e3, 1),
-                     "frac_of_8000_GBps": round(nb / us / 1e3 / PEAK_HBM_GBPS, 4)}
-    res["fp8_decode_b60_engine_shape"] = row
-    del kp, vp
+    if "fp8_decode_b60_engine_shape" in which:
+        g = torch.Generator().manual_seed(11)
+        ctx = torch.randint(300, 801, (60,), generator=g)
+        N = 60 * 4 + 16
+        bt = W.fragmented_block_tables(ctx, 256, N, g, max_blocks=16).to(dev)
+        kp = torch.empty(N, 256, 8, HEAD_DIM, dtype=torch.float8_e4m3fn, device=dev)
+        vp = torch.empty_like(kp)
+        W.fill_pool_on_device(kp, 3001)
+        W.fill_pool_on_device(vp, 3002)
+        qd = torch.randn(60, 16, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+        sc = torch.full((1,), 0.0125, device=dev)
+        ctxd = ctx.to(dev)
+        out = torch.empty_like(qd)
+        nb = W.alg_bytes_decode(ctx, 256, 16, 8, kv_bytes=1, q_bytes=2)
+        row = {"workload": f"FP8 per-tensor KV, bf16 q, batch 60, 16 q / 8 kv heads, contexts U[300, 800] "
+                           f"sum {int(ctx.sum())}, 16-block tables (the end-to-end engine's decode shape)",
+               "algorithmic_bytes": nb}
+        for name, st in (("stream_k", 0), ("split_k_256", 256), ("workgroup", A.DECODE_WORKGROUP)):
+            fn = lambda st=st: A._decode(qd, kp, vp, bt, ctxd, 0.088, 16, 8, HEAD_DIM, sc, sc,
+                                         split_tokens=st, out=out)
+            us = graph_time_us(fn)
+            row[name] = {"us": round(us, 2), "GBps": round(nb / us / 1e3, 1),
+                         "frac_of_8000_GBps": round(nb / us / 1e3 / PEAK_HBM_GBPS, 4)}
+        res["fp8_decode_b60_engine_shape"] = row
+        del kp, vp
 
     # bf16 decode, the batch-256 workload
-    meta = W.decode_b256_metadata(seed=3)
-    N, bs = meta["num_blocks"], meta["block_size"]
-    pools = []
-    for l in range(4):
-        kc = torch.empty(N, bs, 8, HEAD_DIM, dtype=torch.bfloat16, device=dev)
-        vc = torch.empty_like(kc)
-        W.fill_pool_on_device(kc, 2000 + 2 * l)
-        W.fill_pool_on_device(vc, 2001 + 2 * l)
-        pools.append((kc, vc))
-    g = torch.Generator().manual_seed(3)
-    q = torch.randn(256, 32, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
-    bt, ctx = meta["block_tables"].to(dev), meta["context_lens"].to(dev)
-    out = torch.empty_like(q)
-    sm = 1.0 / math.sqrt(HEAD_DIM)
+    if "bf16_decode_b256" in which:
+        meta = W.decode_b256_metadata(seed=3)
+        N, bs = meta["num_blocks"], meta["block_size"]
+        pools = []
+        for l in range(4):
+            kc = torch.empty(N, bs, 8, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+            vc = torch.empty_like(kc)
+            W.fill_pool_on_device(kc, 2000 + 2 * l)
+            W.fill_pool_on_device(vc, 2001 + 2 * l)
+            pools.append((kc, vc))
+        g = torch.Generator().manual_seed(3)
+        q = torch.randn(256, 32, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+        bt, ctx = meta["block_tables"].to(dev), meta["context_lens"].to(dev)
+        out = torch.empty_like(q)
+        sm = 1.0 / math.sqrt(HEAD_DIM)
 
-    def step(i):
-        kc, vc = pools[i % len(pools)]
-        A._decode(q, kc, vc, bt, ctx, sm, 32, 8, HEAD_DIM, out=out)
+        def step(i):
+            kc, vc = pools[i % len(pools)]
+            A._decode(q, kc, vc, bt, ctx, sm, 32, 8, HEAD_DIM, out=out)
 
-    ms, rec_settle = time_launches(step, 40, 5, stream, settle_first=True)
-    nb = W.alg_bytes_decode(meta["context_lens"], bs, 32, 8, kv_bytes=2)
-    row = {"workload": "the batch-256 decode workload (32 q / 8 kv heads, contexts log-U[512, 8192]) "
-                       "with bf16 KV, 4 rotating layer pools (16 GiB)",
-           "us": round(ms * 1e3, 2), "algorithmic_bytes": nb, "GBps": round(nb / ms / 1e6, 1),
-           "frac_of_8000_GBps": round(nb / ms / 1e6 / PEAK_HBM_GBPS, 4), "settle": rec_settle}
-    if cpu:
-        step(0)
-        torch.cuda.synchronize()
-        kc, vc = pools[0]
-        n = 32
-        used = sorted({int(x) for x in meta["block_tables"][:n].flatten() if x >= 0})
-        remap = {p: i for i, p in enumerate(used)}
-        idx = torch.tensor(used, device=dev)
-        bt_c = meta["block_tables"][:n].clone()
-        bt_c.apply_(lambda x: remap[x] if x >= 0 else -1)
-        nbs = W.alg_bytes_decode(meta["context_lens"][:n], bs, 32, 8, kv_bytes=2)
-        rec, o = cpu_decode_baseline(q[:n].float().cpu(), kc.index_select(0, idx).cpu(),
-                                     vc.index_select(0, idx).cpu(), bt_c, meta["context_lens"][:n],
-                                     sm, 32, 8, bs, None, None, nbs,
-                                     f"first {n} of 256 sequences, fp32 on the upcast bf16 cache")
-        row["cpu_baseline"] = rec
-        row["max_abs_err_vs_cpu"] = float((out[:n].float().cpu() - o).abs().max())
-    res["bf16_decode_b256"] = row
-    del pools
+        ms, rec_settle = time_launches(step, 40, 5, stream, settle_first=True)
+        nb = W.alg_bytes_decode(meta["context_lens"], bs, 32, 8, kv_bytes=2)
+        row = {"workload": "the batch-256 decode workload (32 q / 8 kv heads, contexts log-U[512, 8192]) "
+                           "with bf16 KV, 4 rotating layer pools (16 GiB)",
+               "us": round(ms * 1e3, 2), "algorithmic_bytes": nb, "GBps": round(nb / ms / 1e6, 1),
+               "frac_of_8000_GBps": round(nb / ms / 1e6 / PEAK_HBM_GBPS, 4), "settle": rec_settle}
+        if cpu:
+            step(0)
+            torch.cuda.synchronize()
+            kc, vc = pools[0]
+            n = 32
+            used = sorted({int(x) for x in meta["block_tables"][:n].flatten() if x >= 0})
+            remap = {p: i for i, p in enumerate(used)}
+            idx = torch.tensor(used, device=dev)
+            bt_c = meta["block_tables"][:n].clone()
+            bt_c.apply_(lambda x: remap[x] if x >= 0 else -1)
+            nbs = W.alg_bytes_decode(meta["context_lens"][:n], bs, 32, 8, kv_bytes=2)
+            rec, o = cpu_decode_baseline(q[:n].float().cpu(), kc.index_select(0, idx).cpu(),
+                                         vc.index_select(0, idx).cpu(), bt_c, meta["context_lens"][:n],
+                                         sm, 32, 8, bs, None, None, nbs,
+                                         f"first {n} of 256 sequences, fp32 on the upcast bf16 cache")
+            row["cpu_baseline"] = rec
+            row["max_abs_err_vs_cpu"] = float((out[:n].float().cpu() - o).abs().max())
+        res["bf16_decode_b256"] = row
+        del pools
     return res
 
 
@@ -1245,7 +1259,8 @@ def main() -> int:
         # caches full of dirty lines (fp32 batch 4: 21 µs alone, 25-29 µs
         # right after the append lines)
         if "configs" in wanted:
-            extra["decode_configs"] = configs_extra(dev, stream, cpu=args.cpu_seqs > 0)
+            extra["decode_configs"] = configs_extra(dev, stream, cpu=args.cpu_seqs > 0,
+                                                    which=args.decode_config_set)
         # KV append + FP8 quantisation: 4096 tokens (5% padding) and 65536 tokens
         for T in ((4096, 65536) if "append" in wanted else ()):
             w = W.append_fp8(seed=2, num_tokens=T) if T == 4096 else None
