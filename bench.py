@@ -45,6 +45,7 @@ KV_DESC = {"fp8": "per-tensor e4m3fn", "bf16": "bf16",
            "int8_token": "int8 codes, fp32 scale per token and kv head"}
 
 
+ROUTE_NAMES = {0: "stream-K", 1: "split-K", 2: "workgroup"}
 DECODE_CONFIGS = ("fp32_decode_b4", "fp8_decode_b32", "fp8_decode_b60_engine_shape", "bf16_decode_b256")
 EXTRAS = ("configs", "e2e", "append", "prefill", "latency", "producer", "mixed", "copy", "gather")
 
@@ -635,11 +636,18 @@ def configs_extra(dev, stream, cpu: bool = True, which=DECODE_CONFIGS) -> dict:
     fp32 decode at batch 4 (16 q / 8 kv heads, pool of 64 blocks, contexts
     U[64, 2048]); FP8 decode at batch 32 (32 q / 8 kv heads) over the pool the
     4096-token FP8 append workload leaves (every slot filled first, then the
-    append); the batch-256 decode workload with a bf16 cache."""
+    append); the end-to-end engine's decode shape under the library's choice
+    and each schedule; the batch-256 decode workload with a bf16 cache.
+    Each line runs the library's choice of schedule (split_tokens 0) and
+    names it.  `which` selects a subset (names as in DECODE_CONFIGS)."""
     import torch
 
+    import mkv
     from mkv import attention as A
     from mkv import workloads as W
+
+    def route(B, Hq, Hkv, mb, bs, kv_dtype):
+        return ROUTE_NAMES[mkv._lib.query("mkv_paged_decode_route", B, Hq, Hkv, mb, bs, HEAD_DIM, kv_dtype, 0, 0)]
 
     res = {}
     # fp32 decode, batch 4
@@ -655,7 +663,8 @@ def configs_extra(dev, stream, cpu: bool = True, which=DECODE_CONFIGS) -> dict:
                "us": round(us, 2), "algorithmic_bytes": nb, "GBps": round(nb / us / 1e3, 1),
                "frac_of_8000_GBps": round(nb / us / 1e3 / PEAK_HBM_GBPS, 4),
                "note": "35 MB of KV: the step is launch- and latency-bound and the bytes fit the "
-                       "256 MB Infinity Cache, so this is not an HBM rate"}
+                       "256 MB Infinity Cache, so this is not an HBM rate",
+               "library_route": route(4, 16, 8, w["block_tables"].shape[1], 256, mkv._lib.DTYPE_F32)}
         if cpu:
             rec, o = cpu_decode_baseline(w["q"], w["k_cache"], w["v_cache"], w["block_tables"],
                                          w["context_lens"], w["scale"], 16, 8, 256, None, None, nb,
@@ -685,7 +694,8 @@ def configs_extra(dev, stream, cpu: bool = True, which=DECODE_CONFIGS) -> dict:
         row = {"workload": f"FP8 per-tensor KV (scales {float(ks):.6g} / {float(vs):.6g}), bf16 q, batch 32, "
                            f"32 q / 8 kv heads, contexts U[256, 4096] sum {int(w['context_lens'].sum())}",
                "us": round(us, 2), "algorithmic_bytes": nb, "GBps": round(nb / us / 1e3, 1),
-               "frac_of_8000_GBps": round(nb / us / 1e3 / PEAK_HBM_GBPS, 4)}
+               "frac_of_8000_GBps": round(nb / us / 1e3 / PEAK_HBM_GBPS, 4),
+               "library_route": route(32, 32, 8, w["block_tables"].shape[1], bs, mkv._lib.DTYPE_FP8E4M3)}
         if cpu:
             rec, o = cpu_decode_baseline(w["q"].float(), kp.cpu(), vp.cpu(), w["block_tables"],
                                          w["context_lens"], w["scale"], 32, 8, bs, float(ks), float(vs),
@@ -696,13 +706,14 @@ def configs_extra(dev, stream, cpu: bool = True, which=DECODE_CONFIGS) -> dict:
         del kp, vp
 
     # FP8 decode at the end-to-end engine's decode shape (60 rows of 300-800
-    # tokens, 16 q / 8 kv heads, 16-block tables as the engine's): the three
-    # schedules, the workgroup route being the one the engine uses
+    # tokens, 16 q / 8 kv heads, 4-block tables: the engine pads each decode
+    # step's tables to its longest sequence, rounded up to a power of two):
+    # the library's choice (the workgroup route here) and each schedule
     if "fp8_decode_b60_engine_shape" in which:
         g = torch.Generator().manual_seed(11)
         ctx = torch.randint(300, 801, (60,), generator=g)
         N = 60 * 4 + 16
-        bt = W.fragmented_block_tables(ctx, 256, N, g, max_blocks=16).to(dev)
+        bt = W.fragmented_block_tables(ctx, 256, N, g, max_blocks=4).to(dev)
         kp = torch.empty(N, 256, 8, HEAD_DIM, dtype=torch.float8_e4m3fn, device=dev)
         vp = torch.empty_like(kp)
         W.fill_pool_on_device(kp, 3001)
@@ -713,9 +724,12 @@ def configs_extra(dev, stream, cpu: bool = True, which=DECODE_CONFIGS) -> dict:
         out = torch.empty_like(qd)
         nb = W.alg_bytes_decode(ctx, 256, 16, 8, kv_bytes=1, q_bytes=2)
         row = {"workload": f"FP8 per-tensor KV, bf16 q, batch 60, 16 q / 8 kv heads, contexts U[300, 800] "
-                           f"sum {int(ctx.sum())}, 16-block tables (the end-to-end engine's decode shape)",
-               "algorithmic_bytes": nb}
-        for name, st in (("stream_k", 0), ("split_k_256", 256), ("workgroup", A.DECODE_WORKGROUP)):
+                           f"sum {int(ctx.sum())}, 4-block tables (the end-to-end engine's decode shape)",
+               "algorithmic_bytes": nb,
+               "library_route": ROUTE_NAMES[mkv._lib.query("mkv_paged_decode_route", 60, 16, 8, 4, 256,
+                                                           HEAD_DIM, mkv._lib.DTYPE_FP8E4M3, 0, 0)]}
+        for name, st in (("library", 0), ("stream_k", A.DECODE_STREAM), ("split_k_256", 256),
+                         ("workgroup", A.DECODE_WORKGROUP)):
             fn = lambda st=st: A._decode(qd, kp, vp, bt, ctxd, 0.088, 16, 8, HEAD_DIM, sc, sc,
                                          split_tokens=st, out=out)
             us = graph_time_us(fn)
@@ -793,12 +807,10 @@ def e2e_extra(dev, baselines: bool = True) -> dict:
     prompts = [torch.randint(0, 151936, (L,), generator=g).tolist() for L in lens]
     cfg = E.ModelConfig()
     model = E.Qwen3Model(cfg, dev, seed=5, block_size=256)
-    # decode by the workgroup route (one workgroup per sequence and KV head,
-    # waves merged in LDS): with 60 rows of 300-800 tokens it beats the
-    # stream-K default and 256-token split-K (17.4 / 24.1 / 22.8 us per call)
+    # decode schedule: the library's choice (the workgroup route for these 60
+    # rows: one workgroup per sequence and KV head, waves merged in LDS)
     eng = E.Engine(model, num_blocks=512, max_num_seqs=64, max_num_batched_tokens=1024,
-                   kv_cache_dtype="fp8_per_tensor", max_model_len=4096, seed=0,
-                   decode_split_tokens=E.DECODE_WORKGROUP)
+                   kv_cache_dtype="fp8_per_tensor", max_model_len=4096, seed=0)
     eng.generate(prompts, max_tokens=256)  # warm-up: captures the decode graphs
     eng.stats.clear()
     torch.cuda.synchronize()
@@ -816,8 +828,7 @@ def e2e_extra(dev, baselines: bool = True) -> dict:
         return res
     # the same engine with eager decode steps (no captured graphs)
     eager = E.Engine(model, num_blocks=512, max_num_seqs=64, max_num_batched_tokens=1024,
-                     kv_cache_dtype="fp8_per_tensor", max_model_len=4096, seed=0, use_graphs=False,
-                     decode_split_tokens=E.DECODE_WORKGROUP)
+                     kv_cache_dtype="fp8_per_tensor", max_model_len=4096, seed=0, use_graphs=False)
     eager.generate(prompts[:4], max_tokens=4)  # warm-up
     eager.stats.clear()
     torch.cuda.synchronize()

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MKV_ABI_VERSION 3
+#define MKV_ABI_VERSION 4
 
 /* Element dtypes (torch.float32, torch.bfloat16, torch.float16,
  * torch.float8_e4m3fn, torch.int8).  FP8 is OCP e4m3fn: max 448, no
@@ -205,23 +205,38 @@ int mkv_fp8_calibrate_per_tensor(const void* key, int64_t key_row_stride,
  * q, out: (batch, num_heads, head_dim), rows contiguous, row stride
  * q_batch_stride / out_batch_stride elements; out has q's dtype.
  * block_tables: int32 (batch, bt_stride) with max_blocks usable columns.
- * head_dim == 128; num_heads / num_kv_heads in 1..16; block_size a power of
- * two >= 16.  q_dtype is F32, BF16 or F16 with any kv_dtype.
+ * head_dim 128, num_heads / num_kv_heads in 1..16; or head_dim 64 (the
+ * Llama-3.2-1B shape, main_llama32.py:29-34) with an even num_kv_heads and
+ * num_heads / num_kv_heads in 1..8.  block_size a power of two >= 16.
+ * q_dtype is F32, BF16 or F16 with any kv_dtype.
  *
- * split_tokens: 0 = the library's schedule (stream-K over 32-token tiles on
- * a persistent grid, groups of num_kv_heads waves sharing each tile range,
- * for BF16/F16/FP8/INT8 KV and batch <= 8192, else split-K with a
- * library-chosen split); > 0 = split-K with that many tokens per work item
- * (a multiple of 32); MKV_DECODE_WORKGROUP = one workgroup per (sequence,
- * KV head) whose waves split the sequence and merge in LDS (every KV
- * format; no workspace, one launch; MKV_ERR_BAD_SHAPE when a wave's share of
- * the widest block table would span more than 62 blocks).
+ * split_tokens selects the schedule:
+ *   0 = the library's choice from (batch, num_kv_heads, max_blocks,
+ *       block_size, kv_dtype): the workgroup route when the (sequence, KV
+ *       head) items fill the device's CUs and each still gets at least 4
+ *       waves, else stream-K (BF16/F16/FP8/INT8 KV, batch <= 8192), else
+ *       split-K with a library-chosen split (mkv_paged_decode_route reports
+ *       the choice);
+ *   MKV_DECODE_STREAM = stream-K over 32-token tiles on a persistent grid,
+ *       groups of num_kv_heads waves sharing each tile range, and a merge
+ *       kernel (split-K where stream-K does not apply);
+ *   MKV_DECODE_WORKGROUP = one workgroup per (sequence, KV head) whose waves
+ *       split the sequence and merge in LDS (every KV format; no workspace,
+ *       one launch);
+ *   > 0 = split-K with that many tokens per work item (a multiple of 32).
+ * Every route reads any block-table width (block-table entries are looked
+ * up tile by tile).
  * workspace: >= mkv_paged_decode_workspace_size(...)
  * bytes with the same arguments (the size of the route those arguments
  * select: stream-K partial slots for the persistent grid, or split-K
- * partials); calls that share a workspace must be ordered on one stream.
+ * partials, or 0); calls that share a workspace must be ordered on one
+ * stream.
  */
 #define MKV_DECODE_WORKGROUP (-1)
+#define MKV_DECODE_STREAM (-2)
+#define MKV_DECODE_ROUTE_STREAM 0
+#define MKV_DECODE_ROUTE_SPLIT 1
+#define MKV_DECODE_ROUTE_WORKGROUP 2
 size_t mkv_paged_decode_workspace_size(int batch, int num_heads,
                                        int num_kv_heads, int max_blocks,
                                        int block_size, int head_dim,
@@ -231,6 +246,16 @@ size_t mkv_paged_decode_workspace_size(int batch, int num_heads,
  * (split_tokens itself when it is > 0). */
 int mkv_paged_decode_split_tokens(int batch, int num_kv_heads, int max_blocks,
                                   int block_size, int split_tokens);
+
+/* The schedule mkv_paged_decode takes for these arguments on a device of
+ * num_cus compute units (num_cus <= 0: the current device): one of
+ * MKV_DECODE_ROUTE_STREAM / _SPLIT / _WORKGROUP, or a negative status for
+ * an unsupported shape.  The reference has one decode entry and no schedule
+ * (attention.py:895-950); this reports the library's choice for split_tokens
+ * 0 and the route an explicit value selects. */
+int mkv_paged_decode_route(int batch, int num_heads, int num_kv_heads,
+                           int max_blocks, int block_size, int head_dim,
+                           int kv_dtype, int split_tokens, int num_cus);
 int mkv_paged_decode(void* out, int64_t out_batch_stride,
                      const void* q, int64_t q_batch_stride, int q_dtype,
                      const void* k_cache, const void* v_cache, int kv_dtype,
@@ -254,9 +279,12 @@ int mkv_paged_decode(void* out, int64_t out_batch_stride,
  * workspace_bytes: the partials live in a static per-device scratch array of
  * MKV_NOALLOC_SCRATCH_BYTES (32 MiB) that the library holds on each GPU it
  * runs on until the process ends.  The call allocates
- * and frees nothing.  A call whose route needs more than that (see
- * mkv_paged_decode_workspace_size) returns MKV_ERR_SCRATCH_LIMIT before any
- * launch.  Every call on one GPU shares that GPU's array: calls that overlap
+ * and frees nothing.  When the route that mkv_paged_decode would take needs
+ * more than that (see mkv_paged_decode_workspace_size; e.g. stream-K slots
+ * for 16 query heads per KV head on 256 CUs), the library's choice
+ * (split_tokens 0) takes the workgroup route instead, which needs no
+ * workspace and agrees within rounding rather than bit for bit; an explicit
+ * route returns MKV_ERR_SCRATCH_LIMIT before any launch.  Every call on one GPU shares that GPU's array: calls that overlap
  * on one GPU (different streams, or different host threads without
  * ordering) race and must be ordered by the caller.  The first call on a
  * device resolves the array's address on that device (make it outside graph

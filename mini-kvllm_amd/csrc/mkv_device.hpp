@@ -373,4 +373,51 @@ struct PagedIndex {
   }
 };
 
+// ---------------------------------------------------------------------------
+// Head pairing (head_dim 64).  The attention kernels work on 128-element
+// head rows.  KV heads 2v and 2v+1 of a head_dim-64 cache are adjacent
+// 64-element segments of a token row, so the kernels read them as one
+// 128-element segment, KV head v of the kernel, whose group holds the 2G
+// query heads 2vG .. 2vG+2G-1 (those of KV head 2v, then those of 2v+1).
+// Query head j of that group takes dims 64*hi(j) .. +63 of the segment,
+// hi(j) = (j >= G): its q is zero on the other half, so its scores are
+// exact, and only its own half of the output is stored.  Pool, block tables
+// and every K/V tile load are those of a head_dim-128 pool with Hkv/2 KV
+// heads; q, the output and the per-token-head scales are addressed with the
+// caller's shape.
+// ---------------------------------------------------------------------------
+template <bool PAIR>
+constexpr int kQDim = PAIR ? 64 : 128;
+
+// q slice of lane (c, kg): dims 32kg .. 32kg+31 of head c of the kernel's
+// group.  Returns false for a lane that holds zeros (a padding head, or the
+// other half of a paired head); dim0 = the slice's first element in q's head
+// row.
+template <bool PAIR>
+MKV_DEV bool q_slice(int group, int c, int kg, int& dim0) {
+  if constexpr (PAIR) {
+    const bool hi = c >= (group >> 1);
+    dim0 = 32 * (kg & 1);
+    return c < group && (kg >> 1) == (hi ? 1 : 0);
+  } else {
+    dim0 = 32 * kg;
+    return c < group;
+  }
+}
+
+// Output columns 8c .. 8c+7 of head h of the kernel's group: whether they
+// belong to the head's own output, and their first element in its output
+// row.
+template <bool PAIR>
+MKV_DEV bool out_cols(int group, int h, int c, int& col0) {
+  if constexpr (PAIR) {
+    const bool hi = h >= (group >> 1);
+    col0 = 8 * c - (hi ? 64 : 0);
+    return (c >= 8) == hi;
+  } else {
+    col0 = 8 * c;
+    return true;
+  }
+}
+
 }  // namespace mkv

@@ -74,6 +74,8 @@ struct DecodeArgs {
   int first_pct;    // percent of the split that the first dispatch round's groups take
   int num_waves;    // persistent waves in the grid
   int first_waves;  // waves of the first dispatch round (== num_waves: even split)
+  int scale_heads;  // KV heads of the per-token-head scale tensors (the caller's Hkv)
+  int pair;         // head_dim 64: KV heads read in pairs (kQDim in mkv_device.hpp)
 };
 
 MKV_DEV float wave_max(float v) {
@@ -139,6 +141,7 @@ MKV_DEV int64_t wave_work_index() {
 // Final normalisation / partial write for one wave.  Lane (kg, c) holds
 // O[head 4kg + r][dim 8c + mm] in acc[mm][r]; m_col / l_col hold the running
 // max and the (lane-group summed) denominator of head c.
+template <bool PAIR>
 MKV_DEV void finish_item(const DecodeArgs& a, const WorkItem& it, f32x4 (&acc)[8], float m_col,
                          float l_col, float v_mul) {
   const int lane = threadIdx.x & 63;
@@ -155,7 +158,9 @@ MKV_DEV void finish_item(const DecodeArgs& a, const WorkItem& it, f32x4 (&acc)[8
       const float inv = lh > 0.0f ? v_mul / lh : 0.0f;
 #pragma unroll
       for (int mm = 0; mm < 8; ++mm) x[mm] = acc[mm][r] * inv;
-      store_out8(a.out, a.q_dtype, (int64_t)it.b * a.out_stride + (int64_t)hq * kHeadDim + 8 * c, x);
+      int col0;
+      if (out_cols<PAIR>(a.group, h, c, col0))
+        store_out8(a.out, a.q_dtype, (int64_t)it.b * a.out_stride + (int64_t)hq * kQDim<PAIR> + col0, x);
     } else {
       const int64_t slot = ((int64_t)it.b * a.num_heads + hq) * a.max_splits + it.split;
       float* p = a.ws_acc + slot * kHeadDim + 8 * c;
@@ -244,8 +249,6 @@ MKV_DEV __amdgpu_buffer_rsrc_t rows_rsrc(const char* pool, int64_t phys, int64_t
 
 // Per work item constants of the tile loads.
 struct ItemLoad {
-  int my_phys;   // lane i: physical block of logical block blk0 + i (-1 if absent)
-  int blk0;      // first logical block of the split
   int k_voff;    // lane byte offset of its K row chunk inside a 16-token group
   int v_voff;    // lane byte offset of its V row chunk (token 4kg, dims 8c..)
   int row_bytes; // bytes per token row (all KV heads)
@@ -259,15 +262,32 @@ MKV_DEV ItemLoad item_load_setup(const DecodeArgs& a, const WorkItem& it) {
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
   ItemLoad L;
-  L.blk0 = it.t_begin >> a.idx.bs_log2;
-  const int nblk = it.t_end > it.t_begin ? ((it.t_end - 1) >> a.idx.bs_log2) - L.blk0 + 1 : 0;
-  L.my_phys = lane < nblk ? (int)a.idx.physical_block(it.b, L.blk0 + lane) : -1;
   L.row_bytes = (int)(a.idx.row_elems * kEb);
   L.blk_bytes = (int64_t)L.row_bytes << a.idx.bs_log2;
   L.head_bytes = (int64_t)it.kvh * kHeadDim * kEb;
   L.k_voff = c * L.row_bytes + 32 * kg * kEb;
   L.v_voff = 4 * kg * L.row_bytes + 8 * c * kEb;
   return L;
+}
+
+struct PhysPair {
+  int64_t p[2];
+};
+
+// Block-table entries of the 16-token halves at t0 and t0 + 16 of sequence
+// b (-1 at or past t_end, or absent).  Wave-uniform lookups through the
+// constant address space, i.e. scalar loads counted on lgkmcnt: the split-K
+// and workgroup loops issue them one tile ahead of the K/V loads that use
+// them, so no lookup waits for the tiles in flight, and a range may span any
+// number of blocks.
+MKV_DEV int64_t item_phys1(const DecodeArgs& a, int b, int tok, int t_end) {
+  return tok < t_end ? a.idx.physical_block(b, tok >> a.idx.bs_log2) : -1;
+}
+MKV_DEV PhysPair item_phys(const DecodeArgs& a, int b, int t0, int t_end) {
+  PhysPair ph;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) ph.p[h] = item_phys1(a, b, t0 + 16 * h, t_end);
+  return ph;
 }
 
 template <int KV_DT>
@@ -279,6 +299,7 @@ struct Tile16 {
   u32x4 k[2][kKVec];
   VT v[8];
   float sc;    // per-token-head formats: one K or V scale (load_tile_scales)
+  float sc2;   // with head pairing: the same scale of the pair's second KV head
   bool ok[2];  // sub-tile block present
 };
 
@@ -286,25 +307,28 @@ struct Tile16 {
 // entries ph0 / ph1 of its two 16-token halves).  Lane (c, kg) loads the K
 // (c < 8) or V (c >= 8) scale of token t0 + 16m + 4kg + r with m = (c >> 2) & 1,
 // r = c & 3: row kg of the wave then holds exactly the 16 scales of the 8
-// tokens whose scores it computes.  An absent block reads slot 0 of block 0
-// (a valid address; the value is masked where it is used).  The load is
-// issued unconditionally, like the K/V loads.
+// tokens whose scores it computes.  With head pairing the lane also loads
+// the scale of the pair's second KV head (the next entry).  An absent block
+// reads slot 0 of block 0 (a valid address; the value is masked where it is
+// used).  The loads are issued unconditionally, like the K/V loads.
 typedef const float __attribute__((address_space(1))) global_f32;
-template <int KV_DT>
+template <int KV_DT, bool PAIR>
 MKV_DEV void load_tile_scales(const DecodeArgs& a, int64_t ph0, int64_t ph1, int t0, int kvh,
                               Tile16<KV_DT>& T) {
   if constexpr (kPerTokenScale<KV_DT>) {
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, kg = lane >> 4;
     const int bs_mask = (1 << a.idx.bs_log2) - 1;
+    const int sh = a.scale_heads;
+    const int kvr = PAIR ? 2 * kvh : kvh;  // the caller's KV head
     // scale index of the first token of each half (the host checks that the
     // scale tensor has fewer than 2^31 entries)
-    const int s0 = (int)((((ph0 < 0 ? 0 : ph0) << a.idx.bs_log2) + (t0 & bs_mask)) * a.num_kv_heads) + kvh;
-    const int s1 =
-        (int)((((ph1 < 0 ? 0 : ph1) << a.idx.bs_log2) + ((t0 + 16) & bs_mask)) * a.num_kv_heads) + kvh;
-    const int idx = ((c & 4) ? s1 : s0) + (4 * kg + (c & 3)) * a.num_kv_heads;
+    const int s0 = (int)((((ph0 < 0 ? 0 : ph0) << a.idx.bs_log2) + (t0 & bs_mask)) * sh) + kvr;
+    const int s1 = (int)((((ph1 < 0 ? 0 : ph1) << a.idx.bs_log2) + ((t0 + 16) & bs_mask)) * sh) + kvr;
+    const int idx = ((c & 4) ? s1 : s0) + (4 * kg + (c & 3)) * sh;
     const float* base = c < 8 ? a.k_scale : a.v_scale;
     T.sc = *((global_f32*)(base + idx));
+    if constexpr (PAIR) T.sc2 = *((global_f32*)(base + idx + 1));
   }
 }
 
@@ -347,30 +371,23 @@ MKV_DEV void load_tile_rows(const __amdgpu_buffer_rsrc_t (&rk)[2], const __amdgp
   }
 }
 
-// Issue every load of the 32-token tile starting at t0 (wave-uniform).  Tokens
-// past the split end and absent blocks read as zeros; no branches.
-template <int KV_DT>
+// Issue every load of the 32-token tile starting at t0 (wave-uniform) with
+// its block-table entries ph (item_phys).  Tokens past the split end and
+// absent blocks read as zeros; no branches.
+template <int KV_DT, bool PAIR>
 MKV_DEV void load_tile16(const DecodeArgs& a, const WorkItem& it, const ItemLoad& L, int t0,
-                         Tile16<KV_DT>& T) {
-  constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
-  const int lane = threadIdx.x & 63;
-  const int c = lane & 15, kg = lane >> 4;
+                         const PhysPair& ph, Tile16<KV_DT>& T) {
   const int bs_mask = (1 << a.idx.bs_log2) - 1;
   __amdgpu_buffer_rsrc_t rk[2], rv[2];
-  int64_t phys[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int th = t0 + 16 * h;
-    int slot = (th >> a.idx.bs_log2) - L.blk0;
-    slot = slot > 63 ? 63 : slot;
-    phys[h] = __builtin_amdgcn_readlane(L.my_phys, slot);
-    const int64_t off = L.head_bytes + (int64_t)(th & bs_mask) * L.row_bytes;
-    rk[h] = rows_rsrc(a.k_cache, phys[h], L.blk_bytes, off);
-    rv[h] = rows_rsrc(a.v_cache, phys[h], L.blk_bytes, off);
-    T.ok[h] = phys[h] >= 0;
+    const int64_t off = L.head_bytes + (int64_t)((t0 + 16 * h) & bs_mask) * L.row_bytes;
+    rk[h] = rows_rsrc(a.k_cache, ph.p[h], L.blk_bytes, off);
+    rv[h] = rows_rsrc(a.v_cache, ph.p[h], L.blk_bytes, off);
+    T.ok[h] = ph.p[h] >= 0;
   }
   load_tile_rows<KV_DT>(rk, rv, t0, it.t_end, L.k_voff, L.v_voff, L.row_bytes, T);
-  load_tile_scales<KV_DT>(a, phys[0], phys[1], t0, it.kvh, T);
+  load_tile_scales<KV_DT, PAIR>(a, ph.p[0], ph.p[1], t0, it.kvh, T);
 }
 
 // Formats that run on the bf16 MFMA (bf16 caches and the per-token-head codes,
@@ -496,10 +513,12 @@ MKV_DEV void row_scales(float sc, float (&ks)[8], float (&vs)[8]) {
 }
 
 // One 32-token tile: S^T = K q^T, online softmax (log2 domain), O += P V.
-// t0: first token of the tile, t_end: end of the visible range.
-template <int KV_DT>
+// t0: first token of the tile, t_end: end of the visible range.  hi (head
+// pairing, per-token-head formats): this lane's head c belongs to the
+// pair's second KV head, whose scales it uses.
+template <int KV_DT, bool PAIR>
 MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const QOps<KV_DT>& qop,
-                            float score_mul, f32x4 (&acc)[8], float& m_run, float& l_run) {
+                            float score_mul, f32x4 (&acc)[8], float& m_run, float& l_run, bool hi) {
   const int lane = threadIdx.x & 63;
   const int kg = lane >> 4;
   // S^T = K q^T: lane holds scores of tokens t0 + 16m + 4kg + r for head c.
@@ -525,7 +544,18 @@ MKV_DEV void compute_tile16(const Tile16<KV_DT>& cur, int t0, int t_end, const Q
   // Per-token-head formats: K scales (lanes 0-7 of the row) and V scales
   // (lanes 8-15) of this lane's tokens 16m + 4kg + r, index 4m + r.
   float ks[8], vs[8];
-  if constexpr (kPerTokenScale<KV_DT>) row_scales(cur.sc, ks, vs);
+  if constexpr (kPerTokenScale<KV_DT>) {
+    row_scales(cur.sc, ks, vs);
+    if constexpr (PAIR) {
+      float ks2[8], vs2[8];
+      row_scales(cur.sc2, ks2, vs2);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        ks[j] = hi ? ks2[j] : ks[j];
+        vs[j] = hi ? vs2[j] : vs[j];
+      }
+    }
+  }
   float mx = kNegBig;
   bool okt[8];
 #pragma unroll
@@ -631,13 +661,14 @@ MKV_DEV float q_operands(const DecodeArgs& a, float (&qf)[32], QOps<KV_DT>& qop,
 
 // q of item (b, kvh) loaded and converted on the spot (any q dtype).  k_mul:
 // the K dequantisation scale (1 for 16-bit caches).
-template <int KV_DT>
+template <int KV_DT, bool PAIR>
 MKV_DEV float load_q_operands(const DecodeArgs& a, int b, int kvh, QOps<KV_DT>& qop, float k_mul) {
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
   float qf[32];
-  if (c < a.group) {
-    const int64_t qoff = (int64_t)b * a.q_stride + (int64_t)(kvh * a.group + c) * kHeadDim + 32 * kg;
+  int d0;
+  if (q_slice<PAIR>(a.group, c, kg, d0)) {
+    const int64_t qoff = (int64_t)b * a.q_stride + (int64_t)(kvh * a.group + c) * kQDim<PAIR> + d0;
     load_q32(a.q, a.q_dtype, qoff, qf);
   } else {
 #pragma unroll
@@ -659,14 +690,17 @@ struct QStage {
 // every pipeline step: a load issued on only some steps makes the wait-count
 // pass assume the worst at the join and wait for it, i.e. for a full memory
 // round trip, before the next tile.
+template <bool PAIR>
 MKV_DEV void load_q_stage(const DecodeArgs& a, int b, int kvh, bool need, QStage& qs) {
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
+  constexpr int kQd = kQDim<PAIR>;
   const char* base = reinterpret_cast<const char*>(a.q) +
-                     ((int64_t)b * a.q_stride + (int64_t)kvh * a.group * kHeadDim) * 2;
+                     ((int64_t)b * a.q_stride + (int64_t)kvh * a.group * kQd) * 2;
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)base, (short)0, need ? a.group * kHeadDim * 2 : 0, kRsrcFlags);
-  const uint32_t off = c < a.group ? (uint32_t)((c * kHeadDim + 32 * kg) * 2) : kOob;
+      (void*)base, (short)0, need ? a.group * kQd * 2 : 0, kRsrcFlags);
+  int d0;
+  const uint32_t off = q_slice<PAIR>(a.group, c, kg, d0) ? (uint32_t)((c * kQd + d0) * 2) : kOob;
 #pragma unroll
   for (int i = 0; i < 4; ++i) qs.w[i] = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 0);
 }
@@ -687,13 +721,14 @@ MKV_DEV float staged_q_operands(const DecodeArgs& a, const QStage& qs, QOps<KV_D
   return q_operands<KV_DT>(a, qf, qop, k_mul);
 }
 
-template <int KV_DT>
+template <int KV_DT, bool PAIR>
 MKV_DEV void split_decode(const DecodeArgs& a) {
   WorkItem it;
   if (!decode_work_item(a, wave_work_index(), it)) return;
   QOps<KV_DT> qop;
   const float k_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.k_scale) : 1.0f;
-  const float score_mul = load_q_operands<KV_DT>(a, it.b, it.kvh, qop, k_mul);
+  const float score_mul = load_q_operands<KV_DT, PAIR>(a, it.b, it.kvh, qop, k_mul);
+  const bool hi = PAIR && (threadIdx.x & 15) >= (a.group >> 1);
 
   f32x4 acc[8];
 #pragma unroll
@@ -702,21 +737,25 @@ MKV_DEV void split_decode(const DecodeArgs& a) {
 
 
   // Software pipeline over two register tiles: the loads of tile i+1 are in
-  // flight while tile i is computed.  The prefetch is unconditional (a tile
-  // past the split end reads zeros through the descriptor range check and
-  // touches no memory), so no branch splits the load stream and the waits
-  // before tile i only cover tile i's loads.
+  // flight while tile i is computed, and the block-table entries of tile i+2
+  // (scalar loads) while tile i+1's loads go out.  The prefetch is
+  // unconditional (a tile past the split end reads zeros through the
+  // descriptor range check and touches no memory), so no branch splits the
+  // load stream and the waits before tile i only cover tile i's loads.
   if (it.t_begin < it.t_end) {
     const ItemLoad L = item_load_setup<KV_DT>(a, it);
     Tile16<KV_DT> ta, tb;
-    load_tile16<KV_DT>(a, it, L, it.t_begin, ta);
+    load_tile16<KV_DT, PAIR>(a, it, L, it.t_begin, item_phys(a, it.b, it.t_begin, it.t_end), ta);
+    PhysPair ph = item_phys(a, it.b, it.t_begin + 32, it.t_end);
     for (int t0 = it.t_begin;;) {
-      load_tile16<KV_DT>(a, it, L, t0 + 32, tb);
-      compute_tile16<KV_DT>(ta, t0, it.t_end, qop, score_mul, acc, m_run, l_run);
+      load_tile16<KV_DT, PAIR>(a, it, L, t0 + 32, ph, tb);
+      ph = item_phys(a, it.b, t0 + 64, it.t_end);
+      compute_tile16<KV_DT, PAIR>(ta, t0, it.t_end, qop, score_mul, acc, m_run, l_run, hi);
       t0 += 32;
       if (t0 >= it.t_end) break;
-      load_tile16<KV_DT>(a, it, L, t0 + 32, ta);
-      compute_tile16<KV_DT>(tb, t0, it.t_end, qop, score_mul, acc, m_run, l_run);
+      load_tile16<KV_DT, PAIR>(a, it, L, t0 + 32, ph, ta);
+      ph = item_phys(a, it.b, t0 + 64, it.t_end);
+      compute_tile16<KV_DT, PAIR>(tb, t0, it.t_end, qop, score_mul, acc, m_run, l_run, hi);
       t0 += 32;
       if (t0 >= it.t_end) break;
     }
@@ -724,20 +763,20 @@ MKV_DEV void split_decode(const DecodeArgs& a) {
   float l_col = l_run + __shfl_xor(l_run, 16);
   l_col += __shfl_xor(l_col, 32);
   const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
-  finish_item(a, it, acc, m_run, l_col, v_mul);
+  finish_item<PAIR>(a, it, acc, m_run, l_col, v_mul);
 }
 
-template <int KV_DT>
+template <int KV_DT, bool PAIR>
 __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma16_kernel(DecodeArgs a) {
-  split_decode<KV_DT>(a);
+  split_decode<KV_DT, PAIR>(a);
 }
 
 // Per-token-head formats: two waves per SIMD requested explicitly (as for
 // the stream-K kernel below).
-template <int KV_DT>
+template <int KV_DT, bool PAIR>
 __global__ __launch_bounds__(kDecWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
 paged_decode_mfma16_2w_kernel(DecodeArgs a) {
-  split_decode<KV_DT>(a);
+  split_decode<KV_DT, PAIR>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -757,6 +796,7 @@ constexpr int kWgMaxWaves = 8;
 // head c), then the workgroup combines the nw partials of each (head, 8-dim
 // chunk) with the log-sum-exp rule and writes the output row.  v_mul: the
 // per-tensor V scale (1 otherwise).
+template <bool PAIR>
 MKV_DEV void wg_merge_store(const DecodeArgs& a, const WorkItem& it, const f32x4 (&acc)[8], float m_run,
                             float l_col, float v_mul) {
   extern __shared__ float wg_lds[];
@@ -784,6 +824,8 @@ MKV_DEV void wg_merge_store(const DecodeArgs& a, const WorkItem& it, const f32x4
   __syncthreads();
   for (int u = threadIdx.x; u < G * 16; u += blockDim.x) {
     const int h = u >> 4, d0 = (u & 15) * 8;
+    int col0;
+    if (!out_cols<PAIR>(G, h, u & 15, col0)) continue;  // the other half of a paired head
     float M = kNegBig;
     for (int w = 0; w < nw; ++w) M = fmaxf(M, m_l[w * G + h]);
     float lsum = 0.0f, o[8];
@@ -805,7 +847,7 @@ MKV_DEV void wg_merge_store(const DecodeArgs& a, const WorkItem& it, const f32x4
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] *= inv;
     store_out8(a.out, a.q_dtype,
-               (int64_t)it.b * a.out_stride + (int64_t)(it.kvh * G + h) * kHeadDim + d0, o);
+               (int64_t)it.b * a.out_stride + (int64_t)(it.kvh * G + h) * kQDim<PAIR> + col0, o);
   }
 }
 
@@ -830,13 +872,14 @@ MKV_DEV WorkItem wg_item(const DecodeArgs& a) {
   return it;
 }
 
-template <int KV_DT>
+template <int KV_DT, bool PAIR>
 MKV_DEV void wg_decode(const DecodeArgs& a) {
   const WorkItem it = wg_item(a);
 
   QOps<KV_DT> qop;
   const float k_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.k_scale) : 1.0f;
-  const float score_mul = load_q_operands<KV_DT>(a, it.b, it.kvh, qop, k_mul);
+  const float score_mul = load_q_operands<KV_DT, PAIR>(a, it.b, it.kvh, qop, k_mul);
+  const bool hi = PAIR && (threadIdx.x & 15) >= (a.group >> 1);
   f32x4 acc[8];
 #pragma unroll
   for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -844,14 +887,17 @@ MKV_DEV void wg_decode(const DecodeArgs& a) {
   if (it.t_begin < it.t_end) {
     const ItemLoad Ld = item_load_setup<KV_DT>(a, it);
     Tile16<KV_DT> ta, tb2;
-    load_tile16<KV_DT>(a, it, Ld, it.t_begin, ta);
+    load_tile16<KV_DT, PAIR>(a, it, Ld, it.t_begin, item_phys(a, it.b, it.t_begin, it.t_end), ta);
+    PhysPair ph = item_phys(a, it.b, it.t_begin + 32, it.t_end);
     for (int t0 = it.t_begin;;) {
-      load_tile16<KV_DT>(a, it, Ld, t0 + 32, tb2);
-      compute_tile16<KV_DT>(ta, t0, it.t_end, qop, score_mul, acc, m_run, l_run);
+      load_tile16<KV_DT, PAIR>(a, it, Ld, t0 + 32, ph, tb2);
+      ph = item_phys(a, it.b, t0 + 64, it.t_end);
+      compute_tile16<KV_DT, PAIR>(ta, t0, it.t_end, qop, score_mul, acc, m_run, l_run, hi);
       t0 += 32;
       if (t0 >= it.t_end) break;
-      load_tile16<KV_DT>(a, it, Ld, t0 + 32, ta);
-      compute_tile16<KV_DT>(tb2, t0, it.t_end, qop, score_mul, acc, m_run, l_run);
+      load_tile16<KV_DT, PAIR>(a, it, Ld, t0 + 32, ph, ta);
+      ph = item_phys(a, it.b, t0 + 64, it.t_end);
+      compute_tile16<KV_DT, PAIR>(tb2, t0, it.t_end, qop, score_mul, acc, m_run, l_run, hi);
       t0 += 32;
       if (t0 >= it.t_end) break;
     }
@@ -859,13 +905,13 @@ MKV_DEV void wg_decode(const DecodeArgs& a) {
   float l_col = l_run + __shfl_xor(l_run, 16);
   l_col += __shfl_xor(l_col, 32);
   const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
-  wg_merge_store(a, it, acc, m_run, l_col, v_mul);
+  wg_merge_store<PAIR>(a, it, acc, m_run, l_col, v_mul);
 }
 
-template <int KV_DT>
+template <int KV_DT, bool PAIR>
 __global__ __launch_bounds__(kWgMaxWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
 paged_decode_wg_kernel(DecodeArgs a) {
-  wg_decode<KV_DT>(a);
+  wg_decode<KV_DT, PAIR>(a);
 }
 
 // fp32 caches on the workgroup route: 16-token tiles on v_mfma_f32_16x16x4_f32
@@ -877,13 +923,12 @@ struct TileF32 {
   bool ok;        // block present
 };
 
-MKV_DEV void load_tile_f32(const DecodeArgs& a, const WorkItem& it, const ItemLoad& L, int t0, TileF32& T) {
+// The loads of the 16-token tile at t0 in block phys (item_phys1).
+MKV_DEV void load_tile_f32(const DecodeArgs& a, const WorkItem& it, const ItemLoad& L, int t0, int64_t phys,
+                           TileF32& T) {
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
   const int bs_mask = (1 << a.idx.bs_log2) - 1;
-  int slot = (t0 >> a.idx.bs_log2) - L.blk0;
-  slot = slot > 63 ? 63 : slot;
-  const int64_t phys = __builtin_amdgcn_readlane(L.my_phys, slot);
   const int64_t off = L.head_bytes + (int64_t)(t0 & bs_mask) * L.row_bytes;
   const __amdgpu_buffer_rsrc_t rk = rows_rsrc(a.k_cache, phys, L.blk_bytes, off);
   const __amdgpu_buffer_rsrc_t rv = rows_rsrc(a.v_cache, phys, L.blk_bytes, off);
@@ -942,42 +987,61 @@ MKV_DEV void compute_tile_f32(const TileF32& T, int t0, int t_end, const float (
   }
 }
 
-__global__ __launch_bounds__(kWgMaxWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
-paged_decode_wg_f32_kernel(DecodeArgs a) {
-  const WorkItem it = wg_item(a);
+// The fp32 tile pipeline of one wave over its range [t_begin, t_end): the
+// loads of tile i+1 in flight while tile i is computed, the block-table entry
+// of tile i+2 (a scalar load) while tile i+1's loads go out.
+MKV_DEV void f32_range(const DecodeArgs& a, const WorkItem& it, const float (&qf)[32], float score_mul,
+                       f32x4 (&acc)[8], float& m_run, float& l_run) {
+  if (it.t_begin >= it.t_end) return;
+  const ItemLoad Ld = item_load_setup<MKV_DTYPE_F32>(a, it);
+  TileF32 ta, tb;
+  load_tile_f32(a, it, Ld, it.t_begin, item_phys1(a, it.b, it.t_begin, it.t_end), ta);
+  int64_t ph = item_phys1(a, it.b, it.t_begin + 16, it.t_end);
+  for (int t0 = it.t_begin;;) {
+    load_tile_f32(a, it, Ld, t0 + 16, ph, tb);
+    ph = item_phys1(a, it.b, t0 + 32, it.t_end);
+    compute_tile_f32(ta, t0, it.t_end, qf, score_mul, acc, m_run, l_run);
+    t0 += 16;
+    if (t0 >= it.t_end) break;
+    load_tile_f32(a, it, Ld, t0 + 16, ph, ta);
+    ph = item_phys1(a, it.b, t0 + 32, it.t_end);
+    compute_tile_f32(tb, t0, it.t_end, qf, score_mul, acc, m_run, l_run);
+    t0 += 16;
+    if (t0 >= it.t_end) break;
+  }
+}
+
+// q of item (b, kvh) as fp32 for the fp32 kernels (same lane slice as the
+// 16-bit kernels).
+template <bool PAIR>
+MKV_DEV void load_q_f32(const DecodeArgs& a, int b, int kvh, float (&qf)[32]) {
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
-  float qf[32];
-  if (c < a.group) {
-    const int64_t qoff = (int64_t)it.b * a.q_stride + (int64_t)(it.kvh * a.group + c) * kHeadDim + 32 * kg;
+  int d0;
+  if (q_slice<PAIR>(a.group, c, kg, d0)) {
+    const int64_t qoff = (int64_t)b * a.q_stride + (int64_t)(kvh * a.group + c) * kQDim<PAIR> + d0;
     load_q32(a.q, a.q_dtype, qoff, qf);
   } else {
 #pragma unroll
     for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
   }
+}
+
+template <bool PAIR>
+__global__ __launch_bounds__(kWgMaxWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
+paged_decode_wg_f32_kernel(DecodeArgs a) {
+  const WorkItem it = wg_item(a);
+  float qf[32];
+  load_q_f32<PAIR>(a, it.b, it.kvh, qf);
   const float score_mul = a.sm_scale * kLog2e;
   f32x4 acc[8];
 #pragma unroll
   for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegBig, l_run = 0.0f;
-  if (it.t_begin < it.t_end) {
-    const ItemLoad Ld = item_load_setup<MKV_DTYPE_F32>(a, it);
-    TileF32 ta, tb;
-    load_tile_f32(a, it, Ld, it.t_begin, ta);
-    for (int t0 = it.t_begin;;) {
-      load_tile_f32(a, it, Ld, t0 + 16, tb);
-      compute_tile_f32(ta, t0, it.t_end, qf, score_mul, acc, m_run, l_run);
-      t0 += 16;
-      if (t0 >= it.t_end) break;
-      load_tile_f32(a, it, Ld, t0 + 16, ta);
-      compute_tile_f32(tb, t0, it.t_end, qf, score_mul, acc, m_run, l_run);
-      t0 += 16;
-      if (t0 >= it.t_end) break;
-    }
-  }
+  f32_range(a, it, qf, score_mul, acc, m_run, l_run);
   float l_col = l_run + __shfl_xor(l_run, 16);
   l_col += __shfl_xor(l_col, 32);
-  wg_merge_store(a, it, acc, m_run, l_col, 1.0f);
+  wg_merge_store<PAIR>(a, it, acc, m_run, l_col, 1.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -1062,10 +1126,6 @@ MKV_DEV void cursor_next(Cursor& c, const int* pre, const int* lens, int B) {
   }
 }
 
-struct PhysPair {
-  int64_t p[2];
-};
-
 // Block-table entries of the two 16-token halves of tile c (scalar loads).
 MKV_DEV PhysPair tile_phys(const DecodeArgs& a, const Cursor& c) {
   PhysPair ph;
@@ -1078,7 +1138,7 @@ MKV_DEV PhysPair tile_phys(const DecodeArgs& a, const Cursor& c) {
 }
 
 // Issue the K/V loads of tile c (same lane mapping as load_tile16).
-template <int KV_DT>
+template <int KV_DT, bool PAIR>
 MKV_DEV void load_tile_sk(const DecodeArgs& a, const Cursor& c, const PhysPair& ph, int row_bytes,
                           int64_t blk_bytes, int k_voff, int v_voff, Tile16<KV_DT>& T) {
   constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
@@ -1096,11 +1156,12 @@ MKV_DEV void load_tile_sk(const DecodeArgs& a, const Cursor& c, const PhysPair& 
     T.ok[h] = ph.p[h] >= 0;
   }
   load_tile_rows<KV_DT>(rk, rv, t0, c.L, k_voff, v_voff, row_bytes, T);
-  load_tile_scales<KV_DT>(a, ph.p[0], ph.p[1], t0, c.kvh, T);
+  load_tile_scales<KV_DT, PAIR>(a, ph.p[0], ph.p[1], t0, c.kvh, T);
 }
 
 // Write the finished item of cursor c: the normalised output if the whole item
 // ran in this wave, else a partial in slot (wave, k).
+template <bool PAIR>
 MKV_DEV void finish_sk(const DecodeArgs& a, const Cursor& c, bool whole, int w, int k,
                        f32x4 (&acc)[8], float m_col, float l_col, float v_mul) {
   const int lane = threadIdx.x & 63;
@@ -1117,7 +1178,9 @@ MKV_DEV void finish_sk(const DecodeArgs& a, const Cursor& c, bool whole, int w, 
 #pragma unroll
       for (int mm = 0; mm < 8; ++mm) x[mm] = acc[mm][r] * inv;
       const int hq = c.kvh * a.group + h;
-      store_out8(a.out, a.q_dtype, (int64_t)c.b * a.out_stride + (int64_t)hq * kHeadDim + 8 * cc, x);
+      int col0;
+      if (out_cols<PAIR>(a.group, h, cc, col0))
+        store_out8(a.out, a.q_dtype, (int64_t)c.b * a.out_stride + (int64_t)hq * kQDim<PAIR> + col0, x);
     } else {
       const int64_t slot = ((int64_t)w * 2 + k) * a.group + h;
       float* p = a.ws_acc + slot * kHeadDim + 8 * cc;
@@ -1159,12 +1222,13 @@ MKV_DEV void finish_none(FinishStores& f) {
 
 // Store descriptors of an item's finish: its output row (whole) or its
 // partial slot k of wave w (acc, then (m, l)).  All inputs wave-uniform.
+template <bool PAIR>
 MKV_DEV void finish_rsrc(const DecodeArgs& a, bool whole, int b, int kvh, int w, int k, FinishStores& f) {
   if (whole) {
     const int ob = a.q_dtype == MKV_DTYPE_F32 ? 4 : 2;
     const char* base = reinterpret_cast<const char*>(a.out) +
-                       ((int64_t)b * a.out_stride + (int64_t)kvh * a.group * kHeadDim) * ob;
-    f.ra = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, a.group * kHeadDim * ob, kRsrcFlags);
+                       ((int64_t)b * a.out_stride + (int64_t)kvh * a.group * kQDim<PAIR>) * ob;
+    f.ra = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, a.group * kQDim<PAIR> * ob, kRsrcFlags);
     f.rc = f.ra;
   } else {
     const int64_t slot0 = ((int64_t)w * 2 + k) * a.group;
@@ -1175,6 +1239,7 @@ MKV_DEV void finish_rsrc(const DecodeArgs& a, bool whole, int b, int kvh, int w,
   }
 }
 
+template <bool PAIR>
 MKV_DEV void finish_small_group(const DecodeArgs& a, const Cursor& c, bool whole, int w, int k,
                                 const f32x4 (&acc)[8], float m_col, float l_col, float v_mul,
                                 FinishStores& f) {
@@ -1195,16 +1260,18 @@ MKV_DEV void finish_small_group(const DecodeArgs& a, const Cursor& c, bool whole
 #pragma unroll
     for (int mm = 0; mm < 8; ++mm) x[mm] *= inv;
     const int ob = a.q_dtype == MKV_DTYPE_F32 ? 4 : 2;
-    finish_rsrc(a, true, c.b, c.kvh, w, k, f);
-    const uint32_t off = (uint32_t)((h * kHeadDim + 8 * cc) * ob);
+    finish_rsrc<PAIR>(a, true, c.b, c.kvh, w, k, f);
+    int col0;
+    const bool own = out_cols<PAIR>(a.group, h, cc, col0);
+    const uint32_t off = (uint32_t)((h * kQDim<PAIR> + col0) * ob);
     if (a.q_dtype == MKV_DTYPE_F32) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         f.da[j] = __float_as_uint(x[j]);
         f.db[j] = __float_as_uint(x[4 + j]);
       }
-      f.oa = valid ? off : kOob;
-      f.ob = valid ? off + 16 : kOob;
+      f.oa = valid && own ? off : kOob;
+      f.ob = valid && own ? off + 16 : kOob;
     } else {
       const bool bf = a.q_dtype == MKV_DTYPE_BF16;
 #pragma unroll
@@ -1213,12 +1280,12 @@ MKV_DEV void finish_small_group(const DecodeArgs& a, const Cursor& c, bool whole
         const uint32_t hi = bf ? f32_to_bf16_bits(x[2 * j + 1]) : f32_to_f16_bits(x[2 * j + 1]);
         f.da[j] = lo | (hi << 16);
       }
-      f.oa = valid ? off : kOob;
+      f.oa = valid && own ? off : kOob;
       f.ob = kOob;
     }
     f.oc = kOob;
   } else {
-    finish_rsrc(a, false, c.b, c.kvh, w, k, f);
+    finish_rsrc<PAIR>(a, false, c.b, c.kvh, w, k, f);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       f.da[j] = __float_as_uint(x[j]);
@@ -1411,7 +1478,7 @@ MKV_DEV void publish_merge_meta(const DecodeArgs& a, const StreamSplit& sp, cons
   for (int i = threadIdx.x; i <= a.batch; i += blockDim.x) a.sk_meta[i] = pre[i];
 }
 
-template <int KV_DT, bool kSmallGroup>
+template <int KV_DT, bool kSmallGroup, bool PAIR>
 MKV_DEV void stream_decode(const DecodeArgs& a) {
   constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
   extern __shared__ int sk_lds[];
@@ -1443,6 +1510,7 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
   const int v_voff = 4 * kg * row_bytes + 8 * c * kEb;
   const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
   const float k_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.k_scale) : 1.0f;
+  const bool hi = PAIR && c >= (a.group >> 1);
 
   Cursor cc = cursor_at(pre, lens, a.batch, kvh, g0);  // tile being computed
   Cursor lc = cc;                                                  // next tile to load
@@ -1466,8 +1534,8 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
   QStage qs;
   const bool q16 = a.q_dtype != MKV_DTYPE_F32;
   ph_next = tile_phys(a, lc);
-  load_tile_sk<KV_DT>(a, lc, ph_next, row_bytes, blk_bytes, k_voff, v_voff, t0b);
-  load_q_stage(a, lc.b, lc.kvh, true, qs);
+  load_tile_sk<KV_DT, PAIR>(a, lc, ph_next, row_bytes, blk_bytes, k_voff, v_voff, t0b);
+  load_q_stage<PAIR>(a, lc.b, lc.kvh, true, qs);
   advance_load();
 
   QOps<KV_DT> qop;
@@ -1478,10 +1546,10 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
 
   // One pipeline step: prefetch tile g+1 into `nxt`, compute tile g in `cur`.
   auto step = [&](Tile16<KV_DT>& cur, Tile16<KV_DT>& nxt, int64_t g) {
-    load_tile_sk<KV_DT>(a, lc, ph_next, row_bytes, blk_bytes, k_voff, v_voff, nxt);
+    load_tile_sk<KV_DT, PAIR>(a, lc, ph_next, row_bytes, blk_bytes, k_voff, v_voff, nxt);
     if (cc.t == 0 || g == g0) {  // a new item starts: its q, fresh softmax state
       score_mul = q16 ? staged_q_operands<KV_DT>(a, qs, qop, k_mul)
-                      : load_q_operands<KV_DT>(a, cc.b, cc.kvh, qop, k_mul);
+                      : load_q_operands<KV_DT, PAIR>(a, cc.b, cc.kvh, qop, k_mul);
 #pragma unroll
       for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
       m_run = kNegBig;
@@ -1489,9 +1557,9 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
       item_g0 = g - cc.t;
     }
     // q of the item that the tile just issued starts (an empty load otherwise)
-    load_q_stage(a, lc.b, lc.kvh, lc.t == 0, qs);
+    load_q_stage<PAIR>(a, lc.b, lc.kvh, lc.t == 0, qs);
     advance_load();
-    compute_tile16<KV_DT>(cur, cc.t * kTileTok, cc.L, qop, score_mul, acc, m_run, l_run);
+    compute_tile16<KV_DT, PAIR>(cur, cc.t * kTileTok, cc.L, qop, score_mul, acc, m_run, l_run, hi);
     const bool item_end = cc.t == cc.n - 1;
     const bool fin = item_end || g == g1 - 1;
     const bool whole = item_end && item_g0 >= g0;
@@ -1502,7 +1570,7 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
       if (fin) {
         float l_col = l_run + __shfl_xor(l_run, 16);
         l_col += __shfl_xor(l_col, 32);
-        finish_small_group(a, cc, whole, w, kslot, acc, m_run, l_col, v_mul, fs);
+        finish_small_group<PAIR>(a, cc, whole, w, kslot, acc, m_run, l_col, v_mul, fs);
         // Finishes before the range's last tile wait in LDS (up to
         // a.defer of them) and go out after it, so that their stores do not
         // sit between the tile loads of the read stream.
@@ -1527,7 +1595,7 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
     } else if (fin) {
       float l_col = l_run + __shfl_xor(l_run, 16);
       l_col += __shfl_xor(l_col, 32);
-      finish_sk(a, cc, whole, w, kslot, acc, m_run, l_col, v_mul);
+      finish_sk<PAIR>(a, cc, whole, w, kslot, acc, m_run, l_col, v_mul);
     }
     cursor_next(cc, pre, lens, a.batch);
   };
@@ -1541,7 +1609,8 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
     for (int i = 0; i < ndef; ++i) {
       const int* u = dqu + 4 * i;
       FinishStores fs;
-      finish_rsrc(a, lds_uniform(u, 0) != 0, lds_uniform(u, 1), lds_uniform(u, 2), w, lds_uniform(u, 3), fs);
+      finish_rsrc<PAIR>(a, lds_uniform(u, 0) != 0, lds_uniform(u, 1), lds_uniform(u, 2), w, lds_uniform(u, 3),
+                        fs);
       const u32x4* rec = dq + (i * kWave + lane) * 4;
       fs.da = rec[0];
       fs.db = rec[1];
@@ -1555,28 +1624,51 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
   }
 }
 
-template <int KV_DT, bool kSmallGroup>
+template <int KV_DT, bool kSmallGroup, bool PAIR>
 __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_kernel(DecodeArgs a) {
-  stream_decode<KV_DT, kSmallGroup>(a);
+  stream_decode<KV_DT, kSmallGroup, PAIR>(a);
 }
 
 // Per-token-head formats (and per-tensor FP8 with groups above 4) ask for
 // the two-waves-per-SIMD register budget explicitly: left to itself the
 // scheduler takes a few registers more than two waves can hold, and the
 // residency halves.
-template <int KV_DT, bool kSmallGroup>
+template <int KV_DT, bool kSmallGroup, bool PAIR>
 __global__ __launch_bounds__(kDecWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
 paged_decode_stream_2w_kernel(DecodeArgs a) {
-  stream_decode<KV_DT, kSmallGroup>(a);
+  stream_decode<KV_DT, kSmallGroup, PAIR>(a);
 }
 
-template <int KV_DT, bool kSmallGroup>
+template <int KV_DT, bool kSmallGroup, bool PAIR>
 constexpr auto stream_kernel() {
   // (per-tensor FP8 with groups above 4 lands a few registers past 256 on its own)
   if constexpr (kPerTokenScale<KV_DT> || (KV_DT == MKV_DTYPE_FP8E4M3 && !kSmallGroup))
-    return paged_decode_stream_2w_kernel<KV_DT, kSmallGroup>;
+    return paged_decode_stream_2w_kernel<KV_DT, kSmallGroup, PAIR>;
   else
-    return paged_decode_stream_kernel<KV_DT, kSmallGroup>;
+    return paged_decode_stream_kernel<KV_DT, kSmallGroup, PAIR>;
+}
+
+// Element offset, inside the batch row, of the two output dims 2 lane and
+// 2 lane + 1 of query head hq (head h of its group) that a merge wave's lane
+// writes; own = false when they belong to the other half of a paired head.
+MKV_DEV int64_t merge_out_offset(const DecodeArgs& a, int hq, int h, int lane, bool& own) {
+  if (!a.pair) {
+    own = true;
+    return (int64_t)hq * kHeadDim + 2 * lane;
+  }
+  const bool hi = h >= (a.group >> 1);
+  own = (lane >= 32) == hi;
+  return (int64_t)hq * (kHeadDim / 2) + 2 * lane - (hi ? 64 : 0);
+}
+
+MKV_DEV void store_out2(const DecodeArgs& a, int64_t off, float x0, float x1) {
+  if (a.q_dtype == MKV_DTYPE_F32) {
+    *reinterpret_cast<f32x2*>(reinterpret_cast<float*>(a.out) + off) = f32x2{x0, x1};
+  } else {
+    const uint32_t lo = a.q_dtype == MKV_DTYPE_BF16 ? f32_to_bf16_bits(x0) : f32_to_f16_bits(x0);
+    const uint32_t hi = a.q_dtype == MKV_DTYPE_BF16 ? f32_to_bf16_bits(x1) : f32_to_f16_bits(x1);
+    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + off) = lo | (hi << 16);
+  }
 }
 
 // Merge of stream-K partials: one wave per (sequence, query head).  The
@@ -1601,7 +1693,8 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_ke
   const int kvh = hq / a.group, h = hq - kvh * a.group;
   const int p0 = a.sk_meta[b], n = a.sk_meta[b + 1] - p0;
   const int* meta = a.sk_meta + a.batch + 1 + 3 * b;
-  const int64_t off = (int64_t)b * a.out_stride + (int64_t)hq * kHeadDim + 2 * lane;
+  bool own;
+  const int64_t off = (int64_t)b * a.out_stride + merge_out_offset(a, hq, h, lane, own);
   float o0 = 0.0f, o1 = 0.0f, l = 0.0f;
   if (n > 0) {
     const int glo = meta[0], ghi = meta[1], s0 = meta[2];
@@ -1689,131 +1782,27 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_stream_merge_ke
     for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
   }
   const float inv = l > 0.0f ? (kv_fp8 ? load_uniform_f32(a.v_scale) : 1.0f) / l : 0.0f;
-  if (a.q_dtype == MKV_DTYPE_F32) {
-    *reinterpret_cast<f32x2*>(reinterpret_cast<float*>(a.out) + off) = f32x2{o0 * inv, o1 * inv};
-  } else {
-    const uint32_t lo = a.q_dtype == MKV_DTYPE_BF16 ? f32_to_bf16_bits(o0 * inv) : f32_to_f16_bits(o0 * inv);
-    const uint32_t hi = a.q_dtype == MKV_DTYPE_BF16 ? f32_to_bf16_bits(o1 * inv) : f32_to_f16_bits(o1 * inv);
-    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + off) = lo | (hi << 16);
-  }
+  if (own) store_out2(a, off, o0 * inv, o1 * inv);
 }
 
 // ---------------------------------------------------------------------------
 // fp32 KV kernel: v_mfma_f32_16x16x4_f32, 16-token tiles, same lane mapping.
 // ---------------------------------------------------------------------------
+template <bool PAIR>
 __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_mfma32_kernel(DecodeArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int c = lane & 15, kg = lane >> 4;
   WorkItem it;
   if (!decode_work_item(a, wave_work_index(), it)) return;
-
   float qf[32];
-  const int hq = it.kvh * a.group + c;
-  if (c < a.group) {
-    const int64_t qoff = (int64_t)it.b * a.q_stride + (int64_t)hq * kHeadDim + 32 * kg;
-    load_q32(a.q, a.q_dtype, qoff, qf);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
-  }
+  load_q_f32<PAIR>(a, it.b, it.kvh, qf);
   const float score_mul = a.sm_scale * kLog2e;
   f32x4 acc[8];
 #pragma unroll
   for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegBig, l_run = 0.0f;
-  // Splits that span at most 64 blocks (every default split): the K/V of
-  // the next 16-token tile are in flight while this one is computed.
-  const int nblk = it.t_end > it.t_begin
-                       ? ((it.t_end - 1) >> a.idx.bs_log2) - (it.t_begin >> a.idx.bs_log2) + 1
-                       : 0;
-  if (nblk > 0 && nblk <= 64) {
-    const ItemLoad Ld = item_load_setup<MKV_DTYPE_F32>(a, it);
-    TileF32 ta, tb;
-    load_tile_f32(a, it, Ld, it.t_begin, ta);
-    for (int t0 = it.t_begin;;) {
-      load_tile_f32(a, it, Ld, t0 + 16, tb);
-      compute_tile_f32(ta, t0, it.t_end, qf, score_mul, acc, m_run, l_run);
-      t0 += 16;
-      if (t0 >= it.t_end) break;
-      load_tile_f32(a, it, Ld, t0 + 16, ta);
-      compute_tile_f32(tb, t0, it.t_end, qf, score_mul, acc, m_run, l_run);
-      t0 += 16;
-      if (t0 >= it.t_end) break;
-    }
-    float l_col = l_run + __shfl_xor(l_run, 16);
-    l_col += __shfl_xor(l_col, 32);
-    finish_item(a, it, acc, m_run, l_col, 1.0f);
-    return;
-  }
-  const int64_t bs_mask = (int64_t(1) << a.idx.bs_log2) - 1;
-  const int64_t head_off = (int64_t)it.kvh * kHeadDim;
-  const float* kc = reinterpret_cast<const float*>(a.k_cache);
-  const float* vc = reinterpret_cast<const float*>(a.v_cache);
-
-  for (int64_t t0 = it.t_begin; t0 < it.t_end; t0 += 16) {
-    const int64_t phys = a.idx.physical_block(it.b, t0 >> a.idx.bs_log2);
-    // K row of token t0 + c, dims 32kg .. 32kg+31.
-    u32x4 kr[8];
-    {
-      const int64_t t = t0 + c;
-      const bool ok = t < it.t_end && phys >= 0;
-      const int64_t base = ((phys << a.idx.bs_log2) + (t & bs_mask)) * a.idx.row_elems + head_off + 32 * kg;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) kr[i] = ok ? ld16_stream(kc + base + 4 * i) : u32x4{0, 0, 0, 0};
-    }
-    // V rows of tokens t0 + 4kg + r, dims 8c .. 8c+7.
-    u32x4 vr[4][2];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t t = t0 + 4 * kg + r;
-      const bool ok = t < it.t_end && phys >= 0;
-      const int64_t base = ((phys << a.idx.bs_log2) + (t & bs_mask)) * a.idx.row_elems + head_off + 8 * c;
-      vr[r][0] = ok ? ld16_stream(vc + base) : u32x4{0, 0, 0, 0};
-      vr[r][1] = ok ? ld16_stream(vc + base + 4) : u32x4{0, 0, 0, 0};
-    }
-    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int st = 0; st < 32; ++st)
-      s = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kr[st >> 2][st & 3]), qf[st], s, 0, 0, 0);
-    float mx = kNegBig;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t t = t0 + 4 * kg + r;
-      const bool ok = t < it.t_end && phys >= 0;
-      s[r] = ok ? s[r] * score_mul : -__builtin_huge_valf();
-      mx = fmaxf(mx, s[r]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
-    float p[4], psum = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = __builtin_amdgcn_exp2f(s[r] - m_new);
-      psum += p[r];
-    }
-    l_run = l_run * alpha + psum;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float ar = __shfl(alpha, 4 * kg + r);
-#pragma unroll
-        for (int mm = 0; mm < 8; ++mm) acc[mm][r] *= ar;
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-#pragma unroll
-      for (int mm = 0; mm < 8; ++mm)
-        acc[mm] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], __uint_as_float(vr[r][mm >> 2][mm & 3]),
-                                                        acc[mm], 0, 0, 0);
-    }
-  }
+  f32_range(a, it, qf, score_mul, acc, m_run, l_run);
   float l_col = l_run + __shfl_xor(l_run, 16);
   l_col += __shfl_xor(l_col, 32);
-  finish_item(a, it, acc, m_run, l_col, 1.0f);
+  finish_item<PAIR>(a, it, acc, m_run, l_col, 1.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -1843,14 +1832,9 @@ __global__ __launch_bounds__(kDecWaves* kWave) void paged_decode_merge_kernel(De
     o1 += wgt * x[1];
   }
   const float inv = l > 0.0f ? (kv_fp8 ? load_uniform_f32(a.v_scale) : 1.0f) / l : 0.0f;
-  const int64_t off = (int64_t)b * a.out_stride + (int64_t)hq * kHeadDim + 2 * lane;
-  if (a.q_dtype == MKV_DTYPE_F32) {
-    *reinterpret_cast<f32x2*>(reinterpret_cast<float*>(a.out) + off) = f32x2{o0 * inv, o1 * inv};
-  } else {
-    const uint32_t lo = a.q_dtype == MKV_DTYPE_BF16 ? f32_to_bf16_bits(o0 * inv) : f32_to_f16_bits(o0 * inv);
-    const uint32_t hi = a.q_dtype == MKV_DTYPE_BF16 ? f32_to_bf16_bits(o1 * inv) : f32_to_f16_bits(o1 * inv);
-    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + off) = lo | (hi << 16);
-  }
+  bool own;
+  const int64_t off = (int64_t)b * a.out_stride + merge_out_offset(a, hq, hq % a.group, lane, own);
+  if (own) store_out2(a, off, o0 * inv, o1 * inv);
 }
 
 int ilog2_exact(int v) {
@@ -1877,6 +1861,11 @@ int resolve_split(int split_tokens, int batch, int num_kv_heads, int max_blocks,
   if (split_tokens <= 0) return default_split_tokens(batch, num_kv_heads, max_blocks, block_size);
   return split_tokens;
 }
+
+// The three decode schedules (mkv_paged_decode_route reports them).
+constexpr int kRouteStream = MKV_DECODE_ROUTE_STREAM;
+constexpr int kRouteSplit = MKV_DECODE_ROUTE_SPLIT;
+constexpr int kRouteWorkgroup = MKV_DECODE_ROUTE_WORKGROUP;
 
 // Compute units of the current device (cached per device).  Without a usable
 // device the size query assumes a generous count; no kernel runs then.
@@ -1915,17 +1904,18 @@ size_t stream_ws_bytes(int batch, int group) {
 // Persistent stream-K launch: one wave per SIMD slot the kernel can hold
 // (residency cached per device and LDS bucket), the first dispatch round
 // marked for the uneven split.
-template <int DT, bool SMALL>
+template <int DT, bool SMALL, bool PAIR>
 void launch_stream(DecodeArgs& a, int lds_bucket, size_t lds_bound, size_t lds, hipStream_t s) {
-  static int per_cu[64][2];
+  static int per_cu[64][2][2];
   int dev = 0;
   (void)hipGetDevice(&dev);
   const int slot = dev >= 0 && dev < 64 ? dev : 0;
-  constexpr auto kernel = stream_kernel<DT, SMALL>();
-  if (per_cu[slot][lds_bucket] == 0) per_cu[slot][lds_bucket] = resident_wgs_per_cu(kernel, lds_bound);
-  const int wgs = device_cus() * per_cu[slot][lds_bucket];
+  constexpr auto kernel = stream_kernel<DT, SMALL, PAIR>();
+  int& res = per_cu[slot][lds_bucket][PAIR ? 1 : 0];
+  if (res == 0) res = resident_wgs_per_cu(kernel, lds_bound);
+  const int wgs = device_cus() * res;
   a.num_waves = wgs * kDecWaves;
-  a.first_waves = per_cu[slot][lds_bucket] > 1 ? device_cus() * kDecWaves : a.num_waves;
+  a.first_waves = res > 1 ? device_cus() * kDecWaves : a.num_waves;
   hipLaunchKernelGGL(kernel, dim3(wgs), dim3(kDecWaves * kWave), lds, s, a);
 }
 
@@ -1935,21 +1925,41 @@ size_t split_ws_bytes(int batch, int num_heads, int max_blocks, int block_size, 
   return (size_t)batch * num_heads * max_splits * (kHeadDim + 2) * sizeof(float);
 }
 
-// The route mkv_paged_decode takes: stream-K (library schedule, 16-bit / FP8
-// / INT8 KV, batch <= kStreamMaxBatch; it needs a group of num_kv_heads
-// waves, and a grid holds at least CUs x kDecWaves waves), else split-K.
-bool use_stream(int split_tokens, int kv_dtype, int batch, int num_kv_heads) {
-  return split_tokens == 0 && kv_dtype != MKV_DTYPE_F32 && batch <= kStreamMaxBatch &&
-         num_kv_heads <= device_cus() * kDecWaves;
+// Kernel shape of a call: its KV heads and group as the kernels see them
+// (head_dim 64: KV heads read in pairs, see kQDim).
+struct KernelShape {
+  int kv_heads;
+  int group;
+  bool pair;
+};
+
+// MKV_OK, or the status of a shape the kernels do not support.
+int kernel_shape(int num_heads, int num_kv_heads, int head_dim, KernelShape& ks) {
+  if (num_heads <= 0 || num_kv_heads <= 0) return MKV_ERR_BAD_SHAPE;
+  if (head_dim != kHeadDim && head_dim != kHeadDim / 2) return MKV_ERR_UNSUPPORTED_HEAD_DIM;
+  if (num_heads % num_kv_heads) return MKV_ERR_UNSUPPORTED_GROUP;
+  const int g = num_heads / num_kv_heads;
+  ks.pair = head_dim == kHeadDim / 2;
+  if (ks.pair) {
+    if (num_kv_heads & 1) return MKV_ERR_UNSUPPORTED_HEAD_DIM;  // heads pair up
+    if (g > 8) return MKV_ERR_UNSUPPORTED_GROUP;                // 2g query heads per pair
+    ks.kv_heads = num_kv_heads / 2;
+    ks.group = 2 * g;
+  } else {
+    if (g > 16) return MKV_ERR_UNSUPPORTED_GROUP;
+    ks.kv_heads = num_kv_heads;
+    ks.group = g;
+  }
+  return MKV_OK;
 }
 
-// Waves per workgroup of the workgroup-split route: as many as fill the
-// chip's two-waves-per-SIMD slots once (at most kWgMaxWaves), no more than
-// the widest sequence's tiles, and few enough that the LDS merge buffers fit
-// in 64 KiB.
-int wg_waves(int batch, int num_kv_heads, int group, int max_blocks, int block_size) {
-  const int64_t items = (int64_t)batch * num_kv_heads;
-  const int64_t slots = (int64_t)device_cus() * 8;
+// Waves per workgroup of the workgroup route: as many as fill the chip's
+// two-waves-per-SIMD slots once (at most kWgMaxWaves), no more than the
+// widest sequence's tiles, and few enough that the LDS merge buffers fit in
+// 64 KiB.
+int wg_waves(int batch, int kv_heads, int group, int max_blocks, int block_size, int cus) {
+  const int64_t items = (int64_t)batch * kv_heads;
+  const int64_t slots = (int64_t)cus * 8;
   const int64_t max_tiles = ((int64_t)max_blocks * block_size + 31) / 32;
   int nw = kWgMaxWaves;
   while (nw > 1 && (items * nw > slots || nw > max_tiles ||
@@ -1958,13 +1968,46 @@ int wg_waves(int batch, int num_kv_heads, int group, int max_blocks, int block_s
   return nw;
 }
 
-// Workspace bytes of the route that these arguments select.
-size_t decode_ws_bytes(int batch, int num_heads, int num_kv_heads, int max_blocks, int block_size,
-                       int kv_dtype, int split_tokens) {
-  if (split_tokens == MKV_DECODE_WORKGROUP) return 0;
-  if (use_stream(split_tokens, kv_dtype, batch, num_kv_heads))
-    return stream_ws_bytes(batch, num_heads / num_kv_heads);
-  const int st = resolve_split(split_tokens, batch, num_kv_heads, max_blocks, block_size);
+// The route of a call.  split_tokens > 0: split-K with that split;
+// MKV_DECODE_WORKGROUP: the workgroup route; MKV_DECODE_STREAM: stream-K
+// (split-K where stream-K does not apply: fp32 caches, batches above
+// kStreamMaxBatch).  0, the library's choice, from the shape alone, with the
+// block-table width as the bound of the longest context (the reference's
+// runner pads each decode step's tables to its longest sequence,
+// model_runner.py:640-644):
+//   * the workgroup route when its waves fill at least a quarter of the
+//     wave slots (items x waves >= 2 x CUs) and the longest possible item
+//     gives each of its waves at most 256 tokens (512 for fp32 caches): one
+//     launch, no workspace, no partial round trip through HBM.  Its time is
+//     set by the longest item's tile chain, so short contexts favour it
+//     (batches 16-128 of 300-800 tokens in 4-block tables: 12.3 / 13.4 /
+//     19.0 / 20.5 us at batches 16 / 32 / 40 / 60 against 17.6 / 20.1 /
+//     21.7 / 25.2 us for stream-K and its merge) and long ones do not (batch
+//     32 of 256-4096 tokens: 42.9 against 34.8 us);
+//   * stream-K otherwise (16-bit / FP8 / INT8 caches): balanced over every
+//     wave whatever the lengths, at the cost of a merge launch;
+//   * split-K for fp32 caches otherwise (default split).
+int choose_route(int split_tokens, int kv_dtype, int batch, const KernelShape& ks, int max_blocks,
+                 int block_size, int cus) {
+  if (split_tokens == MKV_DECODE_WORKGROUP) return kRouteWorkgroup;
+  if (split_tokens > 0) return kRouteSplit;
+  const bool stream_ok =
+      kv_dtype != MKV_DTYPE_F32 && batch <= kStreamMaxBatch && ks.kv_heads <= cus * kDecWaves;
+  if (split_tokens == MKV_DECODE_STREAM) return stream_ok ? kRouteStream : kRouteSplit;
+  const int64_t items = (int64_t)batch * ks.kv_heads;
+  const int nw = wg_waves(batch, ks.kv_heads, ks.group, max_blocks, block_size, cus);
+  const int64_t wave_tokens = ((int64_t)max_blocks * block_size + nw - 1) / nw;
+  const int64_t bound = kv_dtype == MKV_DTYPE_F32 ? 16 * kTileTok : 8 * kTileTok;
+  if (items * nw >= 2 * (int64_t)cus && wave_tokens <= bound) return kRouteWorkgroup;
+  return stream_ok ? kRouteStream : kRouteSplit;
+}
+
+// Workspace bytes of a route.
+size_t route_ws_bytes(int route, int batch, int num_heads, const KernelShape& ks, int max_blocks,
+                      int block_size, int split_tokens) {
+  if (route == kRouteWorkgroup) return 0;
+  if (route == kRouteStream) return stream_ws_bytes(batch, ks.group);
+  const int st = resolve_split(split_tokens, batch, ks.kv_heads, max_blocks, block_size);
   return split_ws_bytes(batch, num_heads, max_blocks, block_size, st);
 }
 
@@ -1978,33 +2021,179 @@ extern "C" int mkv_paged_decode_split_tokens(int batch, int num_kv_heads, int ma
   return resolve_split(split_tokens, batch, num_kv_heads, max_blocks, block_size);
 }
 
+extern "C" int mkv_paged_decode_route(int batch, int num_heads, int num_kv_heads, int max_blocks,
+                                      int block_size, int head_dim, int kv_dtype, int split_tokens,
+                                      int num_cus) {
+  KernelShape ks;
+  if (batch <= 0 || max_blocks <= 0 || block_size <= 0) return MKV_ERR_BAD_SHAPE;
+  const int st = kernel_shape(num_heads, num_kv_heads, head_dim, ks);
+  if (st != MKV_OK) return st;
+  return choose_route(split_tokens, kv_dtype, batch, ks, max_blocks, block_size,
+                      num_cus > 0 ? num_cus : device_cus());
+}
+
 extern "C" size_t mkv_paged_decode_workspace_size(int batch, int num_heads, int num_kv_heads,
                                                   int max_blocks, int block_size, int head_dim,
                                                   int kv_dtype, int split_tokens) {
-  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks <= 0 || block_size <= 0 ||
-      head_dim <= 0 || num_heads % num_kv_heads)
+  KernelShape ks;
+  if (batch <= 0 || max_blocks <= 0 || block_size <= 0 ||
+      kernel_shape(num_heads, num_kv_heads, head_dim, ks) != MKV_OK)
     return 0;
-  return decode_ws_bytes(batch, num_heads, num_kv_heads, max_blocks, block_size, kv_dtype, split_tokens);
+  const int route = choose_route(split_tokens, kv_dtype, batch, ks, max_blocks, block_size, device_cus());
+  return route_ws_bytes(route, batch, num_heads, ks, max_blocks, block_size, split_tokens);
 }
 
 namespace {
 
-int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_t q_batch_stride,
-                      int q_dtype, const void* k_cache, const void* v_cache, int kv_dtype,
-                      int64_t num_blocks, const float* k_scale, const float* v_scale,
-                      int kv_scale_mode, const int32_t* block_tables, int64_t bt_stride,
-                      int max_blocks, const void* context_lens, int context_lens_dtype, int batch,
-                      int num_heads, int num_kv_heads, int head_dim, int block_size,
-                      float sm_scale, int split_tokens, void* workspace, size_t workspace_bytes,
-                      void* stream) {
+// Launch the kernels of `route` (arguments validated, a filled in except the
+// route's own fields).
+template <bool PAIR>
+int launch_route(DecodeArgs& a, int route, int fmt, int split_tokens, int max_blocks, int block_size,
+                 void* workspace, size_t workspace_bytes, hipStream_t s) {
+  const int batch = a.batch, group = a.group;
+  // the merge kernels apply the per-tensor V scale
+  const bool fp8 = fmt == MKV_DTYPE_FP8E4M3;
+  if (route == kRouteWorkgroup) {
+    const int nw = wg_waves(batch, a.num_kv_heads, group, max_blocks, block_size, device_cus());
+    const size_t lds = (size_t)nw * group * (kHeadDim + 2) * sizeof(float);
+    a.split_tokens = 0;
+    a.max_splits = 0;
+    a.ws_acc = nullptr;
+    a.ws_ml = nullptr;
+    const dim3 grid((unsigned)((int64_t)batch * a.num_kv_heads)), block(nw * kWave);
+    switch (fmt) {
+      case MKV_DTYPE_F32:
+        hipLaunchKernelGGL(paged_decode_wg_f32_kernel<PAIR>, grid, block, lds, s, a);
+        break;
+      case MKV_DTYPE_FP8E4M3:
+        hipLaunchKernelGGL((paged_decode_wg_kernel<MKV_DTYPE_FP8E4M3, PAIR>), grid, block, lds, s, a);
+        break;
+      case kKvFp8PerToken:
+        hipLaunchKernelGGL((paged_decode_wg_kernel<kKvFp8PerToken, PAIR>), grid, block, lds, s, a);
+        break;
+      case kKvI8PerToken:
+        hipLaunchKernelGGL((paged_decode_wg_kernel<kKvI8PerToken, PAIR>), grid, block, lds, s, a);
+        break;
+      case MKV_DTYPE_BF16:
+        hipLaunchKernelGGL((paged_decode_wg_kernel<MKV_DTYPE_BF16, PAIR>), grid, block, lds, s, a);
+        break;
+      default:
+        hipLaunchKernelGGL((paged_decode_wg_kernel<MKV_DTYPE_F16, PAIR>), grid, block, lds, s, a);
+        break;
+    }
+    return (int)hipGetLastError();
+  }
+  if (route == kRouteStream) {
+    const size_t need = stream_ws_bytes(batch, group);
+    if (!workspace) return MKV_ERR_NULL_POINTER;
+    if (workspace_bytes < need) return MKV_ERR_WORKSPACE_TOO_SMALL;
+    if (reinterpret_cast<uintptr_t>(workspace) & 15u) return MKV_ERR_MISALIGNED;
+    // (held finishes: the kernels for groups of at most 4 query heads)
+    a.defer = batch <= kStreamDeferMaxBatch && group <= 4 ? kStreamDefer : 0;
+
+    const size_t lds = stream_lds_bytes(batch, a.defer);
+    // Workspace slots are laid out for the largest grid (stream_waves()).
+    const size_t slots = (size_t)stream_waves() * 2 * group;
+    a.split_tokens = kTileTok;
+    a.max_splits = 0;
+    a.ws_acc = reinterpret_cast<float*>(workspace);
+    a.ws_ml = a.ws_acc + slots * kHeadDim;
+    a.sk_meta = reinterpret_cast<int*>(a.ws_ml + slots * 2);
+    a.seq_cost = kSeqCost;
+    a.first_pct = kFirstSharePct;
+    // Residency depends on the launch's LDS (the per-sequence prefix): query it
+    // once per device for batches up to kStreamSmallBatch and once for larger.
+    const int lds_bucket = batch <= kStreamSmallBatch ? 0 : 1;
+    const size_t lds_bound = lds_bucket ? kStreamMaxLds : kStreamSmallLds;
+    const bool small = group <= 4;
+    switch (fmt) {
+      case MKV_DTYPE_FP8E4M3:
+        small ? launch_stream<MKV_DTYPE_FP8E4M3, true, PAIR>(a, lds_bucket, lds_bound, lds, s)
+              : launch_stream<MKV_DTYPE_FP8E4M3, false, PAIR>(a, lds_bucket, lds_bound, lds, s);
+        break;
+      case kKvFp8PerToken:
+        small ? launch_stream<kKvFp8PerToken, true, PAIR>(a, lds_bucket, lds_bound, lds, s)
+              : launch_stream<kKvFp8PerToken, false, PAIR>(a, lds_bucket, lds_bound, lds, s);
+        break;
+      case kKvI8PerToken:
+        small ? launch_stream<kKvI8PerToken, true, PAIR>(a, lds_bucket, lds_bound, lds, s)
+              : launch_stream<kKvI8PerToken, false, PAIR>(a, lds_bucket, lds_bound, lds, s);
+        break;
+      case MKV_DTYPE_BF16:
+        small ? launch_stream<MKV_DTYPE_BF16, true, PAIR>(a, lds_bucket, lds_bound, lds, s)
+              : launch_stream<MKV_DTYPE_BF16, false, PAIR>(a, lds_bucket, lds_bound, lds, s);
+        break;
+      default:
+        small ? launch_stream<MKV_DTYPE_F16, true, PAIR>(a, lds_bucket, lds_bound, lds, s)
+              : launch_stream<MKV_DTYPE_F16, false, PAIR>(a, lds_bucket, lds_bound, lds, s);
+        break;
+    }
+    const int64_t mitems = (int64_t)batch * a.num_heads;
+    hipLaunchKernelGGL(paged_decode_stream_merge_kernel,
+                       dim3((unsigned)((mitems + kDecWaves - 1) / kDecWaves)), dim3(kDecWaves * kWave), 0,
+                       s, a, (int)fp8);
+    return (int)hipGetLastError();
+  }
+
+  const int st = resolve_split(split_tokens, batch, a.num_kv_heads, max_blocks, block_size);
+  a.split_tokens = st;
+  const int64_t max_len = (int64_t)max_blocks * block_size;
+  a.max_splits = max_len > 0 ? (int)((max_len + st - 1) / st) : 1;
+  a.ws_acc = nullptr;
+  a.ws_ml = nullptr;
+  if (a.max_splits > 1) {
+    const size_t need = (size_t)batch * a.num_heads * a.max_splits * (kHeadDim + 2) * sizeof(float);
+    if (!workspace) return MKV_ERR_NULL_POINTER;
+    if (workspace_bytes < need) return MKV_ERR_WORKSPACE_TOO_SMALL;
+    if (reinterpret_cast<uintptr_t>(workspace) & 15u) return MKV_ERR_MISALIGNED;
+    a.ws_acc = reinterpret_cast<float*>(workspace);
+    a.ws_ml = a.ws_acc + (size_t)batch * a.num_heads * a.max_splits * kHeadDim;
+  }
+  const int64_t items = (int64_t)batch * a.num_kv_heads * a.max_splits;
+  const dim3 grid((unsigned)((items + kDecWaves - 1) / kDecWaves));
+  const dim3 block(kDecWaves * kWave);
+  switch (fmt) {
+    case MKV_DTYPE_FP8E4M3:
+      hipLaunchKernelGGL((paged_decode_mfma16_kernel<MKV_DTYPE_FP8E4M3, PAIR>), grid, block, 0, s, a);
+      break;
+    case kKvFp8PerToken:
+      hipLaunchKernelGGL((paged_decode_mfma16_2w_kernel<kKvFp8PerToken, PAIR>), grid, block, 0, s, a);
+      break;
+    case kKvI8PerToken:
+      hipLaunchKernelGGL((paged_decode_mfma16_2w_kernel<kKvI8PerToken, PAIR>), grid, block, 0, s, a);
+      break;
+    case MKV_DTYPE_BF16:
+      hipLaunchKernelGGL((paged_decode_mfma16_kernel<MKV_DTYPE_BF16, PAIR>), grid, block, 0, s, a);
+      break;
+    case MKV_DTYPE_F16:
+      hipLaunchKernelGGL((paged_decode_mfma16_kernel<MKV_DTYPE_F16, PAIR>), grid, block, 0, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL(paged_decode_mfma32_kernel<PAIR>, grid, block, 0, s, a);
+      break;
+  }
+  if (a.max_splits > 1) {
+    const int64_t mitems = (int64_t)batch * a.num_heads;
+    hipLaunchKernelGGL(paged_decode_merge_kernel, dim3((unsigned)((mitems + kDecWaves - 1) / kDecWaves)),
+                       block, 0, s, a, (int)fp8);
+  }
+  return (int)hipGetLastError();
+}
+
+// Validate the arguments and fill the kernel arguments; returns the status
+// and, on success, the call's kernel shape and format in ks / fmt.
+int decode_args(void* out, int64_t out_batch_stride, const void* q, int64_t q_batch_stride, int q_dtype,
+                const void* k_cache, const void* v_cache, int kv_dtype, int64_t num_blocks,
+                const float* k_scale, const float* v_scale, int kv_scale_mode,
+                const int32_t* block_tables, int64_t bt_stride, int max_blocks, const void* context_lens,
+                int context_lens_dtype, int batch, int num_heads, int num_kv_heads, int head_dim,
+                int block_size, float sm_scale, int split_tokens, DecodeArgs& a, KernelShape& ks,
+                int& fmt) {
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks < 0 || num_blocks < 0)
     return MKV_ERR_BAD_SHAPE;
-  if (batch == 0) return MKV_OK;
   if (!out || !q || !k_cache || !v_cache || !block_tables || !context_lens) return MKV_ERR_NULL_POINTER;
-  if (head_dim != kHeadDim) return MKV_ERR_UNSUPPORTED_HEAD_DIM;
-  if (num_heads % num_kv_heads != 0) return MKV_ERR_UNSUPPORTED_GROUP;
-  const int group = num_heads / num_kv_heads;
-  if (group < 1 || group > 16) return MKV_ERR_UNSUPPORTED_GROUP;
+  const int shp = kernel_shape(num_heads, num_kv_heads, head_dim, ks);
+  if (shp != MKV_OK) return shp;
   const int bs_log2 = ilog2_exact(block_size);
   if (bs_log2 < 4) return MKV_ERR_BAD_BLOCK_SIZE;
   if (q_dtype != MKV_DTYPE_F32 && q_dtype != MKV_DTYPE_BF16 && q_dtype != MKV_DTYPE_F16)
@@ -2022,13 +2211,14 @@ int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_
   if (per_token && num_blocks * (int64_t)block_size * num_kv_heads >= (int64_t(1) << 31))
     return MKV_ERR_BAD_SHAPE;
   // kernel format: the dtype, or a per-token-head code
-  const int fmt = per_token ? (kv_dtype == MKV_DTYPE_I8 ? kKvI8PerToken : kKvFp8PerToken) : kv_dtype;
+  fmt = per_token ? (kv_dtype == MKV_DTYPE_I8 ? kKvI8PerToken : kKvFp8PerToken) : kv_dtype;
   if (context_lens_dtype != MKV_INDEX_I32 && context_lens_dtype != MKV_INDEX_I64)
     return MKV_ERR_UNSUPPORTED_DTYPE;
   if (q_batch_stride < (int64_t)num_heads * head_dim || out_batch_stride < (int64_t)num_heads * head_dim ||
       bt_stride < max_blocks)
     return MKV_ERR_BAD_STRIDE;
-  if (split_tokens != MKV_DECODE_WORKGROUP && (split_tokens < 0 || split_tokens % 32 != 0))
+  if (split_tokens != MKV_DECODE_WORKGROUP && split_tokens != MKV_DECODE_STREAM &&
+      (split_tokens < 0 || split_tokens % 32 != 0))
     return MKV_ERR_BAD_SHAPE;
   const int qb = q_dtype == MKV_DTYPE_F32 ? 4 : 2;
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
@@ -2036,7 +2226,7 @@ int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_
     return MKV_ERR_MISALIGNED;
   if ((q_batch_stride * qb) % 16 || (out_batch_stride * qb) % 16) return MKV_ERR_MISALIGNED;
 
-  DecodeArgs a;
+  a = DecodeArgs{};
   a.out = out;
   a.out_stride = out_batch_stride;
   a.q = q;
@@ -2056,143 +2246,46 @@ int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_
   a.ctx_i64 = context_lens_dtype == MKV_INDEX_I64;
   a.batch = batch;
   a.num_heads = num_heads;
-  a.num_kv_heads = num_kv_heads;
-  a.group = group;
+  a.num_kv_heads = ks.kv_heads;
+  a.group = ks.group;
+  a.scale_heads = num_kv_heads;
+  a.pair = ks.pair ? 1 : 0;
   a.sm_scale = sm_scale;
+  return MKV_OK;
+}
+
+int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_t q_batch_stride,
+                      int q_dtype, const void* k_cache, const void* v_cache, int kv_dtype,
+                      int64_t num_blocks, const float* k_scale, const float* v_scale,
+                      int kv_scale_mode, const int32_t* block_tables, int64_t bt_stride,
+                      int max_blocks, const void* context_lens, int context_lens_dtype, int batch,
+                      int num_heads, int num_kv_heads, int head_dim, int block_size,
+                      float sm_scale, int split_tokens, void* workspace, size_t workspace_bytes,
+                      void* stream, bool noalloc) {
+  DecodeArgs a;
+  KernelShape ks;
+  int fmt = 0;
+  const int st = decode_args(out, out_batch_stride, q, q_batch_stride, q_dtype, k_cache, v_cache, kv_dtype,
+                             num_blocks, k_scale, v_scale, kv_scale_mode, block_tables, bt_stride, max_blocks,
+                             context_lens, context_lens_dtype, batch, num_heads, num_kv_heads, head_dim,
+                             block_size, sm_scale, split_tokens, a, ks, fmt);
+  if (st != MKV_OK) return st;
+  if (batch == 0) return MKV_OK;
+  const int cus = device_cus();
+  int route = choose_route(split_tokens, kv_dtype, batch, ks, max_blocks, block_size, cus);
+  if (noalloc && route_ws_bytes(route, batch, num_heads, ks, max_blocks, block_size, split_tokens) >
+                     workspace_bytes) {
+    // The caller's scratch cannot hold this route's partials: the library's
+    // choice falls back to the workgroup route (no workspace); an explicit
+    // route is refused.
+    if (split_tokens != 0) return MKV_ERR_SCRATCH_LIMIT;
+    route = kRouteWorkgroup;
+  }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  // the merge kernels apply the per-tensor V scale
-  const bool fp8 = fmt == MKV_DTYPE_FP8E4M3;
-  if (split_tokens == MKV_DECODE_WORKGROUP) {
-    const int nw = wg_waves(batch, num_kv_heads, group, max_blocks, block_size);
-    // a wave's tile range must span at most 64 blocks (one lane each)
-    const int64_t max_tiles = ((int64_t)max_blocks * block_size + 31) / 32;
-    const int64_t wave_tokens = ((max_tiles + nw - 1) / nw) * 32;
-    if ((wave_tokens >> bs_log2) + 2 > 64) return MKV_ERR_BAD_SHAPE;
-    const size_t lds = (size_t)nw * group * (kHeadDim + 2) * sizeof(float);
-    a.split_tokens = 0;
-    a.max_splits = 0;
-    a.ws_acc = nullptr;
-    a.ws_ml = nullptr;
-    const dim3 grid((unsigned)((int64_t)batch * num_kv_heads)), block(nw * kWave);
-    switch (fmt) {
-      case MKV_DTYPE_F32:
-        hipLaunchKernelGGL(paged_decode_wg_f32_kernel, grid, block, lds, s, a);
-        break;
-      case MKV_DTYPE_FP8E4M3:
-        hipLaunchKernelGGL(paged_decode_wg_kernel<MKV_DTYPE_FP8E4M3>, grid, block, lds, s, a);
-        break;
-      case kKvFp8PerToken:
-        hipLaunchKernelGGL(paged_decode_wg_kernel<kKvFp8PerToken>, grid, block, lds, s, a);
-        break;
-      case kKvI8PerToken:
-        hipLaunchKernelGGL(paged_decode_wg_kernel<kKvI8PerToken>, grid, block, lds, s, a);
-        break;
-      case MKV_DTYPE_BF16:
-        hipLaunchKernelGGL(paged_decode_wg_kernel<MKV_DTYPE_BF16>, grid, block, lds, s, a);
-        break;
-      default:
-        hipLaunchKernelGGL(paged_decode_wg_kernel<MKV_DTYPE_F16>, grid, block, lds, s, a);
-        break;
-    }
-    return (int)hipGetLastError();
-  }
-  if (use_stream(split_tokens, kv_dtype, batch, num_kv_heads)) {
-    // stream-K path
-    const size_t need = stream_ws_bytes(batch, group);
-    if (!workspace) return MKV_ERR_NULL_POINTER;
-    if (workspace_bytes < need) return MKV_ERR_WORKSPACE_TOO_SMALL;
-    if (reinterpret_cast<uintptr_t>(workspace) & 15u) return MKV_ERR_MISALIGNED;
-    // (held finishes: the kernels for groups of at most 4 query heads)
-    a.defer = batch <= kStreamDeferMaxBatch && group <= 4 ? kStreamDefer : 0;
-
-    const size_t lds = stream_lds_bytes(batch, a.defer);
-    // Workspace slots are laid out for the largest grid (stream_waves()).
-    const size_t slots = (size_t)stream_waves() * 2 * group;
-    a.split_tokens = kTileTok;
-    a.max_splits = 0;
-    a.ws_acc = reinterpret_cast<float*>(workspace);
-    a.ws_ml = a.ws_acc + slots * kHeadDim;
-    a.sk_meta = reinterpret_cast<int*>(a.ws_ml + slots * 2);
-    a.seq_cost = kSeqCost;
-    a.first_pct = kFirstSharePct;
-    const dim3 block(kDecWaves * kWave);
-    // Residency depends on the launch's LDS (the per-sequence prefix): query it
-    // once per device for batches up to kStreamSmallBatch and once for larger.
-    const int lds_bucket = batch <= kStreamSmallBatch ? 0 : 1;
-    const size_t lds_bound = lds_bucket ? kStreamMaxLds : kStreamSmallLds;
-    const bool small = group <= 4;
-    switch (fmt) {
-      case MKV_DTYPE_FP8E4M3:
-        small ? launch_stream<MKV_DTYPE_FP8E4M3, true>(a, lds_bucket, lds_bound, lds, s)
-              : launch_stream<MKV_DTYPE_FP8E4M3, false>(a, lds_bucket, lds_bound, lds, s);
-        break;
-      case kKvFp8PerToken:
-        small ? launch_stream<kKvFp8PerToken, true>(a, lds_bucket, lds_bound, lds, s)
-              : launch_stream<kKvFp8PerToken, false>(a, lds_bucket, lds_bound, lds, s);
-        break;
-      case kKvI8PerToken:
-        small ? launch_stream<kKvI8PerToken, true>(a, lds_bucket, lds_bound, lds, s)
-              : launch_stream<kKvI8PerToken, false>(a, lds_bucket, lds_bound, lds, s);
-        break;
-      case MKV_DTYPE_BF16:
-        small ? launch_stream<MKV_DTYPE_BF16, true>(a, lds_bucket, lds_bound, lds, s)
-              : launch_stream<MKV_DTYPE_BF16, false>(a, lds_bucket, lds_bound, lds, s);
-        break;
-      default:
-        small ? launch_stream<MKV_DTYPE_F16, true>(a, lds_bucket, lds_bound, lds, s)
-              : launch_stream<MKV_DTYPE_F16, false>(a, lds_bucket, lds_bound, lds, s);
-        break;
-    }
-    const int64_t mitems = (int64_t)batch * num_heads;
-    hipLaunchKernelGGL(paged_decode_stream_merge_kernel,
-                       dim3((unsigned)((mitems + kDecWaves - 1) / kDecWaves)), dim3(kDecWaves * kWave), 0,
-                       s, a, (int)fp8);
-    return (int)hipGetLastError();
-  }
-
-  const int st = resolve_split(split_tokens, batch, num_kv_heads, max_blocks, block_size);
-  a.split_tokens = st;
-  const int64_t max_len = (int64_t)max_blocks * block_size;
-  a.max_splits = max_len > 0 ? (int)((max_len + st - 1) / st) : 1;
-  a.ws_acc = nullptr;
-  a.ws_ml = nullptr;
-  if (a.max_splits > 1) {
-    const size_t need = (size_t)batch * num_heads * a.max_splits * (head_dim + 2) * sizeof(float);
-    if (!workspace) return MKV_ERR_NULL_POINTER;
-    if (workspace_bytes < need) return MKV_ERR_WORKSPACE_TOO_SMALL;
-    if (reinterpret_cast<uintptr_t>(workspace) & 15u) return MKV_ERR_MISALIGNED;
-    a.ws_acc = reinterpret_cast<float*>(workspace);
-    a.ws_ml = a.ws_acc + (size_t)batch * num_heads * a.max_splits * head_dim;
-  }
-  const int64_t items = (int64_t)batch * num_kv_heads * a.max_splits;
-  const dim3 grid((unsigned)((items + kDecWaves - 1) / kDecWaves));
-  const dim3 block(kDecWaves * kWave);
-  switch (fmt) {
-    case MKV_DTYPE_FP8E4M3:
-      hipLaunchKernelGGL(paged_decode_mfma16_kernel<MKV_DTYPE_FP8E4M3>, grid, block, 0, s, a);
-      break;
-    case kKvFp8PerToken:
-      hipLaunchKernelGGL(paged_decode_mfma16_2w_kernel<kKvFp8PerToken>, grid, block, 0, s, a);
-      break;
-    case kKvI8PerToken:
-      hipLaunchKernelGGL(paged_decode_mfma16_2w_kernel<kKvI8PerToken>, grid, block, 0, s, a);
-      break;
-    case MKV_DTYPE_BF16:
-      hipLaunchKernelGGL(paged_decode_mfma16_kernel<MKV_DTYPE_BF16>, grid, block, 0, s, a);
-      break;
-    case MKV_DTYPE_F16:
-      hipLaunchKernelGGL(paged_decode_mfma16_kernel<MKV_DTYPE_F16>, grid, block, 0, s, a);
-      break;
-    default:
-      hipLaunchKernelGGL(paged_decode_mfma32_kernel, grid, block, 0, s, a);
-      break;
-  }
-  if (a.max_splits > 1) {
-    const int64_t mitems = (int64_t)batch * num_heads;
-    hipLaunchKernelGGL(paged_decode_merge_kernel, dim3((unsigned)((mitems + kDecWaves - 1) / kDecWaves)),
-                       block, 0, s, a, (int)fp8);
-  }
-  return (int)hipGetLastError();
+  return ks.pair ? launch_route<true>(a, route, fmt, split_tokens, max_blocks, block_size, workspace,
+                                      workspace_bytes, s)
+                 : launch_route<false>(a, route, fmt, split_tokens, max_blocks, block_size, workspace,
+                                       workspace_bytes, s);
 }
 
 }  // namespace
@@ -2248,7 +2341,7 @@ extern "C" int mkv_paged_decode(void* out, int64_t out_batch_stride, const void*
   return paged_decode_impl(out, out_batch_stride, q, q_batch_stride, q_dtype, k_cache, v_cache, kv_dtype,
                            num_blocks, k_scale, v_scale, kv_scale_mode, block_tables, bt_stride, max_blocks,
                            context_lens, context_lens_dtype, batch, num_heads, num_kv_heads, head_dim,
-                           block_size, sm_scale, split_tokens, workspace, workspace_bytes, stream);
+                           block_size, sm_scale, split_tokens, workspace, workspace_bytes, stream, false);
 }
 
 extern "C" int mkv_paged_decode_noalloc(void* out, int64_t out_batch_stride, const void* q,
@@ -2259,16 +2352,20 @@ extern "C" int mkv_paged_decode_noalloc(void* out, int64_t out_batch_stride, con
                                         const void* context_lens, int context_lens_dtype, int batch,
                                         int num_heads, int num_kv_heads, int head_dim, int block_size,
                                         float sm_scale, int split_tokens, void* stream) {
-  if (batch > 0 && num_heads > 0 && num_kv_heads > 0 && max_blocks > 0 && block_size > 0 &&
-      num_heads % num_kv_heads == 0 && split_tokens >= 0 &&
-      decode_ws_bytes(batch, num_heads, num_kv_heads, max_blocks, block_size, kv_dtype, split_tokens) >
-          kScratchBytes)
-    return MKV_ERR_SCRATCH_LIMIT;
+  // An explicit route whose partials do not fit is refused on the host,
+  // before the device is touched (the library's choice falls back instead).
+  KernelShape ks;
+  if (split_tokens != 0 && batch > 0 && max_blocks > 0 && block_size > 0 &&
+      kernel_shape(num_heads, num_kv_heads, head_dim, ks) == MKV_OK) {
+    const int route = choose_route(split_tokens, kv_dtype, batch, ks, max_blocks, block_size, device_cus());
+    if (route_ws_bytes(route, batch, num_heads, ks, max_blocks, block_size, split_tokens) > kScratchBytes)
+      return MKV_ERR_SCRATCH_LIMIT;
+  }
   void* ws = nullptr;
   const int st = scratch_address(&ws);
   if (st != MKV_OK) return st;
   return paged_decode_impl(out, out_batch_stride, q, q_batch_stride, q_dtype, k_cache, v_cache, kv_dtype,
                            num_blocks, k_scale, v_scale, kv_scale_mode, block_tables, bt_stride, max_blocks,
                            context_lens, context_lens_dtype, batch, num_heads, num_kv_heads, head_dim,
-                           block_size, sm_scale, split_tokens, ws, kScratchBytes, stream);
+                           block_size, sm_scale, split_tokens, ws, kScratchBytes, stream, true);
 }

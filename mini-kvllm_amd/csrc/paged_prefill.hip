@@ -42,9 +42,12 @@ constexpr int kRowsPerWg = kPfWaves * kRowTiles * 16;  // 128
 static_assert(kRowsPerWg == 2 * kWave, "the row visibility reduction assumes the rows fill waves 0 and 1");
 constexpr int kBN = 64;                            // keys per LDS tile
 // static LDS: 4 tiles of 64 keys x 256 bytes (K and V, double-buffered);
-// dynamic LDS: row visibility [128] + 4 ints, per-token scales [2][128],
-// then the inline tile list (8-aligned)
-constexpr int kTileListOffset = (128 + 4) * 4 + 2 * 128 * 4;
+// dynamic LDS: row visibility [128] + 4 ints, per-token scales [2][256]
+// (per tile buffer: K then V scales of the tile's 64 keys, and with head
+// pairing the same for the pair's second KV head), then the inline tile
+// list (8-aligned)
+constexpr int kScPerBuf = 256;
+constexpr int kTileListOffset = (128 + 4) * 4 + 2 * kScPerBuf * 4;
 static_assert(kTileListOffset % 8 == 0, "TilePick holds 64-bit fields");
 constexpr int kXcds = 8;
 constexpr float kNegBig = -1e30f;
@@ -80,6 +83,8 @@ struct PrefillArgs {
   const int32_t* order; // [num_seqs]: sequence visited at position k
   int inline_list;      // num_seqs <= kInlineSeqs: each workgroup builds the list in LDS
   int64_t tiles_ub;     // upper bound of tiles per KV head (grid rows)
+  int scale_heads;      // KV heads of the per-token-head scale tensors (the caller's Hkv)
+  int pair;             // head_dim 64: KV heads read in pairs (kQDim in mkv_device.hpp)
 };
 
 // ---------------------------------------------------------------------------
@@ -534,7 +539,7 @@ struct LdsTile {
 // QSPLIT (bf16 caches with an fp32 / fp16 q only): bf16 holds such a q to 8
 // bits, so q is split into bf16 hi + lo terms and each QK step takes a second
 // MFMA, giving ~16 significant bits like the fp32 reference.
-template <int KV_DT, bool PAGED, bool QSPLIT>
+template <int KV_DT, bool PAGED, bool QSPLIT, bool PAIR>
 __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4))) void prefill_mfma_kernel(PrefillArgs a) {
   using LT = LdsTile<KV_DT>;
   // CT: the element type of the LDS tiles and the MFMA operands (fp16 for
@@ -561,7 +566,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   int* red_lds = vis_lds + kRowsPerWg;                             // [2]
   // per-token-head scales of the staged tiles: [buffer][K keys 0..63, V keys 0..63]
   float* sc_lds = reinterpret_cast<float*>(red_lds + 4);
-  static_assert(kTileListOffset == (kRowsPerWg + 4) * 4 + 2 * 128 * 4, "LDS layout");
+  static_assert(kTileListOffset == (kRowsPerWg + 4) * 4 + 2 * kScPerBuf * 4, "LDS layout");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -624,12 +629,16 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   for (int rt = 0; rt < kRowTiles; ++rt) {
     const int row = (kRowTiles * wave + rt) * 16 + c;
     const int64_t tok = q0 + row / G;
+    int d0 = 32 * kg;
     q_ok[rt] = row < a.tok_per_wg * G && tok < q1;
+    if constexpr (PAIR) q_ok[rt] = q_ok[rt] && q_slice<PAIR>(G, row % G, kg, d0);
     if (q_ok[rt]) {
       const int hq = kvh * G + row % G;
-      q32_issue(a.q, a.q_dtype, (tok * a.num_heads + hq) * kHeadDim + 32 * kg, qraw[rt]);
+      q32_issue(a.q, a.q_dtype, (tok * a.num_heads + hq) * kQDim<PAIR> + d0, qraw[rt]);
     }
   }
+  // head pairing: this lane's row belongs to the pair's second KV head
+  const bool row_hi = PAIR && (kRowTiles * wave * 16 + c) % G >= (G >> 1);
   if constexpr (QSPLIT) convert_q();
   wg_rows<PAGED>(a, vis_lds, red_lds, wk);
   const int min_vis = wk.min_vis, max_vis = wk.max_vis;
@@ -725,7 +734,9 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       st.phys = ok ? e : -1;
       // (the pool holds at most 2^32 token slots)
       st.row = ((uint32_t)e << a.idx.bs_log2) + (uint32_t)(t0 & (int)bmask);
-      st.sidx = (int64_t)((uint64_t)(st.row + (uint32_t)(lane & 15)) * (uint64_t)a.num_kv_heads) + kvh;
+      // (head pairing: threads 128-255 load the scales of the pair's second KV head)
+      st.sidx = (int64_t)((uint64_t)(st.row + (uint32_t)(lane & 15)) * (uint64_t)a.scale_heads) +
+                (PAIR ? 2 * kvh + ((tid >> 7) & 1) : kvh);
       const uint64_t b = __builtin_amdgcn_ballot_w64(ok);  // bits 16j: sub-tile j
       st.present = (uint32_t)((b & 1u) | ((b >> 15) & 2u) | ((b >> 30) & 4u) | ((b >> 45) & 8u));
     } else {
@@ -777,15 +788,18 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     }
   };
   u32x4 stg[kLoads];
-  // Per-token-head scales of a tile: lane tid < 128 loads the K (tid < 64) or
-  // V scale of key tid % 64 (0 for keys past max_vis or in absent blocks;
-  // every lane loads, the others from index 0, so the load is unconditional).
+  // Per-token-head scales of a tile: lane tid < 128 loads the K (tid % 128 <
+  // 64) or V scale of key tid % 64, and with head pairing lanes 128-255 the
+  // same for the pair's second KV head (0 for keys past max_vis or in absent
+  // blocks; every lane loads, the others from index 0, so the load is
+  // unconditional).
+  constexpr int kScLoads = PAIR ? 256 : 128;
   float stg_sc = 0.0f;
   auto load_scales = [&](int kb, const SubTiles& st) {
     if constexpr (kTokScale && PAGED) {
       // lane tid % 64 holds key kb + tid % 64 (sub-tile (tid % 64) / 16)
-      const bool valid = tid < 128 && st.phys >= 0 && kb + (tid & 63) < max_vis;
-      const float* base = tid >= 64 ? a.v_scale : a.k_scale;
+      const bool valid = tid < kScLoads && st.phys >= 0 && kb + (tid & 63) < max_vis;
+      const float* base = (PAIR ? (tid & 64) != 0 : tid >= 64) ? a.v_scale : a.k_scale;
       const float x = base[valid ? st.sidx : 0];
       stg_sc = valid ? x : 0.0f;
     }
@@ -835,7 +849,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       }
     }
     if constexpr (kTokScale)
-      if (tid < 128) sc_lds[buf * 128 + tid] = stg_sc;
+      if (tid < kScLoads) sc_lds[buf * kScPerBuf + tid] = stg_sc;
   };
 
   // Transposed V reads.  ds_read_b64_tr_b16: within each 16-lane group, lane
@@ -1004,7 +1018,8 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     if constexpr (kTokScale) {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        const f32x4 ksc = *reinterpret_cast<const f32x4*>(sc_lds + buf * 128 + 16 * kt + 4 * kg);
+        const f32x4 ksc =
+            *reinterpret_cast<const f32x4*>(sc_lds + buf * kScPerBuf + (row_hi ? 128 : 0) + 16 * kt + 4 * kg);
 #pragma unroll
         for (int rt = 0; rt < kRowTiles; ++rt)
 #pragma unroll
@@ -1074,7 +1089,8 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
         // per-token-head V scales of keys 16kt + 4kg + r, folded into P
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
-          const f32x4 vs = *reinterpret_cast<const f32x4*>(sc_lds + buf * 128 + 64 + 16 * kt + 4 * kg);
+          const f32x4 vs = *reinterpret_cast<const f32x4*>(sc_lds + buf * kScPerBuf + (row_hi ? 128 : 0) + 64 +
+                                                           16 * kt + 4 * kg);
 #pragma unroll
           for (int r = 0; r < 4; ++r) p[kt][rt][r] *= vs[r];
         }
@@ -1237,9 +1253,10 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       const int rq = (int)(((uint32_t)row * gm) >> 16);
       const int64_t tok = q0 + rq;
       const u32x4 d = *reinterpret_cast<const u32x4*>(stage + rr * kStageRow + 16 * ch);
-      if (row < a.tok_per_wg * G && tok < q1) {
+      int col0;
+      if (row < a.tok_per_wg * G && tok < q1 && out_cols<PAIR>(G, row - rq * G, ch, col0)) {
         const int hq = kvh * G + (row - rq * G);
-        st16(reinterpret_cast<uint16_t*>(a.out) + (tok * a.num_heads + hq) * kHeadDim + 8 * ch, d);
+        st16(reinterpret_cast<uint16_t*>(a.out) + (tok * a.num_heads + hq) * kQDim<PAIR> + col0, d);
       }
     }
     return;
@@ -1264,10 +1281,13 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       const int64_t tok = q0 + row / G;
       if (row >= a.tok_per_wg * G || tok >= q1) continue;
       const int hq = kvh * G + row % G;
-      // lane c holds dims 16mm + c
-      const int64_t o = (tok * a.num_heads + hq) * kHeadDim + c;
+      // lane c holds dims 16mm + c (head pairing: a row keeps dims 64 hi ..
+      // 64 hi + 63, i.e. mm = 4 hi .. 4 hi + 3)
+      const bool hi = PAIR && row % G >= (G >> 1);
+      const int64_t o = (tok * a.num_heads + hq) * kQDim<PAIR> + c - (hi ? 64 : 0);
 #pragma unroll
-      for (int mm = 0; mm < 8; ++mm) reinterpret_cast<float*>(a.out)[o + 16 * mm] = acc[rt][mm][r] * inv_r[r];
+      for (int mm = 0; mm < 8; ++mm)
+        if (!PAIR || (mm >= 4) == hi) reinterpret_cast<float*>(a.out)[o + 16 * mm] = acc[rt][mm][r] * inv_r[r];
     }
   }
 }
@@ -1302,7 +1322,7 @@ constexpr int kBN32 = 32;
 constexpr int kRowBytes32 = kHeadDim * 4;          // 512
 constexpr int kTileBytes32 = kBN32 * kRowBytes32;  // 16 KB per K or V tile
 
-template <bool PAGED>
+template <bool PAGED, bool PAIR>
 __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4))) void prefill_f32_kernel(PrefillArgs a) {
   extern __shared__ __align__(16) char smem[];
   __shared__ __align__(16) char lds_k0[kTileBytes32], lds_v0[kTileBytes32], lds_k1[kTileBytes32],
@@ -1326,9 +1346,12 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   float qf[32];
   {
     const int64_t tok = q0 + my_row / G;
-    if (my_row < a.tok_per_wg * G && tok < q1) {
+    int d0 = 32 * kg;
+    bool ok = my_row < a.tok_per_wg * G && tok < q1;
+    if constexpr (PAIR) ok = ok && q_slice<PAIR>(G, my_row % G, kg, d0);
+    if (ok) {
       const int hq = kvh * G + my_row % G;
-      const int64_t off = (tok * a.num_heads + hq) * kHeadDim + 32 * kg;
+      const int64_t off = (tok * a.num_heads + hq) * kQDim<PAIR> + d0;
       load_q32(a.q, a.q_dtype, off, qf);
     } else {
 #pragma unroll
@@ -1509,11 +1532,16 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       lo[mm] = acc[mm][r] * inv;
       hi[mm] = acc[4 + mm][r] * inv;
     }
-    const int64_t o = (tok * a.num_heads + hq) * kHeadDim;
+    const int64_t o = (tok * a.num_heads + hq) * kQDim<PAIR>;
+    // head pairing: a row of the pair's first KV head keeps dims 0-63 (lo),
+    // one of its second dims 64-127 (hi), stored at the row's dims 0-63
+    const bool row_hi = PAIR && row % G >= (G >> 1);
+    const bool keep_lo = !PAIR || !row_hi, keep_hi = !PAIR || row_hi;
+    const int hi_off = PAIR ? 0 : 64;
     if (a.q_dtype == MKV_DTYPE_F32) {
       float* po = reinterpret_cast<float*>(a.out) + o;
-      *reinterpret_cast<f32x4*>(po + 4 * c) = f32x4{lo[0], lo[1], lo[2], lo[3]};
-      *reinterpret_cast<f32x4*>(po + 64 + 4 * c) = f32x4{hi[0], hi[1], hi[2], hi[3]};
+      if (keep_lo) *reinterpret_cast<f32x4*>(po + 4 * c) = f32x4{lo[0], lo[1], lo[2], lo[3]};
+      if (keep_hi) *reinterpret_cast<f32x4*>(po + hi_off + 4 * c) = f32x4{hi[0], hi[1], hi[2], hi[3]};
     } else {
       const bool bf = a.q_dtype == MKV_DTYPE_BF16;
       auto pack = [&](float x, float y) -> uint32_t {
@@ -1523,8 +1551,9 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       };
       uint16_t* po = reinterpret_cast<uint16_t*>(a.out) + o;
       typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-      *reinterpret_cast<u32x2*>(po + 4 * c) = u32x2{pack(lo[0], lo[1]), pack(lo[2], lo[3])};
-      *reinterpret_cast<u32x2*>(po + 64 + 4 * c) = u32x2{pack(hi[0], hi[1]), pack(hi[2], hi[3])};
+      if (keep_lo) *reinterpret_cast<u32x2*>(po + 4 * c) = u32x2{pack(lo[0], lo[1]), pack(lo[2], lo[3])};
+      if (keep_hi)
+        *reinterpret_cast<u32x2*>(po + hi_off + 4 * c) = u32x2{pack(hi[0], hi[1]), pack(hi[2], hi[3])};
     }
   }
 }
@@ -1545,12 +1574,15 @@ int64_t tiles_upper_bound(int num_seqs, int64_t total_q, int group) {
 
 template <int KV_DT, bool PAGED, bool QSPLIT>
 int launch_prefill(const PrefillArgs& a, hipStream_t s) {
-  using LT = LdsTile<KV_DT>;
   const size_t lds = kTileListOffset + (a.inline_list ? sizeof(TilePick) : 0);
   int64_t nwg = a.tiles_ub * a.num_kv_heads;
   nwg = ((nwg + kXcds - 1) / kXcds) * kXcds;
-  hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED, QSPLIT>), dim3((unsigned)nwg), dim3(kPfThreads), lds,
-                     s, a);
+  if (a.pair)
+    hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED, QSPLIT, true>), dim3((unsigned)nwg), dim3(kPfThreads),
+                       lds, s, a);
+  else
+    hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED, QSPLIT, false>), dim3((unsigned)nwg), dim3(kPfThreads),
+                       lds, s, a);
   return (int)hipGetLastError();
 }
 
@@ -1559,7 +1591,10 @@ int launch_prefill_f32(const PrefillArgs& a, hipStream_t s) {
   const size_t lds = kTileListOffset + (a.inline_list ? sizeof(TilePick) : 0);
   int64_t nwg = a.tiles_ub * a.num_kv_heads;
   nwg = ((nwg + kXcds - 1) / kXcds) * kXcds;
-  hipLaunchKernelGGL((prefill_f32_kernel<PAGED>), dim3((unsigned)nwg), dim3(kPfThreads), lds, s, a);
+  if (a.pair)
+    hipLaunchKernelGGL((prefill_f32_kernel<PAGED, true>), dim3((unsigned)nwg), dim3(kPfThreads), lds, s, a);
+  else
+    hipLaunchKernelGGL((prefill_f32_kernel<PAGED, false>), dim3((unsigned)nwg), dim3(kPfThreads), lds, s, a);
   return (int)hipGetLastError();
 }
 
@@ -1585,13 +1620,22 @@ extern "C" size_t mkv_flash_prefill_workspace_size(int num_seqs, int64_t total, 
 
 namespace {
 
+// Shape checks shared by both entry points; fills the kernel's view of the
+// heads (head_dim 64: KV heads read in pairs, kQDim in mkv_device.hpp).
 int check_common(int num_seqs, int64_t total_q, int num_heads, int num_kv_heads, int head_dim,
-                 int q_dtype, int kv_dtype) {
+                 int q_dtype, int kv_dtype, PrefillArgs& a) {
   if (num_seqs < 0 || total_q < 0 || num_heads <= 0 || num_kv_heads <= 0) return MKV_ERR_BAD_SHAPE;
-  if (head_dim != kHeadDim) return MKV_ERR_UNSUPPORTED_HEAD_DIM;
+  if (head_dim != kHeadDim && head_dim != kHeadDim / 2) return MKV_ERR_UNSUPPORTED_HEAD_DIM;
   if (num_heads % num_kv_heads) return MKV_ERR_UNSUPPORTED_GROUP;
   const int g = num_heads / num_kv_heads;
-  if (g < 1 || g > 16) return MKV_ERR_UNSUPPORTED_GROUP;
+  const bool pair = head_dim == kHeadDim / 2;
+  if (pair && (num_kv_heads & 1)) return MKV_ERR_UNSUPPORTED_HEAD_DIM;
+  if (g < 1 || g > (pair ? 8 : 16)) return MKV_ERR_UNSUPPORTED_GROUP;
+  a.num_heads = num_heads;
+  a.num_kv_heads = pair ? num_kv_heads / 2 : num_kv_heads;
+  a.group = pair ? 2 * g : g;
+  a.scale_heads = num_kv_heads;
+  a.pair = pair ? 1 : 0;
   if (q_dtype != MKV_DTYPE_F32 && q_dtype != MKV_DTYPE_BF16 && q_dtype != MKV_DTYPE_F16)
     return MKV_ERR_UNSUPPORTED_DTYPE;
   if (kv_dtype != MKV_DTYPE_F32 && kv_dtype != MKV_DTYPE_BF16 && kv_dtype != MKV_DTYPE_F16 &&
@@ -1646,7 +1690,8 @@ extern "C" int mkv_paged_prefill(void* out, const void* q, int q_dtype, const vo
                                  int num_seqs, int64_t total_q, int num_heads, int num_kv_heads,
                                  int head_dim, int block_size, float sm_scale, void* workspace,
                                  size_t workspace_bytes, void* stream) {
-  int st = check_common(num_seqs, total_q, num_heads, num_kv_heads, head_dim, q_dtype, kv_dtype);
+  PrefillArgs a{};
+  int st = check_common(num_seqs, total_q, num_heads, num_kv_heads, head_dim, q_dtype, kv_dtype, a);
   if (st) return st;
   if (num_seqs == 0 || total_q == 0) return MKV_OK;
   if (!out || !q || !k_cache || !v_cache || !block_tables || !context_lens || !cu_seqlens_q ||
@@ -1671,7 +1716,6 @@ extern "C" int mkv_paged_prefill(void* out, const void* q, int q_dtype, const vo
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u)
     return MKV_ERR_MISALIGNED;
-  PrefillArgs a{};
   a.out = out;
   a.q = q;
   a.q_dtype = q_dtype;
@@ -1691,9 +1735,6 @@ extern "C" int mkv_paged_prefill(void* out, const void* q, int q_dtype, const vo
   a.positions = positions;
   a.num_seqs = num_seqs;
   a.total_q = total_q;
-  a.num_heads = num_heads;
-  a.num_kv_heads = num_kv_heads;
-  a.group = num_heads / num_kv_heads;
   a.sm_scale = sm_scale;
   return dispatch_prefill<true>(a, fmt, workspace, workspace_bytes,
                                 reinterpret_cast<hipStream_t>(stream));
@@ -1703,14 +1744,14 @@ extern "C" int mkv_flash_prefill(void* out, const void* q, const void* k, const 
                                  const int32_t* cu_seqlens, int num_seqs, int64_t total,
                                  int num_heads, int num_kv_heads, int head_dim, float sm_scale,
                                  void* workspace, size_t workspace_bytes, void* stream) {
-  int st = check_common(num_seqs, total, num_heads, num_kv_heads, head_dim, dtype, dtype);
+  PrefillArgs a{};
+  int st = check_common(num_seqs, total, num_heads, num_kv_heads, head_dim, dtype, dtype, a);
   if (st) return st;
   if (num_seqs == 0 || total == 0) return MKV_OK;
   if (!out || !q || !k || !v || !cu_seqlens) return MKV_ERR_NULL_POINTER;
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u)
     return MKV_ERR_MISALIGNED;
-  PrefillArgs a{};
   a.out = out;
   a.q = q;
   a.q_dtype = dtype;
@@ -1719,9 +1760,6 @@ extern "C" int mkv_flash_prefill(void* out, const void* q, const void* k, const 
   a.cu_seqlens_q = cu_seqlens;
   a.num_seqs = num_seqs;
   a.total_q = total;
-  a.num_heads = num_heads;
-  a.num_kv_heads = num_kv_heads;
-  a.group = num_heads / num_kv_heads;
   a.sm_scale = sm_scale;
   return dispatch_prefill<false>(a, dtype, workspace, workspace_bytes,
                                  reinterpret_cast<hipStream_t>(stream));

@@ -15,7 +15,7 @@ with the reference engine's Python call signatures:
 * :class:`Attention` and :mod:`mkv.context` — the layer and per-step
   metadata the runner drives.
 """
-from .attention import (DECODE_WORKGROUP, FP8_E4M3_MAX, Attention, calibrate_fp8_per_tensor,
+from .attention import (DECODE_STREAM, DECODE_WORKGROUP, FP8_E4M3_MAX, Attention, calibrate_fp8_per_tensor,
                         flash_attention_prefill, gather_kv, paged_attention_decode,
                         paged_attention_decode_quantized, paged_attention_prefill_triton,
                         store_kvcache, store_kvcache_fp8, store_kvcache_int8)
@@ -23,7 +23,7 @@ from .context import (Context, MixedAttentionSplit, current_context, get_context
                       set_context, split_mixed_decode_prefill_metadata, use_context_provider)
 
 __all__ = [
-    "DECODE_WORKGROUP", "FP8_E4M3_MAX", "Attention", "Context", "MixedAttentionSplit", "calibrate_fp8_per_tensor",
+    "DECODE_STREAM", "DECODE_WORKGROUP", "FP8_E4M3_MAX", "Attention", "Context", "MixedAttentionSplit", "calibrate_fp8_per_tensor",
     "flash_attention_prefill", "gather_kv", "get_context", "paged_attention_decode",
     "paged_attention_decode_quantized", "paged_attention_prefill_triton", "reset_context",
     "set_context", "split_mixed_decode_prefill_metadata", "store_kvcache", "store_kvcache_fp8",

@@ -14,7 +14,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmkv.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -28,6 +28,11 @@ NOALLOC_SCRATCH_BYTES = 32 << 20  # MKV_NOALLOC_SCRATCH_BYTES
 INDEX_I32 = 0
 INDEX_I64 = 1
 DECODE_WORKGROUP = -1  # MKV_DECODE_WORKGROUP: split_tokens value of the workgroup route
+DECODE_STREAM = -2  # MKV_DECODE_STREAM: split_tokens value of the stream-K route
+# mkv_paged_decode_route results
+ROUTE_STREAM = 0
+ROUTE_SPLIT = 1
+ROUTE_WORKGROUP = 2
 
 # name -> (restype, argtypes); mirrors include/mkv.h one to one.
 SIGNATURES: dict[str, tuple] = {
@@ -45,6 +50,7 @@ SIGNATURES: dict[str, tuple] = {
         c_void_p, c_void_p]),
     "mkv_paged_decode_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
     "mkv_paged_decode_split_tokens": (c_int, [c_int, c_int, c_int, c_int, c_int]),
+    "mkv_paged_decode_route": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
     "mkv_paged_decode": (c_int, [
         c_void_p, c_int64, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_int, c_int64,
         c_void_p, c_void_p, c_int, c_void_p, c_int64, c_int, c_void_p, c_int, c_int, c_int, c_int,

@@ -35,6 +35,7 @@ from . import _lib
 from .context import current_context
 
 DECODE_WORKGROUP = _lib.DECODE_WORKGROUP
+DECODE_STREAM = _lib.DECODE_STREAM
 
 FP8_E4M3_MAX = 448.0
 INT8_MAX = 127.0
@@ -390,10 +391,14 @@ def paged_attention_decode(query: torch.Tensor, k_cache: torch.Tensor, v_cache: 
     """Decode attention over the paged cache: query (batch, num_heads,
     head_dim) -> output of the same shape and dtype.  Reference:
     attention.py:895-950.  Rows with context_lens == 0 yield zeros.
+    head_dim 128, or 64 with an even num_kv_heads (the Llama-3.2-1B shape).
     split_tokens (an addition; 0 by default) selects the schedule:
-    0 = stream-K over the whole batch, n > 0 = split-K in n-token splits,
-    DECODE_WORKGROUP (-1) = one workgroup per (sequence, KV head) whose
-    waves split the sequence and merge in LDS (one launch, no workspace)."""
+    0 = the library's choice from the shape (the workgroup route when the
+    (sequence, KV head) items fill the GPU's CUs with at least 4 waves each,
+    else stream-K, else split-K); DECODE_STREAM (-2) = stream-K over the
+    whole batch; n > 0 = split-K in n-token splits; DECODE_WORKGROUP (-1) =
+    one workgroup per (sequence, KV head) whose waves split the sequence and
+    merge in LDS (one launch, no workspace)."""
     return _decode(query, k_cache, v_cache, block_tables, context_lens, scale, num_heads,
                    num_kv_heads, head_dim, split_tokens=split_tokens)
 
@@ -589,9 +594,9 @@ class Attention(nn.Module):
         # first and fills in around them, with no gathers and no second
         # launch.
         self.mixed_batch = "unified"
-        # decode schedule (0: stream-K, the default; n > 0: n-token split-K;
-        # DECODE_WORKGROUP: one workgroup per sequence and KV head, fastest for
-        # batches of a few dozen short contexts, e.g. 60 rows of 300-800 tokens)
+        # decode schedule: 0 = the library's choice (the default), or an
+        # explicit one (DECODE_STREAM, n > 0 for n-token split-K,
+        # DECODE_WORKGROUP), as for paged_attention_decode
         self.decode_split_tokens = 0
 
     def _mode(self) -> str:

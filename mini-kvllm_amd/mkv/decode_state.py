@@ -17,9 +17,10 @@ lengths and derives ``context_lens`` and ``slot_mapping`` for the step, so a
 steady decode step sends nothing from the host.  The host writes a table row
 when a sequence joins and one entry when it gets a new block.
 :class:`DecodeGraphs` captures a user step function (metadata advance +
-the layers' append/decode) once per batch bucket over these buffers and
-replays the smallest bucket that holds the batch; captures run with every row
-inactive, so they write no K/V and leave the state untouched.
+the layers' append/decode) once per batch bucket and block-table width over
+these buffers and replays the smallest bucket and narrowest width that hold
+the batch; captures run with every row inactive, so they write no K/V and
+leave the state untouched.
 """
 from __future__ import annotations
 
@@ -97,35 +98,46 @@ class DecodeMetadata:
         self.clear_row(src)
 
     # -- per step (device only, capturable) ---------------------------------
-    def step(self, rows: int, increment: int = 1):
+    def step(self, rows: int, increment: int = 1, width: int | None = None):
         """Advance the active rows among the first ``rows`` by ``increment``
         tokens and derive the step's metadata (one kernel, no host sync).
         Returns (slot_mapping, context_lens, block_tables) views of ``rows``
-        rows."""
+        rows; the block-table view has ``width`` columns (default: all
+        ``max_blocks``), which must cover every active row's blocks, as the
+        reference pads each decode step's tables to its longest sequence
+        (model_runner.py:640-644)."""
         if not 0 <= rows <= self.max_rows:
             raise ValueError(f"rows {rows} outside 0..{self.max_rows}")
+        width = self.max_blocks if width is None else width
+        if not 1 <= width <= self.max_blocks:
+            raise ValueError(f"width {width} outside 1..{self.max_blocks}")
         _lib.call("mkv_decode_metadata", self.seq_lens.data_ptr(), self.context_lens.data_ptr(),
                   self.slot_mapping.data_ptr(), self.block_tables.data_ptr(),
                   self.block_tables.stride(0), self.max_blocks, self.num_blocks, self.block_size,
                   rows, increment, _stream(self.device))
-        return (self.slot_mapping[:rows], self.context_lens[:rows], self.block_tables[:rows])
+        return (self.slot_mapping[:rows], self.context_lens[:rows], self.block_tables[:rows, :width])
 
 
 class DecodeGraphs:
-    """Decode steps captured per batch bucket over one :class:`DecodeMetadata`.
+    """Decode steps captured per (batch bucket, table width) over one
+    :class:`DecodeMetadata`.
 
     ``step_fn(rows, slot_mapping, context_lens, block_tables)`` runs one
     decode step's device work for ``rows`` rows (e.g. every layer's append
     and decode over persistent input/output buffers); it must not allocate
-    after its first call and must not synchronise.  Each bucket's graph holds
-    the metadata advance followed by ``step_fn``.  Buckets follow the
+    after its first call and must not synchronise.  Each graph holds the
+    metadata advance followed by ``step_fn``.  Batch buckets follow the
     reference (1, 2, 4, 8, then multiples of 16 up to max_rows,
-    model_runner.py:783), and ``run(batch)`` replays the smallest bucket that
-    holds ``batch`` (the reference picks it the same way, :689); rows past
-    ``batch`` must be inactive.
+    model_runner.py:783), and ``run(batch, blocks)`` replays the smallest
+    bucket that holds ``batch`` (the reference picks it the same way, :689)
+    with the narrowest of ``widths`` that holds ``blocks`` block-table
+    columns (default: one width, all ``max_blocks`` columns); rows past
+    ``batch`` must be inactive.  A (bucket, width) pair that ``capture``
+    left out is captured on its first ``run``.
     """
 
-    def __init__(self, meta: DecodeMetadata, step_fn: Callable, buckets: Iterable[int] | None = None):
+    def __init__(self, meta: DecodeMetadata, step_fn: Callable, buckets: Iterable[int] | None = None,
+                 widths: Iterable[int] | None = None):
         self.meta = meta
         self.step_fn = step_fn
         if buckets is None:
@@ -134,42 +146,53 @@ class DecodeGraphs:
         self.buckets = sorted(set(buckets))
         if not self.buckets or self.buckets[-1] > meta.max_rows:
             raise ValueError("buckets must be non-empty and <= max_rows")
-        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self.widths = sorted(set(widths)) if widths is not None else [meta.max_blocks]
+        if not self.widths or self.widths[0] < 1 or self.widths[-1] > meta.max_blocks:
+            raise ValueError("widths must be non-empty and in 1..max_blocks")
+        self.graphs: dict[tuple[int, int], torch.cuda.CUDAGraph] = {}
         self.pool = None
+        self.scales: list[torch.Tensor] = []
 
-    def capture(self, scales: Iterable[torch.Tensor] = ()) -> None:
-        """Capture one graph per bucket, largest first, sharing one memory
-        pool.  The state is saved, every row deactivated for the warm-up and
-        the capture (so no K/V is written anywhere), and then restored.
+    def capture(self, scales: Iterable[torch.Tensor] = (),
+                keys: Iterable[tuple[int, int]] | None = None) -> None:
+        """Capture one graph per (bucket, width) key (default: every bucket
+        at the widest width), largest first, sharing one memory pool.  The
+        state is saved, every row deactivated for the warm-up and the
+        capture (so no K/V is written anywhere), and then restored.
 
         ``scales``: the per-tensor FP8 scale tensors that ``step_fn``'s
-        appends use.  The warm-up runs the appends eagerly on the inactive
-        rows, and a scale that still holds the 1.0 "not yet calibrated"
-        sentinel would be calibrated there from those rows' dummy K/V and
-        then frozen (the reference's capture has the same hazard,
-        model_runner.py:769-794).  Their values and calibration flags are
-        saved before the warm-up and restored after the capture, so a scale
-        that held 1.0 is calibrated by the first real step (eager, or a
-        replay: the captured append keeps the sentinel test)."""
+        appends use (kept for the captures that ``run`` makes later).  The
+        warm-up runs the appends eagerly on the inactive rows, and a scale
+        that still holds the 1.0 "not yet calibrated" sentinel would be
+        calibrated there from those rows' dummy K/V and then frozen (the
+        reference's capture has the same hazard, model_runner.py:769-794).
+        Their values and calibration flags are saved before the warm-up and
+        restored after the capture, so a scale that held 1.0 is calibrated by
+        the first real step (eager, or a replay: the captured append keeps
+        the sentinel test)."""
         m = self.meta
         scales = list(scales)
-        saved_scales = [(s, s.clone(), getattr(s, "_mkv_calibrated", None)) for s in scales]
+        if scales:
+            self.scales = scales
+        keys = sorted(keys if keys is not None else [(b, self.widths[-1]) for b in self.buckets],
+                      reverse=True)
+        saved_scales = [(s, s.clone(), getattr(s, "_mkv_calibrated", None)) for s in self.scales]
         saved = (m.seq_lens.clone(), m.context_lens.clone(), m.slot_mapping.clone())
         m.seq_lens.zero_()
         side = torch.cuda.Stream(m.device)
         side.wait_stream(torch.cuda.current_stream(m.device))
         with torch.cuda.stream(side):
-            for rows in reversed(self.buckets):  # warm-up: workspaces allocated here
-                self.step_fn(rows, *m.step(rows, 0))
+            for rows, width in keys:  # warm-up: workspaces allocated here
+                self.step_fn(rows, *m.step(rows, 0, width))
         torch.cuda.current_stream(m.device).wait_stream(side)
         torch.cuda.synchronize(m.device)
-        for rows in reversed(self.buckets):
+        for rows, width in keys:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, self.pool):
-                self.step_fn(rows, *m.step(rows, 1))
+                self.step_fn(rows, *m.step(rows, 1, width))
             if self.pool is None:
                 self.pool = g.pool()
-            self.graphs[rows] = g
+            self.graphs[(rows, width)] = g
             torch.cuda.synchronize(m.device)
         m.seq_lens.copy_(saved[0])
         m.context_lens.copy_(saved[1])
@@ -189,10 +212,23 @@ class DecodeGraphs:
                 return b
         raise ValueError(f"batch {batch} exceeds the largest bucket {self.buckets[-1]}")
 
-    def run(self, batch: int) -> int:
-        """Replay one decode step for ``batch`` active rows; returns the
-        bucket replayed (rows of the step's outputs that are meaningful:
-        the first ``batch``)."""
-        rows = self.bucket(batch)
-        self.graphs[rows].replay()
-        return rows
+    def width(self, blocks: int | None = None) -> int:
+        """The narrowest table width that holds ``blocks`` columns (None: the
+        widest)."""
+        if blocks is None:
+            return self.widths[-1]
+        for w in self.widths:
+            if w >= blocks:
+                return w
+        raise ValueError(f"{blocks} blocks exceed the widest table width {self.widths[-1]}")
+
+    def run(self, batch: int, blocks: int | None = None) -> int:
+        """Replay one decode step for ``batch`` active rows whose block
+        tables hold at most ``blocks`` entries; returns the bucket replayed
+        (rows of the step's outputs that are meaningful: the first
+        ``batch``)."""
+        key = (self.bucket(batch), self.width(blocks))
+        if key not in self.graphs:
+            self.capture(keys=[key])
+        self.graphs[key].replay()
+        return key[0]

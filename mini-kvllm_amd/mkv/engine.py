@@ -37,7 +37,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from . import context as C
-from .attention import DECODE_WORKGROUP, Attention, _dtype_code, _stream
+from .attention import DECODE_STREAM, DECODE_WORKGROUP, Attention, _dtype_code, _stream
 from .decode_state import DecodeGraphs, DecodeMetadata
 from .producer import qkv_norm_rope_append
 
@@ -404,10 +404,11 @@ class StepStats:
 class Engine:
     """Generation over a :class:`Qwen3Model` with the scheduler above.
 
-    Decode-only steps replay a graph captured per batch bucket (the first
-    decode-only step captures them, after the prefills have calibrated the
-    FP8 scales); a step with any prompt chunk runs eagerly through the
-    paged-prefill path (a decode row is a one-token chunk there)."""
+    Decode-only steps replay a graph captured per batch bucket and table
+    width (each captured on its first use, after the prefills have
+    calibrated the FP8 scales); a step with any prompt chunk runs eagerly
+    through the paged-prefill path (a decode row is a one-token chunk
+    there)."""
 
     def __init__(self, model: Qwen3Model, num_blocks: int, max_num_seqs: int = 64,
                  max_num_batched_tokens: int = 1024, kv_cache_dtype: str = "fp8_per_tensor",
@@ -518,14 +519,21 @@ class Engine:
                                           dtype=self.model.embed.dtype, device=self.dev)
         self._load_rows(reqs)
         if self.graphs is None:
-            self.graphs = DecodeGraphs(self.meta, self._decode_step_fn)
+            # decode tables as wide as the batch's longest sequence, rounded up
+            # to a power of two (the reference pads each decode step's tables to
+            # its longest sequence, model_runner.py:640-644); the decode
+            # kernels' schedule follows the width.  Graphs are captured per
+            # (batch bucket, width) on first use.
+            widths = sorted({min(1 << i, self.max_blocks) for i in range(self.max_blocks.bit_length() + 1)})
+            self.graphs = DecodeGraphs(self.meta, self._decode_step_fn, widths=widths)
             if self.use_graphs:
-                self.graphs.capture(scales=self.model.scales())
+                self.graphs.capture(scales=self.model.scales(), keys=[])
+        blocks = max(len(r.blocks) for r in reqs)
         if self.use_graphs:
-            self.graphs.run(n)
+            self.graphs.run(n, blocks)
         else:  # the same work eagerly, on the bucket's rows (the same GEMM shapes)
             rows = self.graphs.bucket(n)
-            self._decode_step_fn(rows, *self.meta.step(rows, 1))
+            self._decode_step_fn(rows, *self.meta.step(rows, 1, self.graphs.width(blocks)))
         self.last_logits = self.logits_buf[:n]
         tok = sample(self.logits_buf[:n], self.temp_buf[:n], self.gen)
         self.ids_buf[:n].copy_(tok)

@@ -57,3 +57,23 @@ def assert_close_out(got: torch.Tensor, want: torch.Tensor, out_dtype: torch.dty
     assert not bool(bad.any()), (
         f"{int(bad.sum())} of {err.numel()} elements out of tolerance; max abs err "
         f"{float(err.max()):.3e}, max excess {float((err - tol).max()):.3e} (abs_tol {abs_tol})")
+
+
+def compact_pool(k_cache, v_cache, block_tables, context_lens):
+    """The blocks that the given sequences use, gathered on the device and
+    copied to the host as a small pool, with their block tables renumbered
+    into it (absent entries stay -1): the float64 oracle then checks sampled
+    rows of a full-size workload without copying the whole pool."""
+    bs = k_cache.shape[1]
+    bt = block_tables.cpu().clone()
+    used = sorted({int(x) for s in range(bt.shape[0])
+                   for x in bt[s, :(int(context_lens[s]) + bs - 1) // bs] if int(x) >= 0})
+    remap = {p: i for i, p in enumerate(used)}
+    nb = bt.shape[1]
+    for s in range(bt.shape[0]):
+        need = (int(context_lens[s]) + bs - 1) // bs
+        for j in range(nb):
+            x = int(bt[s, j])
+            bt[s, j] = remap[x] if (j < need and x >= 0) else -1
+    idx = torch.tensor(used if used else [0], dtype=torch.int64, device=k_cache.device)
+    return k_cache.index_select(0, idx).cpu(), v_cache.index_select(0, idx).cpu(), bt

@@ -11,7 +11,7 @@ import math
 import pytest
 import torch
 
-from conftest import announce, assert_close_out
+from conftest import announce, assert_close_out, compact_pool
 from mkv import attention as A
 from mkv import workloads as W
 from oracle import reference as R
@@ -100,9 +100,10 @@ def _case(seed, B, Hq, Hkv, bs, N, max_blocks, dtype, ctx=None):
 
 
 WG = A.DECODE_WORKGROUP
+SK = A.DECODE_STREAM
 
 
-@pytest.mark.parametrize("route", [0, WG])
+@pytest.mark.parametrize("route", [0, SK, WG])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn, torch.float32])
 @pytest.mark.parametrize("group", [1, 2, 4, 8, 16])
 def test_decode_group_sizes(dev, dtype, group, route):
@@ -198,6 +199,12 @@ def test_decode_batch256_full_size(dev, kv):
     got = A._decode(q, kc, vc, bt, ctx, 1 / math.sqrt(128), 32, 8, 128, ksd, vsd)
     want = _torch_gpu_reference(q, kc, vc, bt, ctx, 1 / math.sqrt(128), 32, 8, ks, vs)
     assert_close_out(got, want, got.dtype, 2e-2 if kv == "fp8" else 2e-3)
+    # 8 sampled sequences (shortest, longest and spread) against the float64 oracle
+    lens = m["context_lens"]
+    idx = torch.tensor(sorted({int(lens.argmin()), int(lens.argmax())} | set(range(5, 256, 43))))[:8]
+    kcs, vcs, bts = compact_pool(kc, vc, m["block_tables"][idx], lens[idx])
+    ref = R.paged_decode_ref(q[idx].cpu().double(), kcs, vcs, bts, lens[idx], 1 / math.sqrt(128), 32, 8, ks, vs)
+    assert_close_out(got[idx].cpu(), ref, got.dtype, 2e-2 if kv == "fp8" else 2e-3)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn, torch.float16])
@@ -211,7 +218,7 @@ def test_decode_stream_k_vs_split_k_and_empty_rows(dev, dtype):
     ctx[[0, 7, 8, 39]] = 0
     q, k, v, bt, ctx, ks, vs = _case(72, B, 16, 4, 64, 400, 16, dtype, ctx=ctx)
     want = _oracle(q, k, v, bt, ctx, 0.11, 16, 4, ks, vs)
-    sk = _run(dev, q, k, v, bt, ctx, 0.11, 16, 4, ks, vs)
+    sk = _run(dev, q, k, v, bt, ctx, 0.11, 16, 4, ks, vs, split_tokens=SK)
     sp = _run(dev, q, k, v, bt, ctx, 0.11, 16, 4, ks, vs, split_tokens=128)
     assert_close_out(sk, want, sk.dtype, TOL[dtype])
     assert_close_out(sp, want, sp.dtype, TOL[dtype])
@@ -230,7 +237,7 @@ def test_decode_stream_k_kv_head_counts(dev, dtype, Hkv):
     ctx[2] = 0
     q, k, v, bt, ctx, ks, vs = _case(94 + Hkv, 5, 2 * Hkv, Hkv, 128, 96, 16, dtype, ctx=ctx)
     want = _oracle(q, k, v, bt, ctx, 0.09, 2 * Hkv, Hkv, ks, vs)
-    got = _run(dev, q, k, v, bt, ctx, 0.09, 2 * Hkv, Hkv, ks, vs)
+    got = _run(dev, q, k, v, bt, ctx, 0.09, 2 * Hkv, Hkv, ks, vs, split_tokens=SK)
     assert_close_out(got, want, got.dtype, TOL[dtype])
 
 
@@ -244,7 +251,7 @@ def test_decode_stream_k_item_over_many_groups(dev, dtype):
     ctx = torch.tensor([6000, 300])
     q, k, v, bt, ctx, ks, vs = _case(91, 2, 32, 8, 256, 64, 24, dtype, ctx=ctx)
     want = _oracle(q, k, v, bt, ctx, 0.08, 32, 8, ks, vs)
-    got = _run(dev, q, k, v, bt, ctx, 0.08, 32, 8, ks, vs)
+    got = _run(dev, q, k, v, bt, ctx, 0.08, 32, 8, ks, vs, split_tokens=SK)
     assert_close_out(got, want, got.dtype, TOL[dtype])
 
 
@@ -260,7 +267,7 @@ def test_decode_stream_k_large_batches(dev, B, dtype):
     ctx = torch.randint(0, 70, (B,), generator=g)
     ctx[::37] = 0
     q, k, v, bt, ctx, ks, vs = _case(76 + B, B, 8, 2, 16, 3 * B, 5, dtype, ctx=ctx)
-    got = _run(dev, q, k, v, bt, ctx, 0.1, 8, 2, ks, vs)
+    got = _run(dev, q, k, v, bt, ctx, 0.1, 8, 2, ks, vs, split_tokens=SK)
     idx = torch.arange(0, B, 61)
     want = _oracle(q[idx], k, v, bt[idx], ctx[idx], 0.1, 8, 2, ks, vs)
     assert_close_out(got[idx], want, got.dtype, TOL[dtype])
@@ -291,7 +298,7 @@ def test_decode_q_dtype_differs_from_cache(dev, kv, qdt, group):
     q, k, v, bt, ctx, ks, vs = _case(81, 12, group * Hkv, Hkv, 16, 160, 12, kv)
     q = torch.randn(q.shape, generator=torch.Generator().manual_seed(82)).to(qdt)
     want = _oracle(q, k, v, bt, ctx, 0.09, group * Hkv, Hkv, ks, vs)
-    for st in (0, 64, WG):
+    for st in (0, SK, 64, WG):
         got = _run(dev, q, k, v, bt, ctx, 0.09, group * Hkv, Hkv, ks, vs, split_tokens=st)
         assert got.dtype == qdt
         assert_close_out(got, want, got.dtype, TOL[kv])
@@ -314,14 +321,49 @@ def test_decode_workgroup_route_small_batches(dev, dtype):
         got = _run(dev, q, k, v, bt, ctx, 0.088, Hq, 8, ks, vs, split_tokens=WG)
         assert_close_out(got, want, got.dtype, TOL[dtype])
         assert torch.count_nonzero(got[[1, B - 1]].float()) == 0
-        sk = _run(dev, q, k, v, bt, ctx, 0.088, Hq, 8, ks, vs)
+        sk = _run(dev, q, k, v, bt, ctx, 0.088, Hq, 8, ks, vs, split_tokens=SK)
         assert_close_out(got, sk.double(), got.dtype, TOL[dtype])
 
 
-def test_decode_workgroup_route_refusal(dev):
-    """A block table whose per-wave share would span more than 62 blocks is
-    refused before any launch."""
-    from mkv._lib import MkvError
-    q, k, v, bt, ctx, ks, vs = _case(10, 1, 8, 2, 16, 600, 600, torch.bfloat16)
-    with pytest.raises(MkvError):
-        _run(dev, q, k, v, bt, ctx, 0.1, 8, 2, split_tokens=WG)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn, torch.float32])
+def test_decode_long_block_spans_on_every_route(dev, dtype):
+    """Block-table entries are looked up tile by tile on every route, so a
+    wave's range may span any number of blocks: one sequence of up to 9600
+    tokens in 16-token blocks (600 blocks) through the workgroup route (one
+    wave spans ~75 blocks), split-K with 4096-token splits (256 blocks per
+    split), stream-K and the library's choice, each against the oracle."""
+    announce(f"decode {dtype} long block spans (600 blocks of 16) on every route")
+    g = torch.Generator().manual_seed(10)
+    ctx = torch.tensor([9600, 5000, 17])
+    q, k, v, bt, ctx, ks, vs = _case(10, 3, 8, 2, 16, 1300, 600, dtype, ctx=ctx)
+    bt[0, 300] = -1  # an absent block deep inside the long context
+    want = _oracle(q, k, v, bt, ctx, 0.1, 8, 2, ks, vs)
+    for st in (WG, 4096, SK, 0):
+        got = _run(dev, q, k, v, bt, ctx, 0.1, 8, 2, ks, vs, split_tokens=st)
+        assert_close_out(got, want, got.dtype, TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float8_e4m3fn, torch.bfloat16])
+def test_decode_default_route_block16_long_contexts(dev, dtype):
+    """60 sequences x 8 KV heads with 16-token blocks and contexts of
+    4000-5000 tokens (320-block tables) through the library's choice
+    (stream-K: a workgroup wave would take up to 1280 tokens) and through
+    the workgroup route, whose waves then span ~80 blocks each (the route
+    refused such tables before its block-table entries were looked up tile
+    by tile).  Checked on every 7th row."""
+    announce(f"decode {dtype} default route, batch 60, block 16, contexts 4000-5000")
+    from mkv import _lib
+    g = torch.Generator().manual_seed(4000)
+    B, mb, N = 60, 320, 400
+    # one 400-block pool; the tables share its blocks between sequences (reads only)
+    q, k, v, _, _, ks, vs = _case(4001, B, 16, 8, 16, N, 8, dtype)
+    ctx = torch.randint(4000, 5001, (B,), generator=g)
+    bt = torch.randint(0, N, (B, mb), generator=g, dtype=torch.int32)
+    dt = {torch.float8_e4m3fn: _lib.DTYPE_FP8E4M3, torch.bfloat16: _lib.DTYPE_BF16}[dtype]
+    route = _lib.query("mkv_paged_decode_route", B, 16, 8, mb, 16, 128, dt, 0, 0)
+    assert route == _lib.ROUTE_STREAM
+    idx = torch.arange(0, B, 7)
+    want = _oracle(q[idx], k, v, bt[idx], ctx[idx], 0.088, 16, 8, ks, vs)
+    for st in (0, WG):
+        got = _run(dev, q, k, v, bt, ctx, 0.088, 16, 8, ks, vs, split_tokens=st)
+        assert_close_out(got[idx], want, got.dtype, TOL[dtype])

@@ -130,3 +130,86 @@ def test_engine_logits_match_the_oracle_attention_engine(dev, monkeypatch, split
     assert eng.sched.done() and ref.sched.done()
     assert "mixed" in kinds and "decode" in kinds and compared >= 6, kinds
     print(f"max logit difference over {compared} steps: {worst:.2e}")
+
+
+# The end-to-end workload's model shape (Qwen3-0.6B: hidden 1024, 16 q / 8 kv
+# heads, head_dim 128, intermediate 3072, vocab 151936) with 2 of its 28
+# layers.
+FULL = E.ModelConfig(num_layers=2)
+
+
+def _full_engine(dev, model_cls, use_graphs, dtype):
+    model = model_cls(FULL, dev, dtype=dtype, seed=5, block_size=256)
+    return E.Engine(model, num_blocks=40, max_num_seqs=8, max_num_batched_tokens=1024,
+                    kv_cache_dtype="fp8_per_tensor", max_model_len=1024, seed=0, use_graphs=use_graphs)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_engine_logits_full_shape_match_the_oracle_attention_engine(dev, monkeypatch, dtype):
+    """The end-to-end workload's shape (Qwen3-0.6B attention and projections,
+    vocab 151936, 256-token blocks, FP8 per-tensor KV, a 1024-token step
+    budget with chunked prefill) on 2 layers and 8 prompts of 32-512 tokens:
+    every step's logits (mixed prefill steps, then captured decode steps
+    through the library's decode schedule) against the same engine with the
+    oracle's float64 attention over its own cache.
+
+    fp32 weights (the reference engine's default precision,
+    model_runner.py:87): only the attention arithmetic differs, within 3e-2.
+    bf16 weights (the end-to-end workload's): each attention output is one
+    bf16 rounding of the oracle's or of the kernel's value, and a one-ulp
+    difference there moves the hidden state by 2^-8 relative, which the
+    layers after it carry to the logits; the bound is 6e-2 plus one bf16
+    ulp of the logit (both engines round their logits to bf16), and the mean
+    difference at most 1e-2."""
+    announce(f"engine: full-shape (hidden 1024, 16/8 heads, vocab 151936, block 256), {dtype} weights, "
+             "logits vs oracle attention")
+    g = torch.Generator().manual_seed(55)
+    lens = [int(x) for x in torch.randint(32, 513, (8,), generator=g)]
+    lens[0], lens[1] = 512, 32
+    prompts = [torch.randint(0, FULL.vocab_size, (L,), generator=g).tolist() for L in lens]
+    eng = _full_engine(dev, E.Qwen3Model, True, dtype)
+    ref = _full_engine(dev, OracleAttentionModel, False, dtype)
+    for e in (eng, ref):
+        for p in prompts:
+            e.add_request(p, max_tokens=6)
+    forced = {}
+    real_sample = E.sample
+
+    def sample_forced(logits, temperature, gen):
+        if "tok" in forced:
+            return forced.pop("tok")
+        return real_sample(logits, temperature, gen)
+
+    monkeypatch.setattr(E, "sample", sample_forced)
+    kinds, worst, compared = [], 0.0, 0
+    for step in range(40):
+        if eng.sched.done():
+            break
+        eng.step()
+        kinds.append(eng.stats[-1].kind)
+        sampled = eng.last_sampled
+        if sampled:
+            forced["tok"] = torch.tensor(sampled, dtype=torch.int64, device=dev)
+        ref.step()
+        assert "tok" not in forced
+        assert [r.tokens for r in eng.sched.running] == [r.tokens for r in ref.sched.running]
+        if not sampled:
+            continue
+        got, want = eng.last_logits.float(), ref.last_logits.float()
+        assert got.shape == want.shape == (len(sampled), FULL.vocab_size)
+        diff = (got - want).abs()
+        if dtype == torch.float32:
+            tol = torch.full_like(want, 3e-2)
+        else:
+            tol = 6e-2 + torch.exp2(torch.floor(torch.log2(want.abs().clamp(min=2.0 ** -14))) - 7)
+        err, mean = float(diff.max()), float(diff.mean())
+        worst = max(worst, err)
+        compared += 1
+        print(f"step {step} ({kinds[-1]}, {len(sampled)} rows): max logit difference {err:.3e}, "
+              f"mean {mean:.2e}, max |logit| {float(want.abs().max()):.2f}")
+        assert bool((diff <= tol).all()), f"step {step} ({kinds[-1]}): max logit difference {err:.3e}"
+        assert mean <= 1e-2, f"step {step} ({kinds[-1]}): mean logit difference {mean:.3e}"
+    assert eng.sched.done() and ref.sched.done()
+    assert kinds.count("mixed") >= 2 and kinds.count("decode") >= 4, kinds
+    assert all(float(s) != 1.0 for s in eng.model.scales()), "scales calibrated"
+    print(f"max logit difference over {compared} steps: {worst:.2e}; steps {kinds}")

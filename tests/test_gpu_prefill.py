@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import announce, assert_close_out
+from conftest import announce, assert_close_out, compact_pool
 import mkv
 from mkv import attention as A
 from mkv import context as C
@@ -415,6 +415,23 @@ def test_attention_layer_mixed_batch_full_size(dev, kv, route):
                               pos.to(dev), 1 / math.sqrt(128), Hq, Hkv, ks, vs)
     assert out.shape == (T, Hq * 128)
     assert_close_out(out.reshape(T, Hq, 128), want, out.dtype, 2e-2 if fp8 else 2e-3)
+    # sampled rows against the float64 oracle over the appended cache: the
+    # first, middle and last rows of 4 prefill chunks and 4 decode rows
+    cuh = cu.tolist()
+    pre = [s_ for s_ in range(len(qlen)) if not is_dec[s_]][:4]
+    dec = [s_ for s_ in range(len(qlen)) if is_dec[s_]][:4]
+    seqs, rows = [], []
+    for s_ in pre + dec:
+        a, b = cuh[s_], cuh[s_ + 1]
+        r = sorted({a, (a + b) // 2, b - 1})
+        seqs.append(s_)
+        rows.append(r)
+    sel = torch.tensor([r for rr in rows for r in rr])
+    cu_s = torch.tensor([0] + list(np.cumsum([len(rr) for rr in rows])), dtype=torch.int32)
+    kcs, vcs, bts = compact_pool(layer.k_cache, layer.v_cache, bt[seqs], ctx[seqs])
+    ref = R.paged_prefill_ref(q[sel].double(), kcs, vcs, bts, ctx[seqs], cu_s, pos[sel], 1 / math.sqrt(128),
+                              Hq, Hkv, ks, vs)
+    assert_close_out(out.reshape(T, Hq, 128)[sel].cpu(), ref, out.dtype, 2e-2 if fp8 else 2e-3)
 
 
 def test_attention_layer_fp32_auto_full_then_chunked_then_decode(dev):

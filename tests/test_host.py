@@ -70,7 +70,11 @@ def test_argument_validation_without_launch():
     # unsupported head_dim / group / block size in decode
     p = ctypes.c_void_p(16)
     base = [p, 4096, p, 4096, 1, p, p, 1, 10, nul, nul, 0, p, 4, 4, p, 1, 2]
-    assert lib.mkv_paged_decode(*base, 32, 8, 64, 256, 0.1, 0, nul, 0, nul) == -4
+    assert lib.mkv_paged_decode(*base, 32, 8, 96, 256, 0.1, 0, nul, 0, nul) == -4
+    # head_dim 64 pairs KV heads: an odd KV-head count, or more than 8 query
+    # heads per KV head, is rejected
+    assert lib.mkv_paged_decode(*base, 21, 7, 64, 256, 0.1, 0, nul, 0, nul) == -4
+    assert lib.mkv_paged_decode(*base, 32, 2, 64, 256, 0.1, 0, nul, 0, nul) == -5
     assert lib.mkv_paged_decode(*base, 32, 6, 128, 256, 0.1, 0, nul, 0, nul) == -5
     assert lib.mkv_paged_decode(*base, 32, 8, 128, 100, 0.1, 0, nul, 0, nul) == -6
     assert lib.mkv_paged_decode(*base, 32, 8, 128, 8, 0.1, 0, nul, 0, nul) == -6
@@ -158,6 +162,46 @@ def test_decode_workspace_and_split_queries():
     assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 1, 256, 128, FP8, 0) > 0
     # small batches split finer
     assert lib.mkv_paged_decode_split_tokens(4, 8, 8, 256, 0) < st or st == 64
+
+
+def test_decode_route_choice():
+    """The library's schedule for split_tokens 0 (mkv_paged_decode_route on
+    a 256-CU device), for the decode workloads that are measured, and the
+    explicit overrides."""
+    lib = _lib.load()
+    F32, FP8, BF16 = _lib.DTYPE_F32, _lib.DTYPE_FP8E4M3, _lib.DTYPE_BF16
+    SK, SP, WG = _lib.ROUTE_STREAM, _lib.ROUTE_SPLIT, _lib.ROUTE_WORKGROUP
+
+    def route(B, Hq, Hkv, mb, bs, D, dt, st=0):
+        return lib.mkv_paged_decode_route(B, Hq, Hkv, mb, bs, D, dt, st, 256)
+
+    # batch 256, 32 / 8 heads, contexts up to 8192 in 32-block tables: stream-K
+    assert route(256, 32, 8, 32, 256, 128, FP8) == SK
+    assert route(256, 32, 8, 32, 256, 128, BF16) == SK
+    # batch 32 over the appended pool, contexts up to 4096 (16-block tables):
+    # a workgroup wave would take up to 512 tokens -> stream-K
+    assert route(32, 32, 8, 16, 256, 128, FP8) == SK
+    # the end-to-end engine's decode rows: 60 (bucket 64) sequences of at most
+    # 768 tokens, 16 / 8 heads, tables padded to 4 blocks -> workgroup
+    assert route(60, 16, 8, 4, 256, 128, FP8) == WG
+    assert route(64, 16, 8, 4, 256, 128, FP8) == WG
+    # the same rows in tables padded to max_model_len 4096 (16 blocks): stream-K
+    assert route(60, 16, 8, 16, 256, 128, FP8) == SK
+    # fp32 batch 4: too few workgroups -> split-K; batch 60 in 16-block tables:
+    # workgroup (up to 512 tokens per wave for fp32)
+    assert route(4, 16, 8, 8, 256, 128, F32) == SP
+    assert route(60, 16, 8, 4, 256, 128, F32) == WG
+    # head_dim 64 pairs KV heads: Llama-3.2-1B decode, batch 48, 12-block tables
+    assert route(48, 32, 8, 12, 256, 64, FP8) == SK
+    assert route(64, 32, 8, 2, 256, 64, BF16) == WG
+    # explicit schedules
+    assert route(60, 16, 8, 4, 256, 128, FP8, _lib.DECODE_STREAM) == SK
+    assert route(60, 16, 8, 4, 256, 128, F32, _lib.DECODE_STREAM) == SP
+    assert route(256, 32, 8, 32, 256, 128, FP8, _lib.DECODE_WORKGROUP) == WG
+    assert route(256, 32, 8, 32, 256, 128, FP8, 256) == SP
+    # unsupported shapes report their status
+    assert route(4, 16, 8, 8, 256, 96, FP8) == -4
+    assert route(4, 21, 7, 8, 256, 64, FP8) == -4
 
 
 def test_wrappers_reject_cpu_tensors_and_unimplemented_modes():

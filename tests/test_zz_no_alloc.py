@@ -5,7 +5,10 @@ It must give the same bytes as mkv_paged_decode with a caller workspace (the
 same kernels and schedule) on consecutive calls that reuse the scratch, the
 second with a smaller batch, for the stream-K route (FP8 per tensor, bf16,
 per-token-head FP8) and the split-K route (fp32 cache, explicit splits); and
-refuse a request larger than the scratch before launching anything.
+refuse an explicit route larger than the scratch before launching anything.
+With the library's choice of route, a call whose stream-K slots do not fit
+(16 query heads per KV head on 256 CUs) takes the workgroup route instead:
+the same result within rounding.
 """
 from __future__ import annotations
 
@@ -15,10 +18,11 @@ import math
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, assert_close_out
 from mkv import _lib
 from mkv import attention as A
 from mkv import workloads as W
+from oracle import reference as R
 
 pytestmark = pytest.mark.gpu
 
@@ -115,3 +119,44 @@ def test_noalloc_decode_refuses_oversized_requests(dev):
     assert e.value.status == -10
     torch.cuda.synchronize()
     assert bool((out == 3.0).all()), "a refused call must not launch"
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "fp8"])
+def test_noalloc_default_route_falls_back_when_stream_slots_do_not_fit(dev, fmt):
+    """16 query heads per KV head: stream-K's partial slots for the whole
+    persistent grid (2048 waves x 2 slots x 16 heads x 130 fp32 on 256 CUs,
+    34 MB) exceed the 32 MiB scratch.  The library's choice (split_tokens
+    0) then runs the workgroup route, which needs no workspace: within
+    rounding of the workspace call and of the oracle, on two calls in a row
+    (the second smaller).  Where the slots fit (fewer CUs), the two calls
+    take the same route and agree bit for bit."""
+    Hq, Hkv, bs = 32, 2, 64
+    announce(f"noalloc decode, {fmt}, group 16, library route")
+    g = torch.Generator().manual_seed(1616)
+    N, mb = 96, 24
+    kc, vc, ks, vs, mode = _pools(dev, fmt, N, bs, Hkv, g)
+    tol = 2e-2 if fmt == "fp8" else 2e-3
+    for B in (12, 3):
+        ctx = torch.randint(1, mb * bs + 1, (B,), generator=g)
+        ctx[0] = 0
+        bt = torch.randint(0, N, (B, mb), generator=g, dtype=torch.int32)
+        q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16).to(dev)
+        bt_d, ctx_d = bt.to(dev), ctx.to(dev)
+        need = _lib.query("mkv_paged_decode_workspace_size", B, Hq, Hkv, mb, bs, D, A._dtype_code(kc, "k"), 0)
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+        want = torch.full_like(q, float("nan"))
+        got = torch.full_like(q, float("nan"))
+        _call("mkv_paged_decode", want, q, kc, vc, ks, vs, mode, bt_d, ctx_d, Hq, Hkv, bs, 0, ws)
+        _call("mkv_paged_decode_noalloc", got, q, kc, vc, ks, vs, mode, bt_d, ctx_d, Hq, Hkv, bs, 0)
+        torch.cuda.synchronize()
+        print(f"batch {B}: workspace route needs {need} bytes (scratch {_lib.NOALLOC_SCRATCH_BYTES})")
+        if need <= _lib.NOALLOC_SCRATCH_BYTES:
+            assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+        else:
+            assert_close_out(got.cpu(), want.cpu().double(), got.dtype, tol)
+        ksf = float(ks) if ks is not None else None
+        vsf = float(vs) if vs is not None else None
+        ref = R.paged_decode_ref(q.cpu().double(), kc.cpu(), vc.cpu(), bt, ctx, 1.0 / math.sqrt(D), Hq, Hkv,
+                                 ksf, vsf)
+        assert_close_out(got.cpu(), ref, got.dtype, tol)
+        assert torch.count_nonzero(got[0].float()) == 0
