@@ -872,13 +872,17 @@ MKV_DEV WorkItem wg_item(const DecodeArgs& a) {
   return it;
 }
 
-template <int KV_DT, bool PAIR>
+// QS: the q split of the bf16 MFMA formats (an fp32 / fp16 q over a bf16 or
+// per-token-head cache) as a compile-time choice, so that the common case
+// (a bf16 q) holds no residual terms.
+template <int KV_DT, bool PAIR, bool QS>
 MKV_DEV void wg_decode(const DecodeArgs& a) {
   const WorkItem it = wg_item(a);
 
   QOps<KV_DT> qop;
   const float k_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.k_scale) : 1.0f;
   const float score_mul = load_q_operands<KV_DT, PAIR>(a, it.b, it.kvh, qop, k_mul);
+  qop.split = QS;
   const bool hi = PAIR && (threadIdx.x & 15) >= (a.group >> 1);
   f32x4 acc[8];
 #pragma unroll
@@ -911,7 +915,16 @@ MKV_DEV void wg_decode(const DecodeArgs& a) {
 template <int KV_DT, bool PAIR>
 __global__ __launch_bounds__(kWgMaxWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
 paged_decode_wg_kernel(DecodeArgs a) {
-  wg_decode<KV_DT, PAIR>(a);
+  wg_decode<KV_DT, PAIR, false>(a);
+}
+
+// The split-q variant of the bf16 MFMA formats holds 16 more registers of q
+// than two waves per SIMD leave room for: it runs at one wave per SIMD with
+// at most kWgSplitWaves waves per workgroup (a workgroup still fits one CU).
+constexpr int kWgSplitWaves = 4;
+template <int KV_DT, bool PAIR>
+__global__ __launch_bounds__(kWgSplitWaves* kWave) void paged_decode_wg_qsplit_kernel(DecodeArgs a) {
+  wg_decode<KV_DT, PAIR, true>(a);
 }
 
 // fp32 caches on the workgroup route: 16-token tiles on v_mfma_f32_16x16x4_f32
@@ -1954,14 +1967,15 @@ int kernel_shape(int num_heads, int num_kv_heads, int head_dim, KernelShape& ks)
 }
 
 // Waves per workgroup of the workgroup route: as many as fill the chip's
-// two-waves-per-SIMD slots once (at most kWgMaxWaves), no more than the
-// widest sequence's tiles, and few enough that the LDS merge buffers fit in
-// 64 KiB.
-int wg_waves(int batch, int kv_heads, int group, int max_blocks, int block_size, int cus) {
+// wave slots once (a CU holds max_waves waves of the kernel: 8 at two waves
+// per SIMD, 4 for the split-q kernel at one), no more than the widest
+// sequence's tiles, and few enough that the LDS merge buffers fit in 64 KiB.
+int wg_waves(int batch, int kv_heads, int group, int max_blocks, int block_size, int cus,
+             int max_waves = kWgMaxWaves) {
   const int64_t items = (int64_t)batch * kv_heads;
-  const int64_t slots = (int64_t)cus * 8;
+  const int64_t slots = (int64_t)cus * max_waves;
   const int64_t max_tiles = ((int64_t)max_blocks * block_size + 31) / 32;
-  int nw = kWgMaxWaves;
+  int nw = max_waves;
   while (nw > 1 && (items * nw > slots || nw > max_tiles ||
                     (size_t)nw * group * (kHeadDim + 2) * sizeof(float) > 65536))
     nw >>= 1;
@@ -2054,13 +2068,31 @@ int launch_route(DecodeArgs& a, int route, int fmt, int split_tokens, int max_bl
   // the merge kernels apply the per-tensor V scale
   const bool fp8 = fmt == MKV_DTYPE_FP8E4M3;
   if (route == kRouteWorkgroup) {
-    const int nw = wg_waves(batch, a.num_kv_heads, group, max_blocks, block_size, device_cus());
+    // bf16 MFMA formats with an fp32 / fp16 q: the split-q kernel
+    const bool qsplit = (fmt == MKV_DTYPE_BF16 || fmt == kKvFp8PerToken || fmt == kKvI8PerToken) &&
+                        a.q_dtype != MKV_DTYPE_BF16;
+    const int nw = wg_waves(batch, a.num_kv_heads, group, max_blocks, block_size, device_cus(),
+                            qsplit ? kWgSplitWaves : kWgMaxWaves);
     const size_t lds = (size_t)nw * group * (kHeadDim + 2) * sizeof(float);
     a.split_tokens = 0;
     a.max_splits = 0;
     a.ws_acc = nullptr;
     a.ws_ml = nullptr;
     const dim3 grid((unsigned)((int64_t)batch * a.num_kv_heads)), block(nw * kWave);
+    if (qsplit) {
+      switch (fmt) {
+        case kKvFp8PerToken:
+          hipLaunchKernelGGL((paged_decode_wg_qsplit_kernel<kKvFp8PerToken, PAIR>), grid, block, lds, s, a);
+          break;
+        case kKvI8PerToken:
+          hipLaunchKernelGGL((paged_decode_wg_qsplit_kernel<kKvI8PerToken, PAIR>), grid, block, lds, s, a);
+          break;
+        default:
+          hipLaunchKernelGGL((paged_decode_wg_qsplit_kernel<MKV_DTYPE_BF16, PAIR>), grid, block, lds, s, a);
+          break;
+      }
+      return (int)hipGetLastError();
+    }
     switch (fmt) {
       case MKV_DTYPE_F32:
         hipLaunchKernelGGL(paged_decode_wg_f32_kernel<PAIR>, grid, block, lds, s, a);

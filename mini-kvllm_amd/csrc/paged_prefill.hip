@@ -540,7 +540,7 @@ struct LdsTile {
 // bits, so q is split into bf16 hi + lo terms and each QK step takes a second
 // MFMA, giving ~16 significant bits like the fp32 reference.
 template <int KV_DT, bool PAGED, bool QSPLIT, bool PAIR>
-__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4))) void prefill_mfma_kernel(PrefillArgs a) {
+MKV_DEV void prefill_mfma_body(const PrefillArgs& a) {
   using LT = LdsTile<KV_DT>;
   // CT: the element type of the LDS tiles and the MFMA operands (fp16 for
   // an FP8 cache, converted exactly while staging).
@@ -1185,6 +1185,12 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
 #undef KBUF
 #undef VBUF
   __builtin_amdgcn_s_setprio(3);
+  {
+  // the lane's indices again, recomputed here rather than held in registers
+  // across the key loop (held, they were spilled to scratch)
+  const int lane = lane_id_volatile();
+  const int c = lane & 15, kg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // ---- normalise and write rows 4kg + r of each row tile ----
   const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
   static_assert(kRowTiles == 1, "the staged epilogue holds one 16-row tile per wave");
@@ -1261,7 +1267,10 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     }
     return;
   }
-  // fp32 outputs: 1 / l as above
+  // fp32 outputs: 1 / l as above; row / G by the multiply-shift below (a
+  // division by G here would keep the divider's reciprocal in a register
+  // across the key loop)
+  const uint32_t gm32 = 65536u / (uint32_t)G + 1u;
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt) {
     float inv_r[4];
@@ -1278,19 +1287,38 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = (kRowTiles * wave + rt) * 16 + 4 * kg + r;
-      const int64_t tok = q0 + row / G;
+      const int rq = (int)(((uint32_t)row * gm32) >> 16), rm = row - rq * G;
+      const int64_t tok = q0 + rq;
       if (row >= a.tok_per_wg * G || tok >= q1) continue;
-      const int hq = kvh * G + row % G;
+      const int hq = kvh * G + rm;
       // lane c holds dims 16mm + c (head pairing: a row keeps dims 64 hi ..
       // 64 hi + 63, i.e. mm = 4 hi .. 4 hi + 3)
-      const bool hi = PAIR && row % G >= (G >> 1);
+      const bool hi = PAIR && rm >= (G >> 1);
       const int64_t o = (tok * a.num_heads + hq) * kQDim<PAIR> + c - (hi ? 64 : 0);
 #pragma unroll
       for (int mm = 0; mm < 8; ++mm)
         if (!PAIR || (mm >= 4) == hi) reinterpret_cast<float*>(a.out)[o + 16 * mm] = acc[rt][mm][r] * inv_r[r];
     }
   }
+  }
 }
+
+template <int KV_DT, bool PAGED, bool QSPLIT, bool PAIR>
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4))) void prefill_mfma_kernel(PrefillArgs a) {
+  prefill_mfma_body<KV_DT, PAGED, QSPLIT, PAIR>(a);
+}
+
+// The variants that do not fit four waves per SIMD without spilling (the
+// per-token-head formats with a split q, or with head pairing, which holds
+// a second scale set per key) run at two waves per SIMD, one workgroup per
+// CU, with up to 256 registers.
+template <int KV_DT, bool PAGED, bool QSPLIT, bool PAIR>
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_mfma_2w_kernel(PrefillArgs a) {
+  prefill_mfma_body<KV_DT, PAGED, QSPLIT, PAIR>(a);
+}
+
+template <int KV_DT, bool QSPLIT, bool PAIR>
+constexpr bool kPrefill2w = kPerTokenScale<KV_DT> && (QSPLIT || PAIR);
 
 // ---------------------------------------------------------------------------
 // fp32 caches (the reference engine's default precision, model_runner.py:87,
@@ -1516,15 +1544,21 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   }
 
   // ---- normalise and write rows 4 kg + r ----
+  // (the lane's indices recomputed rather than held across the key loop, and
+  // row / G by multiply-shift for row < 128: no divider kept across it)
+  const int lane_e = lane_id_volatile();
+  const int ce = lane_e & 15, kge = lane_e >> 4;
+  const uint32_t gm = 65536u / (uint32_t)G + 1u;
   float l_col = l_run + __shfl_xor(l_run, 16);
   l_col += __shfl_xor(l_col, 32);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const float lh = __shfl(l_col, 4 * kg + r);
-    const int row = 16 * wave + 4 * kg + r;
-    const int64_t tok = q0 + row / G;
+    const float lh = __shfl(l_col, 4 * kge + r);
+    const int row = 16 * wave + 4 * kge + r;
+    const int rq = (int)(((uint32_t)row * gm) >> 16), rm = row - rq * G;
+    const int64_t tok = q0 + rq;
     if (row >= a.tok_per_wg * G || tok >= q1) continue;
-    const int hq = kvh * G + row % G;
+    const int hq = kvh * G + rm;
     const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
     float lo[8], hi[8];
 #pragma unroll
@@ -1535,13 +1569,13 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     const int64_t o = (tok * a.num_heads + hq) * kQDim<PAIR>;
     // head pairing: a row of the pair's first KV head keeps dims 0-63 (lo),
     // one of its second dims 64-127 (hi), stored at the row's dims 0-63
-    const bool row_hi = PAIR && row % G >= (G >> 1);
+    const bool row_hi = PAIR && rm >= (G >> 1);
     const bool keep_lo = !PAIR || !row_hi, keep_hi = !PAIR || row_hi;
     const int hi_off = PAIR ? 0 : 64;
     if (a.q_dtype == MKV_DTYPE_F32) {
       float* po = reinterpret_cast<float*>(a.out) + o;
-      if (keep_lo) *reinterpret_cast<f32x4*>(po + 4 * c) = f32x4{lo[0], lo[1], lo[2], lo[3]};
-      if (keep_hi) *reinterpret_cast<f32x4*>(po + hi_off + 4 * c) = f32x4{hi[0], hi[1], hi[2], hi[3]};
+      if (keep_lo) *reinterpret_cast<f32x4*>(po + 4 * ce) = f32x4{lo[0], lo[1], lo[2], lo[3]};
+      if (keep_hi) *reinterpret_cast<f32x4*>(po + hi_off + 4 * ce) = f32x4{hi[0], hi[1], hi[2], hi[3]};
     } else {
       const bool bf = a.q_dtype == MKV_DTYPE_BF16;
       auto pack = [&](float x, float y) -> uint32_t {
@@ -1551,9 +1585,9 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       };
       uint16_t* po = reinterpret_cast<uint16_t*>(a.out) + o;
       typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-      if (keep_lo) *reinterpret_cast<u32x2*>(po + 4 * c) = u32x2{pack(lo[0], lo[1]), pack(lo[2], lo[3])};
+      if (keep_lo) *reinterpret_cast<u32x2*>(po + 4 * ce) = u32x2{pack(lo[0], lo[1]), pack(lo[2], lo[3])};
       if (keep_hi)
-        *reinterpret_cast<u32x2*>(po + hi_off + 4 * c) = u32x2{pack(hi[0], hi[1]), pack(hi[2], hi[3])};
+        *reinterpret_cast<u32x2*>(po + hi_off + 4 * ce) = u32x2{pack(hi[0], hi[1]), pack(hi[2], hi[3])};
     }
   }
 }
@@ -1577,12 +1611,21 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   const size_t lds = kTileListOffset + (a.inline_list ? sizeof(TilePick) : 0);
   int64_t nwg = a.tiles_ub * a.num_kv_heads;
   nwg = ((nwg + kXcds - 1) / kXcds) * kXcds;
-  if (a.pair)
-    hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED, QSPLIT, true>), dim3((unsigned)nwg), dim3(kPfThreads),
-                       lds, s, a);
-  else
-    hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED, QSPLIT, false>), dim3((unsigned)nwg), dim3(kPfThreads),
-                       lds, s, a);
+  if (a.pair) {
+    if constexpr (kPrefill2w<KV_DT, QSPLIT, true>)
+      hipLaunchKernelGGL((prefill_mfma_2w_kernel<KV_DT, PAGED, QSPLIT, true>), dim3((unsigned)nwg),
+                         dim3(kPfThreads), lds, s, a);
+    else
+      hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED, QSPLIT, true>), dim3((unsigned)nwg), dim3(kPfThreads),
+                         lds, s, a);
+  } else {
+    if constexpr (kPrefill2w<KV_DT, QSPLIT, false>)
+      hipLaunchKernelGGL((prefill_mfma_2w_kernel<KV_DT, PAGED, QSPLIT, false>), dim3((unsigned)nwg),
+                         dim3(kPfThreads), lds, s, a);
+    else
+      hipLaunchKernelGGL((prefill_mfma_kernel<KV_DT, PAGED, QSPLIT, false>), dim3((unsigned)nwg), dim3(kPfThreads),
+                         lds, s, a);
+  }
   return (int)hipGetLastError();
 }
 

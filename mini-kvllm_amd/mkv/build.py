@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -44,14 +45,26 @@ def sources() -> list[Path]:
     return sorted(list(SRC_DIR.glob("*.hip")) + list(SRC_DIR.glob("*.cpp")))
 
 
+# The compiler's per-kernel resource report (registers, spills, scratch,
+# occupancy) for each source, kept beside its object file.
+RESOURCE_FLAG = "-Rpass-analysis=kernel-resource-usage"
+
+
+def _resource_path(obj: Path) -> Path:
+    return obj.with_suffix(obj.suffix + ".resources.txt")
+
+
 def _compile(hipcc: str, src: Path, obj: Path) -> str:
-    cmd = [hipcc, *DEVICE_FLAGS, f"-I{INCLUDE_DIR}", f"-I{SRC_DIR}", "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, *DEVICE_FLAGS, RESOURCE_FLAG, f"-I{INCLUDE_DIR}", f"-I{SRC_DIR}", "-c", str(src), "-o",
+           str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "'-packed-fp32-ops' is not a recognized feature for this target"
-    msg = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if noise not in l)
+    lines = [l for l in (r.stdout + r.stderr).splitlines() if noise not in l]
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed on {src.name}:\n{msg}")
-    return msg
+        raise RuntimeError(f"hipcc failed on {src.name}:\n" + "\n".join(lines))
+    _resource_path(obj).write_text("\n".join(l for l in lines if "remark:" in l) + "\n")
+    return "\n".join(l for l in lines if "remark:" not in l and l.strip() and not l.lstrip()[:1].isdigit()
+                     and not l.lstrip().startswith("|"))
 
 
 def build(verbose: bool = False) -> Path:
@@ -72,6 +85,42 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
+
+
+def parse_resources(text: str) -> dict[str, dict[str, int]]:
+    """Per-kernel figures of a -Rpass-analysis=kernel-resource-usage report:
+    {mangled kernel name: {"VGPRs", "AGPRs", "SGPRs", "VGPRs Spill", "SGPRs
+    Spill", "ScratchSize", "Occupancy", ...}}."""
+    out: dict[str, dict[str, int]] = {}
+    cur = None
+    for line in text.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            cur = out.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"remark:\s+([A-Za-z ]+?)(?: \[[^\]]*\])?: (\d+) \[-Rpass", line)
+        if m and cur is not None:
+            cur[m.group(1).strip()] = int(m.group(2))
+    return out
+
+
+def kernel_resources() -> dict[str, dict[str, int]]:
+    """The resource report of every kernel in csrc/: from the last build's
+    reports when they are newer than every source and header, else by
+    compiling the sources' device code again (no link)."""
+    hipcc = _hipcc()
+    headers = list(SRC_DIR.glob("*.hpp")) + list(INCLUDE_DIR.glob("*.h"))
+    newest_header = max((h.stat().st_mtime for h in headers), default=0.0)
+    res: dict[str, dict[str, int]] = {}
+    for src in sources():
+        if src.suffix != ".hip":
+            continue
+        rep = _resource_path(BUILD_DIR / (src.name + ".o"))
+        if not (rep.exists() and rep.stat().st_mtime >= max(src.stat().st_mtime, newest_header)):
+            BUILD_DIR.mkdir(parents=True, exist_ok=True)
+            _compile(hipcc, src, BUILD_DIR / (src.name + ".o"))
+        res.update(parse_resources(rep.read_text()))
+    return res
 
 
 if __name__ == "__main__":

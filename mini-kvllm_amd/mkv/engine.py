@@ -110,6 +110,7 @@ class Scheduler:
     def __init__(self, num_blocks: int, block_size: int, max_num_seqs: int,
                  max_num_batched_tokens: int, eos: int | None = None):
         self.pool = BlockPool(num_blocks)
+        self.num_blocks = num_blocks
         self.block_size = block_size
         self.max_num_seqs = max_num_seqs
         self.max_num_batched_tokens = max_num_batched_tokens
@@ -119,6 +120,13 @@ class Scheduler:
         self.num_preemptions = 0
 
     def add(self, req: Request) -> None:
+        """Queue a request.  One that needs more blocks than the whole pool
+        (prompt + max_tokens) is refused here: admitted, it would preempt
+        itself and be re-admitted forever."""
+        need = (req.prompt_len + req.max_tokens + self.block_size - 1) // self.block_size
+        if need > self.num_blocks:
+            raise ValueError(f"request {req.req_id} needs {need} KV blocks (prompt {req.prompt_len} + "
+                             f"max_tokens {req.max_tokens}) but the pool holds {self.num_blocks}")
         self.waiting.append(req)
 
     def done(self) -> bool:

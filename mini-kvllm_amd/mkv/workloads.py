@@ -207,13 +207,13 @@ def prefill_mixed(seed: int = 4, num_prefill: int = 8, chunk: int = 512, num_dec
 
 def alg_bytes_decode(context_lens: torch.Tensor, block_size: int, num_heads: int,
                      num_kv_heads: int, kv_bytes: int, q_bytes: int = 2,
-                     ctx_bytes: int = 8, scale_bytes: int = 0) -> int:
+                     ctx_bytes: int = 8, scale_bytes: int = 0, head_dim: int = HEAD_DIM) -> int:
     """Algorithmic HBM bytes of one decode step: every visible K and V element
     once (plus its K and V scales for per-token-head caches, scale_bytes = 4),
     q and out once, the used block-table entries and context_lens."""
     L = context_lens.to(torch.int64)
-    kv = int(L.sum()) * num_kv_heads * (HEAD_DIM * kv_bytes + scale_bytes) * 2
-    qo = int(L.numel()) * num_heads * HEAD_DIM * 2 * q_bytes
+    kv = int(L.sum()) * num_kv_heads * (head_dim * kv_bytes + scale_bytes) * 2
+    qo = int(L.numel()) * num_heads * head_dim * 2 * q_bytes
     bt = int(((L + block_size - 1) // block_size).sum()) * 4
     return kv + qo + bt + int(L.numel()) * ctx_bytes
 

@@ -116,3 +116,18 @@ def test_sequence_cap_limits_running_requests():
         sched.add(E.Request(i, 5, [0] * 5, max_tokens=2))
     items = sched.schedule()
     assert len(items) == 3 and len(sched.running) == 3 and len(sched.waiting) == 2
+
+
+def test_request_larger_than_the_pool_is_refused():
+    """A request whose prompt + max_tokens needs more blocks than the pool
+    holds would preempt itself and be re-admitted forever; it is refused
+    when it is added, and one that fits exactly still completes."""
+    bs = 16
+    sched = E.Scheduler(num_blocks=4, block_size=bs, max_num_seqs=4, max_num_batched_tokens=64)
+    with pytest.raises(ValueError, match="KV blocks"):
+        sched.add(E.Request(0, 60, list(range(60)), max_tokens=5))  # 65 tokens: 5 blocks
+    assert sched.done()
+    fits = E.Request(1, 60, list(range(60)), max_tokens=4)  # 64 tokens: 4 blocks
+    sched.add(fits)
+    _run(sched, [fits], bs)
+    assert fits.num_generated == 4
