@@ -872,11 +872,105 @@ MKV_DEV WorkItem wg_item(const DecodeArgs& a) {
   return it;
 }
 
-// QS: the q split of the bf16 MFMA formats (an fp32 / fp16 q over a bf16 or
-// per-token-head cache) as a compile-time choice, so that the common case
-// (a bf16 q) holds no residual terms.
+// Work of wave wv of the workgroup route: the sequence's 32-token tiles wv,
+// wv + nw, wv + 2nw, ...  Dealt round robin, a wave's first tile does not
+// depend on the context length, so its block-table entries and K/V loads go
+// out in the same round trip as the length's own load: t_end starts at the
+// table's capacity and is set when the length arrives.
+MKV_DEV WorkItem wg_item_rr(const DecodeArgs& a) {
+  WorkItem it;
+  it.num_splits = blockDim.x >> 6;
+  it.split = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  it.b = (int)(blockIdx.x / (unsigned)a.num_kv_heads);
+  it.kvh = (int)blockIdx.x - it.b * a.num_kv_heads;
+  it.t_begin = 32 * it.split;
+  const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
+  it.t_end = (int)(cap < 0x7fffffff ? cap : 0x7fffffff);
+  return it;
+}
+
+// Zero the V rows of a tile at or past t_end (token t0 + 16hf + 4kg + r in
+// V word 4hf + r).  A tile loaded before the context length was known may
+// hold stale pool bytes there, and a NaN among them would survive its zero
+// weight in the PV product.  K rows need nothing: their scores are replaced
+// by -inf.
+template <int KV_DT>
+MKV_DEV void zero_v_rows_past(Tile16<KV_DT>& T, int t0, int t_end) {
+  const int kg = (threadIdx.x & 63) >> 4;
+  using VT = typename Tile16<KV_DT>::VT;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bool keep = t0 + 16 * (i >> 2) + 4 * kg + (i & 3) < t_end;
+    T.v[i] = keep ? T.v[i] : VT{};
+  }
+}
+
+// The workgroup route over 1-byte caches (FP8, per-token-head FP8 / INT8).
+// Start-up in two round trips: a 16-bit q's loads, the context length, the
+// first tile's block-table entries (scalar loads) and then that tile's K/V
+// loads are issued before anything is waited for; the second tile's loads go
+// out as soon as the length is known, and q is converted after them.
 template <int KV_DT, bool PAIR, bool QS>
-MKV_DEV void wg_decode(const DecodeArgs& a) {
+MKV_DEV void wg_decode_rr(const DecodeArgs& a) {
+  WorkItem it = wg_item_rr(a);
+  const int step = 32 * it.num_splits;
+  const bool q16 = a.q_dtype != MKV_DTYPE_F32;
+  QOps<KV_DT> qop;
+  QStage qs;
+  float score_mul = 0.0f;
+  const float k_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.k_scale) : 1.0f;
+  if (q16)
+    load_q_stage<PAIR>(a, it.b, it.kvh, true, qs);
+  else
+    score_mul = load_q_operands<KV_DT, PAIR>(a, it.b, it.kvh, qop, k_mul);
+  const int64_t L_raw = load_index(a.context_lens, it.b, a.ctx_i64);
+  const ItemLoad Ld = item_load_setup<KV_DT>(a, it);
+  // (two tiles in flight, as in the other routes: a third measured 1-2 us
+  // slower on the engine's decode shapes)
+  Tile16<KV_DT> ta, tb2;
+  load_tile16<KV_DT, PAIR>(a, it, Ld, it.t_begin, item_phys(a, it.b, it.t_begin, it.t_end), ta);
+  it.t_end = (int)(L_raw < 0 ? 0 : (L_raw < it.t_end ? L_raw : it.t_end));
+  const bool hi = PAIR && (threadIdx.x & 15) >= (a.group >> 1);
+  f32x4 acc[8];
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegBig, l_run = 0.0f;
+  if (it.t_begin < it.t_end) {
+    PhysPair ph = item_phys(a, it.b, it.t_begin + step, it.t_end);
+    load_tile16<KV_DT, PAIR>(a, it, Ld, it.t_begin + step, ph, tb2);
+    ph = item_phys(a, it.b, it.t_begin + 2 * step, it.t_end);
+    if (q16) score_mul = staged_q_operands<KV_DT>(a, qs, qop, k_mul);
+    qop.split = QS;
+    zero_v_rows_past<KV_DT>(ta, it.t_begin, it.t_end);
+    compute_tile16<KV_DT, PAIR>(ta, it.t_begin, it.t_end, qop, score_mul, acc, m_run, l_run, hi);
+    for (int t0 = it.t_begin + step; t0 < it.t_end;) {
+      load_tile16<KV_DT, PAIR>(a, it, Ld, t0 + step, ph, ta);
+      ph = item_phys(a, it.b, t0 + 2 * step, it.t_end);
+      compute_tile16<KV_DT, PAIR>(tb2, t0, it.t_end, qop, score_mul, acc, m_run, l_run, hi);
+      t0 += step;
+      if (t0 >= it.t_end) break;
+      load_tile16<KV_DT, PAIR>(a, it, Ld, t0 + step, ph, tb2);
+      ph = item_phys(a, it.b, t0 + 2 * step, it.t_end);
+      compute_tile16<KV_DT, PAIR>(ta, t0, it.t_end, qop, score_mul, acc, m_run, l_run, hi);
+      t0 += step;
+    }
+  } else {
+    // no tile in the context: let the speculative loads land before the
+    // registers they write are reused
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  }
+  float l_col = l_run + __shfl_xor(l_run, 16);
+  l_col += __shfl_xor(l_col, 32);
+  const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
+  wg_merge_store<PAIR>(a, it, acc, m_run, l_col, v_mul);
+}
+
+// The workgroup route over 16-bit caches: consecutive tile ranges, started
+// once the context length is known.  (Their tiles take twice the registers
+// of the 1-byte formats', and the kernel sits at the two-waves-per-SIMD
+// limit: the round-robin form below spills 8-14 registers here.)
+template <int KV_DT, bool PAIR, bool QS>
+MKV_DEV void wg_decode_contig(const DecodeArgs& a) {
   const WorkItem it = wg_item(a);
 
   QOps<KV_DT> qop;
@@ -910,6 +1004,17 @@ MKV_DEV void wg_decode(const DecodeArgs& a) {
   l_col += __shfl_xor(l_col, 32);
   const float v_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.v_scale) : 1.0f;
   wg_merge_store<PAIR>(a, it, acc, m_run, l_col, v_mul);
+}
+
+// QS: the q split of the bf16 MFMA formats (an fp32 / fp16 q over a bf16 or
+// per-token-head cache) as a compile-time choice, so that the common case
+// (a bf16 q) holds no residual terms.
+template <int KV_DT, bool PAIR, bool QS>
+MKV_DEV void wg_decode(const DecodeArgs& a) {
+  if constexpr (DTypeInfo<KV_DT>::kBytes == 2)
+    wg_decode_contig<KV_DT, PAIR, QS>(a);
+  else
+    wg_decode_rr<KV_DT, PAIR, QS>(a);
 }
 
 template <int KV_DT, bool PAIR>
