@@ -197,6 +197,41 @@ def test_prefill_peaked_attention_long_context(dev, scale):
     assert_close_out(gotf, wantf, gotf.dtype, 2e-3)
 
 
+@pytest.mark.parametrize("paged", [True, False])
+def test_prefill_bf16_values_beyond_fp16_range(dev, paged):
+    """V values beyond the fp16 range in a bf16 cache (7e4, -3e5 and 2e9
+    inside sequence 0's context, none in sequence 1, one launch) stay exact
+    through the PV products: against the float64 oracle, whose half-ulp term
+    scales with the large outputs, paged and contiguous."""
+    announce(f"prefill bf16 V beyond fp16, paged={paged}")
+    prior, qlen = [300, 90], [70, 130]
+    q, k, v, bt, ctx, cu, pos, _, _ = _make(505, prior, qlen, 8, 2, 64, torch.bfloat16)
+    sc = 0.3
+    if paged:
+        blk = int(bt[0, 1])
+        v[blk, 5, 0, 17] = 7e4
+        v[blk, 40, 1, 100] = -3e5
+        v[int(bt[0, 0]), 3, 0, 0] = 2e9
+        got = _gpu(dev, q, k, v, bt, ctx, cu, pos, sc, 8, 2, None, None)
+        want = R.paged_prefill_ref(q.double(), k, v, bt, ctx, cu, pos, sc, 8, 2)
+    else:
+        lens = [370, 220]
+        cuf = torch.tensor([0, 370, 590], dtype=torch.int32)
+        g = torch.Generator().manual_seed(506)
+        qf = torch.randn(590, 8, 128, generator=g).to(torch.bfloat16)
+        kf = torch.randn(590, 2, 128, generator=g).to(torch.bfloat16)
+        vf = torch.randn(590, 2, 128, generator=g).to(torch.bfloat16)
+        vf[69, 0, 17] = 7e4
+        vf[200, 1, 100] = -3e5
+        vf[3, 0, 0] = 2e9
+        got = mkv.flash_attention_prefill(qf.to(dev), kf.to(dev), vf.to(dev), cuf.to(dev), sc, 8, 2,
+                                          128).cpu()
+        want = R.flash_prefill_ref(qf.double(), kf.double(), vf.double(), cuf, sc, 8, 2)
+        assert lens[0] + lens[1] == 590
+    assert float(want.abs().max()) > 1e4  # the large values reach the output
+    assert_close_out(got, want, got.dtype, 2e-3)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("group", [1, 4, 16])
 def test_flash_prefill_contiguous(dev, dtype, group):
