@@ -264,6 +264,11 @@ def prefill_extra(dev, stream, cpu: bool = True) -> dict:
         tf = flops / (ms * 1e-3) / 1e12
         out[f"{name}_kv"] = {"us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1),
                              "frac_of_2500_TFLOPs": round(tf / 2500.0, 4)}
+        if name != "bf16":
+            # 1-byte caches: also against the 5.0 PF dense FP8 (and INT8) MFMA
+            # peak; the kernel converts the codes exactly to 16-bit operands
+            # and runs the fp16 / bf16 MFMA, whose peak is the 2.5 PF above
+            out[f"{name}_kv"]["frac_of_5000_TFLOPs_fp8_peak"] = round(tf / 5000.0, 4)
         if name == "bf16" and cpu:
             out["cpu_baseline"] = cpu_prefill_baseline(q, kc, vc, bt, ctx, cu_p, pos, pm["block_size"])
         del kc, vc
@@ -558,6 +563,7 @@ def mixed_batch_extra(dev, stream, cpu: bool = True) -> dict:
             row["roofline"] = {
                 "alg_flops": flops, "alg_kv_bytes": kv_bytes,
                 "TFLOPs": round(flops / us / 1e6, 1), "frac_of_2500_TFLOPs": round(flops / us / 1e6 / 2500, 4),
+                **({"frac_of_5000_TFLOPs_fp8_peak": round(flops / us / 1e6 / 5000, 4)} if name != "bf16" else {}),
                 "GBps": round(kv_bytes / us / 1e3, 1),
                 "frac_of_8000_GBps": round(kv_bytes / us / 1e3 / PEAK_HBM_GBPS, 4),
                 "bound": "mfma" if flops / 2.5e15 > kv_bytes / 8e12 else "hbm"}
