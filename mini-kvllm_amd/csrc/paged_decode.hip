@@ -1209,24 +1209,6 @@ struct Cursor {
 
 MKV_DEV int lds_uniform(const int* p, int i) { return __builtin_amdgcn_readfirstlane(p[i]); }
 
-// Tile of KV head kvh at column g (pre: per-sequence tile prefix, lens:
-// lengths; g < pre[B]).
-MKV_DEV Cursor cursor_at(const int* pre, const int* lens, int B, int kvh, int64_t g) {
-  int lo = 0, hi = B;  // largest b with pre[b] <= g; that b has tiles
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (lds_uniform(pre, mid) <= g) lo = mid; else hi = mid;
-  }
-  Cursor c;
-  c.b = lo;
-  c.kvh = kvh;
-  const int p0 = lds_uniform(pre, lo);
-  c.n = lds_uniform(pre, lo + 1) - p0;
-  c.t = (int)(g - p0);
-  c.L = lds_uniform(lens, lo);
-  return c;
-}
-
 // The next column of the same KV head.
 MKV_DEV void cursor_next(Cursor& c, const int* pre, const int* lens, int B) {
   if (++c.t < c.n) return;
@@ -1473,7 +1455,10 @@ MKV_DEV int64_t stream_prefix(const DecodeArgs& a, int* pre, int* lens) {
 // waves (w1 of them) therefore get kFirstSharePct percent of the columns and
 // the second-round groups the rest; with one workgroup per CU the split is
 // even (w1 = W / Hkv).
-constexpr int kFirstSharePct = 58;  // (55 / 61 / 64 with the cost-balanced ranges: -0.6% / +0.2% / -0.8%)
+// (Batch-256 FP8 step with the reversed head order below, against 58: 60
+// +0.3%, 62 -1.5%; per-wave timestamps at 58 had the second-round groups
+// end ~2.6 us after the first-round ones.)
+constexpr int kFirstSharePct = 60;
 // Split units per column (the cost-balanced split below).  Every range is at
 // least kColCost units wide, so a range inside an item holds at least one of
 // its columns: the merge kernel reads every group between an item's first and
@@ -1551,22 +1536,63 @@ MKV_DEV int64_t stream_cost_total(const DecodeArgs& a, int64_t columns) {
   return kColCost * columns + (int64_t)a.seq_cost * a.batch;
 }
 
-// The first column whose cost is at least x (the column count past the end).
-MKV_DEV int64_t cost_to_col(const DecodeArgs& a, const int* pre, int64_t x) {
-  int lo = 0, hi = a.batch;  // largest b whose first column costs <= x
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (kColCost * (int64_t)lds_uniform(pre, mid) + (int64_t)a.seq_cost * mid <= x) lo = mid; else hi = mid;
+
+// The sequences holding the costs x0 and x1 (<= the stream's total): the
+// largest b < B with cost(b) = kColCost * pre[b] + seq_cost * b <= x, found
+// lane-parallel (64 sequences per LDS read, one ballot each; b = 0 always
+// qualifies), where a binary search took a chain of dependent LDS reads.
+MKV_DEV void cost_seqs(const DecodeArgs& a, const int* pre, int64_t x0, int64_t x1, int& b0, int& b1) {
+  const int lane = threadIdx.x & 63;
+  int n0 = 0, n1 = 0;
+  for (int j0 = 0; j0 < a.batch; j0 += kWave) {
+    const int j = j0 + lane;
+    bool c0 = false, c1 = false;
+    if (j < a.batch) {
+      const int64_t cj = kColCost * (int64_t)pre[j] + (int64_t)a.seq_cost * j;
+      c0 = cj <= x0;
+      c1 = cj <= x1;
+    }
+    n0 += __builtin_popcountll(__builtin_amdgcn_ballot_w64(c0));
+    n1 += __builtin_popcountll(__builtin_amdgcn_ballot_w64(c1));
   }
-  const int64_t p0 = lds_uniform(pre, lo), p1 = lds_uniform(pre, lo + 1);
-  const int64_t rem = x - kColCost * p0 - (int64_t)a.seq_cost * lo;
+  b0 = n0 - 1;
+  b1 = n1 - 1;
+}
+
+// The first column of sequence b (from cost_seqs) whose cost is at least x;
+// the sequence's column count past its end.
+MKV_DEV int64_t cost_col_in_seq(const DecodeArgs& a, const int* pre, int b, int64_t x) {
+  const int64_t p0 = lds_uniform(pre, b), p1 = lds_uniform(pre, b + 1);
+  const int64_t rem = x - kColCost * p0 - (int64_t)a.seq_cost * b;
   const int64_t g = p0 + (rem <= 0 ? 0 : (rem + kColCost - 1) / kColCost);
   return g < p1 ? g : p1;
 }
 
+// The tile of KV head kvh at column g (g < pre[B]): sequence b is the largest
+// b < B with pre[b] <= g (it has tiles), found lane-parallel as in cost_seqs.
+MKV_DEV Cursor cursor_at_par(const int* pre, const int* lens, int B, int kvh, int64_t g) {
+  const int lane = threadIdx.x & 63;
+  int n = 0;
+  for (int j0 = 0; j0 < B; j0 += kWave) {
+    const int j = j0 + lane;
+    n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(j < B && pre[j] <= g));
+  }
+  const int b = n - 1;
+  Cursor c;
+  c.b = b;
+  c.kvh = kvh;
+  const int p0 = lds_uniform(pre, b);
+  c.n = lds_uniform(pre, b + 1) - p0;
+  c.t = (int)(g - p0);
+  c.L = lds_uniform(lens, b);
+  return c;
+}
+
 // Workgroup 0 publishes, per sequence, the groups whose ranges hold its
 // first and last columns and the partial slot the first of them used (0 when
-// its range starts exactly at the sequence), for the merge kernel.
+// its range starts exactly at the sequence), for the merge kernel.  (Spread
+// over the grid, one sequence per workgroup, it delayed the first wave of
+// every workgroup instead of one workgroup: the step ran 0.3% slower.)
 MKV_DEV void publish_merge_meta(const DecodeArgs& a, const StreamSplit& sp, const int* pre) {
   int* meta = a.sk_meta + a.batch + 1;
   for (int b = threadIdx.x; b < a.batch; b += blockDim.x) {
@@ -1576,7 +1602,7 @@ MKV_DEV void publish_merge_meta(const DecodeArgs& a, const StreamSplit& sp, cons
       const int64_t base = (int64_t)a.seq_cost * b;
       glo = sp.part_of(kColCost * p0 + base);
       ghi = sp.part_of(kColCost * (p1 - 1) + base);
-      // first column of glo's range, by the same rule as cost_to_col
+      // first column of glo's range, by the same rule as cost_col_in_seq
       const int64_t x = sp.begin(glo);
       int lo = 0, hi = a.batch;
       while (hi - lo > 1) {
@@ -1596,6 +1622,17 @@ MKV_DEV void publish_merge_meta(const DecodeArgs& a, const StreamSplit& sp, cons
   for (int i = threadIdx.x; i <= a.batch; i += blockDim.x) a.sk_meta[i] = pre[i];
 }
 
+// KV head of wave slot k of a stream-K group (k = w % Hkv), and the slot of
+// KV head kvh: reversed.  With 8 KV heads a group is two workgroups, which
+// the dispatcher puts on neighbouring XCDs; the identity (first workgroup:
+// heads 0-3, the first half of every 1 KB token row) left that workgroup's
+// waves ~2.5% behind the other's on every group (per-wave timestamps), and
+// every other order measured (reversed, halves swapped, interleaved) ran
+// the batch-256 FP8 step 1.1% faster (6302 -> 6373-6380 GB/s, three A/B
+// repeats in one call).
+MKV_DEV int sk_head(int k, int hkv) { return hkv - 1 - k; }
+MKV_DEV int sk_slot(int kvh, int hkv) { return hkv - 1 - kvh; }
+
 template <int KV_DT, bool kSmallGroup, bool PAIR>
 MKV_DEV void stream_decode(const DecodeArgs& a) {
   constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
@@ -1610,17 +1647,27 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
                                     kDecWaves * a.defer * kWave * 4) + wl * a.defer * 4;
   int ndef = 0;
   const StreamSplit sp = stream_split(a, stream_cost_total(a, stream_prefix(a, pre, lens)));
-  if (blockIdx.x == 0) publish_merge_meta(a, sp, pre);
+  // Workgroup 0's waves publish the merge metadata when they leave (each
+  // lane its own sequences; pre stays in LDS), not before their first tile.
+  auto leave = [&]() {
+    if (blockIdx.x == 0) publish_merge_meta(a, sp, pre);
+  };
 
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
   const int w = blockIdx.x * kDecWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = w / a.num_kv_heads;  // this wave: KV head w % Hkv of its group's columns
-  const int kvh = w - grp * a.num_kv_heads;
-  if (grp >= sp.parts) return;
-  const int64_t g0 = cost_to_col(a, pre, sp.begin(grp));
-  const int64_t g1 = cost_to_col(a, pre, sp.end(grp));
-  if (g0 >= g1) return;
+  const int kvh = sk_head(w - grp * a.num_kv_heads, a.num_kv_heads);
+  if (grp >= sp.parts) return leave();
+  int64_t g0, g1;
+  {
+    const int64_t x0 = sp.begin(grp), x1 = sp.end(grp);
+    int b0, b1;
+    cost_seqs(a, pre, x0, x1, b0, b1);
+    g0 = cost_col_in_seq(a, pre, b0, x0);
+    g1 = cost_col_in_seq(a, pre, b1, x1);
+  }
+  if (g0 >= g1) return leave();
 
   const int row_bytes = (int)(a.idx.row_elems * kEb);
   const int64_t blk_bytes = (int64_t)row_bytes << a.idx.bs_log2;
@@ -1630,7 +1677,7 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
   const float k_mul = (KV_DT == MKV_DTYPE_FP8E4M3) ? load_uniform_f32(a.k_scale) : 1.0f;
   const bool hi = PAIR && c >= (a.group >> 1);
 
-  Cursor cc = cursor_at(pre, lens, a.batch, kvh, g0);  // tile being computed
+  Cursor cc = cursor_at_par(pre, lens, a.batch, kvh, g0);  // tile being computed
   Cursor lc = cc;                                                  // next tile to load
   int64_t lg = g0;                                                 // its global index
   PhysPair ph_next;
@@ -1740,6 +1787,7 @@ MKV_DEV void stream_decode(const DecodeArgs& a) {
       issue_finish(fs);
     }
   }
+  leave();
 }
 
 template <int KV_DT, bool kSmallGroup, bool PAIR>
@@ -1797,7 +1845,7 @@ MKV_DEV void store_out2(const DecodeArgs& a, int64_t off, float x0, float x1) {
 // the accumulator rows are read four contributors at a time (independent
 // loads in flight) with each contributor's weight taken from its lane.
 MKV_DEV int merge_slot(const DecodeArgs& a, int glo, int s0, int grp, int kvh, int h) {
-  const int wp = grp * a.num_kv_heads + kvh;
+  const int wp = grp * a.num_kv_heads + sk_slot(kvh, a.num_kv_heads);
   return ((wp * 2 + (grp == glo ? s0 : 0)) * a.group + h);
 }
 
