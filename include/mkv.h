@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MKV_ABI_VERSION 4
+#define MKV_ABI_VERSION 5
 
 /* Element dtypes (torch.float32, torch.bfloat16, torch.float16,
  * torch.float8_e4m3fn, torch.int8).  FP8 is OCP e4m3fn: max 448, no
@@ -427,6 +427,46 @@ int mkv_qkv_norm_rope_append(const void* qkv, int64_t qkv_row_stride,
                              int kv_scale_mode, float* k_scale, float* v_scale,
                              const int64_t* slot_mapping, int block_size,
                              int64_t num_blocks, int flags, void* stream);
+
+/*
+ * K6 + K2 in one launch for a decode step: one layer's producer step for the
+ * one new token of each sequence, then the decode attention over the cache
+ * that holds it.
+ *
+ * Replaces, for a decode step, mkv_qkv_norm_rope_append over the batch's
+ * qkv rows (token b of sequence b; Qwen3Attention.forward, qwen3.py:73-118,
+ * and the append of Attention.forward, attention.py:1654-1691) followed by
+ * mkv_paged_decode on its q (paged_attention_decode_quantized,
+ * attention.py:1213-1268), and gives the same bits as that pair: the same
+ * cache bytes and scales, and out equal to the decode of the producer's q
+ * with out_dtype as its dtype.  The arguments are those of the two calls
+ * (num_tokens = batch, q_out / k_out absent, split_tokens
+ * MKV_DECODE_WORKGROUP: this runs the workgroup route).  slot_mapping[b]
+ * (required; -1 or out of the pool: nothing is appended for row b) must be
+ * the cache row of position context_lens[b] - 1 of sequence b, as the
+ * reference's prepare_decode builds it (model_runner.py:621-640), and no
+ * other row of the batch may read it: the attention sees the appended row
+ * at that position only.
+ * Supported: kv_dtype FP8E4M3 with kv_scale_mode PER_TENSOR, head_dim 128,
+ * num_heads / num_kv_heads <= 8 (MKV_ERR_UNSUPPORTED_DTYPE /
+ * MKV_ERR_UNSUPPORTED_HEAD_DIM / MKV_ERR_UNSUPPORTED_GROUP otherwise, before
+ * any launch: run the two calls).  flags as mkv_qkv_norm_rope_append (the 1.0-sentinel
+ * calibration uses this call's rows).
+ */
+int mkv_qkv_norm_rope_append_decode(
+    void* out, int64_t out_batch_stride, int out_dtype,
+    const void* qkv, int64_t qkv_row_stride, int in_dtype,
+    const void* q_norm_weight, const void* k_norm_weight,
+    int norm_weight_dtype, float eps,
+    const void* cos_sin_cache, int cos_sin_dtype, int64_t max_position,
+    const int64_t* positions,
+    void* k_cache, void* v_cache, int kv_dtype, int64_t num_blocks,
+    float* k_scale, float* v_scale, int kv_scale_mode,
+    const int64_t* slot_mapping, int flags,
+    const int32_t* block_tables, int64_t bt_stride, int max_blocks,
+    const void* context_lens, int context_lens_dtype,
+    int batch, int num_heads, int num_kv_heads, int head_dim,
+    int block_size, float sm_scale, void* stream);
 
 /*
  * Decode-step metadata on the device.

@@ -36,6 +36,7 @@
 #include <mutex>
 
 #include "mkv_device.hpp"
+#include "qkv_producer.hpp"
 
 namespace mkv {
 namespace {
@@ -1030,6 +1031,267 @@ constexpr int kWgSplitWaves = 4;
 template <int KV_DT, bool PAIR>
 __global__ __launch_bounds__(kWgSplitWaves* kWave) void paged_decode_wg_qsplit_kernel(DecodeArgs a) {
   wg_decode<KV_DT, PAIR, true>(a);
+}
+
+// ---------------------------------------------------------------------------
+// A decode step's producer and attention in one launch (per-tensor FP8
+// caches, head_dim 128).  Per layer, the reference's decode step runs the
+// q/k norm, rotary embedding and append of every sequence's new token
+// (qwen3.py:73-118, attention.py:1654-1691) and then the decode attention
+// over the cache that now holds it (attention.py:1213-1268).  Here the
+// workgroup of (sequence b, KV head kvh) of the workgroup route does both:
+// its waves share out the token's q heads of the group and its K and V
+// heads kvh (one head per wave pass, 64 lanes wide, with the producer
+// kernel's operations in the producer kernel's order), put q and the FP8
+// K / V row in LDS, and append the row; the wave whose tile holds the
+// token's position takes that row from LDS instead of from the cache (the
+// tile's loads may have left before the append landed).  The result is the
+// producer kernel followed by the workgroup route, bit for bit.
+// LDS (dynamic): the workgroup merge area of wg_merge_store, then q of the
+// group's heads (fp32 [G][128]) and the new token's FP8 K row and V row
+// (128 bytes each).
+// ---------------------------------------------------------------------------
+constexpr int kFusedMaxGroup = 8;  // query heads per KV head
+
+struct ProduceDecodeArgs {
+  DecodeArgs d;    // the attention (d.q is not read: q comes from the producer step)
+  ProducerArgs p;  // the producer step of the batch's one token per sequence
+};
+
+// Replace row p (0..31, wave-uniform) of an FP8 tile, as loaded (before
+// k_exchange), with the K / V bytes at kv (128 + 128 bytes in LDS).
+MKV_DEV void patch_tile_row_fp8(Tile16<MKV_DTYPE_FP8E4M3>& T, int p, const unsigned char* kv) {
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, kg = lane >> 4;
+  const bool top = c < 8;
+  // load A of sub-tile m holds row c & 7, bytes 32kg + (top ? 0 : 16); load B
+  // row (c & 7) + 8, bytes 32kg + (top ? 16 : 0) (fp8_k_lanes)
+  const u32x4 na = *reinterpret_cast<const u32x4*>(kv + 32 * kg + (top ? 0 : 16));
+  const u32x4 nb = *reinterpret_cast<const u32x4*>(kv + 32 * kg + (top ? 16 : 0));
+  const u32x2 nv = *reinterpret_cast<const u32x2*>(kv + 128 + 8 * c);
+  const int r = p & 15;
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const bool sub = (p >> 4) == m;
+    T.k[m][0] = sub && r < 8 && (c & 7) == r ? na : T.k[m][0];
+    T.k[m][1] = sub && r >= 8 && (c & 7) == r - 8 ? nb : T.k[m][1];
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) T.v[i] = 16 * (i >> 2) + 4 * kg + (i & 3) == p ? nv : T.v[i];
+}
+
+// Raw word holding element i of a dtype-dt row at p (the element's own
+// dword for fp32, the aligned dword of its pair for 16-bit types), and the
+// element in fp32 (exact, as load8_f32 gives it).
+MKV_DEV uint32_t elem_word(const char* p, int i, int dt) {
+  return *reinterpret_cast<const uint32_t*>(p + (dt == MKV_DTYPE_F32 ? 4 * i : ((2 * i) & ~3)));
+}
+MKV_DEV float word_elem(uint32_t w, int i, int dt) {
+  const uint32_t h = (i & 1) ? w >> 16 : w & 0xffffu;
+  const float x16 = dt == MKV_DTYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+  return dt == MKV_DTYPE_F32 ? __uint_as_float(w) : x16;
+}
+
+// The FP8 code of one element at a per-tensor scale (quantize4_fp8's byte).
+MKV_DEV uint32_t fp8_code(float x, const Fp8Quant& q) {
+  const float v[4] = {x, 0.0f, 0.0f, 0.0f};
+  return quantize4_fp8(v, q) & 0xffu;
+}
+
+template <int IN_DT>
+MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
+  constexpr int KV_DT = MKV_DTYPE_FP8E4M3;
+  constexpr int kIb = DTypeInfo<IN_DT>::kBytes;
+  extern __shared__ float wg_lds[];
+  const DecodeArgs& a = f.d;
+  const ProducerArgs& pa = f.p;
+  WorkItem it = wg_item_rr(a);
+  const int nw = it.num_splits, wv = it.split;
+  const int step = 32 * nw;
+  const int lane = threadIdx.x & 63;
+  const int G = a.group;
+
+  // The producer step of token b for KV head kvh, one head per wave pass:
+  // head slot hs < G is q head kvh * G + hs, hs == G the k head, hs == G + 1
+  // the v head; wave wv takes slots wv, wv + nw, ...; lane l holds elements
+  // l and 64 + l of the slot's head (a rotary pair).  The loads of a wave's
+  // first two slots depend on nothing: they go out before anything else.
+  const char* row = pa.qkv + it.b * pa.qkv_stride * kIb;
+  auto head_row = [&](int hs) -> const char* {
+    const int head = hs < G ? it.kvh * G + hs
+                            : (hs == G ? a.num_heads + it.kvh : a.num_heads + a.num_kv_heads + it.kvh);
+    return row + (int64_t)head * kHeadDim * kIb;
+  };
+  // (no weight: the row stands in as a readable address; unused)
+  auto weight = [&](int hs) -> const char* {
+    const void* w = hs < G ? pa.q_w : pa.k_w;
+    return w ? reinterpret_cast<const char*>(w) : row;
+  };
+  struct SlotIn {
+    uint32_t x1, x2, w1, w2;
+  };
+  auto slot_loads = [&](int hs) {
+    const int h = hs < G + 2 ? hs : G + 1;
+    const char* hr = head_row(h);
+    const char* w = weight(h);
+    return SlotIn{elem_word(hr, lane, IN_DT), elem_word(hr, 64 + lane, IN_DT), elem_word(w, lane, pa.w_dtype),
+                  elem_word(w, 64 + lane, pa.w_dtype)};
+  };
+  const SlotIn in0 = slot_loads(wv), in1 = slot_loads(wv + nw);
+
+  // Scalars: the context length, the token's position and slot, the
+  // per-tensor scales (the stored values, or the calibration of this call's
+  // rows while the 1.0 sentinel is there: every wave computes the same value,
+  // as the producer kernel's waves do).
+  const int64_t L_raw = load_index(a.context_lens, it.b, a.ctx_i64);
+  const int64_t pos = pa.positions[it.b];
+  const int64_t slot = pa.slot_mapping[it.b];
+  float ks = load_uniform_f32(pa.k_scale), vs = load_uniform_f32(pa.v_scale);
+  if (pa.calibrate && (ks == 1.0f || vs == 1.0f)) {
+    const int m = lane & 7, wb = dtype_bytes(pa.w_dtype);
+    float wkl[8] = {}, wkh[8] = {};
+    if (pa.k_w) {
+      load8_f32(reinterpret_cast<const char*>(pa.k_w) + (8 * m) * wb, pa.w_dtype, wkl);
+      load8_f32(reinterpret_cast<const char*>(pa.k_w) + (64 + 8 * m) * wb, pa.w_dtype, wkh);
+    }
+    if (ks == 1.0f) ks = producer_calibrate(pa, true, pa.k_scale, IN_DT, wkl, wkh);
+    if (vs == 1.0f) vs = producer_calibrate(pa, false, pa.v_scale, IN_DT, wkl, wkh);
+  }
+  const bool append = slot >= 0 && slot < pa.num_slots;
+
+  // The wave's first tile (speculative, as in wg_decode_rr), then the cos /
+  // sin pair of the position (rotary_row's values).
+  const ItemLoad Ld = item_load_setup<KV_DT>(a, it);
+  Tile16<KV_DT> ta, tb2;
+  load_tile16<KV_DT, false>(a, it, Ld, it.t_begin, item_phys(a, it.b, it.t_begin, it.t_end), ta);
+  const bool pos_ok = pos >= 0 && pos < pa.max_position;
+  const char* csr = reinterpret_cast<const char*>(pa.cos_sin) +
+                    (pos_ok ? pos : 0) * kHeadDim * dtype_bytes(pa.cs_dtype);
+  const uint32_t cw = elem_word(csr, lane, pa.cs_dtype), sw = elem_word(csr, 64 + lane, pa.cs_dtype);
+
+  // The context length is known: the second tile's loads go out (empty past
+  // the context) before the producer's math waits for its inputs.  The new
+  // token's row is patched into the tile that holds position L - 1 when this
+  // call appends it there (slot = that position's cache row).
+  it.t_end = (int)(L_raw < 0 ? 0 : (L_raw < it.t_end ? L_raw : it.t_end));
+  const int pl = it.t_end - 1;
+  const int64_t phys_pl = pl >= 0 ? a.idx.physical_block(it.b, pl >> a.idx.bs_log2) : -1;
+  const bool patch = append && phys_pl >= 0 &&
+                     (phys_pl << a.idx.bs_log2) + (pl & ((1 << a.idx.bs_log2) - 1)) == slot;
+  PhysPair ph = item_phys(a, it.b, it.t_begin + step, it.t_end);
+  load_tile16<KV_DT, false>(a, it, Ld, it.t_begin + step, ph, tb2);
+  ph = item_phys(a, it.b, it.t_begin + 2 * step, it.t_end);
+
+  // The producer's math (produce_qk / load_v and store_kv's FP8 bytes, the
+  // same operations in the same order): q into the workgroup's q area (fp32
+  // [G][128]), the K and V codes into its 256-byte row area, and the wave of
+  // the k / v slot appends them.
+  float* qsh = wg_lds + nw * G * (kHeadDim + 2);
+  uint32_t* kvsh = reinterpret_cast<uint32_t*>(qsh + G * kHeadDim);  // [K 32 words | V 32 words]
+  const float c = pos_ok ? word_elem(cw, lane, pa.cs_dtype) : __builtin_nanf("");
+  const float sn = pos_ok ? word_elem(sw, lane, pa.cs_dtype) : __builtin_nanf("");
+  auto produce = [&](int hs, const SlotIn& in) {
+    float o1 = word_elem(in.x1, lane, IN_DT), o2 = word_elem(in.x2, lane, IN_DT);
+    if (hs <= G) {
+      float x1 = o1, x2 = o2;
+      if (hs < G ? pa.q_w != nullptr : pa.k_w != nullptr) {
+        // norm: the sum of squares in produce_qk's order (pair 8m + j of lane
+        // m, j = 0..7 in turn, then a butterfly over m)
+        const float t = __fadd_rn(__fmul_rn(x1, x1), __fmul_rn(x2, x2));
+        const int base = lane & ~7;
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = __fadd_rn(ss, __shfl(t, base + j));
+        ss = ss + __shfl_xor(ss, 8);
+        ss = ss + __shfl_xor(ss, 16);
+        ss = ss + __shfl_xor(ss, 32);
+        const float var = __fadd_rn(ss / (float)kHeadDim, pa.eps);
+        const float r = sqrtf(var);
+        x1 = round_to_dtype(__fmul_rn(x1 / r, word_elem(in.w1, lane, pa.w_dtype)), IN_DT);
+        x2 = round_to_dtype(__fmul_rn(x2 / r, word_elem(in.w2, lane, pa.w_dtype)), IN_DT);
+      }
+      o1 = round_to_dtype(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, sn)), pa.out_dtype);
+      o2 = round_to_dtype(__fadd_rn(__fmul_rn(x1, sn), __fmul_rn(x2, c)), pa.out_dtype);
+    }
+    if (hs < G) {
+      qsh[hs * kHeadDim + lane] = o1;
+      qsh[hs * kHeadDim + 64 + lane] = o2;
+    } else if (hs < G + 2) {
+      // FP8 codes of elements l and 64 + l, gathered four lanes to a word
+      const Fp8Quant qz = fp8_quant(hs == G ? ks : vs);
+      const uint32_t b1 = fp8_code(o1, qz), b2 = fp8_code(o2, qz);
+      const uint32_t w1 = b1 | (uint32_t)__shfl(b1, lane + 1) << 8 | (uint32_t)__shfl(b1, lane + 2) << 16 |
+                          (uint32_t)__shfl(b1, lane + 3) << 24;
+      const uint32_t w2 = b2 | (uint32_t)__shfl(b2, lane + 1) << 8 | (uint32_t)__shfl(b2, lane + 2) << 16 |
+                          (uint32_t)__shfl(b2, lane + 3) << 24;
+      if ((lane & 3) == 0) {
+        uint32_t* dst = kvsh + (hs == G ? 0 : 32);
+        dst[lane >> 2] = w1;
+        dst[16 + (lane >> 2)] = w2;
+        if (append) {
+          char* base = (hs == G ? pa.k_cache : pa.v_cache) + slot * a.idx.row_elems + (int64_t)it.kvh * kHeadDim;
+          *reinterpret_cast<uint32_t*>(base + lane) = w1;
+          *reinterpret_cast<uint32_t*>(base + 64 + lane) = w2;
+        }
+      }
+    }
+  };
+  produce(wv, in0);
+  produce(wv + nw, in1);
+  for (int hs = wv + 2 * nw; hs < G + 2; hs += nw) produce(hs, slot_loads(hs));
+  __syncthreads();  // q and the new K / V row are in LDS
+  const unsigned char* kv_new = reinterpret_cast<const unsigned char*>(kvsh);
+  float* qst = qsh;
+
+  auto fix = [&](Tile16<KV_DT>& T, int t0) {
+    if (patch && pl >= t0 && pl < t0 + 32) patch_tile_row_fp8(T, pl - t0, kv_new);
+  };
+  QOps<KV_DT> qop;
+  f32x4 acc[8];
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegBig, l_run = 0.0f;
+  if (it.t_begin < it.t_end) {
+    // q of head c, dims 32kg .. 32kg+31 (zeros for padding heads)
+    const int c = lane & 15, kg = lane >> 4;
+    float qf[32];
+    const float* q = qst + (c < G ? c : 0) * kHeadDim + 32 * kg;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(q + 4 * i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qf[4 * i + j] = c < G ? x[j] : 0.0f;
+    }
+    const float score_mul = q_operands<KV_DT>(a, qf, qop, ks);
+    qop.split = false;
+    zero_v_rows_past<KV_DT>(ta, it.t_begin, it.t_end);
+    fix(ta, it.t_begin);
+    compute_tile16<KV_DT, false>(ta, it.t_begin, it.t_end, qop, score_mul, acc, m_run, l_run, false);
+    for (int t0 = it.t_begin + step; t0 < it.t_end;) {
+      load_tile16<KV_DT, false>(a, it, Ld, t0 + step, ph, ta);
+      ph = item_phys(a, it.b, t0 + 2 * step, it.t_end);
+      fix(tb2, t0);
+      compute_tile16<KV_DT, false>(tb2, t0, it.t_end, qop, score_mul, acc, m_run, l_run, false);
+      t0 += step;
+      if (t0 >= it.t_end) break;
+      load_tile16<KV_DT, false>(a, it, Ld, t0 + step, ph, tb2);
+      ph = item_phys(a, it.b, t0 + 2 * step, it.t_end);
+      fix(ta, t0);
+      compute_tile16<KV_DT, false>(ta, t0, it.t_end, qop, score_mul, acc, m_run, l_run, false);
+      t0 += step;
+    }
+  } else {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the speculative loads land first
+  }
+  float l_col = l_run + __shfl_xor(l_run, 16);
+  l_col += __shfl_xor(l_col, 32);
+  wg_merge_store<false>(a, it, acc, m_run, l_col, vs);
+}
+
+template <int IN_DT>
+__global__ __launch_bounds__(kWgMaxWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
+paged_decode_wg_produce_kernel(ProduceDecodeArgs f) {
+  wg_produce_decode<IN_DT>(f);
 }
 
 // fp32 caches on the workgroup route: 16-token tiles on v_mfma_f32_16x16x4_f32
@@ -2553,4 +2815,93 @@ extern "C" int mkv_paged_decode_noalloc(void* out, int64_t out_batch_stride, con
                            num_blocks, k_scale, v_scale, kv_scale_mode, block_tables, bt_stride, max_blocks,
                            context_lens, context_lens_dtype, batch, num_heads, num_kv_heads, head_dim,
                            block_size, sm_scale, split_tokens, ws, kScratchBytes, stream, true);
+}
+
+extern "C" int mkv_qkv_norm_rope_append_decode(
+    void* out, int64_t out_batch_stride, int out_dtype, const void* qkv, int64_t qkv_row_stride,
+    int in_dtype, const void* q_norm_weight, const void* k_norm_weight, int norm_weight_dtype, float eps,
+    const void* cos_sin_cache, int cos_sin_dtype, int64_t max_position, const int64_t* positions,
+    void* k_cache, void* v_cache, int kv_dtype, int64_t num_blocks, float* k_scale, float* v_scale,
+    int kv_scale_mode, const int64_t* slot_mapping, int flags, const int32_t* block_tables,
+    int64_t bt_stride, int max_blocks, const void* context_lens, int context_lens_dtype, int batch,
+    int num_heads, int num_kv_heads, int head_dim, int block_size, float sm_scale, void* stream) {
+  DecodeArgs d;
+  KernelShape ks;
+  int fmt = 0;
+  // the attention's arguments (q is produced in the kernel: qkv stands in
+  // for its pointer in the checks)
+  int st = decode_args(out, out_batch_stride, qkv, (int64_t)num_heads * head_dim, out_dtype, k_cache, v_cache,
+                       kv_dtype, num_blocks, k_scale, v_scale, kv_scale_mode, block_tables, bt_stride, max_blocks,
+                       context_lens, context_lens_dtype, batch, num_heads, num_kv_heads, head_dim, block_size,
+                       sm_scale, MKV_DECODE_WORKGROUP, d, ks, fmt);
+  if (st != MKV_OK) return st;
+  if (head_dim != kHeadDim || ks.pair) return MKV_ERR_UNSUPPORTED_HEAD_DIM;
+  if (fmt != MKV_DTYPE_FP8E4M3) return MKV_ERR_UNSUPPORTED_DTYPE;
+  if (d.group > kFusedMaxGroup) return MKV_ERR_UNSUPPORTED_GROUP;
+  // the producer's arguments
+  if (max_position <= 0) return MKV_ERR_BAD_SHAPE;
+  if (!cos_sin_cache || !positions || !slot_mapping) return MKV_ERR_NULL_POINTER;
+  auto is_float = [](int dt) { return dt == MKV_DTYPE_F32 || dt == MKV_DTYPE_BF16 || dt == MKV_DTYPE_F16; };
+  if (!is_float(in_dtype) || !is_float(cos_sin_dtype) ||
+      ((q_norm_weight || k_norm_weight) && !is_float(norm_weight_dtype)))
+    return MKV_ERR_UNSUPPORTED_DTYPE;
+  if (flags & ~MKV_APPEND_CALIBRATE_SENTINEL) return MKV_ERR_BAD_SHAPE;
+  if (qkv_row_stride < (int64_t)(num_heads + 2 * num_kv_heads) * head_dim) return MKV_ERR_BAD_STRIDE;
+  const int ib = in_dtype == MKV_DTYPE_F32 ? 4 : 2;
+  const int cb = cos_sin_dtype == MKV_DTYPE_F32 ? 4 : 2;
+  const int wb = norm_weight_dtype == MKV_DTYPE_F32 ? 4 : 2;
+  auto misaligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; };
+  if ((qkv_row_stride * ib) % 16 || misaligned(cos_sin_cache) || (head_dim * cb) % 16 ||
+      (q_norm_weight && misaligned(q_norm_weight)) || (k_norm_weight && misaligned(k_norm_weight)) ||
+      (head_dim / 2 * wb) % 16)
+    return MKV_ERR_MISALIGNED;
+  if (batch == 0) return MKV_OK;
+
+  ProduceDecodeArgs f;
+  f.d = d;
+  f.d.q = nullptr;
+  f.d.split_tokens = 0;
+  f.d.max_splits = 0;
+  ProducerArgs& p = f.p;
+  p = ProducerArgs{};
+  p.qkv = reinterpret_cast<const char*>(qkv);
+  p.qkv_stride = qkv_row_stride;
+  p.num_tokens = batch;
+  p.num_heads = num_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.head_dim = head_dim;
+  p.q_w = q_norm_weight;
+  p.k_w = k_norm_weight;
+  p.w_dtype = norm_weight_dtype;
+  p.eps = eps;
+  p.cos_sin = cos_sin_cache;
+  p.cs_dtype = cos_sin_dtype;
+  p.max_position = max_position;
+  p.positions = positions;
+  p.out_dtype = out_dtype;
+  p.k_cache = reinterpret_cast<char*>(k_cache);
+  p.v_cache = reinterpret_cast<char*>(v_cache);
+  p.cache_dtype = kv_dtype;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.calibrate = (flags & MKV_APPEND_CALIBRATE_SENTINEL) ? 1 : 0;
+  p.slot_mapping = slot_mapping;
+  p.num_slots = num_blocks * (int64_t)block_size;
+
+  const int nw = wg_waves(batch, d.num_kv_heads, d.group, max_blocks, block_size, device_cus());
+  const size_t lds = ((size_t)nw * d.group * (kHeadDim + 2) + (size_t)d.group * kHeadDim) * sizeof(float) + 256;
+  const dim3 grid((unsigned)((int64_t)batch * d.num_kv_heads)), block(nw * kWave);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (in_dtype) {
+    case MKV_DTYPE_BF16:
+      hipLaunchKernelGGL(paged_decode_wg_produce_kernel<MKV_DTYPE_BF16>, grid, block, lds, s, f);
+      break;
+    case MKV_DTYPE_F16:
+      hipLaunchKernelGGL(paged_decode_wg_produce_kernel<MKV_DTYPE_F16>, grid, block, lds, s, f);
+      break;
+    default:
+      hipLaunchKernelGGL(paged_decode_wg_produce_kernel<MKV_DTYPE_F32>, grid, block, lds, s, f);
+      break;
+  }
+  return (int)hipGetLastError();
 }

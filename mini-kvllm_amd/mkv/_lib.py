@@ -14,7 +14,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmkv.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -72,6 +72,11 @@ SIGNATURES: dict[str, tuple] = {
         c_void_p, c_int64, c_int, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_int, c_float,
         c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int,
         c_int, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int, c_void_p]),
+    "mkv_qkv_norm_rope_append_decode": (c_int, [
+        c_void_p, c_int64, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_int, c_float,
+        c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_void_p,
+        c_void_p, c_int, c_void_p, c_int, c_void_p, c_int64, c_int, c_void_p, c_int, c_int,
+        c_int, c_int, c_int, c_int, c_float, c_void_p]),
     "mkv_decode_metadata": (c_int, [
         c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int64, c_int, c_int, c_int,
         c_void_p]),

@@ -39,7 +39,7 @@ from . import _lib
 from . import context as C
 from .attention import DECODE_STREAM, DECODE_WORKGROUP, Attention, _dtype_code, _stream
 from .decode_state import DecodeGraphs, DecodeMetadata
-from .producer import qkv_norm_rope_append
+from .producer import qkv_norm_rope_append, qkv_norm_rope_append_decode
 
 
 # ---------------------------------------------------------------------------
@@ -344,12 +344,23 @@ class Qwen3Model(torch.nn.Module):
                 h = rms_norm(x, lay["in_norm"], cfg.eps, residual)
             qkv = F.linear(h, lay["qkv"])
             att = lay["attn"]
-            q, k, v = qkv_norm_rope_append(
-                qkv, positions, Hq, Hkv, D, self.cos_sin, att.k_cache, att.v_cache, slot_mapping,
-                self.block_size, q_norm_weight=lay["q_norm"], k_norm_weight=lay["k_norm"],
-                eps=cfg.eps, kv_cache_dtype=att.kv_cache_dtype, k_scale=att.k_scale,
-                v_scale=att.v_scale, return_k=full_prefill)
-            o = self.attention(li, q, k, v)
+            ctx = C.current_context()
+            if not ctx.is_prefill and att.kv_cache_dtype == "fp8_per_tensor":
+                # a decode step: the producer step and the attention in one
+                # launch where the decode schedule allows it
+                o = qkv_norm_rope_append_decode(
+                    qkv, positions, Hq, Hkv, D, self.cos_sin, att.k_cache, att.v_cache, slot_mapping,
+                    self.block_size, ctx.block_tables, ctx.context_lens,
+                    att.scale / (D ** 0.5), q_norm_weight=lay["q_norm"], k_norm_weight=lay["k_norm"],
+                    eps=cfg.eps, kv_cache_dtype=att.kv_cache_dtype, k_scale=att.k_scale,
+                    v_scale=att.v_scale, split_tokens=att.decode_split_tokens).reshape(-1, Hq * D)
+            else:
+                q, k, v = qkv_norm_rope_append(
+                    qkv, positions, Hq, Hkv, D, self.cos_sin, att.k_cache, att.v_cache, slot_mapping,
+                    self.block_size, q_norm_weight=lay["q_norm"], k_norm_weight=lay["k_norm"],
+                    eps=cfg.eps, kv_cache_dtype=att.kv_cache_dtype, k_scale=att.k_scale,
+                    v_scale=att.v_scale, return_k=full_prefill)
+                o = self.attention(li, q, k, v)
             x = F.linear(o, lay["o"])
             h = rms_norm(x, lay["post_norm"], cfg.eps, residual)
             x = F.linear(silu_and_mul(F.linear(h, lay["gate_up"])), lay["down"])

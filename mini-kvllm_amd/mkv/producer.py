@@ -14,9 +14,9 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .attention import (PER_TOKEN_HEAD_MODES, _DTYPES, _append, _check_cache,
-                        _check_token_scales, _dtype_code, _require_gpu, _stream,
-                        calibrate_fp8_per_tensor)
+from .attention import (PER_TOKEN_HEAD_MODES, _DTYPES, _append, _block_table, _check_cache,
+                        _check_token_scales, _ctx_lens, _decode, _dtype_code, _index_dtype, _require_gpu,
+                        _stream, calibrate_fp8_per_tensor)
 
 
 def qkv_norm_rope_append(qkv: torch.Tensor, positions: torch.Tensor, num_heads: int,
@@ -124,3 +124,98 @@ def qkv_norm_rope_append(qkv: torch.Tensor, positions: torch.Tensor, num_heads: 
         slots.data_ptr() if append else None, block_size,
         k_cache.shape[0] if append else 0, flags, _stream(dev))
     return q, k, v
+
+
+def qkv_norm_rope_append_decode(qkv: torch.Tensor, positions: torch.Tensor, num_heads: int,
+                                num_kv_heads: int, head_dim: int, cos_sin_cache: torch.Tensor,
+                                k_cache: torch.Tensor, v_cache: torch.Tensor,
+                                slot_mapping: torch.Tensor, block_size: int,
+                                block_tables: torch.Tensor, context_lens: torch.Tensor,
+                                scale: float, *, q_norm_weight: torch.Tensor | None = None,
+                                k_norm_weight: torch.Tensor | None = None, eps: float = 1e-5,
+                                kv_cache_dtype: str = "auto", k_scale: torch.Tensor | None = None,
+                                v_scale: torch.Tensor | None = None,
+                                out_dtype: torch.dtype | None = None, split_tokens: int = 0,
+                                out: torch.Tensor | None = None) -> torch.Tensor:
+    """One layer's decode step from its qkv rows: the producer step of
+    :func:`qkv_norm_rope_append` for the batch's one new token per sequence
+    (row b of qkv is sequence b's token, appended at slot_mapping[b]), then
+    the decode attention over the paged cache (mkv.attention's decode with
+    split_tokens) on the produced q.  Returns the attention output
+    (batch, num_heads, head_dim) in out_dtype (default: qkv's dtype).
+
+    For a per-tensor FP8 cache at head_dim 128 with at most 8 query heads
+    per KV head, whose scales are calibrated,
+    when the decode schedule is the workgroup route (the library's choice for
+    the shape, or split_tokens = DECODE_WORKGROUP), both run in one launch
+    (``mkv_qkv_norm_rope_append_decode``, the same bits as the two calls);
+    otherwise as the two calls.  slot_mapping[b] must be the cache row of
+    position context_lens[b] - 1 of sequence b (or -1), as a decode step's
+    metadata has it."""
+    T = qkv.shape[0] if qkv.dim() == 2 else -1
+    out_dtype = out_dtype or qkv.dtype
+    fused = (kv_cache_dtype == "fp8_per_tensor" and head_dim == 128 and T > 0
+             and num_heads % num_kv_heads == 0 and num_heads // num_kv_heads <= 8
+             and k_cache is not None and k_cache.dtype == torch.float8_e4m3fn
+             and getattr(k_scale, "_mkv_calibrated", False) and getattr(v_scale, "_mkv_calibrated", False))
+    if fused:
+        bt = _block_table(block_tables)
+        cl = _ctx_lens(context_lens)
+        route = split_tokens
+        if split_tokens == 0:
+            route = (_lib.DECODE_WORKGROUP
+                     if _lib.query("mkv_paged_decode_route", T, num_heads, num_kv_heads, bt.shape[1],
+                                   k_cache.shape[1], head_dim, _lib.DTYPE_FP8E4M3, 0, 0)
+                     == _lib.ROUTE_WORKGROUP else 0)
+        fused = route == _lib.DECODE_WORKGROUP
+    if not fused:
+        q, _, _ = qkv_norm_rope_append(
+            qkv, positions, num_heads, num_kv_heads, head_dim, cos_sin_cache, k_cache, v_cache,
+            slot_mapping, block_size, q_norm_weight=q_norm_weight, k_norm_weight=k_norm_weight,
+            eps=eps, kv_cache_dtype=kv_cache_dtype, k_scale=k_scale, v_scale=v_scale,
+            out_dtype=out_dtype)
+        quant = kv_cache_dtype != "auto"
+        return _decode(q, k_cache, v_cache, block_tables, context_lens, scale, num_heads,
+                       num_kv_heads, head_dim, k_scale if quant else None, v_scale if quant else None,
+                       split_tokens=split_tokens, out=out,
+                       per_token_head=kv_cache_dtype in PER_TOKEN_HEAD_MODES)
+
+    width = (num_heads + 2 * num_kv_heads) * head_dim
+    if qkv.shape[1] < width or qkv.stride(1) != 1:
+        raise ValueError(f"qkv rows must hold {width} contiguous elements")
+    dev = _require_gpu(qkv, positions, cos_sin_cache, k_cache, v_cache, block_tables, context_lens)
+    _check_cache(k_cache, v_cache, num_kv_heads, head_dim)
+    pos = positions.to(torch.int64).contiguous()
+    slots = slot_mapping.to(torch.int64).contiguous()
+    if pos.numel() < T or slots.numel() < T:
+        raise ValueError(f"positions / slot_mapping cover fewer than the batch's {T} rows")
+    if bt.dim() != 2 or bt.shape[0] < T or cl.numel() < T:
+        raise ValueError(f"block_tables {tuple(bt.shape)} / context_lens {tuple(cl.shape)} cover fewer "
+                         f"than the batch's {T} sequences")
+    cs = cos_sin_cache.contiguous()
+    if cs.shape[-1] != head_dim:
+        raise ValueError(f"cos_sin_cache must be (max_position, {head_dim})")
+    wdt = None
+    for w in (q_norm_weight, k_norm_weight):
+        if w is not None:
+            if w.numel() != head_dim or not w.is_contiguous():
+                raise ValueError(f"norm weights must be contiguous ({head_dim},)")
+            wdt = w.dtype
+    if q_norm_weight is not None and k_norm_weight is not None and q_norm_weight.dtype != k_norm_weight.dtype:
+        raise TypeError("q_norm_weight and k_norm_weight must share a dtype")
+    if out is None:
+        out = torch.empty(T, num_heads, head_dim, dtype=out_dtype, device=dev)
+    elif out.dtype != out_dtype or tuple(out.shape) != (T, num_heads, head_dim) or out.stride(2) != 1:
+        raise ValueError(f"out must be ({T}, {num_heads}, {head_dim}) {out_dtype}")
+    _lib.call(
+        "mkv_qkv_norm_rope_append_decode", out.data_ptr(), out.stride(0), _dtype_code(out, "out"),
+        qkv.data_ptr(), qkv.stride(0), _dtype_code(qkv, "qkv"),
+        q_norm_weight.data_ptr() if q_norm_weight is not None else None,
+        k_norm_weight.data_ptr() if k_norm_weight is not None else None,
+        _DTYPES.get(wdt, 0) if wdt is not None else 0, float(eps), cs.data_ptr(),
+        _dtype_code(cs, "cos_sin_cache"), cs.shape[0], pos.data_ptr(), k_cache.data_ptr(),
+        v_cache.data_ptr(), _lib.DTYPE_FP8E4M3, k_cache.shape[0], k_scale.data_ptr(),
+        v_scale.data_ptr(), _lib.SCALE_PER_TENSOR, slots.data_ptr(), _lib.APPEND_CALIBRATE_SENTINEL,
+        bt.data_ptr(), bt.stride(0), bt.shape[1], cl.data_ptr(), _index_dtype(cl), T, num_heads,
+        num_kv_heads, head_dim, k_cache.shape[1], float(scale), _stream(dev))
+    return out
