@@ -744,6 +744,40 @@ def configs_extra(dev, stream, cpu: bool = True, which=DECODE_CONFIGS) -> dict:
             us = graph_time_us(fn)
             row[name] = {"us": round(us, 2), "GBps": round(nb / us / 1e3, 1),
                          "frac_of_8000_GBps": round(nb / us / 1e3 / PEAK_HBM_GBPS, 4)}
+        # The whole decode step of one layer from its qkv rows (bf16): the
+        # producer (q/k RMSNorm, rotary embedding, FP8 append at each row's
+        # last position) and the attention, as two calls and in one launch
+        from mkv import producer as P
+
+        qkv = (torch.randn(60, 32 * HEAD_DIM, generator=g)).to(torch.bfloat16).to(dev)
+        inv = 1000000.0 ** (-torch.arange(0, HEAD_DIM, 2, dtype=torch.float64) / HEAD_DIM)
+        ang = torch.arange(4096, dtype=torch.float64)[:, None] * inv[None, :]
+        cs = torch.cat([ang.cos(), ang.sin()], dim=1).to(torch.bfloat16).to(dev)  # [cos | sin] rows
+        nw_ = (torch.rand(HEAD_DIM, generator=g) + 0.5).to(torch.bfloat16).to(dev)
+        pos = (ctx - 1).to(dev)
+        btc = bt.cpu()
+        slots = torch.tensor([int(btc[b, (int(ctx[b]) - 1) // 256]) * 256 + (int(ctx[b]) - 1) % 256
+                              for b in range(60)], device=dev)
+        sc._mkv_calibrated = True
+
+        def producer_step():
+            return P.qkv_norm_rope_append(qkv, pos, 16, 8, HEAD_DIM, cs, kp, vp, slots, 256, q_norm_weight=nw_,
+                                          k_norm_weight=nw_, kv_cache_dtype="fp8_per_tensor", k_scale=sc,
+                                          v_scale=sc)[0]
+
+        def two_calls():
+            A._decode(producer_step(), kp, vp, bt, ctxd, 0.088, 16, 8, HEAD_DIM, sc, sc, out=out)
+
+        def one_launch():
+            P.qkv_norm_rope_append_decode(qkv, pos, 16, 8, HEAD_DIM, cs, kp, vp, slots, 256, bt, ctxd, 0.088,
+                                          q_norm_weight=nw_, k_norm_weight=nw_, kv_cache_dtype="fp8_per_tensor",
+                                          k_scale=sc, v_scale=sc, out=out)
+        row["decode_step_from_qkv"] = {
+            "what": "producer (q/k norm, rotary, FP8 append of each row's new token) + attention, "
+                    "library schedule",
+            "two_calls_us": round(graph_time_us(two_calls), 2),
+            "one_launch_us": round(graph_time_us(one_launch), 2),
+            "producer_alone_us": round(graph_time_us(producer_step), 2)}
         res["fp8_decode_b60_engine_shape"] = row
         del kp, vp
 
