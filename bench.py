@@ -983,6 +983,8 @@ def _torch_attention_model():
     from mkv import engine as E
 
     class TorchAttentionModel(E.Qwen3Model):
+        fuse_decode_step = False  # every step's attention through attention() below
+
         def attention(self, li, q, k, v):
             ctx = C.current_context()
             att = self.layers[li]["attn"]

@@ -1191,13 +1191,14 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
   const float c = pos_ok ? word_elem(cw, lane, pa.cs_dtype) : __builtin_nanf("");
   const float sn = pos_ok ? word_elem(sw, lane, pa.cs_dtype) : __builtin_nanf("");
   auto produce = [&](int hs, const SlotIn& in) {
+    // (products that feed a sum through mul_rn, as in norm_rope)
     float o1 = word_elem(in.x1, lane, IN_DT), o2 = word_elem(in.x2, lane, IN_DT);
     if (hs <= G) {
       float x1 = o1, x2 = o2;
       if (hs < G ? pa.q_w != nullptr : pa.k_w != nullptr) {
         // norm: the sum of squares in produce_qk's order (pair 8m + j of lane
         // m, j = 0..7 in turn, then a butterfly over m)
-        const float t = __fadd_rn(__fmul_rn(x1, x1), __fmul_rn(x2, x2));
+        const float t = __fadd_rn(mul_rn(x1, x1), mul_rn(x2, x2));
         const int base = lane & ~7;
         float ss = 0.0f;
 #pragma unroll
@@ -1205,13 +1206,13 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
         ss = ss + __shfl_xor(ss, 8);
         ss = ss + __shfl_xor(ss, 16);
         ss = ss + __shfl_xor(ss, 32);
-        const float var = __fadd_rn(ss / (float)kHeadDim, pa.eps);
+        const float var = __fadd_rn(ss / (float)pa.head_dim, pa.eps);  // (a division, as in norm_rope)
         const float r = sqrtf(var);
         x1 = round_to_dtype(__fmul_rn(x1 / r, word_elem(in.w1, lane, pa.w_dtype)), IN_DT);
         x2 = round_to_dtype(__fmul_rn(x2 / r, word_elem(in.w2, lane, pa.w_dtype)), IN_DT);
       }
-      o1 = round_to_dtype(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, sn)), pa.out_dtype);
-      o2 = round_to_dtype(__fadd_rn(__fmul_rn(x1, sn), __fmul_rn(x2, c)), pa.out_dtype);
+      o1 = round_to_dtype(__fsub_rn(mul_rn(x1, c), mul_rn(x2, sn)), pa.out_dtype);
+      o2 = round_to_dtype(__fadd_rn(mul_rn(x1, sn), mul_rn(x2, c)), pa.out_dtype);
     }
     if (hs < G) {
       qsh[hs * kHeadDim + lane] = o1;

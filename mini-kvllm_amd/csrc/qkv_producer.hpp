@@ -96,20 +96,33 @@ MKV_DEV float head_max(float v, int lanes) {
   return v;
 }
 
+// An fp32 product rounded on its own.  hipcc compiles with
+// -ffp-contract=fast, which fuses a product into the sum that consumes it
+// (one FMA, one rounding) whatever the source asks for (__fmul_rn is the
+// plain operator, and `#pragma clang fp contract(off)` is not honoured); an
+// empty asm statement on the product hides its origin from that fusion and
+// emits nothing.
+MKV_DEV float mul_rn(float x, float y) {
+  float p = x * y;
+  asm volatile("" : "+v"(p));
+  return p;
+}
+
 // Norm (if a weight is given) and rotation of the lane's 8 + 8 elements x1
 // (offsets 8m..) and x2 (D/2 + 8m..) of a q/k head, in fp32 after rounding
 // to out_dtype: the value of the reference's rotated tensor.
 //   norm:   y = round_in(x / sqrt(sum(x^2) / D + eps) * w)
 //   rotary: o1 = y1 * cos - y2 * sin, o2 = y1 * sin + y2 * cos  (no FMA)
 // (the head's D/16 lanes must run it together: the sum of squares is a
-// shuffle reduction over them)
+// shuffle reduction over them).  Every product that feeds a sum goes
+// through mul_rn, so that it is rounded before the sum as in the reference.
 MKV_DEV void norm_rope(const ProducerArgs& a, float (&x1)[8], float (&x2)[8], const void* w,
                        const float (&wl)[8], const float (&wh)[8], const float (&c)[8], const float (&s)[8],
                        int in_dt, float (&o1)[8], float (&o2)[8]) {
   if (w) {
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ss = __fadd_rn(ss, __fadd_rn(__fmul_rn(x1[j], x1[j]), __fmul_rn(x2[j], x2[j])));
+    for (int j = 0; j < 8; ++j) ss = __fadd_rn(ss, __fadd_rn(mul_rn(x1[j], x1[j]), mul_rn(x2[j], x2[j])));
     ss = head_sum(ss, a.head_dim / 16);
     const float var = __fadd_rn(ss / (float)a.head_dim, a.eps);
     const float r = sqrtf(var);
@@ -121,8 +134,8 @@ MKV_DEV void norm_rope(const ProducerArgs& a, float (&x1)[8], float (&x2)[8], co
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    o1[j] = round_to_dtype(__fsub_rn(__fmul_rn(x1[j], c[j]), __fmul_rn(x2[j], s[j])), a.out_dtype);
-    o2[j] = round_to_dtype(__fadd_rn(__fmul_rn(x1[j], s[j]), __fmul_rn(x2[j], c[j])), a.out_dtype);
+    o1[j] = round_to_dtype(__fsub_rn(mul_rn(x1[j], c[j]), mul_rn(x2[j], s[j])), a.out_dtype);
+    o2[j] = round_to_dtype(__fadd_rn(mul_rn(x1[j], s[j]), mul_rn(x2[j], c[j])), a.out_dtype);
   }
 }
 

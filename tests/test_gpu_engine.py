@@ -60,7 +60,10 @@ def test_captured_decode_generates_the_eager_tokens(dev, kv):
 
 class OracleAttentionModel(E.Qwen3Model):
     """The same model with the oracle's attention on the CPU in float64 over
-    the layer's own (dequantised) cache."""
+    the layer's own (dequantised) cache, on every step (decode steps too:
+    no fused producer + attention call)."""
+
+    fuse_decode_step = False
 
     def attention(self, li, q, k, v):
         ctx = C.current_context()
@@ -213,3 +216,52 @@ def test_engine_logits_full_shape_match_the_oracle_attention_engine(dev, monkeyp
     assert kinds.count("mixed") >= 2 and kinds.count("decode") >= 4, kinds
     assert all(float(s) != 1.0 for s in eng.model.scales()), "scales calibrated"
     print(f"max logit difference over {compared} steps: {worst:.2e}; steps {kinds}")
+
+
+class UnfusedModel(E.Qwen3Model):
+    """The engine's model with each decode step's producer step and attention
+    as two calls."""
+
+    fuse_decode_step = False
+
+
+@pytest.mark.parametrize("use_graphs", [True, False])
+def test_fused_decode_steps_give_the_unfused_logits(dev, monkeypatch, use_graphs):
+    """The end-to-end workload's shape (2 layers, bf16 weights, FP8 per-tensor
+    KV, 8 prompts of 32-512 tokens): with each decode step's producer step
+    and attention in one launch (mkv_qkv_norm_rope_append_decode), every
+    step's logits are bit-identical to the two calls' and so are the
+    generated tokens, captured or eager."""
+    announce(f"engine: fused decode steps vs two calls, graphs {use_graphs}")
+    from mkv import _lib
+
+    names = []
+    real_call = _lib.call
+
+    def spy(name, *args):
+        names.append(name)
+        return real_call(name, *args)
+
+    monkeypatch.setattr(_lib, "call", spy)
+    g = torch.Generator().manual_seed(56)
+    lens = [int(x) for x in torch.randint(32, 513, (8,), generator=g)]
+    prompts = [torch.randint(0, FULL.vocab_size, (L,), generator=g).tolist() for L in lens]
+    eng = _full_engine(dev, E.Qwen3Model, use_graphs, torch.bfloat16)
+    ref = _full_engine(dev, UnfusedModel, use_graphs, torch.bfloat16)
+    for e in (eng, ref):
+        for p in prompts:
+            e.add_request(p, max_tokens=8)
+    kinds, compared = [], 0
+    for step in range(40):
+        if eng.sched.done():
+            break
+        eng.step()
+        ref.step()
+        kinds.append(eng.stats[-1].kind)
+        assert eng.last_sampled == ref.last_sampled, f"step {step}: tokens differ"
+        if eng.last_sampled:
+            assert torch.equal(eng.last_logits, ref.last_logits), f"step {step} ({kinds[-1]}): logits differ"
+            compared += 1
+    assert eng.sched.done() and ref.sched.done()
+    assert "decode" in kinds and compared >= 6, kinds
+    assert "mkv_qkv_norm_rope_append_decode" in names, "the fused call never ran"

@@ -125,6 +125,17 @@ def test_fused_decode_step_engine_shape(dev):
     _assert_same(_fused(c), _two_calls(c))
 
 
+def test_fused_decode_step_large_batch(dev):
+    """256 rows (0.5 M q elements): enough products and sums that an FMA the
+    compiler fused in one of the two paths and not in the other would show
+    (every product and sum is rounded on its own in both)."""
+    announce("fused decode step, batch 256")
+    g = torch.Generator().manual_seed(12)
+    ctx = torch.randint(1, 801, (256,), generator=g)
+    c = _case(dev, 12, 256, 16, 8, 256, torch.bfloat16, ctx=ctx, no_slot=(7, 100))
+    _assert_same(_fused(c), _two_calls(c))
+
+
 def test_fused_decode_step_calibrates_a_sentinel_scale(dev):
     """Scales still holding the 1.0 sentinel: the call calibrates them from
     its rows (every workgroup computes the same value), appends with them and
