@@ -1563,13 +1563,17 @@ MKV_DEV void finish_sk(const DecodeArgs& a, const Cursor& c, bool whole, int w, 
   }
 }
 
-// Finish of an item for groups of at most 4 query heads, issued as exactly
-// three buffer stores on every pipeline step (an unused store gets an empty
-// range and writes nothing), for the same reason as load_q_stage's need flag.
-// Heads live in lane group 0 (head r in acc[.][r]); four shuffles per output
-// register spread head r to lane group r, so one 16-byte store per lane covers
-// all heads.  Store A/B: the output (bf16/fp16: A only; fp32: A and B) or the
-// fp32 partial accumulator; store C: the partial's (m, l).
+// Finish of an item for groups of at most 4 query heads (8 with head
+// pairing, whose heads own 64 dims each), issued as exactly three buffer
+// stores on every pipeline step (an unused store gets an empty range and
+// writes nothing), for the same reason as load_q_stage's need flag.  Heads
+// live in lane group 0 (head r in acc[.][r]; with pairing head j in lane
+// group j / 4, its own dims in lanes c < 8 or c >= 8); four shuffles per
+// output register spread them so that every lane holds 8 dims of one head
+// (lane group h: head h, or with pairing lane 8j + d: head j, its own dims
+// 8d ..), and one 16-byte store per lane covers all heads.  Store A/B: the
+// output (bf16/fp16: A only; fp32: A and B) or the fp32 partial accumulator;
+// store C: the partial's (m, l).
 struct FinishStores {
   __amdgpu_buffer_rsrc_t ra, rc;
   uint32_t oa, ob, oc;
@@ -1607,34 +1611,51 @@ MKV_DEV void finish_small_group(const DecodeArgs& a, const Cursor& c, bool whole
                                 const f32x4 (&acc)[8], float m_col, float l_col, float v_mul,
                                 FinishStores& f) {
   const int lane = threadIdx.x & 63;
-  const int cc = lane & 15, h = lane >> 4;  // this lane's head after the spread
+  // this lane's head after the spread, the lane holding its dims, its
+  // register among acc[.][0..3], and the dims' offsets in the output row and
+  // in the partial slots (head-major, 128 floats per head)
+  int h, src, sel, out_off, part_off;
+  if constexpr (PAIR) {
+    h = lane >> 3;
+    const int d = lane & 7;
+    const bool hi = h >= (a.group >> 1);
+    src = 16 * (h >> 2) + (hi ? 8 : 0) + d;
+    sel = h & 3;
+    out_off = h * kQDim<PAIR> + 8 * d;
+    part_off = h * kHeadDim + (hi ? 64 : 0) + 8 * d;
+  } else {
+    h = lane >> 4;
+    src = lane & 15;
+    sel = h;
+    out_off = h * kQDim<PAIR> + 8 * src;
+    part_off = h * kHeadDim + 8 * src;
+  }
   float x[8];
 #pragma unroll
   for (int mm = 0; mm < 8; ++mm) {
-    const float t0 = __shfl(acc[mm][0], cc), t1 = __shfl(acc[mm][1], cc);
-    const float t2 = __shfl(acc[mm][2], cc), t3 = __shfl(acc[mm][3], cc);
-    x[mm] = h == 0 ? t0 : (h == 1 ? t1 : (h == 2 ? t2 : t3));
+    const float t0 = __shfl(acc[mm][0], src), t1 = __shfl(acc[mm][1], src);
+    const float t2 = __shfl(acc[mm][2], src), t3 = __shfl(acc[mm][3], src);
+    x[mm] = sel == 0 ? t0 : (sel == 1 ? t1 : (sel == 2 ? t2 : t3));
   }
   const float lh = __shfl(l_col, h);
   const float mh = __shfl(m_col, h);
   const bool valid = h < a.group;
+  const bool first = PAIR ? (lane & 7) == 0 : (lane & 15) == 0;  // stores the head's (m, l)
   if (whole) {
     const float inv = lh > 0.0f ? v_mul / lh : 0.0f;
 #pragma unroll
     for (int mm = 0; mm < 8; ++mm) x[mm] *= inv;
     const int ob = a.q_dtype == MKV_DTYPE_F32 ? 4 : 2;
     finish_rsrc<PAIR>(a, true, c.b, c.kvh, w, k, f);
-    int col0;
-    const bool own = out_cols<PAIR>(a.group, h, cc, col0);
-    const uint32_t off = (uint32_t)((h * kQDim<PAIR> + col0) * ob);
+    const uint32_t off = (uint32_t)(out_off * ob);
     if (a.q_dtype == MKV_DTYPE_F32) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         f.da[j] = __float_as_uint(x[j]);
         f.db[j] = __float_as_uint(x[4 + j]);
       }
-      f.oa = valid && own ? off : kOob;
-      f.ob = valid && own ? off + 16 : kOob;
+      f.oa = valid ? off : kOob;
+      f.ob = valid ? off + 16 : kOob;
     } else {
       const bool bf = a.q_dtype == MKV_DTYPE_BF16;
 #pragma unroll
@@ -1643,22 +1664,24 @@ MKV_DEV void finish_small_group(const DecodeArgs& a, const Cursor& c, bool whole
         const uint32_t hi = bf ? f32_to_bf16_bits(x[2 * j + 1]) : f32_to_f16_bits(x[2 * j + 1]);
         f.da[j] = lo | (hi << 16);
       }
-      f.oa = valid && own ? off : kOob;
+      f.oa = valid ? off : kOob;
       f.ob = kOob;
     }
     f.oc = kOob;
   } else {
+    // (with pairing only the head's own half of its 128-float slot is
+    // written; the merge kernel stores only that half)
     finish_rsrc<PAIR>(a, false, c.b, c.kvh, w, k, f);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       f.da[j] = __float_as_uint(x[j]);
       f.db[j] = __float_as_uint(x[4 + j]);
     }
-    const uint32_t off = (uint32_t)((h * kHeadDim + 8 * cc) * 4);
+    const uint32_t off = (uint32_t)(part_off * 4);
     f.oa = valid ? off : kOob;
     f.ob = valid ? off + 16 : kOob;
     f.dc = u32x2{__float_as_uint(mh), __float_as_uint(lh)};
-    f.oc = valid && cc == 0 ? (uint32_t)(h * 8) : kOob;
+    f.oc = valid && first ? (uint32_t)(h * 8) : kOob;
   }
 }
 
@@ -2537,7 +2560,8 @@ int launch_route(DecodeArgs& a, int route, int fmt, int split_tokens, int max_bl
     if (workspace_bytes < need) return MKV_ERR_WORKSPACE_TOO_SMALL;
     if (reinterpret_cast<uintptr_t>(workspace) & 15u) return MKV_ERR_MISALIGNED;
     // (held finishes: the kernels for groups of at most 4 query heads)
-    a.defer = batch <= kStreamDeferMaxBatch && group <= 4 ? kStreamDefer : 0;
+    const bool small = group <= (PAIR ? 8 : 4);  // finish_small_group's heads
+    a.defer = batch <= kStreamDeferMaxBatch && small ? kStreamDefer : 0;
 
     const size_t lds = stream_lds_bytes(batch, a.defer);
     // Workspace slots are laid out for the largest grid (stream_waves()).
@@ -2553,7 +2577,6 @@ int launch_route(DecodeArgs& a, int route, int fmt, int split_tokens, int max_bl
     // once per device for batches up to kStreamSmallBatch and once for larger.
     const int lds_bucket = batch <= kStreamSmallBatch ? 0 : 1;
     const size_t lds_bound = lds_bucket ? kStreamMaxLds : kStreamSmallLds;
-    const bool small = group <= 4;
     switch (fmt) {
       case MKV_DTYPE_FP8E4M3:
         small ? launch_stream<MKV_DTYPE_FP8E4M3, true, PAIR>(a, lds_bucket, lds_bound, lds, s)
