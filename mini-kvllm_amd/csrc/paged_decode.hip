@@ -1058,14 +1058,27 @@ struct ProduceDecodeArgs {
   ProducerArgs p;  // the producer step of the batch's one token per sequence
 };
 
+// Replace row p (0..31, wave-uniform) of a tile, as loaded (before
+// k_exchange), with the new token's K / V row at kv in LDS (the cache row's
+// bytes of this KV head: K, then V).
+//   FP8: load A of sub-tile m holds row c & 7, bytes 32kg + (c < 8 ? 0 : 16);
+//     load B row (c & 7) + 8, bytes 32kg + (c < 8 ? 16 : 0) (fp8_k_lanes);
+//     V word i: row 16 (i >> 2) + 4kg + (i & 3), bytes 8c .. 8c+7.
+//   16-bit: K word i of sub-tile m: row 16m + c, bytes 64kg + 16i; V word i:
+//     row 16 (i >> 2) + 4kg + (i & 3), bytes 16c .. 16c+15.
 // Replace row p (0..31, wave-uniform) of an FP8 tile, as loaded (before
-// k_exchange), with the K / V bytes at kv (128 + 128 bytes in LDS).
-MKV_DEV void patch_tile_row_fp8(Tile16<MKV_DTYPE_FP8E4M3>& T, int p, const unsigned char* kv) {
+// k_exchange), with the new token's K / V row at kv in LDS (the cache row's
+// bytes of this KV head: K, then V).  Load A of sub-tile m holds row c & 7,
+// bytes 32kg + (c < 8 ? 0 : 16); load B row (c & 7) + 8, bytes
+// 32kg + (c < 8 ? 16 : 0) (fp8_k_lanes); V word i: row 16 (i >> 2) + 4kg +
+// (i & 3), bytes 8c .. 8c+7.  (Selects, not branches: a tile changed on two
+// paths lands in scratch memory.)
+template <int KV_DT>
+MKV_DEV void patch_tile_row(Tile16<KV_DT>& T, int p, const unsigned char* kv) {
+  static_assert(DTypeInfo<KV_DT>::kBytes == 1, "1-byte caches");
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, kg = lane >> 4;
   const bool top = c < 8;
-  // load A of sub-tile m holds row c & 7, bytes 32kg + (top ? 0 : 16); load B
-  // row (c & 7) + 8, bytes 32kg + (top ? 16 : 0) (fp8_k_lanes)
   const u32x4 na = *reinterpret_cast<const u32x4*>(kv + 32 * kg + (top ? 0 : 16));
   const u32x4 nb = *reinterpret_cast<const u32x4*>(kv + 32 * kg + (top ? 16 : 0));
   const u32x2 nv = *reinterpret_cast<const u32x2*>(kv + 128 + 8 * c);
@@ -1098,16 +1111,20 @@ MKV_DEV uint32_t fp8_code(float x, const Fp8Quant& q) {
   return quantize4_fp8(v, q) & 0xffu;
 }
 
-template <int IN_DT>
+// KV_DT: MKV_DTYPE_FP8E4M3 (per-tensor scales) or a 16-bit cache (copy
+// append, cast to the cache dtype).  1-byte caches take the workgroup
+// route's round-robin tiles with a speculative first tile (wg_decode_rr),
+// 16-bit caches its consecutive ranges (wg_decode_contig).
+template <int IN_DT, int KV_DT>
 MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
-  constexpr int KV_DT = MKV_DTYPE_FP8E4M3;
+  constexpr bool kFp8 = KV_DT == MKV_DTYPE_FP8E4M3;
+  constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
   constexpr int kIb = DTypeInfo<IN_DT>::kBytes;
   extern __shared__ float wg_lds[];
   const DecodeArgs& a = f.d;
   const ProducerArgs& pa = f.p;
   WorkItem it = wg_item_rr(a);
   const int nw = it.num_splits, wv = it.split;
-  const int step = 32 * nw;
   const int lane = threadIdx.x & 63;
   const int G = a.group;
 
@@ -1146,48 +1163,72 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
   const int64_t L_raw = load_index(a.context_lens, it.b, a.ctx_i64);
   const int64_t pos = pa.positions[it.b];
   const int64_t slot = pa.slot_mapping[it.b];
-  float ks = load_uniform_f32(pa.k_scale), vs = load_uniform_f32(pa.v_scale);
-  if (pa.calibrate && (ks == 1.0f || vs == 1.0f)) {
-    const int m = lane & 7, wb = dtype_bytes(pa.w_dtype);
-    float wkl[8] = {}, wkh[8] = {};
-    if (pa.k_w) {
-      load8_f32(reinterpret_cast<const char*>(pa.k_w) + (8 * m) * wb, pa.w_dtype, wkl);
-      load8_f32(reinterpret_cast<const char*>(pa.k_w) + (64 + 8 * m) * wb, pa.w_dtype, wkh);
+  float ks = 1.0f, vs = 1.0f;
+  if constexpr (kFp8) {
+    ks = load_uniform_f32(pa.k_scale);
+    vs = load_uniform_f32(pa.v_scale);
+    if (pa.calibrate && (ks == 1.0f || vs == 1.0f)) {
+      const int m = lane & 7, wb = dtype_bytes(pa.w_dtype);
+      float wkl[8] = {}, wkh[8] = {};
+      if (pa.k_w) {
+        load8_f32(reinterpret_cast<const char*>(pa.k_w) + (8 * m) * wb, pa.w_dtype, wkl);
+        load8_f32(reinterpret_cast<const char*>(pa.k_w) + (64 + 8 * m) * wb, pa.w_dtype, wkh);
+      }
+      if (ks == 1.0f) ks = producer_calibrate(pa, true, pa.k_scale, IN_DT, wkl, wkh);
+      if (vs == 1.0f) vs = producer_calibrate(pa, false, pa.v_scale, IN_DT, wkl, wkh);
     }
-    if (ks == 1.0f) ks = producer_calibrate(pa, true, pa.k_scale, IN_DT, wkl, wkh);
-    if (vs == 1.0f) vs = producer_calibrate(pa, false, pa.v_scale, IN_DT, wkl, wkh);
   }
   const bool append = slot >= 0 && slot < pa.num_slots;
 
-  // The wave's first tile (speculative, as in wg_decode_rr), then the cos /
-  // sin pair of the position (rotary_row's values).
+  // The first tile: 1-byte caches load it speculatively (as in
+  // wg_decode_rr); 16-bit caches take consecutive ranges, known once the
+  // context length is (wg_item's split).  Then the cos / sin pair of the
+  // position (rotary_row's values).
+  const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
+  const int64_t L = L_raw < 0 ? 0 : (L_raw > cap ? cap : L_raw);
+  int step = 32 * nw;
+  if constexpr (!kFp8) {
+    const int tiles = (int)((L + 31) >> 5);
+    const int per = (tiles + nw - 1) / nw;
+    const int64_t tb = (int64_t)wv * per * 32, te = tb + (int64_t)per * 32;
+    it.t_begin = (int)(tb < L ? tb : L);
+    it.t_end = (int)(te < L ? te : L);
+    step = 32;
+  }
   const ItemLoad Ld = item_load_setup<KV_DT>(a, it);
   Tile16<KV_DT> ta, tb2;
-  load_tile16<KV_DT, false>(a, it, Ld, it.t_begin, item_phys(a, it.b, it.t_begin, it.t_end), ta);
+  PhysPair ph = item_phys(a, it.b, it.t_begin, it.t_end);
+  if constexpr (kFp8) load_tile16<KV_DT, false>(a, it, Ld, it.t_begin, ph, ta);
   const bool pos_ok = pos >= 0 && pos < pa.max_position;
   const char* csr = reinterpret_cast<const char*>(pa.cos_sin) +
                     (pos_ok ? pos : 0) * kHeadDim * dtype_bytes(pa.cs_dtype);
   const uint32_t cw = elem_word(csr, lane, pa.cs_dtype), sw = elem_word(csr, 64 + lane, pa.cs_dtype);
 
-  // The context length is known: the second tile's loads go out (empty past
-  // the context) before the producer's math waits for its inputs.  The new
-  // token's row is patched into the tile that holds position L - 1 when this
-  // call appends it there (slot = that position's cache row).
-  it.t_end = (int)(L_raw < 0 ? 0 : (L_raw < it.t_end ? L_raw : it.t_end));
-  const int pl = it.t_end - 1;
-  const int64_t phys_pl = pl >= 0 ? a.idx.physical_block(it.b, pl >> a.idx.bs_log2) : -1;
-  const bool patch = append && phys_pl >= 0 &&
-                     (phys_pl << a.idx.bs_log2) + (pl & ((1 << a.idx.bs_log2) - 1)) == slot;
-  PhysPair ph = item_phys(a, it.b, it.t_begin + step, it.t_end);
-  load_tile16<KV_DT, false>(a, it, Ld, it.t_begin + step, ph, tb2);
-  ph = item_phys(a, it.b, it.t_begin + 2 * step, it.t_end);
+  // 1-byte caches: the context length is known, the second tile's loads go
+  // out (empty past the range) before the producer's math waits for its
+  // inputs, and the new token's row is patched into the tile that holds
+  // position L - 1 when this call appends it there (slot = that position's
+  // cache row): that tile's loads may have left before the append landed.
+  // 16-bit caches load their tiles after the append has landed instead (the
+  // patch's registers beside two 16-bit tiles would spill).
+  bool patch = false;
+  const int pl = (int)L - 1;
+  if constexpr (kFp8) {
+    it.t_end = (int)(L < it.t_end ? L : it.t_end);
+    const int64_t phys_pl = pl >= 0 ? a.idx.physical_block(it.b, pl >> a.idx.bs_log2) : -1;
+    patch = append && phys_pl >= 0 && (phys_pl << a.idx.bs_log2) + (pl & ((1 << a.idx.bs_log2) - 1)) == slot;
+    ph = item_phys(a, it.b, it.t_begin + step, it.t_end);
+    load_tile16<KV_DT, false>(a, it, Ld, it.t_begin + step, ph, tb2);
+    ph = item_phys(a, it.b, it.t_begin + 2 * step, it.t_end);
+  }
 
-  // The producer's math (produce_qk / load_v and store_kv's FP8 bytes, the
-  // same operations in the same order): q into the workgroup's q area (fp32
-  // [G][128]), the K and V codes into its 256-byte row area, and the wave of
-  // the k / v slot appends them.
+  // The producer's math (produce_qk / load_v and store_kv's bytes, the same
+  // operations in the same order): q into the workgroup's q area (fp32
+  // [G][128]), the new token's K and V cache rows of head kvh into its row
+  // area (2 x 128 x kEb bytes), and the wave of the k / v slot appends them.
   float* qsh = wg_lds + nw * G * (kHeadDim + 2);
-  uint32_t* kvsh = reinterpret_cast<uint32_t*>(qsh + G * kHeadDim);  // [K 32 words | V 32 words]
+  uint32_t* kvsh = reinterpret_cast<uint32_t*>(qsh + G * kHeadDim);  // [K row | V row]
+  constexpr int kRowWords = kHeadDim * kEb / 4;
   const float c = pos_ok ? word_elem(cw, lane, pa.cs_dtype) : __builtin_nanf("");
   const float sn = pos_ok ? word_elem(sw, lane, pa.cs_dtype) : __builtin_nanf("");
   auto produce = [&](int hs, const SlotIn& in) {
@@ -1218,21 +1259,35 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
       qsh[hs * kHeadDim + lane] = o1;
       qsh[hs * kHeadDim + 64 + lane] = o2;
     } else if (hs < G + 2) {
-      // FP8 codes of elements l and 64 + l, gathered four lanes to a word
-      const Fp8Quant qz = fp8_quant(hs == G ? ks : vs);
-      const uint32_t b1 = fp8_code(o1, qz), b2 = fp8_code(o2, qz);
-      const uint32_t w1 = b1 | (uint32_t)__shfl(b1, lane + 1) << 8 | (uint32_t)__shfl(b1, lane + 2) << 16 |
-                          (uint32_t)__shfl(b1, lane + 3) << 24;
-      const uint32_t w2 = b2 | (uint32_t)__shfl(b2, lane + 1) << 8 | (uint32_t)__shfl(b2, lane + 2) << 16 |
-                          (uint32_t)__shfl(b2, lane + 3) << 24;
-      if ((lane & 3) == 0) {
-        uint32_t* dst = kvsh + (hs == G ? 0 : 32);
-        dst[lane >> 2] = w1;
-        dst[16 + (lane >> 2)] = w2;
+      // the cache bytes of elements l and 64 + l, gathered to words (4 FP8
+      // codes or 2 16-bit values)
+      uint32_t w1, w2;
+      bool lead;
+      if constexpr (kFp8) {
+        const Fp8Quant qz = fp8_quant(hs == G ? ks : vs);
+        const uint32_t b1 = fp8_code(o1, qz), b2 = fp8_code(o2, qz);
+        w1 = b1 | (uint32_t)__shfl(b1, lane + 1) << 8 | (uint32_t)__shfl(b1, lane + 2) << 16 |
+             (uint32_t)__shfl(b1, lane + 3) << 24;
+        w2 = b2 | (uint32_t)__shfl(b2, lane + 1) << 8 | (uint32_t)__shfl(b2, lane + 2) << 16 |
+             (uint32_t)__shfl(b2, lane + 3) << 24;
+        lead = (lane & 3) == 0;
+      } else {
+        const bool bf = KV_DT == MKV_DTYPE_BF16;
+        const uint32_t h1 = bf ? f32_to_bf16_bits(o1) : f32_to_f16_bits(o1);
+        const uint32_t h2 = bf ? f32_to_bf16_bits(o2) : f32_to_f16_bits(o2);
+        w1 = h1 | (uint32_t)__shfl(h1, lane + 1) << 16;
+        w2 = h2 | (uint32_t)__shfl(h2, lane + 1) << 16;
+        lead = (lane & 1) == 0;
+      }
+      if (lead) {
+        const int wi = lane * kEb / 4;  // word of element l in the row
+        uint32_t* dst = kvsh + (hs == G ? 0 : kRowWords);
+        dst[wi] = w1;
+        dst[kRowWords / 2 + wi] = w2;
         if (append) {
-          char* base = (hs == G ? pa.k_cache : pa.v_cache) + slot * a.idx.row_elems + (int64_t)it.kvh * kHeadDim;
-          *reinterpret_cast<uint32_t*>(base + lane) = w1;
-          *reinterpret_cast<uint32_t*>(base + 64 + lane) = w2;
+          char* base = (hs == G ? pa.k_cache : pa.v_cache) + (slot * a.idx.row_elems + (int64_t)it.kvh * kHeadDim) * kEb;
+          *reinterpret_cast<uint32_t*>(base + lane * kEb) = w1;
+          *reinterpret_cast<uint32_t*>(base + (64 + lane) * kEb) = w2;
         }
       }
     }
@@ -1240,12 +1295,19 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
   produce(wv, in0);
   produce(wv + nw, in1);
   for (int hs = wv + 2 * nw; hs < G + 2; hs += nw) produce(hs, slot_loads(hs));
-  __syncthreads();  // q and the new K / V row are in LDS
+  if constexpr (!kFp8) __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the append has landed
+  __syncthreads();  // q and the new K / V row are in LDS (16-bit: and in the cache)
   const unsigned char* kv_new = reinterpret_cast<const unsigned char*>(kvsh);
-  float* qst = qsh;
+  if constexpr (!kFp8) {
+    load_tile16<KV_DT, false>(a, it, Ld, it.t_begin, ph, ta);
+    ph = item_phys(a, it.b, it.t_begin + step, it.t_end);
+    load_tile16<KV_DT, false>(a, it, Ld, it.t_begin + step, ph, tb2);
+    ph = item_phys(a, it.b, it.t_begin + 2 * step, it.t_end);
+  }
 
   auto fix = [&](Tile16<KV_DT>& T, int t0) {
-    if (patch && pl >= t0 && pl < t0 + 32) patch_tile_row_fp8(T, pl - t0, kv_new);
+    if constexpr (kFp8)
+      if (patch && pl >= t0 && pl < t0 + 32) patch_tile_row<KV_DT>(T, pl - t0, kv_new);
   };
   QOps<KV_DT> qop;
   f32x4 acc[8];
@@ -1254,18 +1316,18 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
   float m_run = kNegBig, l_run = 0.0f;
   if (it.t_begin < it.t_end) {
     // q of head c, dims 32kg .. 32kg+31 (zeros for padding heads)
-    const int c = lane & 15, kg = lane >> 4;
+    const int cq = lane & 15, kg = lane >> 4;
     float qf[32];
-    const float* q = qst + (c < G ? c : 0) * kHeadDim + 32 * kg;
+    const float* q = qsh + (cq < G ? cq : 0) * kHeadDim + 32 * kg;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const f32x4 x = *reinterpret_cast<const f32x4*>(q + 4 * i);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) qf[4 * i + j] = c < G ? x[j] : 0.0f;
+      for (int j = 0; j < 4; ++j) qf[4 * i + j] = cq < G ? x[j] : 0.0f;
     }
     const float score_mul = q_operands<KV_DT>(a, qf, qop, ks);
     qop.split = false;
-    zero_v_rows_past<KV_DT>(ta, it.t_begin, it.t_end);
+    if constexpr (kFp8) zero_v_rows_past<KV_DT>(ta, it.t_begin, it.t_end);
     fix(ta, it.t_begin);
     compute_tile16<KV_DT, false>(ta, it.t_begin, it.t_end, qop, score_mul, acc, m_run, l_run, false);
     for (int t0 = it.t_begin + step; t0 < it.t_end;) {
@@ -1282,17 +1344,17 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
       t0 += step;
     }
   } else {
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the speculative loads land first
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the loads in flight land first
   }
   float l_col = l_run + __shfl_xor(l_run, 16);
   l_col += __shfl_xor(l_col, 32);
   wg_merge_store<false>(a, it, acc, m_run, l_col, vs);
 }
 
-template <int IN_DT>
+template <int IN_DT, int KV_DT>
 __global__ __launch_bounds__(kWgMaxWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void
 paged_decode_wg_produce_kernel(ProduceDecodeArgs f) {
-  wg_produce_decode<IN_DT>(f);
+  wg_produce_decode<IN_DT, KV_DT>(f);
 }
 
 // fp32 caches on the workgroup route: 16-token tiles on v_mfma_f32_16x16x4_f32
@@ -2860,7 +2922,10 @@ extern "C" int mkv_qkv_norm_rope_append_decode(
                        sm_scale, MKV_DECODE_WORKGROUP, d, ks, fmt);
   if (st != MKV_OK) return st;
   if (head_dim != kHeadDim || ks.pair) return MKV_ERR_UNSUPPORTED_HEAD_DIM;
-  if (fmt != MKV_DTYPE_FP8E4M3) return MKV_ERR_UNSUPPORTED_DTYPE;
+  // per-tensor FP8, or a 16-bit cache (a bf16 cache with a bf16 q: the
+  // workgroup route's kernel without the split q)
+  if (fmt != MKV_DTYPE_FP8E4M3 && fmt != MKV_DTYPE_F16 && !(fmt == MKV_DTYPE_BF16 && out_dtype == MKV_DTYPE_BF16))
+    return MKV_ERR_UNSUPPORTED_DTYPE;
   if (d.group > kFusedMaxGroup) return MKV_ERR_UNSUPPORTED_GROUP;
   // the producer's arguments
   if (max_position <= 0) return MKV_ERR_BAD_SHAPE;
@@ -2913,19 +2978,24 @@ extern "C" int mkv_qkv_norm_rope_append_decode(
   p.num_slots = num_blocks * (int64_t)block_size;
 
   const int nw = wg_waves(batch, d.num_kv_heads, d.group, max_blocks, block_size, device_cus());
-  const size_t lds = ((size_t)nw * d.group * (kHeadDim + 2) + (size_t)d.group * kHeadDim) * sizeof(float) + 256;
+  const size_t row_bytes = (size_t)kHeadDim * (fmt == MKV_DTYPE_FP8E4M3 ? 1 : 2);
+  const size_t lds = ((size_t)nw * d.group * (kHeadDim + 2) + (size_t)d.group * kHeadDim) * sizeof(float) +
+                     2 * row_bytes;
   const dim3 grid((unsigned)((int64_t)batch * d.num_kv_heads)), block(nw * kWave);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  switch (in_dtype) {
-    case MKV_DTYPE_BF16:
-      hipLaunchKernelGGL(paged_decode_wg_produce_kernel<MKV_DTYPE_BF16>, grid, block, lds, s, f);
-      break;
-    case MKV_DTYPE_F16:
-      hipLaunchKernelGGL(paged_decode_wg_produce_kernel<MKV_DTYPE_F16>, grid, block, lds, s, f);
-      break;
-    default:
-      hipLaunchKernelGGL(paged_decode_wg_produce_kernel<MKV_DTYPE_F32>, grid, block, lds, s, f);
-      break;
+#define MKV_PD(IDT, KDT) hipLaunchKernelGGL((paged_decode_wg_produce_kernel<IDT, KDT>), grid, block, lds, s, f)
+#define MKV_PD_KV(IDT)                                           \
+  switch (fmt) {                                                 \
+    case MKV_DTYPE_FP8E4M3: MKV_PD(IDT, MKV_DTYPE_FP8E4M3); break; \
+    case MKV_DTYPE_BF16: MKV_PD(IDT, MKV_DTYPE_BF16); break;       \
+    default: MKV_PD(IDT, MKV_DTYPE_F16); break;                    \
   }
+  switch (in_dtype) {
+    case MKV_DTYPE_BF16: MKV_PD_KV(MKV_DTYPE_BF16); break;
+    case MKV_DTYPE_F16: MKV_PD_KV(MKV_DTYPE_F16); break;
+    default: MKV_PD_KV(MKV_DTYPE_F32); break;
+  }
+#undef MKV_PD_KV
+#undef MKV_PD
   return (int)hipGetLastError();
 }

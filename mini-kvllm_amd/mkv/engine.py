@@ -262,8 +262,8 @@ def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
 
 class Qwen3Model(torch.nn.Module):
     """Random-init Qwen3 decoder (weights N(0, std), norm weights 1) whose
-    attention layers run on the mkv operators.  With an FP8 per-tensor cache
-    a decode step runs each layer's producer step and attention as one call
+    attention layers run on the mkv operators.  A decode step runs each
+    layer's producer step and attention as one call
     (:func:`mkv.producer.qkv_norm_rope_append_decode`) unless
     fuse_decode_step is False (then through :meth:`attention`, which a
     subclass may replace)."""
@@ -351,7 +351,7 @@ class Qwen3Model(torch.nn.Module):
             qkv = F.linear(h, lay["qkv"])
             att = lay["attn"]
             ctx = C.current_context()
-            if self.fuse_decode_step and not ctx.is_prefill and att.kv_cache_dtype == "fp8_per_tensor":
+            if self.fuse_decode_step and not ctx.is_prefill:
                 # a decode step: the producer step and the attention in one
                 # launch where the decode schedule allows it
                 o = qkv_norm_rope_append_decode(

@@ -144,28 +144,34 @@ def qkv_norm_rope_append_decode(qkv: torch.Tensor, positions: torch.Tensor, num_
     split_tokens) on the produced q.  Returns the attention output
     (batch, num_heads, head_dim) in out_dtype (default: qkv's dtype).
 
-    For a per-tensor FP8 cache at head_dim 128 with at most 8 query heads
-    per KV head, whose scales are calibrated,
-    when the decode schedule is the workgroup route (the library's choice for
-    the shape, or split_tokens = DECODE_WORKGROUP), both run in one launch
-    (``mkv_qkv_norm_rope_append_decode``, the same bits as the two calls);
-    otherwise as the two calls.  slot_mapping[b] must be the cache row of
-    position context_lens[b] - 1 of sequence b (or -1), as a decode step's
-    metadata has it."""
+    At head_dim 128 with at most 8 query heads per KV head, for a per-tensor
+    FP8 cache whose scales are calibrated, an fp16 cache, or a bf16 cache
+    with a bf16 out_dtype, when the decode schedule is the workgroup route
+    (the library's choice for the shape, or split_tokens = DECODE_WORKGROUP),
+    both run in one launch (``mkv_qkv_norm_rope_append_decode``, the same
+    bits as the two calls); otherwise as the two calls.  slot_mapping[b]
+    must be the cache row of position context_lens[b] - 1 of sequence b (or
+    -1), as a decode step's metadata has it."""
     T = qkv.shape[0] if qkv.dim() == 2 else -1
     out_dtype = out_dtype or qkv.dtype
-    fused = (kv_cache_dtype == "fp8_per_tensor" and head_dim == 128 and T > 0
-             and num_heads % num_kv_heads == 0 and num_heads // num_kv_heads <= 8
-             and k_cache is not None and k_cache.dtype == torch.float8_e4m3fn
-             and getattr(k_scale, "_mkv_calibrated", False) and getattr(v_scale, "_mkv_calibrated", False))
+    kdt = k_cache.dtype if k_cache is not None else None
+    if kv_cache_dtype == "fp8_per_tensor":
+        cache_ok = (kdt == torch.float8_e4m3fn and getattr(k_scale, "_mkv_calibrated", False)
+                    and getattr(v_scale, "_mkv_calibrated", False))
+    else:
+        cache_ok = kv_cache_dtype == "auto" and (
+            kdt == torch.float16 or (kdt == torch.bfloat16 and out_dtype == torch.bfloat16))
+    fused = (cache_ok and head_dim == 128 and T > 0
+             and num_heads % num_kv_heads == 0 and num_heads // num_kv_heads <= 8)
     if fused:
+        kv_code = _DTYPES[kdt]
         bt = _block_table(block_tables)
         cl = _ctx_lens(context_lens)
         route = split_tokens
         if split_tokens == 0:
             route = (_lib.DECODE_WORKGROUP
                      if _lib.query("mkv_paged_decode_route", T, num_heads, num_kv_heads, bt.shape[1],
-                                   k_cache.shape[1], head_dim, _lib.DTYPE_FP8E4M3, 0, 0)
+                                   k_cache.shape[1], head_dim, kv_code, 0, 0)
                      == _lib.ROUTE_WORKGROUP else 0)
         fused = route == _lib.DECODE_WORKGROUP
     if not fused:
@@ -214,8 +220,11 @@ def qkv_norm_rope_append_decode(qkv: torch.Tensor, positions: torch.Tensor, num_
         k_norm_weight.data_ptr() if k_norm_weight is not None else None,
         _DTYPES.get(wdt, 0) if wdt is not None else 0, float(eps), cs.data_ptr(),
         _dtype_code(cs, "cos_sin_cache"), cs.shape[0], pos.data_ptr(), k_cache.data_ptr(),
-        v_cache.data_ptr(), _lib.DTYPE_FP8E4M3, k_cache.shape[0], k_scale.data_ptr(),
-        v_scale.data_ptr(), _lib.SCALE_PER_TENSOR, slots.data_ptr(), _lib.APPEND_CALIBRATE_SENTINEL,
+        v_cache.data_ptr(), kv_code, k_cache.shape[0],
+        k_scale.data_ptr() if kv_code == _lib.DTYPE_FP8E4M3 else None,
+        v_scale.data_ptr() if kv_code == _lib.DTYPE_FP8E4M3 else None,
+        _lib.SCALE_PER_TENSOR, slots.data_ptr(),
+        _lib.APPEND_CALIBRATE_SENTINEL if kv_code == _lib.DTYPE_FP8E4M3 else 0,
         bt.data_ptr(), bt.stride(0), bt.shape[1], cl.data_ptr(), _index_dtype(cl), T, num_heads,
         num_kv_heads, head_dim, k_cache.shape[1], float(scale), _stream(dev))
     return out

@@ -141,10 +141,10 @@ def test_engine_logits_match_the_oracle_attention_engine(dev, monkeypatch, split
 FULL = E.ModelConfig(num_layers=2)
 
 
-def _full_engine(dev, model_cls, use_graphs, dtype):
+def _full_engine(dev, model_cls, use_graphs, dtype, kv_cache_dtype="fp8_per_tensor"):
     model = model_cls(FULL, dev, dtype=dtype, seed=5, block_size=256)
     return E.Engine(model, num_blocks=40, max_num_seqs=8, max_num_batched_tokens=1024,
-                    kv_cache_dtype="fp8_per_tensor", max_model_len=1024, seed=0, use_graphs=use_graphs)
+                    kv_cache_dtype=kv_cache_dtype, max_model_len=1024, seed=0, use_graphs=use_graphs)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -225,14 +225,14 @@ class UnfusedModel(E.Qwen3Model):
     fuse_decode_step = False
 
 
-@pytest.mark.parametrize("use_graphs", [True, False])
-def test_fused_decode_steps_give_the_unfused_logits(dev, monkeypatch, use_graphs):
+@pytest.mark.parametrize("use_graphs,kv", [(True, "fp8_per_tensor"), (False, "fp8_per_tensor"), (True, "auto")])
+def test_fused_decode_steps_give_the_unfused_logits(dev, monkeypatch, use_graphs, kv):
     """The end-to-end workload's shape (2 layers, bf16 weights, FP8 per-tensor
-    KV, 8 prompts of 32-512 tokens): with each decode step's producer step
-    and attention in one launch (mkv_qkv_norm_rope_append_decode), every
-    step's logits are bit-identical to the two calls' and so are the
+    or bf16 KV, 8 prompts of 32-512 tokens): with each decode step's producer
+    step and attention in one launch (mkv_qkv_norm_rope_append_decode),
+    every step's logits are bit-identical to the two calls' and so are the
     generated tokens, captured or eager."""
-    announce(f"engine: fused decode steps vs two calls, graphs {use_graphs}")
+    announce(f"engine: fused decode steps vs two calls, graphs {use_graphs}, kv {kv}")
     from mkv import _lib
 
     names = []
@@ -246,8 +246,8 @@ def test_fused_decode_steps_give_the_unfused_logits(dev, monkeypatch, use_graphs
     g = torch.Generator().manual_seed(56)
     lens = [int(x) for x in torch.randint(32, 513, (8,), generator=g)]
     prompts = [torch.randint(0, FULL.vocab_size, (L,), generator=g).tolist() for L in lens]
-    eng = _full_engine(dev, E.Qwen3Model, use_graphs, torch.bfloat16)
-    ref = _full_engine(dev, UnfusedModel, use_graphs, torch.bfloat16)
+    eng = _full_engine(dev, E.Qwen3Model, use_graphs, torch.bfloat16, kv)
+    ref = _full_engine(dev, UnfusedModel, use_graphs, torch.bfloat16, kv)
     for e in (eng, ref):
         for p in prompts:
             e.add_request(p, max_tokens=8)

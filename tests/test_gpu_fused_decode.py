@@ -1,6 +1,6 @@
 """GPU parity of the fused decode step (``mkv_qkv_norm_rope_append_decode``):
 one layer's producer step for each sequence's new token (q/k RMSNorm,
-rotary embedding, FP8 append; reference qwen3.py:73-118,
+rotary embedding, FP8 or 16-bit append; reference qwen3.py:73-118,
 attention.py:1654-1691) and the decode attention over the cache that holds
 it (attention.py:1213-1268), in one launch.
 
@@ -9,7 +9,8 @@ it (attention.py:1213-1268), in one launch.
   bytes and the scales are bit-identical, over group sizes 1-8, block
   sizes 16 and 256, contexts 0-800 (the new token in a wave's first,
   second or a later tile), rows without a slot, every input dtype and the
-  1.0-sentinel calibration.
+  1.0-sentinel calibration; bf16 and fp16 caches (loaded after the append
+  has landed) over the same group sizes.
 * Against the oracle (qkv_norm_rope_ref, then paged_decode_ref on the
   dequantised cache): within the FP8 bound, 2e-2 abs.
 """
@@ -30,7 +31,8 @@ D = 128
 CTX_EDGES = [0, 1, 2, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 256, 257, 511, 512, 513]
 
 
-def _case(dev, seed, B, Hq, Hkv, bs, in_dtype, ctx=None, no_slot=(), scale_val=None):
+def _case(dev, seed, B, Hq, Hkv, bs, in_dtype, ctx=None, no_slot=(), scale_val=None,
+          cache_dtype=torch.float8_e4m3fn):
     g = torch.Generator().manual_seed(seed)
     if ctx is None:
         ctx = torch.tensor((CTX_EDGES * ((B + len(CTX_EDGES) - 1) // len(CTX_EDGES)))[:B])
@@ -49,30 +51,33 @@ def _case(dev, seed, B, Hq, Hkv, bs, in_dtype, ctx=None, no_slot=(), scale_val=N
     cs = R.rope_cos_sin_cache(1000000.0, D, 4096).to(in_dtype)
     qw = (torch.rand(D, generator=g) + 0.5).to(in_dtype)
     kw = (torch.rand(D, generator=g) + 0.5).to(in_dtype)
-    kc = torch.empty(N, bs, Hkv, D, dtype=torch.float8_e4m3fn, device=dev)
+    kc = torch.empty(N, bs, Hkv, D, dtype=cache_dtype, device=dev)
     vc = torch.empty_like(kc)
     sk = 0.02 if scale_val is None else scale_val
     sv = 0.03 if scale_val is None else scale_val
     W.fill_pool_on_device(kc, seed + 1, sk)
     W.fill_pool_on_device(vc, seed + 2, sv)
-    ks = torch.full((1,), sk, device=dev)
-    vs = torch.full((1,), sv, device=dev)
+    fp8 = cache_dtype == torch.float8_e4m3fn
+    ks = torch.full((1,), sk, device=dev) if fp8 else None
+    vs = torch.full((1,), sv, device=dev) if fp8 else None
     return dict(qkv=qkv.to(dev), pos=pos.to(dev), cs=cs.to(dev), qw=qw.to(dev), kw=kw.to(dev), kc=kc,
                 vc=vc, ks=ks, vs=vs, slots=slots.to(dev), bt=bt.to(dev), ctx=ctx.to(dev), B=B, Hq=Hq,
-                Hkv=Hkv, bs=bs, scale=D ** -0.5)
+                Hkv=Hkv, bs=bs, scale=D ** -0.5, kv="fp8_per_tensor" if fp8 else "auto")
 
 
 def _calibrated(t):
-    t._mkv_calibrated = True
+    if t is not None:
+        t = t.clone()
+        t._mkv_calibrated = True
     return t
 
 
 def _two_calls(c):
     kc, vc = c["kc"].clone(), c["vc"].clone()
-    ks, vs = _calibrated(c["ks"].clone()), _calibrated(c["vs"].clone())
+    ks, vs = _calibrated(c["ks"]), _calibrated(c["vs"])
     q, _, _ = P.qkv_norm_rope_append(
         c["qkv"], c["pos"], c["Hq"], c["Hkv"], D, c["cs"], kc, vc, c["slots"], c["bs"],
-        q_norm_weight=c["qw"], k_norm_weight=c["kw"], kv_cache_dtype="fp8_per_tensor", k_scale=ks,
+        q_norm_weight=c["qw"], k_norm_weight=c["kw"], kv_cache_dtype=c["kv"], k_scale=ks,
         v_scale=vs)
     out = A._decode(q, kc, vc, c["bt"], c["ctx"], c["scale"], c["Hq"], c["Hkv"], D, ks, vs,
                     split_tokens=A.DECODE_WORKGROUP)
@@ -81,11 +86,23 @@ def _two_calls(c):
 
 def _fused(c):
     kc, vc = c["kc"].clone(), c["vc"].clone()
-    ks, vs = _calibrated(c["ks"].clone()), _calibrated(c["vs"].clone())
-    out = P.qkv_norm_rope_append_decode(
-        c["qkv"], c["pos"], c["Hq"], c["Hkv"], D, c["cs"], kc, vc, c["slots"], c["bs"], c["bt"],
-        c["ctx"], c["scale"], q_norm_weight=c["qw"], k_norm_weight=c["kw"],
-        kv_cache_dtype="fp8_per_tensor", k_scale=ks, v_scale=vs, split_tokens=A.DECODE_WORKGROUP)
+    ks, vs = _calibrated(c["ks"]), _calibrated(c["vs"])
+    calls = []
+    orig = _lib.call
+
+    def spy(name, *args):
+        calls.append(name)
+        return orig(name, *args)
+
+    _lib.call = spy
+    try:
+        out = P.qkv_norm_rope_append_decode(
+            c["qkv"], c["pos"], c["Hq"], c["Hkv"], D, c["cs"], kc, vc, c["slots"], c["bs"], c["bt"],
+            c["ctx"], c["scale"], q_norm_weight=c["qw"], k_norm_weight=c["kw"],
+            kv_cache_dtype=c["kv"], k_scale=ks, v_scale=vs, split_tokens=A.DECODE_WORKGROUP)
+    finally:
+        _lib.call = orig
+    assert calls == ["mkv_qkv_norm_rope_append_decode"], calls
     return out, kc, vc, ks, vs
 
 
@@ -94,7 +111,8 @@ def _assert_same(f, u):
     out_u, kc_u, vc_u, ks_u, vs_u = u[:5]
     assert torch.equal(kc.view(torch.uint8), kc_u.view(torch.uint8)), "K cache bytes differ"
     assert torch.equal(vc.view(torch.uint8), vc_u.view(torch.uint8)), "V cache bytes differ"
-    assert torch.equal(ks, ks_u) and torch.equal(vs, vs_u), "scales differ"
+    if ks is not None:
+        assert torch.equal(ks, ks_u) and torch.equal(vs, vs_u), "scales differ"
     diff = (out.float() != out_u.float()) & ~(torch.isnan(out.float()) & torch.isnan(out_u.float()))
     assert not bool(diff.any()), (f"{int(diff.sum())} outputs differ, max "
                                   f"{float((out.float() - out_u.float()).abs().max()):.3e}")
@@ -105,6 +123,26 @@ def _assert_same(f, u):
 def test_fused_decode_step_equals_the_two_calls(dev, Hq, Hkv, bs):
     announce(f"fused decode step {Hq}/{Hkv} block {bs}")
     c = _case(dev, Hq * 7 + bs, 40, Hq, Hkv, bs, torch.bfloat16, no_slot=(5, 21))
+    _assert_same(_fused(c), _two_calls(c))
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(16, 8), (32, 8), (8, 8), (64, 8), (24, 3)])
+@pytest.mark.parametrize("cache_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bs", [16, 256])
+def test_fused_decode_step_16bit_caches(dev, Hq, Hkv, cache_dtype, bs):
+    """bf16 (with a bf16 q) and fp16 caches: the rows are appended as the
+    producer's cast, and the attention reads every tile after the append."""
+    announce(f"fused decode step {cache_dtype} cache {Hq}/{Hkv} block {bs}")
+    c = _case(dev, Hq * 5 + bs + 1, 40, Hq, Hkv, bs, torch.bfloat16, no_slot=(4, 30),
+              cache_dtype=cache_dtype)
+    _assert_same(_fused(c), _two_calls(c))
+
+
+@pytest.mark.parametrize("in_dtype", [torch.float16, torch.float32])
+def test_fused_decode_step_16bit_cache_input_dtypes(dev, in_dtype):
+    """An fp16 cache under fp16 / fp32 qkv rows (q in the rows' dtype)."""
+    announce(f"fused decode step fp16 cache, {in_dtype} rows")
+    c = _case(dev, 9, 24, 16, 8, 256, in_dtype, cache_dtype=torch.float16)
     _assert_same(_fused(c), _two_calls(c))
 
 

@@ -48,21 +48,26 @@ def test_status_strings():
 
 def test_fused_decode_step_refuses_what_it_does_not_cover():
     """mkv_qkv_norm_rope_append_decode checks its arguments on the host,
-    before any launch: a bf16 cache, head_dim 64 and 16 query heads per KV
-    head are refused (the caller runs the producer and the decode instead),
-    and so are a missing slot mapping and a short qkv row."""
+    before any launch: an fp32 cache, a bf16 cache under an fp32 q (whose
+    decode splits q in two bf16 parts), per-token-head scales, head_dim 64
+    and 16 query heads per KV head are refused (the caller runs the producer
+    and the decode instead), and so are a missing slot mapping and a short
+    qkv row."""
     lib = _lib.load()
     P = 1 << 12  # an aligned stand-in address: nothing is dereferenced
 
-    def call(kv_dtype=_lib.DTYPE_FP8E4M3, Hq=16, Hkv=8, D=128, slots=P, qkv_stride=None):
+    def call(kv_dtype=_lib.DTYPE_FP8E4M3, Hq=16, Hkv=8, D=128, slots=P, qkv_stride=None,
+             out_dtype=_lib.DTYPE_BF16, scale_mode=_lib.SCALE_PER_TENSOR):
         width = (Hq + 2 * Hkv) * D
         return lib.mkv_qkv_norm_rope_append_decode(
-            P, Hq * D, _lib.DTYPE_BF16, P, width if qkv_stride is None else qkv_stride, _lib.DTYPE_BF16,
+            P, Hq * D, out_dtype, P, width if qkv_stride is None else qkv_stride, _lib.DTYPE_BF16,
             P, P, _lib.DTYPE_BF16, 1e-6, P, _lib.DTYPE_BF16, 4096, P, P, P, kv_dtype, 64, P, P,
-            _lib.SCALE_PER_TENSOR, slots, 0, P, 4, 4, P, _lib.INDEX_I64, 60, Hq, Hkv, D, 256, 0.088,
+            scale_mode, slots, 0, P, 4, 4, P, _lib.INDEX_I64, 60, Hq, Hkv, D, 256, 0.088,
             None)
 
-    assert call(kv_dtype=_lib.DTYPE_BF16) == -3
+    assert call(kv_dtype=_lib.DTYPE_F32) == -3
+    assert call(kv_dtype=_lib.DTYPE_BF16, out_dtype=_lib.DTYPE_F32) == -3
+    assert call(scale_mode=_lib.SCALE_PER_TOKEN_HEAD) == -3
     assert call(Hq=16, Hkv=8, D=64) == -4
     assert call(Hq=128, Hkv=8) == -5
     assert call(slots=None) == -1
