@@ -778,8 +778,26 @@ def configs_extra(dev, stream, cpu: bool = True, which=DECODE_CONFIGS) -> dict:
             "two_calls_us": round(graph_time_us(two_calls), 2),
             "one_launch_us": round(graph_time_us(one_launch), 2),
             "producer_alone_us": round(graph_time_us(producer_step), 2)}
+        # the same step over bf16 pools of the same shape (kv_cache_dtype 'auto')
+        kb = torch.empty(N, 256, 8, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+        vb = torch.empty_like(kb)
+        W.fill_pool_on_device(kb, 3003)
+        W.fill_pool_on_device(vb, 3004)
+
+        def two_calls_bf16():
+            q16 = P.qkv_norm_rope_append(qkv, pos, 16, 8, HEAD_DIM, cs, kb, vb, slots, 256, q_norm_weight=nw_,
+                                         k_norm_weight=nw_)[0]
+            A._decode(q16, kb, vb, bt, ctxd, 0.088, 16, 8, HEAD_DIM, out=out)
+
+        def one_launch_bf16():
+            P.qkv_norm_rope_append_decode(qkv, pos, 16, 8, HEAD_DIM, cs, kb, vb, slots, 256, bt, ctxd, 0.088,
+                                          q_norm_weight=nw_, k_norm_weight=nw_, out=out)
+        row["decode_step_from_qkv_bf16_cache"] = {
+            "what": "the same step over bf16 KV pools of the same shape",
+            "two_calls_us": round(graph_time_us(two_calls_bf16), 2),
+            "one_launch_us": round(graph_time_us(one_launch_bf16), 2)}
         res["fp8_decode_b60_engine_shape"] = row
-        del kp, vp
+        del kp, vp, kb, vb
 
     # bf16 decode, the batch-256 workload
     if "bf16_decode_b256" in which:
