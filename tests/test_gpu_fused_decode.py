@@ -138,6 +138,31 @@ def test_fused_decode_step_16bit_caches(dev, Hq, Hkv, cache_dtype, bs):
     _assert_same(_fused(c), _two_calls(c))
 
 
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("cache_dtype", [torch.float8_e4m3fn, torch.bfloat16])
+def test_fused_decode_step_other_block_sizes(dev, bs, cache_dtype):
+    """Block sizes between the two above: the row patch's (1-byte) and the
+    tiles' block lookups at 2-8 blocks per 256 tokens."""
+    announce(f"fused decode step {cache_dtype} cache, block {bs}")
+    c = _case(dev, 100 + bs, 36, 16, 8, bs, torch.bfloat16, no_slot=(2,), cache_dtype=cache_dtype)
+    _assert_same(_fused(c), _two_calls(c))
+
+
+@pytest.mark.parametrize("cache_dtype", [torch.float8_e4m3fn, torch.float16])
+def test_fused_decode_step_int32_lengths_and_wide_rows(dev, cache_dtype):
+    """int32 context lengths, and qkv rows that are a slice of wider rows
+    (a row stride of width + 136 elements)."""
+    announce(f"fused decode step {cache_dtype} cache, int32 lengths, strided qkv")
+    c = _case(dev, 77, 28, 32, 8, 16, torch.bfloat16, no_slot=(9,), cache_dtype=cache_dtype)
+    c["ctx"] = c["ctx"].to(torch.int32)
+    width = c["qkv"].shape[1]
+    wide = torch.zeros(c["qkv"].shape[0], width + 136, dtype=c["qkv"].dtype, device=dev)
+    wide[:, :width] = c["qkv"]
+    c["qkv"] = wide[:, :width]
+    assert c["qkv"].stride(0) == width + 136
+    _assert_same(_fused(c), _two_calls(c))
+
+
 @pytest.mark.parametrize("in_dtype", [torch.float16, torch.float32])
 def test_fused_decode_step_16bit_cache_input_dtypes(dev, in_dtype):
     """An fp16 cache under fp16 / fp32 qkv rows (q in the rows' dtype)."""
