@@ -253,6 +253,16 @@ MKV_DEV bf16x2 i8x2_to_bf16x2(uint32_t w) {
   return __builtin_bit_cast(bf16x2, pack_hi16(__float_as_uint(a), __float_as_uint(b)));
 }
 
+// Two int8 codes (bytes 0-1 of w, or bytes 2-3 with kHi) -> exact fp16 pair
+// (an integer of magnitude <= 128 is exact in fp16; the truncating pack
+// changes no exact value).
+template <bool kHi>
+MKV_DEV f16x2 i8x2_to_f16x2(uint32_t w) {
+  const float a = (float)(int8_t)(w >> (kHi ? 16 : 0));
+  const float b = (float)(int8_t)(w >> (kHi ? 24 : 8));
+  return __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+
 // Value of lane N of this lane's 16-lane row (DPP row broadcast).
 template <int N>
 MKV_DEV float row_bcast(float v) {

@@ -44,10 +44,11 @@ constexpr int kBN = 64;                            // keys per LDS tile
 // static LDS: 4 tiles of 64 keys x 256 bytes (K and V, double-buffered);
 // dynamic LDS: row visibility [128] + 4 ints, per-token scales [2][256]
 // (per tile buffer: K then V scales of the tile's 64 keys, and with head
-// pairing the same for the pair's second KV head), then the inline tile
+// pairing the same for the pair's second KV head), the largest V scale of
+// each buffer's tile [2][2] (per KV head of a pair), then the inline tile
 // list (8-aligned)
 constexpr int kScPerBuf = 256;
-constexpr int kTileListOffset = (128 + 4) * 4 + 2 * kScPerBuf * 4;
+constexpr int kTileListOffset = (128 + 4) * 4 + 2 * kScPerBuf * 4 + 4 * 4;
 static_assert(kTileListOffset % 8 == 0, "TilePick holds 64-bit fields");
 constexpr int kXcds = 8;
 constexpr float kNegBig = -1e30f;
@@ -360,6 +361,24 @@ MKV_DEV float max_xor32(float x) {
   return vmax_quiet(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Maximum over the wave's 64 lanes by DPP moves (quad_perm xor 1 and xor 2,
+// the half-row and row mirrors) and the two lane swaps: no lane index
+// arithmetic (__shfl_xor's would stay live across the key loop) and no LDS.
+MKV_DEV float wave_max_dpp(float x) {
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xf, 0xf, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xf, 0xf, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xf, 0xf, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xf, 0xf, false)));
+  return max_xor32(max_xor16(x));
+}
+
+// A workgroup-uniform 64-bit value in scalar registers.
+MKV_DEV int64_t uniform_i64(int64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // mask bit of the lane set ? b : a, as one v_cndmask_b32 (opaque to LLVM,
 // which folds two such selects of one vector into a dynamic index)
 MKV_DEV uint32_t lane_select(uint32_t a, uint32_t b, uint64_t mask) {
@@ -536,18 +555,21 @@ struct LdsTile {
 // from busy at two waves per SIMD; the compiler keeps the kernel within 128
 // registers, and the paged variants hold nothing in scratch inside the key
 // loop (a reload there waits for the tile prefetch as well).
-// QSPLIT (bf16 caches with an fp32 / fp16 q only): bf16 holds such a q to 8
-// bits, so q is split into bf16 hi + lo terms and each QK step takes a second
-// MFMA, giving ~16 significant bits like the fp32 reference.
+// QSPLIT (bf16 caches with an fp32 / fp16 q, per-token-head caches with an
+// fp32 q): the operand type holds such a q to 8 (bf16) or 11 (fp16) bits, so
+// q is split into hi + lo terms and each QK step takes a second MFMA, giving
+// ~16 or more significant bits like the fp32 reference.
 template <int KV_DT, bool PAGED, bool QSPLIT, bool PAIR>
 MKV_DEV void prefill_mfma_body(const PrefillArgs& a) {
   using LT = LdsTile<KV_DT>;
   // CT: the element type of the LDS tiles and the MFMA operands (fp16 for
-  // an FP8 cache, converted exactly while staging).
-  // Per-token-head FP8 / INT8 caches: codes staged as exact bf16, scales
-  // applied per key (K scale to the score, V scale to P).
+  // 1-byte caches, converted exactly while staging).
+  // Per-token-head FP8 / INT8 caches: codes staged as exact fp16, scales
+  // applied per key (K scale to the score, V scale to P, which stays one
+  // fp16 term: the running max is raised where a tile's V scales would take
+  // P * v_scale past the fp16 range, see the softmax below).
   constexpr bool kTokScale = kPerTokenScale<KV_DT>;
-  constexpr int CT = kTokScale ? MKV_DTYPE_BF16 : (KV_DT == MKV_DTYPE_FP8E4M3 ? MKV_DTYPE_F16 : KV_DT);
+  constexpr int CT = (KV_DT == MKV_DTYPE_FP8E4M3 || kTokScale) ? MKV_DTYPE_F16 : KV_DT;
   constexpr int kEbG = DTypeInfo<KV_DT>::kBytes;  // cache element bytes
   constexpr int kChunksG = kHeadDim * kEbG / 16;   // 16-byte chunks per cache row
   extern __shared__ __align__(16) char smem[];
@@ -566,7 +588,8 @@ MKV_DEV void prefill_mfma_body(const PrefillArgs& a) {
   int* red_lds = vis_lds + kRowsPerWg;                             // [2]
   // per-token-head scales of the staged tiles: [buffer][K keys 0..63, V keys 0..63]
   float* sc_lds = reinterpret_cast<float*>(red_lds + 4);
-  static_assert(kTileListOffset == (kRowsPerWg + 4) * 4 + 2 * kScPerBuf * 4, "LDS layout");
+  float* vmax_lds = sc_lds + 2 * kScPerBuf;  // [buffer][KV head of a pair]: the tile's largest V scale
+  static_assert(kTileListOffset == (kRowsPerWg + 4) * 4 + 2 * kScPerBuf * 4 + 4 * 4, "LDS layout");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -580,7 +603,9 @@ MKV_DEV void prefill_mfma_body(const PrefillArgs& a) {
   WgWork wk;
   if (!wg_tile<PAGED>(a, smem, wk)) return;
   const int kvh = wk.kvh, seq = wk.seq;
-  const int64_t q_seq0 = wk.q_seq0, q0 = wk.q0, q1 = wk.q1;
+  // (uniform: in scalar registers, not held in vector registers across the
+  // key loop for the epilogue)
+  const int64_t q_seq0 = uniform_i64(wk.q_seq0), q0 = uniform_i64(wk.q0), q1 = uniform_i64(wk.q1);
   const int G = a.group;
 
   // Block-table entries of a tile, read one tile ahead of their use by a
@@ -824,14 +849,12 @@ MKV_DEV void prefill_mfma_body(const PrefillArgs& a) {
       if constexpr (kEbG == 2) {
         *reinterpret_cast<u32x4*>(dst + lds_base) = stg[u];
       } else {
-        // e4m3 -> fp16 (per tensor) or e4m3 / int8 -> bf16 (per token and
-        // head) is exact; elements 8h .. 8h+7 of the chunk from dwords 2h, 2h+1
+        // e4m3 / int8 -> fp16 is exact; elements 8h .. 8h+7 of the chunk
+        // from dwords 2h, 2h+1
         auto pair = [&](uint32_t d, auto hi_tag) -> uint32_t {
           constexpr bool kHi = decltype(hi_tag)::value;
           if constexpr (KV_DT == kKvI8PerToken)
-            return __builtin_bit_cast(uint32_t, i8x2_to_bf16x2<kHi>(d));
-          else if constexpr (KV_DT == kKvFp8PerToken)
-            return __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<kHi>(d));
+            return __builtin_bit_cast(uint32_t, i8x2_to_f16x2<kHi>(d));
           else
             return __builtin_bit_cast(uint32_t, fp8x2_to_f16x2<kHi>(d));
         };
@@ -848,8 +871,15 @@ MKV_DEV void prefill_mfma_body(const PrefillArgs& a) {
             half(lane_select(stg[u][2], stg[u][0], ld_b_mask), lane_select(stg[u][3], stg[u][1], ld_b_mask));
       }
     }
-    if constexpr (kTokScale)
+    if constexpr (kTokScale) {
       if (tid < kScLoads) sc_lds[buf * kScPerBuf + tid] = stg_sc;
+      // the waves holding V scales (tid & 64; with head pairing one per KV
+      // head) also store the tile's largest one
+      if (tid < kScLoads && (tid & 64)) {
+        const float vm = wave_max_dpp(stg_sc);
+        if (lane == 0) vmax_lds[2 * buf + (tid >> 7)] = vm;
+      }
+    }
   };
 
   // Transposed V reads.  ds_read_b64_tr_b16: within each 16-lane group, lane
@@ -906,8 +936,7 @@ MKV_DEV void prefill_mfma_body(const PrefillArgs& a) {
   if constexpr (KV_DT == MKV_DTYPE_FP8E4M3) score_mul *= load_uniform_f32(a.k_scale);
   if constexpr (CT != MKV_DTYPE_BF16) {
     // power-of-two normalisation so that q is exact and in range in fp16
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) qmax = fmaxf(qmax, __shfl_xor(qmax, off));
+    qmax = wave_max_dpp(qmax);
     if (qmax > 0.0f && qmax < __builtin_huge_valf()) {
       const int e = ilogbf(qmax);
       const float f = ldexpf(1.0f, 8 - e);
@@ -1014,6 +1043,22 @@ MKV_DEV void prefill_mfma_body(const PrefillArgs& a) {
     // is the scaled max of the raw ones (rounding a product by a positive
     // constant is monotonic), and each P takes one FMA.
     float l_scaled[kRowTiles];
+    // Per-token-head V scales fold into P, which must stay below the fp16
+    // maximum: P <= 2^8 (the lazy rescale), so a tile whose largest V scale
+    // is 2^e times a fraction in [1/2, 1) with e > 7 lifts the max it offers
+    // the running max by e - 7 (log2 units), which keeps P * v_scale <= 2^15.
+    // Any offset of the running max cancels in the normalisation; with every
+    // V scale below 128 (FP8 amax < 57344, INT8 amax < 16256) it is 0.
+    // (The scale is the same in every lane: its exponent is taken from the
+    // bits in scalar registers, e = biased exponent - 126, so the lift holds
+    // no vector register through the softmax.)
+    float v_lift = 0.0f;
+    if constexpr (kTokScale) {
+      float vm = vmax_lds[2 * buf];
+      if constexpr (PAIR) vm = fmaxf(vm, vmax_lds[2 * buf + 1]);
+      const int e = ((__builtin_amdgcn_readfirstlane(__float_as_int(vm)) >> 23) & 0xff) - 126;
+      v_lift = e > 7 ? (float)(e - 7) : 0.0f;
+    }
     // per-token-head K scales of this lane's keys 16kt + 4kg + r
     if constexpr (kTokScale) {
 #pragma unroll
@@ -1043,7 +1088,7 @@ MKV_DEV void prefill_mfma_body(const PrefillArgs& a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][rt][r]);
       mx = max_xor32(max_xor16(mx));
-      mx = fmaxf(mx * score_mul, kNegBig);
+      mx = fmaxf(mx * score_mul, kNegBig) + v_lift;
       // Lazy rescale: the running max only moves when the tile's max exceeds
       // it by more than kRescaleSlack (log2 units), so P <= 2^kRescaleSlack,
       // exact and in range in bf16/fp16; the output rescale below then runs
@@ -1703,7 +1748,9 @@ int dispatch_prefill(PrefillArgs& a, int kv_dtype, void* workspace, size_t works
                        PAGED ? a.context_lens : nullptr, a.ctx_i64, ctx_cap, a.num_seqs, a.tok_per_wg,
                        a.tile_start, order);
   }
-  const bool q16 = a.q_dtype == MKV_DTYPE_BF16;
+  // per-token-head caches run fp16 operands: a bf16 / fp16 q is exact in
+  // fp16 after its power-of-two normalisation, an fp32 q takes two terms
+  const bool q16 = a.q_dtype != MKV_DTYPE_F32;
   switch (kv_dtype) {
     case MKV_DTYPE_F32: return launch_prefill_f32<PAGED>(a, s);
     case MKV_DTYPE_FP8E4M3: return launch_prefill<MKV_DTYPE_FP8E4M3, PAGED, false>(a, s);

@@ -14,8 +14,10 @@ likewise.  The Attention layer runs full prefill -> chunked prefill ->
 decode at head_dim 64.
 
 Tolerances (absolute, before the output's own rounding): 2e-3 for fp32 /
-bf16 / fp16 KV and per-token-head codes (the oracle reads the same codes and
-scales), 2e-2 for FP8 per tensor (as at head_dim 128).
+bf16 / fp16 KV and for decode over per-token-head codes (the oracle reads
+the same codes and scales), 2e-2 for FP8 per tensor and for prefill over
+per-token-head codes (as at head_dim 128: their prefill takes P times the V
+scale as one fp16 MFMA operand, 11 bits).
 """
 from __future__ import annotations
 
@@ -36,6 +38,7 @@ pytestmark = pytest.mark.gpu
 D = 64
 FORMATS = ["f32", "bf16", "f16", "fp8", "fp8_token", "int8_token"]
 TOL = {"f32": 2e-3, "bf16": 2e-3, "f16": 2e-3, "fp8": 2e-2, "fp8_token": 2e-3, "int8_token": 2e-3}
+PREFILL_TOL = {**TOL, "fp8_token": 2e-2, "int8_token": 2e-2}
 ROUTES = [0, A.DECODE_STREAM, 64, A.DECODE_WORKGROUP]
 MODE = {"fp8": "fp8_per_tensor", "fp8_token": "fp8_per_token_head", "int8_token": "int8_per_token_head"}
 
@@ -197,7 +200,7 @@ def test_prefill_head_dim64_groups_formats(dev, fmt, group):
         k_scale=dp[2], v_scale=dp[3], kv_cache_dtype=mode).cpu()
     want = R.paged_prefill_ref(q.double(), hp[0], hp[1], bt, ctx, cu, pos, sc, Hq, Hkv, hp[2], hp[3])
     assert got.shape == q.shape and got.dtype == q.dtype
-    assert_close_out(got, want, got.dtype, TOL[fmt])
+    assert_close_out(got, want, got.dtype, PREFILL_TOL[fmt])
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
@@ -243,6 +246,7 @@ def test_attention_layer_head_dim64_full_then_chunked_then_decode(dev, mode):
     bt = torch.tensor(tables, dtype=torch.int32)
     lens = [0, 0, 0]
     tol = TOL["fp8"] if mode == "fp8_per_tensor" else 2e-3
+    tol_prefill = TOL["fp8"] if mode != "auto" else 2e-3
 
     def step(new_tokens, full):
         seqs = [s for s in range(3) if new_tokens[s] > 0]
@@ -288,7 +292,7 @@ def test_attention_layer_head_dim64_full_then_chunked_then_decode(dev, mode):
             want = R.flash_prefill_ref(q.double(), k.double(), v.double(), cu, sm, Hq, Hkv)
         else:
             want = R.paged_prefill_ref(q.double(), kc, vc, btd, ctx, cu, pos, sm, Hq, Hkv, ks, vs)
-        assert_close_out(out.reshape(T, Hq, D), want, torch.bfloat16, tol)
+        assert_close_out(out.reshape(T, Hq, D), want, torch.bfloat16, tol if decode or full else tol_prefill)
 
     step([37, 100, 5], full=True)
     step([20, 1, 64], full=False)

@@ -12,7 +12,10 @@ KV against unquantised values).
 
 Chunked prefill over the same caches (an extension; the reference's prefill
 raises for quantised caches): the operator and the Attention layer's mixed
-batch, against the oracle on the same codes and scales, with the same bound.
+batch, against the oracle on the same codes and scales, within the FP8 KV
+bound of 2e-2 (plus half an output ulp): the prefill kernel takes P times
+the V scale as one fp16 MFMA operand (11 bits, as its per-tensor FP8 form
+takes P), which leaves up to ~2^-12 |v| (3e-3 on these caches' |v| <= 16).
 """
 from __future__ import annotations
 
@@ -30,6 +33,7 @@ pytestmark = pytest.mark.gpu
 FP8_MODE, INT8_MODE = "fp8_per_token_head", "int8_per_token_head"
 CACHE_DT = {FP8_MODE: torch.float8_e4m3fn, INT8_MODE: torch.int8}
 TOL = 2e-3
+PREFILL_TOL = 2e-2
 
 
 def _u8(t):
@@ -331,7 +335,32 @@ def test_per_token_prefill_matches_oracle(dev, mode, group, qdt):
     sc = 1 / math.sqrt(128)
     got = _prefill_gpu(dev, mode, q, kq, vq, ks, vs, bt, ctx, cu, pos, sc, Hkv * group, Hkv)
     want = R.paged_prefill_ref(q.double(), kq, vq, bt, ctx, cu, pos, sc, Hkv * group, Hkv, ks, vs)
-    assert_close_out(got, want, got.dtype, TOL)
+    assert_close_out(got, want, got.dtype, PREFILL_TOL)
+    # and the arithmetic's own bound: one fp16 rounding of each P * v_scale
+    # (2^-12 relative) weighs at most max |v|, taken here with a factor 2
+    vmax = float((vq.float() * vs[..., None]).abs().max())
+    assert_close_out(got, want, got.dtype, 2e-3 + 2.0 ** -11 * vmax)
+
+
+@pytest.mark.parametrize("mode", [FP8_MODE, INT8_MODE])
+@pytest.mark.parametrize("qdt,group", [(torch.bfloat16, 4), (torch.float32, 4), (torch.bfloat16, 16)])
+def test_per_token_prefill_large_v_scales(dev, mode, qdt, group):
+    """V scales 2^20 times the usual (V values of ~10^6): the prefill's P
+    times the V scale is an fp16 MFMA operand, and a tile whose V scales
+    would carry it past the fp16 maximum lifts the running max instead.
+    The output is 2^20 times the unscaled one; divided back (exact for a
+    power of two) it meets the oracle on the unscaled caches within the
+    prefill bound."""
+    announce(f"per-token prefill {mode} q {qdt} group {group}, V scales x 2^20")
+    Hkv = 2
+    q, kq, vq, ks, vs, bt, ctx, cu, pos = _prefill_case(60 + group, mode, [0, 400, 90], [130, 70, 200],
+                                                        Hkv * group, Hkv, 16, qdt)
+    sc = 1 / math.sqrt(128)
+    S = float(2 ** 20)
+    got = _prefill_gpu(dev, mode, q, kq, vq, ks, vs * S, bt, ctx, cu, pos, sc, Hkv * group, Hkv)
+    assert torch.isfinite(got.float()).all()
+    want = R.paged_prefill_ref(q.double(), kq, vq, bt, ctx, cu, pos, sc, Hkv * group, Hkv, ks, vs)
+    assert_close_out(got / S, want, got.dtype, PREFILL_TOL)
 
 
 @pytest.mark.parametrize("mode", [FP8_MODE, INT8_MODE])
@@ -344,7 +373,7 @@ def test_per_token_prefill_block_sizes_holes_and_context_caps(dev, mode, bs):
     ctx2[0] = 50  # context shorter than some positions: visible = min(ctx, pos + 1)
     got = _prefill_gpu(dev, mode, q, kq, vq, ks, vs, bt, ctx2, cu, pos, 0.1, 8, 2)
     want = R.paged_prefill_ref(q.double(), kq, vq, bt, ctx2, cu, pos, 0.1, 8, 2, ks, vs)
-    assert_close_out(got, want, got.dtype, TOL)
+    assert_close_out(got, want, got.dtype, PREFILL_TOL)
 
 
 @pytest.mark.parametrize("mode", [FP8_MODE, INT8_MODE])
@@ -380,4 +409,4 @@ def test_attention_layer_per_token_mixed_batch(dev, mode, route):
         C.reset_context()
     want = R.paged_prefill_ref(q.double(), kq, vq, bt, ctx, cu, pos, 1 / math.sqrt(128), Hq, Hkv,
                                ks, vs)
-    assert_close_out(out, want, out.dtype, TOL)
+    assert_close_out(out, want, out.dtype, PREFILL_TOL)
