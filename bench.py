@@ -595,7 +595,10 @@ def mixed_batch_extra(dev, stream, cpu: bool = True) -> dict:
 def graph_time_us(fn, reps: int = 20, replays: int = 10) -> float:
     """Device time per call of fn (µs), from replays of a HIP graph that
     holds `reps` back-to-back calls: for launches shorter than the host's
-    enqueue time, where an eager loop would time the host."""
+    enqueue time, where an eager loop would time the host.  The replays are
+    settled first (chunks of 4 until four chunk means agree within 1%, at
+    most 200 replays), as the headline step is: a series that starts from
+    an idle GPU runs through the power controller's transient."""
     import torch
 
     fn()
@@ -612,6 +615,7 @@ def graph_time_us(fn, reps: int = 20, replays: int = 10) -> float:
             fn()
     for _ in range(3):
         g.replay()
+    settle(lambda i: g.replay(), torch.cuda.current_stream(), chunk=4, tol=0.01, max_steps=200)
     torch.cuda.synchronize()
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
