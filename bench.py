@@ -961,7 +961,21 @@ def e2e_extra(dev, baselines: bool = True) -> dict:
     torch.cuda.synchronize()
     eres = eager.summary(time.perf_counter() - t0)
     res["mkv_eager_engine"] = {k: eres[k] for k in ("e2e_decode_tok_s", "decode_only_tok_s", "wall_s")}
-    del eng, eager, model
+    # the same captured engine with the reference's most accurate KV mode,
+    # FP8 codes with one scale per slot and KV head (decode steps as the
+    # producer and the per-token-head decode, two calls per layer)
+    ptok = E.Engine(model, num_blocks=512, max_num_seqs=64, max_num_batched_tokens=1024,
+                    kv_cache_dtype="fp8_per_token_head", max_model_len=4096, seed=0)
+    ptok.generate(prompts, max_tokens=256)  # warm-up
+    ptok.stats.clear()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ptok.generate(prompts, max_tokens=256)
+    torch.cuda.synchronize()
+    pres = ptok.summary(time.perf_counter() - t0)
+    res["mkv_engine_fp8_per_token_head_kv"] = {k: pres[k] for k in ("e2e_decode_tok_s", "decode_only_tok_s",
+                                                                     "wall_s")}
+    del eng, eager, ptok, model
     torch.cuda.empty_cache()
     # the same engine and workload with the reference's PyTorch attention on the GPU
     base_model = _torch_attention_model()(cfg, dev, seed=5, block_size=256)

@@ -303,16 +303,20 @@ class Qwen3Model(torch.nn.Module):
     def attach_kv_cache(self, num_blocks: int, kv_cache_dtype: str = "fp8_per_tensor",
                         cache_dtype: torch.dtype | None = None) -> None:
         """Allocate every layer's pools (num_blocks, block_size, Hkv, D) and
-        per-tensor scales (the 1.0 sentinel, model_runner.py:311-329) and
-        inject them into the attention layers (:376-395)."""
+        scales and inject them into the attention layers (:376-395):
+        per-tensor scales hold the 1.0 sentinel (model_runner.py:311-329);
+        the per-token-head modes ('fp8_per_token_head', 'int8_per_token_head')
+        keep one fp32 K and one V scale per slot and KV head,
+        (num_blocks, block_size, Hkv) (:330-338), written by the append."""
         cfg = self.cfg
         dev = self.embed.device
-        if kv_cache_dtype == "fp8_per_tensor":
-            cdt = torch.float8_e4m3fn
-        elif kv_cache_dtype == "auto":
+        cdt = {"fp8_per_tensor": torch.float8_e4m3fn, "fp8_per_token_head": torch.float8_e4m3fn,
+               "int8_per_token_head": torch.int8}.get(kv_cache_dtype)
+        if kv_cache_dtype == "auto":
             cdt = cache_dtype or self.embed.dtype
-        else:
-            raise ValueError(f"kv_cache_dtype {kv_cache_dtype!r}: the engine runs 'auto' or 'fp8_per_tensor'")
+        elif cdt is None:
+            raise ValueError(f"kv_cache_dtype {kv_cache_dtype!r}: the engine runs 'auto', 'fp8_per_tensor', "
+                             "'fp8_per_token_head' or 'int8_per_token_head'")
         self.kv_cache_dtype = kv_cache_dtype
         for lay in self.layers:
             att = lay["attn"]
@@ -323,8 +327,16 @@ class Qwen3Model(torch.nn.Module):
             if kv_cache_dtype == "fp8_per_tensor":
                 att.k_scale = torch.ones(1, device=dev)
                 att.v_scale = torch.ones(1, device=dev)
+            elif kv_cache_dtype != "auto":
+                att.k_scale = torch.zeros(num_blocks, self.block_size, cfg.num_kv_heads, device=dev)
+                att.v_scale = torch.zeros_like(att.k_scale)
 
     def scales(self) -> list[torch.Tensor]:
+        """The per-tensor FP8 scales (what a decode graph's capture must
+        leave as it found them); per-token-head scales are written only by
+        appends to real slots."""
+        if self.kv_cache_dtype != "fp8_per_tensor":
+            return []
         return [s for lay in self.layers for s in (lay["attn"].k_scale, lay["attn"].v_scale)
                 if s is not None]
 

@@ -42,7 +42,7 @@ def _engine(dev, use_graphs=True, model_cls=E.Qwen3Model, kv="fp8_per_tensor", s
                     decode_split_tokens=split)
 
 
-@pytest.mark.parametrize("kv", ["fp8_per_tensor", "auto"])
+@pytest.mark.parametrize("kv", ["fp8_per_tensor", "auto", "fp8_per_token_head", "int8_per_token_head"])
 def test_captured_decode_generates_the_eager_tokens(dev, kv):
     announce(f"engine: captured vs eager decode, 2-layer model, {kv} KV")
     prompts = _prompts(11)
@@ -70,9 +70,12 @@ class OracleAttentionModel(E.Qwen3Model):
         att = self.layers[li]["attn"]
         Hq, Hkv = self.cfg.num_heads, self.cfg.num_kv_heads
         sm = 1.0 / math.sqrt(self.cfg.head_dim)
-        fp8 = att.kv_cache_dtype == "fp8_per_tensor"
-        ks = float(att.k_scale) if fp8 else None
-        vs = float(att.v_scale) if fp8 else None
+        if att.kv_cache_dtype == "fp8_per_tensor":
+            ks, vs = float(att.k_scale), float(att.v_scale)
+        elif att.kv_cache_dtype == "auto":
+            ks = vs = None
+        else:  # per-token-head: the (N, bs, Hkv) scales the appends wrote
+            ks, vs = att.k_scale.cpu(), att.v_scale.cpu()
         kc, vc = att.k_cache.cpu(), att.v_cache.cpu()
         if ctx.is_prefill and ctx.is_full_prefill:
             out = R.flash_prefill_ref(q.cpu().double(), k.cpu().double(), v.cpu().double(),
@@ -93,9 +96,23 @@ def test_engine_logits_match_the_oracle_attention_engine(dev, monkeypatch, split
     attention; decode by stream-K (split 0), by 32-token split-K and by the
     workgroup route (-1, one workgroup per sequence and KV head)."""
     announce(f"engine: logits vs the same engine with oracle attention, every step, split {split}")
+    _logits_vs_oracle(dev, monkeypatch, split, "fp8_per_tensor")
+
+
+@pytest.mark.parametrize("kv", ["fp8_per_token_head", "int8_per_token_head"])
+def test_engine_per_token_head_kv_logits_match_the_oracle_attention_engine(dev, monkeypatch, kv):
+    """The per-token-head KV modes through the engine (per-slot scales
+    written by the producer's append; decode, chunked prefill and the mixed
+    steps on the per-token-head kernels): every step's logits against the
+    oracle-attention engine over its own codes and scales."""
+    announce(f"engine: {kv} KV, logits vs the same engine with oracle attention, every step")
+    _logits_vs_oracle(dev, monkeypatch, 0, kv)
+
+
+def _logits_vs_oracle(dev, monkeypatch, split, kv):
     prompts = _prompts(12)
-    eng = _engine(dev, True, split=split)
-    ref = _engine(dev, False, model_cls=OracleAttentionModel)
+    eng = _engine(dev, True, split=split, kv=kv)
+    ref = _engine(dev, False, model_cls=OracleAttentionModel, kv=kv)
     for e in (eng, ref):
         for p in prompts:
             e.add_request(p, max_tokens=6)
