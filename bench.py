@@ -962,8 +962,8 @@ def e2e_extra(dev, baselines: bool = True) -> dict:
     eres = eager.summary(time.perf_counter() - t0)
     res["mkv_eager_engine"] = {k: eres[k] for k in ("e2e_decode_tok_s", "decode_only_tok_s", "wall_s")}
     # the same captured engine with the reference's most accurate KV mode,
-    # FP8 codes with one scale per slot and KV head (decode steps as the
-    # producer and the per-token-head decode, two calls per layer)
+    # FP8 codes with one scale per slot and KV head (each decode step's
+    # producer and per-token-head decode in one launch per layer)
     ptok = E.Engine(model, num_blocks=512, max_num_seqs=64, max_num_batched_tokens=1024,
                     kv_cache_dtype="fp8_per_token_head", max_model_len=4096, seed=0)
     ptok.generate(prompts, max_tokens=256)  # warm-up

@@ -447,12 +447,14 @@ int mkv_qkv_norm_rope_append(const void* qkv, int64_t qkv_row_stride,
  * reference's prepare_decode builds it (model_runner.py:621-640), and no
  * other row of the batch may read it: the attention sees the appended row
  * at that position only.
- * Supported: kv_dtype FP8E4M3 with kv_scale_mode PER_TENSOR, F16, or BF16
- * with out_dtype BF16; head_dim 128; num_heads / num_kv_heads <= 8
- * (MKV_ERR_UNSUPPORTED_DTYPE / MKV_ERR_UNSUPPORTED_HEAD_DIM /
- * MKV_ERR_UNSUPPORTED_GROUP otherwise, before any launch: run the two
- * calls).  flags as mkv_qkv_norm_rope_append (the 1.0-sentinel calibration
- * uses this call's rows; 16-bit caches take no scales).
+ * Supported: kv_dtype FP8E4M3 with kv_scale_mode PER_TENSOR; F16; BF16,
+ * or FP8E4M3 / I8 with kv_scale_mode PER_TOKEN_HEAD (k_scale / v_scale the
+ * per-slot scales, written for the appended rows), with out_dtype BF16;
+ * head_dim 128; num_heads / num_kv_heads <= 8 (MKV_ERR_UNSUPPORTED_DTYPE /
+ * MKV_ERR_UNSUPPORTED_HEAD_DIM / MKV_ERR_UNSUPPORTED_GROUP otherwise,
+ * before any launch: run the two calls).  flags as mkv_qkv_norm_rope_append
+ * (the 1.0-sentinel calibration uses this call's rows; it applies to
+ * per-tensor FP8 only; 16-bit caches take no scales).
  */
 int mkv_qkv_norm_rope_append_decode(
     void* out, int64_t out_batch_stride, int out_dtype,

@@ -176,7 +176,11 @@ MKV_DEV u32x4 quantize16_fp8(const float (&x)[16], const Fp8Quant& q) {
 // 1 / scale), rounded half away from zero, clamped to [-128, 127] with
 // maxNum / minNum (a NaN becomes -128), truncated.
 MKV_DEV uint32_t quantize_i8(float xv, float inv) {
+  // (the product is rounded on its own, as in the reference: hipcc
+  // compiles with -ffp-contract=fast, which could fuse it into the +-0.5
+  // as one FMA with a single rounding; the empty asm keeps it apart)
   float y = xv * inv;
+  asm volatile("" : "+v"(y));
   y = y >= 0.0f ? y + 0.5f : y - 0.5f;
   y = fminf(fmaxf(y, -128.0f), 127.0f);
   return (uint32_t)((int)y & 0xff);

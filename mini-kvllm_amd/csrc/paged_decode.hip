@@ -1042,14 +1042,16 @@ __global__ __launch_bounds__(kWgSplitWaves* kWave) void paged_decode_wg_qsplit_k
 // workgroup of (sequence b, KV head kvh) of the workgroup route does both:
 // its waves share out the token's q heads of the group and its K and V
 // heads kvh (one head per wave pass, 64 lanes wide, with the producer
-// kernel's operations in the producer kernel's order), put q and the FP8
-// K / V row in LDS, and append the row; the wave whose tile holds the
-// token's position takes that row from LDS instead of from the cache (the
-// tile's loads may have left before the append landed).  The result is the
-// producer kernel followed by the workgroup route, bit for bit.
+// kernel's operations in the producer kernel's order), put q and the new
+// K / V cache rows in LDS, and append the rows.  Per-tensor FP8: the tiles'
+// loads go out before the append lands, and the wave whose tile holds the
+// token's position takes that row from LDS instead of from the cache.
+// 16-bit and per-token-head caches: every tile is loaded after the append
+// has landed.  The result is the producer kernel followed by the workgroup
+// route, bit for bit.
 // LDS (dynamic): the workgroup merge area of wg_merge_store, then q of the
-// group's heads (fp32 [G][128]) and the new token's FP8 K row and V row
-// (128 bytes each).
+// group's heads (fp32 [G][128]) and the new token's K row and V row (128
+// elements each in the cache dtype).
 // ---------------------------------------------------------------------------
 constexpr int kFusedMaxGroup = 8;  // query heads per KV head
 
@@ -1058,14 +1060,6 @@ struct ProduceDecodeArgs {
   ProducerArgs p;  // the producer step of the batch's one token per sequence
 };
 
-// Replace row p (0..31, wave-uniform) of a tile, as loaded (before
-// k_exchange), with the new token's K / V row at kv in LDS (the cache row's
-// bytes of this KV head: K, then V).
-//   FP8: load A of sub-tile m holds row c & 7, bytes 32kg + (c < 8 ? 0 : 16);
-//     load B row (c & 7) + 8, bytes 32kg + (c < 8 ? 16 : 0) (fp8_k_lanes);
-//     V word i: row 16 (i >> 2) + 4kg + (i & 3), bytes 8c .. 8c+7.
-//   16-bit: K word i of sub-tile m: row 16m + c, bytes 64kg + 16i; V word i:
-//     row 16 (i >> 2) + 4kg + (i & 3), bytes 16c .. 16c+15.
 // Replace row p (0..31, wave-uniform) of an FP8 tile, as loaded (before
 // k_exchange), with the new token's K / V row at kv in LDS (the cache row's
 // bytes of this KV head: K, then V).  Load A of sub-tile m holds row c & 7,
@@ -1111,13 +1105,16 @@ MKV_DEV uint32_t fp8_code(float x, const Fp8Quant& q) {
   return quantize4_fp8(v, q) & 0xffu;
 }
 
-// KV_DT: MKV_DTYPE_FP8E4M3 (per-tensor scales) or a 16-bit cache (copy
-// append, cast to the cache dtype).  1-byte caches take the workgroup
-// route's round-robin tiles with a speculative first tile (wg_decode_rr),
-// 16-bit caches its consecutive ranges (wg_decode_contig).
+// KV_DT: MKV_DTYPE_FP8E4M3 (per-tensor scales), a per-token-head FP8 /
+// INT8 format (one scale per slot and KV head, from the head's amax, as
+// store_kv writes it) or a 16-bit cache (copy append, cast to the cache
+// dtype).  1-byte caches take the workgroup route's round-robin tiles
+// (wg_decode_rr; per-tensor FP8 with its speculative first tile), 16-bit
+// caches its consecutive ranges (wg_decode_contig).
 template <int IN_DT, int KV_DT>
 MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
   constexpr bool kFp8 = KV_DT == MKV_DTYPE_FP8E4M3;
+  constexpr bool kTok = kPerTokenScale<KV_DT>;
   constexpr int kEb = DTypeInfo<KV_DT>::kBytes;
   constexpr int kIb = DTypeInfo<IN_DT>::kBytes;
   extern __shared__ float wg_lds[];
@@ -1187,7 +1184,8 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
   const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
   const int64_t L = L_raw < 0 ? 0 : (L_raw > cap ? cap : L_raw);
   int step = 32 * nw;
-  if constexpr (!kFp8) {
+  if constexpr (kTok) it.t_end = (int)(L < it.t_end ? L : it.t_end);
+  if constexpr (kEb == 2) {
     const int tiles = (int)((L + 31) >> 5);
     const int per = (tiles + nw - 1) / nw;
     const int64_t tb = (int64_t)wv * per * 32, te = tb + (int64_t)per * 32;
@@ -1209,8 +1207,9 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
   // inputs, and the new token's row is patched into the tile that holds
   // position L - 1 when this call appends it there (slot = that position's
   // cache row): that tile's loads may have left before the append landed.
-  // 16-bit caches load their tiles after the append has landed instead (the
-  // patch's registers beside two 16-bit tiles would spill).
+  // 16-bit and per-token-head caches load their tiles after the append has
+  // landed instead (the patch's registers beside two 16-bit tiles would
+  // spill; a per-token-head tile would also need the row's scales patched).
   bool patch = false;
   const int pl = (int)L - 1;
   if constexpr (kFp8) {
@@ -1263,9 +1262,29 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
       // codes or 2 16-bit values)
       uint32_t w1, w2;
       bool lead;
-      if constexpr (kFp8) {
-        const Fp8Quant qz = fp8_quant(hs == G ? ks : vs);
-        const uint32_t b1 = fp8_code(o1, qz), b2 = fp8_code(o2, qz);
+      if constexpr (kEb == 1) {
+        // per-tensor: the tensor's scale; per token and head: store_kv's
+        // scale of the head's amax (exact whatever the order), stored by one
+        // lane, and its codes
+        uint32_t b1, b2;
+        if constexpr (kTok) {
+          const float am = wave_max(fmaxf(fmaxf(0.0f, fabsf(o1)), fabsf(o2)));
+          const float hsc = KV_DT == kKvI8PerToken ? i8_head_scale(am) : fp8_head_scale(am);
+          if constexpr (KV_DT == kKvI8PerToken) {
+            const float inv = 1.0f / hsc;
+            b1 = quantize_i8(o1, inv) & 0xffu;
+            b2 = quantize_i8(o2, inv) & 0xffu;
+          } else {
+            const Fp8Quant qz = fp8_quant(hsc);
+            b1 = fp8_code(o1, qz);
+            b2 = fp8_code(o2, qz);
+          }
+          if (append && lane == 0) (hs == G ? pa.k_scale : pa.v_scale)[slot * pa.num_kv_heads + it.kvh] = hsc;
+        } else {
+          const Fp8Quant qz = fp8_quant(hs == G ? ks : vs);
+          b1 = fp8_code(o1, qz);
+          b2 = fp8_code(o2, qz);
+        }
         w1 = b1 | (uint32_t)__shfl(b1, lane + 1) << 8 | (uint32_t)__shfl(b1, lane + 2) << 16 |
              (uint32_t)__shfl(b1, lane + 3) << 24;
         w2 = b2 | (uint32_t)__shfl(b2, lane + 1) << 8 | (uint32_t)__shfl(b2, lane + 2) << 16 |
@@ -2922,9 +2941,10 @@ extern "C" int mkv_qkv_norm_rope_append_decode(
                        sm_scale, MKV_DECODE_WORKGROUP, d, ks, fmt);
   if (st != MKV_OK) return st;
   if (head_dim != kHeadDim || ks.pair) return MKV_ERR_UNSUPPORTED_HEAD_DIM;
-  // per-tensor FP8, or a 16-bit cache (a bf16 cache with a bf16 q: the
-  // workgroup route's kernel without the split q)
-  if (fmt != MKV_DTYPE_FP8E4M3 && fmt != MKV_DTYPE_F16 && !(fmt == MKV_DTYPE_BF16 && out_dtype == MKV_DTYPE_BF16))
+  // per-tensor FP8, fp16, or a bf16-MFMA format (bf16, per-token-head FP8 /
+  // INT8) with a bf16 q: the workgroup route's kernel without the split q
+  const bool bf16_mfma = fmt == MKV_DTYPE_BF16 || fmt == kKvFp8PerToken || fmt == kKvI8PerToken;
+  if (fmt != MKV_DTYPE_FP8E4M3 && fmt != MKV_DTYPE_F16 && !(bf16_mfma && out_dtype == MKV_DTYPE_BF16))
     return MKV_ERR_UNSUPPORTED_DTYPE;
   if (d.group > kFusedMaxGroup) return MKV_ERR_UNSUPPORTED_GROUP;
   // the producer's arguments
@@ -2978,7 +2998,7 @@ extern "C" int mkv_qkv_norm_rope_append_decode(
   p.num_slots = num_blocks * (int64_t)block_size;
 
   const int nw = wg_waves(batch, d.num_kv_heads, d.group, max_blocks, block_size, device_cus());
-  const size_t row_bytes = (size_t)kHeadDim * (fmt == MKV_DTYPE_FP8E4M3 ? 1 : 2);
+  const size_t row_bytes = (size_t)kHeadDim * (fmt == MKV_DTYPE_F16 || fmt == MKV_DTYPE_BF16 ? 2 : 1);
   const size_t lds = ((size_t)nw * d.group * (kHeadDim + 2) + (size_t)d.group * kHeadDim) * sizeof(float) +
                      2 * row_bytes;
   const dim3 grid((unsigned)((int64_t)batch * d.num_kv_heads)), block(nw * kWave);
@@ -2987,6 +3007,8 @@ extern "C" int mkv_qkv_norm_rope_append_decode(
 #define MKV_PD_KV(IDT)                                           \
   switch (fmt) {                                                 \
     case MKV_DTYPE_FP8E4M3: MKV_PD(IDT, MKV_DTYPE_FP8E4M3); break; \
+    case kKvFp8PerToken: MKV_PD(IDT, kKvFp8PerToken); break;       \
+    case kKvI8PerToken: MKV_PD(IDT, kKvI8PerToken); break;         \
     case MKV_DTYPE_BF16: MKV_PD(IDT, MKV_DTYPE_BF16); break;       \
     default: MKV_PD(IDT, MKV_DTYPE_F16); break;                    \
   }

@@ -145,8 +145,9 @@ def qkv_norm_rope_append_decode(qkv: torch.Tensor, positions: torch.Tensor, num_
     (batch, num_heads, head_dim) in out_dtype (default: qkv's dtype).
 
     At head_dim 128 with at most 8 query heads per KV head, for a per-tensor
-    FP8 cache whose scales are calibrated, an fp16 cache, or a bf16 cache
-    with a bf16 out_dtype, when the decode schedule is the workgroup route
+    FP8 cache whose scales are calibrated, an fp16 cache, or a bf16 or
+    per-token-head FP8 / INT8 cache with a bf16 out_dtype, when the decode
+    schedule is the workgroup route
     (the library's choice for the shape, or split_tokens = DECODE_WORKGROUP),
     both run in one launch (``mkv_qkv_norm_rope_append_decode``, the same
     bits as the two calls); otherwise as the two calls.  slot_mapping[b]
@@ -158,6 +159,9 @@ def qkv_norm_rope_append_decode(qkv: torch.Tensor, positions: torch.Tensor, num_
     if kv_cache_dtype == "fp8_per_tensor":
         cache_ok = (kdt == torch.float8_e4m3fn and getattr(k_scale, "_mkv_calibrated", False)
                     and getattr(v_scale, "_mkv_calibrated", False))
+    elif kv_cache_dtype in PER_TOKEN_HEAD_MODES:
+        want = torch.int8 if kv_cache_dtype == "int8_per_token_head" else torch.float8_e4m3fn
+        cache_ok = kdt == want and out_dtype == torch.bfloat16
     else:
         cache_ok = kv_cache_dtype == "auto" and (
             kdt == torch.float16 or (kdt == torch.bfloat16 and out_dtype == torch.bfloat16))
@@ -165,6 +169,9 @@ def qkv_norm_rope_append_decode(qkv: torch.Tensor, positions: torch.Tensor, num_
              and num_heads % num_kv_heads == 0 and num_heads // num_kv_heads <= 8)
     if fused:
         kv_code = _DTYPES[kdt]
+        per_token = kv_cache_dtype in PER_TOKEN_HEAD_MODES
+        if per_token:
+            _check_token_scales(k_scale, v_scale, k_cache)
         bt = _block_table(block_tables)
         cl = _ctx_lens(context_lens)
         route = split_tokens
@@ -221,10 +228,10 @@ def qkv_norm_rope_append_decode(qkv: torch.Tensor, positions: torch.Tensor, num_
         _DTYPES.get(wdt, 0) if wdt is not None else 0, float(eps), cs.data_ptr(),
         _dtype_code(cs, "cos_sin_cache"), cs.shape[0], pos.data_ptr(), k_cache.data_ptr(),
         v_cache.data_ptr(), kv_code, k_cache.shape[0],
-        k_scale.data_ptr() if kv_code == _lib.DTYPE_FP8E4M3 else None,
-        v_scale.data_ptr() if kv_code == _lib.DTYPE_FP8E4M3 else None,
-        _lib.SCALE_PER_TENSOR, slots.data_ptr(),
-        _lib.APPEND_CALIBRATE_SENTINEL if kv_code == _lib.DTYPE_FP8E4M3 else 0,
+        k_scale.data_ptr() if kv_code in (_lib.DTYPE_FP8E4M3, _lib.DTYPE_I8) else None,
+        v_scale.data_ptr() if kv_code in (_lib.DTYPE_FP8E4M3, _lib.DTYPE_I8) else None,
+        _lib.SCALE_PER_TOKEN_HEAD if per_token else _lib.SCALE_PER_TENSOR, slots.data_ptr(),
+        _lib.APPEND_CALIBRATE_SENTINEL if kv_code == _lib.DTYPE_FP8E4M3 and not per_token else 0,
         bt.data_ptr(), bt.stride(0), bt.shape[1], cl.data_ptr(), _index_dtype(cl), T, num_heads,
         num_kv_heads, head_dim, k_cache.shape[1], float(scale), _stream(dev))
     return out

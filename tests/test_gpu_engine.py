@@ -242,10 +242,11 @@ class UnfusedModel(E.Qwen3Model):
     fuse_decode_step = False
 
 
-@pytest.mark.parametrize("use_graphs,kv", [(True, "fp8_per_tensor"), (False, "fp8_per_tensor"), (True, "auto")])
+@pytest.mark.parametrize("use_graphs,kv", [(True, "fp8_per_tensor"), (False, "fp8_per_tensor"), (True, "auto"),
+                                           (True, "fp8_per_token_head"), (True, "int8_per_token_head")])
 def test_fused_decode_steps_give_the_unfused_logits(dev, monkeypatch, use_graphs, kv):
-    """The end-to-end workload's shape (2 layers, bf16 weights, FP8 per-tensor
-    or bf16 KV, 8 prompts of 32-512 tokens): with each decode step's producer
+    """The end-to-end workload's shape (2 layers, bf16 weights, FP8 per-tensor,
+    bf16 or per-token-head KV, 8 prompts of 32-512 tokens): with each decode step's producer
     step and attention in one launch (mkv_qkv_norm_rope_append_decode),
     every step's logits are bit-identical to the two calls' and so are the
     generated tokens, captured or eager."""

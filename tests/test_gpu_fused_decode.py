@@ -1,6 +1,6 @@
 """GPU parity of the fused decode step (``mkv_qkv_norm_rope_append_decode``):
 one layer's producer step for each sequence's new token (q/k RMSNorm,
-rotary embedding, FP8 or 16-bit append; reference qwen3.py:73-118,
+rotary embedding, FP8, per-token-head or 16-bit append; reference qwen3.py:73-118,
 attention.py:1654-1691) and the decode attention over the cache that holds
 it (attention.py:1213-1268), in one launch.
 
@@ -9,8 +9,8 @@ it (attention.py:1213-1268), in one launch.
   bytes and the scales are bit-identical, over group sizes 1-8, block
   sizes 16 and 256, contexts 0-800 (the new token in a wave's first,
   second or a later tile), rows without a slot, every input dtype and the
-  1.0-sentinel calibration; bf16 and fp16 caches (loaded after the append
-  has landed) over the same group sizes.
+  1.0-sentinel calibration; bf16, fp16 and per-token-head FP8 / INT8
+  caches (loaded after the append has landed) over the same group sizes.
 * Against the oracle (qkv_norm_rope_ref, then paged_decode_ref on the
   dequantised cache): within the FP8 bound, 2e-2 abs.
 """
@@ -32,7 +32,7 @@ CTX_EDGES = [0, 1, 2, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 256, 257, 511,
 
 
 def _case(dev, seed, B, Hq, Hkv, bs, in_dtype, ctx=None, no_slot=(), scale_val=None,
-          cache_dtype=torch.float8_e4m3fn):
+          cache_dtype=torch.float8_e4m3fn, per_token=False):
     g = torch.Generator().manual_seed(seed)
     if ctx is None:
         ctx = torch.tensor((CTX_EDGES * ((B + len(CTX_EDGES) - 1) // len(CTX_EDGES)))[:B])
@@ -55,14 +55,21 @@ def _case(dev, seed, B, Hq, Hkv, bs, in_dtype, ctx=None, no_slot=(), scale_val=N
     vc = torch.empty_like(kc)
     sk = 0.02 if scale_val is None else scale_val
     sv = 0.03 if scale_val is None else scale_val
-    W.fill_pool_on_device(kc, seed + 1, sk)
-    W.fill_pool_on_device(vc, seed + 2, sv)
     fp8 = cache_dtype == torch.float8_e4m3fn
-    ks = torch.full((1,), sk, device=dev) if fp8 else None
-    vs = torch.full((1,), sv, device=dev) if fp8 else None
+    if per_token:
+        kv = "int8_per_token_head" if cache_dtype == torch.int8 else "fp8_per_token_head"
+        ks = torch.empty(N, bs, Hkv, dtype=torch.float32, device=dev)
+        vs = torch.empty_like(ks)
+        W.fill_pools_per_token_head_on_device(kc, vc, ks, vs, seed + 1, kv)
+    else:
+        kv = "fp8_per_tensor" if fp8 else "auto"
+        W.fill_pool_on_device(kc, seed + 1, sk)
+        W.fill_pool_on_device(vc, seed + 2, sv)
+        ks = torch.full((1,), sk, device=dev) if fp8 else None
+        vs = torch.full((1,), sv, device=dev) if fp8 else None
     return dict(qkv=qkv.to(dev), pos=pos.to(dev), cs=cs.to(dev), qw=qw.to(dev), kw=kw.to(dev), kc=kc,
                 vc=vc, ks=ks, vs=vs, slots=slots.to(dev), bt=bt.to(dev), ctx=ctx.to(dev), B=B, Hq=Hq,
-                Hkv=Hkv, bs=bs, scale=D ** -0.5, kv="fp8_per_tensor" if fp8 else "auto")
+                Hkv=Hkv, bs=bs, scale=D ** -0.5, kv=kv)
 
 
 def _calibrated(t):
@@ -80,7 +87,7 @@ def _two_calls(c):
         q_norm_weight=c["qw"], k_norm_weight=c["kw"], kv_cache_dtype=c["kv"], k_scale=ks,
         v_scale=vs)
     out = A._decode(q, kc, vc, c["bt"], c["ctx"], c["scale"], c["Hq"], c["Hkv"], D, ks, vs,
-                    split_tokens=A.DECODE_WORKGROUP)
+                    split_tokens=A.DECODE_WORKGROUP, per_token_head=c["kv"] in A.PER_TOKEN_HEAD_MODES)
     return out, kc, vc, ks, vs, q
 
 
@@ -160,6 +167,20 @@ def test_fused_decode_step_int32_lengths_and_wide_rows(dev, cache_dtype):
     wide[:, :width] = c["qkv"]
     c["qkv"] = wide[:, :width]
     assert c["qkv"].stride(0) == width + 136
+    _assert_same(_fused(c), _two_calls(c))
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(16, 8), (32, 8), (8, 8), (64, 8), (24, 3)])
+@pytest.mark.parametrize("cache_dtype", [torch.float8_e4m3fn, torch.int8])
+@pytest.mark.parametrize("bs", [16, 256])
+def test_fused_decode_step_per_token_head_caches(dev, Hq, Hkv, cache_dtype, bs):
+    """Per-token-head FP8 / INT8 caches: each appended row's scale from its
+    head's amax (store_kv's), its codes, and the attention over every tile
+    loaded after the append; the codes, the per-slot scales and the output
+    equal the two calls'."""
+    announce(f"fused decode step per-token-head {cache_dtype} cache {Hq}/{Hkv} block {bs}")
+    c = _case(dev, Hq * 3 + bs + 2, 40, Hq, Hkv, bs, torch.bfloat16, no_slot=(6, 33),
+              cache_dtype=cache_dtype, per_token=True)
     _assert_same(_fused(c), _two_calls(c))
 
 

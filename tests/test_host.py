@@ -48,8 +48,8 @@ def test_status_strings():
 
 def test_fused_decode_step_refuses_what_it_does_not_cover():
     """mkv_qkv_norm_rope_append_decode checks its arguments on the host,
-    before any launch: an fp32 cache, a bf16 cache under an fp32 q (whose
-    decode splits q in two bf16 parts), per-token-head scales, head_dim 64
+    before any launch: an fp32 cache, a bf16 or per-token-head cache under
+    a q other than bf16 (whose decode splits q in two bf16 parts), head_dim 64
     and 16 query heads per KV head are refused (the caller runs the producer
     and the decode instead), and so are a missing slot mapping and a short
     qkv row."""
@@ -67,7 +67,8 @@ def test_fused_decode_step_refuses_what_it_does_not_cover():
 
     assert call(kv_dtype=_lib.DTYPE_F32) == -3
     assert call(kv_dtype=_lib.DTYPE_BF16, out_dtype=_lib.DTYPE_F32) == -3
-    assert call(scale_mode=_lib.SCALE_PER_TOKEN_HEAD) == -3
+    assert call(scale_mode=_lib.SCALE_PER_TOKEN_HEAD, out_dtype=_lib.DTYPE_F32) == -3
+    assert call(kv_dtype=_lib.DTYPE_I8, scale_mode=_lib.SCALE_PER_TOKEN_HEAD, out_dtype=_lib.DTYPE_F16) == -3
     assert call(Hq=16, Hkv=8, D=64) == -4
     assert call(Hq=128, Hkv=8) == -5
     assert call(slots=None) == -1
