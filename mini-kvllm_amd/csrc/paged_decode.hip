@@ -1177,10 +1177,11 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
   }
   const bool append = slot >= 0 && slot < pa.num_slots;
 
-  // The first tile: 1-byte caches load it speculatively (as in
-  // wg_decode_rr); 16-bit caches take consecutive ranges, known once the
-  // context length is (wg_item's split).  Then the cos / sin pair of the
-  // position (rotary_row's values).
+  // The first tile: per-tensor FP8 loads it speculatively (as in
+  // wg_decode_rr); per-token-head caches take the same round-robin tiles,
+  // 16-bit caches consecutive ranges, known once the context length is
+  // (wg_item's split), both loaded after the append.  Then the cos / sin
+  // pair of the position (rotary_row's values).
   const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
   const int64_t L = L_raw < 0 ? 0 : (L_raw > cap ? cap : L_raw);
   int step = 32 * nw;
@@ -1202,7 +1203,7 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
                     (pos_ok ? pos : 0) * kHeadDim * dtype_bytes(pa.cs_dtype);
   const uint32_t cw = elem_word(csr, lane, pa.cs_dtype), sw = elem_word(csr, 64 + lane, pa.cs_dtype);
 
-  // 1-byte caches: the context length is known, the second tile's loads go
+  // Per-tensor FP8: the context length is known, the second tile's loads go
   // out (empty past the range) before the producer's math waits for its
   // inputs, and the new token's row is patched into the tile that holds
   // position L - 1 when this call appends it there (slot = that position's
