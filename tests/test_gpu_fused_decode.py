@@ -10,7 +10,7 @@ it (attention.py:1213-1268), in one launch.
   sizes 16 and 256, contexts 0-800 (the new token in a wave's first,
   second or a later tile), rows without a slot, every input dtype and the
   1.0-sentinel calibration; bf16, fp16 and per-token-head FP8 / INT8
-  caches (loaded after the append has landed) over the same group sizes.
+  caches (loaded after the append has landed) over groups 1-8.
 * Against the oracle (qkv_norm_rope_ref, then paged_decode_ref on the
   dequantised cache): within the FP8 bound, 2e-2 abs.
 """
@@ -133,7 +133,8 @@ def test_fused_decode_step_equals_the_two_calls(dev, Hq, Hkv, bs):
     _assert_same(_fused(c), _two_calls(c))
 
 
-@pytest.mark.parametrize("Hq,Hkv", [(16, 8), (32, 8), (8, 8), (64, 8), (24, 3)])
+@pytest.mark.parametrize("Hq,Hkv", [(16, 8), (32, 8), (8, 8), (64, 8), (24, 3), (12, 4), (40, 8), (48, 8),
+                                    (56, 8)])
 @pytest.mark.parametrize("cache_dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("bs", [16, 256])
 def test_fused_decode_step_16bit_caches(dev, Hq, Hkv, cache_dtype, bs):
@@ -170,7 +171,8 @@ def test_fused_decode_step_int32_lengths_and_wide_rows(dev, cache_dtype):
     _assert_same(_fused(c), _two_calls(c))
 
 
-@pytest.mark.parametrize("Hq,Hkv", [(16, 8), (32, 8), (8, 8), (64, 8), (24, 3)])
+@pytest.mark.parametrize("Hq,Hkv", [(16, 8), (32, 8), (8, 8), (64, 8), (24, 3), (12, 4), (40, 8), (48, 8),
+                                    (56, 8)])
 @pytest.mark.parametrize("cache_dtype", [torch.float8_e4m3fn, torch.int8])
 @pytest.mark.parametrize("bs", [16, 256])
 def test_fused_decode_step_per_token_head_caches(dev, Hq, Hkv, cache_dtype, bs):
