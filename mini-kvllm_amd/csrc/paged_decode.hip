@@ -2510,20 +2510,34 @@ int wg_waves(int batch, int kv_heads, int group, int max_blocks, int block_size,
 // block-table width as the bound of the longest context (the reference's
 // runner pads each decode step's tables to its longest sequence,
 // model_runner.py:640-644):
-//   * the workgroup route when its waves fill at least a quarter of the
-//     wave slots (items x waves >= 2 x CUs) and the longest possible item
-//     gives each of its waves at most 256 tokens (512 for fp32 caches): one
-//     launch, no workspace, no partial round trip through HBM.  Its time is
-//     set by the longest item's tile chain, so short contexts favour it
-//     (batches 16-128 of 300-800 tokens in 4-block tables: 12.3 / 13.4 /
-//     19.0 / 20.5 us at batches 16 / 32 / 40 / 60 against 17.6 / 20.1 /
-//     21.7 / 25.2 us for stream-K and its merge) and long ones do not (batch
-//     32 of 256-4096 tokens: 42.9 against 34.8 us);
+//   * the workgroup route (one launch, no workspace, no partial round trip
+//     through HBM) when the longest possible item gives each of its waves
+//     at most 128 tokens, whatever the batch; or at most 256 tokens when
+//     its waves also fill enough wave slots (items x waves >= 2 x CUs for
+//     per-tensor FP8, 6 x CUs for 16-bit caches, whose tiles are twice the
+//     bytes; per-token-head FP8 / INT8 never); fp32 caches: at most 512
+//     tokens with items x waves >= 2 x CUs.  Its time is set by the longest item's
+//     tile chain, so short contexts favour it and long ones do not.
+//     Measured (graph replays, 8 KV heads, FP8 / bf16 / FP8 per-token-head):
+//     batches 1 / 4 of 300-800 tokens in 4-block tables (128 tokens a wave)
+//     9.1 / 10.5, 11.5 / 13.3, 11.6 / 15.4 us against 13.9 / 15.0, 13.8 /
+//     14.9, 14.0 / 15.0 us for stream-K and its merge; batches 8 / 16 of
+//     1024-2048 tokens in 8-block tables (256 tokens a wave) FP8 20.1 / 21.6
+//     against 22.5 / 23.9 us, bf16 28.3 / 30.7 against 21.0 / 28.1 us, at
+//     batch 32 bf16 38.3 against 41.4 us; FP8 batches 1 / 4 there 15.4 /
+//     17.8 against 18.4 / 21.0 us, per-token-head FP8 22.2 / 27.8 against
+//     18.3 / 20.9 us (batches 8-32 and 60 likewise: 26-36 against 23-31
+//     us); batch 32 of 256-4096 tokens: 42.9 against 34.8 us.
+//     per_token: the call's scales are per token and head (INT8 always);
+//     mkv_paged_decode_route, which has no scale mode, reports per-tensor
+//     FP8's route for an FP8 dtype, and mkv_paged_decode_workspace_size
+//     sizes for the larger of the two;
 //   * stream-K otherwise (16-bit / FP8 / INT8 caches): balanced over every
 //     wave whatever the lengths, at the cost of a merge launch;
-//   * split-K for fp32 caches otherwise (default split).
+//   * split-K for fp32 caches otherwise (default split; the workgroup route
+//     took 37.0 us against 21.0 us for fp32 batch 4 of 207-798 tokens).
 int choose_route(int split_tokens, int kv_dtype, int batch, const KernelShape& ks, int max_blocks,
-                 int block_size, int cus) {
+                 int block_size, int cus, bool per_token = false) {
   if (split_tokens == MKV_DECODE_WORKGROUP) return kRouteWorkgroup;
   if (split_tokens > 0) return kRouteSplit;
   const bool stream_ok =
@@ -2532,8 +2546,19 @@ int choose_route(int split_tokens, int kv_dtype, int batch, const KernelShape& k
   const int64_t items = (int64_t)batch * ks.kv_heads;
   const int nw = wg_waves(batch, ks.kv_heads, ks.group, max_blocks, block_size, cus);
   const int64_t wave_tokens = ((int64_t)max_blocks * block_size + nw - 1) / nw;
-  const int64_t bound = kv_dtype == MKV_DTYPE_F32 ? 16 * kTileTok : 8 * kTileTok;
-  if (items * nw >= 2 * (int64_t)cus && wave_tokens <= bound) return kRouteWorkgroup;
+  const int64_t fill = items * nw;
+  bool wg;
+  if (kv_dtype == MKV_DTYPE_F32)
+    wg = fill >= 2 * (int64_t)cus && wave_tokens <= 16 * kTileTok;
+  else if (wave_tokens <= 4 * kTileTok)
+    wg = true;
+  else if (per_token || kv_dtype == MKV_DTYPE_I8)
+    wg = false;
+  else if (kv_dtype == MKV_DTYPE_FP8E4M3)
+    wg = fill >= 2 * (int64_t)cus && wave_tokens <= 8 * kTileTok;
+  else
+    wg = fill >= 6 * (int64_t)cus && wave_tokens <= 8 * kTileTok;
+  if (wg) return kRouteWorkgroup;
   return stream_ok ? kRouteStream : kRouteSplit;
 }
 
@@ -2574,8 +2599,14 @@ extern "C" size_t mkv_paged_decode_workspace_size(int batch, int num_heads, int 
   if (batch <= 0 || max_blocks <= 0 || block_size <= 0 ||
       kernel_shape(num_heads, num_kv_heads, head_dim, ks) != MKV_OK)
     return 0;
-  const int route = choose_route(split_tokens, kv_dtype, batch, ks, max_blocks, block_size, device_cus());
-  return route_ws_bytes(route, batch, num_heads, ks, max_blocks, block_size, split_tokens);
+  const int cus = device_cus();
+  const int route = choose_route(split_tokens, kv_dtype, batch, ks, max_blocks, block_size, cus);
+  const size_t n = route_ws_bytes(route, batch, num_heads, ks, max_blocks, block_size, split_tokens);
+  if (kv_dtype != MKV_DTYPE_FP8E4M3) return n;
+  // (per-token-head FP8 scales may take another route)
+  const int rt = choose_route(split_tokens, kv_dtype, batch, ks, max_blocks, block_size, cus, true);
+  const size_t nt = route_ws_bytes(rt, batch, num_heads, ks, max_blocks, block_size, split_tokens);
+  return n > nt ? n : nt;
 }
 
 namespace {
@@ -2825,7 +2856,8 @@ int paged_decode_impl(void* out, int64_t out_batch_stride, const void* q, int64_
   if (st != MKV_OK) return st;
   if (batch == 0) return MKV_OK;
   const int cus = device_cus();
-  int route = choose_route(split_tokens, kv_dtype, batch, ks, max_blocks, block_size, cus);
+  int route = choose_route(split_tokens, kv_dtype, batch, ks, max_blocks, block_size, cus,
+                           fmt == kKvFp8PerToken || fmt == kKvI8PerToken);
   if (noalloc && route_ws_bytes(route, batch, num_heads, ks, max_blocks, block_size, split_tokens) >
                      workspace_bytes) {
     // The caller's scratch cannot hold this route's partials: the library's

@@ -176,9 +176,16 @@ def qkv_norm_rope_append_decode(qkv: torch.Tensor, positions: torch.Tensor, num_
         cl = _ctx_lens(context_lens)
         route = split_tokens
         if split_tokens == 0:
+            # 1-byte caches: where per-tensor FP8 would take the workgroup
+            # route (the query's answer for that dtype); per-token-head
+            # scales alone would take stream-K at up to 256 tokens a wave,
+            # but the one launch saves the producer's (~6 us), more than the
+            # workgroup route gives up there at the engine's decode shape
+            # (27.5 against 24.8 us for 60 rows in 4-block tables)
+            route_dt = _lib.DTYPE_FP8E4M3 if kv_code in (_lib.DTYPE_FP8E4M3, _lib.DTYPE_I8) else kv_code
             route = (_lib.DECODE_WORKGROUP
                      if _lib.query("mkv_paged_decode_route", T, num_heads, num_kv_heads, bt.shape[1],
-                                   k_cache.shape[1], head_dim, kv_code, 0, 0)
+                                   k_cache.shape[1], head_dim, route_dt, 0, 0)
                      == _lib.ROUTE_WORKGROUP else 0)
         fused = route == _lib.DECODE_WORKGROUP
     if not fused:

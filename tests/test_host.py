@@ -188,7 +188,14 @@ def test_decode_workspace_and_split_queries():
     assert nsk % (2 * 4 * 130 * 4) == (4 * 256 + 2) * 4
     waves = (nsk - (4 * 256 + 2) * 4) // (2 * 4 * 130 * 4)
     assert waves in (4096, 2048) and nsk < n
-    assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 1, 256, 128, FP8, 0) > 0
+    # (a 1-block table: 32 tokens a wave take the workgroup route, no
+    # workspace; 16 blocks take stream-K)
+    assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 1, 256, 128, BF16, 0) == 0
+    assert lib.mkv_paged_decode_workspace_size(4, 16, 8, 16, 256, 128, FP8, 0) > 0
+    # FP8 at 256 tokens a wave: per-tensor scales take the workgroup route at
+    # this fill, per-token-head scales stream-K; the query, which has no
+    # scale mode, sizes for the larger
+    assert lib.mkv_paged_decode_workspace_size(8, 32, 8, 8, 256, 128, FP8, 0) > 0
     # small batches split finer
     assert lib.mkv_paged_decode_split_tokens(4, 8, 8, 256, 0) < st or st == 64
 
@@ -220,6 +227,19 @@ def test_decode_route_choice():
     # workgroup (up to 512 tokens per wave for fp32)
     assert route(4, 16, 8, 8, 256, 128, F32) == SP
     assert route(60, 16, 8, 4, 256, 128, F32) == WG
+    # small batches: at most 128 tokens a wave (4-block tables, 8 waves) take
+    # the workgroup route whatever the fill; 256 tokens a wave only with the
+    # fill (FP8 2 x CUs, 16-bit 6 x CUs, INT8 per-token-head never)
+    I8 = _lib.DTYPE_I8
+    for B in (1, 4):
+        for dt in (FP8, BF16, I8):
+            assert route(B, 16, 8, 4, 256, 128, dt) == WG
+        assert route(B, 32, 8, 8, 256, 128, FP8) == SK
+        assert route(B, 32, 8, 8, 256, 128, BF16) == SK
+    assert route(8, 32, 8, 8, 256, 128, FP8) == WG
+    assert route(8, 32, 8, 8, 256, 128, BF16) == SK
+    assert route(32, 32, 8, 8, 256, 128, BF16) == WG
+    assert route(60, 16, 8, 4, 256, 128, I8) == SK
     # head_dim 64 pairs KV heads: Llama-3.2-1B decode, batch 48, 12-block tables
     assert route(48, 32, 8, 12, 256, 64, FP8) == SK
     assert route(64, 32, 8, 2, 256, 64, BF16) == WG
