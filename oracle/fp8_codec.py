@@ -1,7 +1,7 @@
 """Independent OCP e4m3fn codec in numpy (test infrastructure only).
 
 ORACLE — used only by tests/, __graft_entry__.smoke() and bench.py's CPU
-baseline as a checker; never by the product path.
+baseline, to check results against; never by the product path.
 
 Purpose: pin torch's ``Tensor.to(torch.float8_e4m3fn)`` — the byte-level
 authority of the reference's FP8 append (attention.py:190, cast after the

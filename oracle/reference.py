@@ -1,8 +1,9 @@
 """CPU restatement of the reference's KV-cache hot path (torch on CPU).
 
 ORACLE — test infrastructure only.  Only tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg may import this module, and only as the checker
-or as the timed CPU baseline; the product (mini-kvllm_amd/mkv) never does.
+bench.py's cpu_baseline leg may import this module, and only as the reference
+results are checked against or as the timed CPU baseline; the product
+(mini-kvllm_amd/mkv) never does.
 
 Every function names the reference code (paths relative to the reference
 repository heart1128/mini-kvllm) whose behaviour it restates.  Two kinds of
