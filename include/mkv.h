@@ -212,11 +212,14 @@ int mkv_fp8_calibrate_per_tensor(const void* key, int64_t key_row_stride,
  *
  * split_tokens selects the schedule:
  *   0 = the library's choice from (batch, num_kv_heads, max_blocks,
- *       block_size, kv_dtype): the workgroup route when the (sequence, KV
- *       head) items fill the device's CUs and each still gets at least 4
- *       waves, else stream-K (BF16/F16/FP8/INT8 KV, batch <= 8192), else
- *       split-K with a library-chosen split (mkv_paged_decode_route reports
- *       the choice);
+ *       block_size, kv_dtype, kv_scale_mode): the workgroup route when the
+ *       widest context the table allows gives each of its waves at most 128
+ *       tokens, or at most 256 tokens when its waves also fill enough of
+ *       the device (per-tensor FP8: 2 x CUs waves, BF16/F16: 6 x CUs;
+ *       never for per-token-head scales; FP32: at most 512 tokens and
+ *       2 x CUs waves); else stream-K (BF16/F16/FP8/INT8 KV, batch <= 8192),
+ *       else split-K with a library-chosen split (mkv_paged_decode_route
+ *       reports the choice);
  *   MKV_DECODE_STREAM = stream-K over 32-token tiles on a persistent grid,
  *       groups of num_kv_heads waves sharing each tile range, and a merge
  *       kernel (split-K where stream-K does not apply);
@@ -229,8 +232,9 @@ int mkv_fp8_calibrate_per_tensor(const void* key, int64_t key_row_stride,
  * workspace: >= mkv_paged_decode_workspace_size(...)
  * bytes with the same arguments (the size of the route those arguments
  * select: stream-K partial slots for the persistent grid, or split-K
- * partials, or 0); calls that share a workspace must be ordered on one
- * stream.
+ * partials, or 0; for an FP8 kv_dtype, which the query takes without a
+ * scale mode, the larger of the per-tensor and the per-token-head route's);
+ * calls that share a workspace must be ordered on one stream.
  */
 #define MKV_DECODE_WORKGROUP (-1)
 #define MKV_DECODE_STREAM (-2)
@@ -252,7 +256,9 @@ int mkv_paged_decode_split_tokens(int batch, int num_kv_heads, int max_blocks,
  * MKV_DECODE_ROUTE_STREAM / _SPLIT / _WORKGROUP, or a negative status for
  * an unsupported shape.  The reference has one decode entry and no schedule
  * (attention.py:895-950); this reports the library's choice for split_tokens
- * 0 and the route an explicit value selects. */
+ * 0 (for an FP8 kv_dtype, with per-tensor scales: per-token-head scales may
+ * take stream-K where this reports the workgroup route; INT8 is always per
+ * token and head) and the route an explicit value selects. */
 int mkv_paged_decode_route(int batch, int num_heads, int num_kv_heads,
                            int max_blocks, int block_size, int head_dim,
                            int kv_dtype, int split_tokens, int num_cus);
