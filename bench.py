@@ -805,8 +805,31 @@ def configs_extra(dev, stream, cpu: bool = True, which=DECODE_CONFIGS) -> dict:
             "what": "the same step over bf16 KV pools of the same shape",
             "two_calls_us": round(graph_time_us(two_calls_bf16), 2),
             "one_launch_us": round(graph_time_us(one_launch_bf16), 2)}
+        del kb, vb
+        # and over FP8 pools with per-token-head scales (one per slot and KV head)
+        kt = torch.empty(N, 256, 8, HEAD_DIM, dtype=torch.float8_e4m3fn, device=dev)
+        vt = torch.empty_like(kt)
+        kst = torch.empty(N, 256, 8, dtype=torch.float32, device=dev)
+        vst = torch.empty_like(kst)
+        W.fill_pools_per_token_head_on_device(kt, vt, kst, vst, 3005, "fp8_per_token_head")
+
+        def two_calls_tok():
+            qt = P.qkv_norm_rope_append(qkv, pos, 16, 8, HEAD_DIM, cs, kt, vt, slots, 256, q_norm_weight=nw_,
+                                        k_norm_weight=nw_, kv_cache_dtype="fp8_per_token_head", k_scale=kst,
+                                        v_scale=vst)[0]
+            A._decode(qt, kt, vt, bt, ctxd, 0.088, 16, 8, HEAD_DIM, kst, vst, out=out, per_token_head=True)
+
+        def one_launch_tok():
+            P.qkv_norm_rope_append_decode(qkv, pos, 16, 8, HEAD_DIM, cs, kt, vt, slots, 256, bt, ctxd, 0.088,
+                                          q_norm_weight=nw_, k_norm_weight=nw_, kv_cache_dtype="fp8_per_token_head",
+                                          k_scale=kst, v_scale=vst, out=out)
+        row["decode_step_from_qkv_fp8_per_token_head_cache"] = {
+            "what": "the same step over FP8 pools with per-token-head scales (the two calls' decode on the "
+                    "library's route for those scales)",
+            "two_calls_us": round(graph_time_us(two_calls_tok), 2),
+            "one_launch_us": round(graph_time_us(one_launch_tok), 2)}
         res["fp8_decode_b60_engine_shape"] = row
-        del kp, vp, kb, vb
+        del kp, vp, kt, vt
 
     # bf16 decode, the batch-256 workload
     if "bf16_decode_b256" in which:
