@@ -184,6 +184,29 @@ def _prefill_case(seed, fmt, Hq, Hkv, bs, prior, qlen, dev, holes=()):
     return q, dpools, hpools, bt, ctx, cu, pos
 
 
+@pytest.mark.parametrize("fmt", ["fp8_token", "int8_token"])
+@pytest.mark.parametrize("qdt", [torch.bfloat16, torch.float32])
+def test_prefill_head_dim64_large_v_scales(dev, fmt, qdt):
+    """Paired KV heads with V scales 2^20 times the usual: the prefill's
+    running-max lift takes the larger of the two heads' largest V scales of
+    a tile.  Divided back by 2^20 (exact), the output meets the oracle on
+    the unscaled caches within the prefill bound."""
+    announce(f"chunked prefill head_dim 64: {fmt}, q {qdt}, V scales x 2^20")
+    Hkv, group = 4, 4
+    Hq = Hkv * group
+    prior, qlen = [0, 300, 70], [130, 64, 150]
+    q, dp, hp, bt, ctx, cu, pos = _prefill_case(6400, fmt, Hq, Hkv, 16, prior, qlen, dev)
+    q = q.to(qdt)
+    S = float(2 ** 20)
+    sc = 1 / math.sqrt(D)
+    got = A.paged_attention_prefill_triton(
+        q.to(dev), dp[0], dp[1], bt.to(dev), ctx.to(dev), cu.to(dev), pos.to(dev), sc, Hq, Hkv, D, 16,
+        k_scale=dp[2], v_scale=dp[3] * S, kv_cache_dtype=MODE[fmt]).cpu()
+    assert torch.isfinite(got.float()).all()
+    want = R.paged_prefill_ref(q.double(), hp[0], hp[1], bt, ctx, cu, pos, sc, Hq, Hkv, hp[2], hp[3])
+    assert_close_out(got / S, want, got.dtype, PREFILL_TOL[fmt])
+
+
 @pytest.mark.parametrize("group", [1, 2, 4, 8])
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_prefill_head_dim64_groups_formats(dev, fmt, group):
