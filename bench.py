@@ -601,6 +601,8 @@ def graph_time_us(fn, reps: int = 20, replays: int = 10) -> float:
     an idle GPU runs through the power controller's transient."""
     import torch
 
+    from mkv.decode_state import graph_capture
+
     fn()
     torch.cuda.synchronize()
     side = torch.cuda.Stream()
@@ -610,7 +612,7 @@ def graph_time_us(fn, reps: int = 20, replays: int = 10) -> float:
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with graph_capture(g):
         for _ in range(reps):
             fn()
     for _ in range(3):

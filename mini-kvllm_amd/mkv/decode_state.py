@@ -24,6 +24,8 @@ leave the state untouched.
 """
 from __future__ import annotations
 
+import contextlib
+import gc
 from typing import Callable, Iterable
 
 import torch
@@ -118,6 +120,25 @@ class DecodeMetadata:
         return (self.slot_mapping[:rows], self.context_lens[:rows], self.block_tables[:rows, :width])
 
 
+@contextlib.contextmanager
+def graph_capture(graph: torch.cuda.CUDAGraph, pool=None):
+    """``torch.cuda.graph(graph, pool)`` with Python's cyclic garbage
+    collector run first and held off until the capture ends.  An object
+    freed by a collection inside the capture frees what it owns there (a
+    dead engine's graphs and their memory pool, a workspace), and those
+    calls are not allowed while a stream captures: the process aborts.
+    torch (2.10) no longer collects before a capture by itself."""
+    gc.collect()
+    enabled = gc.isenabled()
+    gc.disable()
+    try:
+        with torch.cuda.graph(graph, pool):
+            yield
+    finally:
+        if enabled:
+            gc.enable()
+
+
 class DecodeGraphs:
     """Decode steps captured per (batch bucket, table width) over one
     :class:`DecodeMetadata`.
@@ -188,7 +209,7 @@ class DecodeGraphs:
         torch.cuda.synchronize(m.device)
         for rows, width in keys:
             g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, self.pool):
+            with graph_capture(g, self.pool):
                 self.step_fn(rows, *m.step(rows, 1, width))
             if self.pool is None:
                 self.pool = g.pool()

@@ -18,6 +18,7 @@ import torch
 
 from conftest import announce
 from mkv import attention as A
+from mkv.decode_state import graph_capture
 
 pytestmark = pytest.mark.gpu
 
@@ -69,7 +70,7 @@ def test_fp8_append_and_decode_replay_in_a_graph(dev):
         step(kc.clone(), vc.clone())
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    with torch.cuda.graph(graph):
+    with graph_capture(graph):
         out_g = step(kc, vc)
     torch.cuda.synchronize()
     # capturing does not execute: the graph's caches are still the prior state

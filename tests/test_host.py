@@ -435,3 +435,48 @@ def test_stream_read_probe_checks_arguments_on_the_host():
     assert lib.mkv_stream_read_probe(16, 4096, 16, (1 << 20) + 1, None) == -2  # grid too large (above 2^20)
     assert lib.mkv_stream_read_probe(None, 4096, 16, 64, None) == -1
     assert lib.mkv_stream_read_probe(24, 4096, 16, 64, None) == -8     # misaligned buffer
+
+
+def test_graph_capture_runs_the_collector_first_and_holds_it_off(monkeypatch):
+    """A cycle collected inside a capture frees what it owns there (a dead
+    engine's graphs and their pool), which aborts a capturing process: the
+    capture helper collects first and keeps the collector off until the
+    capture ends, an error in it included, and restores its state."""
+    import contextlib
+    import gc
+
+    from mkv import decode_state as DS
+
+    seen = []
+
+    @contextlib.contextmanager
+    def fake_graph(graph, pool=None):
+        seen.append(("enter", gc.isenabled(), pool))
+        yield
+        seen.append(("exit", gc.isenabled()))
+
+    class Cycle:
+        def __init__(self):
+            self.me = self
+
+        def __del__(self):
+            seen.append("collected")
+
+    monkeypatch.setattr(DS.torch.cuda, "graph", fake_graph)
+    assert gc.isenabled()
+    Cycle()  # garbage only a collection frees
+    with DS.graph_capture(object(), pool="p"):
+        assert not gc.isenabled()
+    assert seen == ["collected", ("enter", False, "p"), ("exit", False)]
+    assert gc.isenabled()
+    with pytest.raises(RuntimeError):
+        with DS.graph_capture(object()):
+            raise RuntimeError("step failed under capture")
+    assert gc.isenabled()
+    gc.disable()
+    try:
+        with DS.graph_capture(object()):
+            pass
+        assert not gc.isenabled()  # a caller's disabled collector stays disabled
+    finally:
+        gc.enable()
