@@ -1173,15 +1173,25 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
       }
       if (ks == 1.0f) ks = producer_calibrate(pa, true, pa.k_scale, IN_DT, wkl, wkh);
       if (vs == 1.0f) vs = producer_calibrate(pa, false, pa.v_scale, IN_DT, wkl, wkh);
+      // vmcnt(0) before the paths join: with this branch's loads pending
+      // there, the compiler's wait at the join also held every call's tile
+      // loads back until the producer's loads had returned
+      __builtin_amdgcn_s_waitcnt(0x0f70);
     }
   }
   const bool append = slot >= 0 && slot < pa.num_slots;
+  // The cos / sin pair of the position (rotary_row's values), issued before
+  // any tile's loads: the load counter returns loads in issue order, and the
+  // producer's math waits only for its own inputs.
+  const bool pos_ok = pos >= 0 && pos < pa.max_position;
+  const char* csr = reinterpret_cast<const char*>(pa.cos_sin) +
+                    (pos_ok ? pos : 0) * kHeadDim * dtype_bytes(pa.cs_dtype);
+  const uint32_t cw = elem_word(csr, lane, pa.cs_dtype), sw = elem_word(csr, 64 + lane, pa.cs_dtype);
 
   // The first tile: per-tensor FP8 loads it speculatively (as in
   // wg_decode_rr); per-token-head caches take the same round-robin tiles,
   // 16-bit caches consecutive ranges, known once the context length is
-  // (wg_item's split), both loaded after the append.  Then the cos / sin
-  // pair of the position (rotary_row's values).
+  // (wg_item's split), both loaded after the append.
   const int64_t cap = (int64_t)a.idx.max_blocks << a.idx.bs_log2;
   const int64_t L = L_raw < 0 ? 0 : (L_raw > cap ? cap : L_raw);
   int step = 32 * nw;
@@ -1198,10 +1208,6 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
   Tile16<KV_DT> ta, tb2;
   PhysPair ph = item_phys(a, it.b, it.t_begin, it.t_end);
   if constexpr (kFp8) load_tile16<KV_DT, false>(a, it, Ld, it.t_begin, ph, ta);
-  const bool pos_ok = pos >= 0 && pos < pa.max_position;
-  const char* csr = reinterpret_cast<const char*>(pa.cos_sin) +
-                    (pos_ok ? pos : 0) * kHeadDim * dtype_bytes(pa.cs_dtype);
-  const uint32_t cw = elem_word(csr, lane, pa.cs_dtype), sw = elem_word(csr, 64 + lane, pa.cs_dtype);
 
   // Per-tensor FP8: the context length is known, the second tile's loads go
   // out (empty past the range) before the producer's math waits for its
