@@ -1043,9 +1043,11 @@ __global__ __launch_bounds__(kWgSplitWaves* kWave) void paged_decode_wg_qsplit_k
 // its waves share out the token's q heads of the group and its K and V
 // heads kvh (one head per wave pass, 64 lanes wide, with the producer
 // kernel's operations in the producer kernel's order), put q and the new
-// K / V cache rows in LDS, and append the rows.  Per-tensor FP8: the tiles'
-// loads go out before the append lands, and the wave whose tile holds the
-// token's position takes that row from LDS instead of from the cache.
+// K / V cache rows in LDS, and append the rows.  Per-tensor FP8: the first
+// tile's loads go out before the producer's math, the second tile's after
+// the barrier, either before the append lands, and the wave whose tile
+// holds the token's position takes that row from LDS instead of from the
+// cache.
 // 16-bit and per-token-head caches: every tile is loaded after the append
 // has landed.  The result is the producer kernel followed by the workgroup
 // route, bit for bit.
@@ -1209,14 +1211,19 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
   PhysPair ph = item_phys(a, it.b, it.t_begin, it.t_end);
   if constexpr (kFp8) load_tile16<KV_DT, false>(a, it, Ld, it.t_begin, ph, ta);
 
-  // Per-tensor FP8: the context length is known, the second tile's loads go
-  // out (empty past the range) before the producer's math waits for its
-  // inputs, and the new token's row is patched into the tile that holds
-  // position L - 1 when this call appends it there (slot = that position's
-  // cache row): that tile's loads may have left before the append landed.
-  // 16-bit and per-token-head caches load their tiles after the append has
-  // landed instead (the patch's registers beside two 16-bit tiles would
-  // spill; a per-token-head tile would also need the row's scales patched).
+  // Per-tensor FP8: the context length is known; the second tile's
+  // block-table entries are looked up here and its loads go out after the
+  // barrier.  A wave issues in order, and while the grid's first tiles are
+  // in flight a load's issue stalls: 12 more loads ahead of the producer's
+  // math held back the math and the barrier that every wave of the
+  // workgroup waits at (the step measured 20.1 us with them there, 19.2-19.3
+  // us with them after the barrier, at 60 rows of 300-800 tokens).  The new
+  // token's row is patched into the tile that holds position L - 1 when
+  // this call appends it there (slot = that position's cache row): that
+  // tile's loads may have left before the append landed.  16-bit and
+  // per-token-head caches load their tiles after the append has landed
+  // instead (the patch's registers beside two 16-bit tiles would spill; a
+  // per-token-head tile would also need the row's scales patched).
   bool patch = false;
   const int pl = (int)L - 1;
   if constexpr (kFp8) {
@@ -1224,8 +1231,6 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
     const int64_t phys_pl = pl >= 0 ? a.idx.physical_block(it.b, pl >> a.idx.bs_log2) : -1;
     patch = append && phys_pl >= 0 && (phys_pl << a.idx.bs_log2) + (pl & ((1 << a.idx.bs_log2) - 1)) == slot;
     ph = item_phys(a, it.b, it.t_begin + step, it.t_end);
-    load_tile16<KV_DT, false>(a, it, Ld, it.t_begin + step, ph, tb2);
-    ph = item_phys(a, it.b, it.t_begin + 2 * step, it.t_end);
   }
 
   // The producer's math (produce_qk / load_v and store_kv's bytes, the same
@@ -1341,6 +1346,10 @@ MKV_DEV void wg_produce_decode(const ProduceDecodeArgs& f) {
   for (int mm = 0; mm < 8; ++mm) acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegBig, l_run = 0.0f;
   if (it.t_begin < it.t_end) {
+    if constexpr (kFp8) {  // the second tile (empty past the range)
+      load_tile16<KV_DT, false>(a, it, Ld, it.t_begin + step, ph, tb2);
+      ph = item_phys(a, it.b, it.t_begin + 2 * step, it.t_end);
+    }
     // q of head c, dims 32kg .. 32kg+31 (zeros for padding heads)
     const int cq = lane & 15, kg = lane >> 4;
     float qf[32];
