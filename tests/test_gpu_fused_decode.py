@@ -177,9 +177,11 @@ def test_fused_decode_step_int32_lengths_and_wide_rows(dev, cache_dtype):
 @pytest.mark.parametrize("bs", [16, 256])
 def test_fused_decode_step_per_token_head_caches(dev, Hq, Hkv, cache_dtype, bs):
     """Per-token-head FP8 / INT8 caches: each appended row's scale from its
-    head's amax (store_kv's), its codes, and the attention over every tile
-    loaded after the append; the codes, the per-slot scales and the output
-    equal the two calls'."""
+    head's amax (store_kv's), its codes, and the attention over tiles loaded
+    after the append, except each wave's first tile, which goes out before
+    it and is loaded again by the wave that holds the new token (the edge
+    contexts of the first rows put it in a first tile); the codes, the
+    per-slot scales and the output equal the two calls'."""
     announce(f"fused decode step per-token-head {cache_dtype} cache {Hq}/{Hkv} block {bs}")
     c = _case(dev, Hq * 3 + bs + 2, 40, Hq, Hkv, bs, torch.bfloat16, no_slot=(6, 33),
               cache_dtype=cache_dtype, per_token=True)
